@@ -1,0 +1,396 @@
+#!/usr/bin/env python3
+"""tiler-hip benchmark on one MI355X.
+
+A "step" is one launch of the hot path over one batch of synthetic input that
+is already resident in HBM.  The headline line measures BASELINE.json's metric
+on configs[1] (RMS normalization, bf16 [8192 x 4096], w bf16 [4096], eps 1e-5,
+f32 accumulation, bf16 output) as achieved HBM GB/s of algorithmic bytes; the
+other four configs are measured the same way and reported under "families".
+
+Measurement rules: fixed seeds; input/output buffer sets are
+rotated so more than the 256 MB Infinity Cache is touched per sweep; W untimed
+warm-up launches, then K back-to-back launches between HIP events recorded on
+the context stream the kernels run on (median/p10/p90 from per-launch event
+pairs in the same region).  The CPU baseline is the oracle's restatement of
+the reference loops (strict binary32 folds, no FMA) on the GPU box's host,
+single-threaded, on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+                       [--no-families] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA, TFLOP/s
+EPS_BITS = 0x3727C5AC           # 1e-5 as binary32 (config eps)
+METRIC = "achieved HBM GB/s (% peak) for RMSNorm/softmax/gather; bf16 GEMM TFLOP/s"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Workload:
+    name = ""
+    bound = "hbm"
+    unit = "GB/s"
+
+    def __init__(self, ctx):
+        self.ctx = ctx
+        self.buffers = []
+
+    def _keep(self, *bufs):
+        self.buffers.extend(bufs)
+        return bufs if len(bufs) > 1 else bufs[0]
+
+    def teardown(self):
+        for b in self.buffers:
+            b.free()
+        self.buffers = []
+
+
+class RmsNorm(Workload):
+    """RMS normalization over rows."""
+    name = "rms_norm"
+    rows, extent = 8192, 4096
+    sets = 6  # 6 x 128 MiB touched per sweep
+
+    def config(self):
+        return {"workload": "rms_norm bf16 [8192 x 4096] x w[4096] eps=1e-5, f32 accumulation, bf16 out",
+                "rows": self.rows, "hidden": self.extent, "storage": "bf16", "eps_bits": hex(EPS_BITS),
+                "buffer_sets": self.sets}
+
+    def work(self):  # algorithmic bytes per launch
+        return self.rows * self.extent * 2 * 2 + self.extent * 2
+
+    def setup(self):
+        import oracle
+        from tiler_amd import _lib as L
+        self.L = L
+        rng = np.random.default_rng(1)
+        w = oracle.bf16_narrow(rng.normal(1.0, 0.1, self.extent).astype(np.float32))
+        self.w = self._keep(self.ctx.to_device(w))
+        self.sets_ = []
+        for s in range(self.sets):
+            x = oracle.bf16_narrow(rng.standard_normal((self.rows, self.extent), dtype=np.float32))
+            self.sets_.append(self._keep(self.ctx.to_device(x), self.ctx.alloc(x.nbytes)))
+        return len(self.sets_)
+
+    def launch(self, i):
+        x, y = self.sets_[i % len(self.sets_)]
+        self.ctx.rms_norm(self.L.BF16, x, self.w, self.rows, self.extent, EPS_BITS, y,
+                          weight_broadcast=True)
+
+    def cpu_baseline(self, budget_s):
+        """The oracle's strict RMSNorm (widen, normalize, narrow) on whole rows."""
+        import oracle
+        rng = np.random.default_rng(7)
+        rows = 512
+        xb = oracle.bf16_narrow(rng.standard_normal((rows, self.extent), dtype=np.float32))
+        wb = oracle.bf16_narrow(rng.normal(1.0, 0.1, self.extent).astype(np.float32))
+        wfull = np.broadcast_to(oracle.bf16_widen(wb), (rows, self.extent)).copy()
+        done, t0 = 0, time.perf_counter()
+        while True:
+            xf = oracle.bf16_widen(xb)
+            y = oracle.rms_norm_f32(xf, wfull, (rows, self.extent), 1, EPS_BITS)
+            oracle.bf16_narrow(y)
+            done += rows
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        by = done * self.extent * 4 + self.extent * 2
+        return {"value": by / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done} rows x {self.extent} of the config in {el:.1f} s, single thread "
+                          "(oracle rms_norm_f32 over widened bf16, then narrowing)"}
+
+
+class Sum(Workload):
+    """f32[2^24] -> scalar, the two-level tree."""
+    name = "sum"
+    n = 1 << 24
+    sets = 6
+
+    def config(self):
+        return {"workload": "serial-sum f32[2^24] ~U[-1,1] -> f32 scalar (two-level tree)",
+                "buffer_sets": self.sets}
+
+    def work(self):
+        return self.n * 4 + 4
+
+    def setup(self):
+        rng = np.random.default_rng(0)
+        self.xs = [self._keep(self.ctx.to_device(rng.uniform(-1, 1, self.n).astype(np.float32)))
+                   for _ in range(self.sets)]
+        self.out = self._keep(self.ctx.alloc(4))
+        return self.sets
+
+    def launch(self, i):
+        self.ctx.sum_f32(self.xs[i % self.sets], 1, self.n, self.out)
+
+    def cpu_baseline(self, budget_s):
+        import oracle
+        x = np.random.default_rng(0).uniform(-1, 1, self.n).astype(np.float32)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            oracle.strict_sum(x, (self.n,), 0)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        return {"value": done * self.work() / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done} x strict_sum over 2^24 in {el:.1f} s, single thread"}
+
+
+class Softmax(Workload):
+    """f32 [32 x 2048 x 2048] softmax over the last axis."""
+    name = "softmax"
+    rows, extent = 32 * 2048, 2048
+    sets = 2
+
+    def config(self):
+        return {"workload": "softmax f32 [32 x 2048 x 2048] ~N(0,3), last axis", "buffer_sets": self.sets}
+
+    def work(self):
+        return self.rows * self.extent * 4 * 2
+
+    def setup(self):
+        rng = np.random.default_rng(3)
+        self.sets_ = []
+        for _ in range(self.sets):
+            x = rng.standard_normal((self.rows, self.extent), dtype=np.float32) * np.float32(3.0)
+            self.sets_.append(self._keep(self.ctx.to_device(x), self.ctx.alloc(x.nbytes)))
+        return self.sets
+
+    def launch(self, i):
+        x, y = self.sets_[i % self.sets]
+        self.ctx.softmax_f32(x, self.rows, self.extent, y)
+
+    def cpu_baseline(self, budget_s):
+        import oracle
+        rows = 256
+        x = np.random.default_rng(3).standard_normal((rows, self.extent), dtype=np.float32) * np.float32(3.0)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            oracle.softmax_f32(x, (rows, self.extent), 1)
+            done += rows
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        return {"value": done * self.extent * 8 / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done} rows x {self.extent} in {el:.1f} s, single thread (certified exp)"}
+
+
+class Gather(Workload):
+    """tied embedding gather."""
+    name = "gather"
+    vocab, hidden, count = 128256, 4096, 16384
+    sets = 6
+
+    def config(self):
+        return {"workload": "gather bf16 [128256 x 4096] by int32[16384] -> bf16 [16384 x 4096]",
+                "index_sets": self.sets}
+
+    def work(self):
+        return self.count * self.hidden * 2 * 2 + self.count * 4
+
+    def setup(self):
+        import oracle
+        rng = np.random.default_rng(4)
+        table = np.empty((self.vocab, self.hidden), np.uint16)
+        for lo in range(0, self.vocab, 16384):
+            hi = min(self.vocab, lo + 16384)
+            table[lo:hi] = oracle.bf16_narrow(
+                rng.standard_normal((hi - lo, self.hidden), dtype=np.float32) * np.float32(0.02))
+        self.table = self._keep(self.ctx.to_device(table))
+        del table
+        self.idx = [self._keep(self.ctx.to_device(rng.integers(0, self.vocab, self.count).astype(np.int32)))
+                    for _ in range(self.sets)]
+        self.outs = [self._keep(self.ctx.alloc(self.count * self.hidden * 2)) for _ in range(2)]
+        return self.sets
+
+    def launch(self, i):
+        self.ctx.gather(self.table, 1, self.vocab, self.hidden, 2, self.idx[i % self.sets], self.count,
+                        self.outs[i % 2], index_signed=True)
+
+    def cpu_baseline(self, budget_s):
+        import oracle
+        rng = np.random.default_rng(4)
+        vocab = 8192
+        table = rng.integers(0, 65535, (vocab, self.hidden), dtype=np.uint16)
+        idx = rng.integers(0, vocab, self.count).astype(np.int32)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            oracle.gather(table.reshape(-1), 1, vocab, self.hidden, idx.view(np.uint32), index_signed=True)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        return {"value": done * self.work() / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done} x {self.count}-row gather (table of {vocab} rows) in {el:.1f} s"}
+
+
+class Contract(Workload):
+    """bf16 4096^3 contraction with fused SiLU."""
+    name = "contract"
+    bound = "mfma"
+    unit = "TFLOP/s"
+    m = n = k = 4096
+    sets = 4
+
+    def config(self):
+        return {"workload": "contraction bf16 A[4096x4096] . B[4096x4096]^T, f32 acc, fused SiLU, bf16 C",
+                "buffer_sets": self.sets}
+
+    def work(self):  # flops per launch
+        return 2 * self.m * self.n * self.k
+
+    def setup(self):
+        import oracle
+        from tiler_amd import _lib as L
+        self.L = L
+        rng = np.random.default_rng(5)
+        self.sets_ = []
+        for _ in range(self.sets):
+            a = oracle.bf16_narrow(rng.standard_normal((self.m, self.k), dtype=np.float32) / np.float32(64.0))
+            b = oracle.bf16_narrow(rng.standard_normal((self.n, self.k), dtype=np.float32) / np.float32(64.0))
+            self.sets_.append(self._keep(self.ctx.to_device(a), self.ctx.to_device(b),
+                                         self.ctx.alloc(self.m * self.n * 2)))
+        return self.sets
+
+    def launch(self, i):
+        a, b, c = self.sets_[i % self.sets]
+        self.ctx.contract_bf16(a, b, self.m, self.n, self.k, c, self.L.EPILOGUE_SILU)
+
+    def cpu_baseline(self, budget_s):
+        import oracle
+        rng = np.random.default_rng(5)
+        a = rng.standard_normal((self.m, self.k), dtype=np.float32) / np.float32(64.0)
+        b = rng.standard_normal((self.n, self.k), dtype=np.float32) / np.float32(64.0)
+        done, rows, t0 = 0, 2, time.perf_counter()
+        while True:
+            oracle.contract_strict_f32(a[done % self.m:done % self.m + rows], b, rows, self.n, self.k,
+                                       threads=1)
+            done += rows
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        flops = 2.0 * done * self.n * self.k
+        return {"value": flops / el / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                "sample": f"{done} output rows of the strict f32 fold (x{self.n}, k={self.k}) in {el:.1f} s, "
+                          "single thread; extrapolated per row"}
+
+
+WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, Gather, Contract)}
+
+
+def measure(ctx, wl, steps, warmup):
+    log(f"{wl.name}: preparing synthetic inputs")
+    wl.setup()
+    for i in range(warmup):
+        wl.launch(i)
+    ctx.synchronize()
+    events = [ctx.event() for _ in range(steps + 1)]
+    log(f"{wl.name}: timing {steps} launches")
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ctx.record(events[i])
+        wl.launch(warmup + i)
+    ctx.record(events[steps])
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = ctx.elapsed_ms(events[0], events[steps])
+    per = np.asarray([ctx.elapsed_ms(events[i], events[i + 1]) for i in range(steps)])
+    for e in events:
+        ctx.destroy_event(e)
+    wl.teardown()
+    mean_ms = total_ms / steps
+    work = wl.work()
+    if wl.bound == "hbm":
+        achieved = work / (mean_ms / 1e3) / 1e9
+        peak = HBM_PEAK_GBS
+    else:
+        achieved = work / (mean_ms / 1e3) / 1e12
+        peak = MFMA_BF16_PEAK_TFLOPS
+    return {
+        "value": achieved, "unit": wl.unit, "ms_per_step": mean_ms,
+        "median_ms": float(np.median(per)), "p10_ms": float(np.percentile(per, 10)),
+        "p90_ms": float(np.percentile(per, 90)), "wall_s": wall,
+        "roofline": {"bound": wl.bound, "achieved": achieved, "peak": peak,
+                     "unit": wl.unit, "frac": achieved / peak, "traffic": None,
+                     "work_per_launch": work},
+        "config": wl.config(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="rms_norm", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-families", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("tiler-hip bench runs on one GPU: this build has no multi-GPU path "
+              "(the reference has no multi-device notion); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import tiler_amd
+    ctx = tiler_amd.Context(0)
+    log(f"device {ctx.environment['device_name']} {ctx.environment['gcn_arch_name']} "
+        f"CUs={ctx.environment['compute_units']}")
+
+    head = measure(ctx, WORKLOADS[args.workload](ctx), args.steps, args.warmup)
+    families = {}
+    if not args.no_families:
+        for name, cls in WORKLOADS.items():
+            if name == args.workload:
+                continue
+            r = measure(ctx, cls(ctx), max(20, args.steps // 2), args.warmup)
+            families[name] = {k: r[k] for k in ("value", "unit", "ms_per_step", "median_ms", "roofline", "config")}
+            log(f"{name}: {r['value']:.1f} {r['unit']} ({100 * r['roofline']['frac']:.1f}% of peak)")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline ({args.workload}), ~{args.cpu_seconds:.0f} s")
+        cpu = WORKLOADS[args.workload](ctx).cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if args.workload != "contract" else "bf16",
+        "data": "synthetic (seeded numpy; BASELINE.json config shapes and distributions)",
+        "config": head["config"],
+        "timing": {"median_ms": head["median_ms"], "p10_ms": head["p10_ms"], "p90_ms": head["p90_ms"]},
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "families": families,
+        "device": {k: ctx.environment[k] for k in ("device_name", "gcn_arch_name", "compute_units")},
+    }
+    ctx.close()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,346 @@
+/*
+ * tiler_hip.h -- C ABI of the tiler-hip MI355X (gfx950) backend.
+ *
+ * The reference is a Rust compiler whose backend seams are traits; this ABI is
+ * what a thin Rust (or any FFI) shim binds to realize them on MI355X.  Each
+ * entry point cites the reference interface it replaces (paths relative to
+ * /root/reference/crates/).  Plain pointers and sizes only; no C++ types, no
+ * exceptions cross the boundary, and all state lives in a tiler_hip_context
+ * (the adapter's `Self`).  One context = one device and one ordered stream,
+ * the reference's single-device profile (docs/decisions/0090-...md:152):
+ * calls on one context must not overlap from several threads.
+ *
+ * Status convention (tiler-runtime/src/adapter.rs:222-231, ADR 0051):
+ *   0                 success
+ *   negative          Refusal: pre-commit, nothing irreversible happened,
+ *                     a fallback route is still permitted
+ *   positive          Failure: post-commit, reported and never retried
+ *
+ * Device pointers are plain device addresses (hipMalloc'd or from
+ * tiler_hip_buffer_alloc).  `stream` arguments take a hipStream_t; NULL means
+ * the context's own stream.  Launch entry points are asynchronous: they
+ * enqueue on the stream and return once the launch is accepted.
+ */
+#ifndef TILER_HIP_H
+#define TILER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t tiler_hip_status;
+
+#define TILER_HIP_OK 0
+/* Refusals (pre-commit; RuntimeAdapter::Refusal). */
+#define TILER_HIP_REFUSE_NO_DEVICE (-1)
+#define TILER_HIP_REFUSE_FOREIGN_TARGET (-2)
+#define TILER_HIP_REFUSE_INVALID_ARGUMENT (-3)
+#define TILER_HIP_REFUSE_MALFORMED_PAYLOAD (-4)
+#define TILER_HIP_REFUSE_ABSENT_SYMBOL (-5)
+#define TILER_HIP_REFUSE_BINDING_MISMATCH (-6)
+#define TILER_HIP_REFUSE_CAPACITY (-7)
+#define TILER_HIP_REFUSE_UNSUPPORTED (-8)
+#define TILER_HIP_REFUSE_GATHER_INDEX_OUT_OF_BOUNDS (-9)
+#define TILER_HIP_REFUSE_UNRECOGNIZED_KEY (-10)
+#define TILER_HIP_REFUSE_NOT_PREPARED (-11)
+/* Failures (post-commit; RuntimeAdapter::Failure). */
+#define TILER_HIP_FAIL_ALLOCATION 1
+#define TILER_HIP_FAIL_LAUNCH 2
+#define TILER_HIP_FAIL_DEVICE 3
+#define TILER_HIP_FAIL_GATHER_INDEX_OUT_OF_BOUNDS 4
+#define TILER_HIP_FAIL_TRANSFER 5
+
+typedef struct tiler_hip_context tiler_hip_context;
+typedef void *tiler_hip_stream; /* hipStream_t */
+typedef void *tiler_hip_event;  /* hipEvent_t */
+
+/* ------------------------------------------------------------------------
+ * Target profile (replaces the declare_* rows of
+ * tiler-compiler/src/target/builder.rs:97-1171 and the feasibility axes of
+ * target/feasibility.rs:241-256 for gfx950).  Device-free.
+ */
+typedef struct {
+    char profile_key[64];           /* "tiler.hip.gfx950.profile-v1" */
+    char target_triple[64];         /* "amdgcn-amd-amdhsa--gfx950" */
+    uint32_t wavefront_size;        /* 64 */
+    uint32_t compute_units;         /* 256 */
+    uint32_t xcds;                  /* 8 accelerator complex dies */
+    uint32_t simds_per_cu;          /* 4 */
+    uint32_t max_threads_per_workgroup;
+    uint32_t max_grid_dim[3];
+    uint64_t lds_bytes_per_workgroup; /* 163840 */
+    uint64_t device_memory_bytes;     /* 288 GB HBM3E */
+    uint64_t l2_bytes_per_xcd;
+    uint64_t infinity_cache_bytes;    /* 256 MB MALL */
+    uint32_t address_bits;            /* 64 */
+    uint32_t index_u64;               /* 1: 64-bit indexing admitted */
+    uint32_t subgroup_width;          /* 64: SubgroupRealizationSubject width */
+    uint32_t f32_subnormals_preserved;/* 1: IEEE f32 denormals kept */
+    double hbm_bytes_per_second;      /* 8.0e12 */
+    double mfma_bf16_dense_flops;     /* 2.5e15 */
+    double mfma_fp8_dense_flops;      /* 5.0e15 */
+    double vector_f32_flops;          /* 157.3e12 */
+    double vector_f64_flops;          /* 78.6e12 */
+    uint32_t parallel_threads;        /* measured-cost row: concurrent threads */
+} tiler_hip_target_profile;
+
+tiler_hip_status tiler_hip_profile_declare(tiler_hip_target_profile *out);
+
+/* ------------------------------------------------------------------------
+ * Producer seam (tiler-build/src/plan_artifact.rs:228-363 assemble_plan_artifact
+ * closures; tiler-metal-aot/src/driver.rs:61-453 Toolchain).  The gfx950 code
+ * object is compiled offline by hipcc --genco and carried in this library; the
+ * payload view describes it the way PayloadMetadata/PayloadProvenance do
+ * (tiler-artifact/src/codec/payload.rs:228-424).  Device-free.
+ */
+typedef struct {
+    const char *backend;          /* "tiler.hip" */
+    const char *representation;   /* "tiler.hip.gfx950.code-object-v1" */
+    const char *payload_schema;   /* "tiler.hip.payload.v1" */
+    const char *target;           /* "amdgcn-amd-amdhsa--gfx950" */
+    const char *toolchain;        /* compiler identity recorded at build */
+    const char *flags;            /* compile flags recorded at build */
+    const uint8_t *code;          /* code-object bytes (ELF) */
+    uint64_t code_bytes;
+    uint32_t entry_count;
+} tiler_hip_payload_view;
+
+typedef struct {
+    const char *symbol;       /* kernel symbol in the code object */
+    const char *family;       /* realization family it serves */
+    uint32_t buffer_bindings; /* device-buffer arguments, in kernel order */
+    uint32_t kernarg_bytes;   /* kernel argument segment size */
+} tiler_hip_entry_info;
+
+tiler_hip_status tiler_hip_payload(tiler_hip_payload_view *out);
+tiler_hip_status tiler_hip_payload_entry(uint32_t index, tiler_hip_entry_info *out);
+
+/* Validates a code object from its own bytes (ADR 0090 item 8;
+ * RuntimeAdapter::validate_payload, tiler-runtime/src/adapter.rs:330-345):
+ * an AMDGPU HSA ELF for gfx950 that defines `symbol` and its kernel descriptor
+ * `symbol.kd`, whose kernarg segment is `kernarg_bytes` long (0 = unchecked).
+ * Device-free. */
+tiler_hip_status tiler_hip_validate_payload(const void *code, uint64_t code_bytes,
+                                            const char *symbol, uint32_t kernarg_bytes,
+                                            char *diagnostic, uint64_t diagnostic_bytes);
+
+/* ------------------------------------------------------------------------
+ * Runtime seam: the RuntimeAdapter stages (tiler-runtime/src/adapter.rs:260-511)
+ * driven by route_with_adapter (adapter.rs:545-678).
+ */
+typedef struct {
+    int32_t device_ordinal;
+    char device_name[64];
+    char gcn_arch_name[64]; /* e.g. "gfx950:sramecc+:xnack-" */
+    uint32_t compute_units;
+    uint32_t wavefront_size;
+    uint32_t max_threads_per_workgroup;
+    uint64_t lds_bytes_per_workgroup;
+    uint64_t global_memory_bytes;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width_bits;
+    int32_t runtime_version;
+    int32_t driver_version;
+} tiler_hip_execution_environment;
+
+/* bind_execution_context (adapter.rs:297): binds device `ordinal`, creates the
+ * context's stream and workspace, loads this library's own gfx950 code object,
+ * and reports what it observed.  Refuses a device that is not gfx950. */
+tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context **out,
+                                tiler_hip_execution_environment *environment,
+                                char *diagnostic, uint64_t diagnostic_bytes);
+void tiler_hip_release(tiler_hip_context *ctx);
+const char *tiler_hip_last_diagnostic(const tiler_hip_context *ctx);
+
+/* observe_live_device (adapter.rs:372): reports, never decides.  Keys:
+ * "wavefront-size", "compute-units", "max-threads-per-workgroup",
+ * "lds-bytes-per-workgroup", "global-memory-bytes", "target-is-gfx950".
+ * Unknown keys answer TILER_HIP_REFUSE_UNRECOGNIZED_KEY (fail-closed). */
+tiler_hip_status tiler_hip_observe_live_device(tiler_hip_context *ctx, const char *key,
+                                               uint64_t *value);
+
+typedef struct {
+    const void *code;      /* code-object bytes (borrowed for the call) */
+    uint64_t code_bytes;
+    const char *symbol;
+} tiler_hip_routed_entry;
+
+/* prepare_entries (adapter.rs:401): loads each entry's code object and
+ * resolves its symbol; reversible.  Prepared entries are numbered from
+ * *first_index in order. */
+tiler_hip_status tiler_hip_prepare_entries(tiler_hip_context *ctx,
+                                           const tiler_hip_routed_entry *entries,
+                                           uint32_t count, uint32_t *first_index);
+
+/* observe_prepared_entry (adapter.rs:436): keys "max-threads-per-workgroup",
+ * "static-lds-bytes", "private-bytes-per-lane", "vgprs". */
+tiler_hip_status tiler_hip_observe_prepared_entry(tiler_hip_context *ctx, uint32_t prepared,
+                                                  const char *key, uint64_t *value);
+
+typedef struct {
+    uint32_t prepared;         /* index from tiler_hip_prepare_entries */
+    uint32_t grid[3];          /* workgroups per dimension */
+    uint32_t block[3];         /* threads per workgroup per dimension */
+    uint32_t dynamic_lds_bytes;
+    const void *kernargs;      /* packed kernel argument segment */
+    uint32_t kernarg_bytes;
+    uint32_t binding_count;    /* buffer bindings patched into kernargs */
+    const uint32_t *binding_slots;   /* slot of each binding */
+    const uint32_t *binding_offsets; /* byte offset of its pointer in kernargs */
+} tiler_hip_dispatch_entry;
+
+typedef struct {
+    uint32_t slot_count;
+    const uint64_t *slot_bytes;     /* required bytes per storage slot */
+    uint32_t entry_count;
+    const tiler_hip_dispatch_entry *entries; /* in execution order */
+} tiler_hip_dispatch_plan;
+
+/* plan_dispatch (adapter.rs:473): sizes and checks the route against the
+ * profile and the prepared entries, acquiring nothing. */
+tiler_hip_status tiler_hip_plan_dispatch(tiler_hip_context *ctx,
+                                         const tiler_hip_dispatch_plan *plan);
+/* allocate_dispatch (adapter.rs:490): post-commit program storage.  Slots
+ * whose caller pointer is non-NULL are caller-supplied and not allocated. */
+tiler_hip_status tiler_hip_allocate_dispatch(tiler_hip_context *ctx,
+                                             const tiler_hip_dispatch_plan *plan,
+                                             void **slot_pointers);
+/* dispatch (adapter.rs:511): encodes every entry in order on the context
+ * stream, submits, and waits for terminal success. */
+tiler_hip_status tiler_hip_dispatch(tiler_hip_context *ctx, const tiler_hip_dispatch_plan *plan,
+                                    void *const *slot_pointers);
+/* Releases the storage tiler_hip_allocate_dispatch acquired for the plan. */
+tiler_hip_status tiler_hip_release_dispatch(tiler_hip_context *ctx,
+                                            const tiler_hip_dispatch_plan *plan,
+                                            void **slot_pointers, const void **caller_owned);
+
+/* ------------------------------------------------------------------------
+ * Device storage, transfer, stream and timing plumbing.
+ */
+tiler_hip_status tiler_hip_buffer_alloc(tiler_hip_context *ctx, uint64_t bytes, void **out);
+tiler_hip_status tiler_hip_buffer_free(tiler_hip_context *ctx, void *ptr);
+tiler_hip_status tiler_hip_upload(tiler_hip_context *ctx, void *device_dst, const void *host_src,
+                                  uint64_t bytes);
+tiler_hip_status tiler_hip_download(tiler_hip_context *ctx, void *host_dst,
+                                    const void *device_src, uint64_t bytes);
+tiler_hip_status tiler_hip_fill_u32(tiler_hip_context *ctx, void *device_dst, uint32_t value,
+                                    uint64_t words, tiler_hip_stream stream);
+tiler_hip_status tiler_hip_synchronize(tiler_hip_context *ctx);
+tiler_hip_stream tiler_hip_context_stream(tiler_hip_context *ctx);
+tiler_hip_status tiler_hip_event_create(tiler_hip_context *ctx, tiler_hip_event *out);
+tiler_hip_status tiler_hip_event_record(tiler_hip_context *ctx, tiler_hip_event ev,
+                                        tiler_hip_stream stream);
+tiler_hip_status tiler_hip_event_elapsed_ms(tiler_hip_context *ctx, tiler_hip_event start,
+                                            tiler_hip_event stop, float *ms);
+tiler_hip_status tiler_hip_event_destroy(tiler_hip_context *ctx, tiler_hip_event ev);
+
+/* ------------------------------------------------------------------------
+ * Realization families.  Each replaces one ScalarProgram x ReductionTopology
+ * cell the planner selects (tiler-ir/src/schedule/model.rs:661-920,
+ * 1327-1555) and is checked against the tiler-reference function cited.
+ */
+
+/* Sum over the last axis of a dense [rows, extent] f32 tensor
+ * (strict-serial-sum-f32@1; tiler-reference/src/evaluate.rs:498-589). */
+#define TILER_HIP_SUM_TREE 0        /* reassociating two-level tree (declared grouping) */
+#define TILER_HIP_SUM_SERIAL 1      /* ReductionTopology::Serial, bit-exact strict_sum */
+#define TILER_HIP_SUM_MULTIPASS 2   /* ::MultiPass, bit-exact strict_partitioned_sum
+                                       (evaluate.rs:788-832) */
+#define TILER_HIP_SUM_COOPERATIVE 3 /* ::CooperativeWorkgroup, bit-exact
+                                       cooperative_grouped_sum (evaluate.rs:845-1158) */
+typedef struct {
+    uint32_t topology;
+    uint32_t participant_major; /* cooperative layout: 0 RoundMajor, 1 ParticipantMajor */
+    uint64_t partitions;        /* multipass */
+    uint64_t participants;      /* cooperative (<= 1024) */
+    uint64_t per_partition;     /* multipass / cooperative contributors per cell */
+    uint64_t rounds;            /* cooperative */
+} tiler_hip_sum_plan;
+
+tiler_hip_status tiler_hip_sum_f32(tiler_hip_context *ctx, const float *x, uint64_t rows,
+                                   uint64_t extent, float *out, const tiler_hip_sum_plan *plan,
+                                   tiler_hip_stream stream);
+/* Workgroups the single-output tree uses for n contributors (its grouping). */
+uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context *ctx, uint64_t n);
+
+/* RMS normalization over the last axis (rms-norm-f32@1;
+ * tiler-reference/src/rms_norm.rs:405-489).  dtype: TILER_HIP_F32 or
+ * TILER_HIP_BF16 (binary32 arithmetic on exactly widened operands, one
+ * narrowing of y).  weight_broadcast != 0: w is one row of `extent` shared by
+ * every row; otherwise w has the input's shape (the reference's form). */
+#define TILER_HIP_F32 0
+#define TILER_HIP_BF16 1
+tiler_hip_status tiler_hip_rms_norm(tiler_hip_context *ctx, uint32_t dtype, const void *x,
+                                    const void *w, int32_t weight_broadcast, uint64_t rows,
+                                    uint64_t extent, uint32_t eps_bits, void *y,
+                                    tiler_hip_stream stream);
+
+/* Softmax over the last axis with the governed-maximum shift (softmax-f32@1;
+ * tiler-reference/src/softmax.rs:200-315). */
+tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context *ctx, const float *x, uint64_t rows,
+                                       uint64_t extent, float *y, tiler_hip_stream stream);
+
+/* Pointwise maps (tiler-reference/src/evaluate.rs:448-485; silu.rs:511-533).
+ * op: 0 scale-bias y = x*a + b, 1 SiLU, 2 add x + x2, 3 multiply x * x2.
+ * x2_broadcast != 0 reads x2 as a rank-0 operand. */
+#define TILER_HIP_MAP_SCALE_BIAS 0
+#define TILER_HIP_MAP_SILU 1
+#define TILER_HIP_MAP_ADD 2
+#define TILER_HIP_MAP_MULTIPLY 3
+tiler_hip_status tiler_hip_map(tiler_hip_context *ctx, uint32_t op, uint32_t dtype,
+                               const void *x, const void *x2, int32_t x2_broadcast, uint64_t n,
+                               float a, float b, void *y, tiler_hip_stream stream);
+
+/* Broadcast / reindex move (broadcast-f32@2; tiler-reference/src/structural.rs:75-108):
+ * out (row-major over out_dims) element reads source offset
+ * sum coord_d * src_strides[d] (elements; stride 0 broadcasts). rank <= 8;
+ * element_bytes 2 or 4. */
+tiler_hip_status tiler_hip_broadcast(tiler_hip_context *ctx, const void *src, uint32_t rank,
+                                     const uint64_t *out_dims, const uint64_t *src_strides,
+                                     uint32_t element_bytes, void *out, tiler_hip_stream stream);
+
+/* Gather (gather-f32@1; tiler-reference/src/structural.rs:513-606, bound rule
+ * tiler-ir/src/semantic/gather.rs:438-455): source [outer, gathered, inner] of
+ * element_bytes elements, 32-bit index (index_signed: int32, else uint32),
+ * output [outer, index_count, inner].  Byte moves only.  An out-of-range index
+ * is never clamped or wrapped: its run is not written and the lowest offending
+ * position is recorded for tiler_hip_gather_status. */
+tiler_hip_status tiler_hip_gather(tiler_hip_context *ctx, const void *source, uint64_t outer,
+                                  uint64_t gathered, uint64_t inner, uint32_t element_bytes,
+                                  const uint32_t *index, uint64_t index_count,
+                                  int32_t index_signed, void *out, tiler_hip_stream stream);
+/* Waits for the stream and reports the gathers since the last call:
+ * TILER_HIP_OK, or TILER_HIP_FAIL_GATHER_INDEX_OUT_OF_BOUNDS with the lowest
+ * offending position.  Re-arms the record. */
+tiler_hip_status tiler_hip_gather_status(tiler_hip_context *ctx, tiler_hip_stream stream,
+                                         uint64_t *bad_position);
+/* Pre-commit form of the same bound rule for host-resident indices:
+ * TILER_HIP_REFUSE_GATHER_INDEX_OUT_OF_BOUNDS naming the first position. */
+tiler_hip_status tiler_hip_validate_gather_index(const uint32_t *index, uint64_t index_count,
+                                                 int32_t index_signed, uint64_t gathered,
+                                                 uint64_t *bad_position, int64_t *bad_value);
+
+/* Contraction td,od->to: C[m, n] = sum_k A[m, k] * B[n, k]
+ * (tensor-contraction-f32@1; tiler-reference/src/contraction.rs:297-630). */
+/* Strict f32: bit-exact with the reference's fold (first-product seed, no FMA). */
+tiler_hip_status tiler_hip_contract_strict_f32(tiler_hip_context *ctx, const float *a,
+                                               const float *b, uint64_t m, uint64_t n,
+                                               uint64_t k, float *c, tiler_hip_stream stream);
+/* Cooperative bf16 on MFMA: bf16 operands, f32 accumulation, optional fused
+ * SiLU on the accumulator, one bf16 narrowing of C. */
+#define TILER_HIP_EPILOGUE_NONE 0
+#define TILER_HIP_EPILOGUE_SILU 1
+tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context *ctx, const uint16_t *a,
+                                         const uint16_t *b, uint64_t m, uint64_t n, uint64_t k,
+                                         uint16_t *c, uint32_t epilogue,
+                                         tiler_hip_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILER_HIP_H */

@@ -1,0 +1,310 @@
+"""CPU restatement of ``tiler-reference`` for the tiler-hip hot path.
+
+TEST INFRASTRUCTURE ONLY. This package is the parity checker: only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it. The product (``libtiler_hip.so`` and the ``tiler_amd`` package) never
+imports, links or executes anything here.
+
+The reference (``/root/reference/crates/tiler-reference``) is Rust and no Rust
+toolchain exists in this image, so ``oracle/_ref`` is never built; the
+restatement in ``tiler_oracle.c`` is pinned by the reference's own golden
+vectors (``tests/golden``) and by independent mathematical checks (see the
+header of ``tiler_oracle.c`` for which check pins which function).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+BUILD_DIR = os.path.join(HERE, "_build")
+LIB_PATH = os.path.join(BUILD_DIR, "libtiler_oracle.so")
+
+OK = 0
+INVALID_APPLICATION = 1
+UNDECIDED = 2
+GATHER_INDEX_OUT_OF_BOUNDS = 3
+
+PRESERVE = 0
+FLUSH_SIGN_PRESERVING = 1
+FLUSH_POSITIVE_ZERO = 2
+
+ROUND_MAJOR = 0
+PARTICIPANT_MAJOR = 1
+
+CANONICAL_F32_NAN = 0x7FC00000
+
+
+class OracleError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"{what}: oracle status {status}")
+        self.status = status
+
+
+def build() -> str:
+    """Compiles the restatement with strict binary32 arithmetic (no FMA)."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    cmd = [
+        "gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
+        "-Wall", "-o", LIB_PATH + ".tmp", os.path.join(HERE, "tiler_oracle.c"),
+        "-lquadmath", "-lm", "-lpthread",
+    ]
+    subprocess.run(cmd, check=True)
+    os.replace(LIB_PATH + ".tmp", LIB_PATH)
+    return LIB_PATH
+
+
+_lib = None
+
+_P = ctypes.c_void_p
+_U64 = ctypes.c_uint64
+_U32 = ctypes.c_uint32
+_I32 = ctypes.c_int32
+_SIGS = {
+    "tiler_oracle_canonical_nan_bits": (_U32, []),
+    "tiler_oracle_apply_subnormal_mode": (ctypes.c_float, [_I32, ctypes.c_float]),
+    "tiler_oracle_maximum_f32": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+    "tiler_oracle_bf16_narrow": (ctypes.c_uint16, [ctypes.c_float]),
+    "tiler_oracle_bf16_widen": (ctypes.c_float, [ctypes.c_uint16]),
+    "tiler_oracle_bf16_narrow_array": (None, [_P, _U64, _P]),
+    "tiler_oracle_bf16_widen_array": (None, [_P, _U64, _P]),
+    "tiler_oracle_strict_sum_f32": (_I32, [_P, _U64, _U64, _U64, _P, _I32, _I32]),
+    "tiler_oracle_strict_partial_sums_f32": (_I32, [_P, _U64, _U64, _U64, _U64, _P, _I32, _I32]),
+    "tiler_oracle_strict_partitioned_sum_f32": (_I32, [_P, _U64, _U64, _U64, _U64, _P, _I32, _I32]),
+    "tiler_oracle_cooperative_grouped_sum_f32": (
+        _I32, [_P, _U64, _U64, _U64, _U64, _U64, _I32, _P, _I32, _I32]),
+    "tiler_oracle_certified_exp_f32": (_I32, [ctypes.c_float, _P]),
+    "tiler_oracle_certified_rsqrt_f32": (_I32, [ctypes.c_float, _P]),
+    "tiler_oracle_silu_f32": (_I32, [_P, _U64, _P, _I32, _I32]),
+    "tiler_oracle_softmax_f32": (_I32, [_P, _U64, _U64, _U64, _P, _I32, _I32]),
+    "tiler_oracle_rms_norm_f32": (_I32, [_P, _P, _U64, _U64, _U64, _U32, _P, _I32, _I32]),
+    "tiler_oracle_gather": (_I32, [_P, _U64, _U64, _U64, _U32, _P, _U64, _I32, _P, _P, _P]),
+    "tiler_oracle_contract_strict_f32": (_I32, [_P, _P, _U64, _U64, _U64, _P, _U64, _U64, _U32]),
+    "tiler_oracle_row_grouped_sum_f32": (_I32, [_P, _U64, _U64, _U32, _U32, _P]),
+    "tiler_oracle_grid_tree_sum_f32": (_I32, [_P, _U64, _U32, _P]),
+    "tiler_oracle_rms_norm_grouped_f32": (_I32, [_P, _P, _U64, _U64, _U32, _I32, _U32, _U32, _P]),
+    "tiler_oracle_softmax_grouped_f32": (_I32, [_P, _U64, _U64, _U32, _U32, _P]),
+}
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _check(st: int, what: str):
+    if st != OK:
+        raise OracleError(st, what)
+
+
+def f32_from_bits(bits) -> np.ndarray:
+    return np.asarray(bits, dtype=np.uint32).view(np.float32)
+
+
+def bits_of(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32)).view(np.uint32)
+
+
+# --- scalar helpers ----------------------------------------------------------
+
+def maximum_f32(a: float, b: float) -> float:
+    return lib().tiler_oracle_maximum_f32(a, b)
+
+
+def certified_exp_f32(x: float) -> float:
+    out = np.zeros(1, np.float32)
+    _check(lib().tiler_oracle_certified_exp_f32(float(np.float32(x)), _ptr(out)), "certified_exp_f32")
+    return out[0]
+
+
+def certified_rsqrt_f32(x: float) -> float:
+    out = np.zeros(1, np.float32)
+    _check(lib().tiler_oracle_certified_rsqrt_f32(float(np.float32(x)), _ptr(out)),
+           "certified_rsqrt_f32")
+    return out[0]
+
+
+def bf16_narrow(a) -> np.ndarray:
+    a = _f32(a)
+    out = np.empty(a.shape, np.uint16)
+    lib().tiler_oracle_bf16_narrow_array(_ptr(a), a.size, _ptr(out))
+    return out
+
+
+def bf16_widen(a) -> np.ndarray:
+    a = np.ascontiguousarray(np.asarray(a, dtype=np.uint16))
+    out = np.empty(a.shape, np.float32)
+    lib().tiler_oracle_bf16_widen_array(_ptr(a), a.size, _ptr(out))
+    return out
+
+
+# --- families ----------------------------------------------------------------
+
+def _geometry(shape, axis):
+    shape = tuple(int(s) for s in shape)
+    if not 0 <= axis < len(shape):
+        raise OracleError(INVALID_APPLICATION, "axis outside the shape")
+    outer = int(np.prod(shape[:axis], dtype=np.int64)) if axis else 1
+    inner = int(np.prod(shape[axis + 1:], dtype=np.int64)) if axis + 1 < len(shape) else 1
+    return outer, shape[axis], inner
+
+
+def strict_sum(values, shape, axis, input_mode=PRESERVE, result_mode=PRESERVE) -> np.ndarray:
+    x = _f32(values).reshape(-1)
+    outer, extent, inner = _geometry(shape, axis)
+    if x.size != outer * extent * inner:
+        raise OracleError(INVALID_APPLICATION, "payload length")
+    out = np.empty(outer * inner, np.float32)
+    _check(lib().tiler_oracle_strict_sum_f32(_ptr(x), outer, extent, inner, _ptr(out),
+                                             input_mode, result_mode), "strict_sum")
+    return out
+
+
+def strict_partial_sums(values, rows, extent, partitions, per_partition,
+                        input_mode=PRESERVE, result_mode=PRESERVE) -> np.ndarray:
+    x = _f32(values).reshape(-1)
+    out = np.empty(rows * partitions, np.float32)
+    _check(lib().tiler_oracle_strict_partial_sums_f32(_ptr(x), rows, extent, partitions,
+                                                      per_partition, _ptr(out), input_mode,
+                                                      result_mode), "strict_partial_sums")
+    return out
+
+
+def strict_partitioned_sum(values, rows, extent, partitions, per_partition,
+                           input_mode=PRESERVE, result_mode=PRESERVE) -> np.ndarray:
+    x = _f32(values).reshape(-1)
+    out = np.empty(rows, np.float32)
+    _check(lib().tiler_oracle_strict_partitioned_sum_f32(_ptr(x), rows, extent, partitions,
+                                                         per_partition, _ptr(out), input_mode,
+                                                         result_mode), "strict_partitioned_sum")
+    return out
+
+
+def cooperative_grouped_sum(values, rows, extent, participants, per_partition, rounds,
+                            layout=ROUND_MAJOR, input_mode=PRESERVE,
+                            result_mode=PRESERVE) -> np.ndarray:
+    x = _f32(values).reshape(-1)
+    out = np.empty(rows, np.float32)
+    _check(lib().tiler_oracle_cooperative_grouped_sum_f32(
+        _ptr(x), rows, extent, participants, per_partition, rounds, layout, _ptr(out),
+        input_mode, result_mode), "cooperative_grouped_sum")
+    return out
+
+
+def silu_f32(values, input_mode=PRESERVE, result_mode=PRESERVE) -> np.ndarray:
+    x = _f32(values)
+    out = np.empty(x.shape, np.float32)
+    _check(lib().tiler_oracle_silu_f32(_ptr(x), x.size, _ptr(out), input_mode, result_mode),
+           "silu_f32")
+    return out
+
+
+def softmax_f32(values, shape, axis, input_mode=PRESERVE, result_mode=PRESERVE) -> np.ndarray:
+    x = _f32(values).reshape(-1)
+    outer, extent, inner = _geometry(shape, axis)
+    if x.size != outer * extent * inner:
+        raise OracleError(INVALID_APPLICATION, "payload length")
+    out = np.empty(x.size, np.float32)
+    _check(lib().tiler_oracle_softmax_f32(_ptr(x), outer, extent, inner, _ptr(out), input_mode,
+                                          result_mode), "softmax_f32")
+    return out
+
+
+def rms_norm_f32(values, weights, shape, axis, eps_bits, input_mode=PRESERVE,
+                 result_mode=PRESERVE) -> np.ndarray:
+    x = _f32(values).reshape(-1)
+    w = _f32(weights).reshape(-1)
+    outer, extent, inner = _geometry(shape, axis)
+    if x.size != outer * extent * inner or w.size != x.size:
+        raise OracleError(INVALID_APPLICATION, "payload length")
+    out = np.empty(x.size, np.float32)
+    _check(lib().tiler_oracle_rms_norm_f32(_ptr(x), _ptr(w), outer, extent, inner, eps_bits,
+                                           _ptr(out), input_mode, result_mode), "rms_norm_f32")
+    return out
+
+
+def gather(source: np.ndarray, outer: int, gathered: int, inner: int, index,
+           index_signed: bool = False):
+    """Byte-exact gather; returns (output bytes, None) or (None, (position, value))."""
+    src = np.ascontiguousarray(source)
+    elem = src.dtype.itemsize
+    idx = np.ascontiguousarray(np.asarray(index).astype(np.int64).astype(np.uint32)
+                               if np.asarray(index).dtype != np.uint32 else np.asarray(index))
+    count = idx.size
+    out = np.empty(outer * count * inner, src.dtype)
+    pos = ctypes.c_uint64(0)
+    val = ctypes.c_int64(0)
+    st = lib().tiler_oracle_gather(_ptr(src), outer, gathered, inner, elem, _ptr(idx), count,
+                                   1 if index_signed else 0, _ptr(out), ctypes.byref(pos),
+                                   ctypes.byref(val))
+    if st == GATHER_INDEX_OUT_OF_BOUNDS:
+        return None, (pos.value, val.value)
+    _check(st, "gather")
+    return out, None
+
+
+def contract_strict_f32(a, b, m, n, k, row_begin=0, row_end=None, threads=None) -> np.ndarray:
+    """``td,od->to``: C[m, n] from A[m, k] and B[n, k]; rows [row_begin, row_end)."""
+    a = _f32(a).reshape(-1)
+    b = _f32(b).reshape(-1)
+    row_end = m if row_end is None else row_end
+    c = np.zeros(m * n, np.float32)
+    threads = threads or max(1, min(os.cpu_count() or 1, 16))
+    _check(lib().tiler_oracle_contract_strict_f32(_ptr(a), _ptr(b), m, n, k, _ptr(c), row_begin,
+                                                  row_end, threads), "contract_strict_f32")
+    return c.reshape(m, n)
+
+
+def row_grouped_sum(contributors, rows, extent, vec, waves) -> np.ndarray:
+    x = _f32(contributors).reshape(-1)
+    out = np.empty(rows, np.float32)
+    _check(lib().tiler_oracle_row_grouped_sum_f32(_ptr(x), rows, extent, vec, waves, _ptr(out)),
+           "row_grouped_sum")
+    return out
+
+
+def grid_tree_sum(values, blocks) -> float:
+    x = _f32(values).reshape(-1)
+    out = np.empty(1, np.float32)
+    _check(lib().tiler_oracle_grid_tree_sum_f32(_ptr(x), x.size, blocks, _ptr(out)),
+           "grid_tree_sum")
+    return out[0]
+
+
+def rms_norm_grouped(values, weights, rows, extent, eps_bits, weight_broadcast, vec,
+                     waves) -> np.ndarray:
+    x = _f32(values).reshape(-1)
+    w = _f32(weights).reshape(-1)
+    out = np.empty(rows * extent, np.float32)
+    _check(lib().tiler_oracle_rms_norm_grouped_f32(_ptr(x), _ptr(w), rows, extent, eps_bits,
+                                                   1 if weight_broadcast else 0, vec, waves,
+                                                   _ptr(out)), "rms_norm_grouped")
+    return out
+
+
+def softmax_grouped(values, rows, extent, vec, waves) -> np.ndarray:
+    x = _f32(values).reshape(-1)
+    out = np.empty(rows * extent, np.float32)
+    _check(lib().tiler_oracle_softmax_grouped_f32(_ptr(x), rows, extent, vec, waves, _ptr(out)),
+           "softmax_grouped")
+    return out

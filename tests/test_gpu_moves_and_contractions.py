@@ -1,0 +1,226 @@
+"""GPU parity: pointwise maps, broadcast, gather and both contractions.
+
+Gather and broadcast are byte moves and must be bit-exact; the strict f32
+contraction must reproduce the reference's own device digests; the bf16 MFMA
+contraction is held to the north-star 1e-2 relative Frobenius error against
+the strict f32 fold of the same (exactly widened) operands.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import tiler_amd
+from helpers import (bits, bf16_widen, f32, golden, hexbits, sha256_le_f32, splitmix_operands)
+from tiler_amd import _lib as L
+from tiler_amd import families
+
+pytestmark = pytest.mark.gpu
+G = golden()
+
+
+# -- maps -------------------------------------------------------------------------------
+
+def test_silu_boundary_corpus_on_device(ctx):
+    corpus = G["silu"]["corpus"]
+    y = families.silu_f32(f32([a for a, _ in corpus]), ctx=ctx)
+    assert [int(v) for v in bits(y)] == [hexbits(b) for _, b in corpus]
+
+
+def test_silu_random_matches_oracle(ctx):
+    x = (np.random.default_rng(41).standard_normal(100000) * 20).astype(np.float32)
+    got = families.silu_f32(x, ctx=ctx)
+    assert np.array_equal(bits(got), bits(oracle.silu_f32(x)))
+
+
+def _map(ctx, op, dtype, x, x2=None, bcast=False, a=0.0, b=0.0):
+    dx = ctx.to_device(x)
+    d2 = ctx.to_device(x2) if x2 is not None else None
+    dy = ctx.alloc(x.nbytes)
+    try:
+        ctx.map(op, dtype, dx, x.size, dy, x2=d2, x2_broadcast=bcast, a=a, b=b)
+        ctx.synchronize()
+        return dy.download(x.dtype, x.shape)
+    finally:
+        dx.free(); dy.free()
+        if d2 is not None:
+            d2.free()
+
+
+def _canon(a):
+    a = np.asarray(a, np.float32)
+    return np.where(np.isnan(a), f32(["0x7fc00000"])[0], a).astype(np.float32)
+
+
+def test_scale_bias_and_binary_maps(ctx):
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal(7777).astype(np.float32)
+    x[:4] = f32(["0x7fc01234", "0x7f800000", "0x00000001", "0x80000000"])
+    y = _map(ctx, L.MAP_SCALE_BIAS, L.F32, x, a=2.0, b=1.0)
+    want = _canon((x * np.float32(2.0)).astype(np.float32) + np.float32(1.0))
+    assert np.array_equal(bits(y), bits(want))
+    x2 = rng.standard_normal(7777).astype(np.float32)
+    assert np.array_equal(bits(_map(ctx, L.MAP_ADD, L.F32, x, x2)), bits(_canon(x + x2)))
+    s = np.asarray([3.0], np.float32)
+    got = _map(ctx, L.MAP_MULTIPLY, L.F32, x, s, bcast=True)
+    assert np.array_equal(bits(got), bits(_canon(x * s[0])))
+
+
+def test_bf16_maps_round_once_per_operation(ctx):
+    rng = np.random.default_rng(43)
+    xb = oracle.bf16_narrow(rng.standard_normal(5000).astype(np.float32))
+    yb = _map(ctx, L.MAP_SCALE_BIAS, L.BF16, xb, a=2.0, b=1.0)
+    t = oracle.bf16_narrow(bf16_widen(xb) * np.float32(2.0))
+    want = oracle.bf16_narrow(bf16_widen(t) + np.float32(1.0))
+    assert np.array_equal(yb, want)
+    x2 = oracle.bf16_narrow(rng.standard_normal(5000).astype(np.float32))
+    got = _map(ctx, L.MAP_ADD, L.BF16, xb, x2)
+    assert np.array_equal(got, oracle.bf16_narrow(bf16_widen(xb) + bf16_widen(x2)))
+
+
+def test_broadcast_moves_bytes(ctx):
+    src = np.arange(6, dtype=np.float32).reshape(2, 3)
+    src[0, 0] = f32(["0x7fc01234"])[0]
+    ds = ctx.to_device(src)
+    do = ctx.alloc(4 * 2 * 3 * 4)
+    try:
+        ctx.broadcast(ds, [4, 2, 3], [0, 3, 1], 4, do)
+        ctx.synchronize()
+        got = do.download(np.uint32, (4, 2, 3))
+    finally:
+        ds.free(); do.free()
+    assert np.array_equal(got, np.broadcast_to(bits(src), (4, 2, 3)))
+
+
+# -- gather -------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", G["gather"]["cases"], ids=lambda c: c["name"])
+def test_gather_golden_on_device(ctx, case):
+    shape = tuple(case["source_shape"])
+    src = np.arange(int(np.prod(shape)), dtype=np.uint32).reshape(shape)
+    idx = np.asarray(case["index"], np.uint32).reshape(case["index_shape"])
+    got = families.gather(src, case["axis"], idx, ctx=ctx)
+    assert list(got.shape) == case["result_shape"]
+    assert got.reshape(-1).tolist() == case["result"]
+
+
+def test_gather_refuses_before_commit_naming_position(ctx):
+    src = np.arange(15, dtype=np.uint32).reshape(5, 3)
+    for ref in G["gather"]["refusals"]:
+        with pytest.raises(tiler_amd.GatherIndexOutOfBounds) as err:
+            families.gather(src, 0, np.asarray(ref["index"], np.uint32), ctx=ctx)
+        assert err.value.position == ref["position"] and err.value.value == ref["value"]
+        assert err.value.fallback_permitted
+
+
+def test_gather_device_bound_check_reports_lowest_position(ctx):
+    """An index that reaches the device unvalidated is not clamped or wrapped:
+    its run is not written and the committed dispatch fails naming it."""
+    src = np.arange(15, dtype=np.uint32)
+    idx = np.asarray([1, 7, 2, 5, 0], np.uint32)
+    ds, di = ctx.to_device(src), ctx.to_device(idx)
+    do = ctx.alloc(5 * 3 * 4)
+    try:
+        ctx.fill_u32(do, 0xDEADBEEF, 15)
+        ctx.gather(ds, 1, 5, 3, 4, di, 5, do)
+        with pytest.raises(tiler_amd.GatherIndexOutOfBounds) as err:
+            ctx.gather_status()
+        assert err.value.position == 1 and not err.value.fallback_permitted
+        got = do.download(np.uint32, (5, 3))
+        assert got[0].tolist() == [3, 4, 5] and got[2].tolist() == [6, 7, 8]
+        assert got[1].tolist() == [0xDEADBEEF] * 3 and got[3].tolist() == [0xDEADBEEF] * 3
+        ctx.gather_status()  # the record re-armed
+        sidx = np.asarray([0, -3], np.int32).view(np.uint32)
+        di2 = ctx.to_device(sidx)
+        ctx.gather(ds, 1, 5, 3, 4, di2, 2, do, index_signed=True)
+        with pytest.raises(tiler_amd.GatherIndexOutOfBounds) as err:
+            ctx.gather_status()
+        assert err.value.position == 1
+        di2.free()
+    finally:
+        ds.free(); di.free(); do.free()
+
+
+def test_gather_preserves_every_payload(ctx):
+    p = G["gather"]["payloads"]
+    src = np.asarray([hexbits(b) for b in p["source_bits"]], np.uint32)
+    got = families.gather(src, 0, np.asarray(p["index"], np.uint32), ctx=ctx)
+    assert [int(v) for v in got] == [hexbits(b) for b in p["result_bits"]]
+
+
+@pytest.mark.parametrize("dtype,inner", [(np.uint16, 4096), (np.uint16, 7), (np.uint8, 33), (np.uint32, 12)])
+def test_gather_ragged_runs_match_oracle(ctx, dtype, inner):
+    rng = np.random.default_rng(inner)
+    src = rng.integers(0, np.iinfo(dtype).max, (3, 50, inner), dtype=dtype)
+    idx = rng.integers(0, 50, 77).astype(np.int32)
+    got = families.gather(src, 1, idx, index_signed=True, ctx=ctx)
+    want, err = oracle.gather(src.reshape(-1), 3, 50, inner, idx.view(np.uint32), index_signed=True)
+    assert err is None and np.array_equal(got.reshape(-1), want)
+
+
+def test_gather_full_size_config(ctx):
+    """C4: bf16 table [128256 x 4096] ~ N(0, 0.02), int32 indices [16384]
+    ~ U[0, 128256): bit-exact."""
+    vocab, hidden, count = 128256, 4096, 16384
+    rng = np.random.default_rng(4)
+    table = oracle.bf16_narrow((rng.standard_normal((vocab, hidden), dtype=np.float32) * np.float32(0.02)))
+    idx = rng.integers(0, vocab, count).astype(np.int32)
+    got = families.gather(table, 0, idx, index_signed=True, ctx=ctx)
+    assert np.array_equal(got, table[idx])
+
+
+# -- contractions -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cell", G["contraction"]["cells"], ids=lambda c: c["id"])
+def test_strict_contraction_reproduces_reference_digests_on_device(ctx, cell):
+    seed = hexbits(G["contraction"]["workload_seed"])
+    mask = hexbits(G["contraction"]["right_seed_mask"])
+    a = splitmix_operands(seed, cell["m"] * cell["k"]).reshape(cell["m"], cell["k"])
+    b = splitmix_operands(seed ^ mask, cell["n"] * cell["k"]).reshape(cell["n"], cell["k"])
+    c = families.contract_strict_f32(a, b, ctx=ctx)
+    assert sha256_le_f32(c) == cell["sha256"]
+
+
+def test_strict_contraction_tails_and_signed_zero(ctx):
+    rng = np.random.default_rng(51)
+    a = rng.standard_normal((19, 37)).astype(np.float32)
+    b = rng.standard_normal((23, 37)).astype(np.float32)
+    got = families.contract_strict_f32(a, b, ctx=ctx)
+    assert np.array_equal(bits(got), bits(oracle.contract_strict_f32(a, b, 19, 23, 37)))
+    z = families.contract_strict_f32(np.asarray([[-0.0]], np.float32), np.asarray([[1.0]], np.float32), ctx=ctx)
+    assert bits(z)[0, 0] == 0x80000000
+
+
+def _frob(got_bits, ref32):
+    g = bf16_widen(got_bits).astype(np.float64)
+    r = np.asarray(ref32, np.float64)
+    return float(np.linalg.norm(g - r) / np.linalg.norm(r))
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (256, 384, 512), (200, 136, 72), (77, 45, 13), (1, 300, 1000)])
+@pytest.mark.parametrize("silu", [False, True])
+def test_bf16_contraction_within_frobenius_bound(ctx, m, n, k, silu):
+    rng = np.random.default_rng(m * n + k)
+    ab = oracle.bf16_narrow((rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32))
+    bb = oracle.bf16_narrow((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
+    got = families.contract_bf16(ab, bb, L.EPILOGUE_SILU if silu else L.EPILOGUE_NONE, ctx=ctx)
+    ref = oracle.contract_strict_f32(bf16_widen(ab), bf16_widen(bb), m, n, k)
+    if silu:
+        ref = oracle.silu_f32(ref).reshape(m, n)
+    assert _frob(got, ref) <= 1e-2
+
+
+def test_bf16_contraction_full_size_config(ctx):
+    """C5: bf16 A, B [4096 x 4096] ~ N(0, 1/sqrt(4096)), f32 accumulation,
+    fused SiLU, bf16 C: relative Frobenius error <= 1e-2 against the strict
+    f32 reference on a sample of 64 rows (rows are independent outputs)."""
+    m = n = k = 4096
+    rng = np.random.default_rng(5)
+    ab = oracle.bf16_narrow((rng.standard_normal((m, k), dtype=np.float32) / np.float32(64.0)))
+    bb = oracle.bf16_narrow((rng.standard_normal((n, k), dtype=np.float32) / np.float32(64.0)))
+    got = families.contract_bf16(ab, bb, L.EPILOGUE_SILU, ctx=ctx)
+    rows = np.arange(0, m, m // 64)
+    ref = oracle.contract_strict_f32(bf16_widen(ab[rows]), bf16_widen(bb), rows.size, n, k)
+    ref = oracle.silu_f32(ref).reshape(rows.size, n)
+    assert _frob(got[rows], ref) <= 1e-2

@@ -1,0 +1,233 @@
+"""ctypes binding of libtiler_hip.so (the C ABI in include/tiler_hip.h).
+
+The library is built ahead of time (``python -m tiler_amd.build``) and loaded
+from ``tiler_amd/_build``.  There is no fallback: if the library is missing
+every entry point raises, so nothing can silently run on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "libtiler_hip.so")
+
+OK = 0
+REFUSE_NO_DEVICE = -1
+REFUSE_FOREIGN_TARGET = -2
+REFUSE_INVALID_ARGUMENT = -3
+REFUSE_MALFORMED_PAYLOAD = -4
+REFUSE_ABSENT_SYMBOL = -5
+REFUSE_BINDING_MISMATCH = -6
+REFUSE_CAPACITY = -7
+REFUSE_UNSUPPORTED = -8
+REFUSE_GATHER_INDEX_OUT_OF_BOUNDS = -9
+REFUSE_UNRECOGNIZED_KEY = -10
+REFUSE_NOT_PREPARED = -11
+FAIL_ALLOCATION = 1
+FAIL_LAUNCH = 2
+FAIL_DEVICE = 3
+FAIL_GATHER_INDEX_OUT_OF_BOUNDS = 4
+FAIL_TRANSFER = 5
+
+F32 = 0
+BF16 = 1
+
+SUM_TREE = 0
+SUM_SERIAL = 1
+SUM_MULTIPASS = 2
+SUM_COOPERATIVE = 3
+
+MAP_SCALE_BIAS = 0
+MAP_SILU = 1
+MAP_ADD = 2
+MAP_MULTIPLY = 3
+
+EPILOGUE_NONE = 0
+EPILOGUE_SILU = 1
+
+
+class TargetProfile(ctypes.Structure):
+    _fields_ = [
+        ("profile_key", ctypes.c_char * 64),
+        ("target_triple", ctypes.c_char * 64),
+        ("wavefront_size", ctypes.c_uint32),
+        ("compute_units", ctypes.c_uint32),
+        ("xcds", ctypes.c_uint32),
+        ("simds_per_cu", ctypes.c_uint32),
+        ("max_threads_per_workgroup", ctypes.c_uint32),
+        ("max_grid_dim", ctypes.c_uint32 * 3),
+        ("lds_bytes_per_workgroup", ctypes.c_uint64),
+        ("device_memory_bytes", ctypes.c_uint64),
+        ("l2_bytes_per_xcd", ctypes.c_uint64),
+        ("infinity_cache_bytes", ctypes.c_uint64),
+        ("address_bits", ctypes.c_uint32),
+        ("index_u64", ctypes.c_uint32),
+        ("subgroup_width", ctypes.c_uint32),
+        ("f32_subnormals_preserved", ctypes.c_uint32),
+        ("hbm_bytes_per_second", ctypes.c_double),
+        ("mfma_bf16_dense_flops", ctypes.c_double),
+        ("mfma_fp8_dense_flops", ctypes.c_double),
+        ("vector_f32_flops", ctypes.c_double),
+        ("vector_f64_flops", ctypes.c_double),
+        ("parallel_threads", ctypes.c_uint32),
+    ]
+
+
+class PayloadView(ctypes.Structure):
+    _fields_ = [
+        ("backend", ctypes.c_char_p),
+        ("representation", ctypes.c_char_p),
+        ("payload_schema", ctypes.c_char_p),
+        ("target", ctypes.c_char_p),
+        ("toolchain", ctypes.c_char_p),
+        ("flags", ctypes.c_char_p),
+        ("code", ctypes.c_void_p),
+        ("code_bytes", ctypes.c_uint64),
+        ("entry_count", ctypes.c_uint32),
+    ]
+
+
+class EntryInfo(ctypes.Structure):
+    _fields_ = [
+        ("symbol", ctypes.c_char_p),
+        ("family", ctypes.c_char_p),
+        ("buffer_bindings", ctypes.c_uint32),
+        ("kernarg_bytes", ctypes.c_uint32),
+    ]
+
+
+class ExecutionEnvironment(ctypes.Structure):
+    _fields_ = [
+        ("device_ordinal", ctypes.c_int32),
+        ("device_name", ctypes.c_char * 64),
+        ("gcn_arch_name", ctypes.c_char * 64),
+        ("compute_units", ctypes.c_uint32),
+        ("wavefront_size", ctypes.c_uint32),
+        ("max_threads_per_workgroup", ctypes.c_uint32),
+        ("lds_bytes_per_workgroup", ctypes.c_uint64),
+        ("global_memory_bytes", ctypes.c_uint64),
+        ("clock_khz", ctypes.c_int32),
+        ("memory_clock_khz", ctypes.c_int32),
+        ("memory_bus_width_bits", ctypes.c_int32),
+        ("runtime_version", ctypes.c_int32),
+        ("driver_version", ctypes.c_int32),
+    ]
+
+
+class RoutedEntry(ctypes.Structure):
+    _fields_ = [
+        ("code", ctypes.c_void_p),
+        ("code_bytes", ctypes.c_uint64),
+        ("symbol", ctypes.c_char_p),
+    ]
+
+
+class DispatchEntry(ctypes.Structure):
+    _fields_ = [
+        ("prepared", ctypes.c_uint32),
+        ("grid", ctypes.c_uint32 * 3),
+        ("block", ctypes.c_uint32 * 3),
+        ("dynamic_lds_bytes", ctypes.c_uint32),
+        ("kernargs", ctypes.c_void_p),
+        ("kernarg_bytes", ctypes.c_uint32),
+        ("binding_count", ctypes.c_uint32),
+        ("binding_slots", ctypes.POINTER(ctypes.c_uint32)),
+        ("binding_offsets", ctypes.POINTER(ctypes.c_uint32)),
+    ]
+
+
+class DispatchPlan(ctypes.Structure):
+    _fields_ = [
+        ("slot_count", ctypes.c_uint32),
+        ("slot_bytes", ctypes.POINTER(ctypes.c_uint64)),
+        ("entry_count", ctypes.c_uint32),
+        ("entries", ctypes.POINTER(DispatchEntry)),
+    ]
+
+
+class SumPlan(ctypes.Structure):
+    _fields_ = [
+        ("topology", ctypes.c_uint32),
+        ("participant_major", ctypes.c_uint32),
+        ("partitions", ctypes.c_uint64),
+        ("participants", ctypes.c_uint64),
+        ("per_partition", ctypes.c_uint64),
+        ("rounds", ctypes.c_uint64),
+    ]
+
+
+_P = ctypes.c_void_p
+_U64 = ctypes.c_uint64
+_U32 = ctypes.c_uint32
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+_S = ctypes.c_int32
+_CTX = ctypes.c_void_p
+
+SIGNATURES = {
+    "tiler_hip_profile_declare": (_S, [ctypes.POINTER(TargetProfile)]),
+    "tiler_hip_payload": (_S, [ctypes.POINTER(PayloadView)]),
+    "tiler_hip_payload_entry": (_S, [_U32, ctypes.POINTER(EntryInfo)]),
+    "tiler_hip_validate_payload": (_S, [_P, _U64, ctypes.c_char_p, _U32, ctypes.c_char_p, _U64]),
+    "tiler_hip_bind": (_S, [_I32, ctypes.POINTER(_CTX), ctypes.POINTER(ExecutionEnvironment),
+                            ctypes.c_char_p, _U64]),
+    "tiler_hip_release": (None, [_CTX]),
+    "tiler_hip_last_diagnostic": (ctypes.c_char_p, [_CTX]),
+    "tiler_hip_observe_live_device": (_S, [_CTX, ctypes.c_char_p, ctypes.POINTER(_U64)]),
+    "tiler_hip_prepare_entries": (_S, [_CTX, ctypes.POINTER(RoutedEntry), _U32,
+                                       ctypes.POINTER(_U32)]),
+    "tiler_hip_observe_prepared_entry": (_S, [_CTX, _U32, ctypes.c_char_p, ctypes.POINTER(_U64)]),
+    "tiler_hip_plan_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan)]),
+    "tiler_hip_allocate_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan), ctypes.POINTER(_P)]),
+    "tiler_hip_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan), ctypes.POINTER(_P)]),
+    "tiler_hip_release_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan), ctypes.POINTER(_P),
+                                        ctypes.POINTER(_P)]),
+    "tiler_hip_buffer_alloc": (_S, [_CTX, _U64, ctypes.POINTER(_P)]),
+    "tiler_hip_buffer_free": (_S, [_CTX, _P]),
+    "tiler_hip_upload": (_S, [_CTX, _P, _P, _U64]),
+    "tiler_hip_download": (_S, [_CTX, _P, _P, _U64]),
+    "tiler_hip_fill_u32": (_S, [_CTX, _P, _U32, _U64, _P]),
+    "tiler_hip_synchronize": (_S, [_CTX]),
+    "tiler_hip_context_stream": (_P, [_CTX]),
+    "tiler_hip_event_create": (_S, [_CTX, ctypes.POINTER(_P)]),
+    "tiler_hip_event_record": (_S, [_CTX, _P, _P]),
+    "tiler_hip_event_elapsed_ms": (_S, [_CTX, _P, _P, ctypes.POINTER(_F)]),
+    "tiler_hip_event_destroy": (_S, [_CTX, _P]),
+    "tiler_hip_sum_f32": (_S, [_CTX, _P, _U64, _U64, _P, ctypes.POINTER(SumPlan), _P]),
+    "tiler_hip_sum_tree_workgroups": (_U32, [_CTX, _U64]),
+    "tiler_hip_rms_norm": (_S, [_CTX, _U32, _P, _P, _I32, _U64, _U64, _U32, _P, _P]),
+    "tiler_hip_softmax_f32": (_S, [_CTX, _P, _U64, _U64, _P, _P]),
+    "tiler_hip_map": (_S, [_CTX, _U32, _U32, _P, _P, _I32, _U64, _F, _F, _P, _P]),
+    "tiler_hip_broadcast": (_S, [_CTX, _P, _U32, ctypes.POINTER(_U64), ctypes.POINTER(_U64), _U32,
+                                 _P, _P]),
+    "tiler_hip_gather": (_S, [_CTX, _P, _U64, _U64, _U64, _U32, _P, _U64, _I32, _P, _P]),
+    "tiler_hip_gather_status": (_S, [_CTX, _P, ctypes.POINTER(_U64)]),
+    "tiler_hip_validate_gather_index": (_S, [_P, _U64, _I32, _U64, ctypes.POINTER(_U64),
+                                             ctypes.POINTER(ctypes.c_int64)]),
+    "tiler_hip_contract_strict_f32": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _P]),
+    "tiler_hip_contract_bf16": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _U32, _P]),
+}
+
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def lib():
+    """Loads libtiler_hip.so; raises LibraryMissing if it was never built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissing(
+                f"{LIB_PATH} is not built; run `python -m tiler_amd.build` (tiler-hip has no "
+                "CPU fallback)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(handle, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = handle
+    return _lib

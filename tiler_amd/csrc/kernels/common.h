@@ -1,0 +1,147 @@
+// Shared device helpers for the tiler-hip gfx950 kernels.
+//
+// Every kernel in this library is compiled with -ffp-contract=off: a written
+// multiply followed by an add is two IEEE roundings, which is the arithmetic
+// the reference pins (tiler-reference/src/contraction.rs:612-624 "no FMA",
+// rms_norm.rs:155-162 "one rounding per square, then one per combine").
+// Fused multiply-adds appear only where written as __builtin_fma/__builtin_fmaf
+// (the exponential's range reduction and polynomial, which are internal to a
+// correctly rounded step).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "exp_table.h"
+
+#define TILER_CANONICAL_F32_NAN 0x7fc00000u  // tiler-ir/src/semantic/operation.rs:21
+#define TILER_CANONICAL_BF16_NAN 0x7fc0u     // ADR 0091 decision 2
+
+// Native clang vectors: the nontemporal builtins and bit casts need them
+// (HIP's float4/uint4 are wrapper structs).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+namespace tiler {
+
+__device__ __forceinline__ float canon(float v) {
+  return v != v ? __uint_as_float(TILER_CANONICAL_F32_NAN) : v;
+}
+
+// bf16 <-> f32 (ADR 0091 decision 2): widening is exact; narrowing is
+// round-to-nearest-even on the upper half, every NaN to 0x7fc0, signed zero
+// kept, gradual underflow, overflow to infinity at the inclusive midpoint.
+__device__ __forceinline__ float bf16_widen(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ uint32_t bf16_narrow(float v) {
+  uint32_t u = __float_as_uint(v);
+  if (v != v) return TILER_CANONICAL_BF16_NAN;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
+  return bf16_narrow(lo) | (bf16_narrow(hi) << 16);
+}
+
+// IEEE 754-2019 maximum with -0 < +0, NaN-propagating
+// (tiler-reference/src/softmax.rs:168-186).
+__device__ __forceinline__ float maximum_f32(float a, float b) {
+  if (a != a || b != b) return __uint_as_float(TILER_CANONICAL_F32_NAN);
+  if (a == b) return __uint_as_float(__float_as_uint(a) & __float_as_uint(b));
+  return a > b ? a : b;
+}
+
+// Wave64 xor butterfly: after it every lane holds the same value,
+// v[l] = v[l] + v[l ^ o] for o = 32, 16, 8, 4, 2, 1.  Addition is commutative
+// bit for bit, so the order inside each pair is immaterial.
+__device__ __forceinline__ float wave_sum_butterfly(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = maximum_f32(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Correctly rounded binary32 reciprocal square root of a binary32 argument,
+// the value certified_rsqrt_f32 admits (tiler-reference/src/rms_norm.rs:219-293,
+// special arguments :246-262).  The binary64 candidate 1/sqrt(t) is within
+// 2^-52 relative, so its binary32 rounding is at most one step from the
+// correctly rounded value; each neighbouring midpoint m is then decided
+// exactly by the sign of m^2*t - 1: m^2 has at most 50 significant bits so it
+// is exact in binary64, and p + e = m^2*t exactly with p = fl(m^2*t) and
+// e = fma(m^2, t, -p), p - 1 exact by Sterbenz.  No midpoint is ever hit
+// exactly (rms_norm.rs:22-45), so the strict sign test is total.
+__device__ __forceinline__ int midpoint_sq_times_t_minus_one_sign(double m, double t) {
+  double m2 = m * m;
+  double p = m2 * t;
+  double e = __builtin_fma(m2, t, -p);
+  double d = p - 1.0;
+  if (d > -e) return 1;
+  if (d < -e) return -1;
+  return 0;
+}
+__device__ __forceinline__ float rsqrt_f32_cr(float t) {
+  if (t != t) return __uint_as_float(TILER_CANONICAL_F32_NAN);
+  if (t == __builtin_huge_valf()) return 0.0f;
+  if (t == 0.0f) return __uint_as_float(__float_as_uint(t) | 0x7f800000u);  // +-inf
+  if (t < 0.0f) return __uint_as_float(TILER_CANONICAL_F32_NAN);
+  double td = (double)t;
+  float c = (float)(1.0 / __builtin_sqrt(td));
+  uint32_t cb = __float_as_uint(c);
+  double cd = (double)c;
+  double up = (cd + (double)__uint_as_float(cb + 1u)) * 0.5;
+  if (midpoint_sq_times_t_minus_one_sign(up, td) < 0) return __uint_as_float(cb + 1u);
+  double dn = (cd + (double)__uint_as_float(cb - 1u)) * 0.5;
+  if (midpoint_sq_times_t_minus_one_sign(dn, td) > 0) return __uint_as_float(cb - 1u);
+  return c;
+}
+
+// binary32 e^s for the softmax and SiLU families, with the reference's guards
+// (tiler-reference/src/silu.rs:573-588): NaN -> NaN, s >= 89 -> +inf,
+// s <= -104 -> +0.  Between them: k = rint(s*64/ln2), r = s - k*ln2/64 with
+// ln2/64 split so k*hi is exact (|r| <= 0.0055), e^r by its degree-6 Taylor
+// polynomial (truncation < 2^-64), times the binary64 table entry 2^(j/64),
+// scaled by 2^(k>>6), then one rounding to binary32.  The binary64 value is
+// within 2^-50 relative of e^s.
+__device__ __forceinline__ double exp_f64_core(double x, int& m_out) {
+  double kd = __builtin_rint(x * TILER_64_OVER_LN2);
+  int k = (int)kd;
+  double r = __builtin_fma(-kd, TILER_LN2_OVER_64_HI, x);
+  r = __builtin_fma(-kd, TILER_LN2_OVER_64_LO, r);
+  double p = 1.0 / 720.0;
+  p = __builtin_fma(p, r, 1.0 / 120.0);
+  p = __builtin_fma(p, r, 1.0 / 24.0);
+  p = __builtin_fma(p, r, 1.0 / 6.0);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  m_out = k >> 6;
+  return kExp2Table64[k & 63] * p;
+}
+__device__ __forceinline__ float exp_f32_cr(float s) {
+  if (s != s) return s;
+  if (s >= 89.0f) return __builtin_huge_valf();
+  if (s <= -104.0f) return 0.0f;
+  int m;
+  double v = exp_f64_core((double)s, m);
+  v = __builtin_ldexp(v, m);
+  return (float)v;
+}
+
+// Reference SiLU, tiler-reference/src/silu.rs:511-533: x / fl(1 + exp(-x)),
+// NaN -> NaN, +inf -> +inf, -inf -> NaN.
+__device__ __forceinline__ float silu_f32(float x) {
+  if (x != x) return x;
+  if (x == __builtin_huge_valf()) return x;
+  if (x == -__builtin_huge_valf()) return __uint_as_float(TILER_CANONICAL_F32_NAN);
+  float e = exp_f32_cr(-x);
+  float divisor = 1.0f + e;
+  return x / divisor;
+}
+
+}  // namespace tiler

@@ -1,0 +1,843 @@
+// tiler-hip host runtime: the C ABI of include/tiler_hip.h over the HIP
+// module API.  The gfx950 code object is compiled ahead of time and linked
+// into this library as bytes (payload.S); bind() loads it with
+// hipModuleLoadData and every launch goes through hipModuleLaunchKernel.
+#include "tiler_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "build_info.h"
+#include "code_object.h"
+
+extern "C" const uint8_t tiler_hip_code_object[];
+extern "C" const uint8_t tiler_hip_code_object_end[];
+
+namespace {
+
+constexpr const char* kBackend = "tiler.hip";
+constexpr const char* kRepresentation = "tiler.hip.gfx950.code-object-v1";
+constexpr const char* kPayloadSchema = "tiler.hip.payload.v1";
+constexpr const char* kTarget = "amdgcn-amd-amdhsa--gfx950";
+constexpr const char* kProfileKey = "tiler.hip.gfx950.profile-v1";
+
+struct EntryRow {
+  const char* symbol;
+  const char* family;
+  uint32_t buffers;
+};
+
+// Every kernel the payload carries, in a fixed order (the entry mapping).
+const EntryRow kEntries[] = {
+    {"tiler_sum_f32_serial", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_partials", "strict-serial-sum-f32/multipass", 2},
+    {"tiler_sum_f32_cooperative", "strict-serial-sum-f32/cooperative-workgroup", 2},
+    {"tiler_sum_f32_grid", "strict-serial-sum-f32/tree", 4},
+    {"tiler_sum_f32_grid_unaligned", "strict-serial-sum-f32/tree", 4},
+    {"tiler_sum_f32_rows", "strict-serial-sum-f32/tree", 2},
+    {"tiler_rms_norm_bf16_ch1", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch1_u", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch2", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch2_u", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch4", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch4_u", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch8", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch8_u", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch16", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch16_u", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_f32_ch1", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch1_u", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch2", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch2_u", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch4", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch4_u", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch8", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch8_u", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch16", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch16_u", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch32", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch32_u", "rms-norm-f32", 3},
+    {"tiler_softmax_f32_ch1", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch1_u", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch2", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch2_u", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch4", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch4_u", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch8", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch8_u", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch16", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch16_u", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch32", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch32_u", "softmax-f32", 2},
+    {"tiler_gather_u128", "gather", 4},
+    {"tiler_gather_u64", "gather", 4},
+    {"tiler_gather_u32", "gather", 4},
+    {"tiler_gather_u16", "gather", 4},
+    {"tiler_gather_u8", "gather", 4},
+    {"tiler_map_f32", "pointwise-f32", 3},
+    {"tiler_map_bf16", "pointwise-bf16", 3},
+    {"tiler_broadcast_u32", "broadcast", 2},
+    {"tiler_broadcast_u16", "broadcast", 2},
+    {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_bf16_t128", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_t128", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_t128_k", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_t128_k", "tensor-contraction-bf16/cooperative+silu", 3},
+};
+constexpr uint32_t kEntryCount = sizeof(kEntries) / sizeof(kEntries[0]);
+
+constexpr uint32_t kMaxSumWorkgroups = 4096;
+
+void copy_text(char* dst, uint64_t cap, const std::string& s) {
+  if (!dst || cap == 0) return;
+  uint64_t n = s.size() < cap - 1 ? s.size() : cap - 1;
+  std::memcpy(dst, s.data(), n);
+  dst[n] = 0;
+}
+
+uint64_t code_object_bytes() {
+  return (uint64_t)(tiler_hip_code_object_end - tiler_hip_code_object);
+}
+
+}  // namespace
+
+struct tiler_hip_context {
+  int device = -1;
+  hipStream_t stream = nullptr;
+  hipModule_t module = nullptr;
+  std::unordered_map<std::string, hipFunction_t> fns;
+  std::vector<hipModule_t> routed_modules;
+  std::vector<hipFunction_t> prepared;
+  // workspace: [partials kMaxSumWorkgroups f32][ticket u32 + pad][gather_bad u64]
+  uint8_t* workspace = nullptr;
+  float* sum_partials = nullptr;
+  uint32_t* sum_ticket = nullptr;
+  unsigned long long* gather_bad = nullptr;
+  uint32_t compute_units = 0;
+  uint64_t lds_bytes = 0;
+  uint32_t max_threads = 0;
+  uint64_t global_bytes = 0;
+  std::string arch;
+  std::string diag;
+};
+
+namespace {
+
+tiler_hip_status fail(tiler_hip_context* ctx, tiler_hip_status st, const std::string& what) {
+  if (ctx) ctx->diag = what;
+  return st;
+}
+
+hipStream_t pick(tiler_hip_context* ctx, tiler_hip_stream s) {
+  return s ? static_cast<hipStream_t>(s) : ctx->stream;
+}
+
+hipFunction_t fn(tiler_hip_context* ctx, const char* symbol) {
+  auto it = ctx->fns.find(symbol);
+  return it == ctx->fns.end() ? nullptr : it->second;
+}
+
+tiler_hip_status launch(tiler_hip_context* ctx, const char* symbol, uint32_t gx, uint32_t gy,
+                        uint32_t bx, hipStream_t s, void** args) {
+  hipFunction_t f = fn(ctx, symbol);
+  if (!f) return fail(ctx, TILER_HIP_REFUSE_NOT_PREPARED, std::string("kernel not loaded: ") + symbol);
+  if (gx == 0 || gy == 0) return TILER_HIP_OK;
+  hipError_t e = hipModuleLaunchKernel(f, gx, gy, 1, bx, 1, 1, 0, s, args, nullptr);
+  if (e != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_LAUNCH,
+                std::string("hipModuleLaunchKernel(") + symbol + "): " + hipGetErrorString(e));
+  return TILER_HIP_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+uint32_t pow2_at_least(uint64_t v) {
+  uint32_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+tiler_hip_status tiler_hip_profile_declare(tiler_hip_target_profile* out) {
+  if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  std::memset(out, 0, sizeof(*out));
+  copy_text(out->profile_key, sizeof(out->profile_key), kProfileKey);
+  copy_text(out->target_triple, sizeof(out->target_triple), kTarget);
+  out->wavefront_size = 64;
+  out->compute_units = 256;
+  out->xcds = 8;
+  out->simds_per_cu = 4;
+  out->max_threads_per_workgroup = 1024;
+  out->max_grid_dim[0] = 0x7fffffffu;
+  out->max_grid_dim[1] = 65535;
+  out->max_grid_dim[2] = 65535;
+  out->lds_bytes_per_workgroup = 163840;
+  out->device_memory_bytes = 288ull * 1000 * 1000 * 1000;
+  out->l2_bytes_per_xcd = 4ull << 20;
+  out->infinity_cache_bytes = 256ull << 20;
+  out->address_bits = 64;
+  out->index_u64 = 1;
+  out->subgroup_width = 64;
+  out->f32_subnormals_preserved = 1;
+  out->hbm_bytes_per_second = 8.0e12;
+  out->mfma_bf16_dense_flops = 2.5e15;
+  out->mfma_fp8_dense_flops = 5.0e15;
+  out->vector_f32_flops = 157.3e12;
+  out->vector_f64_flops = 78.6e12;
+  out->parallel_threads = 256u * 4u * 64u;  // one wave64 per SIMD
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+tiler_hip_status tiler_hip_payload(tiler_hip_payload_view* out) {
+  if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  out->backend = kBackend;
+  out->representation = kRepresentation;
+  out->payload_schema = kPayloadSchema;
+  out->target = kTarget;
+  out->toolchain = TILER_HIP_BUILD_TOOLCHAIN;
+  out->flags = TILER_HIP_BUILD_FLAGS;
+  out->code = tiler_hip_code_object;
+  out->code_bytes = code_object_bytes();
+  out->entry_count = kEntryCount;
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_payload_entry(uint32_t index, tiler_hip_entry_info* out) {
+  if (!out || index >= kEntryCount) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_hip::KernelDescriptorFacts facts;
+  bool absent = false;
+  std::string why = tiler_hip::inspect_code_object(tiler_hip_code_object, code_object_bytes(),
+                                                   kEntries[index].symbol, &facts, &absent);
+  if (!why.empty()) return absent ? TILER_HIP_REFUSE_ABSENT_SYMBOL : TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+  out->symbol = kEntries[index].symbol;
+  out->family = kEntries[index].family;
+  out->buffer_bindings = kEntries[index].buffers;
+  out->kernarg_bytes = facts.kernarg_bytes;
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_validate_payload(const void* code, uint64_t code_bytes,
+                                            const char* symbol, uint32_t kernarg_bytes,
+                                            char* diagnostic, uint64_t diagnostic_bytes) {
+  tiler_hip::KernelDescriptorFacts facts;
+  bool absent = false;
+  std::string why = tiler_hip::inspect_code_object(code, code_bytes, symbol, &facts, &absent);
+  if (!why.empty()) {
+    copy_text(diagnostic, diagnostic_bytes, why);
+    return absent ? TILER_HIP_REFUSE_ABSENT_SYMBOL : TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+  }
+  if (symbol && kernarg_bytes != 0 && facts.kernarg_bytes != kernarg_bytes) {
+    copy_text(diagnostic, diagnostic_bytes,
+              "kernel " + std::string(symbol) + " takes " + std::to_string(facts.kernarg_bytes) +
+                  " kernarg bytes, the entry declares " + std::to_string(kernarg_bytes));
+    return TILER_HIP_REFUSE_BINDING_MISMATCH;
+  }
+  copy_text(diagnostic, diagnostic_bytes, "");
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
+                                tiler_hip_execution_environment* env, char* diagnostic,
+                                uint64_t diagnostic_bytes) {
+  if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+    copy_text(diagnostic, diagnostic_bytes, "no HIP device is visible");
+    return TILER_HIP_REFUSE_NO_DEVICE;
+  }
+  if (ordinal < 0 || ordinal >= count) {
+    copy_text(diagnostic, diagnostic_bytes, "device ordinal out of range");
+    return TILER_HIP_REFUSE_NO_DEVICE;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, ordinal) != hipSuccess) {
+    copy_text(diagnostic, diagnostic_bytes, "hipGetDeviceProperties failed");
+    return TILER_HIP_REFUSE_NO_DEVICE;
+  }
+  std::string arch = prop.gcnArchName;
+  if (arch.rfind("gfx950", 0) != 0) {
+    copy_text(diagnostic, diagnostic_bytes, "device is " + arch + ", this backend targets gfx950");
+    return TILER_HIP_REFUSE_FOREIGN_TARGET;
+  }
+  if (hipSetDevice(ordinal) != hipSuccess) {
+    copy_text(diagnostic, diagnostic_bytes, "hipSetDevice failed");
+    return TILER_HIP_REFUSE_NO_DEVICE;
+  }
+  auto* ctx = new tiler_hip_context();
+  ctx->device = ordinal;
+  ctx->arch = arch;
+  ctx->compute_units = (uint32_t)prop.multiProcessorCount;
+  ctx->lds_bytes = prop.sharedMemPerBlock;
+  ctx->max_threads = (uint32_t)prop.maxThreadsPerBlock;
+  ctx->global_bytes = prop.totalGlobalMem;
+  hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipModuleLoadData(&ctx->module, tiler_hip_code_object);
+  if (e != hipSuccess) {
+    copy_text(diagnostic, diagnostic_bytes, std::string("loading the gfx950 code object: ") + hipGetErrorString(e));
+    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+  }
+  for (uint32_t i = 0; i < kEntryCount; ++i) {
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, ctx->module, kEntries[i].symbol) != hipSuccess || !f) {
+      copy_text(diagnostic, diagnostic_bytes, std::string("absent entry symbol ") + kEntries[i].symbol);
+      hipModuleUnload(ctx->module);
+      hipStreamDestroy(ctx->stream);
+      delete ctx;
+      return TILER_HIP_REFUSE_ABSENT_SYMBOL;
+    }
+    ctx->fns[kEntries[i].symbol] = f;
+  }
+  const uint64_t ws_bytes = kMaxSumWorkgroups * 4 + 256 + 256;
+  if (hipMalloc(&ctx->workspace, ws_bytes) != hipSuccess) {
+    copy_text(diagnostic, diagnostic_bytes, "workspace allocation failed");
+    hipModuleUnload(ctx->module);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return TILER_HIP_REFUSE_CAPACITY;
+  }
+  ctx->sum_partials = reinterpret_cast<float*>(ctx->workspace);
+  ctx->sum_ticket = reinterpret_cast<uint32_t*>(ctx->workspace + kMaxSumWorkgroups * 4);
+  ctx->gather_bad = reinterpret_cast<unsigned long long*>(ctx->workspace + kMaxSumWorkgroups * 4 + 256);
+  hipMemset(ctx->workspace, 0, ws_bytes);
+  hipMemset(ctx->gather_bad, 0xff, 8);
+  hipDeviceSynchronize();
+  if (env) {
+    std::memset(env, 0, sizeof(*env));
+    env->device_ordinal = ordinal;
+    copy_text(env->device_name, sizeof(env->device_name), prop.name);
+    copy_text(env->gcn_arch_name, sizeof(env->gcn_arch_name), arch);
+    env->compute_units = ctx->compute_units;
+    env->wavefront_size = (uint32_t)prop.warpSize;
+    env->max_threads_per_workgroup = ctx->max_threads;
+    env->lds_bytes_per_workgroup = ctx->lds_bytes;
+    env->global_memory_bytes = ctx->global_bytes;
+    env->clock_khz = prop.clockRate;
+    env->memory_clock_khz = prop.memoryClockRate;
+    env->memory_bus_width_bits = prop.memoryBusWidth;
+    int rv = 0, dv = 0;
+    hipRuntimeGetVersion(&rv);
+    hipDriverGetVersion(&dv);
+    env->runtime_version = rv;
+    env->driver_version = dv;
+  }
+  copy_text(diagnostic, diagnostic_bytes, "");
+  *out = ctx;
+  return TILER_HIP_OK;
+}
+
+void tiler_hip_release(tiler_hip_context* ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  for (hipModule_t m : ctx->routed_modules) hipModuleUnload(m);
+  if (ctx->module) hipModuleUnload(ctx->module);
+  if (ctx->workspace) hipFree(ctx->workspace);
+  if (ctx->stream) hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+const char* tiler_hip_last_diagnostic(const tiler_hip_context* ctx) {
+  return ctx ? ctx->diag.c_str() : "";
+}
+
+tiler_hip_status tiler_hip_observe_live_device(tiler_hip_context* ctx, const char* key,
+                                               uint64_t* value) {
+  if (!ctx || !key || !value) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  std::string k = key;
+  if (k == "wavefront-size") *value = 64;
+  else if (k == "compute-units") *value = ctx->compute_units;
+  else if (k == "max-threads-per-workgroup") *value = ctx->max_threads;
+  else if (k == "lds-bytes-per-workgroup") *value = ctx->lds_bytes;
+  else if (k == "global-memory-bytes") *value = ctx->global_bytes;
+  else if (k == "target-is-gfx950") *value = ctx->arch.rfind("gfx950", 0) == 0 ? 1 : 0;
+  else return fail(ctx, TILER_HIP_REFUSE_UNRECOGNIZED_KEY, "unrecognized live-device key " + k);
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_prepare_entries(tiler_hip_context* ctx,
+                                           const tiler_hip_routed_entry* entries, uint32_t count,
+                                           uint32_t* first_index) {
+  if (!ctx || (count && !entries)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipSetDevice(ctx->device);
+  std::vector<hipModule_t> loaded;
+  std::vector<hipFunction_t> fns;
+  for (uint32_t i = 0; i < count; ++i) {
+    char why[256];
+    tiler_hip_status st = tiler_hip_validate_payload(entries[i].code, entries[i].code_bytes,
+                                                     entries[i].symbol, 0, why, sizeof(why));
+    hipModule_t m = nullptr;
+    hipFunction_t f = nullptr;
+    if (st == TILER_HIP_OK && hipModuleLoadData(&m, entries[i].code) != hipSuccess)
+      st = TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+    if (st == TILER_HIP_OK && (hipModuleGetFunction(&f, m, entries[i].symbol) != hipSuccess || !f))
+      st = TILER_HIP_REFUSE_ABSENT_SYMBOL;
+    if (st != TILER_HIP_OK) {
+      if (m) hipModuleUnload(m);
+      for (hipModule_t mm : loaded) hipModuleUnload(mm);
+      return fail(ctx, st, "entry " + std::to_string(i) + " not prepared: " + std::string(why));
+    }
+    loaded.push_back(m);
+    fns.push_back(f);
+  }
+  if (first_index) *first_index = (uint32_t)ctx->prepared.size();
+  ctx->routed_modules.insert(ctx->routed_modules.end(), loaded.begin(), loaded.end());
+  ctx->prepared.insert(ctx->prepared.end(), fns.begin(), fns.end());
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_observe_prepared_entry(tiler_hip_context* ctx, uint32_t prepared,
+                                                  const char* key, uint64_t* value) {
+  if (!ctx || !key || !value) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (prepared >= ctx->prepared.size())
+    return fail(ctx, TILER_HIP_REFUSE_NOT_PREPARED, "entry not prepared");
+  std::string k = key;
+  hipFunction_attribute attr;
+  if (k == "max-threads-per-workgroup") attr = HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK;
+  else if (k == "static-lds-bytes") attr = HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES;
+  else if (k == "private-bytes-per-lane") attr = HIP_FUNC_ATTRIBUTE_LOCAL_SIZE_BYTES;
+  else if (k == "vgprs") attr = HIP_FUNC_ATTRIBUTE_NUM_REGS;
+  else return fail(ctx, TILER_HIP_REFUSE_UNRECOGNIZED_KEY, "unrecognized prepared-entry key " + k);
+  int v = 0;
+  if (hipFuncGetAttribute(&v, attr, ctx->prepared[prepared]) != hipSuccess)
+    return fail(ctx, TILER_HIP_REFUSE_NOT_PREPARED, "hipFuncGetAttribute failed");
+  *value = (uint64_t)v;
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_plan_dispatch(tiler_hip_context* ctx,
+                                         const tiler_hip_dispatch_plan* plan) {
+  if (!ctx || !plan || (plan->entry_count && !plan->entries) ||
+      (plan->slot_count && !plan->slot_bytes))
+    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  for (uint32_t s = 0; s < plan->slot_count; ++s)
+    if (plan->slot_bytes[s] > ctx->global_bytes)
+      return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "slot " + std::to_string(s) + " exceeds device memory");
+  for (uint32_t i = 0; i < plan->entry_count; ++i) {
+    const tiler_hip_dispatch_entry& e = plan->entries[i];
+    if (e.prepared >= ctx->prepared.size())
+      return fail(ctx, TILER_HIP_REFUSE_NOT_PREPARED, "entry " + std::to_string(i) + " names an unprepared entry");
+    uint64_t threads = (uint64_t)e.block[0] * e.block[1] * e.block[2];
+    int maxt = 0;
+    hipFuncGetAttribute(&maxt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, ctx->prepared[e.prepared]);
+    if (threads == 0 || threads > (uint64_t)maxt)
+      return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "entry " + std::to_string(i) + " workgroup wider than its pipeline admits");
+    if (e.grid[0] == 0 || e.grid[1] == 0 || e.grid[2] == 0 || e.grid[1] > 65535 || e.grid[2] > 65535)
+      return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "entry " + std::to_string(i) + " grid outside the profile");
+    int slds = 0;
+    hipFuncGetAttribute(&slds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, ctx->prepared[e.prepared]);
+    if ((uint64_t)slds + e.dynamic_lds_bytes > ctx->lds_bytes)
+      return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "entry " + std::to_string(i) + " LDS beyond the workgroup limit");
+    if (e.binding_count && (!e.binding_slots || !e.binding_offsets))
+      return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+    for (uint32_t b = 0; b < e.binding_count; ++b) {
+      if (e.binding_slots[b] >= plan->slot_count)
+        return fail(ctx, TILER_HIP_REFUSE_BINDING_MISMATCH, "binding names an undeclared slot");
+      if ((uint64_t)e.binding_offsets[b] + 8 > e.kernarg_bytes)
+        return fail(ctx, TILER_HIP_REFUSE_BINDING_MISMATCH, "binding pointer outside the kernarg segment");
+    }
+  }
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_allocate_dispatch(tiler_hip_context* ctx,
+                                             const tiler_hip_dispatch_plan* plan,
+                                             void** slot_pointers) {
+  if (!ctx || !plan || (plan->slot_count && !slot_pointers)) return TILER_HIP_FAIL_ALLOCATION;
+  hipSetDevice(ctx->device);
+  for (uint32_t s = 0; s < plan->slot_count; ++s) {
+    if (slot_pointers[s]) continue;
+    void* p = nullptr;
+    uint64_t bytes = plan->slot_bytes[s] ? plan->slot_bytes[s] : 1;
+    if (hipMalloc(&p, bytes) != hipSuccess || !p)
+      return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "allocation of slot " + std::to_string(s) + " failed");
+    slot_pointers[s] = p;
+  }
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_dispatch_plan* plan,
+                                    void* const* slot_pointers) {
+  if (!ctx || !plan) return TILER_HIP_FAIL_LAUNCH;
+  hipSetDevice(ctx->device);
+  std::vector<uint8_t> args;
+  for (uint32_t i = 0; i < plan->entry_count; ++i) {
+    const tiler_hip_dispatch_entry& e = plan->entries[i];
+    args.assign((const uint8_t*)e.kernargs, (const uint8_t*)e.kernargs + e.kernarg_bytes);
+    for (uint32_t b = 0; b < e.binding_count; ++b) {
+      void* p = slot_pointers[e.binding_slots[b]];
+      std::memcpy(args.data() + e.binding_offsets[b], &p, sizeof(p));
+    }
+    size_t size = args.size();
+    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE,
+                      &size, HIP_LAUNCH_PARAM_END};
+    hipError_t err = hipModuleLaunchKernel(ctx->prepared[e.prepared], e.grid[0], e.grid[1],
+                                           e.grid[2], e.block[0], e.block[1], e.block[2],
+                                           e.dynamic_lds_bytes, ctx->stream, nullptr, config);
+    if (err != hipSuccess)
+      return fail(ctx, TILER_HIP_FAIL_LAUNCH, "entry " + std::to_string(i) + ": " + hipGetErrorString(err));
+  }
+  hipError_t err = hipStreamSynchronize(ctx->stream);
+  if (err != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, hipGetErrorString(err));
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_release_dispatch(tiler_hip_context* ctx,
+                                            const tiler_hip_dispatch_plan* plan,
+                                            void** slot_pointers, const void** caller_owned) {
+  if (!ctx || !plan) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipSetDevice(ctx->device);
+  for (uint32_t s = 0; s < plan->slot_count; ++s) {
+    if (!slot_pointers[s] || (caller_owned && caller_owned[s])) continue;
+    hipFree(slot_pointers[s]);
+    slot_pointers[s] = nullptr;
+  }
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+tiler_hip_status tiler_hip_buffer_alloc(tiler_hip_context* ctx, uint64_t bytes, void** out) {
+  if (!ctx || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipSetDevice(ctx->device);
+  *out = nullptr;
+  if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_buffer_free(tiler_hip_context* ctx, void* ptr) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipSetDevice(ctx->device);
+  if (ptr && hipFree(ptr) != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, "hipFree failed");
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_upload(tiler_hip_context* ctx, void* dst, const void* src,
+                                  uint64_t bytes) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (bytes == 0) return TILER_HIP_OK;
+  hipSetDevice(ctx->device);
+  if (hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+      hipStreamSynchronize(ctx->stream) != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_TRANSFER, "host-to-device copy failed");
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_download(tiler_hip_context* ctx, void* dst, const void* src,
+                                    uint64_t bytes) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (bytes == 0) return TILER_HIP_OK;
+  hipSetDevice(ctx->device);
+  if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
+      hipStreamSynchronize(ctx->stream) != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_TRANSFER, "device-to-host copy failed");
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_fill_u32(tiler_hip_context* ctx, void* dst, uint32_t value,
+                                    uint64_t words, tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (hipMemsetD32Async(dst, (int)value, words, pick(ctx, stream)) != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_DEVICE, "fill failed");
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_synchronize(tiler_hip_context* ctx) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, hipGetErrorString(e));
+  return TILER_HIP_OK;
+}
+tiler_hip_stream tiler_hip_context_stream(tiler_hip_context* ctx) {
+  return ctx ? static_cast<tiler_hip_stream>(ctx->stream) : nullptr;
+}
+tiler_hip_status tiler_hip_event_create(tiler_hip_context* ctx, tiler_hip_event* out) {
+  if (!ctx || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, "hipEventCreate failed");
+  *out = e;
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_event_record(tiler_hip_context* ctx, tiler_hip_event ev,
+                                        tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (hipEventRecord(static_cast<hipEvent_t>(ev), pick(ctx, stream)) != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_DEVICE, "hipEventRecord failed");
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_event_elapsed_ms(tiler_hip_context* ctx, tiler_hip_event start,
+                                            tiler_hip_event stop, float* ms) {
+  if (!ctx || !ms) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (hipEventSynchronize(static_cast<hipEvent_t>(stop)) != hipSuccess ||
+      hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)) != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_DEVICE, "hipEventElapsedTime failed");
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_event_destroy(tiler_hip_context* ctx, tiler_hip_event ev) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipEventDestroy(static_cast<hipEvent_t>(ev));
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context* ctx, uint64_t n) {
+  uint64_t tiles = (n + 1023) / 1024;
+  uint64_t cap = ctx ? 4ull * ctx->compute_units : 1024;
+  if (cap > kMaxSumWorkgroups) cap = kMaxSumWorkgroups;
+  uint64_t g = tiles < cap ? tiles : cap;
+  return g ? (uint32_t)g : 1u;
+}
+
+tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint64_t rows,
+                                   uint64_t extent, float* out, const tiler_hip_sum_plan* plan,
+                                   tiler_hip_stream stream) {
+  if (!ctx || !plan || (rows && !out) || (rows && extent && !x))
+    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipStream_t s = pick(ctx, stream);
+  if (rows == 0) return TILER_HIP_OK;
+  switch (plan->topology) {
+    case TILER_HIP_SUM_SERIAL: {
+      uint64_t outer = rows, inner = 1;
+      void* args[] = {&x, &outer, &extent, &inner, &out};
+      return launch(ctx, "tiler_sum_f32_serial", (uint32_t)((rows + 255) / 256), 1, 256, s, args);
+    }
+    case TILER_HIP_SUM_MULTIPASS: {
+      uint64_t P = plan->partitions, c = plan->per_partition;
+      if (P == 0 || (c != 0 && P > UINT64_MAX / c) || P * c != extent)
+        return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "partitions do not cover the axis exactly");
+      void* partials = nullptr;
+      if (hipMallocAsync(&partials, rows * P * 4, s) != hipSuccess)
+        return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "partials allocation failed");
+      float* pp = static_cast<float*>(partials);
+      void* a1[] = {&x, &rows, &extent, &P, &c, &pp};
+      tiler_hip_status st = launch(ctx, "tiler_sum_f32_partials", (uint32_t)((rows * P + 255) / 256), 1, 256, s, a1);
+      if (st == TILER_HIP_OK) {
+        uint64_t outer = rows, inner = 1;
+        const float* cp = pp;
+        void* a2[] = {&cp, &outer, &P, &inner, &out};
+        st = launch(ctx, "tiler_sum_f32_serial", (uint32_t)((rows + 255) / 256), 1, 256, s, a2);
+      }
+      hipFreeAsync(partials, s);
+      return st;
+    }
+    case TILER_HIP_SUM_COOPERATIVE: {
+      uint64_t P = plan->participants, c = plan->per_partition, R = plan->rounds;
+      if (P == 0 || P > 1024 || c == 0 || R == 0 || P * c * R != extent)
+        return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "grouping does not cover the axis exactly");
+      uint32_t P32 = (uint32_t)P, pm = plan->participant_major ? 1u : 0u;
+      void* args[] = {&x, &extent, &P32, &c, &R, &pm, &out};
+      return launch(ctx, "tiler_sum_f32_cooperative", (uint32_t)rows, 1, P32, s, args);
+    }
+    case TILER_HIP_SUM_TREE: {
+      if (rows == 1) {
+        uint32_t G = tiler_hip_sum_tree_workgroups(ctx, extent);
+        float* partials = ctx->sum_partials;
+        uint32_t* ticket = ctx->sum_ticket;
+        uint64_t n = extent;
+        void* args[] = {&x, &n, &out, &partials, &ticket};
+        return launch(ctx, aligned16(x) ? "tiler_sum_f32_grid" : "tiler_sum_f32_grid_unaligned", G, 1, 256, s, args);
+      }
+      void* args[] = {&x, &extent, &out};
+      return launch(ctx, "tiler_sum_f32_rows", (uint32_t)rows, 1, 256, s, args);
+    }
+    default:
+      return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "unknown reduction topology");
+  }
+}
+
+tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, const void* x,
+                                    const void* w, int32_t weight_broadcast, uint64_t rows,
+                                    uint64_t extent, uint32_t eps_bits, void* y,
+                                    tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  float eps;
+  std::memcpy(&eps, &eps_bits, 4);
+  // rms_norm.rs:462-466: a non-positive or non-finite eps refuses.
+  if (!(eps > 0.0f) || !std::isfinite(eps))
+    return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "eps must be positive and finite");
+  if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16)
+    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "rms_norm dtype");
+  if (rows == 0 || extent == 0) return TILER_HIP_OK;
+  if (!x || !w || !y) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  const uint32_t vec = dtype == TILER_HIP_BF16 ? 8 : 4;
+  const uint32_t max_ch = dtype == TILER_HIP_BF16 ? 16 : 32;
+  uint64_t chunks = (extent + 64ull * vec - 1) / (64ull * vec);
+  uint32_t ch = pow2_at_least(chunks);
+  if (ch > max_ch || extent > 0xffffffffull)
+    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row longer than the register-resident realization");
+  const uint64_t elem = dtype == TILER_HIP_BF16 ? 2 : 4;
+  bool al = aligned16(x) && aligned16(w) && aligned16(y) && (extent * elem) % 16 == 0;
+  char name[64];
+  std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_ch%u%s",
+                dtype == TILER_HIP_BF16 ? "bf16" : "f32", ch, al ? "" : "_u");
+  uint64_t wstride = weight_broadcast ? 0 : extent;
+  uint32_t ext32 = (uint32_t)extent;
+  void* args[] = {&x, &w, &wstride, &y, &rows, &ext32, &eps};
+  return launch(ctx, name, (uint32_t)((rows + 3) / 4), 1, 256, pick(ctx, stream), args);
+}
+
+tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, uint64_t rows,
+                                       uint64_t extent, float* y, tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (rows == 0 || extent == 0) return TILER_HIP_OK;
+  if (!x || !y) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  uint32_t ch = pow2_at_least((extent + 255) / 256);
+  if (ch > 32 || extent > 0xffffffffull)
+    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row longer than the register-resident realization");
+  bool al = aligned16(x) && aligned16(y) && extent % 4 == 0;
+  char name[64];
+  std::snprintf(name, sizeof(name), "tiler_softmax_f32_ch%u%s", ch, al ? "" : "_u");
+  uint32_t ext32 = (uint32_t)extent;
+  void* args[] = {&x, &y, &rows, &ext32};
+  return launch(ctx, name, (uint32_t)((rows + 3) / 4), 1, 256, pick(ctx, stream), args);
+}
+
+tiler_hip_status tiler_hip_map(tiler_hip_context* ctx, uint32_t op, uint32_t dtype,
+                               const void* x, const void* x2, int32_t x2_broadcast, uint64_t n,
+                               float a, float b, void* y, tiler_hip_stream stream) {
+  if (!ctx || op > TILER_HIP_MAP_MULTIPLY) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16)
+    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "map dtype");
+  if (n == 0) return TILER_HIP_OK;
+  if (!x || !y || ((op == TILER_HIP_MAP_ADD || op == TILER_HIP_MAP_MULTIPLY) && !x2))
+    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (dtype == TILER_HIP_BF16 && op == TILER_HIP_MAP_SILU)
+    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "silu is an f32 family");
+  uint64_t stride2 = x2_broadcast ? 0 : 1;
+  uint64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  void* args[] = {&x, &x2, &stride2, &n, &op, &a, &b, &y};
+  return launch(ctx, dtype == TILER_HIP_BF16 ? "tiler_map_bf16" : "tiler_map_f32",
+                (uint32_t)blocks, 1, 256, pick(ctx, stream), args);
+}
+
+struct BroadcastGeometryHost {
+  uint64_t out_dims[8];
+  uint64_t src_strides[8];
+  uint32_t rank;
+};
+
+tiler_hip_status tiler_hip_broadcast(tiler_hip_context* ctx, const void* src, uint32_t rank,
+                                     const uint64_t* out_dims, const uint64_t* src_strides,
+                                     uint32_t element_bytes, void* out, tiler_hip_stream stream) {
+  if (!ctx || rank > 8 || (rank && (!out_dims || !src_strides)))
+    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (element_bytes != 2 && element_bytes != 4)
+    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "broadcast element width");
+  BroadcastGeometryHost g;
+  std::memset(&g, 0, sizeof(g));
+  g.rank = rank;
+  uint64_t n = 1;
+  for (uint32_t d = 0; d < rank; ++d) {
+    g.out_dims[d] = out_dims[d];
+    g.src_strides[d] = src_strides[d];
+    n *= out_dims[d];
+  }
+  if (n == 0) return TILER_HIP_OK;
+  uint64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  void* args[] = {&src, &out, &n, &g};
+  return launch(ctx, element_bytes == 4 ? "tiler_broadcast_u32" : "tiler_broadcast_u16",
+                (uint32_t)blocks, 1, 256, pick(ctx, stream), args);
+}
+
+tiler_hip_status tiler_hip_validate_gather_index(const uint32_t* index, uint64_t count,
+                                                 int32_t index_signed, uint64_t gathered,
+                                                 uint64_t* bad_position, int64_t* bad_value) {
+  if (count && !index) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  for (uint64_t i = 0; i < count; ++i) {
+    int64_t v = index_signed ? (int64_t)(int32_t)index[i] : (int64_t)index[i];
+    if (v < 0 || (uint64_t)v >= gathered) {
+      if (bad_position) *bad_position = i;
+      if (bad_value) *bad_value = v;
+      return TILER_HIP_REFUSE_GATHER_INDEX_OUT_OF_BOUNDS;
+    }
+  }
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_gather(tiler_hip_context* ctx, const void* source, uint64_t outer,
+                                  uint64_t gathered, uint64_t inner, uint32_t element_bytes,
+                                  const uint32_t* index, uint64_t count, int32_t index_signed,
+                                  void* out, tiler_hip_stream stream) {
+  if (!ctx || element_bytes == 0) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  uint64_t runs = outer * count;
+  uint64_t run_bytes = inner * element_bytes;
+  if (runs == 0 || run_bytes == 0) return TILER_HIP_OK;
+  if (!source || !index || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  uintptr_t both = (uintptr_t)source | (uintptr_t)out;
+  uint32_t unit = 16;
+  while (unit > 1 && (run_bytes % unit != 0 || (both & (unit - 1)) != 0)) unit >>= 1;
+  const char* name = unit == 16 ? "tiler_gather_u128" : unit == 8 ? "tiler_gather_u64"
+                   : unit == 4 ? "tiler_gather_u32" : unit == 2 ? "tiler_gather_u16"
+                               : "tiler_gather_u8";
+  uint64_t run_units = run_bytes / unit;
+  uint32_t sgn = index_signed ? 1u : 0u;
+  unsigned long long* bad = ctx->gather_bad;
+  uint64_t blocks = runs < (1ull << 20) ? runs : (1ull << 20);
+  void* args[] = {&source, &outer, &gathered, &run_units, &index, &count, &sgn, &out, &bad};
+  return launch(ctx, name, (uint32_t)blocks, 1, 256, pick(ctx, stream), args);
+}
+
+tiler_hip_status tiler_hip_gather_status(tiler_hip_context* ctx, tiler_hip_stream stream,
+                                         uint64_t* bad_position) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipStream_t s = pick(ctx, stream);
+  unsigned long long v = 0;
+  if (hipMemcpyAsync(&v, ctx->gather_bad, 8, hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_DEVICE, "reading the gather record failed");
+  if (v == ~0ull) return TILER_HIP_OK;
+  if (bad_position) *bad_position = v;
+  hipMemsetAsync(ctx->gather_bad, 0xff, 8, s);
+  hipStreamSynchronize(s);
+  return fail(ctx, TILER_HIP_FAIL_GATHER_INDEX_OUT_OF_BOUNDS,
+              "gather index out of bounds at position " + std::to_string(v));
+}
+
+tiler_hip_status tiler_hip_contract_strict_f32(tiler_hip_context* ctx, const float* a,
+                                               const float* b, uint64_t m, uint64_t n,
+                                               uint64_t k, float* c, tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  // contraction.rs:420-428: an empty contracted domain has no unseeded result.
+  if (k == 0) return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty contracted extent");
+  if (m == 0 || n == 0) return TILER_HIP_OK;
+  if (!a || !b || !c) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (m > 0xffffffffull || n > 0xffffffffull || k > 0xffffffffull || (m + 15) / 16 > 65535)
+    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
+  uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
+  void* args[] = {&a, &b, &m32, &n32, &k32, &c};
+  return launch(ctx, "tiler_contract_strict_f32", (uint32_t)((n + 15) / 16),
+                (uint32_t)((m + 15) / 16), 256, pick(ctx, stream), args);
+}
+
+tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t* a,
+                                         const uint16_t* b, uint64_t m, uint64_t n, uint64_t k,
+                                         uint16_t* c, uint32_t epilogue,
+                                         tiler_hip_stream stream) {
+  if (!ctx || epilogue > TILER_HIP_EPILOGUE_SILU) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (k == 0) return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty contracted extent");
+  if (m == 0 || n == 0) return TILER_HIP_OK;
+  if (!a || !b || !c) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull || (m + 127) / 128 > 65535)
+    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
+  bool full = k % 8 == 0 && aligned16(a) && aligned16(b);
+  const char* name = epilogue == TILER_HIP_EPILOGUE_SILU
+                         ? (full ? "tiler_contract_bf16_silu_t128" : "tiler_contract_bf16_silu_t128_k")
+                         : (full ? "tiler_contract_bf16_t128" : "tiler_contract_bf16_t128_k");
+  uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
+  void* args[] = {&a, &b, &m32, &n32, &k32, &c};
+  return launch(ctx, name, (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 256,
+                pick(ctx, stream), args);
+}
+
+}  // extern "C"
