@@ -238,6 +238,17 @@ tiler_hip_status tiler_hip_event_elapsed_ms(tiler_hip_context *ctx, tiler_hip_ev
                                             tiler_hip_event stop, float *ms);
 tiler_hip_status tiler_hip_event_destroy(tiler_hip_context *ctx, tiler_hip_event ev);
 
+/* Graph capture of a launch sequence (hipStreamBeginCapture ... hipGraphInstantiate),
+ * for launch-bound loops: every family entry point below may be captured.  The
+ * stream must not be the legacy NULL stream; NULL selects the context stream. */
+typedef void *tiler_hip_graph;
+tiler_hip_status tiler_hip_capture_begin(tiler_hip_context *ctx, tiler_hip_stream stream);
+tiler_hip_status tiler_hip_capture_end(tiler_hip_context *ctx, tiler_hip_stream stream,
+                                       tiler_hip_graph *out);
+tiler_hip_status tiler_hip_graph_launch(tiler_hip_context *ctx, tiler_hip_graph graph,
+                                        tiler_hip_stream stream);
+tiler_hip_status tiler_hip_graph_destroy(tiler_hip_context *ctx, tiler_hip_graph graph);
+
 /* ------------------------------------------------------------------------
  * Realization families.  Each replaces one ScalarProgram x ReductionTopology
  * cell the planner selects (tiler-ir/src/schedule/model.rs:661-920,

@@ -194,6 +194,10 @@ SIGNATURES = {
     "tiler_hip_event_record": (_S, [_CTX, _P, _P]),
     "tiler_hip_event_elapsed_ms": (_S, [_CTX, _P, _P, ctypes.POINTER(_F)]),
     "tiler_hip_event_destroy": (_S, [_CTX, _P]),
+    "tiler_hip_capture_begin": (_S, [_CTX, _P]),
+    "tiler_hip_capture_end": (_S, [_CTX, _P, ctypes.POINTER(_P)]),
+    "tiler_hip_graph_launch": (_S, [_CTX, _P, _P]),
+    "tiler_hip_graph_destroy": (_S, [_CTX, _P]),
     "tiler_hip_sum_f32": (_S, [_CTX, _P, _U64, _U64, _P, ctypes.POINTER(SumPlan), _P]),
     "tiler_hip_sum_tree_workgroups": (_U32, [_CTX, _U64]),
     "tiler_hip_rms_norm": (_S, [_CTX, _U32, _P, _P, _I32, _U64, _U64, _U32, _P, _P]),

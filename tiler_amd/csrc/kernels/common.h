@@ -108,7 +108,9 @@ __device__ __forceinline__ float rsqrt_f32_cr(float t) {
 // polynomial (truncation < 2^-64), times the binary64 table entry 2^(j/64),
 // scaled by 2^(k>>6), then one rounding to binary32.  The binary64 value is
 // within 2^-50 relative of e^s.
-__device__ __forceinline__ double exp_f64_core(double x, int& m_out) {
+// `table` is kExp2Table64 or a copy of it in LDS (divergent lookups from LDS
+// keep the vector-memory path free for the streamed operands).
+__device__ __forceinline__ double exp_f64_core(double x, int& m_out, const double* table) {
   double kd = __builtin_rint(x * TILER_64_OVER_LN2);
   int k = (int)kd;
   double r = __builtin_fma(-kd, TILER_LN2_OVER_64_HI, x);
@@ -121,14 +123,14 @@ __device__ __forceinline__ double exp_f64_core(double x, int& m_out) {
   p = __builtin_fma(p, r, 1.0);
   p = __builtin_fma(p, r, 1.0);
   m_out = k >> 6;
-  return kExp2Table64[k & 63] * p;
+  return table[k & 63] * p;
 }
-__device__ __forceinline__ float exp_f32_cr(float s) {
+__device__ __forceinline__ float exp_f32_cr(float s, const double* table = kExp2Table64) {
   if (s != s) return s;
   if (s >= 89.0f) return __builtin_huge_valf();
   if (s <= -104.0f) return 0.0f;
   int m;
-  double v = exp_f64_core((double)s, m);
+  double v = exp_f64_core((double)s, m, table);
   v = __builtin_ldexp(v, m);
   return (float)v;
 }

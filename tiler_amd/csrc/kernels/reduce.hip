@@ -10,11 +10,11 @@
 //   * tiler_sum_f32_cooperative  CooperativeWorkgroup: one workgroup per output
 //                                with a declared (participants, contributors,
 //                                rounds, layout) grouping, evaluate.rs:845-1158.
-//   * tiler_sum_f32_grid /       The reassociating two-level tree (a
+//   * tiler_sum_f32_grid(+final)/ The reassociating two-level tree (a
 //     tiler_sum_f32_rows         REASSOCIATE-class contract): wave64 xor
 //                                butterflies, an ascending cross-wave fold in LDS
-//                                and, for one output, a last-workgroup combine of
-//                                the workgroup partials in the same launch.
+//                                and, for one output, a second one-workgroup
+//                                launch combining the workgroup partials.
 // The first three are bit-exact with the reference; the tree's exact order is
 // its declared grouping, restated by the oracle's grid/row grouped sums.
 #include "common.h"
@@ -99,18 +99,16 @@ __device__ __forceinline__ float block_sum256(float v, float* lds4) {
   return s;
 }
 
-// One output over n contributors.  Tile = 1024 elements (256 threads x 4);
-// workgroup b folds tiles b, b+G, ... in ascending (tile, component) order per
-// thread; workgroup partial -> partials[b]; the last workgroup to arrive (a
-// device-scope ticket) folds the partials (thread t takes t, t+256, ...) with
-// the same in-workgroup combine and re-arms the ticket for the next launch.
+// One output over n contributors, two launches.  Tile = 1024 elements
+// (256 threads x 4); stage 1: workgroup b folds tiles b, b+G, ... in
+// ascending (tile, component) order per thread and writes its partial;
+// stage 2 (one workgroup): thread t folds partials t, t+256, ..., then the
+// same in-workgroup combine.  The kernel boundary orders the partials: no
+// device-scope fence is taken per workgroup (each costs an L2 write-back).
 template <bool kAligned>
-__device__ __forceinline__ void sum_grid_body(const float* __restrict__ x, uint64_t n,
-                                              float* __restrict__ out,
-                                              float* __restrict__ partials,
-                                              uint32_t* __restrict__ ticket) {
+__device__ __forceinline__ void sum_stage1_body(const float* __restrict__ x, uint64_t n,
+                                                float* __restrict__ partials) {
   __shared__ float lds4[4];
-  __shared__ uint32_t is_last;
   const uint32_t t = threadIdx.x, b = blockIdx.x, G = gridDim.x;
   const uint64_t tiles = (n + 1023) >> 10;
   const uint64_t full = n >> 10;
@@ -140,34 +138,26 @@ __device__ __forceinline__ void sum_grid_body(const float* __restrict__ x, uint6
       if (base + e < n) acc = acc + x[base + e];
   }
   float s = block_sum256(acc, lds4);
-  if (t == 0) {
-    partials[b] = s;
-    __threadfence();
-    uint32_t prev = atomicAdd(ticket, 1u);
-    is_last = (prev == G - 1) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  float a2 = -0.0f;
-  for (uint32_t i = t; i < G; i += 256) a2 = a2 + __hip_atomic_load(&partials[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();  // lds4 reuse
-  float total = block_sum256(a2, lds4);
-  if (t == 0) {
-    out[0] = n == 0 ? 0.0f : canon(total);
-    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (t == 0) partials[b] = s;
 }
 
 extern "C" __global__ void __launch_bounds__(256)
-tiler_sum_f32_grid(const float* __restrict__ x, uint64_t n, float* __restrict__ out,
-                   float* __restrict__ partials, uint32_t* __restrict__ ticket) {
-  sum_grid_body<true>(x, n, out, partials, ticket);
+tiler_sum_f32_grid(const float* __restrict__ x, uint64_t n, float* __restrict__ partials) {
+  sum_stage1_body<true>(x, n, partials);
 }
 extern "C" __global__ void __launch_bounds__(256)
-tiler_sum_f32_grid_unaligned(const float* __restrict__ x, uint64_t n, float* __restrict__ out,
-                             float* __restrict__ partials, uint32_t* __restrict__ ticket) {
-  sum_grid_body<false>(x, n, out, partials, ticket);
+tiler_sum_f32_grid_unaligned(const float* __restrict__ x, uint64_t n,
+                             float* __restrict__ partials) {
+  sum_stage1_body<false>(x, n, partials);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_sum_f32_grid_final(const float* __restrict__ partials, uint32_t G, uint64_t n,
+                         float* __restrict__ out) {
+  __shared__ float lds4[4];
+  float acc = -0.0f;
+  for (uint32_t i = threadIdx.x; i < G; i += 256) acc = acc + partials[i];
+  float total = block_sum256(acc, lds4);
+  if (threadIdx.x == 0) out[0] = n == 0 ? 0.0f : canon(total);
 }
 
 // Many outputs: one 256-thread workgroup per row of `extent` contributors,

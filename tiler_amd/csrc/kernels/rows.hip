@@ -26,14 +26,16 @@ constexpr uint32_t kWavesPerBlock = 4;
 // narrowed to bf16 for bf16 storage (ADR 0091 narrowing).  The weight is
 // either one row broadcast over all rows (w_row_stride 0) or a full tensor.
 
-template <int CH, bool AL>
+template <int CH, int AL>
 __device__ __forceinline__ void rms_bf16_row(const uint16_t* __restrict__ x,
                                              const uint16_t* __restrict__ w,
                                              uint16_t* __restrict__ y, uint32_t extent,
                                              float eps, uint32_t lane) {
-  // chunk c covers positions [c*512 + lane*8, +8)
+  // chunk c covers positions [c*512 + lane*8, +8); x stays packed (4 VGPRs per
+  // chunk) between the fold and the epilogue.
   u32x4 xv[CH];
-  const uint32_t nfull = AL ? extent >> 9 : 0;  // chunks loaded as whole 16 B
+  // AL: 2 every chunk whole (extent == CH*512, no guards), 1 aligned rows, 0 unaligned
+  const uint32_t nfull = AL == 2 ? CH : AL ? extent >> 9 : 0;  // chunks loaded as whole 16 B
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     uint32_t p0 = c * 512u + lane * 8u;
@@ -51,23 +53,25 @@ __device__ __forceinline__ void rms_bf16_row(const uint16_t* __restrict__ x,
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     uint32_t p0 = c * 512u + lane * 8u;
-    uint32_t words[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       if ((uint32_t)c < nfull || p0 + e < extent) {
-        float v = bf16_widen((words[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        float v = bf16_widen((xv[c][e >> 1] >> (16 * (e & 1))) & 0xffffu);
         float sq = v * v;
         acc = acc + sq;
       }
     }
   }
+  // Opaque to the optimizer: the epilogue re-widens from the packed words
+  // instead of keeping 8*CH widened floats live across the butterfly.
+#pragma unroll
+  for (int c = 0; c < CH; ++c) asm volatile("" : "+v"(xv[c]));
   float total = tiler::wave_sum_butterfly(acc);
   float mean = total / (float)extent;
   float s = tiler::rsqrt_f32_cr(mean + eps);
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     uint32_t p0 = c * 512u + lane * 8u;
-    uint32_t words[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
     u32x4 wv;
     if ((uint32_t)c < nfull) {
       wv = *reinterpret_cast<const u32x4*>(w + p0);
@@ -78,34 +82,32 @@ __device__ __forceinline__ void rms_bf16_row(const uint16_t* __restrict__ x,
         if (p0 + e < extent) tmp[e >> 1] |= (uint32_t)w[p0 + e] << (16 * (e & 1));
       wv = u32x4{tmp[0], tmp[1], tmp[2], tmp[3]};
     }
-    uint32_t wwords[4] = {wv.x, wv.y, wv.z, wv.w};
-    uint32_t out[4];
+    u32x4 o;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      float x0 = bf16_widen(words[h] & 0xffffu), x1 = bf16_widen(words[h] >> 16);
-      float w0 = bf16_widen(wwords[h] & 0xffffu), w1 = bf16_widen(wwords[h] >> 16);
+      float x0 = bf16_widen(xv[c][h] & 0xffffu), x1 = bf16_widen(xv[c][h] >> 16);
+      float w0 = bf16_widen(wv[h] & 0xffffu), w1 = bf16_widen(wv[h] >> 16);
       float n0 = x0 * s, n1 = x1 * s;
       float y0 = w0 * n0, y1 = w1 * n1;
-      out[h] = tiler::bf16_pack2(y0, y1);
+      o[h] = tiler::bf16_pack2(y0, y1);
     }
     if ((uint32_t)c < nfull) {
-      __builtin_nontemporal_store(u32x4{out[0], out[1], out[2], out[3]},
-                                  reinterpret_cast<u32x4*>(y + p0));
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(y + p0));
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (p0 + e < extent) y[p0 + e] = (uint16_t)(out[e >> 1] >> (16 * (e & 1)));
+        if (p0 + e < extent) y[p0 + e] = (uint16_t)(o[e >> 1] >> (16 * (e & 1)));
     }
   }
 }
 
-template <int CH, bool AL>
+template <int CH, int AL>
 __device__ __forceinline__ void rms_f32_row(const float* __restrict__ x,
                                             const float* __restrict__ w, float* __restrict__ y,
                                             uint32_t extent, float eps, uint32_t lane) {
   // chunk c covers positions [c*256 + lane*4, +4)
   f32x4 xv[CH];
-  const uint32_t nfull = AL ? extent >> 8 : 0;
+  const uint32_t nfull = AL == 2 ? CH : AL ? extent >> 8 : 0;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     uint32_t p0 = c * 256u + lane * 4u;
@@ -169,12 +171,12 @@ __device__ __forceinline__ void rms_f32_row(const float* __restrict__ x,
 // -0 < +0 is associative and commutative, softmax/tests.rs:112-147);
 // e = exp(fl(x - m)) correctly rounded; d = sum of e in the declared grouping;
 // y = canon(fl(e * fl(1/d))) -- the reciprocal multiply, not a division.
-template <int CH, bool AL>
+template <int CH, int AL>
 __device__ __forceinline__ void softmax_f32_row(const float* __restrict__ x,
                                                 float* __restrict__ y, uint32_t extent,
-                                                uint32_t lane) {
+                                                uint32_t lane, const double* exp_table) {
   f32x4 xv[CH];
-  const uint32_t nfull = AL ? extent >> 8 : 0;
+  const uint32_t nfull = AL == 2 ? CH : AL ? extent >> 8 : 0;
   const float ninf = -__builtin_huge_valf();
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -207,7 +209,7 @@ __device__ __forceinline__ void softmax_f32_row(const float* __restrict__ x,
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       bool live = (uint32_t)c < nfull || p0 + e < extent;
-      float ex = tiler::exp_f32_cr(v4[e] - m);
+      float ex = tiler::exp_f32_cr(v4[e] - m, exp_table);
       v4[e] = ex;
       if (live) acc = acc + ex;
     }
@@ -235,28 +237,44 @@ __device__ __forceinline__ void softmax_f32_row(const float* __restrict__ x,
 
 // Entry points: one 256-thread workgroup = 4 rows (one per wave).  CH is the
 // number of 16-byte chunks per lane, the smallest power of two covering the
-// row; the host picks the instance.  The plain instances load whole 16-byte
-// chunks and need every row 16-byte aligned (aligned base, extent*elem % 16 ==
-// 0); the _u instances load element by element in the same order.
-#define TILER_RMS_BF16(CH, AL, SFX)                                                         \
-  extern "C" __global__ void __launch_bounds__(256) tiler_rms_norm_bf16_ch##CH##SFX(             \
+// row; the host picks the instance.  The _full instances serve rows of exactly
+// CH whole chunks with no guards; the plain instances load whole 16-byte chunks
+// and need every row 16-byte aligned (aligned base, extent*elem % 16 == 0);
+// the _u instances load element by element in the same order.
+// bf16 RMSNorm workgroups are WAVES waves (one row each).  With a broadcast
+// weight (w_row_stride 0) and aligned rows the weight row is staged once per
+// workgroup in LDS (up to 8192 bf16) and every wave's epilogue reads it there.
+#define TILER_RMS_BF16(CH, AL, SFX, WAVES)                                                  \
+  extern "C" __global__ void __launch_bounds__(64 * WAVES) tiler_rms_norm_bf16_ch##CH##SFX(      \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint64_t w_row_stride, \
       uint16_t* __restrict__ y, uint64_t rows, uint32_t extent, float eps) {                 \
-    uint64_t row = (uint64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);             \
+    __shared__ __attribute__((aligned(16))) uint16_t wl[AL ? CH * 512 : 8];                \
+    const uint64_t row = (uint64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);                \
+    const bool stage = AL && w_row_stride == 0;                                             \
+    if (stage) {                                                                            \
+      for (uint32_t i = threadIdx.x; i * 8u < extent; i += blockDim.x)                    \
+        *reinterpret_cast<u32x4*>(wl + i * 8u) = *reinterpret_cast<const u32x4*>(w + i * 8u); \
+      __syncthreads();                                                                      \
+    }                                                                                       \
     if (row >= rows) return;                                                                \
-    rms_bf16_row<CH, AL>(x + row * extent, w + row * w_row_stride, y + row * extent, extent,     \
-                     eps, threadIdx.x & 63u);                                               \
+    rms_bf16_row<CH, AL>(x + row * extent, stage ? wl : w + row * w_row_stride,            \
+                         y + row * extent, extent, eps, threadIdx.x & 63u);                \
   }
-TILER_RMS_BF16(1, true, )
-TILER_RMS_BF16(1, false, _u)
-TILER_RMS_BF16(2, true, )
-TILER_RMS_BF16(2, false, _u)
-TILER_RMS_BF16(4, true, )
-TILER_RMS_BF16(4, false, _u)
-TILER_RMS_BF16(8, true, )
-TILER_RMS_BF16(8, false, _u)
-TILER_RMS_BF16(16, true, )
-TILER_RMS_BF16(16, false, _u)
+TILER_RMS_BF16(1, 2, _full, 16)
+TILER_RMS_BF16(1, 1, , 16)
+TILER_RMS_BF16(1, 0, _u, 16)
+TILER_RMS_BF16(2, 2, _full, 16)
+TILER_RMS_BF16(2, 1, , 16)
+TILER_RMS_BF16(2, 0, _u, 16)
+TILER_RMS_BF16(4, 2, _full, 16)
+TILER_RMS_BF16(4, 1, , 16)
+TILER_RMS_BF16(4, 0, _u, 16)
+TILER_RMS_BF16(8, 2, _full, 16)
+TILER_RMS_BF16(8, 1, , 16)
+TILER_RMS_BF16(8, 0, _u, 16)
+TILER_RMS_BF16(16, 2, _full, 4)
+TILER_RMS_BF16(16, 1, , 4)
+TILER_RMS_BF16(16, 0, _u, 4)
 
 #define TILER_RMS_F32(CH, AL, SFX)                                                          \
   extern "C" __global__ void __launch_bounds__(256) tiler_rms_norm_f32_ch##CH##SFX(              \
@@ -267,35 +285,50 @@ TILER_RMS_BF16(16, false, _u)
     rms_f32_row<CH, AL>(x + row * extent, w + row * w_row_stride, y + row * extent, extent, eps, \
                     threadIdx.x & 63u);                                                     \
   }
-TILER_RMS_F32(1, true, )
-TILER_RMS_F32(1, false, _u)
-TILER_RMS_F32(2, true, )
-TILER_RMS_F32(2, false, _u)
-TILER_RMS_F32(4, true, )
-TILER_RMS_F32(4, false, _u)
-TILER_RMS_F32(8, true, )
-TILER_RMS_F32(8, false, _u)
-TILER_RMS_F32(16, true, )
-TILER_RMS_F32(16, false, _u)
-TILER_RMS_F32(32, true, )
-TILER_RMS_F32(32, false, _u)
+TILER_RMS_F32(1, 2, _full)
+TILER_RMS_F32(1, 1, )
+TILER_RMS_F32(1, 0, _u)
+TILER_RMS_F32(2, 2, _full)
+TILER_RMS_F32(2, 1, )
+TILER_RMS_F32(2, 0, _u)
+TILER_RMS_F32(4, 2, _full)
+TILER_RMS_F32(4, 1, )
+TILER_RMS_F32(4, 0, _u)
+TILER_RMS_F32(8, 2, _full)
+TILER_RMS_F32(8, 1, )
+TILER_RMS_F32(8, 0, _u)
+TILER_RMS_F32(16, 2, _full)
+TILER_RMS_F32(16, 1, )
+TILER_RMS_F32(16, 0, _u)
+TILER_RMS_F32(32, 2, _full)
+TILER_RMS_F32(32, 1, )
+TILER_RMS_F32(32, 0, _u)
 
 #define TILER_SOFTMAX_F32(CH, AL, SFX)                                                      \
   extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_ch##CH##SFX(               \
       const float* __restrict__ x, float* __restrict__ y, uint64_t rows, uint32_t extent) {  \
+    __shared__ double tab[64];                                                              \
+    if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Table64[threadIdx.x];                     \
+    __syncthreads();                                                                        \
     uint64_t row = (uint64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);             \
     if (row >= rows) return;                                                                \
-    softmax_f32_row<CH, AL>(x + row * extent, y + row * extent, extent, threadIdx.x & 63u);     \
+    softmax_f32_row<CH, AL>(x + row * extent, y + row * extent, extent, threadIdx.x & 63u, tab); \
   }
-TILER_SOFTMAX_F32(1, true, )
-TILER_SOFTMAX_F32(1, false, _u)
-TILER_SOFTMAX_F32(2, true, )
-TILER_SOFTMAX_F32(2, false, _u)
-TILER_SOFTMAX_F32(4, true, )
-TILER_SOFTMAX_F32(4, false, _u)
-TILER_SOFTMAX_F32(8, true, )
-TILER_SOFTMAX_F32(8, false, _u)
-TILER_SOFTMAX_F32(16, true, )
-TILER_SOFTMAX_F32(16, false, _u)
-TILER_SOFTMAX_F32(32, true, )
-TILER_SOFTMAX_F32(32, false, _u)
+TILER_SOFTMAX_F32(1, 2, _full)
+TILER_SOFTMAX_F32(1, 1, )
+TILER_SOFTMAX_F32(1, 0, _u)
+TILER_SOFTMAX_F32(2, 2, _full)
+TILER_SOFTMAX_F32(2, 1, )
+TILER_SOFTMAX_F32(2, 0, _u)
+TILER_SOFTMAX_F32(4, 2, _full)
+TILER_SOFTMAX_F32(4, 1, )
+TILER_SOFTMAX_F32(4, 0, _u)
+TILER_SOFTMAX_F32(8, 2, _full)
+TILER_SOFTMAX_F32(8, 1, )
+TILER_SOFTMAX_F32(8, 0, _u)
+TILER_SOFTMAX_F32(16, 2, _full)
+TILER_SOFTMAX_F32(16, 1, )
+TILER_SOFTMAX_F32(16, 0, _u)
+TILER_SOFTMAX_F32(32, 2, _full)
+TILER_SOFTMAX_F32(32, 1, )
+TILER_SOFTMAX_F32(32, 0, _u)

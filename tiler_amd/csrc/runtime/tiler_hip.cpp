@@ -38,42 +38,60 @@ const EntryRow kEntries[] = {
     {"tiler_sum_f32_serial", "strict-serial-sum-f32/serial", 2},
     {"tiler_sum_f32_partials", "strict-serial-sum-f32/multipass", 2},
     {"tiler_sum_f32_cooperative", "strict-serial-sum-f32/cooperative-workgroup", 2},
-    {"tiler_sum_f32_grid", "strict-serial-sum-f32/tree", 4},
-    {"tiler_sum_f32_grid_unaligned", "strict-serial-sum-f32/tree", 4},
+    {"tiler_sum_f32_grid", "strict-serial-sum-f32/tree", 2},
+    {"tiler_sum_f32_grid_unaligned", "strict-serial-sum-f32/tree", 2},
+    {"tiler_sum_f32_grid_final", "strict-serial-sum-f32/tree", 2},
     {"tiler_sum_f32_rows", "strict-serial-sum-f32/tree", 2},
     {"tiler_rms_norm_bf16_ch1", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch1_full", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch1_u", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch2", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch2_full", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch2_u", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch4", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch4_full", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch4_u", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch8", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch8_full", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch8_u", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch16", "rms-norm/bf16", 3},
+    {"tiler_rms_norm_bf16_ch16_full", "rms-norm/bf16", 3},
     {"tiler_rms_norm_bf16_ch16_u", "rms-norm/bf16", 3},
     {"tiler_rms_norm_f32_ch1", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch1_full", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch1_u", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch2", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch2_full", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch2_u", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch4", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch4_full", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch4_u", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch8", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch8_full", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch8_u", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch16", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch16_full", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch16_u", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch32", "rms-norm-f32", 3},
+    {"tiler_rms_norm_f32_ch32_full", "rms-norm-f32", 3},
     {"tiler_rms_norm_f32_ch32_u", "rms-norm-f32", 3},
     {"tiler_softmax_f32_ch1", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch1_full", "softmax-f32", 2},
     {"tiler_softmax_f32_ch1_u", "softmax-f32", 2},
     {"tiler_softmax_f32_ch2", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch2_full", "softmax-f32", 2},
     {"tiler_softmax_f32_ch2_u", "softmax-f32", 2},
     {"tiler_softmax_f32_ch4", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch4_full", "softmax-f32", 2},
     {"tiler_softmax_f32_ch4_u", "softmax-f32", 2},
     {"tiler_softmax_f32_ch8", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch8_full", "softmax-f32", 2},
     {"tiler_softmax_f32_ch8_u", "softmax-f32", 2},
     {"tiler_softmax_f32_ch16", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch16_full", "softmax-f32", 2},
     {"tiler_softmax_f32_ch16_u", "softmax-f32", 2},
     {"tiler_softmax_f32_ch32", "softmax-f32", 2},
+    {"tiler_softmax_f32_ch32_full", "softmax-f32", 2},
     {"tiler_softmax_f32_ch32_u", "softmax-f32", 2},
     {"tiler_gather_u128", "gather", 4},
     {"tiler_gather_u64", "gather", 4},
@@ -114,10 +132,9 @@ struct tiler_hip_context {
   std::unordered_map<std::string, hipFunction_t> fns;
   std::vector<hipModule_t> routed_modules;
   std::vector<hipFunction_t> prepared;
-  // workspace: [partials kMaxSumWorkgroups f32][ticket u32 + pad][gather_bad u64]
+  // workspace: [sum partials kMaxSumWorkgroups f32][gather_bad u64 + pad]
   uint8_t* workspace = nullptr;
   float* sum_partials = nullptr;
-  uint32_t* sum_ticket = nullptr;
   unsigned long long* gather_bad = nullptr;
   uint32_t compute_units = 0;
   uint64_t lds_bytes = 0;
@@ -302,7 +319,7 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
     }
     ctx->fns[kEntries[i].symbol] = f;
   }
-  const uint64_t ws_bytes = kMaxSumWorkgroups * 4 + 256 + 256;
+  const uint64_t ws_bytes = kMaxSumWorkgroups * 4 + 256;
   if (hipMalloc(&ctx->workspace, ws_bytes) != hipSuccess) {
     copy_text(diagnostic, diagnostic_bytes, "workspace allocation failed");
     hipModuleUnload(ctx->module);
@@ -311,8 +328,7 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
     return TILER_HIP_REFUSE_CAPACITY;
   }
   ctx->sum_partials = reinterpret_cast<float*>(ctx->workspace);
-  ctx->sum_ticket = reinterpret_cast<uint32_t*>(ctx->workspace + kMaxSumWorkgroups * 4);
-  ctx->gather_bad = reinterpret_cast<unsigned long long*>(ctx->workspace + kMaxSumWorkgroups * 4 + 256);
+  ctx->gather_bad = reinterpret_cast<unsigned long long*>(ctx->workspace + kMaxSumWorkgroups * 4);
   hipMemset(ctx->workspace, 0, ws_bytes);
   hipMemset(ctx->gather_bad, 0xff, 8);
   hipDeviceSynchronize();
@@ -588,10 +604,53 @@ tiler_hip_status tiler_hip_event_destroy(tiler_hip_context* ctx, tiler_hip_event
   return TILER_HIP_OK;
 }
 
+struct GraphHandle {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+tiler_hip_status tiler_hip_capture_begin(tiler_hip_context* ctx, tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipError_t e = hipStreamBeginCapture(pick(ctx, stream), hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, std::string("capture: ") + hipGetErrorString(e));
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_capture_end(tiler_hip_context* ctx, tiler_hip_stream stream,
+                                       tiler_hip_graph* out) {
+  if (!ctx || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  auto* g = new GraphHandle();
+  hipError_t e = hipStreamEndCapture(pick(ctx, stream), &g->graph);
+  if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
+    return fail(ctx, TILER_HIP_FAIL_LAUNCH, std::string("graph: ") + hipGetErrorString(e));
+  }
+  *out = g;
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_graph_launch(tiler_hip_context* ctx, tiler_hip_graph graph,
+                                        tiler_hip_stream stream) {
+  if (!ctx || !graph) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipError_t e = hipGraphLaunch(static_cast<GraphHandle*>(graph)->exec, pick(ctx, stream));
+  if (e != hipSuccess) return fail(ctx, TILER_HIP_FAIL_LAUNCH, std::string("graph launch: ") + hipGetErrorString(e));
+  return TILER_HIP_OK;
+}
+tiler_hip_status tiler_hip_graph_destroy(tiler_hip_context* ctx, tiler_hip_graph graph) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  auto* g = static_cast<GraphHandle*>(graph);
+  if (g) {
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
+  }
+  return TILER_HIP_OK;
+}
+
 // ---------------------------------------------------------------------------
 uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context* ctx, uint64_t n) {
   uint64_t tiles = (n + 1023) / 1024;
-  uint64_t cap = ctx ? 4ull * ctx->compute_units : 1024;
+  uint64_t cap = ctx ? 2ull * ctx->compute_units : 512;
   if (cap > kMaxSumWorkgroups) cap = kMaxSumWorkgroups;
   uint64_t g = tiles < cap ? tiles : cap;
   return g ? (uint32_t)g : 1u;
@@ -641,10 +700,13 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
       if (rows == 1) {
         uint32_t G = tiler_hip_sum_tree_workgroups(ctx, extent);
         float* partials = ctx->sum_partials;
-        uint32_t* ticket = ctx->sum_ticket;
         uint64_t n = extent;
-        void* args[] = {&x, &n, &out, &partials, &ticket};
-        return launch(ctx, aligned16(x) ? "tiler_sum_f32_grid" : "tiler_sum_f32_grid_unaligned", G, 1, 256, s, args);
+        void* a1[] = {&x, &n, &partials};
+        tiler_hip_status st = launch(ctx, aligned16(x) ? "tiler_sum_f32_grid" : "tiler_sum_f32_grid_unaligned", G, 1, 256, s, a1);
+        if (st != TILER_HIP_OK) return st;
+        const float* cp = partials;
+        void* a2[] = {&cp, &G, &n, &out};
+        return launch(ctx, "tiler_sum_f32_grid_final", 1, 1, 256, s, a2);
       }
       void* args[] = {&x, &extent, &out};
       return launch(ctx, "tiler_sum_f32_rows", (uint32_t)rows, 1, 256, s, args);
@@ -676,12 +738,17 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, cons
     return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row longer than the register-resident realization");
   const uint64_t elem = dtype == TILER_HIP_BF16 ? 2 : 4;
   bool al = aligned16(x) && aligned16(w) && aligned16(y) && (extent * elem) % 16 == 0;
+  bool full = al && extent == (uint64_t)ch * 64 * vec;
   char name[64];
   std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_ch%u%s",
-                dtype == TILER_HIP_BF16 ? "bf16" : "f32", ch, al ? "" : "_u");
+                dtype == TILER_HIP_BF16 ? "bf16" : "f32", ch, full ? "_full" : al ? "" : "_u");
   uint64_t wstride = weight_broadcast ? 0 : extent;
   uint32_t ext32 = (uint32_t)extent;
   void* args[] = {&x, &w, &wstride, &y, &rows, &ext32, &eps};
+  if (dtype == TILER_HIP_BF16) {  // one row per wave: 16-wave workgroups, 4 for the longest rows
+    const uint32_t waves = ch <= 8 ? 16u : 4u;
+    return launch(ctx, name, (uint32_t)((rows + waves - 1) / waves), 1, 64 * waves, pick(ctx, stream), args);
+  }
   return launch(ctx, name, (uint32_t)((rows + 3) / 4), 1, 256, pick(ctx, stream), args);
 }
 
@@ -694,8 +761,9 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
   if (ch > 32 || extent > 0xffffffffull)
     return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row longer than the register-resident realization");
   bool al = aligned16(x) && aligned16(y) && extent % 4 == 0;
+  bool full = al && extent == (uint64_t)ch * 256;
   char name[64];
-  std::snprintf(name, sizeof(name), "tiler_softmax_f32_ch%u%s", ch, al ? "" : "_u");
+  std::snprintf(name, sizeof(name), "tiler_softmax_f32_ch%u%s", ch, full ? "_full" : al ? "" : "_u");
   uint32_t ext32 = (uint32_t)extent;
   void* args[] = {&x, &y, &rows, &ext32};
   return launch(ctx, name, (uint32_t)((rows + 3) / 4), 1, 256, pick(ctx, stream), args);

@@ -184,6 +184,21 @@ class Context:
     def destroy_event(self, event: int):
         L.lib().tiler_hip_event_destroy(self.handle, event)
 
+    # -- graph capture (launch-bound loops) ------------------------------------
+    def capture_begin(self, stream=None):
+        self._check(L.lib().tiler_hip_capture_begin(self.handle, stream), "capture_begin")
+
+    def capture_end(self, stream=None) -> int:
+        g = ctypes.c_void_p()
+        self._check(L.lib().tiler_hip_capture_end(self.handle, stream, ctypes.byref(g)), "capture_end")
+        return g.value
+
+    def graph_launch(self, graph: int, stream=None):
+        self._check(L.lib().tiler_hip_graph_launch(self.handle, graph, stream), "graph_launch")
+
+    def graph_destroy(self, graph: int):
+        self._check(L.lib().tiler_hip_graph_destroy(self.handle, graph), "graph_destroy")
+
     def fill_u32(self, buf, value: int, words: int, stream=None):
         self._check(L.lib().tiler_hip_fill_u32(self.handle, _ptr(buf), value, words, stream),
                     "fill_u32")
