@@ -198,7 +198,8 @@ def _frob(got_bits, ref32):
     return float(np.linalg.norm(g - r) / np.linalg.norm(r))
 
 
-@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (256, 384, 512), (200, 136, 72), (77, 45, 13), (1, 300, 1000)])
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (256, 384, 512), (200, 136, 72), (77, 45, 13), (1, 300, 1000),
+                                   (256, 256, 64), (512, 768, 1024), (1024, 2048, 256)])
 @pytest.mark.parametrize("silu", [False, True])
 def test_bf16_contraction_within_frobenius_bound(ctx, m, n, k, silu):
     rng = np.random.default_rng(m * n + k)

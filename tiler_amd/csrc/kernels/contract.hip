@@ -163,6 +163,167 @@ __device__ __forceinline__ void contract_bf16_body(const uint16_t* __restrict__ 
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Tile-aligned bf16 contraction: m, n multiples of 256, k a multiple of 64,
+// 16-byte aligned operands (the host checks).  One 256-thread workgroup per
+// 256x256 output tile; wave (wm, wn) owns a 128x128 sub-tile held in 16
+// accumulator blocks of v_mfma_f32_32x32x16_bf16 (256 f32 per lane, one wave
+// per SIMD).  Operand tiles of 256 rows x 64 k move global -> LDS with
+// global_load_lds_dwordx4 (no VGPR staging), double-buffered (2 x 64 KiB).
+// LDS rows are 128 B; 16-byte chunk c of row r sits at chunk c ^ (r & 7), so
+// the eight rows a ds_read_b128 phase touches fall in distinct banks.
+// Workgroups are mapped XCD-aware: the 8 XCDs receive workgroups round robin,
+// and the 32 a given XCD runs form a 4 x 8 block of tiles sharing 4 A and 8 B
+// panels in that XCD's L2.  The epilogue (SiLU on the f32 accumulator, one
+// bf16 narrowing) transposes through LDS so C leaves in 16-byte row chunks.
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kT = 256, kK = 64;
+
+__device__ __forceinline__ float silu_fast(float v) {
+  // Epilogue SiLU: hardware exp2 and reciprocal (relative error ~1e-7),
+  // far inside the bf16 narrowing that follows; -inf -> NaN, +inf -> +inf,
+  // large negative -> -0 as the reference's formula gives.
+  float e = __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
+  return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// Issues the direct-to-LDS loads of one 256 x 64 operand tile.  Wave w
+// covers rows [w*64, w*64+64) in 8 instructions of 8 rows: lane i fills row
+// R + i/8, physical chunk i%8, which holds logical chunk (i%8) ^ ((i/8)&7).
+__device__ __forceinline__ void issue_tile(const uint16_t* __restrict__ g, uint32_t ld,
+                                           uint32_t r0, uint32_t k0, uint16_t* lds_tile,
+                                           uint32_t wave, uint32_t lane) {
+  const uint32_t sub = lane >> 3, phys = lane & 7u;
+  const uint32_t logical = phys ^ (sub & 7u);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t R = wave * 64u + j * 8u;
+    const uint16_t* src = g + (uint64_t)(r0 + R + sub) * ld + k0 + logical * 8u;
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                     (lds_void*)(lds_tile + R * kK), 16, 0, 0);
+  }
+}
+
+template <bool kSilu>
+__device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restrict__ a,
+                                                        const uint16_t* __restrict__ b,
+                                                        uint32_t m, uint32_t n, uint32_t k,
+                                                        uint16_t* __restrict__ c) {
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * 2 * kT * kK];  // [buf][A|B][256][64]
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t wm = wave >> 1, wn = wave & 1u;
+
+  // XCD-aware tile order: workgroup id -> (xcd, slot); xcd picks a 4x8 block
+  // of the tile grid, slot a tile inside it.  Falls back to row-major when the
+  // grid is not a whole number of 4x8 blocks per XCD.
+  const uint32_t tiles_n = n / kT, tiles_m = m / kT;
+  uint32_t tm, tn;
+  {
+    const uint32_t id = blockIdx.x;
+    const uint32_t total = tiles_m * tiles_n;
+    if (tiles_m % 4 == 0 && tiles_n % 8 == 0 && total % 256 == 0) {
+      const uint32_t xcd = id & 7u, slot = id >> 3;          // slot: 0 .. total/8-1
+      const uint32_t blocks_n = tiles_n / 8;                 // 4x8 blocks across n
+      const uint32_t blk = xcd + 8u * (slot >> 5);           // block index
+      const uint32_t in = slot & 31u;
+      tm = (blk / blocks_n) * 4u + (in >> 3);
+      tn = (blk % blocks_n) * 8u + (in & 7u);
+    } else {
+      tm = id / tiles_n;
+      tn = id % tiles_n;
+    }
+  }
+  const uint32_t m0 = tm * kT, n0 = tn * kT;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // buffer s: A at smem + s*2*kT*kK, B right after it
+  issue_tile(a, k, m0, 0, smem, wave, lane);
+  issue_tile(b, k, n0, 0, smem + kT * kK, wave, lane);
+
+  const uint32_t ktiles = k / kK;
+  const uint32_t arow = wm * 128u + (lane & 31u), brow = wn * 128u + (lane & 31u);
+  const uint32_t half = lane >> 5, swz = lane & 7u;
+  for (uint32_t kt = 0; kt < ktiles; ++kt) {
+    const uint32_t cur = kt & 1u;
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this wave's loads of tile kt landed
+    __syncthreads();                     // ... and every wave's; buf cur^1 is free
+    if (kt + 1 < ktiles) {
+      uint16_t* nxt = smem + (cur ^ 1u) * (2u * kT * kK);
+      issue_tile(a, k, m0, (kt + 1) * kK, nxt, wave, lane);
+      issue_tile(b, k, n0, (kt + 1) * kK, nxt + kT * kK, wave, lane);
+    }
+    const uint16_t* la = smem + cur * (2u * kT * kK);
+    const uint16_t* lb = la + kT * kK;
+#pragma unroll
+    for (int ks = 0; ks < kK / 16; ++ks) {
+      const uint32_t chunk = ((uint32_t)ks * 2u + half) ^ swz;
+      bf16x8 fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        fa[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(la + (arow + i * 32u) * kK + chunk * 8u));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        fb[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(lb + (brow + j * 32u) * kK + chunk * 8u));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  __syncthreads();  // all waves done with the operand buffers
+
+  // Epilogue through LDS: wave-private 128 x 128 bf16 region (32 KiB), row r
+  // chunk q stored at chunk q ^ (r & 15); then 16-byte row chunks to C.
+  uint16_t* cst = smem + wave * (128 * 128);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t row = i * 32u + (r >> 2) * 8u + half * 4u + (r & 3);
+        const uint32_t col = j * 32u + (lane & 31u);
+        float v = acc[i][j][r];
+        if (kSilu) v = silu_fast(v);
+        const uint32_t q = (col >> 3) ^ (row & 15u);
+        cst[row * 128u + q * 8u + (col & 7u)] = (uint16_t)tiler::bf16_narrow(v);
+      }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t grow0 = m0 + wm * 128u, gcol0 = n0 + wn * 128u;
+#pragma unroll 4
+  for (int it = 0; it < 32; ++it) {
+    const uint32_t qid = it * 64u + lane;
+    const uint32_t row = qid >> 4, q = qid & 15u;
+    u32x4 v = *reinterpret_cast<const u32x4*>(cst + row * 128u + ((q ^ (row & 15u)) * 8u));
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(c + (grow0 + row) * n + gcol0 + q * 8u));
+  }
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_bf16_t256(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m,
+                         uint32_t n, uint32_t k, uint16_t* __restrict__ c) {
+  contract_bf16_t256_body<false>(a, b, m, n, k, c);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_bf16_silu_t256(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                              uint32_t m, uint32_t n, uint32_t k, uint16_t* __restrict__ c) {
+  contract_bf16_t256_body<true>(a, b, m, n, k, c);
+}
+
 #define TILER_CONTRACT_BF16(NAME, FULLK, SILU)                                                 \
   extern "C" __global__ void __launch_bounds__(256)                                            \
       NAME(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m,         \

@@ -107,6 +107,8 @@ const EntryRow kEntries[] = {
     {"tiler_contract_bf16_silu_t128", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_t128_k", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_t128_k", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_t256", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_t256", "tensor-contraction-bf16/cooperative+silu", 3},
 };
 constexpr uint32_t kEntryCount = sizeof(kEntries) / sizeof(kEntries[0]);
 
@@ -898,11 +900,17 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t*
   if (!a || !b || !c) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull || (m + 127) / 128 > 65535)
     return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
+  uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
+  if (m % 256 == 0 && n % 256 == 0 && k % 64 == 0 && aligned16(a) && aligned16(b) && aligned16(c) &&
+      (m / 256) * (n / 256) <= 0x7fffffffull) {
+    void* args[] = {&a, &b, &m32, &n32, &k32, &c};
+    return launch(ctx, epilogue == TILER_HIP_EPILOGUE_SILU ? "tiler_contract_bf16_silu_t256" : "tiler_contract_bf16_t256",
+                  (uint32_t)((m / 256) * (n / 256)), 1, 256, pick(ctx, stream), args);
+  }
   bool full = k % 8 == 0 && aligned16(a) && aligned16(b);
   const char* name = epilogue == TILER_HIP_EPILOGUE_SILU
                          ? (full ? "tiler_contract_bf16_silu_t128" : "tiler_contract_bf16_silu_t128_k")
                          : (full ? "tiler_contract_bf16_t128" : "tiler_contract_bf16_t128_k");
-  uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
   void* args[] = {&a, &b, &m32, &n32, &k32, &c};
   return launch(ctx, name, (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 256,
                 pick(ctx, stream), args);
