@@ -164,23 +164,39 @@ __device__ __forceinline__ void contract_bf16_body(const uint16_t* __restrict__ 
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// Tile-aligned bf16 contraction: m, n multiples of 256, k a multiple of 64,
-// 16-byte aligned operands (the host checks).  One 256-thread workgroup per
-// 256x256 output tile; wave (wm, wn) owns a 128x128 sub-tile held in 16
-// accumulator blocks of v_mfma_f32_32x32x16_bf16 (256 f32 per lane, one wave
-// per SIMD).  Operand tiles of 256 rows x 64 k move global -> LDS with
-// global_load_lds_dwordx4 (no VGPR staging), double-buffered (2 x 64 KiB).
-// LDS rows are 128 B; 16-byte chunk c of row r sits at chunk c ^ (r & 7), so
-// the eight rows a ds_read_b128 phase touches fall in distinct banks.
-// Workgroups are mapped XCD-aware: the 8 XCDs receive workgroups round robin,
-// and the 32 a given XCD runs form a 4 x 8 block of tiles sharing 4 A and 8 B
-// panels in that XCD's L2.  The epilogue (SiLU on the f32 accumulator, one
-// bf16 narrowing) transposes through LDS so C leaves in 16-byte row chunks.
+// Tile-aligned bf16 contraction: m, n multiples of 256, k a multiple of 64 with
+// 256 * k * 2 < 2^31, 16-byte aligned operands (the host checks all of it).
+//
+// One 1024-thread workgroup per 256 x 256 output tile: 16 waves in a 4 x 4
+// grid, wave (wm, wn) owning a 64 x 64 sub-tile as 2 x 2 accumulator blocks of
+// v_mfma_f32_32x32x16_bf16 (64 f32 per lane, four waves per SIMD, whose
+// interleaving hides the LDS latency that a single wave per SIMD exposes).
+//
+// Operands: each workgroup's 256-row A and B panels are addressed through one
+// buffer resource apiece (32-bit offsets, hardware bounds) and move global ->
+// LDS with buffer_load_dwordx4 ... lds, in 256 x 64 tiles double-buffered
+// (2 stages x 64 KiB).  LDS rows are 128 B; 16-byte chunk c of row r sits at
+// chunk c ^ ((r >> 1) & 7), so the 16 rows one ds_read_b128 phase touches
+// cover all 64 banks.
+//
+// Schedule per 64-deep k tile: four k steps of 16; the fragments of step s+1
+// are read while the MFMAs of step s run.  The workgroup barrier that retires
+// stage kt sits before step 3's MFMAs, so the refill of that stage (tile kt+2)
+// and the reads of tile kt+1's step 0 are issued under them.
+//
+// Tile order is XCD-aware: the 8 XCDs receive workgroups round robin, and the
+// 32 that one XCD runs together form a 4 x 8 block of tiles that share 4 A and
+// 8 B panels in that XCD's L2.  The epilogue (optional SiLU on the f32
+// accumulator, then one bf16 narrowing) transposes through LDS so C leaves in
+// 16-byte row chunks.
 namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kT = 256, kK = 64;
+constexpr int kWaves = 16, kWaveRows = 64, kWaveCols = 64;
+constexpr int kLoadsPerOperand = kT / 8 / kWaves;     // 8-row buffer loads per wave per operand tile
+constexpr uint32_t kStageElems = 2u * kT * kK;        // A tile then B tile, bf16 elements
 
 __device__ __forceinline__ float silu_fast(float v) {
   // Epilogue SiLU: hardware exp2 and reciprocal (relative error ~1e-7),
@@ -190,21 +206,24 @@ __device__ __forceinline__ float silu_fast(float v) {
   return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// Issues the direct-to-LDS loads of one 256 x 64 operand tile.  Wave w
-// covers rows [w*64, w*64+64) in 8 instructions of 8 rows: lane i fills row
-// R + i/8, physical chunk i%8, which holds logical chunk (i%8) ^ ((i/8)&7).
-__device__ __forceinline__ void issue_tile(const uint16_t* __restrict__ g, uint32_t ld,
-                                           uint32_t r0, uint32_t k0, uint16_t* lds_tile,
-                                           uint32_t wave, uint32_t lane) {
-  const uint32_t sub = lane >> 3, phys = lane & 7u;
-  const uint32_t logical = phys ^ (sub & 7u);
+// s_waitcnt immediates (gfx9 layout: vmcnt [3:0] and [15:14], expcnt [6:4],
+// lgkmcnt [11:8]); a field at its maximum does not wait.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+constexpr int kWaitVmLgkm0 = 0x0070;  // vmcnt(0) lgkmcnt(0)
+constexpr int kWaitLgkm0 = 0xC07F;    // lgkmcnt(0)
+
+// Issues this wave's share of one 256 x 64 operand tile: load j fills rows
+// R = (wave * kLoadsPerOperand + j) * 8 .. R + 7 of the LDS tile, lane i the
+// physical chunk i % 8 of row R + i / 8.  voff[j] is that lane's byte offset
+// in the panel at k = 0 (with the chunk swizzle applied); k0_bytes moves along k.
+__device__ __forceinline__ void issue_operand_tile(__amdgpu_buffer_rsrc_t panel, const uint32_t* voff,
+                                                   uint32_t k0_bytes, uint16_t* lds_tile,
+                                                   uint32_t wave_s) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t R = wave * 64u + j * 8u;
-    const uint16_t* src = g + (uint64_t)(r0 + R + sub) * ld + k0 + logical * 8u;
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                     (lds_void*)(lds_tile + R * kK), 16, 0, 0);
-  }
+  for (int j = 0; j < kLoadsPerOperand; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        panel, (lds_void*)(lds_tile + (wave_s * kLoadsPerOperand + j) * 8u * kK), 16, voff[j],
+        k0_bytes, 0, 0);
 }
 
 template <bool kSilu>
@@ -212,13 +231,14 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
                                                         const uint16_t* __restrict__ b,
                                                         uint32_t m, uint32_t n, uint32_t k,
                                                         uint16_t* __restrict__ c) {
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * 2 * kT * kK];  // [buf][A|B][256][64]
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * kStageElems];  // 128 KiB
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-  const uint32_t wm = wave >> 1, wn = wave & 1u;
+  const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t wm = wave >> 2, wn = wave & 3u;
 
   // XCD-aware tile order: workgroup id -> (xcd, slot); xcd picks a 4x8 block
-  // of the tile grid, slot a tile inside it.  Falls back to row-major when the
-  // grid is not a whole number of 4x8 blocks per XCD.
+  // of the tile grid, slot a tile inside it.  Row-major when the grid is not a
+  // whole number of 4x8 blocks per XCD.
   const uint32_t tiles_n = n / kT, tiles_m = m / kT;
   uint32_t tm, tn;
   {
@@ -237,88 +257,143 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
     }
   }
   const uint32_t m0 = tm * kT, n0 = tn * kT;
+  const uint32_t ktiles = k / kK;
 
-  f32x16 acc[4][4];
+  const uint32_t panel_bytes = (uint32_t)kT * k * 2u;
+  const __amdgpu_buffer_rsrc_t pa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a + (uint64_t)m0 * k), (short)0, panel_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t pb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(b + (uint64_t)n0 * k), (short)0, panel_bytes, 0x00020000);
+  uint32_t voff[kLoadsPerOperand];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int j = 0; j < kLoadsPerOperand; ++j) {
+    const uint32_t row = (wave * kLoadsPerOperand + j) * 8u + (lane >> 3);
+    voff[j] = row * k * 2u + ((lane & 7u) ^ ((row >> 1) & 7u)) * 16u;
+  }
+
+  f32x16 acc[2][2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // buffer s: A at smem + s*2*kT*kK, B right after it
-  issue_tile(a, k, m0, 0, smem, wave, lane);
-  issue_tile(b, k, n0, 0, smem + kT * kK, wave, lane);
-
-  const uint32_t ktiles = k / kK;
-  const uint32_t arow = wm * 128u + (lane & 31u), brow = wn * 128u + (lane & 31u);
-  const uint32_t half = lane >> 5, swz = lane & 7u;
-  for (uint32_t kt = 0; kt < ktiles; ++kt) {
-    const uint32_t cur = kt & 1u;
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this wave's loads of tile kt landed
-    __syncthreads();                     // ... and every wave's; buf cur^1 is free
-    if (kt + 1 < ktiles) {
-      uint16_t* nxt = smem + (cur ^ 1u) * (2u * kT * kK);
-      issue_tile(a, k, m0, (kt + 1) * kK, nxt, wave, lane);
-      issue_tile(b, k, n0, (kt + 1) * kK, nxt + kT * kK, wave, lane);
-    }
-    const uint16_t* la = smem + cur * (2u * kT * kK);
+  // Fragment reads: A rows arow + 32i, B rows brow + 32j; lane half h takes
+  // k elements 8h .. 8h+7 of the step, i.e. logical chunk 2s + h.
+  const uint32_t arow = wm * kWaveRows + (lane & 31u), brow = wn * kWaveCols + (lane & 31u);
+  const uint32_t half = lane >> 5, swz = ((lane & 31u) >> 1) & 7u;  // (row >> 1) & 7 for row % 32 == lane % 32
+  bf16x8 fa[2][2], fb[2][2];
+  auto read_step = [&](const uint16_t* la, int step, int slot) {
     const uint16_t* lb = la + kT * kK;
+    const uint32_t chunk = ((uint32_t)step * 2u + half) ^ swz;
 #pragma unroll
-    for (int ks = 0; ks < kK / 16; ++ks) {
-      const uint32_t chunk = ((uint32_t)ks * 2u + half) ^ swz;
-      bf16x8 fa[4], fb[4];
+    for (int i = 0; i < 2; ++i)
+      fa[slot][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(la + (arow + i * 32u) * kK + chunk * 8u));
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        fa[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(la + (arow + i * 32u) * kK + chunk * 8u));
+    for (int j = 0; j < 2; ++j)
+      fb[slot][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(lb + (brow + j * 32u) * kK + chunk * 8u));
+  };
+  auto mfma_step = [&](int slot) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        fb[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(lb + (brow + j * 32u) * kK + chunk * 8u));
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
+  };
+  // Steps 0..2 of one tile; the scheduling fences keep each step's reads
+  // ahead of the previous step's MFMAs.
+  auto steps_0_to_2 = [&](const uint16_t* la) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    for (int s = 0; s < 3; ++s) {
+      read_step(la, s + 1, (s + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_step(s & 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
-  }
-  __syncthreads();  // all waves done with the operand buffers
+  };
 
-  // Epilogue through LDS: wave-private 128 x 128 bf16 region (32 KiB), row r
-  // chunk q stored at chunk q ^ (r & 15); then 16-byte row chunks to C.
-  uint16_t* cst = smem + wave * (128 * 128);
+  issue_operand_tile(pa, voff, 0, smem, wave_s);
+  issue_operand_tile(pb, voff, 0, smem + kT * kK, wave_s);
+  if (ktiles > 1) {
+    issue_operand_tile(pa, voff, kK * 2u, smem + kStageElems, wave_s);
+    issue_operand_tile(pb, voff, kK * 2u, smem + kStageElems + kT * kK, wave_s);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kLoadsPerOperand));  // tile 0's loads landed
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+  asm volatile("s_barrier" ::: "memory");
+  read_step(smem, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  for (uint32_t kt = 0; kt + 1 < ktiles; ++kt) {
+    steps_0_to_2(smem + (kt & 1u) * kStageElems);
+    // Tile kt+1 landed (this wave's loads: vmcnt(0)) and this wave's reads of
+    // stage kt retired (lgkmcnt(0)).  After the barrier the stage may be
+    // refilled.  The LDS drain is asm because the compiler relaxes a builtin
+    // wait that no register use needs; the builtin after the barrier is
+    // already satisfied and only tells the compiler nothing is outstanding.
+    // No memory fence: one would drain the refill issued ahead (vmcnt(0)).
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    if (kt + 2 < ktiles) {
+      uint16_t* st = smem + (kt & 1u) * kStageElems;
+      issue_operand_tile(pa, voff, (kt + 2) * kK * 2u, st, wave_s);
+      issue_operand_tile(pb, voff, (kt + 2) * kK * 2u, st + kT * kK, wave_s);
+    }
+    read_step(smem + ((kt + 1) & 1u) * kStageElems, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_step(1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  steps_0_to_2(smem + ((ktiles - 1) & 1u) * kStageElems);
+  mfma_step(1);
+  __builtin_amdgcn_s_waitcnt(kWaitVmLgkm0);
+  __syncthreads();  // every wave is done with the operand stages
+
+  // Epilogue: wave-private 64 x 64 bf16 region (8 KiB) with 128-B rows, chunk
+  // q of row r at q ^ (r & 7).  Lanes 2c and 2c+1 hold adjacent columns of
+  // rows r and r+1; one exchange lets each write a 32-bit column pair.
+  uint16_t* cst = smem + wave * (kWaveRows * kWaveCols);
+  const bool odd = lane & 1u;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t row = i * 32u + (r >> 2) * 8u + half * 4u + (r & 3);
-        const uint32_t col = j * 32u + (lane & 31u);
-        float v = acc[i][j][r];
-        if (kSilu) v = silu_fast(v);
-        const uint32_t q = (col >> 3) ^ (row & 15u);
-        cst[row * 128u + q * 8u + (col & 7u)] = (uint16_t)tiler::bf16_narrow(v);
+      for (int r = 0; r < 16; r += 2) {
+        float v0 = acc[i][j][r], v1 = acc[i][j][r + 1];
+        if (kSilu) {
+          v0 = silu_fast(v0);
+          v1 = silu_fast(v1);
+        }
+        const float recv = __shfl_xor(odd ? v0 : v1, 1, 64);
+        const float lo = odd ? recv : v0, hi = odd ? v1 : recv;
+        const uint32_t row = i * 32u + (r >> 2) * 8u + half * 4u + (r & 3) + (odd ? 1u : 0u);
+        const uint32_t col = j * 32u + ((lane & 31u) & ~1u);
+        const uint32_t q = (col >> 3) ^ (row & 7u);
+        *reinterpret_cast<uint32_t*>(cst + row * kWaveCols + q * 8u + (col & 7u)) = tiler::bf16_pack2(lo, hi);
       }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   __builtin_amdgcn_wave_barrier();
-  const uint64_t grow0 = m0 + wm * 128u, gcol0 = n0 + wn * 128u;
+  const uint64_t grow0 = m0 + wm * kWaveRows, gcol0 = n0 + wn * kWaveCols;
 #pragma unroll 4
-  for (int it = 0; it < 32; ++it) {
+  for (int it = 0; it < kWaveRows * kWaveCols / 8 / 64; ++it) {
     const uint32_t qid = it * 64u + lane;
-    const uint32_t row = qid >> 4, q = qid & 15u;
-    u32x4 v = *reinterpret_cast<const u32x4*>(cst + row * 128u + ((q ^ (row & 15u)) * 8u));
+    const uint32_t row = qid >> 3, q = qid & 7u;
+    u32x4 v = *reinterpret_cast<const u32x4*>(cst + row * kWaveCols + ((q ^ (row & 7u)) * 8u));
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(c + (grow0 + row) * n + gcol0 + q * 8u));
   }
 }
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(1024)
 tiler_contract_bf16_t256(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m,
                          uint32_t n, uint32_t k, uint16_t* __restrict__ c) {
   contract_bf16_t256_body<false>(a, b, m, n, k, c);
 }
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(1024)
 tiler_contract_bf16_silu_t256(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
                               uint32_t m, uint32_t n, uint32_t k, uint16_t* __restrict__ c) {
   contract_bf16_t256_body<true>(a, b, m, n, k, c);

@@ -901,11 +901,13 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t*
   if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull || (m + 127) / 128 > 65535)
     return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
   uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
-  if (m % 256 == 0 && n % 256 == 0 && k % 64 == 0 && aligned16(a) && aligned16(b) && aligned16(c) &&
-      (m / 256) * (n / 256) <= 0x7fffffffull) {
+  // The 256x256 tile path addresses each 256-row operand panel through one
+  // buffer resource with 32-bit offsets: 256 * k * 2 bytes must stay below 2^31.
+  if (m % 256 == 0 && n % 256 == 0 && k % 64 == 0 && k * 512ull < (1ull << 31) && aligned16(a) &&
+      aligned16(b) && aligned16(c) && (m / 256) * (n / 256) <= 0x7fffffffull) {
     void* args[] = {&a, &b, &m32, &n32, &k32, &c};
     return launch(ctx, epilogue == TILER_HIP_EPILOGUE_SILU ? "tiler_contract_bf16_silu_t256" : "tiler_contract_bf16_t256",
-                  (uint32_t)((m / 256) * (n / 256)), 1, 256, pick(ctx, stream), args);
+                  (uint32_t)((m / 256) * (n / 256)), 1, 1024, pick(ctx, stream), args);
   }
   bool full = k % 8 == 0 && aligned16(a) && aligned16(b);
   const char* name = epilogue == TILER_HIP_EPILOGUE_SILU
