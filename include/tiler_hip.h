@@ -119,7 +119,7 @@ tiler_hip_status tiler_hip_payload(tiler_hip_payload_view *out);
 tiler_hip_status tiler_hip_payload_entry(uint32_t index, tiler_hip_entry_info *out);
 
 /* Validates a code object from its own bytes (ADR 0090 item 8;
- * RuntimeAdapter::validate_payload, tiler-runtime/src/adapter.rs:330-345):
+ * RuntimeAdapter::validate_payload, tiler-runtime/src/adapter.rs:341):
  * an AMDGPU HSA ELF for gfx950 that defines `symbol` and its kernel descriptor
  * `symbol.kd`, whose kernarg segment is `kernarg_bytes` long (0 = unchecked).
  * Device-free. */
@@ -147,7 +147,7 @@ typedef struct {
     int32_t driver_version;
 } tiler_hip_execution_environment;
 
-/* bind_execution_context (adapter.rs:297): binds device `ordinal`, creates the
+/* bind_execution_context (adapter.rs:293): binds device `ordinal`, creates the
  * context's stream and workspace, loads this library's own gfx950 code object,
  * and reports what it observed.  Refuses a device that is not gfx950. */
 tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context **out,
@@ -156,7 +156,7 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context **out,
 void tiler_hip_release(tiler_hip_context *ctx);
 const char *tiler_hip_last_diagnostic(const tiler_hip_context *ctx);
 
-/* observe_live_device (adapter.rs:372): reports, never decides.  Keys:
+/* observe_live_device (adapter.rs:363): reports, never decides.  Keys:
  * "wavefront-size", "compute-units", "max-threads-per-workgroup",
  * "lds-bytes-per-workgroup", "global-memory-bytes", "target-is-gfx950".
  * Unknown keys answer TILER_HIP_REFUSE_UNRECOGNIZED_KEY (fail-closed). */
@@ -169,14 +169,14 @@ typedef struct {
     const char *symbol;
 } tiler_hip_routed_entry;
 
-/* prepare_entries (adapter.rs:401): loads each entry's code object and
+/* prepare_entries (adapter.rs:387): loads each entry's code object and
  * resolves its symbol; reversible.  Prepared entries are numbered from
  * *first_index in order. */
 tiler_hip_status tiler_hip_prepare_entries(tiler_hip_context *ctx,
                                            const tiler_hip_routed_entry *entries,
                                            uint32_t count, uint32_t *first_index);
 
-/* observe_prepared_entry (adapter.rs:436): keys "max-threads-per-workgroup",
+/* observe_prepared_entry (adapter.rs:416): keys "max-threads-per-workgroup",
  * "static-lds-bytes", "private-bytes-per-lane", "vgprs". */
 tiler_hip_status tiler_hip_observe_prepared_entry(tiler_hip_context *ctx, uint32_t prepared,
                                                   const char *key, uint64_t *value);
@@ -200,16 +200,16 @@ typedef struct {
     const tiler_hip_dispatch_entry *entries; /* in execution order */
 } tiler_hip_dispatch_plan;
 
-/* plan_dispatch (adapter.rs:473): sizes and checks the route against the
+/* plan_dispatch (adapter.rs:453): sizes and checks the route against the
  * profile and the prepared entries, acquiring nothing. */
 tiler_hip_status tiler_hip_plan_dispatch(tiler_hip_context *ctx,
                                          const tiler_hip_dispatch_plan *plan);
-/* allocate_dispatch (adapter.rs:490): post-commit program storage.  Slots
+/* allocate_dispatch (adapter.rs:486): post-commit program storage.  Slots
  * whose caller pointer is non-NULL are caller-supplied and not allocated. */
 tiler_hip_status tiler_hip_allocate_dispatch(tiler_hip_context *ctx,
                                              const tiler_hip_dispatch_plan *plan,
                                              void **slot_pointers);
-/* dispatch (adapter.rs:511): encodes every entry in order on the context
+/* dispatch (adapter.rs:506): encodes every entry in order on the context
  * stream, submits, and waits for terminal success. */
 tiler_hip_status tiler_hip_dispatch(tiler_hip_context *ctx, const tiler_hip_dispatch_plan *plan,
                                     void *const *slot_pointers);

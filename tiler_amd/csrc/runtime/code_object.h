@@ -1,5 +1,5 @@
 // Device-free reading of AMDGPU HSA code objects (ELF64), for
-// validate-from-bytes (ADR 0090 item 8; tiler-runtime/src/adapter.rs:330-345).
+// validate-from-bytes (ADR 0090 item 8; tiler-runtime/src/adapter.rs:341).
 #pragma once
 
 #include <cstdint>

@@ -19,7 +19,7 @@ from . import _lib as L
 
 class HipError(RuntimeError):
     """A status from the C ABI.  `fallback_permitted` mirrors
-    AdapterRouteFailure::fallback_permitted (adapter.rs:693)."""
+    AdapterRouteFailure::fallback_permitted (adapter.rs:738)."""
 
     def __init__(self, status: int, what: str, diagnostic: str = ""):
         self.status = status
