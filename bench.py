@@ -7,11 +7,12 @@ on configs[1] (RMS normalization, bf16 [8192 x 4096], w bf16 [4096], eps 1e-5,
 f32 accumulation, bf16 output) as achieved HBM GB/s of algorithmic bytes; the
 other four configs are measured the same way and reported under "families".
 
-Measurement rules: fixed seeds; input/output buffer sets are
-rotated so more than the 256 MB Infinity Cache is touched per sweep; W untimed
-warm-up launches, then K back-to-back launches between HIP events recorded on
-the context stream the kernels run on (median/p10/p90 from per-launch event
-pairs in the same region).  The CPU baseline is the oracle's restatement of
+Measurement rules: fixed seeds; input/output buffer sets are rotated so more
+than the 256 MB Infinity Cache is touched per sweep; W untimed warm-up
+launches and at least SETTLE_S of untimed graph replays, then K back-to-back
+launches (one graph replay) between HIP events recorded on the context stream
+the kernels run on (median/p10/p90 from an eager pass with per-launch event
+pairs).  The CPU baseline is the oracle's restatement of
 the reference loops (strict binary32 folds, no FMA) on the GPU box's host,
 single-threaded, on a bounded sample.
 
@@ -34,6 +35,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA, TFLOP/s
 EPS_BITS = 0x3727C5AC           # 1e-5 as binary32 (config eps)
+SETTLE_S = 0.05                 # untimed graph replays before the timed one
 METRIC = "achieved HBM GB/s (% peak) for RMSNorm/softmax/gather; bf16 GEMM TFLOP/s"
 
 
@@ -296,9 +298,10 @@ WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, Gather, Contract)}
 
 def measure(ctx, wl, steps, warmup):
     """W eager warm-up launches; then the K timed launches are captured once
-    into a HIP graph (so Python's launch cost is not in the timed region) and
-    replayed between two events on the context stream.  A second, eager pass
-    with an event pair around every launch gives median/p10/p90."""
+    into a HIP graph (so Python's launch cost is not in the timed region),
+    replayed untimed for at least SETTLE_S, and replayed once more between two
+    events on the context stream: that replay is the K timed steps.  A second,
+    eager pass with an event pair around every launch gives median/p10/p90."""
     log(f"{wl.name}: preparing synthetic inputs")
     wl.setup()
     for i in range(warmup):
@@ -308,8 +311,15 @@ def measure(ctx, wl, steps, warmup):
     for i in range(steps):
         wl.launch(warmup + i)
     graph = ctx.capture_end()
-    ctx.graph_launch(graph)  # first replay warms the instantiated graph
-    ctx.synchronize()
+    # Settle: replay the graph for at least SETTLE_S.  Clocks dip for a few
+    # milliseconds after sustained load begins and recover; timing one replay
+    # right after the first would land in that dip.
+    settle = 0
+    t_settle = time.perf_counter()
+    while settle < 3 or time.perf_counter() - t_settle < SETTLE_S:
+        ctx.graph_launch(graph)
+        ctx.synchronize()
+        settle += 1
     e0, e1 = ctx.event(), ctx.event()
     log(f"{wl.name}: timing {steps} launches (graph replay)")
     t0 = time.perf_counter()

@@ -26,15 +26,15 @@ constexpr uint32_t kWavesPerBlock = 4;
 // narrowed to bf16 for bf16 storage (ADR 0091 narrowing).  The weight is
 // either one row broadcast over all rows (w_row_stride 0) or a full tensor.
 
+// The bf16 row runs in three phases so a workgroup can issue its rows' HBM
+// loads before anything else (staging the weight, the barrier) and fold them
+// while the weight arrives.  Chunk c of lane l covers positions
+// [c*512 + l*8, +8); x stays packed (4 VGPRs per chunk) from load to epilogue.
+// AL: 2 every chunk whole (extent == CH*512, no guards), 1 aligned rows,
+// 0 unaligned (element loads, same order).
 template <int CH, int AL>
-__device__ __forceinline__ void rms_bf16_row(const uint16_t* __restrict__ x,
-                                             const uint16_t* __restrict__ w,
-                                             uint16_t* __restrict__ y, uint32_t extent,
-                                             float eps, uint32_t lane) {
-  // chunk c covers positions [c*512 + lane*8, +8); x stays packed (4 VGPRs per
-  // chunk) between the fold and the epilogue.
-  u32x4 xv[CH];
-  // AL: 2 every chunk whole (extent == CH*512, no guards), 1 aligned rows, 0 unaligned
+__device__ __forceinline__ void rms_bf16_load(u32x4 (&xv)[CH], const uint16_t* __restrict__ x,
+                                              uint32_t extent, uint32_t lane) {
   const uint32_t nfull = AL == 2 ? CH : AL ? extent >> 9 : 0;  // chunks loaded as whole 16 B
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -49,6 +49,12 @@ __device__ __forceinline__ void rms_bf16_row(const uint16_t* __restrict__ x,
       xv[c] = u32x4{tmp[0], tmp[1], tmp[2], tmp[3]};
     }
   }
+}
+
+// This lane's strict fold of fl(x^2) in ascending position.
+template <int CH, int AL>
+__device__ __forceinline__ float rms_bf16_fold(u32x4 (&xv)[CH], uint32_t extent, uint32_t lane) {
+  const uint32_t nfull = AL == 2 ? CH : AL ? extent >> 9 : 0;
   float acc = -0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -66,6 +72,16 @@ __device__ __forceinline__ void rms_bf16_row(const uint16_t* __restrict__ x,
   // instead of keeping 8*CH widened floats live across the butterfly.
 #pragma unroll
   for (int c = 0; c < CH; ++c) asm volatile("" : "+v"(xv[c]));
+  return acc;
+}
+
+// Wave combine, scale, and y = fl(w * fl(x * s)) narrowed to bf16.
+template <int CH, int AL>
+__device__ __forceinline__ void rms_bf16_epilogue(const u32x4 (&xv)[CH], float acc,
+                                                  const uint16_t* __restrict__ w,
+                                                  uint16_t* __restrict__ y, uint32_t extent,
+                                                  float eps, uint32_t lane) {
+  const uint32_t nfull = AL == 2 ? CH : AL ? extent >> 9 : 0;
   float total = tiler::wave_sum_butterfly(acc);
   float mean = total / (float)extent;
   float s = tiler::rsqrt_f32_cr(mean + eps);
@@ -172,10 +188,8 @@ __device__ __forceinline__ void rms_f32_row(const float* __restrict__ x,
 // e = exp(fl(x - m)) correctly rounded; d = sum of e in the declared grouping;
 // y = canon(fl(e * fl(1/d))) -- the reciprocal multiply, not a division.
 template <int CH, int AL>
-__device__ __forceinline__ void softmax_f32_row(const float* __restrict__ x,
-                                                float* __restrict__ y, uint32_t extent,
-                                                uint32_t lane, const double* exp_table) {
-  f32x4 xv[CH];
+__device__ __forceinline__ void softmax_f32_load(f32x4 (&xv)[CH], const float* __restrict__ x,
+                                                 uint32_t extent, uint32_t lane) {
   const uint32_t nfull = AL == 2 ? CH : AL ? extent >> 8 : 0;
   const float ninf = -__builtin_huge_valf();
 #pragma unroll
@@ -191,8 +205,13 @@ __device__ __forceinline__ void softmax_f32_row(const float* __restrict__ x,
       xv[c] = f32x4{tmp[0], tmp[1], tmp[2], tmp[3]};
     }
   }
-  // -inf is the maximum's identity on every operand (including -inf itself).
-  float m = ninf;
+}
+
+// The row maximum.  -inf is the maximum's identity on every operand (including
+// -inf itself), so the padding the load put past the row's end is inert.
+template <int CH>
+__device__ __forceinline__ float softmax_f32_max(const f32x4 (&xv)[CH]) {
+  float m = -__builtin_huge_valf();
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     m = tiler::maximum_f32(m, xv[c].x);
@@ -200,7 +219,14 @@ __device__ __forceinline__ void softmax_f32_row(const float* __restrict__ x,
     m = tiler::maximum_f32(m, xv[c].z);
     m = tiler::maximum_f32(m, xv[c].w);
   }
-  m = tiler::wave_max(m);
+  return tiler::wave_max(m);
+}
+
+template <int CH, int AL>
+__device__ __forceinline__ void softmax_f32_finish(f32x4 (&xv)[CH], float m, float* __restrict__ y,
+                                                   uint32_t extent, uint32_t lane,
+                                                   const double* exp_table) {
+  const uint32_t nfull = AL == 2 ? CH : AL ? extent >> 8 : 0;
   float acc = -0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -241,40 +267,47 @@ __device__ __forceinline__ void softmax_f32_row(const float* __restrict__ x,
 // CH whole chunks with no guards; the plain instances load whole 16-byte chunks
 // and need every row 16-byte aligned (aligned base, extent*elem % 16 == 0);
 // the _u instances load element by element in the same order.
-// bf16 RMSNorm workgroups are WAVES waves (one row each).  With a broadcast
-// weight (w_row_stride 0) and aligned rows the weight row is staged once per
-// workgroup in LDS (up to 8192 bf16) and every wave's epilogue reads it there.
-#define TILER_RMS_BF16(CH, AL, SFX, WAVES)                                                  \
-  extern "C" __global__ void __launch_bounds__(64 * WAVES) tiler_rms_norm_bf16_ch##CH##SFX(      \
+// bf16 RMSNorm workgroups are four waves (one row each).  Each wave issues its
+// row's loads first; with a broadcast weight (w_row_stride 0) and aligned rows
+// the weight row is then staged once per workgroup in LDS (up to 8192 bf16)
+// while those loads are in flight, the row is folded, and the barrier before
+// the epilogue publishes the staged weight.
+#define TILER_RMS_BF16(CH, AL, SFX)                                                         \
+  extern "C" __global__ void __launch_bounds__(256) tiler_rms_norm_bf16_ch##CH##SFX(            \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint64_t w_row_stride, \
       uint16_t* __restrict__ y, uint64_t rows, uint32_t extent, float eps) {                 \
     __shared__ __attribute__((aligned(16))) uint16_t wl[AL ? CH * 512 : 8];                \
-    const uint64_t row = (uint64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);                \
+    const uint64_t row = (uint64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);       \
+    const uint32_t lane = threadIdx.x & 63u;                                                \
+    const bool active = row < rows;                                                         \
     const bool stage = AL && w_row_stride == 0;                                             \
+    u32x4 xv[CH];                                                                           \
+    if (active) rms_bf16_load<CH, AL>(xv, x + row * extent, extent, lane);                 \
     if (stage) {                                                                            \
       for (uint32_t i = threadIdx.x; i * 8u < extent; i += blockDim.x)                    \
         *reinterpret_cast<u32x4*>(wl + i * 8u) = *reinterpret_cast<const u32x4*>(w + i * 8u); \
-      __syncthreads();                                                                      \
     }                                                                                       \
-    if (row >= rows) return;                                                                \
-    rms_bf16_row<CH, AL>(x + row * extent, stage ? wl : w + row * w_row_stride,            \
-                         y + row * extent, extent, eps, threadIdx.x & 63u);                \
+    float acc = active ? rms_bf16_fold<CH, AL>(xv, extent, lane) : 0.0f;                   \
+    if (stage) __syncthreads();                                                             \
+    if (!active) return;                                                                    \
+    rms_bf16_epilogue<CH, AL>(xv, acc, stage ? wl : w + row * w_row_stride, y + row * extent, \
+                              extent, eps, lane);                                           \
   }
-TILER_RMS_BF16(1, 2, _full, 16)
-TILER_RMS_BF16(1, 1, , 16)
-TILER_RMS_BF16(1, 0, _u, 16)
-TILER_RMS_BF16(2, 2, _full, 16)
-TILER_RMS_BF16(2, 1, , 16)
-TILER_RMS_BF16(2, 0, _u, 16)
-TILER_RMS_BF16(4, 2, _full, 16)
-TILER_RMS_BF16(4, 1, , 16)
-TILER_RMS_BF16(4, 0, _u, 16)
-TILER_RMS_BF16(8, 2, _full, 16)
-TILER_RMS_BF16(8, 1, , 16)
-TILER_RMS_BF16(8, 0, _u, 16)
-TILER_RMS_BF16(16, 2, _full, 4)
-TILER_RMS_BF16(16, 1, , 4)
-TILER_RMS_BF16(16, 0, _u, 4)
+TILER_RMS_BF16(1, 2, _full)
+TILER_RMS_BF16(1, 1, )
+TILER_RMS_BF16(1, 0, _u)
+TILER_RMS_BF16(2, 2, _full)
+TILER_RMS_BF16(2, 1, )
+TILER_RMS_BF16(2, 0, _u)
+TILER_RMS_BF16(4, 2, _full)
+TILER_RMS_BF16(4, 1, )
+TILER_RMS_BF16(4, 0, _u)
+TILER_RMS_BF16(8, 2, _full)
+TILER_RMS_BF16(8, 1, )
+TILER_RMS_BF16(8, 0, _u)
+TILER_RMS_BF16(16, 2, _full)
+TILER_RMS_BF16(16, 1, )
+TILER_RMS_BF16(16, 0, _u)
 
 #define TILER_RMS_F32(CH, AL, SFX)                                                          \
   extern "C" __global__ void __launch_bounds__(256) tiler_rms_norm_f32_ch##CH##SFX(              \
@@ -304,15 +337,22 @@ TILER_RMS_F32(32, 2, _full)
 TILER_RMS_F32(32, 1, )
 TILER_RMS_F32(32, 0, _u)
 
+// Softmax workgroups also issue their rows' loads first and stage the 64-entry
+// exp table in LDS while those loads are in flight.
 #define TILER_SOFTMAX_F32(CH, AL, SFX)                                                      \
   extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_ch##CH##SFX(               \
       const float* __restrict__ x, float* __restrict__ y, uint64_t rows, uint32_t extent) {  \
     __shared__ double tab[64];                                                              \
+    const uint64_t row = (uint64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);       \
+    const uint32_t lane = threadIdx.x & 63u;                                                \
+    const bool active = row < rows;                                                         \
+    f32x4 xv[CH];                                                                           \
+    if (active) softmax_f32_load<CH, AL>(xv, x + row * extent, extent, lane);              \
     if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Table64[threadIdx.x];                     \
+    const float m = active ? softmax_f32_max<CH>(xv) : 0.0f;                               \
     __syncthreads();                                                                        \
-    uint64_t row = (uint64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);             \
-    if (row >= rows) return;                                                                \
-    softmax_f32_row<CH, AL>(x + row * extent, y + row * extent, extent, threadIdx.x & 63u, tab); \
+    if (!active) return;                                                                    \
+    softmax_f32_finish<CH, AL>(xv, m, y + row * extent, extent, lane, tab);                \
   }
 TILER_SOFTMAX_F32(1, 2, _full)
 TILER_SOFTMAX_F32(1, 1, )

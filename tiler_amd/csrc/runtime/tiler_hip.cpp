@@ -747,10 +747,9 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, cons
   uint64_t wstride = weight_broadcast ? 0 : extent;
   uint32_t ext32 = (uint32_t)extent;
   void* args[] = {&x, &w, &wstride, &y, &rows, &ext32, &eps};
-  if (dtype == TILER_HIP_BF16) {  // one row per wave: 16-wave workgroups, 4 for the longest rows
-    const uint32_t waves = ch <= 8 ? 16u : 4u;
-    return launch(ctx, name, (uint32_t)((rows + waves - 1) / waves), 1, 64 * waves, pick(ctx, stream), args);
-  }
+  // one row per wave, four waves per workgroup
+  if ((rows + 3) / 4 > 0x7fffffffull)
+    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
   return launch(ctx, name, (uint32_t)((rows + 3) / 4), 1, 256, pick(ctx, stream), args);
 }
 
@@ -768,6 +767,8 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
   std::snprintf(name, sizeof(name), "tiler_softmax_f32_ch%u%s", ch, full ? "_full" : al ? "" : "_u");
   uint32_t ext32 = (uint32_t)extent;
   void* args[] = {&x, &y, &rows, &ext32};
+  if ((rows + 3) / 4 > 0x7fffffffull)
+    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
   return launch(ctx, name, (uint32_t)((rows + 3) / 4), 1, 256, pick(ctx, stream), args);
 }
 
