@@ -17,7 +17,7 @@ the reference loops (strict binary32 folds, no FMA) on the GPU box's host,
 single-threaded, on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
-                       [--no-families] [--no-cpu-baseline]
+                       [--no-families] [--no-cpu-baseline] [--calibration-copy]
 """
 from __future__ import annotations
 
@@ -45,6 +45,7 @@ def log(msg):
 
 class Workload:
     name = ""
+    kernel = ""  # the dominant kernel, whose measured HBM traffic is reported
     bound = "hbm"
     unit = "GB/s"
 
@@ -65,6 +66,7 @@ class Workload:
 class RmsNorm(Workload):
     """RMS normalization over rows."""
     name = "rms_norm"
+    kernel = "tiler_rms_norm_bf16_ch8_full"
     rows, extent = 8192, 4096
     sets = 6  # 6 x 128 MiB touched per sweep
 
@@ -120,6 +122,7 @@ class RmsNorm(Workload):
 class Sum(Workload):
     """f32[2^24] -> scalar, the two-level tree."""
     name = "sum"
+    kernel = "tiler_sum_f32_grid"
     n = 1 << 24
     sets = 6
 
@@ -157,6 +160,7 @@ class Sum(Workload):
 class Softmax(Workload):
     """f32 [32 x 2048 x 2048] softmax over the last axis."""
     name = "softmax"
+    kernel = "tiler_softmax_f32_ch8_full"
     rows, extent = 32 * 2048, 2048
     sets = 2
 
@@ -196,6 +200,7 @@ class Softmax(Workload):
 class Gather(Workload):
     """tied embedding gather."""
     name = "gather"
+    kernel = "tiler_gather_u128"
     vocab, hidden, count = 128256, 4096, 16384
     sets = 6
 
@@ -245,6 +250,7 @@ class Gather(Workload):
 class Contract(Workload):
     """bf16 4096^3 contraction with fused SiLU."""
     name = "contract"
+    kernel = "tiler_contract_bf16_silu_t256"
     bound = "mfma"
     unit = "TFLOP/s"
     m = n = k = 4096
@@ -294,6 +300,39 @@ class Contract(Workload):
 
 
 WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, Gather, Contract)}
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_all_families.md")
+
+
+def measured_traffic() -> dict:
+    """Calibrated HBM bytes per launch by kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (rows '| `kernel` | ... | bytes |', the last
+    column the calibrated total).  Empty when the summary is absent."""
+    out = {}
+    if not os.path.exists(TRAFFIC_FILE):
+        return out
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 2 and cells[0].startswith("`tiler_"):
+                try:
+                    out[cells[0].strip("`")] = int(cells[-1].replace(",", ""))
+                except ValueError:
+                    pass
+    return out
+
+
+def calibration_copy(ctx, nbytes=256 << 20, times=3):
+    """A plain device-to-device copy of known size, for scaling the FETCH_SIZE
+    and WRITE_SIZE counters of a rocprofv3 --pmc run of this script."""
+    src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    ctx.fill_u32(src, 0x3f800000, nbytes // 4)
+    for _ in range(times):
+        ctx.copy(dst, src, nbytes)
+    ctx.synchronize()
+    src.free()
+    dst.free()
 
 
 def measure(ctx, wl, steps, warmup):
@@ -353,8 +392,9 @@ def measure(ctx, wl, steps, warmup):
         "median_ms": float(np.median(per)), "p10_ms": float(np.percentile(per, 10)),
         "p90_ms": float(np.percentile(per, 90)), "wall_s": wall,
         "roofline": {"bound": wl.bound, "achieved": achieved, "peak": peak,
-                     "unit": wl.unit, "frac": achieved / peak, "traffic": None,
-                     "work_per_launch": work},
+                     "unit": wl.unit, "frac": achieved / peak,
+                     "traffic": measured_traffic().get(wl.kernel),
+                     "work_per_launch": work, "kernel": wl.kernel},
         "config": wl.config(),
     }
 
@@ -368,6 +408,8 @@ def main():
     ap.add_argument("--no-families", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="first run a 256 MiB device copy (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("tiler-hip bench runs on one GPU: this build has no multi-GPU path "
@@ -379,6 +421,8 @@ def main():
     log(f"device {ctx.environment['device_name']} {ctx.environment['gcn_arch_name']} "
         f"CUs={ctx.environment['compute_units']}")
 
+    if args.calibration_copy:
+        calibration_copy(ctx)
     head = measure(ctx, WORKLOADS[args.workload](ctx), args.steps, args.warmup)
     families = {}
     if not args.no_families:

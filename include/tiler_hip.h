@@ -227,8 +227,13 @@ tiler_hip_status tiler_hip_upload(tiler_hip_context *ctx, void *device_dst, cons
                                   uint64_t bytes);
 tiler_hip_status tiler_hip_download(tiler_hip_context *ctx, void *host_dst,
                                     const void *device_src, uint64_t bytes);
+/* Writes `value` to `words` 32-bit words with a kernel (never a memset node,
+ * so the call may be captured into a graph). */
 tiler_hip_status tiler_hip_fill_u32(tiler_hip_context *ctx, void *device_dst, uint32_t value,
                                     uint64_t words, tiler_hip_stream stream);
+/* Device-to-device copy of `bytes`, ordered on `stream` (NULL: the context's). */
+tiler_hip_status tiler_hip_copy(tiler_hip_context *ctx, void *device_dst, const void *device_src,
+                                uint64_t bytes, tiler_hip_stream stream);
 tiler_hip_status tiler_hip_synchronize(tiler_hip_context *ctx);
 tiler_hip_stream tiler_hip_context_stream(tiler_hip_context *ctx);
 tiler_hip_status tiler_hip_event_create(tiler_hip_context *ctx, tiler_hip_event *out);

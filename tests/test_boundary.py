@@ -65,7 +65,7 @@ def test_payload_view_and_entry_mapping():
         assert L.lib().tiler_hip_payload_entry(i, ctypes.byref(e)) == L.OK
         assert e.symbol not in seen
         seen.add(e.symbol)
-        assert e.kernarg_bytes > 0 and e.buffer_bindings >= 2
+        assert e.kernarg_bytes > 0 and e.buffer_bindings >= 1
         d = ctypes.create_string_buffer(256)
         assert L.lib().tiler_hip_validate_payload(code, len(code), e.symbol, e.kernarg_bytes, d,
                                                   256) == L.OK, d.value

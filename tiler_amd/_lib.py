@@ -188,6 +188,7 @@ SIGNATURES = {
     "tiler_hip_upload": (_S, [_CTX, _P, _P, _U64]),
     "tiler_hip_download": (_S, [_CTX, _P, _P, _U64]),
     "tiler_hip_fill_u32": (_S, [_CTX, _P, _U32, _U64, _P]),
+    "tiler_hip_copy": (_S, [_CTX, _P, _P, _U64, _P]),
     "tiler_hip_synchronize": (_S, [_CTX]),
     "tiler_hip_context_stream": (_P, [_CTX]),
     "tiler_hip_event_create": (_S, [_CTX, ctypes.POINTER(_P)]),

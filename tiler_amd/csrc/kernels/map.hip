@@ -109,3 +109,12 @@ tiler_broadcast_u16(const uint16_t* __restrict__ src, uint16_t* __restrict__ out
                     BroadcastGeometry g) {
   broadcast_body<uint16_t>(src, out, n, g);
 }
+
+// Fill: dst[i] = value for i < words.  A kernel rather than a memset so that a
+// captured graph holds kernel nodes only.
+extern "C" __global__ void __launch_bounds__(256)
+tiler_fill_u32(uint32_t* __restrict__ dst, uint32_t value, uint64_t words) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride)
+    dst[i] = value;
+}

@@ -102,6 +102,7 @@ const EntryRow kEntries[] = {
     {"tiler_map_bf16", "pointwise-bf16", 3},
     {"tiler_broadcast_u32", "broadcast", 2},
     {"tiler_broadcast_u16", "broadcast", 2},
+    {"tiler_fill_u32", "fill", 1},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_bf16_t128", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_t128", "tensor-contraction-bf16/cooperative+silu", 3},
@@ -564,9 +565,19 @@ tiler_hip_status tiler_hip_download(tiler_hip_context* ctx, void* dst, const voi
 }
 tiler_hip_status tiler_hip_fill_u32(tiler_hip_context* ctx, void* dst, uint32_t value,
                                     uint64_t words, tiler_hip_stream stream) {
-  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (hipMemsetD32Async(dst, (int)value, words, pick(ctx, stream)) != hipSuccess)
-    return fail(ctx, TILER_HIP_FAIL_DEVICE, "fill failed");
+  if (!ctx || (words && !dst)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (words == 0) return TILER_HIP_OK;
+  uint64_t groups = (words + 255) / 256;
+  if (groups > 4096) groups = 4096;
+  void* args[] = {&dst, &value, &words};
+  return launch(ctx, "tiler_fill_u32", (uint32_t)groups, 1, 256, pick(ctx, stream), args);
+}
+tiler_hip_status tiler_hip_copy(tiler_hip_context* ctx, void* dst, const void* src, uint64_t bytes,
+                                tiler_hip_stream stream) {
+  if (!ctx || (bytes && (!dst || !src))) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (bytes == 0) return TILER_HIP_OK;
+  if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, pick(ctx, stream)) != hipSuccess)
+    return fail(ctx, TILER_HIP_FAIL_TRANSFER, "device-to-device copy failed");
   return TILER_HIP_OK;
 }
 tiler_hip_status tiler_hip_synchronize(tiler_hip_context* ctx) {
@@ -869,7 +880,7 @@ tiler_hip_status tiler_hip_gather_status(tiler_hip_context* ctx, tiler_hip_strea
     return fail(ctx, TILER_HIP_FAIL_DEVICE, "reading the gather record failed");
   if (v == ~0ull) return TILER_HIP_OK;
   if (bad_position) *bad_position = v;
-  hipMemsetAsync(ctx->gather_bad, 0xff, 8, s);
+  tiler_hip_fill_u32(ctx, ctx->gather_bad, 0xffffffffu, 2, s);  // re-arm the record
   hipStreamSynchronize(s);
   return fail(ctx, TILER_HIP_FAIL_GATHER_INDEX_OUT_OF_BOUNDS,
               "gather index out of bounds at position " + std::to_string(v));

@@ -199,6 +199,10 @@ class Context:
     def graph_destroy(self, graph: int):
         self._check(L.lib().tiler_hip_graph_destroy(self.handle, graph), "graph_destroy")
 
+    def copy(self, dst, src, nbytes: int, stream=None):
+        """Device-to-device copy, ordered on the stream."""
+        self._check(L.lib().tiler_hip_copy(self.handle, _ptr(dst), _ptr(src), nbytes, stream), "copy")
+
     def fill_u32(self, buf, value: int, words: int, stream=None):
         self._check(L.lib().tiler_hip_fill_u32(self.handle, _ptr(buf), value, words, stream),
                     "fill_u32")
