@@ -50,6 +50,7 @@ def build() -> str:
     cmd = [
         "gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
         "-Wall", "-o", LIB_PATH + ".tmp", os.path.join(HERE, "tiler_oracle.c"),
+        os.path.join(HERE, "device_exp_audit.c"),
         "-lquadmath", "-lm", "-lpthread",
     ]
     subprocess.run(cmd, check=True)
@@ -77,6 +78,8 @@ _SIGS = {
     "tiler_oracle_cooperative_grouped_sum_f32": (
         _I32, [_P, _U64, _U64, _U64, _U64, _U64, _I32, _P, _I32, _I32]),
     "tiler_oracle_certified_exp_f32": (_I32, [ctypes.c_float, _P]),
+    "tiler_oracle_device_exp_f32": (ctypes.c_float, [ctypes.c_float]),
+    "tiler_oracle_audit_device_exp": (_I32, [_I32, _I32, _U32, _P, _U64, _P, _P, _P, _P]),
     "tiler_oracle_certified_rsqrt_f32": (_I32, [ctypes.c_float, _P]),
     "tiler_oracle_silu_f32": (_I32, [_P, _U64, _P, _I32, _I32]),
     "tiler_oracle_softmax_f32": (_I32, [_P, _U64, _U64, _U64, _P, _I32, _I32]),
@@ -308,3 +311,26 @@ def softmax_grouped(values, rows, extent, vec, waves) -> np.ndarray:
     _check(lib().tiler_oracle_softmax_grouped_f32(_ptr(x), rows, extent, vec, waves, _ptr(out)),
            "softmax_grouped")
     return out
+
+
+def audit_device_exp(margin_log2: int = -48, threads: int = 8, cap: int = 1 << 16,
+                     planted_log2: int = 0) -> dict:
+    """Exhaustive audit of the device's binary32 exp (device_exp_audit.c):
+    returns the inputs near a rounding boundary (sorted), how many inputs were
+    scanned, and how many of the near-boundary ones differ from the certified
+    exp."""
+    hard = np.zeros(cap, dtype=np.float32)
+    nh, nc, nm = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    first = ctypes.c_float()
+    _check(lib().tiler_oracle_audit_device_exp(margin_log2, planted_log2, threads, _ptr(hard), cap,
+                                               ctypes.byref(nh), ctypes.byref(nc),
+                                               ctypes.byref(nm), ctypes.byref(first)),
+           "audit_device_exp")
+    kept = np.sort(hard[:min(nh.value, cap)])
+    return {"hard": kept, "hard_count": nh.value, "checked": nc.value,
+            "mismatches": nm.value, "first_mismatch": first.value}
+
+
+def device_exp_f32(s: float) -> float:
+    """The device's binary32 exp, restated (see audit_device_exp)."""
+    return float(lib().tiler_oracle_device_exp_f32(s))

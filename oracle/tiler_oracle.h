@@ -123,6 +123,21 @@ int32_t tiler_oracle_rms_norm_grouped_f32(const float *x, const float *w, uint64
 int32_t tiler_oracle_softmax_grouped_f32(const float *x, uint64_t rows, uint64_t extent,
                                          uint32_t vec, uint32_t waves, float *y);
 
+/* Audit of the device's binary32 exp (device_exp_audit.c): the device
+ * algorithm restated bit for bit, and an exhaustive scan of every binary32
+ * input in (-104, 89).  Inputs whose binary64 value lies within
+ * 2^margin_log2 (relative) of a binary32 rounding boundary are collected in
+ * `hard` (up to hard_cap) and compared with tiler_oracle_certified_exp_f32;
+ * every other input is correctly rounded by the error bound stated in that
+ * file.  planted_log2 != 0 perturbs every value by (1 + 2^planted_log2)
+ * before rounding (a planted mistake for the audit's own test). */
+float tiler_oracle_device_exp_f32(float s);
+int32_t tiler_oracle_audit_device_exp(int32_t margin_log2, int32_t planted_log2,
+                                      uint32_t threads, float *hard,
+                                      uint64_t hard_cap, uint64_t *hard_count,
+                                      uint64_t *checked, uint64_t *mismatches,
+                                      float *first_mismatch);
+
 #ifdef __cplusplus
 }
 #endif
