@@ -287,7 +287,8 @@ uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context *ctx, uint64_t n)
  * tiler-reference/src/rms_norm.rs:405-489).  dtype: TILER_HIP_F32 or
  * TILER_HIP_BF16 (binary32 arithmetic on exactly widened operands, one
  * narrowing of y).  weight_broadcast != 0: w is one row of `extent` shared by
- * every row; otherwise w has the input's shape (the reference's form). */
+ * every row; otherwise w has the input's shape (the reference's form).  Rows
+ * up to 2^32 - 1 elements (see tiler_hip_row_grouping for the fold order). */
 #define TILER_HIP_F32 0
 #define TILER_HIP_BF16 1
 tiler_hip_status tiler_hip_rms_norm(tiler_hip_context *ctx, uint32_t dtype, const void *x,
@@ -299,6 +300,20 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context *ctx, uint32_t dtype, cons
  * tiler-reference/src/softmax.rs:200-315). */
 tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context *ctx, const float *x, uint64_t rows,
                                        uint64_t extent, float *y, tiler_hip_stream stream);
+
+/* The declared grouping of a row reduction: thread t of a 64*waves-thread
+ * group folds the `vec`-element chunks t, t + 64*waves, ... in ascending
+ * position, each wave combines its lanes with an xor butterfly (offsets 32 ..
+ * 1) and the wave results are added in ascending order.  RMSNorm and softmax
+ * rows of up to 8192 elements use one wave (waves 1); longer rows one
+ * 1024-thread workgroup (waves 16); the many-row sum uses (4, 4).  The
+ * reassociation is the one the kernels perform, reported so a planner can
+ * record it.  Device-free. */
+#define TILER_HIP_ROWS_RMS_NORM 0
+#define TILER_HIP_ROWS_SOFTMAX 1
+#define TILER_HIP_ROWS_SUM 2
+tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_t extent,
+                                        uint32_t *vec, uint32_t *waves);
 
 /* Pointwise maps (tiler-reference/src/evaluate.rs:448-485; silu.rs:511-533).
  * op: 0 scale-bias y = x*a + b, 1 SiLU, 2 add x + x2, 3 multiply x * x2.

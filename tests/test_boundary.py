@@ -114,6 +114,20 @@ def test_pre_commit_gather_bound_names_first_position():
     tiler_amd.validate_gather_index(np.zeros(0, np.uint32), 5, False)
 
 
+def test_row_grouping_is_declared_device_free():
+    import tiler_amd
+    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 4096) == (8, 1)
+    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 8192) == (8, 1)
+    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 8193) == (8, 16)
+    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.F32, 100000) == (4, 16)
+    assert tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, 2048) == (4, 1)
+    assert tiler_amd.row_grouping(L.ROWS_SUM, L.F32, 10) == (4, 4)
+    with pytest.raises(tiler_amd.Refusal):
+        tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.BF16, 2048)
+    with pytest.raises(tiler_amd.Refusal):
+        tiler_amd.row_grouping(7, L.F32, 2048)
+
+
 def test_bind_refuses_without_a_device_here():
     if os.path.exists("/dev/kfd"):
         pytest.skip("a GPU is present; covered by the gpu tests")

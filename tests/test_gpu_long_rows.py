@@ -1,0 +1,102 @@
+"""GPU: RMSNorm and softmax rows longer than one wave holds (> 8192 elements).
+
+One 1024-thread workgroup per row, register-resident up to 1024 x 8 chunks per
+row and streamed beyond; the fold order is the declared grouping
+tiler_hip_row_grouping reports (vec, waves 16), restated by the oracle's
+grouped forms (tiler-reference/src/rms_norm.rs:405-489, softmax.rs:200-315
+with that reassociation).  Bit-exact against the oracle on the same inputs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import tiler_amd
+from helpers import bf16_widen, bits
+from tiler_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+EPS = 0x3727C5AC
+
+
+def _dev_rms(ctx, dtype, x, w, rows, extent, broadcast, offset_elems=0):
+    elem = x.dtype.itemsize
+    dx = ctx.alloc(x.nbytes + 16)
+    dw = ctx.to_device(w)
+    dy = ctx.alloc(x.nbytes + 16)
+    try:
+        vx, vy = dx.offset(offset_elems * elem), dy.offset(offset_elems * elem)
+        vx.upload(x)
+        ctx.rms_norm(dtype, vx, dw, rows, extent, EPS, vy, weight_broadcast=broadcast)
+        ctx.synchronize()
+        return vy.download(x.dtype, x.shape)
+    finally:
+        dx.free(); dw.free(); dy.free()
+
+
+@pytest.mark.parametrize("rows,extent,broadcast,offset", [
+    (3, 8200, True, 0),      # register-resident, 2 chunks per thread
+    (2, 12345, True, 0),     # unaligned rows (element path)
+    (2, 65536, True, 0),     # 8 chunks per thread
+    (2, 65544, False, 0),    # streamed, full weight
+    (2, 100001, True, 1),    # streamed, unaligned base
+])
+def test_rms_norm_bf16_long_rows(ctx, rows, extent, broadcast, offset):
+    rng = np.random.default_rng(extent)
+    xb = oracle.bf16_narrow(rng.standard_normal((rows, extent)).astype(np.float32))
+    wshape = (extent,) if broadcast else (rows, extent)
+    wb = oracle.bf16_narrow(rng.normal(1.0, 0.1, wshape).astype(np.float32))
+    vec, waves = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, extent)
+    assert (vec, waves) == (8, 16)
+    got = _dev_rms(ctx, L.BF16, xb, wb, rows, extent, broadcast, offset)
+    y = oracle.rms_norm_grouped(bf16_widen(xb), bf16_widen(wb), rows, extent, EPS, broadcast, vec, waves)
+    assert np.array_equal(got, oracle.bf16_narrow(y).reshape(rows, extent))
+
+
+@pytest.mark.parametrize("rows,extent", [(3, 8193), (2, 32768), (2, 40003)])
+def test_rms_norm_f32_long_rows(ctx, rows, extent):
+    rng = np.random.default_rng(extent + 7)
+    x = rng.standard_normal((rows, extent)).astype(np.float32)
+    w = rng.normal(1.0, 0.1, (rows, extent)).astype(np.float32)
+    vec, waves = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.F32, extent)
+    got = _dev_rms(ctx, L.F32, x, w, rows, extent, False)
+    want = oracle.rms_norm_grouped(x, w, rows, extent, EPS, False, vec, waves).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("rows,extent", [(4, 8196), (2, 20000), (2, 32768), (3, 50001)])
+def test_softmax_long_rows(ctx, rows, extent):
+    rng = np.random.default_rng(extent + 11)
+    x = (rng.standard_normal((rows, extent)) * 3).astype(np.float32)
+    x[0, ::7] = -np.inf                  # masked positions
+    if rows > 2:
+        x[2, extent // 2] = np.nan          # a NaN poisons its row
+    vec, waves = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
+    assert (vec, waves) == (4, 16)
+    dx, dy = ctx.to_device(x), ctx.alloc(x.nbytes)
+    try:
+        ctx.softmax_f32(dx, rows, extent, dy)
+        ctx.synchronize()
+        got = dy.download(np.float32, x.shape)
+    finally:
+        dx.free(); dy.free()
+    want = oracle.softmax_grouped(x, rows, extent, vec, waves).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_long_row_softmax_matches_f64_within_tolerance(ctx):
+    rows, extent = 2, 300000
+    x = (np.random.default_rng(5).standard_normal((rows, extent)) * 3).astype(np.float32)
+    dx, dy = ctx.to_device(x), ctx.alloc(x.nbytes)
+    try:
+        ctx.softmax_f32(dx, rows, extent, dy)
+        ctx.synchronize()
+        got = dy.download(np.float32, x.shape)
+    finally:
+        dx.free(); dy.free()
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+    ref = e / e.sum(axis=1, keepdims=True)
+    assert float((np.abs(got - ref) / ref).max()) <= 1e-5

@@ -9,7 +9,7 @@ functions run on the device), `adapter` (the RuntimeAdapter route), and
 """
 from . import _lib
 from .runtime import (Context, DeviceBuffer, Failure, GatherIndexOutOfBounds, HipError, Refusal,
-                      profile, validate_gather_index)
+                      profile, row_grouping, validate_gather_index)
 
 __all__ = ["Context", "DeviceBuffer", "Failure", "GatherIndexOutOfBounds", "HipError", "Refusal",
-           "profile", "validate_gather_index", "_lib"]
+           "profile", "row_grouping", "validate_gather_index", "_lib"]

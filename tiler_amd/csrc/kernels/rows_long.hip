@@ -1,0 +1,331 @@
+// Long-row realizations of RMS normalization and softmax
+// (tiler-reference/src/rms_norm.rs:134-195, 453-489; softmax.rs:237-315), for
+// rows longer than one wave holds in registers (8192 elements).
+//
+// One 1024-thread workgroup (16 waves) per row.  Thread t owns the 16-byte
+// chunks t, t + 1024, t + 2048, ... of the row and folds their elements in
+// ascending position; each wave combines its lanes with the xor butterfly and
+// the 16 wave results are added in ascending wave order -- the declared
+// grouping (vec = elements per chunk, waves = 16) the oracle restates.
+//
+// CH > 0: the row's chunks stay in registers between passes (CH per thread,
+// rows up to 1024 * CH chunks), so HBM sees each byte once.  CH == 0: rows of
+// any length are streamed -- RMSNorm reads the row twice (fold, epilogue),
+// softmax three times (maximum, exponent sum, output; the exponent is
+// recomputed bit-identically in the last pass).
+// AL: 1 when the row base and extent keep every chunk 16-byte aligned; 0 loads
+// and stores element by element in the same order.
+#include "common.h"
+
+namespace {
+
+constexpr uint32_t kLongThreads = 1024;
+constexpr uint32_t kLongWaves = kLongThreads / 64;
+
+// Strict ascending sum of the 16 wave results (every thread gets the total).
+__device__ __forceinline__ float long_block_sum(float v, float* lds) {
+  v = tiler::wave_sum_butterfly(v);
+  const uint32_t t = threadIdx.x;
+  if ((t & 63u) == 0) lds[t >> 6] = v;
+  __syncthreads();
+  float total = lds[0];
+#pragma unroll
+  for (uint32_t w = 1; w < kLongWaves; ++w) total = total + lds[w];
+  __syncthreads();  // lds may be reused by the caller's next combine
+  return total;
+}
+
+__device__ __forceinline__ float long_block_max(float v, float* lds) {
+  v = tiler::wave_max(v);
+  const uint32_t t = threadIdx.x;
+  if ((t & 63u) == 0) lds[t >> 6] = v;
+  __syncthreads();
+  float m = lds[0];
+#pragma unroll
+  for (uint32_t w = 1; w < kLongWaves; ++w) m = tiler::maximum_f32(m, lds[w]);
+  __syncthreads();
+  return m;
+}
+
+// ---- chunk access --------------------------------------------------------
+// bf16 chunk q = elements [8q, 8q+8); absent elements read as 0 (never folded).
+template <int AL>
+__device__ __forceinline__ u32x4 load_bf16_chunk(const uint16_t* __restrict__ x, uint64_t q,
+                                                 uint32_t extent) {
+  const uint64_t p0 = q * 8u;
+  if (AL && p0 + 8u <= extent) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + p0));
+  uint32_t tmp[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (p0 + e < extent) tmp[e >> 1] |= (uint32_t)x[p0 + e] << (16 * (e & 1));
+  return u32x4{tmp[0], tmp[1], tmp[2], tmp[3]};
+}
+
+template <int AL>
+__device__ __forceinline__ void store_bf16_chunk(uint16_t* __restrict__ y, uint64_t q, uint32_t extent,
+                                                 u32x4 v) {
+  const uint64_t p0 = q * 8u;
+  if (AL && p0 + 8u <= extent) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(y + p0));
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (p0 + e < extent) y[p0 + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+}
+
+// f32 chunk q = elements [4q, 4q+4); absent elements read as `pad`.
+template <int AL>
+__device__ __forceinline__ f32x4 load_f32_chunk(const float* __restrict__ x, uint64_t q, uint32_t extent,
+                                                float pad) {
+  const uint64_t p0 = q * 4u;
+  if (AL && p0 + 4u <= extent) return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + p0));
+  float tmp[4] = {pad, pad, pad, pad};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (p0 + e < extent) tmp[e] = x[p0 + e];
+  return f32x4{tmp[0], tmp[1], tmp[2], tmp[3]};
+}
+
+template <int AL>
+__device__ __forceinline__ void store_f32_chunk(float* __restrict__ y, uint64_t q, uint32_t extent, f32x4 v) {
+  const uint64_t p0 = q * 4u;
+  if (AL && p0 + 4u <= extent) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(y + p0));
+    return;
+  }
+  const float o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (p0 + e < extent) y[p0 + e] = o[e];
+}
+
+// ---- RMSNorm, bf16 -----------------------------------------------------------
+__device__ __forceinline__ float fold_sq_bf16(float acc, u32x4 v, uint64_t q, uint32_t extent) {
+  const uint64_t p0 = q * 8u;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (p0 + e < extent) {
+      float x = tiler::bf16_widen((v[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+      float sq = x * x;
+      acc = acc + sq;
+    }
+  return acc;
+}
+
+__device__ __forceinline__ u32x4 rms_out_bf16(u32x4 xv, u32x4 wv, float s) {
+  u32x4 o;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    float x0 = tiler::bf16_widen(xv[h] & 0xffffu), x1 = tiler::bf16_widen(xv[h] >> 16);
+    float w0 = tiler::bf16_widen(wv[h] & 0xffffu), w1 = tiler::bf16_widen(wv[h] >> 16);
+    float n0 = x0 * s, n1 = x1 * s;
+    o[h] = tiler::bf16_pack2(w0 * n0, w1 * n1);
+  }
+  return o;
+}
+
+template <int CH, int AL>
+__device__ __forceinline__ void rms_bf16_long_row(const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ w,
+                                                  uint16_t* __restrict__ y, uint32_t extent,
+                                                  float eps, float* lds) {
+  const uint32_t t = threadIdx.x;
+  const uint64_t chunks = (extent + 7u) / 8u;
+  float acc = -0.0f;
+  u32x4 xv[CH > 0 ? CH : 1];
+  if (CH > 0) {
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      xv[c] = q < chunks ? load_bf16_chunk<AL>(x, q, extent) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      if (q < chunks) acc = fold_sq_bf16(acc, xv[c], q, extent);
+    }
+  } else {
+    for (uint64_t q = t; q < chunks; q += kLongThreads) acc = fold_sq_bf16(acc, load_bf16_chunk<AL>(x, q, extent), q, extent);
+  }
+  const float total = long_block_sum(acc, lds);
+  const float s = tiler::rsqrt_f32_cr(total / (float)extent + eps);
+  if (CH > 0) {
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      if (q < chunks) store_bf16_chunk<AL>(y, q, extent, rms_out_bf16(xv[c], load_bf16_chunk<AL>(w, q, extent), s));
+    }
+  } else {
+    for (uint64_t q = t; q < chunks; q += kLongThreads)
+      store_bf16_chunk<AL>(y, q, extent, rms_out_bf16(load_bf16_chunk<AL>(x, q, extent), load_bf16_chunk<AL>(w, q, extent), s));
+  }
+}
+
+// ---- RMSNorm, f32 ------------------------------------------------------------
+__device__ __forceinline__ float fold_sq_f32(float acc, f32x4 v, uint64_t q, uint32_t extent) {
+  const uint64_t p0 = q * 4u;
+  const float e4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (p0 + e < extent) {
+      float sq = e4[e] * e4[e];
+      acc = acc + sq;
+    }
+  return acc;
+}
+
+__device__ __forceinline__ f32x4 rms_out_f32(f32x4 xv, f32x4 wv, float s) {
+  return f32x4{tiler::canon(wv.x * (xv.x * s)), tiler::canon(wv.y * (xv.y * s)),
+               tiler::canon(wv.z * (xv.z * s)), tiler::canon(wv.w * (xv.w * s))};
+}
+
+template <int CH, int AL>
+__device__ __forceinline__ void rms_f32_long_row(const float* __restrict__ x, const float* __restrict__ w,
+                                                 float* __restrict__ y, uint32_t extent, float eps,
+                                                 float* lds) {
+  const uint32_t t = threadIdx.x;
+  const uint64_t chunks = (extent + 3u) / 4u;
+  float acc = -0.0f;
+  f32x4 xv[CH > 0 ? CH : 1];
+  if (CH > 0) {
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      xv[c] = q < chunks ? load_f32_chunk<AL>(x, q, extent, 0.0f) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      if (q < chunks) acc = fold_sq_f32(acc, xv[c], q, extent);
+    }
+  } else {
+    for (uint64_t q = t; q < chunks; q += kLongThreads)
+      acc = fold_sq_f32(acc, load_f32_chunk<AL>(x, q, extent, 0.0f), q, extent);
+  }
+  const float total = long_block_sum(acc, lds);
+  const float s = tiler::rsqrt_f32_cr(total / (float)extent + eps);
+  if (CH > 0) {
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      if (q < chunks) store_f32_chunk<AL>(y, q, extent, rms_out_f32(xv[c], load_f32_chunk<AL>(w, q, extent, 0.0f), s));
+    }
+  } else {
+    for (uint64_t q = t; q < chunks; q += kLongThreads)
+      store_f32_chunk<AL>(y, q, extent,
+                          rms_out_f32(load_f32_chunk<AL>(x, q, extent, 0.0f), load_f32_chunk<AL>(w, q, extent, 0.0f), s));
+  }
+}
+
+// ---- softmax, f32 ------------------------------------------------------------
+__device__ __forceinline__ float max_chunk(float m, f32x4 v) {
+  m = tiler::maximum_f32(m, v.x);
+  m = tiler::maximum_f32(m, v.y);
+  m = tiler::maximum_f32(m, v.z);
+  return tiler::maximum_f32(m, v.w);
+}
+
+__device__ __forceinline__ f32x4 exp_chunk(f32x4 v, float m, const double* tab) {
+  return f32x4{tiler::exp_f32_cr(v.x - m, tab), tiler::exp_f32_cr(v.y - m, tab),
+               tiler::exp_f32_cr(v.z - m, tab), tiler::exp_f32_cr(v.w - m, tab)};
+}
+
+__device__ __forceinline__ float fold_chunk(float acc, f32x4 e, uint64_t q, uint32_t extent) {
+  const uint64_t p0 = q * 4u;
+  const float e4[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (p0 + i < extent) acc = acc + e4[i];
+  return acc;
+}
+
+__device__ __forceinline__ f32x4 scale_chunk(f32x4 e, float r) {
+  return f32x4{tiler::canon(e.x * r), tiler::canon(e.y * r), tiler::canon(e.z * r), tiler::canon(e.w * r)};
+}
+
+template <int CH, int AL>
+__device__ __forceinline__ void softmax_f32_long_row(const float* __restrict__ x, float* __restrict__ y,
+                                                     uint32_t extent, float* lds, const double* tab) {
+  const uint32_t t = threadIdx.x;
+  const uint64_t chunks = (extent + 3u) / 4u;
+  const float ninf = -__builtin_huge_valf();
+  f32x4 xv[CH > 0 ? CH : 1];
+  float m = ninf;
+  if (CH > 0) {
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      xv[c] = q < chunks ? load_f32_chunk<AL>(x, q, extent, ninf) : f32x4{ninf, ninf, ninf, ninf};
+    }
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) m = max_chunk(m, xv[c]);
+  } else {
+    for (uint64_t q = t; q < chunks; q += kLongThreads) m = max_chunk(m, load_f32_chunk<AL>(x, q, extent, ninf));
+  }
+  m = long_block_max(m, lds);
+  float acc = -0.0f;
+  if (CH > 0) {
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      xv[c] = exp_chunk(xv[c], m, tab);
+      if (q < chunks) acc = fold_chunk(acc, xv[c], q, extent);
+    }
+  } else {
+    for (uint64_t q = t; q < chunks; q += kLongThreads)
+      acc = fold_chunk(acc, exp_chunk(load_f32_chunk<AL>(x, q, extent, ninf), m, tab), q, extent);
+  }
+  const float d = long_block_sum(acc, lds);
+  const float r = 1.0f / d;
+  if (CH > 0) {
+#pragma unroll
+    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
+      const uint64_t q = t + (uint64_t)c * kLongThreads;
+      if (q < chunks) store_f32_chunk<AL>(y, q, extent, scale_chunk(xv[c], r));
+    }
+  } else {
+    for (uint64_t q = t; q < chunks; q += kLongThreads)
+      store_f32_chunk<AL>(y, q, extent, scale_chunk(exp_chunk(load_f32_chunk<AL>(x, q, extent, ninf), m, tab), r));
+  }
+}
+
+}  // namespace
+
+// Entry points: blockIdx.x is the row; 1024 threads.  Instances CH in
+// {1, 2, 4, 8} (register-resident) and 0 (streamed), each aligned (_a) and
+// element-wise (_u).  RMSNorm weights are one broadcast row (w_row_stride 0)
+// or a full tensor.
+#define TILER_RMS_BF16_LONG(CH, AL, SFX)                                                        \
+  extern "C" __global__ void __launch_bounds__(1024) tiler_rms_norm_bf16_long##CH##SFX(         \
+      const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint64_t w_row_stride,     \
+      uint16_t* __restrict__ y, uint32_t extent, float eps) {                                    \
+    __shared__ float lds[kLongWaves];                                                            \
+    const uint64_t row = blockIdx.x;                                                             \
+    rms_bf16_long_row<CH, AL>(x + row * extent, w + row * w_row_stride, y + row * extent, extent, \
+                              eps, lds);                                                          \
+  }
+#define TILER_RMS_F32_LONG(CH, AL, SFX)                                                         \
+  extern "C" __global__ void __launch_bounds__(1024) tiler_rms_norm_f32_long##CH##SFX(          \
+      const float* __restrict__ x, const float* __restrict__ w, uint64_t w_row_stride,           \
+      float* __restrict__ y, uint32_t extent, float eps) {                                       \
+    __shared__ float lds[kLongWaves];                                                            \
+    const uint64_t row = blockIdx.x;                                                             \
+    rms_f32_long_row<CH, AL>(x + row * extent, w + row * w_row_stride, y + row * extent, extent, \
+                             eps, lds);                                                           \
+  }
+#define TILER_SOFTMAX_F32_LONG(CH, AL, SFX)                                                     \
+  extern "C" __global__ void __launch_bounds__(1024) tiler_softmax_f32_long##CH##SFX(           \
+      const float* __restrict__ x, float* __restrict__ y, uint32_t extent) {                     \
+    __shared__ float lds[kLongWaves];                                                            \
+    __shared__ double tab[64];                                                                   \
+    if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Table64[threadIdx.x];                          \
+    __syncthreads();                                                                             \
+    const uint64_t row = blockIdx.x;                                                             \
+    softmax_f32_long_row<CH, AL>(x + row * extent, y + row * extent, extent, lds, tab);         \
+  }
+#define TILER_LONG_FAMILY(M) M(1, 1, _a) M(1, 0, _u) M(2, 1, _a) M(2, 0, _u) M(4, 1, _a) M(4, 0, _u) \
+  M(8, 1, _a) M(8, 0, _u) M(0, 1, _a) M(0, 0, _u)
+TILER_LONG_FAMILY(TILER_RMS_BF16_LONG)
+TILER_LONG_FAMILY(TILER_RMS_F32_LONG)
+TILER_LONG_FAMILY(TILER_SOFTMAX_F32_LONG)

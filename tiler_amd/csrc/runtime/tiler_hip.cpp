@@ -93,6 +93,36 @@ const EntryRow kEntries[] = {
     {"tiler_softmax_f32_ch32", "softmax-f32", 2},
     {"tiler_softmax_f32_ch32_full", "softmax-f32", 2},
     {"tiler_softmax_f32_ch32_u", "softmax-f32", 2},
+    {"tiler_rms_norm_bf16_long1_a", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long1_u", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long2_a", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long2_u", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long4_a", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long4_u", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long8_a", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long8_u", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long0_a", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_bf16_long0_u", "rms-norm-bf16/long-row", 3},
+    {"tiler_rms_norm_f32_long1_a", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long1_u", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long2_a", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long2_u", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long4_a", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long4_u", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long8_a", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long8_u", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long0_a", "rms-norm-f32/long-row", 3},
+    {"tiler_rms_norm_f32_long0_u", "rms-norm-f32/long-row", 3},
+    {"tiler_softmax_f32_long1_a", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long1_u", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long2_a", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long2_u", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long4_a", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long4_u", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long8_a", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long8_u", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long0_a", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long0_u", "softmax-f32/long-row", 2},
     {"tiler_gather_u128", "gather", 4},
     {"tiler_gather_u64", "gather", 4},
     {"tiler_gather_u32", "gather", 4},
@@ -176,6 +206,18 @@ tiler_hip_status launch(tiler_hip_context* ctx, const char* symbol, uint32_t gx,
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Rows longer than one wave holds (8192 elements) run one 1024-thread
+// workgroup per row: chunks per thread rounded up to a power of two while the
+// row fits in registers (<= 8 chunks), else 0 (the row is streamed).
+constexpr uint64_t kWaveRowMax = 8192;
+uint32_t long_row_chunks(uint64_t extent, uint32_t vec) {
+  uint64_t per = (((extent + vec - 1) / vec) + 1023) / 1024;
+  if (per > 8) return 0;
+  uint32_t ch = 1;
+  while (ch < per) ch <<= 1;
+  return ch;
+}
 
 uint32_t pow2_at_least(uint64_t v) {
   uint32_t p = 1;
@@ -661,6 +703,30 @@ tiler_hip_status tiler_hip_graph_destroy(tiler_hip_context* ctx, tiler_hip_graph
 }
 
 // ---------------------------------------------------------------------------
+tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_t extent,
+                                        uint32_t* vec, uint32_t* waves) {
+  if (!vec || !waves) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  switch (family) {
+    case TILER_HIP_ROWS_RMS_NORM:
+      if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16) return TILER_HIP_REFUSE_UNSUPPORTED;
+      *vec = dtype == TILER_HIP_BF16 ? 8 : 4;
+      *waves = extent > kWaveRowMax ? 16 : 1;
+      return TILER_HIP_OK;
+    case TILER_HIP_ROWS_SOFTMAX:
+      if (dtype != TILER_HIP_F32) return TILER_HIP_REFUSE_UNSUPPORTED;
+      *vec = 4;
+      *waves = extent > kWaveRowMax ? 16 : 1;
+      return TILER_HIP_OK;
+    case TILER_HIP_ROWS_SUM:
+      if (dtype != TILER_HIP_F32) return TILER_HIP_REFUSE_UNSUPPORTED;
+      *vec = 4;
+      *waves = 4;
+      return TILER_HIP_OK;
+    default:
+      return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  }
+}
+
 uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context* ctx, uint64_t n) {
   uint64_t tiles = (n + 1023) / 1024;
   uint64_t cap = ctx ? 2ull * ctx->compute_units : 512;
@@ -745,12 +811,23 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, cons
   if (!x || !w || !y) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   const uint32_t vec = dtype == TILER_HIP_BF16 ? 8 : 4;
   const uint32_t max_ch = dtype == TILER_HIP_BF16 ? 16 : 32;
-  uint64_t chunks = (extent + 64ull * vec - 1) / (64ull * vec);
-  uint32_t ch = pow2_at_least(chunks);
-  if (ch > max_ch || extent > 0xffffffffull)
-    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row longer than the register-resident realization");
+  if (extent > 0xffffffffull)
+    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
   const uint64_t elem = dtype == TILER_HIP_BF16 ? 2 : 4;
   bool al = aligned16(x) && aligned16(w) && aligned16(y) && (extent * elem) % 16 == 0;
+  uint64_t wstride_l = weight_broadcast ? 0 : extent;
+  uint32_t ext32_l = (uint32_t)extent;
+  if (extent > kWaveRowMax) {  // one workgroup per row
+    if (rows > 0x7fffffffull) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+    char lname[64];
+    std::snprintf(lname, sizeof(lname), "tiler_rms_norm_%s_long%u%s", dtype == TILER_HIP_BF16 ? "bf16" : "f32",
+                  long_row_chunks(extent, vec), al ? "_a" : "_u");
+    void* largs[] = {&x, &w, &wstride_l, &y, &ext32_l, &eps};
+    return launch(ctx, lname, (uint32_t)rows, 1, 1024, pick(ctx, stream), largs);
+  }
+  uint64_t chunks = (extent + 64ull * vec - 1) / (64ull * vec);
+  uint32_t ch = pow2_at_least(chunks);
+  if (ch > max_ch) return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row realization");
   bool full = al && extent == (uint64_t)ch * 64 * vec;
   char name[64];
   std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_ch%u%s",
@@ -769,10 +846,19 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (rows == 0 || extent == 0) return TILER_HIP_OK;
   if (!x || !y) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  uint32_t ch = pow2_at_least((extent + 255) / 256);
-  if (ch > 32 || extent > 0xffffffffull)
-    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row longer than the register-resident realization");
+  if (extent > 0xffffffffull)
+    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
   bool al = aligned16(x) && aligned16(y) && extent % 4 == 0;
+  if (extent > kWaveRowMax) {  // one workgroup per row
+    if (rows > 0x7fffffffull) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+    char lname[64];
+    std::snprintf(lname, sizeof(lname), "tiler_softmax_f32_long%u%s", long_row_chunks(extent, 4), al ? "_a" : "_u");
+    uint32_t ext32_l = (uint32_t)extent;
+    void* largs[] = {&x, &y, &ext32_l};
+    return launch(ctx, lname, (uint32_t)rows, 1, 1024, pick(ctx, stream), largs);
+  }
+  uint32_t ch = pow2_at_least((extent + 255) / 256);
+  if (ch > 32) return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row realization");
   bool full = al && extent == (uint64_t)ch * 256;
   char name[64];
   std::snprintf(name, sizeof(name), "tiler_softmax_f32_ch%u%s", ch, full ? "_full" : al ? "" : "_u");

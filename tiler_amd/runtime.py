@@ -278,6 +278,14 @@ class Context:
                                                     _ptr(c), epilogue, stream), "contract_bf16")
 
 
+def row_grouping(family: int, dtype: int, extent: int) -> tuple[int, int]:
+    """The declared (vec, waves) grouping the row kernels use for `extent`."""
+    vec, waves = ctypes.c_uint32(), ctypes.c_uint32()
+    _raise(L.lib().tiler_hip_row_grouping(family, dtype, extent, ctypes.byref(vec), ctypes.byref(waves)),
+           "row_grouping")
+    return vec.value, waves.value
+
+
 def validate_gather_index(index: np.ndarray, gathered: int, index_signed: bool):
     """Pre-commit bound check (a Refusal naming the first offending position)."""
     idx = np.ascontiguousarray(index, dtype=np.uint32) if index.dtype != np.uint32 else \
