@@ -168,9 +168,11 @@ __device__ __forceinline__ void contract_bf16_body(const uint16_t* __restrict__ 
 // 256 * k * 2 < 2^31, 16-byte aligned operands (the host checks all of it).
 //
 // One 1024-thread workgroup per 256 x 256 output tile: 16 waves in a 4 x 4
-// grid, wave (wm, wn) owning a 64 x 64 sub-tile as 2 x 2 accumulator blocks of
-// v_mfma_f32_32x32x16_bf16 (64 f32 per lane, four waves per SIMD, whose
-// interleaving hides the LDS latency that a single wave per SIMD exposes).
+// grid, wave (wm, wn) owning a 64 x 64 sub-tile as 4 x 4 accumulator blocks of
+// v_mfma_f32_16x16x32_bf16 (64 f32 per lane, four waves per SIMD, whose
+// interleaving hides the LDS latency).  The 16x16x32 form moves half the
+// accumulator data per flop of the 32x32x16 one; with Gaussian operands the
+// chip is power-limited, and that runs it at a higher clock.
 //
 // Operands: each workgroup's 256-row A and B panels are addressed through one
 // buffer resource apiece (32-bit offsets, hardware bounds) and move global ->
@@ -179,10 +181,10 @@ __device__ __forceinline__ void contract_bf16_body(const uint16_t* __restrict__ 
 // chunk c ^ ((r >> 1) & 7), so the 16 rows one ds_read_b128 phase touches
 // cover all 64 banks.
 //
-// Schedule per 64-deep k tile: four k steps of 16; the fragments of step s+1
-// are read while the MFMAs of step s run.  The workgroup barrier that retires
-// stage kt sits before step 3's MFMAs, so the refill of that stage (tile kt+2)
-// and the reads of tile kt+1's step 0 are issued under them.
+// Schedule per 64-deep k tile: two k steps of 32, each eight fragment reads
+// and sixteen MFMAs (the compiler waits per fragment, so the MFMAs start as
+// their operands land); the barrier that retires the stage follows, and the
+// refill of that stage with tile kt+2 is issued right after it.
 //
 // Tile order is XCD-aware: the 8 XCDs receive workgroups round robin, and the
 // 32 that one XCD runs together form a 4 x 8 block of tiles that share 4 A and
@@ -271,48 +273,35 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
     voff[j] = row * k * 2u + ((lane & 7u) ^ ((row >> 1) & 7u)) * 16u;
   }
 
-  f32x16 acc[2][2];
+  f32x4 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Fragment reads: A rows arow + 32i, B rows brow + 32j; lane half h takes
-  // k elements 8h .. 8h+7 of the step, i.e. logical chunk 2s + h.
-  const uint32_t arow = wm * kWaveRows + (lane & 31u), brow = wn * kWaveCols + (lane & 31u);
-  const uint32_t half = lane >> 5, swz = ((lane & 31u) >> 1) & 7u;  // (row >> 1) & 7 for row % 32 == lane % 32
-  bf16x8 fa[2][2], fb[2][2];
-  auto read_step = [&](const uint16_t* la, int step, int slot) {
+  // Fragment reads (v_mfma_f32_16x16x32_bf16): A block i covers rows
+  // arow + 16i, lane group g = lane / 16 takes k elements 8g .. 8g+7 of the
+  // 32-deep step, i.e. logical chunk 4s + g.
+  const uint32_t arow = wm * kWaveRows + (lane & 15u), brow = wn * kWaveCols + (lane & 15u);
+  const uint32_t grp = lane >> 4, swz = ((lane & 15u) >> 1) & 7u;  // (row >> 1) & 7 for row % 16 == lane % 16
+  bf16x8 fa[4], fb[4];
+  auto read_step = [&](const uint16_t* la, int step) {
     const uint16_t* lb = la + kT * kK;
-    const uint32_t chunk = ((uint32_t)step * 2u + half) ^ swz;
+    const uint32_t chunk = ((uint32_t)step * 4u + grp) ^ swz;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      fa[slot][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(la + (arow + i * 32u) * kK + chunk * 8u));
+    for (int i = 0; i < 4; ++i)
+      fa[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(la + (arow + i * 16u) * kK + chunk * 8u));
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      fb[slot][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(lb + (brow + j * 32u) * kK + chunk * 8u));
+    for (int j = 0; j < 4; ++j)
+      fb[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(lb + (brow + j * 16u) * kK + chunk * 8u));
   };
-  auto mfma_step = [&](int slot) {
+  auto mfma_step = [&]() {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
   };
-  // Steps 0..2 of one tile; the scheduling fences keep each step's reads
-  // ahead of the previous step's MFMAs.
-  auto steps_0_to_2 = [&](const uint16_t* la) {
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-      read_step(la, s + 1, (s + 1) & 1);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_step(s & 1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
   issue_operand_tile(pa, voff, 0, smem, wave_s);
   issue_operand_tile(pb, voff, 0, smem + kT * kK, wave_s);
   if (ktiles > 1) {
@@ -323,31 +312,29 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   asm volatile("s_barrier" ::: "memory");
-  read_step(smem, 0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  for (uint32_t kt = 0; kt + 1 < ktiles; ++kt) {
-    steps_0_to_2(smem + (kt & 1u) * kStageElems);
-    // Tile kt+1 landed (this wave's loads: vmcnt(0)) and this wave's reads of
-    // stage kt retired (lgkmcnt(0)).  After the barrier the stage may be
-    // refilled.  The LDS drain is asm because the compiler relaxes a builtin
-    // wait that no register use needs; the builtin after the barrier is
-    // already satisfied and only tells the compiler nothing is outstanding.
-    // No memory fence: one would drain the refill issued ahead (vmcnt(0)).
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    if (kt + 2 < ktiles) {
-      uint16_t* st = smem + (kt & 1u) * kStageElems;
-      issue_operand_tile(pa, voff, (kt + 2) * kK * 2u, st, wave_s);
-      issue_operand_tile(pb, voff, (kt + 2) * kK * 2u, st + kT * kK, wave_s);
+  for (uint32_t kt = 0; kt < ktiles; ++kt) {
+    const uint16_t* la = smem + (kt & 1u) * kStageElems;
+    read_step(la, 0);
+    mfma_step();
+    read_step(la, 1);
+    mfma_step();
+    if (kt + 1 < ktiles) {
+      // Tile kt+1 landed (this wave's loads: vmcnt(0)) and this wave's reads of
+      // stage kt retired (lgkmcnt(0)); after the barrier the stage may be
+      // refilled.  The LDS drain is asm because the compiler relaxes a builtin
+      // wait that no register use needs; the builtin after the barrier is
+      // already satisfied and only tells the compiler nothing is outstanding.
+      // No memory fence: one would drain the refill issued ahead (vmcnt(0)).
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      if (kt + 2 < ktiles) {
+        uint16_t* st = smem + (kt & 1u) * kStageElems;
+        issue_operand_tile(pa, voff, (kt + 2) * kK * 2u, st, wave_s);
+        issue_operand_tile(pb, voff, (kt + 2) * kK * 2u, st + kT * kK, wave_s);
+      }
     }
-    read_step(smem + ((kt + 1) & 1u) * kStageElems, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_step(1);
-    __builtin_amdgcn_sched_barrier(0);
   }
-  steps_0_to_2(smem + ((ktiles - 1) & 1u) * kStageElems);
-  mfma_step(1);
   __builtin_amdgcn_s_waitcnt(kWaitVmLgkm0);
   __syncthreads();  // every wave is done with the operand stages
 
@@ -357,11 +344,11 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
   uint16_t* cst = smem + wave * (kWaveRows * kWaveCols);
   const bool odd = lane & 1u;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
+      for (int r = 0; r < 4; r += 2) {
         float v0 = acc[i][j][r], v1 = acc[i][j][r + 1];
         if (kSilu) {
           v0 = silu_fast(v0);
@@ -369,8 +356,8 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
         }
         const float recv = __shfl_xor(odd ? v0 : v1, 1, 64);
         const float lo = odd ? recv : v0, hi = odd ? v1 : recv;
-        const uint32_t row = i * 32u + (r >> 2) * 8u + half * 4u + (r & 3) + (odd ? 1u : 0u);
-        const uint32_t col = j * 32u + ((lane & 31u) & ~1u);
+        const uint32_t row = i * 16u + grp * 4u + r + (odd ? 1u : 0u);
+        const uint32_t col = j * 16u + ((lane & 15u) & ~1u);
         const uint32_t q = (col >> 3) ^ (row & 7u);
         *reinterpret_cast<uint32_t*>(cst + row * kWaveCols + q * 8u + (col & 7u)) = tiler::bf16_pack2(lo, hi);
       }
