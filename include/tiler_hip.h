@@ -329,10 +329,12 @@ tiler_hip_status tiler_hip_map(tiler_hip_context *ctx, uint32_t op, uint32_t dty
 /* Broadcast / reindex move (broadcast-f32@2; tiler-reference/src/structural.rs:75-108):
  * out (row-major over out_dims) element reads source offset
  * sum coord_d * src_strides[d] (elements; stride 0 broadcasts). rank <= 8;
- * element_bytes 2 or 4. */
-tiler_hip_status tiler_hip_broadcast(tiler_hip_context *ctx, const void *src, uint32_t rank,
-                                     const uint64_t *out_dims, const uint64_t *src_strides,
-                                     uint32_t element_bytes, void *out, tiler_hip_stream stream);
+ * element_bytes 2 or 4.  The source holds src_elements elements: a geometry
+ * whose largest offset falls outside it refuses before any launch. */
+tiler_hip_status tiler_hip_broadcast(tiler_hip_context *ctx, const void *src, uint64_t src_elements,
+                                     uint32_t rank, const uint64_t *out_dims,
+                                     const uint64_t *src_strides, uint32_t element_bytes, void *out,
+                                     tiler_hip_stream stream);
 
 /* Gather (gather-f32@1; tiler-reference/src/structural.rs:513-606, bound rule
  * tiler-ir/src/semantic/gather.rs:438-455): source [outer, gathered, inner] of

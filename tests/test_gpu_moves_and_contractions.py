@@ -79,18 +79,107 @@ def test_bf16_maps_round_once_per_operation(ctx):
     assert np.array_equal(got, oracle.bf16_narrow(bf16_widen(xb) + bf16_widen(x2)))
 
 
+def _map_at(ctx, op, dtype, x, x2=None, bcast=False, a=0.0, b=0.0, offset=0):
+    """Runs the map with every operand starting `offset` elements into its buffer."""
+    eb = x.dtype.itemsize
+    dx = ctx.alloc(x.nbytes + 16)
+    dy = ctx.alloc(x.nbytes + 16)
+    d2 = ctx.alloc(x2.nbytes + 16) if x2 is not None else None
+    try:
+        vx, vy = dx.offset(offset * eb), dy.offset(offset * eb)
+        vx.upload(x)
+        v2 = None
+        if d2 is not None:
+            v2 = d2.offset(0 if bcast else offset * eb)
+            v2.upload(x2)
+        ctx.map(op, dtype, vx, x.size, vy, x2=v2, x2_broadcast=bcast, a=a, b=b)
+        ctx.synchronize()
+        return vy.download(x.dtype, x.shape)
+    finally:
+        dx.free(); dy.free()
+        if d2 is not None:
+            d2.free()
+
+
+@pytest.mark.parametrize("n", [1, 7, 8195])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_maps_vector_tail_and_unaligned_paths(ctx, n, offset):
+    """16-byte vector kernels with a scalar tail (aligned) and the scalar kernel
+    alone (offset by one element): identical arithmetic either way."""
+    rng = np.random.default_rng(n * 3 + offset)
+    x = rng.standard_normal(n).astype(np.float32)
+    x2 = rng.standard_normal(n).astype(np.float32)
+    s = np.asarray([0.75], np.float32)
+    got = _map_at(ctx, L.MAP_SCALE_BIAS, L.F32, x, a=2.0, b=-1.0, offset=offset)
+    assert np.array_equal(bits(got), bits(_canon((x * np.float32(2.0)).astype(np.float32) + np.float32(-1.0))))
+    assert np.array_equal(bits(_map_at(ctx, L.MAP_ADD, L.F32, x, x2, offset=offset)), bits(_canon(x + x2)))
+    assert np.array_equal(bits(_map_at(ctx, L.MAP_MULTIPLY, L.F32, x, s, bcast=True, offset=offset)),
+                          bits(_canon(x * s[0])))
+    assert np.array_equal(bits(_map_at(ctx, L.MAP_SILU, L.F32, x * 8, offset=offset)),
+                          bits(oracle.silu_f32(x * 8)))
+    xb, x2b = oracle.bf16_narrow(x), oracle.bf16_narrow(x2)
+    sb = oracle.bf16_narrow(s)
+    t = oracle.bf16_narrow(bf16_widen(xb) * np.float32(2.0))
+    assert np.array_equal(_map_at(ctx, L.MAP_SCALE_BIAS, L.BF16, xb, a=2.0, b=-1.0, offset=offset),
+                          oracle.bf16_narrow(bf16_widen(t) + np.float32(-1.0)))
+    assert np.array_equal(_map_at(ctx, L.MAP_MULTIPLY, L.BF16, xb, x2b, offset=offset),
+                          oracle.bf16_narrow(bf16_widen(xb) * bf16_widen(x2b)))
+    assert np.array_equal(_map_at(ctx, L.MAP_ADD, L.BF16, xb, sb, bcast=True, offset=offset),
+                          oracle.bf16_narrow(bf16_widen(xb) + bf16_widen(sb)[0]))
+
+
 def test_broadcast_moves_bytes(ctx):
     src = np.arange(6, dtype=np.float32).reshape(2, 3)
     src[0, 0] = f32(["0x7fc01234"])[0]
     ds = ctx.to_device(src)
     do = ctx.alloc(4 * 2 * 3 * 4)
     try:
-        ctx.broadcast(ds, [4, 2, 3], [0, 3, 1], 4, do)
+        ctx.broadcast(ds, 6, [4, 2, 3], [0, 3, 1], 4, do)
         ctx.synchronize()
         got = do.download(np.uint32, (4, 2, 3))
     finally:
         ds.free(); do.free()
     assert np.array_equal(got, np.broadcast_to(bits(src), (4, 2, 3)))
+
+
+def _broadcast(ctx, src, out_dims, strides):
+    ds = ctx.to_device(src)
+    n = int(np.prod(out_dims))
+    do = ctx.alloc(max(n * src.itemsize, 4))
+    try:
+        ctx.broadcast(ds, src.size, list(out_dims), list(strides), src.itemsize, do)
+        ctx.synchronize()
+        return do.download(src.dtype, tuple(out_dims))
+    finally:
+        ds.free(); do.free()
+
+
+@pytest.mark.parametrize("dtype,src_shape,out_dims,strides", [
+    (np.uint32, (4, 300), (3, 4, 300), (0, 300, 1)),    # rows copied as 16-byte vectors
+    (np.uint16, (5,), (5, 512), (1, 0)),                # inner axis broadcast: filled rows
+    (np.uint32, (300, 2), (2, 300), (1, 2)),            # transposed: strided rows
+    (np.uint16, (257,), (3, 257), (0, 1)),              # rows not a whole number of vectors
+    (np.uint32, (2, 3), (4, 2, 3), (0, 3, 1)),          # short rows: per-element kernel
+])
+def test_broadcast_row_and_element_modes(ctx, dtype, src_shape, out_dims, strides):
+    src = np.random.default_rng(len(out_dims) * 1000 + out_dims[-1]).integers(0, np.iinfo(dtype).max, src_shape,
+                                                                             dtype=dtype)
+    got = _broadcast(ctx, src, out_dims, strides)
+    want = np.lib.stride_tricks.as_strided(src, shape=out_dims,
+                                           strides=[s * src.itemsize for s in strides])
+    assert np.array_equal(got, want)
+
+
+def test_broadcast_refuses_reads_outside_the_source(ctx):
+    src = np.arange(5, dtype=np.uint32)
+    ds, do = ctx.to_device(src), ctx.alloc(64)
+    try:
+        with pytest.raises(tiler_amd.Refusal):
+            ctx.broadcast(ds, 5, [2, 3], [3, 1], 4, do)   # largest offset 1*3 + 2*1 = 5
+        ctx.broadcast(ds, 6 - 1, [2, 2], [3, 1], 4, do)     # largest offset 4: admitted
+        ctx.synchronize()
+    finally:
+        ds.free(); do.free()
 
 
 # -- gather -------------------------------------------------------------------------------

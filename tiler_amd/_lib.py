@@ -209,8 +209,8 @@ SIGNATURES = {
     "tiler_hip_rms_norm": (_S, [_CTX, _U32, _P, _P, _I32, _U64, _U64, _U32, _P, _P]),
     "tiler_hip_softmax_f32": (_S, [_CTX, _P, _U64, _U64, _P, _P]),
     "tiler_hip_map": (_S, [_CTX, _U32, _U32, _P, _P, _I32, _U64, _F, _F, _P, _P]),
-    "tiler_hip_broadcast": (_S, [_CTX, _P, _U32, ctypes.POINTER(_U64), ctypes.POINTER(_U64), _U32,
-                                 _P, _P]),
+    "tiler_hip_broadcast": (_S, [_CTX, _P, _U64, _U32, ctypes.POINTER(_U64), ctypes.POINTER(_U64),
+                                 _U32, _P, _P]),
     "tiler_hip_gather": (_S, [_CTX, _P, _U64, _U64, _U64, _U32, _P, _U64, _I32, _P, _P]),
     "tiler_hip_gather_status": (_S, [_CTX, _P, ctypes.POINTER(_U64)]),
     "tiler_hip_validate_gather_index": (_S, [_P, _U64, _I32, _U64, ctypes.POINTER(_U64),

@@ -75,6 +75,66 @@ tiler_map_bf16(const uint16_t* __restrict__ x, const uint16_t* __restrict__ x2,
   }
 }
 
+// Vectorized maps: 16 bytes per lane per step (4 f32 or 8 bf16 elements),
+// non-temporal loads and stores, the op and the rank-0 broadcast of x2 fixed at
+// compile time.  Every element sees exactly the scalar kernels' arithmetic.
+// The host uses them on 16-byte-aligned operands for the whole 16-byte chunks
+// and the scalar kernels for the tail.
+template <uint32_t OP, bool BCAST>
+__device__ __forceinline__ void map_f32_v4_body(const f32x4* __restrict__ x, const float* __restrict__ x2,
+                                                uint64_t n4, float a, float b, f32x4* __restrict__ y) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const float s2b = (OP >= 2 && BCAST) ? x2[0] : 0.0f;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const f32x4 v = __builtin_nontemporal_load(&x[i]);
+    f32x4 s2 = {s2b, s2b, s2b, s2b};
+    if (OP >= 2 && !BCAST) s2 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x2) + i);
+    const f32x4 o = {map_op(OP, v.x, s2.x, a, b), map_op(OP, v.y, s2.y, a, b),
+                     map_op(OP, v.z, s2.z, a, b), map_op(OP, v.w, s2.w, a, b)};
+    __builtin_nontemporal_store(o, &y[i]);
+  }
+}
+
+template <uint32_t OP, bool BCAST>
+__device__ __forceinline__ void map_bf16_v8_body(const u32x4* __restrict__ x, const uint16_t* __restrict__ x2,
+                                                 uint64_t n8, float a, float b, u32x4* __restrict__ y) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const float s2b = (OP >= 2 && BCAST) ? tiler::bf16_widen(x2[0]) : 0.0f;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    const u32x4 v = __builtin_nontemporal_load(&x[i]);
+    u32x4 w = {0, 0, 0, 0};
+    if (OP >= 2 && !BCAST) w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x2) + i);
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const float x0 = tiler::bf16_widen(v[h] & 0xffffu), x1 = tiler::bf16_widen(v[h] >> 16);
+      const float w0 = (OP >= 2 && !BCAST) ? tiler::bf16_widen(w[h] & 0xffffu) : s2b;
+      const float w1 = (OP >= 2 && !BCAST) ? tiler::bf16_widen(w[h] >> 16) : s2b;
+      o[h] = tiler::bf16_narrow(map_op_bf16(OP, x0, w0, a, b)) |
+             (tiler::bf16_narrow(map_op_bf16(OP, x1, w1, a, b)) << 16);
+    }
+    __builtin_nontemporal_store(o, &y[i]);
+  }
+}
+
+#define TILER_MAP_VEC(OP, BC, SFX)                                                                 \
+  extern "C" __global__ void __launch_bounds__(256) tiler_map_f32_v4_op##OP##SFX(                    \
+      const f32x4* __restrict__ x, const float* __restrict__ x2, uint64_t n4, float a, float b,      \
+      f32x4* __restrict__ y) {                                                                       \
+    map_f32_v4_body<OP, BC>(x, x2, n4, a, b, y);                                                     \
+  }                                                                                                  \
+  extern "C" __global__ void __launch_bounds__(256) tiler_map_bf16_v8_op##OP##SFX(                   \
+      const u32x4* __restrict__ x, const uint16_t* __restrict__ x2, uint64_t n8, float a, float b,   \
+      u32x4* __restrict__ y) {                                                                       \
+    map_bf16_v8_body<OP, BC>(x, x2, n8, a, b, y);                                                    \
+  }
+TILER_MAP_VEC(0, false, )
+TILER_MAP_VEC(1, false, )
+TILER_MAP_VEC(2, false, )
+TILER_MAP_VEC(2, true, _b)
+TILER_MAP_VEC(3, false, )
+TILER_MAP_VEC(3, true, _b)
+
 // Broadcast / reindex (tiler-reference/src/structural.rs:75-108): a pure move.
 // out element o (row-major over out_dims) reads source offset
 // sum_d coord_d(o) * src_stride_d; a broadcast axis has stride 0.  Rank <= 8.
@@ -97,6 +157,60 @@ __device__ __forceinline__ void broadcast_body(const T* __restrict__ src, T* __r
     }
     out[i] = src[off];
   }
+}
+
+// Row mode (innermost out dimension >= 256): each workgroup step takes one
+// out row, decodes its source row offset once, and copies the row -- in
+// 16-byte vectors when the row is contiguous in the source and both rows are
+// 16-byte aligned, as a replicated fill when the inner axis broadcasts (stride
+// 0), element by element otherwise.
+template <typename T>
+__device__ __forceinline__ void broadcast_rows_body(const T* __restrict__ src, T* __restrict__ out,
+                                                    uint64_t rows, const BroadcastGeometry& g) {
+  constexpr uint32_t kPer = 16 / sizeof(T);
+  const uint64_t inner = g.out_dims[g.rank - 1], sin = g.src_strides[g.rank - 1];
+  for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    uint64_t rem = r, base = 0;
+    for (int d = (int)g.rank - 2; d >= 0; --d) {
+      const uint64_t c = rem % g.out_dims[d];
+      rem /= g.out_dims[d];
+      base += c * g.src_strides[d];
+    }
+    const T* s = src + base;
+    T* o = out + r * inner;
+    const bool vec = ((uintptr_t)o & 15u) == 0 && inner % kPer == 0 &&
+                     (sin == 0 || (sin == 1 && ((uintptr_t)s & 15u) == 0));
+    if (vec) {
+      const uint64_t chunks = inner / kPer;
+      if (sin == 0) {
+        const T v = s[0];
+        T lanes[kPer];
+#pragma unroll
+        for (uint32_t e = 0; e < kPer; ++e) lanes[e] = v;
+        u32x4 fill;
+        __builtin_memcpy(&fill, lanes, 16);
+        for (uint64_t q = threadIdx.x; q < chunks; q += blockDim.x)
+          __builtin_nontemporal_store(fill, reinterpret_cast<u32x4*>(o) + q);
+      } else {
+        for (uint64_t q = threadIdx.x; q < chunks; q += blockDim.x)
+          __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(s) + q),
+                                      reinterpret_cast<u32x4*>(o) + q);
+      }
+    } else {
+      for (uint64_t j = threadIdx.x; j < inner; j += blockDim.x) o[j] = s[j * sin];
+    }
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+tiler_broadcast_rows_u32(const uint32_t* __restrict__ src, uint32_t* __restrict__ out, uint64_t rows,
+                         BroadcastGeometry g) {
+  broadcast_rows_body<uint32_t>(src, out, rows, g);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_broadcast_rows_u16(const uint16_t* __restrict__ src, uint16_t* __restrict__ out, uint64_t rows,
+                         BroadcastGeometry g) {
+  broadcast_rows_body<uint16_t>(src, out, rows, g);
 }
 
 extern "C" __global__ void __launch_bounds__(256)

@@ -130,8 +130,22 @@ const EntryRow kEntries[] = {
     {"tiler_gather_u8", "gather", 4},
     {"tiler_map_f32", "pointwise-f32", 3},
     {"tiler_map_bf16", "pointwise-bf16", 3},
+    {"tiler_map_f32_v4_op0", "pointwise-f32", 3},
+    {"tiler_map_bf16_v8_op0", "pointwise-bf16", 3},
+    {"tiler_map_f32_v4_op1", "pointwise-f32", 3},
+    {"tiler_map_bf16_v8_op1", "pointwise-bf16", 3},
+    {"tiler_map_f32_v4_op2", "pointwise-f32", 3},
+    {"tiler_map_bf16_v8_op2", "pointwise-bf16", 3},
+    {"tiler_map_f32_v4_op2_b", "pointwise-f32", 3},
+    {"tiler_map_bf16_v8_op2_b", "pointwise-bf16", 3},
+    {"tiler_map_f32_v4_op3", "pointwise-f32", 3},
+    {"tiler_map_bf16_v8_op3", "pointwise-bf16", 3},
+    {"tiler_map_f32_v4_op3_b", "pointwise-f32", 3},
+    {"tiler_map_bf16_v8_op3_b", "pointwise-bf16", 3},
     {"tiler_broadcast_u32", "broadcast", 2},
     {"tiler_broadcast_u16", "broadcast", 2},
+    {"tiler_broadcast_rows_u32", "broadcast", 2},
+    {"tiler_broadcast_rows_u16", "broadcast", 2},
     {"tiler_fill_u32", "fill", 1},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_bf16_t128", "tensor-contraction-bf16/cooperative", 3},
@@ -881,11 +895,33 @@ tiler_hip_status tiler_hip_map(tiler_hip_context* ctx, uint32_t op, uint32_t dty
   if (dtype == TILER_HIP_BF16 && op == TILER_HIP_MAP_SILU)
     return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "silu is an f32 family");
   uint64_t stride2 = x2_broadcast ? 0 : 1;
-  uint64_t blocks = (n + 255) / 256;
+  hipStream_t s = pick(ctx, stream);
+  const bool binary = op == TILER_HIP_MAP_ADD || op == TILER_HIP_MAP_MULTIPLY;
+  const uint64_t per = dtype == TILER_HIP_BF16 ? 8 : 4;  // elements per 16-byte chunk
+  uint64_t head = 0;                                      // elements the vector kernel covers
+  if (aligned16(x) && aligned16(y) && (!binary || x2_broadcast || aligned16(x2))) head = n / per * per;
+  if (head) {
+    uint64_t chunks = head / per;
+    uint64_t blocks = (chunks + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    char name[48];
+    std::snprintf(name, sizeof(name), "tiler_map_%s_op%u%s", dtype == TILER_HIP_BF16 ? "bf16_v8" : "f32_v4", op,
+                  binary && x2_broadcast ? "_b" : "");
+    void* vargs[] = {&x, &x2, &chunks, &a, &b, &y};
+    tiler_hip_status st = launch(ctx, name, (uint32_t)blocks, 1, 256, s, vargs);
+    if (st != TILER_HIP_OK || head == n) return st;
+  }
+  // scalar kernel for unaligned operands or the tail after the 16-byte chunks
+  const uint64_t eb = dtype == TILER_HIP_BF16 ? 2 : 4;
+  const void* xt = static_cast<const char*>(x) + head * eb;
+  const void* x2t = x2 && !x2_broadcast ? static_cast<const char*>(x2) + head * eb : x2;
+  void* yt = static_cast<char*>(y) + head * eb;
+  uint64_t rest = n - head;
+  uint64_t blocks = (rest + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  void* args[] = {&x, &x2, &stride2, &n, &op, &a, &b, &y};
+  void* args[] = {&xt, &x2t, &stride2, &rest, &op, &a, &b, &yt};
   return launch(ctx, dtype == TILER_HIP_BF16 ? "tiler_map_bf16" : "tiler_map_f32",
-                (uint32_t)blocks, 1, 256, pick(ctx, stream), args);
+                (uint32_t)blocks, 1, 256, s, args);
 }
 
 struct BroadcastGeometryHost {
@@ -894,9 +930,10 @@ struct BroadcastGeometryHost {
   uint32_t rank;
 };
 
-tiler_hip_status tiler_hip_broadcast(tiler_hip_context* ctx, const void* src, uint32_t rank,
-                                     const uint64_t* out_dims, const uint64_t* src_strides,
-                                     uint32_t element_bytes, void* out, tiler_hip_stream stream) {
+tiler_hip_status tiler_hip_broadcast(tiler_hip_context* ctx, const void* src, uint64_t src_elements,
+                                     uint32_t rank, const uint64_t* out_dims,
+                                     const uint64_t* src_strides, uint32_t element_bytes, void* out,
+                                     tiler_hip_stream stream) {
   if (!ctx || rank > 8 || (rank && (!out_dims || !src_strides)))
     return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (element_bytes != 2 && element_bytes != 4)
@@ -904,18 +941,37 @@ tiler_hip_status tiler_hip_broadcast(tiler_hip_context* ctx, const void* src, ui
   BroadcastGeometryHost g;
   std::memset(&g, 0, sizeof(g));
   g.rank = rank;
-  uint64_t n = 1;
+  uint64_t n = 1, last = 0;  // output elements; largest source offset read
+  bool overflow = false;
   for (uint32_t d = 0; d < rank; ++d) {
     g.out_dims[d] = out_dims[d];
     g.src_strides[d] = src_strides[d];
+    if (out_dims[d] && n > UINT64_MAX / out_dims[d]) overflow = true;
     n *= out_dims[d];
   }
   if (n == 0) return TILER_HIP_OK;
+  for (uint32_t d = 0; d < rank && !overflow; ++d) {
+    const uint64_t span = out_dims[d] - 1;
+    if (span && src_strides[d] > (UINT64_MAX - last) / span) overflow = true;
+    else last += span * src_strides[d];
+  }
+  if (overflow || last >= src_elements)
+    return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "broadcast geometry reads outside the source");
+  if (!src || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipStream_t s = pick(ctx, stream);
+  const uint64_t inner = rank ? out_dims[rank - 1] : 1;
+  if (rank && inner >= 256) {  // row mode: one source row offset per workgroup step
+    uint64_t rows = n / inner;
+    uint64_t blocks = rows < 8192 ? rows : 8192;
+    void* args[] = {&src, &out, &rows, &g};
+    return launch(ctx, element_bytes == 4 ? "tiler_broadcast_rows_u32" : "tiler_broadcast_rows_u16",
+                  (uint32_t)blocks, 1, 256, s, args);
+  }
   uint64_t blocks = (n + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   void* args[] = {&src, &out, &n, &g};
   return launch(ctx, element_bytes == 4 ? "tiler_broadcast_u32" : "tiler_broadcast_u16",
-                (uint32_t)blocks, 1, 256, pick(ctx, stream), args);
+                (uint32_t)blocks, 1, 256, s, args);
 }
 
 tiler_hip_status tiler_hip_validate_gather_index(const uint32_t* index, uint64_t count,

@@ -245,12 +245,14 @@ class Context:
                                           1 if x2_broadcast else 0, n, a, b, _ptr(y), stream),
                     "map")
 
-    def broadcast(self, src, out_dims, src_strides, element_bytes: int, out, stream=None):
+    def broadcast(self, src, src_elements: int, out_dims, src_strides, element_bytes: int, out,
+                  stream=None):
         rank = len(out_dims)
         dims = (ctypes.c_uint64 * max(rank, 1))(*out_dims)
         strides = (ctypes.c_uint64 * max(rank, 1))(*src_strides)
-        self._check(L.lib().tiler_hip_broadcast(self.handle, _ptr(src), rank, dims, strides,
-                                                element_bytes, _ptr(out), stream), "broadcast")
+        self._check(L.lib().tiler_hip_broadcast(self.handle, _ptr(src), src_elements, rank, dims,
+                                                strides, element_bytes, _ptr(out), stream),
+                    "broadcast")
 
     def gather(self, source, outer: int, gathered: int, inner: int, element_bytes: int, index,
                index_count: int, out, index_signed: bool = False, stream=None):
