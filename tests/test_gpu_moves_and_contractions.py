@@ -301,6 +301,31 @@ def test_bf16_contraction_within_frobenius_bound(ctx, m, n, k, silu):
     assert _frob(got, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("m,n,k", [(4000, 4104, 136), (4096, 4096, 72), (1000, 2048, 520), (64, 4096, 256),
+                                   (3, 8, 8)])
+def test_bf16_contraction_ragged_edges(ctx, m, n, k):
+    """Rows past m and n load as zeros, k past a multiple of 64 is masked in both
+    operands, and only in-range outputs are stored (the C buffer is poisoned
+    with NaN bf16 first, so a stray store or a missed one shows)."""
+    rng = np.random.default_rng(m + n + k)
+    ab = oracle.bf16_narrow((rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32))
+    bb = oracle.bf16_narrow((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
+    da, db = ctx.to_device(ab), ctx.to_device(bb)
+    dc = ctx.alloc(m * n * 2 + 64)
+    try:
+        ctx.fill_u32(dc, 0x7FC17FC1, (m * n * 2 + 64) // 4)
+        ctx.contract_bf16(da, db, m, n, k, dc, L.EPILOGUE_SILU)
+        ctx.synchronize()
+        raw = dc.download(np.uint16, (m * n + 32,))
+    finally:
+        da.free(); db.free(); dc.free()
+    got, guard = raw[:m * n].reshape(m, n), raw[m * n:]
+    assert (guard == 0x7FC1).all()
+    ref = oracle.silu_f32(oracle.contract_strict_f32(bf16_widen(ab), bf16_widen(bb), m, n, k)).reshape(m, n)
+    assert _frob(got, ref) <= 1e-2
+    assert not np.isnan(bf16_widen(got)).any()
+
+
 def test_bf16_contraction_full_size_config(ctx):
     """C5: bf16 A, B [4096 x 4096] ~ N(0, 1/sqrt(4096)), f32 accumulation,
     fused SiLU, bf16 C: relative Frobenius error <= 1e-2 against the strict

@@ -5,11 +5,13 @@
 //   seeded at the first product, acc = fl(acc + p) over ascending k, no FMA.
 //   16x16 LDS tiles with a serial in-tile fold, the shape of tiler-metal's
 //   contraction_tiled_cooperative golden; bit-exact with the reference.
-// * tiler_contract_bf16_* -- the cooperative bf16 contraction on MFMA
-//   (v_mfma_f32_32x32x16_bf16): bf16 operands, f32 accumulation, an optional
-//   fused SiLU epilogue on the f32 accumulator, one bf16 narrowing.  Guarded
-//   tails: out-of-range operand elements are zero-filled, out-of-range outputs
-//   are not stored.
+// * tiler_contract_bf16_{,silu_}t256 / t128 -- the cooperative bf16
+//   contraction on MFMA (v_mfma_f32_16x16x32_bf16), LDS-staged by buffer
+//   loads: bf16 operands, f32 accumulation, an optional fused SiLU epilogue on
+//   the f32 accumulator, one bf16 narrowing.  Any m; n and k multiples of 8.
+// * tiler_contract_bf16_{,silu_}g128[_k] -- the guarded general form
+//   (v_mfma_f32_32x32x16_bf16, register-staged) for any n and k: out-of-range
+//   operand elements are zero-filled, out-of-range outputs are not stored.
 #include "common.h"
 
 using tiler::canon;
@@ -164,22 +166,24 @@ __device__ __forceinline__ void contract_bf16_body(const uint16_t* __restrict__ 
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// Tile-aligned bf16 contraction: m, n multiples of 256, k a multiple of 64 with
-// 256 * k * 2 < 2^31, 16-byte aligned operands (the host checks all of it).
+// Staged bf16 contraction: any m >= 1, n and k multiples of 8, 16-byte aligned
+// operands, 256 * k * 2 < 2^31 (the host checks all of it).
 //
-// One 1024-thread workgroup per 256 x 256 output tile: 16 waves in a 4 x 4
-// grid, wave (wm, wn) owning a 64 x 64 sub-tile as 4 x 4 accumulator blocks of
-// v_mfma_f32_16x16x32_bf16 (64 f32 per lane, four waves per SIMD, whose
-// interleaving hides the LDS latency).  The 16x16x32 form moves half the
-// accumulator data per flop of the 32x32x16 one; with Gaussian operands the
-// chip is power-limited, and that runs it at a higher clock.
+// One workgroup per TILE x TILE output tile (TILE 256: 16 waves in a 4 x 4
+// grid; TILE 128: 4 waves in 2 x 2), wave (wm, wn) owning a 64 x 64 sub-tile as
+// 4 x 4 accumulator blocks of v_mfma_f32_16x16x32_bf16 (64 f32 per lane).
+// The 16x16x32 form moves half the accumulator data per flop of the 32x32x16
+// one; with Gaussian operands the chip is power-limited, and that runs it at a
+// higher clock.  The host takes TILE 128 when 256-tiles would leave CUs idle.
 //
-// Operands: each workgroup's 256-row A and B panels are addressed through one
-// buffer resource apiece (32-bit offsets, hardware bounds) and move global ->
-// LDS with buffer_load_dwordx4 ... lds, in 256 x 64 tiles double-buffered
-// (2 stages x 64 KiB).  LDS rows are 128 B; 16-byte chunk c of row r sits at
-// chunk c ^ ((r >> 1) & 7), so the 16 rows one ds_read_b128 phase touches
-// cover all 64 banks.
+// Operands: each workgroup's TILE-row A and B panels are addressed through one
+// buffer resource apiece (32-bit offsets; the record count stops at the last
+// real row, so rows past m or n load as zeros) and move global -> LDS with
+// buffer_load_dwordx4 ... lds, in TILE x 64 tiles double-buffered.  LDS rows
+// are 128 B; 16-byte chunk c of row r sits at chunk c ^ ((r >> 1) & 7), so the
+// 16 rows one ds_read_b128 phase touches cover all 64 banks.  When k is not a
+// multiple of 64, the last tile's fragments past k are zeroed in both operands
+// (the bytes loaded there belong to the next row).
 //
 // Schedule per 64-deep k tile: two k steps of 32, each eight fragment reads
 // and sixteen MFMAs (the compiler waits per fragment, so the MFMAs start as
@@ -190,15 +194,12 @@ __device__ __forceinline__ void contract_bf16_body(const uint16_t* __restrict__ 
 // 32 that one XCD runs together form a 4 x 8 block of tiles that share 4 A and
 // 8 B panels in that XCD's L2.  The epilogue (optional SiLU on the f32
 // accumulator, then one bf16 narrowing) transposes through LDS so C leaves in
-// 16-byte row chunks.
+// 16-byte row chunks; rows past m and chunks past n are not stored.
 namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kT = 256, kK = 64;
-constexpr int kWaves = 16, kWaveRows = 64, kWaveCols = 64;
-constexpr int kLoadsPerOperand = kT / 8 / kWaves;     // 8-row buffer loads per wave per operand tile
-constexpr uint32_t kStageElems = 2u * kT * kK;        // A tile then B tile, bf16 elements
+constexpr int kK = 64;
 
 __device__ __forceinline__ float silu_fast(float v) {
   // Epilogue SiLU: hardware exp2 and reciprocal (relative error ~1e-7),
@@ -214,34 +215,38 @@ constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 constexpr int kWaitVmLgkm0 = 0x0070;  // vmcnt(0) lgkmcnt(0)
 constexpr int kWaitLgkm0 = 0xC07F;    // lgkmcnt(0)
 
-// Issues this wave's share of one 256 x 64 operand tile: load j fills rows
-// R = (wave * kLoadsPerOperand + j) * 8 .. R + 7 of the LDS tile, lane i the
-// physical chunk i % 8 of row R + i / 8.  voff[j] is that lane's byte offset
-// in the panel at k = 0 (with the chunk swizzle applied); k0_bytes moves along k.
+// Issues this wave's share of one TILE x 64 operand tile: load j fills rows
+// R = (wave * LOADS + j) * 8 .. R + 7 of the LDS tile, lane i the physical
+// chunk i % 8 of row R + i / 8.  voff[j] is that lane's byte offset in the
+// panel at k = 0 (with the chunk swizzle applied); k0_bytes moves along k.
+template <int LOADS>
 __device__ __forceinline__ void issue_operand_tile(__amdgpu_buffer_rsrc_t panel, const uint32_t* voff,
                                                    uint32_t k0_bytes, uint16_t* lds_tile,
                                                    uint32_t wave_s) {
 #pragma unroll
-  for (int j = 0; j < kLoadsPerOperand; ++j)
+  for (int j = 0; j < LOADS; ++j)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        panel, (lds_void*)(lds_tile + (wave_s * kLoadsPerOperand + j) * 8u * kK), 16, voff[j],
-        k0_bytes, 0, 0);
+        panel, (lds_void*)(lds_tile + (wave_s * LOADS + j) * 8u * kK), 16, voff[j], k0_bytes, 0, 0);
 }
 
-template <bool kSilu>
-__device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restrict__ a,
-                                                        const uint16_t* __restrict__ b,
-                                                        uint32_t m, uint32_t n, uint32_t k,
-                                                        uint16_t* __restrict__ c) {
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * kStageElems];  // 128 KiB
+template <int TILE, bool kSilu>
+__device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __restrict__ a,
+                                                          const uint16_t* __restrict__ b,
+                                                          uint32_t m, uint32_t n, uint32_t k,
+                                                          uint16_t* __restrict__ c) {
+  constexpr int kGrid = TILE / 64;                    // waves per side
+  constexpr int kWaves = kGrid * kGrid;
+  constexpr int kLoads = TILE / 8 / kWaves;           // 8-row loads per wave per operand tile
+  constexpr uint32_t kStageElems = 2u * TILE * kK;    // A tile then B tile, bf16 elements
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * kStageElems];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
-  const uint32_t wm = wave >> 2, wn = wave & 3u;
+  const uint32_t wm = wave / kGrid, wn = wave % kGrid;
 
   // XCD-aware tile order: workgroup id -> (xcd, slot); xcd picks a 4x8 block
   // of the tile grid, slot a tile inside it.  Row-major when the grid is not a
   // whole number of 4x8 blocks per XCD.
-  const uint32_t tiles_n = n / kT, tiles_m = m / kT;
+  const uint32_t tiles_n = (n + TILE - 1) / TILE, tiles_m = (m + TILE - 1) / TILE;
   uint32_t tm, tn;
   {
     const uint32_t id = blockIdx.x;
@@ -258,18 +263,19 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
       tn = id % tiles_n;
     }
   }
-  const uint32_t m0 = tm * kT, n0 = tn * kT;
-  const uint32_t ktiles = k / kK;
+  const uint32_t m0 = tm * TILE, n0 = tn * TILE;
+  const uint32_t ktiles = (k + kK - 1) / kK;
+  const uint32_t k_last = k - (ktiles - 1) * kK;  // valid k in the last tile (a multiple of 8)
 
-  const uint32_t panel_bytes = (uint32_t)kT * k * 2u;
+  const uint32_t rows_a = m - m0 < TILE ? m - m0 : TILE, rows_b = n - n0 < TILE ? n - n0 : TILE;
   const __amdgpu_buffer_rsrc_t pa = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a + (uint64_t)m0 * k), (short)0, panel_bytes, 0x00020000);
+      (void*)(a + (uint64_t)m0 * k), (short)0, rows_a * k * 2u, 0x00020000);
   const __amdgpu_buffer_rsrc_t pb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(b + (uint64_t)n0 * k), (short)0, panel_bytes, 0x00020000);
-  uint32_t voff[kLoadsPerOperand];
+      (void*)(b + (uint64_t)n0 * k), (short)0, rows_b * k * 2u, 0x00020000);
+  uint32_t voff[kLoads];
 #pragma unroll
-  for (int j = 0; j < kLoadsPerOperand; ++j) {
-    const uint32_t row = (wave * kLoadsPerOperand + j) * 8u + (lane >> 3);
+  for (int j = 0; j < kLoads; ++j) {
+    const uint32_t row = (wave * kLoads + j) * 8u + (lane >> 3);
     voff[j] = row * k * 2u + ((lane & 7u) ^ ((row >> 1) & 7u)) * 16u;
   }
 
@@ -282,11 +288,11 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
   // Fragment reads (v_mfma_f32_16x16x32_bf16): A block i covers rows
   // arow + 16i, lane group g = lane / 16 takes k elements 8g .. 8g+7 of the
   // 32-deep step, i.e. logical chunk 4s + g.
-  const uint32_t arow = wm * kWaveRows + (lane & 15u), brow = wn * kWaveCols + (lane & 15u);
+  const uint32_t arow = wm * 64u + (lane & 15u), brow = wn * 64u + (lane & 15u);
   const uint32_t grp = lane >> 4, swz = ((lane & 15u) >> 1) & 7u;  // (row >> 1) & 7 for row % 16 == lane % 16
   bf16x8 fa[4], fb[4];
   auto read_step = [&](const uint16_t* la, int step) {
-    const uint16_t* lb = la + kT * kK;
+    const uint16_t* lb = la + TILE * kK;
     const uint32_t chunk = ((uint32_t)step * 4u + grp) ^ swz;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -295,6 +301,17 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
     for (int j = 0; j < 4; ++j)
       fb[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(lb + (brow + j * 16u) * kK + chunk * 8u));
   };
+  // The last tile of a k that is not a multiple of 64: zero this lane's
+  // fragments whose 8 k elements lie past k (both operands, so bytes from the
+  // next row never meet a product).
+  auto mask_step = [&](int step) {
+    if ((uint32_t)step * 32u + grp * 8u >= k_last) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fa[i] = as_bf16x8(u32x4{0, 0, 0, 0});
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fb[j] = as_bf16x8(u32x4{0, 0, 0, 0});
+    }
+  };
   auto mfma_step = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -302,38 +319,46 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
       for (int j = 0; j < 4; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
   };
-  issue_operand_tile(pa, voff, 0, smem, wave_s);
-  issue_operand_tile(pb, voff, 0, smem + kT * kK, wave_s);
+
+  issue_operand_tile<kLoads>(pa, voff, 0, smem, wave_s);
+  issue_operand_tile<kLoads>(pb, voff, 0, smem + TILE * kK, wave_s);
   if (ktiles > 1) {
-    issue_operand_tile(pa, voff, kK * 2u, smem + kStageElems, wave_s);
-    issue_operand_tile(pb, voff, kK * 2u, smem + kStageElems + kT * kK, wave_s);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kLoadsPerOperand));  // tile 0's loads landed
+    issue_operand_tile<kLoads>(pa, voff, kK * 2u, smem + kStageElems, wave_s);
+    issue_operand_tile<kLoads>(pb, voff, kK * 2u, smem + kStageElems + TILE * kK, wave_s);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kLoads));  // tile 0's loads landed
   } else {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   asm volatile("s_barrier" ::: "memory");
-  for (uint32_t kt = 0; kt < ktiles; ++kt) {
+  for (uint32_t kt = 0; kt + 1 < ktiles; ++kt) {
     const uint16_t* la = smem + (kt & 1u) * kStageElems;
     read_step(la, 0);
     mfma_step();
     read_step(la, 1);
     mfma_step();
-    if (kt + 1 < ktiles) {
-      // Tile kt+1 landed (this wave's loads: vmcnt(0)) and this wave's reads of
-      // stage kt retired (lgkmcnt(0)); after the barrier the stage may be
-      // refilled.  The LDS drain is asm because the compiler relaxes a builtin
-      // wait that no register use needs; the builtin after the barrier is
-      // already satisfied and only tells the compiler nothing is outstanding.
-      // No memory fence: one would drain the refill issued ahead (vmcnt(0)).
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-      if (kt + 2 < ktiles) {
-        uint16_t* st = smem + (kt & 1u) * kStageElems;
-        issue_operand_tile(pa, voff, (kt + 2) * kK * 2u, st, wave_s);
-        issue_operand_tile(pb, voff, (kt + 2) * kK * 2u, st + kT * kK, wave_s);
-      }
+    // Tile kt+1 landed (this wave's loads: vmcnt(0)) and this wave's reads of
+    // stage kt retired (lgkmcnt(0)); after the barrier the stage may be
+    // refilled.  The LDS drain is asm because the compiler relaxes a builtin
+    // wait that no register use needs; the builtin after the barrier is
+    // already satisfied and only tells the compiler nothing is outstanding.
+    // No memory fence: one would drain the refill issued ahead (vmcnt(0)).
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    if (kt + 2 < ktiles) {
+      uint16_t* st = smem + (kt & 1u) * kStageElems;
+      issue_operand_tile<kLoads>(pa, voff, (kt + 2) * kK * 2u, st, wave_s);
+      issue_operand_tile<kLoads>(pb, voff, (kt + 2) * kK * 2u, st + TILE * kK, wave_s);
     }
+  }
+  {  // the last tile, masked past k when k is not a multiple of 64
+    const uint16_t* la = smem + ((ktiles - 1) & 1u) * kStageElems;
+    read_step(la, 0);
+    if (k_last != (uint32_t)kK) mask_step(0);
+    mfma_step();
+    read_step(la, 1);
+    if (k_last != (uint32_t)kK) mask_step(1);
+    mfma_step();
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmLgkm0);
   __syncthreads();  // every wave is done with the operand stages
@@ -341,7 +366,7 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
   // Epilogue: wave-private 64 x 64 bf16 region (8 KiB) with 128-B rows, chunk
   // q of row r at q ^ (r & 7).  Lanes 2c and 2c+1 hold adjacent columns of
   // rows r and r+1; one exchange lets each write a 32-bit column pair.
-  uint16_t* cst = smem + wave * (kWaveRows * kWaveCols);
+  uint16_t* cst = smem + wave * (64u * 64u);
   const bool odd = lane & 1u;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -359,32 +384,38 @@ __device__ __forceinline__ void contract_bf16_t256_body(const uint16_t* __restri
         const uint32_t row = i * 16u + grp * 4u + r + (odd ? 1u : 0u);
         const uint32_t col = j * 16u + ((lane & 15u) & ~1u);
         const uint32_t q = (col >> 3) ^ (row & 7u);
-        *reinterpret_cast<uint32_t*>(cst + row * kWaveCols + q * 8u + (col & 7u)) = tiler::bf16_pack2(lo, hi);
+        *reinterpret_cast<uint32_t*>(cst + row * 64u + q * 8u + (col & 7u)) = tiler::bf16_pack2(lo, hi);
       }
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   __builtin_amdgcn_wave_barrier();
-  const uint64_t grow0 = m0 + wm * kWaveRows, gcol0 = n0 + wn * kWaveCols;
+  const uint32_t grow0 = m0 + wm * 64u, gcol0 = n0 + wn * 64u;
 #pragma unroll 4
-  for (int it = 0; it < kWaveRows * kWaveCols / 8 / 64; ++it) {
+  for (int it = 0; it < 64 * 8 / 64; ++it) {
     const uint32_t qid = it * 64u + lane;
     const uint32_t row = qid >> 3, q = qid & 7u;
-    u32x4 v = *reinterpret_cast<const u32x4*>(cst + row * kWaveCols + ((q ^ (row & 7u)) * 8u));
-    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(c + (grow0 + row) * n + gcol0 + q * 8u));
+    if (grow0 + row < m && gcol0 + q * 8u < n) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(cst + row * 64u + ((q ^ (row & 7u)) * 8u));
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(c + (uint64_t)(grow0 + row) * n + gcol0 + q * 8u));
+    }
   }
 }
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(1024)
-tiler_contract_bf16_t256(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m,
-                         uint32_t n, uint32_t k, uint16_t* __restrict__ c) {
-  contract_bf16_t256_body<false>(a, b, m, n, k, c);
-}
-extern "C" __global__ void __launch_bounds__(1024)
-tiler_contract_bf16_silu_t256(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
-                              uint32_t m, uint32_t n, uint32_t k, uint16_t* __restrict__ c) {
-  contract_bf16_t256_body<true>(a, b, m, n, k, c);
-}
+#define TILER_CONTRACT_STAGED(TILE, WAVES)                                                          \
+  extern "C" __global__ void __launch_bounds__(64 * WAVES)                                          \
+      tiler_contract_bf16_t##TILE(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,    \
+                                  uint32_t m, uint32_t n, uint32_t k, uint16_t* __restrict__ c) {   \
+    contract_bf16_staged_body<TILE, false>(a, b, m, n, k, c);                                       \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(64 * WAVES)                                          \
+      tiler_contract_bf16_silu_t##TILE(const uint16_t* __restrict__ a,                              \
+                                       const uint16_t* __restrict__ b, uint32_t m, uint32_t n,      \
+                                       uint32_t k, uint16_t* __restrict__ c) {                      \
+    contract_bf16_staged_body<TILE, true>(a, b, m, n, k, c);                                        \
+  }
+TILER_CONTRACT_STAGED(256, 16)
+TILER_CONTRACT_STAGED(128, 4)
 
 #define TILER_CONTRACT_BF16(NAME, FULLK, SILU)                                                 \
   extern "C" __global__ void __launch_bounds__(256)                                            \
@@ -392,7 +423,7 @@ tiler_contract_bf16_silu_t256(const uint16_t* __restrict__ a, const uint16_t* __
            uint32_t n, uint32_t k, uint16_t* __restrict__ c) {                                  \
     contract_bf16_body<FULLK, SILU>(a, b, m, n, k, c);                                          \
   }
-TILER_CONTRACT_BF16(tiler_contract_bf16_t128, true, false)
-TILER_CONTRACT_BF16(tiler_contract_bf16_silu_t128, true, true)
-TILER_CONTRACT_BF16(tiler_contract_bf16_t128_k, false, false)
-TILER_CONTRACT_BF16(tiler_contract_bf16_silu_t128_k, false, true)
+TILER_CONTRACT_BF16(tiler_contract_bf16_g128, true, false)
+TILER_CONTRACT_BF16(tiler_contract_bf16_silu_g128, true, true)
+TILER_CONTRACT_BF16(tiler_contract_bf16_g128_k, false, false)
+TILER_CONTRACT_BF16(tiler_contract_bf16_silu_g128_k, false, true)

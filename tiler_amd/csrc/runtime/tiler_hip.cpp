@@ -148,10 +148,12 @@ const EntryRow kEntries[] = {
     {"tiler_broadcast_rows_u16", "broadcast", 2},
     {"tiler_fill_u32", "fill", 1},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_bf16_g128", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_g128", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_g128_k", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_g128_k", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_t128", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_t128", "tensor-contraction-bf16/cooperative+silu", 3},
-    {"tiler_contract_bf16_t128_k", "tensor-contraction-bf16/cooperative", 3},
-    {"tiler_contract_bf16_silu_t128_k", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_t256", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_t256", "tensor-contraction-bf16/cooperative+silu", 3},
 };
@@ -1055,18 +1057,28 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t*
   if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull || (m + 127) / 128 > 65535)
     return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
   uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
-  // The 256x256 tile path addresses each 256-row operand panel through one
-  // buffer resource with 32-bit offsets: 256 * k * 2 bytes must stay below 2^31.
-  if (m % 256 == 0 && n % 256 == 0 && k % 64 == 0 && k * 512ull < (1ull << 31) && aligned16(a) &&
-      aligned16(b) && aligned16(c) && (m / 256) * (n / 256) <= 0x7fffffffull) {
-    void* args[] = {&a, &b, &m32, &n32, &k32, &c};
-    return launch(ctx, epilogue == TILER_HIP_EPILOGUE_SILU ? "tiler_contract_bf16_silu_t256" : "tiler_contract_bf16_t256",
-                  (uint32_t)((m / 256) * (n / 256)), 1, 1024, pick(ctx, stream), args);
+  // The staged path addresses each operand panel (up to 256 rows) through one
+  // buffer resource with 32-bit offsets (256 * k * 2 bytes must stay below
+  // 2^31) and moves 16-byte rows: n and k multiples of 8, aligned operands.
+  // 256-tiles when they fill every CU, 128-tiles (four times as many) when not.
+  if (n % 8 == 0 && k % 8 == 0 && k * 512ull < (1ull << 31) && aligned16(a) && aligned16(b) &&
+      aligned16(c)) {
+    const uint64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
+    const uint64_t t128 = ((m + 127) / 128) * ((n + 127) / 128);
+    const bool big = t256 >= ctx->compute_units;
+    const uint64_t tiles = big ? t256 : t128;
+    if (tiles <= 0x7fffffffull) {
+      const bool silu = epilogue == TILER_HIP_EPILOGUE_SILU;
+      const char* name = big ? (silu ? "tiler_contract_bf16_silu_t256" : "tiler_contract_bf16_t256")
+                             : (silu ? "tiler_contract_bf16_silu_t128" : "tiler_contract_bf16_t128");
+      void* args[] = {&a, &b, &m32, &n32, &k32, &c};
+      return launch(ctx, name, (uint32_t)tiles, 1, big ? 1024 : 256, pick(ctx, stream), args);
+    }
   }
   bool full = k % 8 == 0 && aligned16(a) && aligned16(b);
   const char* name = epilogue == TILER_HIP_EPILOGUE_SILU
-                         ? (full ? "tiler_contract_bf16_silu_t128" : "tiler_contract_bf16_silu_t128_k")
-                         : (full ? "tiler_contract_bf16_t128" : "tiler_contract_bf16_t128_k");
+                         ? (full ? "tiler_contract_bf16_silu_g128" : "tiler_contract_bf16_silu_g128_k")
+                         : (full ? "tiler_contract_bf16_g128" : "tiler_contract_bf16_g128_k");
   void* args[] = {&a, &b, &m32, &n32, &k32, &c};
   return launch(ctx, name, (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 256,
                 pick(ctx, stream), args);
