@@ -302,11 +302,12 @@ def test_bf16_contraction_within_frobenius_bound(ctx, m, n, k, silu):
 
 
 @pytest.mark.parametrize("m,n,k", [(4000, 4104, 136), (4096, 4096, 72), (1000, 2048, 520), (64, 4096, 256),
-                                   (3, 8, 8)])
+                                   (3, 8, 8), (16, 4104, 4096), (33, 1000, 520), (1, 4096, 8)])
 def test_bf16_contraction_ragged_edges(ctx, m, n, k):
-    """Rows past m and n load as zeros, k past a multiple of 64 is masked in both
-    operands, and only in-range outputs are stored (the C buffer is poisoned
-    with NaN bf16 first, so a stray store or a missed one shows)."""
+    """Staged (m > 64) and skinny (m <= 64) paths on ragged shapes: rows past m
+    and n load as zeros, k past a multiple of 64 is masked in both operands,
+    and only in-range outputs are stored (the C buffer is poisoned with NaN
+    bf16 first, so a stray store or a missed one shows)."""
     rng = np.random.default_rng(m + n + k)
     ab = oracle.bf16_narrow((rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32))
     bb = oracle.bf16_narrow((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))

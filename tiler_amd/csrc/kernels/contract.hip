@@ -9,6 +9,8 @@
 //   contraction on MFMA (v_mfma_f32_16x16x32_bf16), LDS-staged by buffer
 //   loads: bf16 operands, f32 accumulation, an optional fused SiLU epilogue on
 //   the f32 accumulator, one bf16 narrowing.  Any m; n and k multiples of 8.
+// * tiler_contract_bf16_{,silu_}skinny{1..4} -- m <= 64 (decode shapes): B
+//   streamed once into registers, k split over 16 waves, LDS reduction.
 // * tiler_contract_bf16_{,silu_}g128[_k] -- the guarded general form
 //   (v_mfma_f32_32x32x16_bf16, register-staged) for any n and k: out-of-range
 //   operand elements are zero-filled, out-of-range outputs are not stored.
@@ -416,6 +418,85 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
   }
 TILER_CONTRACT_STAGED(256, 16)
 TILER_CONTRACT_STAGED(128, 4)
+
+// ---------------------------------------------------------------------------
+// Skinny bf16 contraction (m <= 64: decode-shaped), bandwidth-bound on B.
+// One 1024-thread workgroup per 16 columns of n.  The 16 waves split k into
+// 32-deep steps (wave w takes steps w, w + 16, ...); per step each lane loads
+// its 16 bytes of the B columns straight into registers (every B element is
+// used by one MFMA only, so LDS would add nothing) and of each 16-row block of
+// A, and issues one v_mfma_f32_16x16x32_bf16 per block.  The 16 partial
+// 16 x 16 tiles are added in LDS in ascending wave order; SiLU, one bf16
+// narrowing and guarded 2-byte stores follow.  k a multiple of 8, 16-byte
+// aligned A and B; rows past m and columns past n read as zeros.
+namespace {
+
+template <int MB, bool kSilu>
+__device__ __forceinline__ void contract_bf16_skinny_body(const uint16_t* __restrict__ a,
+                                                          const uint16_t* __restrict__ b,
+                                                          uint32_t m, uint32_t n, uint32_t k,
+                                                          uint16_t* __restrict__ c) {
+  __shared__ f32x4 red[16][MB][64];
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t n0 = blockIdx.x * 16u, col = lane & 15u, grp = lane >> 4;
+  const bool bvalid = n0 + col < n;
+  const uint16_t* brow = b + (uint64_t)(bvalid ? n0 + col : 0u) * k;
+  f32x4 acc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t steps = (k + 31u) / 32u;
+  const u32x4 zero = {0, 0, 0, 0};
+#pragma unroll 4
+  for (uint32_t s = wave; s < steps; s += 16u) {
+    const uint32_t kk = s * 32u + grp * 8u;  // this lane's 8 k elements
+    const bool kin = kk < k;
+    const u32x4 bv = (bvalid && kin) ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(brow + kk)) : zero;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint32_t row = mb * 16u + col;
+      const u32x4 av = (row < m && kin) ? *reinterpret_cast<const u32x4*>(a + (uint64_t)row * k + kk) : zero;
+      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(bv), acc[mb], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) red[wave][mb][lane] = acc[mb];
+  __syncthreads();
+  if (wave < (uint32_t)MB) {  // wave w finishes 16-row block w
+    f32x4 t = red[0][wave][lane];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) {
+      const f32x4 u = red[v][wave][lane];
+      t = f32x4{t.x + u.x, t.y + u.y, t.z + u.z, t.w + u.w};
+    }
+    const float tv[4] = {t.x, t.y, t.z, t.w};
+    const uint32_t colg = n0 + col;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = wave * 16u + grp * 4u + i;
+      const float v = kSilu ? silu_fast(tv[i]) : tv[i];
+      if (row < m && colg < n) c[(uint64_t)row * n + colg] = (uint16_t)tiler::bf16_narrow(v);
+    }
+  }
+}
+
+}  // namespace
+
+#define TILER_CONTRACT_SKINNY(MB)                                                                   \
+  extern "C" __global__ void __launch_bounds__(1024)                                                \
+      tiler_contract_bf16_skinny##MB(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, \
+                                     uint32_t m, uint32_t n, uint32_t k, uint16_t* __restrict__ c) { \
+    contract_bf16_skinny_body<MB, false>(a, b, m, n, k, c);                                         \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(1024)                                                \
+      tiler_contract_bf16_silu_skinny##MB(const uint16_t* __restrict__ a,                           \
+                                          const uint16_t* __restrict__ b, uint32_t m, uint32_t n,   \
+                                          uint32_t k, uint16_t* __restrict__ c) {                   \
+    contract_bf16_skinny_body<MB, true>(a, b, m, n, k, c);                                          \
+  }
+TILER_CONTRACT_SKINNY(1)
+TILER_CONTRACT_SKINNY(2)
+TILER_CONTRACT_SKINNY(3)
+TILER_CONTRACT_SKINNY(4)
 
 #define TILER_CONTRACT_BF16(NAME, FULLK, SILU)                                                 \
   extern "C" __global__ void __launch_bounds__(256)                                            \

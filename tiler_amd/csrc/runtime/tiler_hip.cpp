@@ -152,6 +152,14 @@ const EntryRow kEntries[] = {
     {"tiler_contract_bf16_silu_g128", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_g128_k", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_g128_k", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_skinny1", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_skinny1", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_skinny2", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_skinny2", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_skinny3", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_skinny3", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_skinny4", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_skinny4", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_t128", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_t128", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_t256", "tensor-contraction-bf16/cooperative", 3},
@@ -1057,6 +1065,14 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t*
   if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull || (m + 127) / 128 > 65535)
     return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
   uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
+  // m <= 64 (decode shapes): B streamed once, one workgroup per 16 columns.
+  if (m <= 64 && k % 8 == 0 && aligned16(a) && aligned16(b) && (n + 15) / 16 <= 0x7fffffffull) {
+    char name[48];
+    std::snprintf(name, sizeof(name), "tiler_contract_bf16_%sskinny%u",
+                  epilogue == TILER_HIP_EPILOGUE_SILU ? "silu_" : "", (uint32_t)((m + 15) / 16));
+    void* args[] = {&a, &b, &m32, &n32, &k32, &c};
+    return launch(ctx, name, (uint32_t)((n + 15) / 16), 1, 1024, pick(ctx, stream), args);
+  }
   // The staged path addresses each operand panel (up to 256 rows) through one
   // buffer resource with 32-bit offsets (256 * k * 2 bytes must stay below
   // 2^31) and moves 16-byte rows: n and k multiples of 8, aligned operands.
