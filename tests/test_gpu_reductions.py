@@ -63,6 +63,10 @@ def test_multipass_sum_matches_strict_partitioned_sum(ctx):
     x = (rng.standard_normal((9, 4096)) * 10).astype(np.float32)
     got = _sum_dev(ctx, x, 9, 4096, topology=L.SUM_MULTIPASS, partitions=64, per_partition=64)
     assert np.array_equal(bits(got), bits(oracle.strict_partitioned_sum(x, 9, 4096, 64, 64)))
+    # 70 x 64 partials exceed the context workspace: the stream-ordered allocation path
+    y = (rng.standard_normal((70, 1024)) * 10).astype(np.float32)
+    got = _sum_dev(ctx, y, 70, 1024, topology=L.SUM_MULTIPASS, partitions=64, per_partition=16)
+    assert np.array_equal(bits(got), bits(oracle.strict_partitioned_sum(y, 70, 1024, 64, 16)))
 
 
 @pytest.mark.parametrize("major", [False, True])

@@ -776,9 +776,16 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
       uint64_t P = plan->partitions, c = plan->per_partition;
       if (P == 0 || (c != 0 && P > UINT64_MAX / c) || P * c != extent)
         return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "partitions do not cover the axis exactly");
+      // Partials live in the context workspace when they fit (ordered on the
+      // stream like the tree sum's); only larger splits allocate, stream-ordered.
       void* partials = nullptr;
-      if (hipMallocAsync(&partials, rows * P * 4, s) != hipSuccess)
-        return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "partials allocation failed");
+      const bool own = rows * P > kMaxSumWorkgroups;
+      if (own) {
+        if (hipMallocAsync(&partials, rows * P * 4, s) != hipSuccess)
+          return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "partials allocation failed");
+      } else {
+        partials = ctx->sum_partials;
+      }
       float* pp = static_cast<float*>(partials);
       void* a1[] = {&x, &rows, &extent, &P, &c, &pp};
       tiler_hip_status st = launch(ctx, "tiler_sum_f32_partials", (uint32_t)((rows * P + 255) / 256), 1, 256, s, a1);
@@ -788,7 +795,7 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
         void* a2[] = {&cp, &outer, &P, &inner, &out};
         st = launch(ctx, "tiler_sum_f32_serial", (uint32_t)((rows + 255) / 256), 1, 256, s, a2);
       }
-      hipFreeAsync(partials, s);
+      if (own) hipFreeAsync(partials, s);
       return st;
     }
     case TILER_HIP_SUM_COOPERATIVE: {
