@@ -2,7 +2,7 @@
 
 Gather and broadcast are byte moves and must be bit-exact; the strict f32
 contraction must reproduce the reference's own device digests; the bf16 MFMA
-contraction is held to the north-star 1e-2 relative Frobenius error against
+contraction is held to the stated 1e-2 relative Frobenius error against
 the strict f32 fold of the same (exactly widened) operands.
 """
 from __future__ import annotations

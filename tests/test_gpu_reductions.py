@@ -2,8 +2,8 @@
 softmax, against the oracle on the same seeded inputs.
 
 Bit-exact where the kernel's order is a reference order (serial, multipass,
-cooperative) or its declared grouping (tree, row families); at the BASELINE
-full sizes additionally within the north-star tolerance of an f64
+cooperative) or its declared grouping (tree, row families); at the full
+configuration sizes additionally within the stated tolerance of an f64
 accumulation: 1e-5 relative (sum, softmax), 2 bf16 ulp (bf16 RMSNorm).
 """
 from __future__ import annotations
@@ -111,7 +111,8 @@ def test_tree_sum_rows_declared_grouping(ctx):
 
 def test_tree_sum_full_size_config(ctx):
     """C1: f32[2^24] ~ U[-1, 1] -> scalar, within 1e-5 of the f64 sum, and
-    repeated launches (ticket re-arming) stay bit-identical."""
+    repeated launches (sharing the context's partials workspace) stay
+    bit-identical."""
     n = 1 << 24
     x = np.random.default_rng(0).uniform(-1, 1, n).astype(np.float32)
     dx = ctx.to_device(x)
