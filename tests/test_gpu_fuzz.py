@@ -1,0 +1,126 @@
+"""GPU: seeded random shapes for every family against the oracle.
+
+Each case draws its shape (and, where the family has them, the axis, offsets
+and groupings) from a fixed seed, so a failure names a reproducible case.
+Sizes stay small enough for the oracle to finish in well under a second each.
+Comparison is bit-exact wherever the oracle restates the kernel's order (or
+its declared grouping), and to the contraction's 1e-2 relative Frobenius bound
+for the bf16 MFMA path.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import tiler_amd
+from helpers import bf16_widen, bits
+from tiler_amd import _lib as L
+from tiler_amd import families
+
+pytestmark = pytest.mark.gpu
+
+EPS = 0x3727C5AC
+CASES = 12
+
+
+def _rng(case, salt):
+    return np.random.default_rng(1000 * salt + case)
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_sums(ctx, case):
+    r = _rng(case, 1)
+    rank = int(r.integers(1, 4))
+    shape = tuple(int(v) for v in r.integers(1, 40, rank))
+    axis = int(r.integers(0, rank))
+    x = (r.standard_normal(shape) * 10).astype(np.float32)
+    assert np.array_equal(bits(families.strict_sum(x, shape, axis, ctx=ctx)).reshape(-1),
+                          bits(oracle.strict_sum(x, shape, axis)).reshape(-1)), (shape, axis)
+    extent = shape[axis]
+    parts = [p for p in range(1, extent + 1) if extent % p == 0]
+    p = parts[int(r.integers(0, len(parts)))]
+    got = families.strict_partitioned_sum(x, shape, axis, p, extent // p, ctx=ctx)
+    moved = np.moveaxis(x, axis, -1)
+    want = oracle.strict_partitioned_sum(moved, moved.size // extent, extent, p, extent // p)
+    assert np.array_equal(bits(got).reshape(-1), bits(want).reshape(-1))
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_tree_sum(ctx, case):
+    r = _rng(case, 2)
+    n = int(r.integers(1, 200000))
+    x = r.uniform(-1, 1, n).astype(np.float32)
+    got = families.tree_sum(x, (n,), 0, ctx=ctx)
+    assert bits(got)[0] == bits([oracle.grid_tree_sum(x, ctx.sum_tree_workgroups(n))])[0]
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_rms_norm_bf16(ctx, case):
+    r = _rng(case, 3)
+    rows = int(r.integers(1, 9))
+    extent = int(r.choice([int(r.integers(1, 9000)), int(r.integers(8193, 70000))]))
+    xb = oracle.bf16_narrow(r.standard_normal((rows, extent)).astype(np.float32))
+    wb = oracle.bf16_narrow(r.normal(1.0, 0.1, extent).astype(np.float32))
+    got = families.rms_norm_bf16(xb, wb, EPS, ctx=ctx)
+    vec, waves = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, extent)
+    y = oracle.rms_norm_grouped(bf16_widen(xb), bf16_widen(wb), rows, extent, EPS, True, vec, waves)
+    assert np.array_equal(got, oracle.bf16_narrow(y).reshape(rows, extent)), (rows, extent)
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_softmax(ctx, case):
+    r = _rng(case, 4)
+    rows = int(r.integers(1, 9))
+    extent = int(r.choice([int(r.integers(1, 9000)), int(r.integers(8193, 50000))]))
+    x = (r.standard_normal((rows, extent)) * 4).astype(np.float32)
+    if extent > 3:
+        x[0, r.integers(0, extent, extent // 3)] = -np.inf
+    got = families.softmax_f32((rows, extent), 1, x, ctx=ctx).reshape(rows, extent)
+    vec, waves = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
+    want = oracle.softmax_grouped(x, rows, extent, vec, waves).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want)), (rows, extent)
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_gather(ctx, case):
+    r = _rng(case, 5)
+    rank = int(r.integers(1, 4))
+    shape = tuple(int(v) for v in r.integers(1, 30, rank))
+    axis = int(r.integers(0, rank))
+    dtype = [np.uint8, np.uint16, np.uint32, np.uint64][int(r.integers(0, 4))]
+    src = r.integers(0, np.iinfo(dtype).max, shape, dtype=dtype)
+    idx = r.integers(0, shape[axis], tuple(int(v) for v in r.integers(0, 6, int(r.integers(0, 3)))))
+    got = families.gather(src, axis, idx.astype(np.uint32), ctx=ctx)
+    assert np.array_equal(got, np.take(src, idx, axis=axis))
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_contractions(ctx, case):
+    r = _rng(case, 6)
+    m, n, k = (int(v) for v in r.integers(1, 300, 3))
+    if case % 3 == 0:  # shapes on the staged path's 8-element grid
+        n, k = 8 * max(1, n // 8), 8 * max(1, k // 8)
+    a = r.standard_normal((m, k)).astype(np.float32) / np.float32(np.sqrt(k))
+    b = r.standard_normal((n, k)).astype(np.float32) / np.float32(np.sqrt(k))
+    ref = oracle.contract_strict_f32(a, b, m, n, k)
+    got = families.contract_strict_f32(a, b, ctx=ctx)
+    assert np.array_equal(bits(got).reshape(-1), bits(ref).reshape(-1))
+    ab, bb = oracle.bf16_narrow(a), oracle.bf16_narrow(b)
+    silu = bool(case % 2)
+    gb = families.contract_bf16(ab, bb, L.EPILOGUE_SILU if silu else L.EPILOGUE_NONE, ctx=ctx)
+    rb = oracle.contract_strict_f32(bf16_widen(ab), bf16_widen(bb), m, n, k).reshape(m, n)
+    if silu:
+        rb = oracle.silu_f32(rb).reshape(m, n)
+    g = bf16_widen(gb).astype(np.float64)
+    den = np.linalg.norm(rb.astype(np.float64))
+    if den > 0:
+        assert np.linalg.norm(g - rb) / den <= 1e-2, (m, n, k, silu)
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_maps(ctx, case):
+    r = _rng(case, 7)
+    n = int(r.integers(1, 20000))
+    x = (r.standard_normal(n) * 6).astype(np.float32)
+    assert np.array_equal(bits(families.silu_f32(x, ctx=ctx)), bits(oracle.silu_f32(x)))
