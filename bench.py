@@ -18,6 +18,7 @@ single-threaded, on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                        [--no-families] [--no-cpu-baseline] [--calibration-copy]
+                       [--vendor-gemm]
 """
 from __future__ import annotations
 
@@ -41,6 +42,14 @@ METRIC = "achieved HBM GB/s (% peak) for RMSNorm/softmax/gather; bf16 GEMM TFLOP
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """binary32 -> bf16 bit patterns, round to nearest even (NaN -> 0x7fc0):
+    synthetic-input generation only (the oracle stays the checker)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    r = ((u + (np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1)))) >> 16).astype(np.uint16)
+    return np.where(np.isnan(x), np.uint16(0x7FC0), r)
 
 
 class Workload:
@@ -79,15 +88,14 @@ class RmsNorm(Workload):
         return self.rows * self.extent * 2 * 2 + self.extent * 2
 
     def setup(self):
-        import oracle
         from tiler_amd import _lib as L
         self.L = L
         rng = np.random.default_rng(1)
-        w = oracle.bf16_narrow(rng.normal(1.0, 0.1, self.extent).astype(np.float32))
+        w = to_bf16(rng.normal(1.0, 0.1, self.extent).astype(np.float32))
         self.w = self._keep(self.ctx.to_device(w))
         self.sets_ = []
         for s in range(self.sets):
-            x = oracle.bf16_narrow(rng.standard_normal((self.rows, self.extent), dtype=np.float32))
+            x = to_bf16(rng.standard_normal((self.rows, self.extent), dtype=np.float32))
             self.sets_.append(self._keep(self.ctx.to_device(x), self.ctx.alloc(x.nbytes)))
         return len(self.sets_)
 
@@ -212,12 +220,11 @@ class Gather(Workload):
         return self.count * self.hidden * 2 * 2 + self.count * 4
 
     def setup(self):
-        import oracle
         rng = np.random.default_rng(4)
         table = np.empty((self.vocab, self.hidden), np.uint16)
         for lo in range(0, self.vocab, 16384):
             hi = min(self.vocab, lo + 16384)
-            table[lo:hi] = oracle.bf16_narrow(
+            table[lo:hi] = to_bf16(
                 rng.standard_normal((hi - lo, self.hidden), dtype=np.float32) * np.float32(0.02))
         self.table = self._keep(self.ctx.to_device(table))
         del table
@@ -263,18 +270,58 @@ class Contract(Workload):
     def work(self):  # flops per launch
         return 2 * self.m * self.n * self.k
 
+    def operands(self):
+        """The seeded bf16 operand sets (A [m,k], B [n,k]) every leg uses."""
+        rng = np.random.default_rng(5)
+        for _ in range(self.sets):
+            a = to_bf16(rng.standard_normal((self.m, self.k), dtype=np.float32) / np.float32(64.0))
+            b = to_bf16(rng.standard_normal((self.n, self.k), dtype=np.float32) / np.float32(64.0))
+            yield a, b
+
     def setup(self):
-        import oracle
         from tiler_amd import _lib as L
         self.L = L
-        rng = np.random.default_rng(5)
         self.sets_ = []
-        for _ in range(self.sets):
-            a = oracle.bf16_narrow(rng.standard_normal((self.m, self.k), dtype=np.float32) / np.float32(64.0))
-            b = oracle.bf16_narrow(rng.standard_normal((self.n, self.k), dtype=np.float32) / np.float32(64.0))
+        for a, b in self.operands():
             self.sets_.append(self._keep(self.ctx.to_device(a), self.ctx.to_device(b),
                                          self.ctx.alloc(self.m * self.n * 2)))
         return self.sets
+
+    def vendor_reference(self, steps, warmup):
+        """The vendor library's bf16 GEMM on the same operands, for comparison
+        only: torch.matmul(A, B^T) (hipBLASLt), no epilogue, bf16 out, its
+        K launches captured in a torch CUDA graph, settled, and one replay
+        timed between events on torch's stream."""
+        import torch
+        dev = torch.device("cuda", 0)
+        sets = [(torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16),
+                 torch.from_numpy(b.view(np.int16)).to(dev).view(torch.bfloat16))
+                for a, b in self.operands()]
+        outs = [torch.empty((self.m, self.n), device=dev, dtype=torch.bfloat16) for _ in sets]
+
+        def run(i):
+            a, b = sets[i % len(sets)]
+            torch.matmul(a, b.t(), out=outs[i % len(sets)])
+        for i in range(warmup):
+            run(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                run(i)
+        t_settle = time.perf_counter()
+        while time.perf_counter() - t_settle < SETTLE_S:
+            g.replay()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        return {"library": f"hipBLASLt via torch.matmul(A, B^T) (torch {torch.__version__})",
+                "epilogue": "none", "value": self.work() / (ms / 1e3) / 1e12, "unit": "TFLOP/s",
+                "ms_per_step": ms, "steps": steps}
 
     def launch(self, i):
         a, b, c = self.sets_[i % self.sets]
@@ -408,6 +455,9 @@ def main():
     ap.add_argument("--no-families", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="also time the vendor bf16 GEMM (torch.matmul) on the contraction operands")
+    ap.add_argument("--vendor-gemm-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--calibration-copy", action="store_true",
                     help="first run a 256 MiB device copy (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -415,6 +465,25 @@ def main():
         print("tiler-hip bench runs on one GPU: this build has no multi-GPU path "
               "(the reference has no multi-device notion); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.vendor_gemm_child:  # torch's own HIP runtime, in a process without tiler-hip's
+        print(json.dumps(Contract(None).vendor_reference(max(20, args.steps // 2), args.warmup)))
+        return
+    vendor = None
+    if args.vendor_gemm:
+        # Before this process touches the GPU: the vendor leg runs as a child
+        # process, because torch's HIP runtime and the one tiler-hip links
+        # cannot share a process.
+        import subprocess
+        log("vendor bf16 GEMM on the contraction operands (child process)")
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-gemm-child",
+                            "--steps", str(args.steps), "--warmup", str(args.warmup)],
+                           stdout=subprocess.PIPE, text=True, timeout=600)
+        if r.returncode != 0:
+            log(f"vendor leg failed with status {r.returncode}")
+            sys.exit(r.returncode)
+        vendor = json.loads(r.stdout.strip().splitlines()[-1])
+        log(f"vendor: {vendor['value']:.1f} TFLOP/s ({vendor['ms_per_step'] * 1e3:.1f} us)")
 
     import tiler_amd
     ctx = tiler_amd.Context(0)
@@ -458,6 +527,7 @@ def main():
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "families": families,
+        **({"vendor_gemm": vendor} if vendor else {}),
         "device": {k: ctx.environment[k] for k in ("device_name", "gcn_arch_name", "compute_units")},
     }
     ctx.close()

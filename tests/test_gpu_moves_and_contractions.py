@@ -327,6 +327,40 @@ def test_bf16_contraction_ragged_edges(ctx, m, n, k):
     assert not np.isnan(bf16_widen(got)).any()
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 64, 64), (300, 264, 136), (70, 30, 20)])
+@pytest.mark.parametrize("silu", [False, True])
+def test_bf16_contraction_exceptional_values(ctx, m, n, k, silu):
+    """Non-finite operands on every dispatch path (skinny m <= 64, staged, and
+    the general form for n, k off the 8-element grid).  A NaN with a negative
+    sign and a payload, +inf meeting a zero (inf * 0), and -inf are planted in
+    A and B.  Every NaN output must be the canonical bf16 0x7fc0 (ADR 0091
+    narrowing), infinities keep their sign, and the finite outputs stay
+    within the Frobenius bound."""
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = (rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
+    b = np.abs(rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32) + np.float32(0.01)
+    ab, bb = oracle.bf16_narrow(a), oracle.bf16_narrow(b)
+    ab[0, 5] = 0xFFC1   # negative NaN with a payload: row 0 is NaN
+    ab[1, 5] = 0x7F80   # +inf against positive B: +inf, except column 0 ...
+    bb[0, 5] = 0x0000   # ... where it meets +0: inf * 0 = NaN
+    ab[2, 7] = 0xFF80   # -inf: -inf (SiLU: NaN)
+    bb[3, 9] = 0x7FA3   # a NaN payload in B: column 3 is NaN
+    got = families.contract_bf16(ab, bb, L.EPILOGUE_SILU if silu else L.EPILOGUE_NONE, ctx=ctx)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = oracle.contract_strict_f32(bf16_widen(ab), bf16_widen(bb), m, n, k).reshape(m, n)
+        if silu:
+            ref = oracle.silu_f32(ref).reshape(m, n)
+    want = oracle.bf16_narrow(ref).reshape(m, n)
+    special = ~np.isfinite(ref)
+    assert special[0].all() and special[:, 3].all() and np.isnan(ref[1, 0])
+    assert np.array_equal(got[special], want[special])
+    assert (got[np.isnan(ref)] == 0x7FC0).all()
+    fin = np.isfinite(ref)
+    g = bf16_widen(got)[fin].astype(np.float64)
+    r = ref[fin].astype(np.float64)
+    assert np.linalg.norm(g - r) / np.linalg.norm(r) <= 1e-2
+
+
 def test_bf16_contraction_full_size_config(ctx):
     """C5: bf16 A, B [4096 x 4096] ~ N(0, 1/sqrt(4096)), f32 accumulation,
     fused SiLU, bf16 C: relative Frobenius error <= 1e-2 against the strict

@@ -211,6 +211,25 @@ __device__ __forceinline__ float silu_fast(float v) {
   return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// Epilogue store word for a pair of adjacent output rows.  Lanes 2c and 2c+1
+// of a 16x16 MFMA block hold the same two rows (v0: row r, v1: row r+1) of
+// columns 2c and 2c+1.  Each lane narrows its (v0, v1) with
+// v_cvt_pk_bf16_f32, which rounds to nearest even exactly like the ADR 0091
+// narrowing for every non-NaN input (NaNs are made canonical first, since
+// the instruction keeps a NaN's sign and payload); a DPP quad_perm [1,0,3,2]
+// swaps the packed words between the two lanes, and v_perm_b32 forms the
+// 32-bit column pair: row r of columns 2c, 2c+1 on the even lane, row r+1 on
+// the odd one.  sel is 0x05040100 on even lanes, 0x03020706 on odd lanes.
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_row_pair(float v0, float v1, uint32_t sel) {
+  const float qnan = __uint_as_float(0x7fc00000u);
+  const f32x2v f = {v0 != v0 ? qnan : v0, v1 != v1 ? qnan : v1};
+  const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2v));
+  const uint32_t q = (uint32_t)__builtin_amdgcn_mov_dpp((int)p, 0xB1, 0xF, 0xF, true);
+  return __builtin_amdgcn_perm(q, p, sel);
+}
+
 // s_waitcnt immediates (gfx9 layout: vmcnt [3:0] and [15:14], expcnt [6:4],
 // lgkmcnt [11:8]); a field at its maximum does not wait.
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
@@ -370,6 +389,7 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
   // rows r and r+1; one exchange lets each write a 32-bit column pair.
   uint16_t* cst = smem + wave * (64u * 64u);
   const bool odd = lane & 1u;
+  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -381,12 +401,10 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
           v0 = silu_fast(v0);
           v1 = silu_fast(v1);
         }
-        const float recv = __shfl_xor(odd ? v0 : v1, 1, 64);
-        const float lo = odd ? recv : v0, hi = odd ? v1 : recv;
         const uint32_t row = i * 16u + grp * 4u + r + (odd ? 1u : 0u);
         const uint32_t col = j * 16u + ((lane & 15u) & ~1u);
         const uint32_t q = (col >> 3) ^ (row & 7u);
-        *reinterpret_cast<uint32_t*>(cst + row * 64u + q * 8u + (col & 7u)) = tiler::bf16_pack2(lo, hi);
+        *reinterpret_cast<uint32_t*>(cst + row * 64u + q * 8u + (col & 7u)) = pack_row_pair(v0, v1, sel);
       }
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   __builtin_amdgcn_wave_barrier();
