@@ -372,6 +372,98 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context *ctx, const uint16_t 
                                          uint16_t *c, uint32_t epilogue,
                                          tiler_hip_stream stream);
 
+/* ------------------------------------------------------------------------
+ * Realization recognizer: one scheduled region -> the dispatches that realize
+ * it on this library's entry points.  It takes the role of tiler-metal's
+ * emit_entry_point (tiler-metal/src/emit.rs:647-840) for a backend whose code
+ * is built ahead of time. Inputs:
+ *   - the region's ScalarProgram (tiler-ir/src/schedule/model.rs:661-930);
+ *   - its ReductionTopology (model.rs:1327-1555);
+ *   - its geometry, which the planner's KernelSchedule/LaunchPlan summarizes
+ *     (model.rs:1785-1812).
+ * The result is exactly the program the family entry point above runs for
+ * the same request. It is what the runtime seam executes:
+ *   1. tiler_hip_prepare_entries on the payload symbols the entries name;
+ *   2. tiler_hip_plan_dispatch;
+ *   3. tiler_hip_allocate_dispatch;
+ *   4. tiler_hip_dispatch.
+ * Device-free: with ctx NULL the declared profile's 256 CUs decide the tile
+ * size and the tree grouping; with a context, its device's CUs do.
+ */
+#define TILER_HIP_PROGRAM_POINTWISE 1   /* ScalarProgram::PointwiseF32 / PointwiseBf16 (model.rs:663, 681) */
+#define TILER_HIP_PROGRAM_SERIAL_SUM 2  /* ::StrictSerialSum (model.rs:698) */
+#define TILER_HIP_PROGRAM_RMS_NORM 3    /* ::SquaredSerialSumThenEpilogue (model.rs:815) */
+#define TILER_HIP_PROGRAM_SOFTMAX 4     /* law StagedSoftmaxF32 (tiler-ir/src/index/law.rs:289) over
+                                           ::StrictSerialMaximum (model.rs:920) */
+#define TILER_HIP_PROGRAM_CONTRACTION 5 /* ::StrictTensorContraction (model.rs:850) */
+#define TILER_HIP_PROGRAM_GATHER 6      /* tiler-reference/src/structural.rs:513-606 */
+#define TILER_HIP_PROGRAM_BROADCAST 7   /* tiler-reference/src/structural.rs:75-108 */
+
+/* Region flags. */
+#define TILER_HIP_REGION_ALIGNED16 1u         /* precondition: every slot's base address is 16-byte aligned */
+#define TILER_HIP_REGION_OPERAND_BROADCAST 2u /* pointwise: x2 is one element; rms_norm: w is one row */
+#define TILER_HIP_REGION_INDEX_SIGNED 4u      /* gather: int32 indices */
+#define TILER_HIP_REGION_PARTICIPANT_MAJOR 8u /* cooperative sum layout */
+
+typedef struct {
+    uint32_t program;      /* TILER_HIP_PROGRAM_* */
+    uint32_t topology;     /* serial sum: TILER_HIP_SUM_* */
+    uint32_t dtype;        /* TILER_HIP_F32 / TILER_HIP_BF16 */
+    uint32_t variant;      /* pointwise: TILER_HIP_MAP_*; contraction (bf16): TILER_HIP_EPILOGUE_*;
+                              gather, broadcast: element bytes */
+    uint32_t flags;        /* TILER_HIP_REGION_* */
+    uint32_t rank;         /* broadcast: output rank (<= 8) */
+    uint64_t extents[8];   /* pointwise {n}; sum, rms_norm, softmax {rows, extent};
+                              contraction {m, n, k}; gather {outer, gathered, inner, index count};
+                              broadcast: the output dims */
+    uint64_t strides[8];   /* broadcast: source stride (elements) per output axis */
+    uint64_t grouping[3];  /* multi-pass sum {partitions, per partition};
+                              cooperative sum {participants, per partition, rounds};
+                              broadcast {source elements} */
+    uint32_t scalars[2];   /* rms_norm {eps bits}; pointwise {a bits, b bits} */
+} tiler_hip_region;
+
+/* Storage slot roles.  Slot order per program:
+ *   pointwise   x, [x2,] y       (x2 only for ADD and MULTIPLY)
+ *   serial sum  x, out, [partials: scratch]
+ *   rms_norm    x, w, y
+ *   softmax     x, y
+ *   contraction a [m, k], b [n, k], c [m, n]
+ *   gather      source, index, out, record (scratch: u64, all ones unless an index was
+ *               out of range; then the lowest such position).  The program arms the
+ *               record itself; validate host indices first (tiler_hip_validate_gather_index).
+ *   broadcast   src, out */
+#define TILER_HIP_SLOT_INPUT 0
+#define TILER_HIP_SLOT_OUTPUT 1
+#define TILER_HIP_SLOT_SCRATCH 2
+
+typedef struct {
+    uint32_t entry;             /* payload entry index (tiler_hip_payload_entry names it) */
+    uint32_t grid[3];           /* workgroups */
+    uint32_t block[3];          /* threads per workgroup */
+    uint32_t kernarg_bytes;
+    uint8_t kernargs[256];      /* argument segment; pointer fields are bound at dispatch */
+    uint32_t binding_count;
+    uint32_t binding_slots[6];
+    uint32_t binding_offsets[6];
+} tiler_hip_realized_entry;
+
+typedef struct {
+    uint32_t slot_count;
+    uint32_t slot_roles[6];     /* TILER_HIP_SLOT_* */
+    uint64_t slot_bytes[6];
+    uint32_t slot_alignment;    /* precondition on every slot base: 16 with ALIGNED16, else 1 */
+    uint32_t entry_count;       /* 0: zero work, nothing to dispatch */
+    tiler_hip_realized_entry entries[4]; /* in execution order */
+} tiler_hip_realization;
+
+/* Refuses (pre-commit, typed) what the family entry point would refuse for
+ * the same request, plus TILER_HIP_REFUSE_UNSUPPORTED for a program or
+ * dtype this library does not realize. */
+tiler_hip_status tiler_hip_realize(const tiler_hip_context *ctx, const tiler_hip_region *region,
+                                   tiler_hip_realization *out, char *diagnostic,
+                                   uint64_t diagnostic_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,197 @@
+"""GPU: realized regions routed through the RuntimeAdapter seam.
+
+For each family the region is realized (`tiler_hip_realize`, with the bound
+device deciding tile sizes and groupings), routed the way route_with_adapter
+drives an adapter:
+1. prepare the payload entries;
+2. plan, acquiring nothing;
+3. allocate scratch after the commit;
+4. dispatch.
+
+The result is compared bit for bit with the family entry point's on the same
+inputs, and with the oracle where the family is bit-exact. Routing refusals
+(storage too small, misaligned against the realization's assumption, missing)
+arrive before anything is committed.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import bf16_widen, bits
+from tiler_amd import _lib as L
+from tiler_amd.realize import realize, route
+from tiler_amd.runtime import GatherIndexOutOfBounds, Refusal
+
+pytestmark = pytest.mark.gpu
+
+EPS = 0x3727C5AC
+
+
+def _routed(ctx, rz, inputs, outputs):
+    """Routes `rz` with device copies of `inputs` and fresh `outputs`
+    ((dtype, shape) per output slot); returns the outputs on the host."""
+    dev_in = [ctx.to_device(a) for a in inputs]
+    dev_out = [ctx.alloc(max(1, int(np.prod(shape)) * np.dtype(dt).itemsize)) for dt, shape in outputs]
+    storage, i_in, i_out = [], 0, 0
+    for role, _ in rz.slots:
+        if role == L.SLOT_INPUT:
+            storage.append(dev_in[i_in]); i_in += 1
+        elif role == L.SLOT_OUTPUT:
+            storage.append(dev_out[i_out]); i_out += 1
+        else:
+            storage.append(None)
+    try:
+        route(ctx, rz, storage)
+        return [b.download(dt, shape) for b, (dt, shape) in zip(dev_out, outputs)]
+    finally:
+        for b in dev_in + dev_out:
+            b.free()
+
+
+def test_serial_sum_routed(ctx):
+    rows, extent = 1000, 37
+    x = np.random.default_rng(71).standard_normal((rows, extent)).astype(np.float32)
+    rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_SERIAL, ctx=ctx)
+    assert rz.symbols == ["tiler_sum_f32_serial"]
+    (got,) = _routed(ctx, rz, [x], [(np.float32, (rows,))])
+    assert np.array_equal(bits(got), bits(oracle.strict_sum(x, (rows, extent), 1)))
+
+
+@pytest.mark.parametrize("topology,rows,extent,grouping,flags", [
+    (L.SUM_MULTIPASS, 7, 120, (4, 30), L.REGION_ALIGNED16),
+    (L.SUM_MULTIPASS, 40, 4000, (200, 20), L.REGION_ALIGNED16),   # partials beyond the context workspace
+    (L.SUM_COOPERATIVE, 5, 24, (4, 3, 2), L.REGION_ALIGNED16 | L.REGION_PARTICIPANT_MAJOR),
+    (L.SUM_TREE, 1, (1 << 20) + 3, (), L.REGION_ALIGNED16),
+    (L.SUM_TREE, 33, 5000, (), L.REGION_ALIGNED16),
+])
+def test_grouped_sums_routed(ctx, topology, rows, extent, grouping, flags):
+    x = np.random.default_rng(rows + extent).uniform(-1, 1, (rows, extent)).astype(np.float32)
+    rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=topology, grouping=grouping, flags=flags, ctx=ctx)
+    (got,) = _routed(ctx, rz, [x], [(np.float32, (rows,))])
+    from tiler_amd import families
+    if topology == L.SUM_MULTIPASS:
+        want = families.strict_partitioned_sum(x, (rows, extent), 1, grouping[0], grouping[1], ctx=ctx)
+    elif topology == L.SUM_COOPERATIVE:
+        want = families.cooperative_grouped_sum(x, (rows, extent), 1, grouping[0], grouping[1], grouping[2],
+                                                participant_major=True, ctx=ctx)
+    else:
+        want = families.tree_sum(x, (rows, extent), 1, ctx=ctx)
+    assert np.array_equal(bits(got).reshape(-1), bits(want).reshape(-1))
+
+
+@pytest.mark.parametrize("dtype,rows,extent", [(L.BF16, 64, 4096), (L.F32, 9, 1000), (L.BF16, 3, 20000)])
+def test_rms_norm_routed(ctx, dtype, rows, extent):
+    rng = np.random.default_rng(rows * extent)
+    if dtype == L.BF16:
+        x = oracle.bf16_narrow(rng.standard_normal((rows, extent)).astype(np.float32))
+        w = oracle.bf16_narrow(rng.normal(1.0, 0.1, extent).astype(np.float32))
+        out_t = np.uint16
+    else:
+        x = rng.standard_normal((rows, extent)).astype(np.float32)
+        w = rng.normal(1.0, 0.1, extent).astype(np.float32)
+        out_t = np.float32
+    rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=dtype, scalars=(EPS,),
+                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=ctx)
+    (got,) = _routed(ctx, rz, [x, w], [(out_t, (rows, extent))])
+    dx, dw, dy = ctx.to_device(x), ctx.to_device(w), ctx.alloc(x.nbytes)
+    try:
+        ctx.rms_norm(dtype, dx, dw, rows, extent, EPS, dy, weight_broadcast=True)
+        want = dy.download(out_t, (rows, extent))
+    finally:
+        dx.free(); dw.free(); dy.free()
+    assert np.array_equal(got.view(np.uint16 if dtype == L.BF16 else np.uint32),
+                          want.view(np.uint16 if dtype == L.BF16 else np.uint32))
+
+
+@pytest.mark.parametrize("rows,extent", [(64, 2048), (5, 300), (2, 40000)])
+def test_softmax_routed(ctx, rows, extent):
+    x = (np.random.default_rng(extent).standard_normal((rows, extent)) * 3).astype(np.float32)
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), ctx=ctx)
+    (got,) = _routed(ctx, rz, [x], [(np.float32, (rows, extent))])
+    import tiler_amd
+    vec, waves = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
+    assert np.array_equal(bits(got).reshape(-1), bits(oracle.softmax_grouped(x, rows, extent, vec, waves)))
+
+
+@pytest.mark.parametrize("op,n", [(L.MAP_ADD, 4096), (L.MAP_MULTIPLY, 1001), (L.MAP_SILU, 8192), (L.MAP_SILU, 77)])
+def test_maps_routed(ctx, op, n):
+    rng = np.random.default_rng(n + op)
+    x = (rng.standard_normal(n) * 5).astype(np.float32)
+    x2 = rng.standard_normal(n).astype(np.float32)
+    rz = realize(L.PROGRAM_POINTWISE, (n,), variant=op, ctx=ctx)
+    binary = op in (L.MAP_ADD, L.MAP_MULTIPLY)
+    (got,) = _routed(ctx, rz, [x, x2] if binary else [x], [(np.float32, (n,))])
+    if op == L.MAP_ADD:
+        want = x + x2            # one binary32 rounding; no NaN among these operands
+    elif op == L.MAP_MULTIPLY:
+        want = x * x2
+    else:
+        want = oracle.silu_f32(x)
+    assert np.array_equal(bits(got), bits(np.asarray(want, np.float32).reshape(-1)))
+
+
+def test_broadcast_and_gather_routed(ctx):
+    rng = np.random.default_rng(72)
+    w = rng.integers(0, 1 << 16, 4096, dtype=np.uint16)
+    rz = realize(L.PROGRAM_BROADCAST, (8, 4096), variant=2, rank=2, strides=(0, 1), grouping=(4096,), ctx=ctx)
+    (got,) = _routed(ctx, rz, [w], [(np.uint16, (8, 4096))])
+    assert np.array_equal(got, np.broadcast_to(w, (8, 4096)))
+
+    table = rng.integers(0, 1 << 16, (500, 256), dtype=np.uint16)
+    idx = rng.integers(0, 500, 300).astype(np.uint32)
+    rz = realize(L.PROGRAM_GATHER, (1, 500, 256, 300), variant=2, ctx=ctx)
+    assert rz.symbols == ["tiler_fill_u32", "tiler_gather_u128"]
+    (got,) = _routed(ctx, rz, [table, idx], [(np.uint16, (300, 256))])
+    assert np.array_equal(got, table[idx])
+
+
+def test_gather_record_reports_post_commit(ctx):
+    """An index the host did not validate is caught by the kernel's own bound
+    check (its run is skipped, nothing is read out of range) and surfaces as
+    the post-commit failure naming the lowest position."""
+    table = np.arange(40 * 8, dtype=np.uint32).reshape(40, 8)
+    idx = np.array([3, 39, 40, 7, 1000], np.uint32)
+    rz = realize(L.PROGRAM_GATHER, (1, 40, 8, 5), variant=4, ctx=ctx)
+    with pytest.raises(GatherIndexOutOfBounds) as e:
+        _routed(ctx, rz, [table, idx], [(np.uint32, (5, 8))])
+    assert e.value.position == 2 and not e.value.fallback_permitted
+
+
+@pytest.mark.parametrize("m,n,k,silu", [(512, 512, 256, True), (16, 1024, 512, False), (300, 130, 72, True)])
+def test_bf16_contraction_routed(ctx, m, n, k, silu):
+    rng = np.random.default_rng(m + n + k)
+    a = oracle.bf16_narrow((rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32))
+    b = oracle.bf16_narrow((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
+    ep = L.EPILOGUE_SILU if silu else L.EPILOGUE_NONE
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=ep, ctx=ctx)
+    (got,) = _routed(ctx, rz, [a, b], [(np.uint16, (m, n))])
+    from tiler_amd import families
+    assert np.array_equal(got, families.contract_bf16(a, b, ep, ctx=ctx))
+
+
+def test_strict_contraction_routed(ctx):
+    rng = np.random.default_rng(73)
+    a = rng.standard_normal((40, 9)).astype(np.float32)
+    b = rng.standard_normal((70, 9)).astype(np.float32)
+    rz = realize(L.PROGRAM_CONTRACTION, (40, 70, 9), ctx=ctx)
+    (got,) = _routed(ctx, rz, [a, b], [(np.float32, (40, 70))])
+    assert np.array_equal(bits(got).reshape(-1), bits(oracle.contract_strict_f32(a, b, 40, 70, 9)).reshape(-1))
+
+
+def test_route_refuses_before_commit(ctx):
+    rz = realize(L.PROGRAM_SOFTMAX, (4, 256), ctx=ctx)
+    x = ctx.alloc(4 * 256 * 4)
+    small = ctx.alloc(64)
+    try:
+        with pytest.raises(Refusal):
+            route(ctx, rz, [x, small])                  # output slot too small
+        with pytest.raises(Refusal):
+            route(ctx, rz, [x.offset(4), x])            # not 16-byte aligned as assumed
+        with pytest.raises(Refusal):
+            route(ctx, rz, [x, None])                   # an output needs caller storage
+        with pytest.raises(Refusal):
+            route(ctx, rz, [x])                         # one binding per slot
+    finally:
+        x.free(); small.free()

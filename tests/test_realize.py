@@ -1,0 +1,167 @@
+"""The realization recognizer, device-free: which entry points realize a
+region, with what launch geometry, storage slots and argument segment, and
+which regions it refuses.
+
+`tiler_hip_realize` plays the role tiler-metal's emit_entry_point plays for
+a scheduled region (tiler-metal/src/emit.rs:647-840).  Its answer is the
+program the family entry point itself runs for the same request, so these
+tests pin the choices the families make at the C5/C2/C3/C4/C1 shapes and at
+the edges: tail variants, long rows, small grids, unaligned storage.
+"""
+from __future__ import annotations
+
+import ctypes
+import struct
+
+import pytest
+
+from tiler_amd import _lib as L
+from tiler_amd.realize import realize
+from tiler_amd.runtime import Refusal
+
+EPS = 0x3727C5AC
+
+
+def _descriptor_kernarg_bytes(symbol: str) -> int:
+    for i in range(1000):
+        e = L.EntryInfo()
+        if L.lib().tiler_hip_payload_entry(i, ctypes.byref(e)) != L.OK:
+            break
+        if e.symbol.decode() == symbol:
+            return e.kernarg_bytes
+    raise KeyError(symbol)
+
+
+def _check_segments(rz):
+    """Every argument segment fits its kernel's descriptor, and kernels with
+    no hidden arguments (descriptor below 256 bytes) match it exactly;
+    pointer fields are 8-byte aligned and name declared slots."""
+    for i, d in enumerate(rz.dispatches):
+        e = rz.raw.entries[i]
+        desc = _descriptor_kernarg_bytes(d.symbol)
+        assert e.kernarg_bytes <= desc, d.symbol
+        if desc < 256:
+            assert (e.kernarg_bytes + 7) // 8 * 8 == (desc + 7) // 8 * 8, d.symbol
+        for slot, off in d.bindings:
+            assert off % 8 == 0 and slot < len(rz.slots)
+
+
+def test_rms_norm_headline_and_variants():
+    rz = realize(L.PROGRAM_RMS_NORM, (8192, 4096), dtype=L.BF16, scalars=(EPS,),
+                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST)
+    assert rz.symbols == ["tiler_rms_norm_bf16_ch8_full"]
+    assert rz.dispatches[0].grid == (2048, 1, 1) and rz.dispatches[0].block == (256, 1, 1)
+    assert rz.slots == [(L.SLOT_INPUT, 8192 * 4096 * 2), (L.SLOT_INPUT, 4096 * 2),
+                        (L.SLOT_OUTPUT, 8192 * 4096 * 2)]
+    assert rz.alignment == 16
+    _check_segments(rz)
+    # kernel arguments: x, w, w_row_stride (0: broadcast), y, rows, extent, eps
+    seg = bytes(rz.raw.entries[0].kernargs[:rz.raw.entries[0].kernarg_bytes])
+    assert struct.unpack_from("<QQQQQII", seg) == (0, 0, 0, 0, 8192, 4096, EPS)
+    unaligned = realize(L.PROGRAM_RMS_NORM, (8, 4096), dtype=L.BF16, scalars=(EPS,), flags=0)
+    assert unaligned.symbols == ["tiler_rms_norm_bf16_ch8_u"] and unaligned.alignment == 1
+    long_row = realize(L.PROGRAM_RMS_NORM, (3, 20000), dtype=L.BF16, scalars=(EPS,))
+    assert long_row.symbols == ["tiler_rms_norm_bf16_long4_a"]
+    assert long_row.dispatches[0].grid == (3, 1, 1) and long_row.dispatches[0].block == (1024, 1, 1)
+    _check_segments(long_row)
+
+
+def test_softmax_and_sums():
+    sm = realize(L.PROGRAM_SOFTMAX, (65536, 2048))
+    assert sm.symbols == ["tiler_softmax_f32_ch8_full"] and sm.dispatches[0].grid == (16384, 1, 1)
+    _check_segments(sm)
+
+    tree = realize(L.PROGRAM_SERIAL_SUM, (1, 1 << 24), topology=L.SUM_TREE)
+    assert tree.symbols == ["tiler_sum_f32_grid", "tiler_sum_f32_grid_final"]
+    G = L.lib().tiler_hip_sum_tree_workgroups(None, 1 << 24)
+    assert tree.dispatches[0].grid == (G, 1, 1) and tree.dispatches[1].grid == (1, 1, 1)
+    assert tree.slots[2] == (L.SLOT_SCRATCH, G * 4)
+    assert [s for s, _ in tree.dispatches[0].bindings] == [0, 2]      # x, partials
+    assert [s for s, _ in tree.dispatches[1].bindings] == [2, 1]      # partials, out
+    _check_segments(tree)
+    assert realize(L.PROGRAM_SERIAL_SUM, (1, 1000), topology=L.SUM_TREE, flags=0).symbols[0] == \
+        "tiler_sum_f32_grid_unaligned"
+    assert realize(L.PROGRAM_SERIAL_SUM, (64, 1000), topology=L.SUM_TREE).symbols == ["tiler_sum_f32_rows"]
+
+    mp = realize(L.PROGRAM_SERIAL_SUM, (3, 120), topology=L.SUM_MULTIPASS, grouping=(4, 30))
+    assert mp.symbols == ["tiler_sum_f32_partials", "tiler_sum_f32_serial"]
+    assert mp.slots[2] == (L.SLOT_SCRATCH, 3 * 4 * 4)
+    _check_segments(mp)
+
+    coop = realize(L.PROGRAM_SERIAL_SUM, (5, 4 * 3 * 2), topology=L.SUM_COOPERATIVE, grouping=(4, 3, 2),
+                   flags=L.REGION_ALIGNED16 | L.REGION_PARTICIPANT_MAJOR)
+    assert coop.symbols == ["tiler_sum_f32_cooperative"]
+    assert coop.dispatches[0].grid == (5, 1, 1) and coop.dispatches[0].block == (4, 1, 1)
+    seg = bytes(coop.raw.entries[0].kernargs[:coop.raw.entries[0].kernarg_bytes])
+    # x, extent, participants, chunk, rounds, participant_major, out (natural alignment)
+    assert struct.unpack_from("<QQI4xQQI4xQ", seg) == (0, 24, 4, 3, 2, 1, 0)
+    _check_segments(coop)
+
+
+def test_contraction_paths():
+    c5 = realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, variant=L.EPILOGUE_SILU)
+    assert c5.symbols == ["tiler_contract_bf16_silu_t256"]
+    assert c5.dispatches[0].grid == (256, 1, 1) and c5.dispatches[0].block == (1024, 1, 1)
+    _check_segments(c5)
+    assert realize(L.PROGRAM_CONTRACTION, (16, 4096, 4096), dtype=L.BF16).symbols == \
+        ["tiler_contract_bf16_skinny1"]
+    small = realize(L.PROGRAM_CONTRACTION, (1000, 2048, 512), dtype=L.BF16)
+    assert small.symbols == ["tiler_contract_bf16_t128"] and small.dispatches[0].grid == (8 * 16, 1, 1)
+    assert realize(L.PROGRAM_CONTRACTION, (300, 130, 64), dtype=L.BF16).symbols == \
+        ["tiler_contract_bf16_g128"]
+    assert realize(L.PROGRAM_CONTRACTION, (300, 128, 60), dtype=L.BF16).symbols == \
+        ["tiler_contract_bf16_g128_k"]
+    strict = realize(L.PROGRAM_CONTRACTION, (40, 70, 9))
+    assert strict.symbols == ["tiler_contract_strict_f32"] and strict.dispatches[0].grid == (5, 3, 1)
+    _check_segments(strict)
+
+
+def test_moves_and_maps():
+    g = realize(L.PROGRAM_GATHER, (1, 128256, 4096, 16384), variant=2)
+    assert g.symbols == ["tiler_fill_u32", "tiler_gather_u128"]
+    assert g.slots[3] == (L.SLOT_SCRATCH, 8)
+    _check_segments(g)
+    assert realize(L.PROGRAM_GATHER, (2, 50, 7, 5), variant=2).symbols[1] == "tiler_gather_u16"   # 14-byte runs
+    assert realize(L.PROGRAM_GATHER, (2, 50, 8, 5), variant=2, flags=0).symbols[1] == "tiler_gather_u8"
+
+    rows_mode = realize(L.PROGRAM_BROADCAST, (8, 4096), variant=2, rank=2, strides=(0, 1), grouping=(4096,))
+    assert rows_mode.symbols == ["tiler_broadcast_rows_u16"]
+    _check_segments(rows_mode)
+    assert realize(L.PROGRAM_BROADCAST, (8, 3), variant=4, rank=2, strides=(0, 1), grouping=(3,)).symbols == \
+        ["tiler_broadcast_u32"]
+
+    add = realize(L.PROGRAM_POINTWISE, (1024,), variant=L.MAP_ADD)
+    assert add.symbols == ["tiler_map_f32_v4_op2"] and len(add.slots) == 3
+    _check_segments(add)
+    # a ragged or unaligned map runs the scalar kernel over all of it (no slot offsets in a plan)
+    assert realize(L.PROGRAM_POINTWISE, (1023,), variant=L.MAP_ADD).symbols == ["tiler_map_f32"]
+    assert realize(L.PROGRAM_POINTWISE, (1024,), variant=L.MAP_SILU, flags=0).symbols == ["tiler_map_f32"]
+    silu = realize(L.PROGRAM_POINTWISE, (4096,), variant=L.MAP_SILU)
+    assert silu.symbols == ["tiler_map_f32_v4_op1"] and len(silu.slots) == 2
+
+
+def test_zero_work_skips_dispatch():
+    assert realize(L.PROGRAM_SOFTMAX, (0, 2048)).raw.entry_count == 0
+    assert realize(L.PROGRAM_CONTRACTION, (0, 64, 64), dtype=L.BF16).raw.entry_count == 0
+    assert realize(L.PROGRAM_GATHER, (1, 10, 4, 0), variant=4).raw.entry_count == 0
+
+
+@pytest.mark.parametrize("kwargs,status", [
+    (dict(program=L.PROGRAM_RMS_NORM, extents=(4, 64), dtype=L.F32, scalars=(0,)), L.REFUSE_INVALID_ARGUMENT),
+    (dict(program=L.PROGRAM_SERIAL_SUM, extents=(2, 100), topology=L.SUM_MULTIPASS, grouping=(3, 30)),
+     L.REFUSE_INVALID_ARGUMENT),
+    (dict(program=L.PROGRAM_SERIAL_SUM, extents=(2, 100), dtype=L.BF16), L.REFUSE_UNSUPPORTED),
+    (dict(program=L.PROGRAM_CONTRACTION, extents=(4, 4, 0), dtype=L.BF16), L.REFUSE_INVALID_ARGUMENT),
+    (dict(program=L.PROGRAM_CONTRACTION, extents=(4, 4, 4), variant=L.EPILOGUE_SILU), L.REFUSE_UNSUPPORTED),
+    (dict(program=L.PROGRAM_SOFTMAX, extents=(4, 64), dtype=L.BF16), L.REFUSE_UNSUPPORTED),
+    (dict(program=L.PROGRAM_POINTWISE, extents=(64,), dtype=L.BF16, variant=L.MAP_SILU), L.REFUSE_UNSUPPORTED),
+    (dict(program=L.PROGRAM_BROADCAST, extents=(4, 8), variant=4, rank=2, strides=(8, 1), grouping=(16,)),
+     L.REFUSE_INVALID_ARGUMENT),
+    (dict(program=99, extents=(1,)), L.REFUSE_UNSUPPORTED),
+])
+def test_refusals_are_typed_and_pre_commit(kwargs, status):
+    program = kwargs.pop("program")
+    extents = kwargs.pop("extents")
+    with pytest.raises(Refusal) as e:
+        realize(program, extents, **kwargs)
+    assert e.value.status == status and e.value.fallback_permitted

@@ -50,6 +50,23 @@ ROWS_SUM = 2
 EPILOGUE_NONE = 0
 EPILOGUE_SILU = 1
 
+PROGRAM_POINTWISE = 1
+PROGRAM_SERIAL_SUM = 2
+PROGRAM_RMS_NORM = 3
+PROGRAM_SOFTMAX = 4
+PROGRAM_CONTRACTION = 5
+PROGRAM_GATHER = 6
+PROGRAM_BROADCAST = 7
+
+REGION_ALIGNED16 = 1
+REGION_OPERAND_BROADCAST = 2
+REGION_INDEX_SIGNED = 4
+REGION_PARTICIPANT_MAJOR = 8
+
+SLOT_INPUT = 0
+SLOT_OUTPUT = 1
+SLOT_SCRATCH = 2
+
 
 class TargetProfile(ctypes.Structure):
     _fields_ = [
@@ -161,6 +178,45 @@ class SumPlan(ctypes.Structure):
     ]
 
 
+class Region(ctypes.Structure):
+    _fields_ = [
+        ("program", ctypes.c_uint32),
+        ("topology", ctypes.c_uint32),
+        ("dtype", ctypes.c_uint32),
+        ("variant", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("rank", ctypes.c_uint32),
+        ("extents", ctypes.c_uint64 * 8),
+        ("strides", ctypes.c_uint64 * 8),
+        ("grouping", ctypes.c_uint64 * 3),
+        ("scalars", ctypes.c_uint32 * 2),
+    ]
+
+
+class RealizedEntry(ctypes.Structure):
+    _fields_ = [
+        ("entry", ctypes.c_uint32),
+        ("grid", ctypes.c_uint32 * 3),
+        ("block", ctypes.c_uint32 * 3),
+        ("kernarg_bytes", ctypes.c_uint32),
+        ("kernargs", ctypes.c_uint8 * 256),
+        ("binding_count", ctypes.c_uint32),
+        ("binding_slots", ctypes.c_uint32 * 6),
+        ("binding_offsets", ctypes.c_uint32 * 6),
+    ]
+
+
+class Realization(ctypes.Structure):
+    _fields_ = [
+        ("slot_count", ctypes.c_uint32),
+        ("slot_roles", ctypes.c_uint32 * 6),
+        ("slot_bytes", ctypes.c_uint64 * 6),
+        ("slot_alignment", ctypes.c_uint32),
+        ("entry_count", ctypes.c_uint32),
+        ("entries", RealizedEntry * 4),
+    ]
+
+
 _P = ctypes.c_void_p
 _U64 = ctypes.c_uint64
 _U32 = ctypes.c_uint32
@@ -217,6 +273,8 @@ SIGNATURES = {
                                              ctypes.POINTER(ctypes.c_int64)]),
     "tiler_hip_contract_strict_f32": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _P]),
     "tiler_hip_contract_bf16": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _U32, _P]),
+    "tiler_hip_realize": (_S, [_CTX, ctypes.POINTER(Region), ctypes.POINTER(Realization),
+                               ctypes.c_char_p, _U64]),
 }
 
 _lib = None

@@ -62,6 +62,7 @@ def build(verbose: bool = False) -> str:
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{ROOT}/include", f"-I{BUILD}",
           "-o", tmp_lib,
           os.path.join(CSRC, "runtime", "tiler_hip.cpp"),
+          os.path.join(CSRC, "runtime", "program.cpp"),
           os.path.join(CSRC, "runtime", "code_object.cpp"),
           payload_obj,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])

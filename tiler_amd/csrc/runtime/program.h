@@ -1,0 +1,114 @@
+// Launch programs: what each realization family dispatches, as data.
+//
+// A planner turns one family request (shape, grouping, dtype, and the base
+// address of every storage slot, which decides the vector width a kernel may
+// assume) into a Program: the storage slots the dispatches touch (inputs,
+// outputs, scratch) and the launches in execution order, each with its symbol,
+// grid, workgroup size, packed kernel-argument segment and the argument fields
+// that hold slot addresses.  The family entry points of the C ABI execute a
+// Program on the spot; tiler_hip_realize exports the same Program as a
+// dispatch plan for the RuntimeAdapter route.  Everything is fixed-capacity:
+// planning allocates nothing.
+#pragma once
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "tiler_hip.h"
+
+namespace tiler_rt {
+
+constexpr uint32_t kMaxKernargBytes = 256;
+constexpr uint32_t kMaxArgs = 12;
+constexpr uint32_t kMaxBindings = 6;
+constexpr uint32_t kMaxSlots = 6;
+constexpr uint32_t kMaxLaunches = 4;
+constexpr uint32_t kMaxSumWorkgroups = 4096;
+
+// Slot roles, as tiler_hip_realization reports them.
+constexpr uint32_t kSlotInput = TILER_HIP_SLOT_INPUT;
+constexpr uint32_t kSlotOutput = TILER_HIP_SLOT_OUTPUT;
+constexpr uint32_t kSlotScratch = TILER_HIP_SLOT_SCRATCH;
+
+struct Binding {
+  uint32_t offset;  // byte offset of the pointer field in the kernarg segment
+  uint32_t slot;
+  uint64_t addend;  // bytes past the slot base (direct execution only)
+};
+
+struct Launch {
+  char symbol[64];
+  uint32_t grid[2];
+  uint32_t block;
+  uint8_t kernargs[kMaxKernargBytes];
+  uint32_t kernarg_bytes;
+  uint32_t arg_offsets[kMaxArgs];
+  uint32_t nargs;
+  Binding bindings[kMaxBindings];
+  uint32_t nbindings;
+  bool overflow;  // an argument did not fit (a planner bug; refused)
+
+  // Kernel arguments in declaration order, each at its natural alignment
+  // (the HIP kernarg layout).
+  Launch& ptr(uint32_t slot, uint64_t addend = 0);  // a slot address
+  Launch& null_ptr();                               // a pointer argument bound to nothing
+  Launch& u32(uint32_t v);
+  Launch& u64(uint64_t v);
+  Launch& f32(float v);
+  Launch& blob(const void* p, uint32_t bytes, uint32_t align);
+};
+
+struct Program {
+  uint64_t slot_bytes[kMaxSlots];
+  uint32_t slot_roles[kMaxSlots];
+  uint32_t nslots;
+  Launch launches[kMaxLaunches];
+  uint32_t nlaunches;
+  std::string diag;
+
+  Program();
+  uint32_t slot(uint64_t bytes, uint32_t role);
+  Launch& add(const char* symbol, uint32_t gx, uint32_t gy, uint32_t block);
+  tiler_hip_status refuse(tiler_hip_status st, const char* what) {
+    diag = what;
+    return st;
+  }
+};
+
+// What a planner may assume about the device.
+struct Target {
+  uint32_t compute_units;
+};
+
+// Direct: the program runs now, on known addresses (it may bind a slot at an
+// offset, and the gather record is armed by the context).  Realized: the
+// program is exported as a dispatch plan (no offsets; it arms its own record).
+enum class Mode { Direct, Realized };
+
+// Workgroups of the single-output tree for n contributors.
+uint32_t tree_workgroups(const Target& t, uint64_t n);
+
+// Planners.  Slot order is part of each contract (tiler_hip_realize documents
+// it); `addr` holds each slot's base address, or a stand-in whose low bits
+// carry the alignment a realization may assume.
+tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
+                              const tiler_hip_sum_plan& sp, const uintptr_t* addr, Program& p);
+tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
+                               uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
+                               Program& p);
+tiler_hip_status plan_softmax_f32(uint64_t rows, uint64_t extent, const uintptr_t* addr,
+                                  Program& p);
+tiler_hip_status plan_map(Mode mode, uint32_t op, uint32_t dtype, int32_t x2_broadcast,
+                          uint64_t n, float a, float b, const uintptr_t* addr, Program& p);
+tiler_hip_status plan_broadcast(uint64_t src_elements, uint32_t rank, const uint64_t* out_dims,
+                                const uint64_t* src_strides, uint32_t element_bytes,
+                                Program& p);
+tiler_hip_status plan_gather(Mode mode, uint64_t outer, uint64_t gathered, uint64_t inner,
+                             uint32_t element_bytes, uint64_t count, int32_t index_signed,
+                             const uintptr_t* addr, Program& p);
+tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p);
+tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
+                                    uint32_t epilogue, const uintptr_t* addr, Program& p);
+
+}  // namespace tiler_rt

@@ -15,6 +15,7 @@
 
 #include "build_info.h"
 #include "code_object.h"
+#include "program.h"
 
 extern "C" const uint8_t tiler_hip_code_object[];
 extern "C" const uint8_t tiler_hip_code_object_end[];
@@ -167,7 +168,8 @@ const EntryRow kEntries[] = {
 };
 constexpr uint32_t kEntryCount = sizeof(kEntries) / sizeof(kEntries[0]);
 
-constexpr uint32_t kMaxSumWorkgroups = 4096;
+constexpr uint32_t kMaxSumWorkgroups = tiler_rt::kMaxSumWorkgroups;
+constexpr uint32_t kProfileComputeUnits = 256;
 
 void copy_text(char* dst, uint64_t cap, const std::string& s) {
   if (!dst || cap == 0) return;
@@ -229,24 +231,39 @@ tiler_hip_status launch(tiler_hip_context* ctx, const char* symbol, uint32_t gx,
   return TILER_HIP_OK;
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-
-// Rows longer than one wave holds (8192 elements) run one 1024-thread
-// workgroup per row: chunks per thread rounded up to a power of two while the
-// row fits in registers (<= 8 chunks), else 0 (the row is streamed).
+// Rows longer than one wave holds run one workgroup per row (the grouping
+// tiler_hip_row_grouping reports).
 constexpr uint64_t kWaveRowMax = 8192;
-uint32_t long_row_chunks(uint64_t extent, uint32_t vec) {
-  uint64_t per = (((extent + vec - 1) / vec) + 1023) / 1024;
-  if (per > 8) return 0;
-  uint32_t ch = 1;
-  while (ch < per) ch <<= 1;
-  return ch;
+
+tiler_rt::Target target_of(const tiler_hip_context* ctx) {
+  return tiler_rt::Target{ctx ? ctx->compute_units : kProfileComputeUnits};
 }
 
-uint32_t pow2_at_least(uint64_t v) {
-  uint32_t p = 1;
-  while (p < v) p <<= 1;
-  return p;
+// Runs a planned program on `s`: slot addresses (plus each binding's offset)
+// patched into a copy of every launch's argument segment, launched in order.
+tiler_hip_status run_program(tiler_hip_context* ctx, const tiler_rt::Program& p, void* const* slots,
+                             hipStream_t s) {
+  for (uint32_t i = 0; i < p.nlaunches; ++i) {
+    const tiler_rt::Launch& l = p.launches[i];
+    if (l.overflow) return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, std::string("argument segment overflow: ") + l.symbol);
+    hipFunction_t f = fn(ctx, l.symbol);
+    if (!f) return fail(ctx, TILER_HIP_REFUSE_NOT_PREPARED, std::string("kernel not loaded: ") + l.symbol);
+    if (l.grid[0] == 0 || l.grid[1] == 0) continue;
+    uint8_t args[tiler_rt::kMaxKernargBytes];
+    std::memcpy(args, l.kernargs, l.kernarg_bytes);
+    for (uint32_t b = 0; b < l.nbindings; ++b) {
+      char* base = static_cast<char*>(slots[l.bindings[b].slot]);
+      char* ptr = base ? base + l.bindings[b].addend : nullptr;
+      std::memcpy(args + l.bindings[b].offset, &ptr, sizeof(ptr));
+    }
+    void* params[tiler_rt::kMaxArgs];
+    for (uint32_t a = 0; a < l.nargs; ++a) params[a] = args + l.arg_offsets[a];
+    hipError_t e = hipModuleLaunchKernel(f, l.grid[0], l.grid[1], 1, l.block, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess)
+      return fail(ctx, TILER_HIP_FAIL_LAUNCH,
+                  std::string("hipModuleLaunchKernel(") + l.symbol + "): " + hipGetErrorString(e));
+  }
+  return TILER_HIP_OK;
 }
 
 }  // namespace
@@ -260,7 +277,7 @@ tiler_hip_status tiler_hip_profile_declare(tiler_hip_target_profile* out) {
   copy_text(out->profile_key, sizeof(out->profile_key), kProfileKey);
   copy_text(out->target_triple, sizeof(out->target_triple), kTarget);
   out->wavefront_size = 64;
-  out->compute_units = 256;
+  out->compute_units = kProfileComputeUnits;
   out->xcds = 8;
   out->simds_per_cu = 4;
   out->max_threads_per_workgroup = 1024;
@@ -752,11 +769,7 @@ tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_
 }
 
 uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context* ctx, uint64_t n) {
-  uint64_t tiles = (n + 1023) / 1024;
-  uint64_t cap = ctx ? 2ull * ctx->compute_units : 512;
-  if (cap > kMaxSumWorkgroups) cap = kMaxSumWorkgroups;
-  uint64_t g = tiles < cap ? tiles : cap;
-  return g ? (uint32_t)g : 1u;
+  return tiler_rt::tree_workgroups(target_of(ctx), n);
 }
 
 tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint64_t rows,
@@ -764,66 +777,27 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
                                    tiler_hip_stream stream) {
   if (!ctx || !plan || (rows && !out) || (rows && extent && !x))
     return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  const uintptr_t addr[3] = {(uintptr_t)x, (uintptr_t)out, 0};
+  tiler_hip_status st = tiler_rt::plan_sum_f32(target_of(ctx), rows, extent, *plan, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
   hipStream_t s = pick(ctx, stream);
-  if (rows == 0) return TILER_HIP_OK;
-  switch (plan->topology) {
-    case TILER_HIP_SUM_SERIAL: {
-      uint64_t outer = rows, inner = 1;
-      void* args[] = {&x, &outer, &extent, &inner, &out};
-      return launch(ctx, "tiler_sum_f32_serial", (uint32_t)((rows + 255) / 256), 1, 256, s, args);
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(x), out, nullptr};
+  // Partials live in the context workspace when they fit (ordered on the
+  // stream); only larger splits allocate, stream-ordered.
+  bool own = false;
+  if (p.nslots > 2 && p.nlaunches) {
+    if (p.slot_bytes[2] <= (uint64_t)kMaxSumWorkgroups * 4) {
+      slots[2] = ctx->sum_partials;
+    } else {
+      if (hipMallocAsync(&slots[2], p.slot_bytes[2], s) != hipSuccess)
+        return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "partials allocation failed");
+      own = true;
     }
-    case TILER_HIP_SUM_MULTIPASS: {
-      uint64_t P = plan->partitions, c = plan->per_partition;
-      if (P == 0 || (c != 0 && P > UINT64_MAX / c) || P * c != extent)
-        return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "partitions do not cover the axis exactly");
-      // Partials live in the context workspace when they fit (ordered on the
-      // stream like the tree sum's); only larger splits allocate, stream-ordered.
-      void* partials = nullptr;
-      const bool own = rows * P > kMaxSumWorkgroups;
-      if (own) {
-        if (hipMallocAsync(&partials, rows * P * 4, s) != hipSuccess)
-          return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "partials allocation failed");
-      } else {
-        partials = ctx->sum_partials;
-      }
-      float* pp = static_cast<float*>(partials);
-      void* a1[] = {&x, &rows, &extent, &P, &c, &pp};
-      tiler_hip_status st = launch(ctx, "tiler_sum_f32_partials", (uint32_t)((rows * P + 255) / 256), 1, 256, s, a1);
-      if (st == TILER_HIP_OK) {
-        uint64_t outer = rows, inner = 1;
-        const float* cp = pp;
-        void* a2[] = {&cp, &outer, &P, &inner, &out};
-        st = launch(ctx, "tiler_sum_f32_serial", (uint32_t)((rows + 255) / 256), 1, 256, s, a2);
-      }
-      if (own) hipFreeAsync(partials, s);
-      return st;
-    }
-    case TILER_HIP_SUM_COOPERATIVE: {
-      uint64_t P = plan->participants, c = plan->per_partition, R = plan->rounds;
-      if (P == 0 || P > 1024 || c == 0 || R == 0 || P * c * R != extent)
-        return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "grouping does not cover the axis exactly");
-      uint32_t P32 = (uint32_t)P, pm = plan->participant_major ? 1u : 0u;
-      void* args[] = {&x, &extent, &P32, &c, &R, &pm, &out};
-      return launch(ctx, "tiler_sum_f32_cooperative", (uint32_t)rows, 1, P32, s, args);
-    }
-    case TILER_HIP_SUM_TREE: {
-      if (rows == 1) {
-        uint32_t G = tiler_hip_sum_tree_workgroups(ctx, extent);
-        float* partials = ctx->sum_partials;
-        uint64_t n = extent;
-        void* a1[] = {&x, &n, &partials};
-        tiler_hip_status st = launch(ctx, aligned16(x) ? "tiler_sum_f32_grid" : "tiler_sum_f32_grid_unaligned", G, 1, 256, s, a1);
-        if (st != TILER_HIP_OK) return st;
-        const float* cp = partials;
-        void* a2[] = {&cp, &G, &n, &out};
-        return launch(ctx, "tiler_sum_f32_grid_final", 1, 1, 256, s, a2);
-      }
-      void* args[] = {&x, &extent, &out};
-      return launch(ctx, "tiler_sum_f32_rows", (uint32_t)rows, 1, 256, s, args);
-    }
-    default:
-      return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "unknown reduction topology");
   }
+  st = run_program(ctx, p, slots, s);
+  if (own) hipFreeAsync(slots[2], s);
+  return st;
 }
 
 tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, const void* x,
@@ -831,164 +805,52 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, cons
                                     uint64_t extent, uint32_t eps_bits, void* y,
                                     tiler_hip_stream stream) {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  float eps;
-  std::memcpy(&eps, &eps_bits, 4);
-  // rms_norm.rs:462-466: a non-positive or non-finite eps refuses.
-  if (!(eps > 0.0f) || !std::isfinite(eps))
-    return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "eps must be positive and finite");
-  if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16)
-    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "rms_norm dtype");
-  if (rows == 0 || extent == 0) return TILER_HIP_OK;
-  if (!x || !w || !y) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  const uint32_t vec = dtype == TILER_HIP_BF16 ? 8 : 4;
-  const uint32_t max_ch = dtype == TILER_HIP_BF16 ? 16 : 32;
-  if (extent > 0xffffffffull)
-    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
-  const uint64_t elem = dtype == TILER_HIP_BF16 ? 2 : 4;
-  bool al = aligned16(x) && aligned16(w) && aligned16(y) && (extent * elem) % 16 == 0;
-  uint64_t wstride_l = weight_broadcast ? 0 : extent;
-  uint32_t ext32_l = (uint32_t)extent;
-  if (extent > kWaveRowMax) {  // one workgroup per row
-    if (rows > 0x7fffffffull) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-    char lname[64];
-    std::snprintf(lname, sizeof(lname), "tiler_rms_norm_%s_long%u%s", dtype == TILER_HIP_BF16 ? "bf16" : "f32",
-                  long_row_chunks(extent, vec), al ? "_a" : "_u");
-    void* largs[] = {&x, &w, &wstride_l, &y, &ext32_l, &eps};
-    return launch(ctx, lname, (uint32_t)rows, 1, 1024, pick(ctx, stream), largs);
-  }
-  uint64_t chunks = (extent + 64ull * vec - 1) / (64ull * vec);
-  uint32_t ch = pow2_at_least(chunks);
-  if (ch > max_ch) return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row realization");
-  bool full = al && extent == (uint64_t)ch * 64 * vec;
-  char name[64];
-  std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_ch%u%s",
-                dtype == TILER_HIP_BF16 ? "bf16" : "f32", ch, full ? "_full" : al ? "" : "_u");
-  uint64_t wstride = weight_broadcast ? 0 : extent;
-  uint32_t ext32 = (uint32_t)extent;
-  void* args[] = {&x, &w, &wstride, &y, &rows, &ext32, &eps};
-  // one row per wave, four waves per workgroup
-  if ((rows + 3) / 4 > 0x7fffffffull)
-    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-  return launch(ctx, name, (uint32_t)((rows + 3) / 4), 1, 256, pick(ctx, stream), args);
+  tiler_rt::Program p;
+  const uintptr_t addr[3] = {(uintptr_t)x, (uintptr_t)w, (uintptr_t)y};
+  tiler_hip_status st = tiler_rt::plan_rms_norm(dtype, weight_broadcast, rows, extent, eps_bits, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!x || !w || !y)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(x), const_cast<void*>(w), y};
+  return run_program(ctx, p, slots, pick(ctx, stream));
 }
 
 tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, uint64_t rows,
                                        uint64_t extent, float* y, tiler_hip_stream stream) {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (rows == 0 || extent == 0) return TILER_HIP_OK;
-  if (!x || !y) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (extent > 0xffffffffull)
-    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
-  bool al = aligned16(x) && aligned16(y) && extent % 4 == 0;
-  if (extent > kWaveRowMax) {  // one workgroup per row
-    if (rows > 0x7fffffffull) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-    char lname[64];
-    std::snprintf(lname, sizeof(lname), "tiler_softmax_f32_long%u%s", long_row_chunks(extent, 4), al ? "_a" : "_u");
-    uint32_t ext32_l = (uint32_t)extent;
-    void* largs[] = {&x, &y, &ext32_l};
-    return launch(ctx, lname, (uint32_t)rows, 1, 1024, pick(ctx, stream), largs);
-  }
-  uint32_t ch = pow2_at_least((extent + 255) / 256);
-  if (ch > 32) return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "row realization");
-  bool full = al && extent == (uint64_t)ch * 256;
-  char name[64];
-  std::snprintf(name, sizeof(name), "tiler_softmax_f32_ch%u%s", ch, full ? "_full" : al ? "" : "_u");
-  uint32_t ext32 = (uint32_t)extent;
-  void* args[] = {&x, &y, &rows, &ext32};
-  if ((rows + 3) / 4 > 0x7fffffffull)
-    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-  return launch(ctx, name, (uint32_t)((rows + 3) / 4), 1, 256, pick(ctx, stream), args);
+  tiler_rt::Program p;
+  const uintptr_t addr[2] = {(uintptr_t)x, (uintptr_t)y};
+  tiler_hip_status st = tiler_rt::plan_softmax_f32(rows, extent, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!x || !y)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(x), y};
+  return run_program(ctx, p, slots, pick(ctx, stream));
 }
 
 tiler_hip_status tiler_hip_map(tiler_hip_context* ctx, uint32_t op, uint32_t dtype,
                                const void* x, const void* x2, int32_t x2_broadcast, uint64_t n,
                                float a, float b, void* y, tiler_hip_stream stream) {
-  if (!ctx || op > TILER_HIP_MAP_MULTIPLY) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16)
-    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "map dtype");
-  if (n == 0) return TILER_HIP_OK;
-  if (!x || !y || ((op == TILER_HIP_MAP_ADD || op == TILER_HIP_MAP_MULTIPLY) && !x2))
-    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (dtype == TILER_HIP_BF16 && op == TILER_HIP_MAP_SILU)
-    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "silu is an f32 family");
-  uint64_t stride2 = x2_broadcast ? 0 : 1;
-  hipStream_t s = pick(ctx, stream);
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   const bool binary = op == TILER_HIP_MAP_ADD || op == TILER_HIP_MAP_MULTIPLY;
-  const uint64_t per = dtype == TILER_HIP_BF16 ? 8 : 4;  // elements per 16-byte chunk
-  uint64_t head = 0;                                      // elements the vector kernel covers
-  if (aligned16(x) && aligned16(y) && (!binary || x2_broadcast || aligned16(x2))) head = n / per * per;
-  if (head) {
-    uint64_t chunks = head / per;
-    uint64_t blocks = (chunks + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    char name[48];
-    std::snprintf(name, sizeof(name), "tiler_map_%s_op%u%s", dtype == TILER_HIP_BF16 ? "bf16_v8" : "f32_v4", op,
-                  binary && x2_broadcast ? "_b" : "");
-    void* vargs[] = {&x, &x2, &chunks, &a, &b, &y};
-    tiler_hip_status st = launch(ctx, name, (uint32_t)blocks, 1, 256, s, vargs);
-    if (st != TILER_HIP_OK || head == n) return st;
-  }
-  // scalar kernel for unaligned operands or the tail after the 16-byte chunks
-  const uint64_t eb = dtype == TILER_HIP_BF16 ? 2 : 4;
-  const void* xt = static_cast<const char*>(x) + head * eb;
-  const void* x2t = x2 && !x2_broadcast ? static_cast<const char*>(x2) + head * eb : x2;
-  void* yt = static_cast<char*>(y) + head * eb;
-  uint64_t rest = n - head;
-  uint64_t blocks = (rest + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
-  void* args[] = {&xt, &x2t, &stride2, &rest, &op, &a, &b, &yt};
-  return launch(ctx, dtype == TILER_HIP_BF16 ? "tiler_map_bf16" : "tiler_map_f32",
-                (uint32_t)blocks, 1, 256, s, args);
+  tiler_rt::Program p;
+  const uintptr_t addr[3] = {(uintptr_t)x, binary ? (uintptr_t)x2 : (uintptr_t)y, (uintptr_t)y};
+  tiler_hip_status st = tiler_rt::plan_map(tiler_rt::Mode::Direct, op, dtype, x2_broadcast, n, a, b, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!x || !y || (binary && !x2))) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(x), binary ? const_cast<void*>(x2) : y, y};
+  return run_program(ctx, p, slots, pick(ctx, stream));
 }
-
-struct BroadcastGeometryHost {
-  uint64_t out_dims[8];
-  uint64_t src_strides[8];
-  uint32_t rank;
-};
 
 tiler_hip_status tiler_hip_broadcast(tiler_hip_context* ctx, const void* src, uint64_t src_elements,
                                      uint32_t rank, const uint64_t* out_dims,
                                      const uint64_t* src_strides, uint32_t element_bytes, void* out,
                                      tiler_hip_stream stream) {
-  if (!ctx || rank > 8 || (rank && (!out_dims || !src_strides)))
-    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (element_bytes != 2 && element_bytes != 4)
-    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, "broadcast element width");
-  BroadcastGeometryHost g;
-  std::memset(&g, 0, sizeof(g));
-  g.rank = rank;
-  uint64_t n = 1, last = 0;  // output elements; largest source offset read
-  bool overflow = false;
-  for (uint32_t d = 0; d < rank; ++d) {
-    g.out_dims[d] = out_dims[d];
-    g.src_strides[d] = src_strides[d];
-    if (out_dims[d] && n > UINT64_MAX / out_dims[d]) overflow = true;
-    n *= out_dims[d];
-  }
-  if (n == 0) return TILER_HIP_OK;
-  for (uint32_t d = 0; d < rank && !overflow; ++d) {
-    const uint64_t span = out_dims[d] - 1;
-    if (span && src_strides[d] > (UINT64_MAX - last) / span) overflow = true;
-    else last += span * src_strides[d];
-  }
-  if (overflow || last >= src_elements)
-    return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "broadcast geometry reads outside the source");
-  if (!src || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  hipStream_t s = pick(ctx, stream);
-  const uint64_t inner = rank ? out_dims[rank - 1] : 1;
-  if (rank && inner >= 256) {  // row mode: one source row offset per workgroup step
-    uint64_t rows = n / inner;
-    uint64_t blocks = rows < 8192 ? rows : 8192;
-    void* args[] = {&src, &out, &rows, &g};
-    return launch(ctx, element_bytes == 4 ? "tiler_broadcast_rows_u32" : "tiler_broadcast_rows_u16",
-                  (uint32_t)blocks, 1, 256, s, args);
-  }
-  uint64_t blocks = (n + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
-  void* args[] = {&src, &out, &n, &g};
-  return launch(ctx, element_bytes == 4 ? "tiler_broadcast_u32" : "tiler_broadcast_u16",
-                (uint32_t)blocks, 1, 256, s, args);
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  tiler_hip_status st = tiler_rt::plan_broadcast(src_elements, rank, out_dims, src_strides, element_bytes, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!src || !out)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(src), out};
+  return run_program(ctx, p, slots, pick(ctx, stream));
 }
 
 tiler_hip_status tiler_hip_validate_gather_index(const uint32_t* index, uint64_t count,
@@ -1010,23 +872,16 @@ tiler_hip_status tiler_hip_gather(tiler_hip_context* ctx, const void* source, ui
                                   uint64_t gathered, uint64_t inner, uint32_t element_bytes,
                                   const uint32_t* index, uint64_t count, int32_t index_signed,
                                   void* out, tiler_hip_stream stream) {
-  if (!ctx || element_bytes == 0) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  uint64_t runs = outer * count;
-  uint64_t run_bytes = inner * element_bytes;
-  if (runs == 0 || run_bytes == 0) return TILER_HIP_OK;
-  if (!source || !index || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  uintptr_t both = (uintptr_t)source | (uintptr_t)out;
-  uint32_t unit = 16;
-  while (unit > 1 && (run_bytes % unit != 0 || (both & (unit - 1)) != 0)) unit >>= 1;
-  const char* name = unit == 16 ? "tiler_gather_u128" : unit == 8 ? "tiler_gather_u64"
-                   : unit == 4 ? "tiler_gather_u32" : unit == 2 ? "tiler_gather_u16"
-                               : "tiler_gather_u8";
-  uint64_t run_units = run_bytes / unit;
-  uint32_t sgn = index_signed ? 1u : 0u;
-  unsigned long long* bad = ctx->gather_bad;
-  uint64_t blocks = runs < (1ull << 20) ? runs : (1ull << 20);
-  void* args[] = {&source, &outer, &gathered, &run_units, &index, &count, &sgn, &out, &bad};
-  return launch(ctx, name, (uint32_t)blocks, 1, 256, pick(ctx, stream), args);
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  const uintptr_t addr[4] = {(uintptr_t)source, (uintptr_t)index, (uintptr_t)out, 0};
+  tiler_hip_status st = tiler_rt::plan_gather(tiler_rt::Mode::Direct, outer, gathered, inner, element_bytes,
+                                              count, index_signed, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!source || !index || !out)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(source), const_cast<uint32_t*>(index), out,
+                                      ctx->gather_bad};
+  return run_program(ctx, p, slots, pick(ctx, stream));
 }
 
 tiler_hip_status tiler_hip_gather_status(tiler_hip_context* ctx, tiler_hip_stream stream,
@@ -1049,62 +904,136 @@ tiler_hip_status tiler_hip_contract_strict_f32(tiler_hip_context* ctx, const flo
                                                const float* b, uint64_t m, uint64_t n,
                                                uint64_t k, float* c, tiler_hip_stream stream) {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  // contraction.rs:420-428: an empty contracted domain has no unseeded result.
-  if (k == 0) return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty contracted extent");
-  if (m == 0 || n == 0) return TILER_HIP_OK;
-  if (!a || !b || !c) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (m > 0xffffffffull || n > 0xffffffffull || k > 0xffffffffull || (m + 15) / 16 > 65535)
-    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
-  uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
-  void* args[] = {&a, &b, &m32, &n32, &k32, &c};
-  return launch(ctx, "tiler_contract_strict_f32", (uint32_t)((n + 15) / 16),
-                (uint32_t)((m + 15) / 16), 256, pick(ctx, stream), args);
+  tiler_rt::Program p;
+  tiler_hip_status st = tiler_rt::plan_contract_strict_f32(m, n, k, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!a || !b || !c)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(a), const_cast<float*>(b), c};
+  return run_program(ctx, p, slots, pick(ctx, stream));
 }
 
 tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t* a,
                                          const uint16_t* b, uint64_t m, uint64_t n, uint64_t k,
                                          uint16_t* c, uint32_t epilogue,
                                          tiler_hip_stream stream) {
-  if (!ctx || epilogue > TILER_HIP_EPILOGUE_SILU) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (k == 0) return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty contracted extent");
-  if (m == 0 || n == 0) return TILER_HIP_OK;
-  if (!a || !b || !c) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull || (m + 127) / 128 > 65535)
-    return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
-  uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
-  // m <= 64 (decode shapes): B streamed once, one workgroup per 16 columns.
-  if (m <= 64 && k % 8 == 0 && aligned16(a) && aligned16(b) && (n + 15) / 16 <= 0x7fffffffull) {
-    char name[48];
-    std::snprintf(name, sizeof(name), "tiler_contract_bf16_%sskinny%u",
-                  epilogue == TILER_HIP_EPILOGUE_SILU ? "silu_" : "", (uint32_t)((m + 15) / 16));
-    void* args[] = {&a, &b, &m32, &n32, &k32, &c};
-    return launch(ctx, name, (uint32_t)((n + 15) / 16), 1, 1024, pick(ctx, stream), args);
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  const uintptr_t addr[3] = {(uintptr_t)a, (uintptr_t)b, (uintptr_t)c};
+  tiler_hip_status st = tiler_rt::plan_contract_bf16(target_of(ctx), m, n, k, epilogue, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!a || !b || !c)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<uint16_t*>(a), const_cast<uint16_t*>(b), c};
+  return run_program(ctx, p, slots, pick(ctx, stream));
+}
+
+// ---------------------------------------------------------------------------
+// Realization recognizer.
+tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip_region* r,
+                                   tiler_hip_realization* out, char* diagnostic,
+                                   uint64_t diagnostic_bytes) {
+  if (!r || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  std::memset(out, 0, sizeof(*out));
+  const bool al = (r->flags & TILER_HIP_REGION_ALIGNED16) != 0;
+  const bool bc = (r->flags & TILER_HIP_REGION_OPERAND_BROADCAST) != 0;
+  // A stand-in address per slot: 0 is 16-byte aligned, 1 is not.
+  const uintptr_t addr[tiler_rt::kMaxSlots] = {al ? 0u : 1u, al ? 0u : 1u, al ? 0u : 1u,
+                                               al ? 0u : 1u, al ? 0u : 1u, al ? 0u : 1u};
+  const uint64_t* e = r->extents;
+  const tiler_rt::Target t = target_of(ctx);
+  tiler_rt::Program p;
+  tiler_hip_status st;
+  switch (r->program) {
+    case TILER_HIP_PROGRAM_POINTWISE: {
+      float a, b;
+      std::memcpy(&a, &r->scalars[0], 4);
+      std::memcpy(&b, &r->scalars[1], 4);
+      st = tiler_rt::plan_map(tiler_rt::Mode::Realized, r->variant, r->dtype, bc ? 1 : 0, e[0], a, b, addr, p);
+      break;
+    }
+    case TILER_HIP_PROGRAM_SERIAL_SUM: {
+      if (r->dtype != TILER_HIP_F32) {
+        st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the serial sum is an f32 family");
+        break;
+      }
+      tiler_hip_sum_plan sp;
+      std::memset(&sp, 0, sizeof(sp));
+      sp.topology = r->topology;
+      sp.participant_major = (r->flags & TILER_HIP_REGION_PARTICIPANT_MAJOR) ? 1u : 0u;
+      if (r->topology == TILER_HIP_SUM_MULTIPASS) {
+        sp.partitions = r->grouping[0];
+        sp.per_partition = r->grouping[1];
+      } else if (r->topology == TILER_HIP_SUM_COOPERATIVE) {
+        sp.participants = r->grouping[0];
+        sp.per_partition = r->grouping[1];
+        sp.rounds = r->grouping[2];
+      }
+      st = tiler_rt::plan_sum_f32(t, e[0], e[1], sp, addr, p);
+      break;
+    }
+    case TILER_HIP_PROGRAM_RMS_NORM:
+      st = tiler_rt::plan_rms_norm(r->dtype, bc ? 1 : 0, e[0], e[1], r->scalars[0], addr, p);
+      break;
+    case TILER_HIP_PROGRAM_SOFTMAX:
+      st = r->dtype == TILER_HIP_F32 ? tiler_rt::plan_softmax_f32(e[0], e[1], addr, p)
+                                     : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "softmax is an f32 family");
+      break;
+    case TILER_HIP_PROGRAM_CONTRACTION:
+      if (r->dtype == TILER_HIP_F32)
+        st = r->variant == TILER_HIP_EPILOGUE_NONE
+                 ? tiler_rt::plan_contract_strict_f32(e[0], e[1], e[2], p)
+                 : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the strict f32 contraction has no epilogue");
+      else if (r->dtype == TILER_HIP_BF16)
+        st = tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p);
+      else
+        st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "contraction dtype");
+      break;
+    case TILER_HIP_PROGRAM_GATHER:
+      st = tiler_rt::plan_gather(tiler_rt::Mode::Realized, e[0], e[1], e[2], r->variant, e[3],
+                                 (r->flags & TILER_HIP_REGION_INDEX_SIGNED) ? 1 : 0, addr, p);
+      break;
+    case TILER_HIP_PROGRAM_BROADCAST:
+      st = tiler_rt::plan_broadcast(r->grouping[0], r->rank, r->extents, r->strides, r->variant, p);
+      break;
+    default:
+      st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "no realization for this scalar program");
   }
-  // The staged path addresses each operand panel (up to 256 rows) through one
-  // buffer resource with 32-bit offsets (256 * k * 2 bytes must stay below
-  // 2^31) and moves 16-byte rows: n and k multiples of 8, aligned operands.
-  // 256-tiles when they fill every CU, 128-tiles (four times as many) when not.
-  if (n % 8 == 0 && k % 8 == 0 && k * 512ull < (1ull << 31) && aligned16(a) && aligned16(b) &&
-      aligned16(c)) {
-    const uint64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
-    const uint64_t t128 = ((m + 127) / 128) * ((n + 127) / 128);
-    const bool big = t256 >= ctx->compute_units;
-    const uint64_t tiles = big ? t256 : t128;
-    if (tiles <= 0x7fffffffull) {
-      const bool silu = epilogue == TILER_HIP_EPILOGUE_SILU;
-      const char* name = big ? (silu ? "tiler_contract_bf16_silu_t256" : "tiler_contract_bf16_t256")
-                             : (silu ? "tiler_contract_bf16_silu_t128" : "tiler_contract_bf16_t128");
-      void* args[] = {&a, &b, &m32, &n32, &k32, &c};
-      return launch(ctx, name, (uint32_t)tiles, 1, big ? 1024 : 256, pick(ctx, stream), args);
+  if (st != TILER_HIP_OK) {
+    copy_text(diagnostic, diagnostic_bytes, p.diag);
+    return st;
+  }
+  out->slot_count = p.nslots;
+  for (uint32_t i = 0; i < p.nslots; ++i) {
+    out->slot_roles[i] = p.slot_roles[i];
+    out->slot_bytes[i] = p.slot_bytes[i];
+  }
+  out->slot_alignment = al ? 16 : 1;
+  for (uint32_t i = 0; i < p.nlaunches; ++i) {
+    const tiler_rt::Launch& l = p.launches[i];
+    tiler_hip_realized_entry& d = out->entries[i];
+    uint32_t idx = kEntryCount;
+    for (uint32_t k = 0; k < kEntryCount; ++k)
+      if (std::strcmp(kEntries[k].symbol, l.symbol) == 0) idx = k;
+    if (idx == kEntryCount || l.overflow) {
+      copy_text(diagnostic, diagnostic_bytes, std::string("no payload entry for ") + l.symbol);
+      std::memset(out, 0, sizeof(*out));
+      return TILER_HIP_REFUSE_ABSENT_SYMBOL;
+    }
+    d.entry = idx;
+    d.grid[0] = l.grid[0];
+    d.grid[1] = l.grid[1];
+    d.grid[2] = 1;
+    d.block[0] = l.block;
+    d.block[1] = d.block[2] = 1;
+    d.kernarg_bytes = l.kernarg_bytes;
+    std::memcpy(d.kernargs, l.kernargs, l.kernarg_bytes);
+    d.binding_count = l.nbindings;
+    for (uint32_t b = 0; b < l.nbindings; ++b) {
+      d.binding_slots[b] = l.bindings[b].slot;
+      d.binding_offsets[b] = l.bindings[b].offset;
     }
   }
-  bool full = k % 8 == 0 && aligned16(a) && aligned16(b);
-  const char* name = epilogue == TILER_HIP_EPILOGUE_SILU
-                         ? (full ? "tiler_contract_bf16_silu_g128" : "tiler_contract_bf16_silu_g128_k")
-                         : (full ? "tiler_contract_bf16_g128" : "tiler_contract_bf16_g128_k");
-  void* args[] = {&a, &b, &m32, &n32, &k32, &c};
-  return launch(ctx, name, (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 256,
-                pick(ctx, stream), args);
+  out->entry_count = p.nlaunches;
+  return TILER_HIP_OK;
 }
 
 }  // extern "C"

@@ -1,0 +1,176 @@
+"""The realization recognizer and the RuntimeAdapter route over its result.
+
+`realize` asks the C ABI (`tiler_hip_realize`) which of the library's entry
+points realize one scheduled region, and with what launch geometry and
+argument segment. The region names:
+- the ScalarProgram (tiler-ir/src/schedule/model.rs:661-930);
+- the ReductionTopology (model.rs:1327-1555);
+- the geometry.
+
+The answer is the same program the family entry point runs for that request.
+
+`route` then executes a realization the way
+`route_with_adapter` drives a RuntimeAdapter (tiler-runtime/src/adapter.rs:
+545-678):
+1. Prepare the payload's entries for the symbols it names (cached per
+   context).
+2. Plan the dispatch, acquiring nothing.
+3. Check the caller's storage against the slot sizes and the alignment the
+   realization assumed.
+4. Allocate scratch after the commit.
+5. Dispatch.
+6. Release the scratch.
+
+Every refusal raises before anything is committed. A gather's
+out-of-range record raises `GatherIndexOutOfBounds` as a post-commit failure.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+from . import _lib as L
+from .runtime import GatherIndexOutOfBounds, Refusal, _raise
+
+
+@dataclass
+class RealizedDispatch:
+    symbol: str
+    family: str
+    grid: tuple
+    block: tuple
+    bindings: list  # (slot, byte offset of the pointer field)
+
+
+@dataclass
+class Realization:
+    program: int
+    raw: L.Realization
+    slots: list = field(default_factory=list)  # (role, bytes)
+    alignment: int = 1
+    dispatches: list = field(default_factory=list)
+
+    @property
+    def symbols(self) -> list:
+        return [d.symbol for d in self.dispatches]
+
+
+def _entry_info(index: int):
+    info = L.EntryInfo()
+    _raise(L.lib().tiler_hip_payload_entry(index, ctypes.byref(info)), "payload_entry")
+    return info.symbol.decode(), info.family.decode()
+
+
+def realize(program: int, extents, *, dtype: int = L.F32, topology: int = 0, variant: int = 0,
+            flags: int = L.REGION_ALIGNED16, rank: int = 0, strides=(), grouping=(), scalars=(),
+            ctx=None) -> Realization:
+    """Realizes one region.  `ctx` (a runtime.Context) lets the bound device's
+    CU count decide tile sizes and groupings; without it the declared
+    profile's does (the call is then device-free)."""
+    r = L.Region()
+    r.program, r.topology, r.dtype, r.variant, r.flags, r.rank = program, topology, dtype, variant, flags, rank
+    for i, v in enumerate(extents):
+        r.extents[i] = int(v)
+    for i, v in enumerate(strides):
+        r.strides[i] = int(v)
+    for i, v in enumerate(grouping):
+        r.grouping[i] = int(v)
+    for i, v in enumerate(scalars):
+        r.scalars[i] = int(v)
+    out = L.Realization()
+    diag = ctypes.create_string_buffer(256)
+    st = L.lib().tiler_hip_realize(ctx.handle if ctx is not None else None, ctypes.byref(r), ctypes.byref(out),
+                                   diag, 256)
+    _raise(st, "realize", diag.value.decode())
+    res = Realization(program=program, raw=out, alignment=out.slot_alignment,
+                      slots=[(out.slot_roles[i], out.slot_bytes[i]) for i in range(out.slot_count)])
+    for i in range(out.entry_count):
+        e = out.entries[i]
+        symbol, family = _entry_info(e.entry)
+        res.dispatches.append(RealizedDispatch(
+            symbol, family, tuple(e.grid), tuple(e.block),
+            [(e.binding_slots[b], e.binding_offsets[b]) for b in range(e.binding_count)]))
+    return res
+
+
+def _payload_code():
+    v = L.PayloadView()
+    _raise(L.lib().tiler_hip_payload(ctypes.byref(v)), "payload")
+    return ctypes.string_at(v.code, v.code_bytes)
+
+
+def _prepared(ctx, symbol: str) -> int:
+    cache = ctx.__dict__.setdefault("_route_prepared", {})
+    if symbol not in cache:
+        if "_route_code" not in ctx.__dict__:
+            code = _payload_code()
+            ctx._route_code = ctypes.create_string_buffer(code, len(code))
+        entry = L.RoutedEntry(ctypes.cast(ctx._route_code, ctypes.c_void_p), len(ctx._route_code.raw),
+                              symbol.encode())
+        first = ctypes.c_uint32()
+        _raise(L.lib().tiler_hip_prepare_entries(ctx.handle, ctypes.byref(entry), 1, ctypes.byref(first)),
+               f"prepare_entries({symbol})", ctx.diagnostic())
+        cache[symbol] = first.value
+    return cache[symbol]
+
+
+def _address(buf) -> int:
+    if buf is None:
+        return 0
+    return int(buf.ptr) if hasattr(buf, "ptr") else int(buf)
+
+
+def _capacity(buf):
+    return getattr(buf, "nbytes", None)
+
+
+def route(ctx, realization: Realization, storage) -> None:
+    """Executes `realization` on `ctx`'s stream and waits for it.  `storage`
+    lists one device buffer (or address) per slot, in the realization's slot
+    order; scratch slots may be None (allocated here, released after)."""
+    rz = realization
+    if len(storage) != len(rz.slots):
+        raise Refusal(L.REFUSE_BINDING_MISMATCH, "route",
+                      f"{len(storage)} storage bindings for {len(rz.slots)} slots")
+    if rz.raw.entry_count == 0:
+        return  # zero work: the dispatch is skipped
+    for i, ((role, nbytes), buf) in enumerate(zip(rz.slots, storage)):
+        if buf is None:
+            if role != L.SLOT_SCRATCH:
+                raise Refusal(L.REFUSE_BINDING_MISMATCH, "route", f"slot {i} needs caller storage")
+            continue
+        cap = _capacity(buf)
+        if cap is not None and cap < nbytes:
+            raise Refusal(L.REFUSE_BINDING_MISMATCH, "route", f"slot {i} holds {cap} of {nbytes} bytes")
+        if _address(buf) % rz.alignment:
+            raise Refusal(L.REFUSE_BINDING_MISMATCH, "route",
+                          f"slot {i} is not {rz.alignment}-byte aligned as the realization assumed")
+    n = rz.raw.entry_count
+    entries = (L.DispatchEntry * n)()
+    keep = []
+    for i in range(n):
+        e = rz.raw.entries[i]
+        slots = (ctypes.c_uint32 * max(1, e.binding_count))(*e.binding_slots[:e.binding_count])
+        offs = (ctypes.c_uint32 * max(1, e.binding_count))(*e.binding_offsets[:e.binding_count])
+        kernargs = ctypes.create_string_buffer(bytes(e.kernargs[:e.kernarg_bytes]), max(1, e.kernarg_bytes))
+        keep += [slots, offs, kernargs]
+        entries[i] = L.DispatchEntry(_prepared(ctx, rz.dispatches[i].symbol), e.grid, e.block, 0,
+                                     ctypes.cast(kernargs, ctypes.c_void_p), e.kernarg_bytes,
+                                     e.binding_count, slots, offs)
+    slot_bytes = (ctypes.c_uint64 * len(rz.slots))(*[b for _, b in rz.slots])
+    plan = L.DispatchPlan(len(rz.slots), slot_bytes, n, entries)
+    h = ctx.handle
+    _raise(L.lib().tiler_hip_plan_dispatch(h, ctypes.byref(plan)), "plan_dispatch", ctx.diagnostic())
+    ptrs = (ctypes.c_void_p * len(rz.slots))(*[_address(b) or None for b in storage])
+    owned = (ctypes.c_void_p * len(rz.slots))(*[None if b is None else 1 for b in storage])
+    _raise(L.lib().tiler_hip_allocate_dispatch(h, ctypes.byref(plan), ptrs), "allocate_dispatch",
+           ctx.diagnostic())
+    try:
+        _raise(L.lib().tiler_hip_dispatch(h, ctypes.byref(plan), ptrs), "dispatch", ctx.diagnostic())
+        if rz.program == L.PROGRAM_GATHER:
+            rec = ctypes.c_uint64()
+            _raise(L.lib().tiler_hip_download(h, ctypes.byref(rec), ptrs[3], 8), "read gather record")
+            if rec.value != 0xFFFFFFFFFFFFFFFF:
+                raise GatherIndexOutOfBounds(L.FAIL_GATHER_INDEX_OUT_OF_BOUNDS, rec.value)
+    finally:
+        L.lib().tiler_hip_release_dispatch(h, ctypes.byref(plan), ptrs, owned)
