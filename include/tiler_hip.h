@@ -92,8 +92,8 @@ tiler_hip_status tiler_hip_profile_declare(tiler_hip_target_profile *out);
 /* ------------------------------------------------------------------------
  * Producer seam (tiler-build/src/plan_artifact.rs:228-363 assemble_plan_artifact
  * closures; tiler-metal-aot/src/driver.rs:61-453 Toolchain).  The gfx950 code
- * object is compiled offline by hipcc --genco and carried in this library; the
- * payload view describes it the way PayloadMetadata/PayloadProvenance do
+ * object is compiled offline (clang --offload-device-only) and carried in this
+ * library; the payload view describes it the way PayloadMetadata/PayloadProvenance do
  * (tiler-artifact/src/codec/payload.rs:228-424).  Device-free.
  */
 typedef struct {
@@ -106,6 +106,10 @@ typedef struct {
     const uint8_t *code;          /* code-object bytes (ELF) */
     uint64_t code_bytes;
     uint32_t entry_count;
+    const uint8_t *source;        /* the kernel sources compiled: the build's source bundle
+                                     (file count, then each path and contents, u64 big-endian
+                                     lengths) */
+    uint64_t source_bytes;
 } tiler_hip_payload_view;
 
 typedef struct {
@@ -117,6 +121,30 @@ typedef struct {
 
 tiler_hip_status tiler_hip_payload(tiler_hip_payload_view *out);
 tiler_hip_status tiler_hip_payload_entry(uint32_t index, tiler_hip_entry_info *out);
+
+/* The payload's compilation subject, PayloadMetadata, in the artifact layer's
+ * canonical encoding (tiler-artifact/src/program/codec/payload.rs:477-580).
+ * Every field is an input to the compilation:
+ *   - source: the source bundle above;
+ *   - toolchain, target, family and language;
+ *   - compiler version, the ordered compile flags;
+ *   - one entry per kernel: key and symbol, and transports 0..buffers-1;
+ *   - two target obligations;
+ *   - the unversioned-platform tag.
+ * Writes up to `capacity` bytes; *required receives the full length (call
+ * with out NULL to size it).  TILER_HIP_REFUSE_CAPACITY if it does not fit. */
+tiler_hip_status tiler_hip_payload_metadata(uint8_t *out, uint64_t capacity, uint64_t *required);
+/* payload_identity (payload.rs:455-461): the governed digest of those bytes
+ * under "tiler.artifact-envelope.payload-identity.v1\0" -- the digest a
+ * DeclaredPayload states (tiler-build/tests/custom_backend/backend.rs:451-530). */
+tiler_hip_status tiler_hip_payload_identity(uint8_t out[32]);
+/* The governed content digest (tiler-digest/src/lib.rs:168-240; algorithm tag
+ * 0x01, "tiler.digest.sha-256.v1"): FIPS 180-4 SHA-256 of the domain, then
+ * each qualifier in order (fixed width by contract), then the byte run. */
+tiler_hip_status tiler_hip_digest(const void *domain, uint64_t domain_bytes,
+                                  const void *const *qualifiers, const uint64_t *qualifier_bytes,
+                                  uint32_t qualifier_count, const void *bytes, uint64_t byte_count,
+                                  uint8_t out[32]);
 
 /* Validates a code object from its own bytes (ADR 0090 item 8;
  * RuntimeAdapter::validate_payload, tiler-runtime/src/adapter.rs:341):

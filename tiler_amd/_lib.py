@@ -106,6 +106,8 @@ class PayloadView(ctypes.Structure):
         ("code", ctypes.c_void_p),
         ("code_bytes", ctypes.c_uint64),
         ("entry_count", ctypes.c_uint32),
+        ("source", ctypes.c_void_p),
+        ("source_bytes", ctypes.c_uint64),
     ]
 
 
@@ -275,6 +277,9 @@ SIGNATURES = {
     "tiler_hip_contract_bf16": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _U32, _P]),
     "tiler_hip_realize": (_S, [_CTX, ctypes.POINTER(Region), ctypes.POINTER(Realization),
                                ctypes.c_char_p, _U64]),
+    "tiler_hip_payload_metadata": (_S, [_P, _U64, ctypes.POINTER(_U64)]),
+    "tiler_hip_payload_identity": (_S, [_P]),
+    "tiler_hip_digest": (_S, [_P, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64), _U32, _P, _U64, _P]),
 }
 
 _lib = None

@@ -53,9 +53,15 @@ def build(verbose: bool = False) -> str:
         fh.write("#pragma once\n")
         fh.write(f"#define TILER_HIP_BUILD_TOOLCHAIN {_c_string(_toolchain_identity())}\n")
         fh.write(f"#define TILER_HIP_BUILD_FLAGS {_c_string(flags)}\n")
+        fh.write("#define TILER_HIP_BUILD_FLAG_LIST " + ", ".join(_c_string(f) for f in DEVICE_FLAGS) + "\n")
+        fh.write(f"#define TILER_HIP_BUILD_FLAG_COUNT {len(DEVICE_FLAGS)}\n")
+    bundle = os.path.join(BUILD, "source_bundle.bin")
+    with open(bundle + ".tmp", "wb") as fh:
+        fh.write(source_bundle())
+    os.replace(bundle + ".tmp", bundle)
 
     payload_obj = os.path.join(BUILD, "payload.o")
-    _run(["gcc", "-c", f'-DTILER_HSACO_PATH="{HSACO}"', "-o", payload_obj,
+    _run(["gcc", "-c", f'-DTILER_HSACO_PATH="{HSACO}"', f'-DTILER_SOURCE_BUNDLE_PATH="{bundle}"', "-o", payload_obj,
           os.path.join(CSRC, "runtime", "payload.S")])
     tmp_lib = LIB + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
@@ -63,6 +69,7 @@ def build(verbose: bool = False) -> str:
           "-o", tmp_lib,
           os.path.join(CSRC, "runtime", "tiler_hip.cpp"),
           os.path.join(CSRC, "runtime", "program.cpp"),
+          os.path.join(CSRC, "runtime", "digest.cpp"),
           os.path.join(CSRC, "runtime", "code_object.cpp"),
           payload_obj,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])
@@ -70,6 +77,23 @@ def build(verbose: bool = False) -> str:
     if verbose:
         print(f"built {LIB}")
     return LIB
+
+
+def source_bundle() -> bytes:
+    """The exact kernel sources the code object is compiled from, as one
+    canonical byte run: the file count, then each file's path (relative to
+    csrc/kernels, sorted) and contents, every run preceded by its length as a
+    u64 big-endian (the identity framing of tiler-ir/src/identity.rs:84-111).
+    The payload metadata carries it as the compiled source."""
+    kdir = os.path.join(CSRC, "kernels")
+    names = sorted(f for f in os.listdir(kdir) if f.endswith((".hip", ".h")))
+    out = bytearray(len(names).to_bytes(8, "big"))
+    for name in names:
+        with open(os.path.join(kdir, name), "rb") as fh:
+            body = fh.read()
+        for run in (name.encode(), body):
+            out += len(run).to_bytes(8, "big") + run
+    return bytes(out)
 
 
 def _c_string(s: str) -> str:

@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -15,10 +16,13 @@
 
 #include "build_info.h"
 #include "code_object.h"
+#include "digest.h"
 #include "program.h"
 
 extern "C" const uint8_t tiler_hip_code_object[];
 extern "C" const uint8_t tiler_hip_code_object_end[];
+extern "C" const uint8_t tiler_hip_source_bundle[];
+extern "C" const uint8_t tiler_hip_source_bundle_end[];
 
 namespace {
 
@@ -313,6 +317,103 @@ tiler_hip_status tiler_hip_payload(tiler_hip_payload_view* out) {
   out->code = tiler_hip_code_object;
   out->code_bytes = code_object_bytes();
   out->entry_count = kEntryCount;
+  out->source = tiler_hip_source_bundle;
+  out->source_bytes = (uint64_t)(tiler_hip_source_bundle_end - tiler_hip_source_bundle);
+  return TILER_HIP_OK;
+}
+
+// The payload's compilation subject in the artifact layer's canonical
+// PayloadMetadata encoding (tiler-artifact/src/program/codec/payload.rs:
+// 477-580): versioned domain, schema (1, 0) as u16 big-endian, then every
+// variable-length run and collection preceded by its u64 big-endian length.
+// Field order: source representation, source, toolchain, target, family,
+// language, deployment major/minor (u16), components (role, version), SDK
+// name/version/build, compile flags, link flags, entries (key, symbol,
+// transports as u32), obligations (key, value); the unversioned platform
+// appends its tag 0x00.  This payload states no SDK and no deployment
+// minimum, like the reference's own unversioned backend
+// (tiler-build/tests/custom_backend/backend.rs:420-438).
+namespace {
+
+constexpr char kPayloadMetadataDomain[] = "tiler.artifact-envelope.payload-metadata.v1\0";
+constexpr char kPayloadIdentityDomain[] = "tiler.artifact-envelope.payload-identity.v1\0";
+
+const std::vector<uint8_t>& payload_metadata_bytes() {
+  static const std::vector<uint8_t> bytes = [] {
+    using namespace tiler_rt;
+    std::vector<uint8_t> b;
+    b.insert(b.end(), kPayloadMetadataDomain, kPayloadMetadataDomain + sizeof(kPayloadMetadataDomain) - 1);
+    push_u16(b, 1);
+    push_u16(b, 0);
+    push_str(b, "tiler.hip.source-bundle.v1");
+    push_slice(b, tiler_hip_source_bundle, (uint64_t)(tiler_hip_source_bundle_end - tiler_hip_source_bundle));
+    push_str(b, "tiler.hip.rocm-clang");
+    push_str(b, kTarget);
+    push_str(b, kBackend);
+    push_str(b, "hip-c++17");
+    push_u16(b, 0);  // deployment major: none (unversioned)
+    push_u16(b, 0);  // deployment minor
+    push_len(b, 1);  // components, in role order
+    push_str(b, "compiler");
+    push_str(b, TILER_HIP_BUILD_TOOLCHAIN);
+    push_str(b, "");  // SDK name, version, build: none
+    push_str(b, "");
+    push_str(b, "");
+    static const char* const flags[] = {TILER_HIP_BUILD_FLAG_LIST};
+    push_len(b, TILER_HIP_BUILD_FLAG_COUNT);
+    for (const char* f : flags) push_str(b, f);
+    push_len(b, 0);  // link flags: the code object is not linked
+    std::vector<uint32_t> order(kEntryCount);
+    for (uint32_t i = 0; i < kEntryCount; ++i) order[i] = i;
+    std::sort(order.begin(), order.end(),
+              [](uint32_t x, uint32_t y) { return std::strcmp(kEntries[x].symbol, kEntries[y].symbol) < 0; });
+    push_len(b, kEntryCount);  // entries, in entry-key order; the key is the symbol
+    for (uint32_t i : order) {
+      push_str(b, kEntries[i].symbol);
+      push_str(b, kEntries[i].symbol);
+      push_len(b, kEntries[i].buffers);
+      for (uint32_t t = 0; t < kEntries[i].buffers; ++t) push_u32(b, t);
+    }
+    push_len(b, 2);  // obligations, in key order
+    push_str(b, "tiler.hip.target-arch");
+    push_str(b, "gfx950");
+    push_str(b, "tiler.hip.wavefront-size");
+    push_str(b, "64");
+    b.push_back(0x00);  // PayloadPlatform::Unversioned
+    return b;
+  }();
+  return bytes;
+}
+
+}  // namespace
+
+tiler_hip_status tiler_hip_payload_metadata(uint8_t* out, uint64_t capacity, uint64_t* required) {
+  const std::vector<uint8_t>& m = payload_metadata_bytes();
+  if (required) *required = m.size();
+  if (!out) return required ? TILER_HIP_OK : TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (capacity < m.size()) return TILER_HIP_REFUSE_CAPACITY;
+  std::memcpy(out, m.data(), m.size());
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_payload_identity(uint8_t* out) {
+  if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  const std::vector<uint8_t>& m = payload_metadata_bytes();
+  tiler_rt::governed_digest(kPayloadIdentityDomain, sizeof(kPayloadIdentityDomain) - 1, nullptr, nullptr, 0,
+                            m.data(), m.size(), out);
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_digest(const void* domain, uint64_t domain_bytes, const void* const* qualifiers,
+                                  const uint64_t* qualifier_bytes, uint32_t qualifier_count,
+                                  const void* bytes, uint64_t byte_count, uint8_t* out) {
+  if (!out || (domain_bytes && !domain) || (byte_count && !bytes) ||
+      (qualifier_count && (!qualifiers || !qualifier_bytes)))
+    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  for (uint32_t i = 0; i < qualifier_count; ++i)
+    if (qualifier_bytes[i] && !qualifiers[i]) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::governed_digest(domain, domain_bytes, qualifiers, qualifier_bytes, qualifier_count, bytes,
+                            byte_count, out);
   return TILER_HIP_OK;
 }
 
