@@ -346,7 +346,45 @@ class Contract(Workload):
                           "single thread; extrapolated per row"}
 
 
-WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, Gather, Contract)}
+class Convert(Workload):
+    """The binary32 -> bf16 narrowing family (ADR 0091 decision 2) over
+    f32[2^26]: not a BASELINE config, measured as a family of its own."""
+    name = "convert"
+    kernel = "tiler_narrow_f32_bf16_v8"
+    n = 1 << 26
+    sets = 2  # 2 x 384 MiB touched per sweep
+
+    def config(self):
+        return {"workload": "narrow f32[2^26] ~N(0,1) -> bf16 (RNE, canonical NaN)", "buffer_sets": self.sets}
+
+    def work(self):  # algorithmic bytes per launch
+        return self.n * 4 + self.n * 2
+
+    def setup(self):
+        from tiler_amd import _lib as L
+        self.L = L
+        rng = np.random.default_rng(6)
+        self.sets_ = [self._keep(self.ctx.to_device(rng.standard_normal(self.n, dtype=np.float32)),
+                                 self.ctx.alloc(self.n * 2)) for _ in range(self.sets)]
+        return self.sets
+
+    def launch(self, i):
+        x, y = self.sets_[i % self.sets]
+        self.ctx.convert(self.L.CONVERT_NARROW_F32_BF16, x, self.n, y)
+
+    def cpu_baseline(self, budget_s):
+        import oracle
+        x = np.random.default_rng(6).standard_normal(1 << 22, dtype=np.float32)
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s:
+            oracle.bf16_narrow(x)
+            done += x.size
+        el = time.perf_counter() - t0
+        return {"value": done * 6 / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done} elements of the oracle's narrowing in {el:.1f} s, single thread"}
+
+
+WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, Gather, Contract, Convert)}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_all_families.md")

@@ -385,6 +385,17 @@ tiler_hip_status tiler_hip_validate_gather_index(const uint32_t *index, uint64_t
                                                  int32_t index_signed, uint64_t gathered,
                                                  uint64_t *bad_position, int64_t *bad_value);
 
+/* bf16 <-> binary32 conversion, one typed family per direction (ADR 0091
+ * decision 2; docs/decisions/0091-...md).  NARROW: binary32 -> bf16, round to
+ * nearest even, overflow to a signed infinity at the inclusive midpoint above
+ * the largest finite bf16, every NaN -> 0x7fc0, gradual underflow, signed zero
+ * kept.  WIDEN: bf16 -> binary32, exact and total (a NaN keeps its payload).
+ * n elements; src and dst must not overlap. */
+#define TILER_HIP_CONVERT_NARROW_F32_BF16 0
+#define TILER_HIP_CONVERT_WIDEN_BF16_F32 1
+tiler_hip_status tiler_hip_convert(tiler_hip_context *ctx, uint32_t direction, const void *src,
+                                   uint64_t n, void *dst, tiler_hip_stream stream);
+
 /* Contraction td,od->to: C[m, n] = sum_k A[m, k] * B[n, k]
  * (tensor-contraction-f32@1; tiler-reference/src/contraction.rs:297-630). */
 /* Strict f32: bit-exact with the reference's fold (first-product seed, no FMA). */
@@ -426,6 +437,7 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context *ctx, const uint16_t 
 #define TILER_HIP_PROGRAM_CONTRACTION 5 /* ::StrictTensorContraction (model.rs:850) */
 #define TILER_HIP_PROGRAM_GATHER 6      /* tiler-reference/src/structural.rs:513-606 */
 #define TILER_HIP_PROGRAM_BROADCAST 7   /* tiler-reference/src/structural.rs:75-108 */
+#define TILER_HIP_PROGRAM_CONVERT 8     /* the ADR 0091 conversion families; variant: TILER_HIP_CONVERT_* */
 
 /* Region flags. */
 #define TILER_HIP_REGION_ALIGNED16 1u         /* precondition: every slot's base address is 16-byte aligned */
@@ -438,10 +450,11 @@ typedef struct {
     uint32_t topology;     /* serial sum: TILER_HIP_SUM_* */
     uint32_t dtype;        /* TILER_HIP_F32 / TILER_HIP_BF16 */
     uint32_t variant;      /* pointwise: TILER_HIP_MAP_*; contraction (bf16): TILER_HIP_EPILOGUE_*;
+                              convert: TILER_HIP_CONVERT_*;
                               gather, broadcast: element bytes */
     uint32_t flags;        /* TILER_HIP_REGION_* */
     uint32_t rank;         /* broadcast: output rank (<= 8) */
-    uint64_t extents[8];   /* pointwise {n}; sum, rms_norm, softmax {rows, extent};
+    uint64_t extents[8];   /* pointwise, convert {n}; sum, rms_norm, softmax {rows, extent};
                               contraction {m, n, k}; gather {outer, gathered, inner, index count};
                               broadcast: the output dims */
     uint64_t strides[8];   /* broadcast: source stride (elements) per output axis */
@@ -460,7 +473,8 @@ typedef struct {
  *   gather      source, index, out, record (scratch: u64, all ones unless an index was
  *               out of range; then the lowest such position).  The program arms the
  *               record itself; validate host indices first (tiler_hip_validate_gather_index).
- *   broadcast   src, out */
+ *   broadcast   src, out
+ *   convert     src, dst */
 #define TILER_HIP_SLOT_INPUT 0
 #define TILER_HIP_SLOT_OUTPUT 1
 #define TILER_HIP_SLOT_SCRATCH 2

@@ -140,6 +140,20 @@ def test_moves_and_maps():
     assert silu.symbols == ["tiler_map_f32_v4_op1"] and len(silu.slots) == 2
 
 
+def test_conversion_families():
+    n = realize(L.PROGRAM_CONVERT, (1 << 20,), variant=L.CONVERT_NARROW_F32_BF16)
+    assert n.symbols == ["tiler_narrow_f32_bf16_v8"]
+    assert n.slots == [(L.SLOT_INPUT, 4 << 20), (L.SLOT_OUTPUT, 2 << 20)]
+    _check_segments(n)
+    w = realize(L.PROGRAM_CONVERT, (1 << 20,), variant=L.CONVERT_WIDEN_BF16_F32)
+    assert w.symbols == ["tiler_widen_bf16_f32_v8"] and w.slots[1] == (L.SLOT_OUTPUT, 4 << 20)
+    assert realize(L.PROGRAM_CONVERT, (1001,), variant=L.CONVERT_WIDEN_BF16_F32).symbols == ["tiler_widen_bf16_f32"]
+    assert realize(L.PROGRAM_CONVERT, (1024,), variant=L.CONVERT_NARROW_F32_BF16, flags=0).symbols == \
+        ["tiler_narrow_f32_bf16"]
+    with pytest.raises(Refusal):
+        realize(L.PROGRAM_CONVERT, (8,), variant=7)
+
+
 def test_zero_work_skips_dispatch():
     assert realize(L.PROGRAM_SOFTMAX, (0, 2048)).raw.entry_count == 0
     assert realize(L.PROGRAM_CONTRACTION, (0, 64, 64), dtype=L.BF16).raw.entry_count == 0

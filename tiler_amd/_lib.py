@@ -57,6 +57,10 @@ PROGRAM_SOFTMAX = 4
 PROGRAM_CONTRACTION = 5
 PROGRAM_GATHER = 6
 PROGRAM_BROADCAST = 7
+PROGRAM_CONVERT = 8
+
+CONVERT_NARROW_F32_BF16 = 0
+CONVERT_WIDEN_BF16_F32 = 1
 
 REGION_ALIGNED16 = 1
 REGION_OPERAND_BROADCAST = 2
@@ -270,6 +274,7 @@ SIGNATURES = {
     "tiler_hip_broadcast": (_S, [_CTX, _P, _U64, _U32, ctypes.POINTER(_U64), ctypes.POINTER(_U64),
                                  _U32, _P, _P]),
     "tiler_hip_gather": (_S, [_CTX, _P, _U64, _U64, _U64, _U32, _P, _U64, _I32, _P, _P]),
+    "tiler_hip_convert": (_S, [_CTX, _U32, _P, _U64, _P, _P]),
     "tiler_hip_gather_status": (_S, [_CTX, _P, ctypes.POINTER(_U64)]),
     "tiler_hip_validate_gather_index": (_S, [_P, _U64, _I32, _U64, ctypes.POINTER(_U64),
                                              ctypes.POINTER(ctypes.c_int64)]),

@@ -6,4 +6,5 @@
 #include "rows_long.hip"
 #include "gather.hip"
 #include "map.hip"
+#include "convert.hip"
 #include "contract.hip"

@@ -344,6 +344,31 @@ tiler_hip_status plan_gather(Mode mode, uint64_t outer, uint64_t gathered, uint6
 }
 
 // ---------------------------------------------------------------------------
+// bf16 <-> binary32 conversion families.  Slots: 0 src, 1 dst.  Like the maps:
+// the 16-byte vector kernel over the aligned head of whole 8-element groups,
+// the scalar kernel for the rest (realized: one kernel over all n).
+tiler_hip_status plan_convert(Mode mode, uint32_t direction, uint64_t n, const uintptr_t* addr,
+                              Program& p) {
+  if (direction != TILER_HIP_CONVERT_NARROW_F32_BF16 && direction != TILER_HIP_CONVERT_WIDEN_BF16_F32)
+    return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "conversion direction");
+  const bool narrow = direction == TILER_HIP_CONVERT_NARROW_F32_BF16;
+  const uint64_t in_b = narrow ? 4 : 2, out_b = narrow ? 2 : 4;
+  const uint32_t src = p.slot(mul_sat(n, in_b), kSlotInput);
+  const uint32_t dst = p.slot(mul_sat(n, out_b), kSlotOutput);
+  if (n == 0) return TILER_HIP_OK;
+  uint64_t head = aligned16(addr[src]) && aligned16(addr[dst]) ? n / 8 * 8 : 0;
+  if (mode == Mode::Realized && head != n) head = 0;
+  if (head) {
+    p.add(narrow ? "tiler_narrow_f32_bf16_v8" : "tiler_widen_bf16_f32_v8", blocks_capped(head / 8, 8192), 1, 256)
+        .ptr(src).u64(head / 8).ptr(dst);
+    if (head == n) return TILER_HIP_OK;
+  }
+  p.add(narrow ? "tiler_narrow_f32_bf16" : "tiler_widen_bf16_f32", blocks_capped(n - head, 8192), 1, 256)
+      .ptr(src, head * in_b).u64(n - head).ptr(dst, head * out_b);
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Contractions.  Slots: 0 a [m, k], 1 b [n, k], 2 c [m, n].
 tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p) {
   const uint32_t a = p.slot(mul_sat(mul_sat(m, k), 4), kSlotInput);

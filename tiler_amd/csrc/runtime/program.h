@@ -107,6 +107,8 @@ tiler_hip_status plan_broadcast(uint64_t src_elements, uint32_t rank, const uint
 tiler_hip_status plan_gather(Mode mode, uint64_t outer, uint64_t gathered, uint64_t inner,
                              uint32_t element_bytes, uint64_t count, int32_t index_signed,
                              const uintptr_t* addr, Program& p);
+tiler_hip_status plan_convert(Mode mode, uint32_t direction, uint64_t n, const uintptr_t* addr,
+                              Program& p);
 tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p);
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
                                     uint32_t epilogue, const uintptr_t* addr, Program& p);

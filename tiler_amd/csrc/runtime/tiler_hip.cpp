@@ -152,6 +152,10 @@ const EntryRow kEntries[] = {
     {"tiler_broadcast_rows_u32", "broadcast", 2},
     {"tiler_broadcast_rows_u16", "broadcast", 2},
     {"tiler_fill_u32", "fill", 1},
+    {"tiler_narrow_f32_bf16_v8", "convert-f32-to-bf16/narrow", 2},
+    {"tiler_narrow_f32_bf16", "convert-f32-to-bf16/narrow", 2},
+    {"tiler_widen_bf16_f32_v8", "convert-bf16-to-f32/widen", 2},
+    {"tiler_widen_bf16_f32", "convert-bf16-to-f32/widen", 2},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_bf16_g128", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_g128", "tensor-contraction-bf16/cooperative+silu", 3},
@@ -954,6 +958,18 @@ tiler_hip_status tiler_hip_broadcast(tiler_hip_context* ctx, const void* src, ui
   return run_program(ctx, p, slots, pick(ctx, stream));
 }
 
+tiler_hip_status tiler_hip_convert(tiler_hip_context* ctx, uint32_t direction, const void* src,
+                                   uint64_t n, void* dst, tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  const uintptr_t addr[2] = {(uintptr_t)src, (uintptr_t)dst};
+  tiler_hip_status st = tiler_rt::plan_convert(tiler_rt::Mode::Direct, direction, n, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!src || !dst)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(src), dst};
+  return run_program(ctx, p, slots, pick(ctx, stream));
+}
+
 tiler_hip_status tiler_hip_validate_gather_index(const uint32_t* index, uint64_t count,
                                                  int32_t index_signed, uint64_t gathered,
                                                  uint64_t* bad_position, int64_t* bad_value) {
@@ -1094,6 +1110,9 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
       break;
     case TILER_HIP_PROGRAM_BROADCAST:
       st = tiler_rt::plan_broadcast(r->grouping[0], r->rank, r->extents, r->strides, r->variant, p);
+      break;
+    case TILER_HIP_PROGRAM_CONVERT:
+      st = tiler_rt::plan_convert(tiler_rt::Mode::Realized, r->variant, e[0], addr, p);
       break;
     default:
       st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "no realization for this scalar program");

@@ -145,6 +145,23 @@ def silu_f32(values, ctx=None) -> np.ndarray:
                      lambda c, dx, dy: c.map(L.MAP_SILU, L.F32, dx, x.size, dy))
 
 
+# --- bf16 <-> binary32 conversion (ADR 0091 decision 2) -------------------------
+
+def narrow_f32_bf16(values, ctx=None) -> np.ndarray:
+    """binary32 -> bf16 bit patterns: round to nearest even, overflow to a
+    signed infinity at the inclusive midpoint, every NaN -> 0x7fc0."""
+    x = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    return _run_rows(ctx, x, np.uint16, x.size,
+                     lambda c, dx, dy: c.convert(L.CONVERT_NARROW_F32_BF16, dx, x.size, dy))
+
+
+def widen_bf16_f32(bits, ctx=None) -> np.ndarray:
+    """bf16 bit patterns -> binary32, exactly (a NaN keeps its payload)."""
+    b = np.ascontiguousarray(bits, dtype=np.uint16).reshape(-1)
+    return _run_rows(ctx, b, np.float32, b.size,
+                     lambda c, dx, dy: c.convert(L.CONVERT_WIDEN_BF16_F32, dx, b.size, dy))
+
+
 # --- gather --------------------------------------------------------------------
 
 def gather(source: np.ndarray, axis: int, index: np.ndarray, index_signed: bool = False,

@@ -254,6 +254,11 @@ class Context:
                                                 strides, element_bytes, _ptr(out), stream),
                     "broadcast")
 
+    def convert(self, direction: int, src, n: int, dst, stream=None):
+        """bf16 <-> binary32 conversion (L.CONVERT_NARROW_F32_BF16 / L.CONVERT_WIDEN_BF16_F32)."""
+        self._check(L.lib().tiler_hip_convert(self.handle, direction, _ptr(src), n, _ptr(dst), stream),
+                    "convert")
+
     def gather(self, source, outer: int, gathered: int, inner: int, element_bytes: int, index,
                index_count: int, out, index_signed: bool = False, stream=None):
         self._check(L.lib().tiler_hip_gather(self.handle, _ptr(source), outer, gathered, inner,
