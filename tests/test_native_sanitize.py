@@ -1,0 +1,35 @@
+"""The host-side planners and the governed digest under AddressSanitizer and
+UndefinedBehaviorSanitizer, on the CPU.
+
+Builds tests/native/planner_sanitize.cpp against the runtime's own
+program.cpp and digest.cpp with g++ -fsanitize=address,undefined (no device
+code, no HIP runtime). It runs every planner over random and edge-case
+requests (zero, huge and overflowing extents, unaligned addresses, invalid
+enums) and the digest over random splits. The run must finish clean: no
+sanitizer report, no argument segment overflow, every binding inside its
+segment and naming a declared slot.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+RT = os.path.join(ROOT, "tiler_amd", "csrc", "runtime")
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_planners_and_digest_are_sanitizer_clean(tmp_path):
+    exe = tmp_path / "planner_sanitize"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                    f"-I{os.path.join(ROOT, 'include')}", f"-I{RT}",
+                    os.path.join(ROOT, "tests", "native", "planner_sanitize.cpp"),
+                    os.path.join(RT, "program.cpp"), os.path.join(RT, "digest.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0", UBSAN_OPTIONS="print_stacktrace=1")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "planner-sanitize ok" in r.stdout and "runtime error" not in r.stderr

@@ -62,6 +62,7 @@ void Sha256::compress(const uint8_t* p) {
 }
 
 void Sha256::update(const void* data, uint64_t n) {
+  if (n == 0) return;  // an empty run may come with a null pointer
   const uint8_t* p = static_cast<const uint8_t*>(data);
   total_ += n;
   if (fill_) {
