@@ -124,3 +124,74 @@ def test_maps(ctx, case):
     n = int(r.integers(1, 20000))
     x = (r.standard_normal(n) * 6).astype(np.float32)
     assert np.array_equal(bits(families.silu_f32(x, ctx=ctx)), bits(oracle.silu_f32(x)))
+
+
+def _route_vs_direct(ctx, rz, inputs, out_spec, direct):
+    """Routes a realization with device copies of `inputs`; returns (routed, direct) outputs."""
+    from tiler_amd.realize import route
+    dev_in = [ctx.to_device(a) for a in inputs]
+    out_t, out_n = out_spec
+    dev_out = ctx.alloc(max(1, out_n * np.dtype(out_t).itemsize))
+    storage, k = [], 0
+    for role, _ in rz.slots:
+        if role == L.SLOT_INPUT:
+            storage.append(dev_in[k]); k += 1
+        elif role == L.SLOT_OUTPUT:
+            storage.append(dev_out)
+        else:
+            storage.append(None)
+    try:
+        route(ctx, rz, storage)
+        routed = dev_out.download(out_t, (out_n,))
+    finally:
+        for b in dev_in + [dev_out]:
+            b.free()
+    return routed, np.asarray(direct()).reshape(-1)
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_realized_plans_match_direct_calls(ctx, case):
+    """The recognizer's plan, routed through the runtime seam, reproduces the
+    family entry point bit for bit on random shapes of every family."""
+    from tiler_amd.realize import realize
+    r = _rng(case, 8)
+    fam = case % 6
+    if fam == 0:
+        rows, extent = int(r.integers(1, 9)), int(r.integers(1, 20000))
+        x = oracle.bf16_narrow(r.standard_normal((rows, extent)).astype(np.float32))
+        w = oracle.bf16_narrow(r.normal(1.0, 0.1, extent).astype(np.float32))
+        rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=L.BF16, scalars=(EPS,),
+                     flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=ctx)
+        got, want = _route_vs_direct(ctx, rz, [x, w], (np.uint16, rows * extent),
+                                     lambda: families.rms_norm_bf16(x, w, EPS, ctx=ctx))
+    elif fam == 1:
+        rows, extent = int(r.integers(1, 9)), int(r.integers(1, 20000))
+        x = (r.standard_normal((rows, extent)) * 3).astype(np.float32)
+        rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), ctx=ctx)
+        got, want = _route_vs_direct(ctx, rz, [x], (np.float32, rows * extent),
+                                     lambda: families.softmax_f32((rows, extent), 1, x, ctx=ctx))
+    elif fam == 2:
+        rows, extent = int(r.integers(1, 40)), int(r.integers(1, 5000))
+        x = r.uniform(-1, 1, (rows, extent)).astype(np.float32)
+        rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_TREE, ctx=ctx)
+        got, want = _route_vs_direct(ctx, rz, [x], (np.float32, rows),
+                                     lambda: families.tree_sum(x, (rows, extent), 1, ctx=ctx))
+    elif fam == 3:
+        m, n, k = (int(v) for v in r.integers(1, 400, 3))
+        n, k = 8 * max(1, n // 8), 8 * max(1, k // 8)
+        a = oracle.bf16_narrow((r.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32))
+        b = oracle.bf16_narrow((r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
+        rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=L.EPILOGUE_SILU, ctx=ctx)
+        got, want = _route_vs_direct(ctx, rz, [a, b], (np.uint16, m * n),
+                                     lambda: families.contract_bf16(a, b, L.EPILOGUE_SILU, ctx=ctx))
+    elif fam == 4:
+        n = 8 * int(r.integers(1, 50000))
+        x = (r.standard_normal(n) * 6).astype(np.float32)
+        rz = realize(L.PROGRAM_POINTWISE, (n,), variant=L.MAP_SILU, ctx=ctx)
+        got, want = _route_vs_direct(ctx, rz, [x], (np.float32, n), lambda: families.silu_f32(x, ctx=ctx))
+    else:
+        n = int(r.integers(1, 100000))
+        x = (r.standard_normal(n) * 1e3).astype(np.float32)
+        rz = realize(L.PROGRAM_CONVERT, (n,), variant=L.CONVERT_NARROW_F32_BF16, ctx=ctx)
+        got, want = _route_vs_direct(ctx, rz, [x], (np.uint16, n), lambda: families.narrow_f32_bf16(x, ctx=ctx))
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), (case, rz.symbols)
