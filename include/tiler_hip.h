@@ -146,6 +146,103 @@ tiler_hip_status tiler_hip_digest(const void *domain, uint64_t domain_bytes,
                                   uint32_t qualifier_count, const void *bytes, uint64_t byte_count,
                                   uint8_t out[32]);
 
+/* ------------------------------------------------------------------------
+ * Artifact envelope reader: what a HIP loader reads of a TILERART envelope
+ * (envelope format 1.0, canonical encoding 1.0, manifest schema 22.0;
+ * tiler-artifact/src/program/codec/encode.rs:29-306, decode.rs:105-437,
+ * validate.rs:68-327).  Device-free; every pointer in a result points into
+ * the caller's bytes, which must outlive it.
+ *
+ * tiler_hip_read_envelope checks, refusing with
+ * TILER_HIP_REFUSE_MALFORMED_PAYLOAD and the name of the ArtifactCodecError
+ * decode.rs reports first (e.g. "BadMagic", "ManifestDigestMismatch",
+ * "SectionDigestMismatch { section: 2 }") in `diagnostic`:
+ *   - the 69-byte header: magic, format, encoding, digest algorithm 0x01,
+ *     total length, budgets, the manifest digest;
+ *   - the manifest through the payload table: domain, schema 22.0,
+ *     component schemas, routing policy, features (sorted, distinct,
+ *     supported), interface entries, providers and payload descriptors (tags,
+ *     budgets, governed keys, canonical order);
+ *   - the section descriptors at the manifest's end (count = the header's):
+ *     purpose, disposition, schema, and each carried payload's references;
+ *   - the section stream: ids, lengths, content digests, no trailing bytes;
+ *   - providers present, the embedded-payload-code feature iff a payload is
+ *     carried, section order, payload sections referenced, and each carried
+ *     payload's identity (its PayloadDigest = payload_identity of its
+ *     metadata section, which must decode).
+ * The expression arena, variants and delivered-realization record are not
+ * parsed (the manifest digest covers them); the identity digest is reported
+ * as carried, not re-derived.
+ */
+typedef struct {
+    const uint8_t *backend;            uint64_t backend_bytes;
+    const uint8_t *representation;     uint64_t representation_bytes;
+    uint16_t payload_schema_major, payload_schema_minor;
+    const uint8_t *digest;             uint64_t digest_bytes;  /* PayloadDigest */
+    const uint8_t *profile_key;        uint64_t profile_key_bytes;
+    const uint8_t *profile_descriptor; uint64_t profile_descriptor_bytes;
+    uint32_t has_environment;          /* target-environment declaration present */
+    uint32_t carried;                  /* 1: metadata and code below are set */
+    uint32_t metadata_section, code_section;
+    const uint8_t *metadata;           uint64_t metadata_bytes;
+    const uint8_t *code;               uint64_t code_bytes;
+} tiler_hip_envelope_payload;
+
+typedef struct {
+    uint64_t total_bytes, manifest_bytes;
+    uint16_t manifest_schema_major, manifest_schema_minor;
+    uint32_t section_count;
+    uint8_t section_purpose[64];       /* 1 kernel program, 2 payload metadata, 3 payload code */
+    uint64_t feature_count, input_count, output_count, provider_count;
+    uint32_t payload_count;
+    tiler_hip_envelope_payload payloads[16];
+    uint8_t identity_digest[32];       /* as carried */
+} tiler_hip_envelope;
+
+tiler_hip_status tiler_hip_read_envelope(const void *bytes, uint64_t byte_count,
+                                         tiler_hip_envelope *out, char *diagnostic,
+                                         uint64_t diagnostic_bytes);
+
+/* One PayloadEntryMapping (codec/payload.rs:589-640): the entry key, the
+ * kernel symbol, and its transports (u32 big-endian each). */
+typedef struct {
+    const uint8_t *key;        uint64_t key_bytes;
+    const uint8_t *symbol;     uint64_t symbol_bytes;
+    uint32_t transport_count;
+    const uint8_t *transports;
+} tiler_hip_payload_mapping;
+
+typedef struct {
+    const uint8_t *source_representation; uint64_t source_representation_bytes;
+    const uint8_t *source;      uint64_t source_bytes;
+    const uint8_t *toolchain;   uint64_t toolchain_bytes;
+    const uint8_t *target;      uint64_t target_bytes;
+    const uint8_t *family;      uint64_t family_bytes;
+    const uint8_t *language;    uint64_t language_bytes;
+    uint16_t deployment_major, deployment_minor;
+    uint32_t unversioned;       /* 1: the PayloadPlatform::Unversioned tag ends the record */
+    uint64_t component_count, compile_flag_count, link_flag_count, obligation_count;
+    uint64_t entry_count;
+} tiler_hip_payload_subject;
+
+/* decode_metadata (codec/payload.rs:589-660) and check_provenance
+ * (payload.rs:291-343).  The first `capacity` mappings go to `mappings`
+ * (NULL with capacity 0 to count them). */
+tiler_hip_status tiler_hip_read_payload_metadata(const void *bytes, uint64_t byte_count,
+                                                 tiler_hip_payload_subject *out,
+                                                 tiler_hip_payload_mapping *mappings,
+                                                 uint32_t capacity, char *diagnostic,
+                                                 uint64_t diagnostic_bytes);
+
+/* The carried payload this backend executes (the role tiler-metal-aot's
+ * loader plays for its own payloads): backend "tiler.hip", representation
+ * "tiler.hip.gfx950.code-object-v1", payload schema major 1, and metadata
+ * target "amdgcn-amd-amdhsa--gfx950".  TILER_HIP_REFUSE_FOREIGN_TARGET when
+ * the envelope carries none; its entries then route through
+ * tiler_hip_prepare_entries with the payload's code bytes. */
+tiler_hip_status tiler_hip_select_payload(const tiler_hip_envelope *envelope, uint32_t *index,
+                                          char *diagnostic, uint64_t diagnostic_bytes);
+
 /* Validates a code object from its own bytes (ADR 0090 item 8;
  * RuntimeAdapter::validate_payload, tiler-runtime/src/adapter.rs:341):
  * an AMDGPU HSA ELF for gfx950 that defines `symbol` and its kernel descriptor

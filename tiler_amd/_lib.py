@@ -223,6 +223,61 @@ class Realization(ctypes.Structure):
     ]
 
 
+class EnvelopePayload(ctypes.Structure):
+    _fields_ = [
+        ("backend", ctypes.c_void_p), ("backend_bytes", ctypes.c_uint64),
+        ("representation", ctypes.c_void_p), ("representation_bytes", ctypes.c_uint64),
+        ("payload_schema_major", ctypes.c_uint16), ("payload_schema_minor", ctypes.c_uint16),
+        ("digest", ctypes.c_void_p), ("digest_bytes", ctypes.c_uint64),
+        ("profile_key", ctypes.c_void_p), ("profile_key_bytes", ctypes.c_uint64),
+        ("profile_descriptor", ctypes.c_void_p), ("profile_descriptor_bytes", ctypes.c_uint64),
+        ("has_environment", ctypes.c_uint32),
+        ("carried", ctypes.c_uint32),
+        ("metadata_section", ctypes.c_uint32), ("code_section", ctypes.c_uint32),
+        ("metadata", ctypes.c_void_p), ("metadata_bytes", ctypes.c_uint64),
+        ("code", ctypes.c_void_p), ("code_bytes", ctypes.c_uint64),
+    ]
+
+
+class Envelope(ctypes.Structure):
+    _fields_ = [
+        ("total_bytes", ctypes.c_uint64), ("manifest_bytes", ctypes.c_uint64),
+        ("manifest_schema_major", ctypes.c_uint16), ("manifest_schema_minor", ctypes.c_uint16),
+        ("section_count", ctypes.c_uint32),
+        ("section_purpose", ctypes.c_uint8 * 64),
+        ("feature_count", ctypes.c_uint64), ("input_count", ctypes.c_uint64),
+        ("output_count", ctypes.c_uint64), ("provider_count", ctypes.c_uint64),
+        ("payload_count", ctypes.c_uint32),
+        ("payloads", EnvelopePayload * 16),
+        ("identity_digest", ctypes.c_uint8 * 32),
+    ]
+
+
+class PayloadMapping(ctypes.Structure):
+    _fields_ = [
+        ("key", ctypes.c_void_p), ("key_bytes", ctypes.c_uint64),
+        ("symbol", ctypes.c_void_p), ("symbol_bytes", ctypes.c_uint64),
+        ("transport_count", ctypes.c_uint32),
+        ("transports", ctypes.c_void_p),
+    ]
+
+
+class PayloadSubject(ctypes.Structure):
+    _fields_ = [
+        ("source_representation", ctypes.c_void_p), ("source_representation_bytes", ctypes.c_uint64),
+        ("source", ctypes.c_void_p), ("source_bytes", ctypes.c_uint64),
+        ("toolchain", ctypes.c_void_p), ("toolchain_bytes", ctypes.c_uint64),
+        ("target", ctypes.c_void_p), ("target_bytes", ctypes.c_uint64),
+        ("family", ctypes.c_void_p), ("family_bytes", ctypes.c_uint64),
+        ("language", ctypes.c_void_p), ("language_bytes", ctypes.c_uint64),
+        ("deployment_major", ctypes.c_uint16), ("deployment_minor", ctypes.c_uint16),
+        ("unversioned", ctypes.c_uint32),
+        ("component_count", ctypes.c_uint64), ("compile_flag_count", ctypes.c_uint64),
+        ("link_flag_count", ctypes.c_uint64), ("obligation_count", ctypes.c_uint64),
+        ("entry_count", ctypes.c_uint64),
+    ]
+
+
 _P = ctypes.c_void_p
 _U64 = ctypes.c_uint64
 _U32 = ctypes.c_uint32
@@ -285,6 +340,10 @@ SIGNATURES = {
     "tiler_hip_payload_metadata": (_S, [_P, _U64, ctypes.POINTER(_U64)]),
     "tiler_hip_payload_identity": (_S, [_P]),
     "tiler_hip_digest": (_S, [_P, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64), _U32, _P, _U64, _P]),
+    "tiler_hip_read_envelope": (_S, [_P, _U64, ctypes.POINTER(Envelope), ctypes.c_char_p, _U64]),
+    "tiler_hip_read_payload_metadata": (_S, [_P, _U64, ctypes.POINTER(PayloadSubject),
+                                             ctypes.POINTER(PayloadMapping), _U32, ctypes.c_char_p, _U64]),
+    "tiler_hip_select_payload": (_S, [ctypes.POINTER(Envelope), ctypes.POINTER(_U32), ctypes.c_char_p, _U64]),
 }
 
 _lib = None

@@ -70,6 +70,7 @@ def build(verbose: bool = False) -> str:
           os.path.join(CSRC, "runtime", "tiler_hip.cpp"),
           os.path.join(CSRC, "runtime", "program.cpp"),
           os.path.join(CSRC, "runtime", "digest.cpp"),
+          os.path.join(CSRC, "runtime", "envelope.cpp"),
           os.path.join(CSRC, "runtime", "code_object.cpp"),
           payload_obj,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])

@@ -17,6 +17,7 @@
 #include "build_info.h"
 #include "code_object.h"
 #include "digest.h"
+#include "envelope.h"
 #include "program.h"
 
 extern "C" const uint8_t tiler_hip_code_object[];
@@ -453,6 +454,113 @@ tiler_hip_status tiler_hip_validate_payload(const void* code, uint64_t code_byte
   }
   copy_text(diagnostic, diagnostic_bytes, "");
   return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_read_envelope(const void* bytes, uint64_t byte_count, tiler_hip_envelope* out,
+                                         char* diagnostic, uint64_t diagnostic_bytes) {
+  if (!out || (byte_count && !bytes)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  static_assert(tiler_rt::kMaxEnvelopeSections == sizeof(out->section_purpose), "section table width");
+  static_assert(tiler_rt::kMaxEnvelopePayloads == sizeof(out->payloads) / sizeof(out->payloads[0]),
+                "payload table width");
+  std::memset(out, 0, sizeof(*out));
+  auto* e = new tiler_rt::Envelope();  // ~2 KB of spans; kept off small host stacks
+  const std::string why = tiler_rt::read_envelope(static_cast<const uint8_t*>(bytes), byte_count, *e);
+  copy_text(diagnostic, diagnostic_bytes, why);
+  if (why.empty()) {
+    out->total_bytes = e->total_bytes;
+    out->manifest_bytes = e->manifest_bytes;
+    out->manifest_schema_major = e->manifest_major;
+    out->manifest_schema_minor = e->manifest_minor;
+    out->section_count = e->section_count;
+    std::memcpy(out->section_purpose, e->section_kind, sizeof(out->section_purpose));
+    out->feature_count = e->feature_count;
+    out->input_count = e->input_count;
+    out->output_count = e->output_count;
+    out->provider_count = e->provider_count;
+    out->payload_count = e->payload_count;
+    for (uint32_t i = 0; i < e->payload_count; ++i) {
+      const tiler_rt::EnvelopePayload& p = e->payloads[i];
+      tiler_hip_envelope_payload& o = out->payloads[i];
+      o.backend = p.backend.p, o.backend_bytes = p.backend.n;
+      o.representation = p.representation.p, o.representation_bytes = p.representation.n;
+      o.payload_schema_major = p.schema_major, o.payload_schema_minor = p.schema_minor;
+      o.digest = p.digest.p, o.digest_bytes = p.digest.n;
+      o.profile_key = p.profile_key.p, o.profile_key_bytes = p.profile_key.n;
+      o.profile_descriptor = p.profile_descriptor.p, o.profile_descriptor_bytes = p.profile_descriptor.n;
+      o.has_environment = p.has_environment;
+      o.carried = p.carried;
+      o.metadata_section = p.metadata_section, o.code_section = p.code_section;
+      o.metadata = p.metadata.p, o.metadata_bytes = p.metadata.n;
+      o.code = p.code.p, o.code_bytes = p.code.n;
+    }
+    std::memcpy(out->identity_digest, e->identity_digest, 32);
+  }
+  delete e;
+  return why.empty() ? TILER_HIP_OK : TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+}
+
+tiler_hip_status tiler_hip_read_payload_metadata(const void* bytes, uint64_t byte_count,
+                                                 tiler_hip_payload_subject* out,
+                                                 tiler_hip_payload_mapping* mappings, uint32_t capacity,
+                                                 char* diagnostic, uint64_t diagnostic_bytes) {
+  if (!out || (byte_count && !bytes) || (capacity && !mappings)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  std::memset(out, 0, sizeof(*out));
+  tiler_rt::PayloadSubject s;
+  std::vector<tiler_rt::PayloadMapping> m(capacity);
+  const std::string why =
+      tiler_rt::read_payload_metadata(static_cast<const uint8_t*>(bytes), byte_count, s, m.data(), capacity);
+  copy_text(diagnostic, diagnostic_bytes, why);
+  if (!why.empty()) return TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+  out->source_representation = s.source_representation.p;
+  out->source_representation_bytes = s.source_representation.n;
+  out->source = s.source.p, out->source_bytes = s.source.n;
+  out->toolchain = s.toolchain.p, out->toolchain_bytes = s.toolchain.n;
+  out->target = s.target.p, out->target_bytes = s.target.n;
+  out->family = s.family.p, out->family_bytes = s.family.n;
+  out->language = s.language.p, out->language_bytes = s.language.n;
+  out->deployment_major = s.deployment_major, out->deployment_minor = s.deployment_minor;
+  out->unversioned = s.unversioned;
+  out->component_count = s.component_count;
+  out->compile_flag_count = s.compile_flag_count;
+  out->link_flag_count = s.link_flag_count;
+  out->obligation_count = s.obligation_count;
+  out->entry_count = s.entry_count;
+  const uint64_t n = s.entry_count < capacity ? s.entry_count : capacity;
+  for (uint64_t i = 0; i < n; ++i) {
+    mappings[i].key = m[i].key.p, mappings[i].key_bytes = m[i].key.n;
+    mappings[i].symbol = m[i].symbol.p, mappings[i].symbol_bytes = m[i].symbol.n;
+    mappings[i].transport_count = (uint32_t)m[i].transport_count;
+    mappings[i].transports = m[i].transports.p;
+  }
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_select_payload(const tiler_hip_envelope* envelope, uint32_t* index,
+                                          char* diagnostic, uint64_t diagnostic_bytes) {
+  if (!envelope || !index || envelope->payload_count > 16) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  auto is = [](const uint8_t* p, uint64_t n, const char* s) {
+    return n == std::strlen(s) && (n == 0 || std::memcmp(p, s, n) == 0);
+  };
+  std::string seen;
+  for (uint32_t i = 0; i < envelope->payload_count; ++i) {
+    const tiler_hip_envelope_payload& p = envelope->payloads[i];
+    if (!seen.empty()) seen += ", ";
+    seen += std::string((const char*)p.backend, p.backend_bytes) + "/" +
+            std::string((const char*)p.representation, p.representation_bytes);
+    if (!p.carried || !is(p.backend, p.backend_bytes, kBackend) ||
+        !is(p.representation, p.representation_bytes, kRepresentation) || p.payload_schema_major != 1)
+      continue;
+    tiler_rt::PayloadSubject s;
+    if (!tiler_rt::read_payload_metadata(p.metadata, p.metadata_bytes, s, nullptr, 0).empty()) continue;
+    if (!is(s.target.p, s.target.n, kTarget)) continue;
+    *index = i;
+    copy_text(diagnostic, diagnostic_bytes, "");
+    return TILER_HIP_OK;
+  }
+  copy_text(diagnostic, diagnostic_bytes,
+            "no carried " + std::string(kBackend) + " payload for " + kTarget +
+                (seen.empty() ? std::string(" (the envelope names no payloads)") : " among: " + seen));
+  return TILER_HIP_REFUSE_FOREIGN_TARGET;
 }
 
 // ---------------------------------------------------------------------------

@@ -99,19 +99,26 @@ def _payload_code():
     return ctypes.string_at(v.code, v.code_bytes)
 
 
-def _prepared(ctx, symbol: str) -> int:
+def _prepared(ctx, symbol: str, payload=None) -> int:
+    """The prepared-entry index of `symbol`, loaded from the library's own
+    code object or, given a carried payload, from that payload's code bytes.
+    Cached per context and per code object."""
+    code = payload.code if payload is not None else None
+    source = payload.digest if payload is not None else b""
     cache = ctx.__dict__.setdefault("_route_prepared", {})
-    if symbol not in cache:
-        if "_route_code" not in ctx.__dict__:
-            code = _payload_code()
-            ctx._route_code = ctypes.create_string_buffer(code, len(code))
-        entry = L.RoutedEntry(ctypes.cast(ctx._route_code, ctypes.c_void_p), len(ctx._route_code.raw),
-                              symbol.encode())
+    if (source, symbol) not in cache:
+        codes = ctx.__dict__.setdefault("_route_code", {})
+        if source not in codes:
+            if code is None:
+                code = _payload_code()
+            codes[source] = ctypes.create_string_buffer(code, len(code))
+        buf = codes[source]
+        entry = L.RoutedEntry(ctypes.cast(buf, ctypes.c_void_p), len(buf.raw), symbol.encode())
         first = ctypes.c_uint32()
         _raise(L.lib().tiler_hip_prepare_entries(ctx.handle, ctypes.byref(entry), 1, ctypes.byref(first)),
                f"prepare_entries({symbol})", ctx.diagnostic())
-        cache[symbol] = first.value
-    return cache[symbol]
+        cache[(source, symbol)] = first.value
+    return cache[(source, symbol)]
 
 
 def _address(buf) -> int:
@@ -124,11 +131,20 @@ def _capacity(buf):
     return getattr(buf, "nbytes", None)
 
 
-def route(ctx, realization: Realization, storage) -> None:
+def route(ctx, realization: Realization, storage, payload=None) -> None:
     """Executes `realization` on `ctx`'s stream and waits for it.  `storage`
     lists one device buffer (or address) per slot, in the realization's slot
-    order; scratch slots may be None (allocated here, released after)."""
+    order; scratch slots may be None (allocated here, released after).
+    `payload` (from `tiler_amd.envelope.select_payload`) routes through a
+    carried code object instead of the library's own: every symbol dispatched
+    must be one of its PayloadEntryMappings."""
     rz = realization
+    if payload is not None:
+        mapped = set(payload.subject.symbols) if payload.subject is not None else set()
+        for d in rz.dispatches:
+            if d.symbol not in mapped:
+                raise Refusal(L.REFUSE_ABSENT_SYMBOL, "route",
+                              f"{d.symbol} is not among the carried payload's entry mappings")
     if len(storage) != len(rz.slots):
         raise Refusal(L.REFUSE_BINDING_MISMATCH, "route",
                       f"{len(storage)} storage bindings for {len(rz.slots)} slots")
@@ -154,7 +170,7 @@ def route(ctx, realization: Realization, storage) -> None:
         offs = (ctypes.c_uint32 * max(1, e.binding_count))(*e.binding_offsets[:e.binding_count])
         kernargs = ctypes.create_string_buffer(bytes(e.kernargs[:e.kernarg_bytes]), max(1, e.kernarg_bytes))
         keep += [slots, offs, kernargs]
-        entries[i] = L.DispatchEntry(_prepared(ctx, rz.dispatches[i].symbol), e.grid, e.block, 0,
+        entries[i] = L.DispatchEntry(_prepared(ctx, rz.dispatches[i].symbol, payload), e.grid, e.block, 0,
                                      ctypes.cast(kernargs, ctypes.c_void_p), e.kernarg_bytes,
                                      e.binding_count, slots, offs)
     slot_bytes = (ctypes.c_uint64 * len(rz.slots))(*[b for _, b in rz.slots])
