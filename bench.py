@@ -135,17 +135,34 @@ class Sum(Workload):
     sets = 6
 
     def config(self):
-        return {"workload": "serial-sum f32[2^24] ~U[-1,1] -> f32 scalar (two-level tree)",
-                "buffer_sets": self.sets}
+        out = {"workload": "serial-sum f32[2^24] ~U[-1,1] -> f32 scalar (two-level tree)",
+               "buffer_sets": self.sets}
+        if hasattr(self, "conditioning"):
+            out["conditioning"] = self.conditioning
+        return out
 
     def work(self):
         return self.n * 4 + 4
 
     def setup(self):
         rng = np.random.default_rng(0)
-        self.xs = [self._keep(self.ctx.to_device(rng.uniform(-1, 1, self.n).astype(np.float32)))
-                   for _ in range(self.sets)]
+        self.xs = []
+        for s in range(self.sets):
+            x = rng.uniform(-1, 1, self.n).astype(np.float32)
+            if s == 0:
+                # Condition of the sum: sum|x| / |sum x| (f64), and the device's
+                # relative error on this set against the f64 sum.
+                exact = float(np.sum(x, dtype=np.float64))
+                self.conditioning = {"set": 0, "sum_f64": exact,
+                                     "sum_abs_f64": float(np.sum(np.abs(x), dtype=np.float64)),
+                                     "condition_number": float(np.sum(np.abs(x), dtype=np.float64)) / abs(exact)}
+            self.xs.append(self._keep(self.ctx.to_device(x)))
         self.out = self._keep(self.ctx.alloc(4))
+        self.ctx.sum_f32(self.xs[0], 1, self.n, self.out)
+        got = float(self.out.download(np.float32, (1,))[0])
+        exact = self.conditioning["sum_f64"]
+        self.conditioning["device_sum"] = got
+        self.conditioning["relative_error_vs_f64"] = abs(got - exact) / abs(exact)
         return self.sets
 
     def launch(self, i):
