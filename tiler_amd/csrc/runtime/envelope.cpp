@@ -662,6 +662,8 @@ std::string read_envelope(const uint8_t* bytes, uint64_t n, Envelope& out) {
     return read_envelope_or_throw(bytes, n, out);
   } catch (const Reject& r) {
     return r.why;
+  } catch (...) {  // allocation failure: nothing crosses the C ABI
+    return "AllocationFailure";
   }
 }
 
@@ -674,6 +676,8 @@ std::string read_payload_metadata(const uint8_t* bytes, uint64_t n, PayloadSubje
     return "";
   } catch (const Reject& r) {
     return r.why;
+  } catch (...) {
+    return "AllocationFailure";
   }
 }
 

@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -463,7 +464,8 @@ tiler_hip_status tiler_hip_read_envelope(const void* bytes, uint64_t byte_count,
   static_assert(tiler_rt::kMaxEnvelopePayloads == sizeof(out->payloads) / sizeof(out->payloads[0]),
                 "payload table width");
   std::memset(out, 0, sizeof(*out));
-  auto* e = new tiler_rt::Envelope();  // ~2 KB of spans; kept off small host stacks
+  auto* e = new (std::nothrow) tiler_rt::Envelope();  // ~2 KB of spans; kept off small host stacks
+  if (!e) return TILER_HIP_REFUSE_CAPACITY;
   const std::string why = tiler_rt::read_envelope(static_cast<const uint8_t*>(bytes), byte_count, *e);
   copy_text(diagnostic, diagnostic_bytes, why);
   if (why.empty()) {
@@ -506,7 +508,12 @@ tiler_hip_status tiler_hip_read_payload_metadata(const void* bytes, uint64_t byt
   if (!out || (byte_count && !bytes) || (capacity && !mappings)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   std::memset(out, 0, sizeof(*out));
   tiler_rt::PayloadSubject s;
-  std::vector<tiler_rt::PayloadMapping> m(capacity);
+  std::vector<tiler_rt::PayloadMapping> m;
+  try {
+    m.resize(capacity);
+  } catch (...) {
+    return TILER_HIP_REFUSE_CAPACITY;
+  }
   const std::string why =
       tiler_rt::read_payload_metadata(static_cast<const uint8_t*>(bytes), byte_count, s, m.data(), capacity);
   copy_text(diagnostic, diagnostic_bytes, why);
@@ -535,8 +542,23 @@ tiler_hip_status tiler_hip_read_payload_metadata(const void* bytes, uint64_t byt
   return TILER_HIP_OK;
 }
 
+namespace {
+tiler_hip_status select_payload(const tiler_hip_envelope* envelope, uint32_t* index, char* diagnostic,
+                                uint64_t diagnostic_bytes);
+}  // namespace
+
 tiler_hip_status tiler_hip_select_payload(const tiler_hip_envelope* envelope, uint32_t* index,
                                           char* diagnostic, uint64_t diagnostic_bytes) {
+  try {
+    return select_payload(envelope, index, diagnostic, diagnostic_bytes);
+  } catch (...) {  // allocation failure: nothing crosses the C ABI
+    return TILER_HIP_REFUSE_CAPACITY;
+  }
+}
+
+namespace {
+tiler_hip_status select_payload(const tiler_hip_envelope* envelope, uint32_t* index, char* diagnostic,
+                                uint64_t diagnostic_bytes) {
   if (!envelope || !index || envelope->payload_count > 16) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   auto is = [](const uint8_t* p, uint64_t n, const char* s) {
     return n == std::strlen(s) && (n == 0 || std::memcmp(p, s, n) == 0);
@@ -562,6 +584,7 @@ tiler_hip_status tiler_hip_select_payload(const tiler_hip_envelope* envelope, ui
                 (seen.empty() ? std::string(" (the envelope names no payloads)") : " among: " + seen));
   return TILER_HIP_REFUSE_FOREIGN_TARGET;
 }
+}  // namespace
 
 // ---------------------------------------------------------------------------
 tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
