@@ -283,7 +283,13 @@ const char *tiler_hip_last_diagnostic(const tiler_hip_context *ctx);
 
 /* observe_live_device (adapter.rs:363): reports, never decides.  Keys:
  * "wavefront-size", "compute-units", "max-threads-per-workgroup",
- * "lds-bytes-per-workgroup", "global-memory-bytes", "target-is-gfx950".
+ * "lds-bytes-per-workgroup", "global-memory-bytes", "target-is-gfx950",
+ * "max-grid-x", "max-grid-y", "max-grid-z", "device-address-bits", and two
+ * measured ones (the rows tiler-compiler/src/target/builder.rs:737-775
+ * declares as measured): "f32-input-subnormals" and "f32-result-subnormals".
+ * Those run a one-lane probe kernel on the context's stream on first query
+ * and answer 1 preserve, 2 flush to a zero of the same sign, 3 flush to +0
+ * (0: a pattern none of them produces).
  * Unknown keys answer TILER_HIP_REFUSE_UNRECOGNIZED_KEY (fail-closed). */
 tiler_hip_status tiler_hip_observe_live_device(tiler_hip_context *ctx, const char *key,
                                                uint64_t *value);

@@ -34,6 +34,20 @@ def test_live_device_observations(ctx):
     assert ctx.observe_live_device("compute-units") >= 1
     assert ctx.observe_live_device("lds-bytes-per-workgroup") >= 64 * 1024
     assert ctx.observe_live_device("no-such-key") is None  # Unrecognized, fail-closed
+    assert ctx.observe_live_device("device-address-bits") == 64
+    assert min(ctx.observe_live_device(f"max-grid-{a}") for a in "xyz") >= 1
+
+
+def test_measured_subnormal_behaviour(ctx):
+    # Measured by the probe kernel on the device: the code object is built
+    # without denormal flushing, so both sides preserve (mode 1), which is what
+    # the declared profile states (f32_subnormals_preserved) and what the
+    # oracle's PRESERVE mode computes.
+    assert ctx.observe_live_device("f32-input-subnormals") == 1
+    assert ctx.observe_live_device("f32-result-subnormals") == 1
+    assert tiler_amd.runtime.profile()["f32_subnormals_preserved"] == 1
+    # Cached: a second query answers without another probe and agrees.
+    assert ctx.observe_live_device("f32-input-subnormals") == 1
 
 
 def test_route_prepare_plan_allocate_dispatch(ctx):

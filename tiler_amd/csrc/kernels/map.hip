@@ -232,3 +232,18 @@ tiler_fill_u32(uint32_t* __restrict__ dst, uint32_t value, uint64_t words) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride)
     dst[i] = value;
 }
+
+// Subnormal probe: the f32 subnormal handling this code object delivers on
+// the live device, measured rather than assumed.  in[] holds the operands, so
+// nothing folds at compile time:
+//   out[0] = in[0] * in[1]: -2^-149 (a subnormal input) times 2^30, whose
+//            exact product -2^-119 is normal -- the input side;
+//   out[1] = in[2] * in[3]: 2^-120 times -2^-10, whose exact product -2^-130
+//            is subnormal -- the result side.
+extern "C" __global__ void __launch_bounds__(64)
+tiler_probe_subnormals(const float* __restrict__ in, uint32_t* __restrict__ out) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    out[0] = __float_as_uint(in[0] * in[1]);
+    out[1] = __float_as_uint(in[2] * in[3]);
+  }
+}

@@ -154,6 +154,7 @@ const EntryRow kEntries[] = {
     {"tiler_broadcast_rows_u32", "broadcast", 2},
     {"tiler_broadcast_rows_u16", "broadcast", 2},
     {"tiler_fill_u32", "fill", 1},
+    {"tiler_probe_subnormals", "probe", 2},
     {"tiler_narrow_f32_bf16_v8", "convert-f32-to-bf16/narrow", 2},
     {"tiler_narrow_f32_bf16", "convert-f32-to-bf16/narrow", 2},
     {"tiler_widen_bf16_f32_v8", "convert-bf16-to-f32/widen", 2},
@@ -209,6 +210,8 @@ struct tiler_hip_context {
   uint64_t lds_bytes = 0;
   uint32_t max_threads = 0;
   uint64_t global_bytes = 0;
+  uint32_t max_grid[3] = {0, 0, 0};
+  int32_t input_subnormals = -1, result_subnormals = -1;  // measured on first query
   std::string arch;
   std::string diag;
 };
@@ -622,6 +625,7 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
   ctx->lds_bytes = prop.sharedMemPerBlock;
   ctx->max_threads = (uint32_t)prop.maxThreadsPerBlock;
   ctx->global_bytes = prop.totalGlobalMem;
+  for (int d = 0; d < 3; ++d) ctx->max_grid[d] = (uint32_t)prop.maxGridSize[d];
   hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipModuleLoadData(&ctx->module, tiler_hip_code_object);
   if (e != hipSuccess) {
@@ -693,16 +697,64 @@ const char* tiler_hip_last_diagnostic(const tiler_hip_context* ctx) {
   return ctx ? ctx->diag.c_str() : "";
 }
 
+namespace {
+
+// Subnormal modes, as the reference names them (conformance.rs:269-521):
+// 1 preserve, 2 flush to a zero of the same sign, 3 flush to +0; 0 a pattern
+// none of them produces.
+uint32_t subnormal_mode(uint32_t bits, uint32_t preserved) {
+  if (bits == preserved) return 1;
+  if (bits == 0x80000000u) return 2;
+  if (bits == 0x00000000u) return 3;
+  return 0;
+}
+
+// Runs tiler_probe_subnormals once per context on its stream and caches the
+// two modes.
+tiler_hip_status measure_subnormals(tiler_hip_context* ctx) {
+  if (ctx->input_subnormals >= 0) return TILER_HIP_OK;
+  const float in[4] = {-0x1p-149f, 0x1p30f, 0x1p-120f, -0x1p-10f};
+  uint32_t out[2] = {0, 0};
+  void* dev = nullptr;
+  if (hipMalloc(&dev, 64) != hipSuccess) return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "probe buffer");
+  float* din = static_cast<float*>(dev);
+  uint32_t* dout = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(dev) + 32);
+  void* args[] = {&din, &dout};
+  hipError_t e = hipMemcpyAsync(din, in, sizeof(in), hipMemcpyHostToDevice, ctx->stream);
+  tiler_hip_status st = e == hipSuccess ? launch(ctx, "tiler_probe_subnormals", 1, 1, 64, ctx->stream, args)
+                                        : TILER_HIP_FAIL_TRANSFER;
+  if (st == TILER_HIP_OK && (hipMemcpyAsync(out, dout, sizeof(out), hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
+                             hipStreamSynchronize(ctx->stream) != hipSuccess))
+    st = TILER_HIP_FAIL_TRANSFER;
+  hipFree(dev);
+  if (st != TILER_HIP_OK) return fail(ctx, st, "subnormal probe");
+  ctx->input_subnormals = (int32_t)subnormal_mode(out[0], 0x80000000u | (0x7fu - 119u + 0u) << 23);
+  ctx->result_subnormals = (int32_t)subnormal_mode(out[1], 0x80000000u | (1u << (149 - 130)));
+  return TILER_HIP_OK;
+}
+
+}  // namespace
+
 tiler_hip_status tiler_hip_observe_live_device(tiler_hip_context* ctx, const char* key,
                                                uint64_t* value) {
   if (!ctx || !key || !value) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   std::string k = key;
+  if (k == "f32-input-subnormals" || k == "f32-result-subnormals") {
+    const tiler_hip_status st = measure_subnormals(ctx);
+    if (st != TILER_HIP_OK) return st;
+    *value = (uint64_t)(k == "f32-input-subnormals" ? ctx->input_subnormals : ctx->result_subnormals);
+    return TILER_HIP_OK;
+  }
   if (k == "wavefront-size") *value = 64;
   else if (k == "compute-units") *value = ctx->compute_units;
   else if (k == "max-threads-per-workgroup") *value = ctx->max_threads;
   else if (k == "lds-bytes-per-workgroup") *value = ctx->lds_bytes;
   else if (k == "global-memory-bytes") *value = ctx->global_bytes;
   else if (k == "target-is-gfx950") *value = ctx->arch.rfind("gfx950", 0) == 0 ? 1 : 0;
+  else if (k == "max-grid-x") *value = ctx->max_grid[0];
+  else if (k == "max-grid-y") *value = ctx->max_grid[1];
+  else if (k == "max-grid-z") *value = ctx->max_grid[2];
+  else if (k == "device-address-bits") *value = 64;
   else return fail(ctx, TILER_HIP_REFUSE_UNRECOGNIZED_KEY, "unrecognized live-device key " + k);
   return TILER_HIP_OK;
 }
