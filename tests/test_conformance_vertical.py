@@ -35,6 +35,18 @@ def test_the_pinned_expectations_are_the_reference_records():
         assert list(ops) == [hexbits(v) for v in s[key]] and want == hexbits(s[want_key])
 
 
+def test_the_row_examples_are_the_reference_records():
+    r = next(c for c in G["rms_norm"]["cases"] if c["name"] == "worked example")
+    sm = next(c for c in G["softmax"]["cases"] if c["name"] == "worked example")
+    cells = {name: (xs, ws, eps, want) for name, _, xs, ws, eps, want in C.ROW_CELLS}
+    xs, ws, eps, want = cells["rms-norm/worked-example"]
+    assert list(np.asarray(xs, np.uint32).view(np.float32)) == r["x"]
+    assert list(np.asarray(ws, np.uint32).view(np.float32)) == r["w"]
+    assert eps == hexbits(G["rms_norm"]["eps_bits"]) and list(want) == [hexbits(v) for v in r["y_bits"]]
+    xs, _, _, want = cells["softmax/worked-example"]
+    assert list(xs) == [hexbits(v) for v in sm["x_bits"]] and list(want) == [hexbits(v) for v in sm["y_bits"]]
+
+
 def test_operands_match_the_test_side_generator():
     for seed in (C.WORKLOAD_SEED, C.WORKLOAD_SEED ^ C.RIGHT_SEED_MASK):
         assert np.array_equal(C.splitmix_operands(seed, 5000), splitmix_operands(seed, 5000))
@@ -60,7 +72,7 @@ def test_require_or_report_outcomes(monkeypatch):
 
 def test_deterministic_half_runs_everywhere():
     d = C.deterministic_half()
-    assert len(d) == len(C.CONTRACTION_CELLS) + len(C.SERIAL_SUM_CELLS)
+    assert len(d) == len(C.CONTRACTION_CELLS) + len(C.SERIAL_SUM_CELLS) + len(C.ROW_CELLS)
 
 
 def test_a_host_without_the_device_reports_unavailable(monkeypatch):

@@ -22,6 +22,8 @@ Verticals:
 - `serial-sum-cells`: the serial, multi-pass and tree sums over the operand
   sets of tiler-conformance/src/serial_sum.rs:202-368, checked bit for bit
   against the results those records state.
+- `row-worked-examples`: the RMSNorm and softmax worked examples whose every
+  bit the reference's tests fix.
 
 `python -m tiler_amd.conformance` prints the boundary and every vertical's
 outcome. It exits non-zero on a failure, or on an unavailable measurement
@@ -70,6 +72,18 @@ SERIAL_SUM_CELLS = (
     ("separating/split-4x3", _GROUPING + (0,) * 8, "multipass", (4, 3), 0x3F800000),
     ("separating-exact/serial", tuple(0x3F800000 + (i << 23) for i in range(12)), "serial", None, 0x457FF000),
     ("separating-exact/tree", tuple(0x3F800000 + (i << 23) for i in range(12)), "tree", None, 0x457FF000),
+)
+
+
+# Worked examples whose every bit the reference's tests fix.
+# tiler-reference/src/rms_norm/tests.rs:253-276 (f32, eps bits 0x358637bd);
+# tiler-reference/src/softmax/tests.rs:362-455 (the last score is the most
+# negative finite f32, a masked contributor).
+ROW_CELLS = (
+    ("rms-norm/worked-example", "rms_norm", (0x40400000, 0x40800000), (0x3F800000, 0x40000000), 0x358637BD,
+     (0x3F593923, 0x4010D0C2)),
+    ("softmax/worked-example", "softmax", (0x3F800000, 0x40000000, 0x40400000, 0xFF7FFFFF), None, None,
+     (0x3DB861F3, 0x3E7A9A1A, 0x3F2A4D3B, 0x00000000)),
 )
 
 
@@ -232,7 +246,31 @@ def serial_sum_cells(ctx, boundary) -> Measured:
     return Measured.ran(boundary, observed)
 
 
-VERTICALS = (("contraction-profile-cells", contraction_profile_cells), ("serial-sum-cells", serial_sum_cells))
+def row_worked_examples(ctx, boundary) -> Measured:
+    observed = []
+    try:
+        for name, family, xs, ws, eps, want in ROW_CELLS:
+            x = np.asarray(xs, dtype=np.uint32).view(np.float32)
+            dx, dy = ctx.to_device(x), ctx.alloc(x.nbytes)
+            dw = ctx.to_device(np.asarray(ws, dtype=np.uint32).view(np.float32)) if ws is not None else None
+            try:
+                if family == "rms_norm":
+                    ctx.rms_norm(L.F32, dx, dw, 1, x.size, eps, dy, weight_broadcast=True)
+                else:
+                    ctx.softmax_f32(dx, 1, x.size, dy)
+                got = [int(v) for v in dy.download(np.float32, (x.size,)).view(np.uint32)]
+            finally:
+                for b in (dx, dy, dw):
+                    if b is not None:
+                        b.free()
+            observed.append({"cell": name, "match": got == list(want), "bits": [f"0x{v:08x}" for v in got]})
+    except Exception as e:
+        return Measured.failed(f"{type(e).__name__}: {e}")
+    return Measured.ran(boundary, observed)
+
+
+VERTICALS = (("contraction-profile-cells", contraction_profile_cells), ("serial-sum-cells", serial_sum_cells),
+             ("row-worked-examples", row_worked_examples))
 
 
 def deterministic_half() -> dict:
@@ -245,6 +283,8 @@ def deterministic_half() -> dict:
         out[cid] = {"operands_sha256": hashlib.sha256(a.tobytes() + b.tobytes()).hexdigest(), "expected": digest}
     for name, operands, topology, grouping, want in SERIAL_SUM_CELLS:
         out[name] = {"operands": len(operands), "topology": topology, "expected": f"0x{want:08x}"}
+    for name, family, xs, ws, eps, want in ROW_CELLS:
+        out[name] = {"family": family, "expected": [f"0x{v:08x}" for v in want]}
     return out
 
 
