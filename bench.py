@@ -243,6 +243,49 @@ class Softmax(Workload):
                 "sample": f"{done} rows x {self.extent} in {el:.1f} s, single thread (certified exp)"}
 
 
+class SoftmaxDecode(Workload):
+    """Few long rows: f32 [32 heads x 131072 keys] softmax over the keys (the
+    shape of decode-attention scores).  16 segments a row, so the split form
+    runs (three launches over 512 workgroups); 16 buffer sets (512 MiB)
+    keep the working set out of the 256 MB last-level cache."""
+    name = "softmax_decode"
+    kernel = "tiler_softmax_f32_split_out_a"
+    rows, extent = 32, 131072
+    sets = 16
+
+    def config(self):
+        return {"workload": "softmax f32 [32 x 131072] ~N(0,3), last axis (split rows)",
+                "buffer_sets": self.sets}
+
+    def work(self):
+        return self.rows * self.extent * 4 * 2
+
+    def setup(self):
+        rng = np.random.default_rng(4)
+        self.sets_ = []
+        for _ in range(self.sets):
+            x = rng.standard_normal((self.rows, self.extent), dtype=np.float32) * np.float32(3.0)
+            self.sets_.append(self._keep(self.ctx.to_device(x), self.ctx.alloc(x.nbytes)))
+        return self.sets
+
+    def launch(self, i):
+        x, y = self.sets_[i % self.sets]
+        self.ctx.softmax_f32(x, self.rows, self.extent, y)
+
+    def cpu_baseline(self, budget_s):
+        import oracle
+        x = np.random.default_rng(4).standard_normal((2, self.extent), dtype=np.float32) * np.float32(3.0)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            oracle.softmax_f32(x, (2, self.extent), 1)
+            done += 2
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        return {"value": done * self.extent * 8 / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done} rows x {self.extent} in {el:.1f} s, single thread (certified exp)"}
+
+
 class Gather(Workload):
     """tied embedding gather."""
     name = "gather"
@@ -422,7 +465,7 @@ class Convert(Workload):
                 "sample": f"{done} elements of the oracle's narrowing in {el:.1f} s, single thread"}
 
 
-WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, Gather, Contract, Convert)}
+WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, SoftmaxDecode, Gather, Contract, Convert)}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_all_families.md")

@@ -428,23 +428,32 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context *ctx, uint32_t dtype, cons
                                     tiler_hip_stream stream);
 
 /* Softmax over the last axis with the governed-maximum shift (softmax-f32@1;
- * tiler-reference/src/softmax.rs:200-315). */
+ * tiler-reference/src/softmax.rs:200-315).  Rows longer than 8192 elements
+ * fold their exponent sum by segments (tiler_hip_row_grouping); rows of more
+ * than 4 segments run each segment in a workgroup of its own, the segment
+ * partials in the context's workspace (up to 32768 segments; more are
+ * allocated on the stream), so such calls on different streams of one
+ * context must not run concurrently. */
 tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context *ctx, const float *x, uint64_t rows,
                                        uint64_t extent, float *y, tiler_hip_stream stream);
 
 /* The declared grouping of a row reduction: thread t of a 64*waves-thread
  * group folds the `vec`-element chunks t, t + 64*waves, ... in ascending
  * position, each wave combines its lanes with an xor butterfly (offsets 32 ..
- * 1) and the wave results are added in ascending order.  RMSNorm and softmax
- * rows of up to 8192 elements use one wave (waves 1); longer rows one
- * 1024-thread workgroup (waves 16); the many-row sum uses (4, 4).  The
- * reassociation is the one the kernels perform, reported so a planner can
- * record it.  Device-free. */
+ * 1) and the wave results are added in ascending order.  segment != 0: the
+ * row is cut into segments of `segment` elements, each segment is folded so
+ * (chunk positions relative to the segment) and the row total is the left
+ * fold of the segment results in ascending order.  RMSNorm and softmax rows
+ * of up to 8192 elements use one wave (waves 1, segment 0); longer RMSNorm
+ * rows one 1024-thread workgroup (waves 16, segment 0); longer softmax rows
+ * segments of 8192 (waves 4); the many-row sum uses (4, 4, 0).  The
+ * reassociation is the one the kernels perform whichever launch form runs,
+ * reported so a planner can record it.  Device-free. */
 #define TILER_HIP_ROWS_RMS_NORM 0
 #define TILER_HIP_ROWS_SOFTMAX 1
 #define TILER_HIP_ROWS_SUM 2
 tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_t extent,
-                                        uint32_t *vec, uint32_t *waves);
+                                        uint32_t *vec, uint32_t *waves, uint64_t *segment);
 
 /* Pointwise maps (tiler-reference/src/evaluate.rs:448-485; silu.rs:511-533).
  * op: 0 scale-bias y = x*a + b, 1 SiLU, 2 add x + x2, 3 multiply x * x2.

@@ -90,6 +90,7 @@ _SIGS = {
     "tiler_oracle_grid_tree_sum_f32": (_I32, [_P, _U64, _U32, _P]),
     "tiler_oracle_rms_norm_grouped_f32": (_I32, [_P, _P, _U64, _U64, _U32, _I32, _U32, _U32, _P]),
     "tiler_oracle_softmax_grouped_f32": (_I32, [_P, _U64, _U64, _U32, _U32, _P]),
+    "tiler_oracle_softmax_segmented_f32": (_I32, [_P, _U64, _U64, _U64, _U32, _U32, _P]),
 }
 
 
@@ -305,11 +306,13 @@ def rms_norm_grouped(values, weights, rows, extent, eps_bits, weight_broadcast, 
     return out
 
 
-def softmax_grouped(values, rows, extent, vec, waves) -> np.ndarray:
+def softmax_grouped(values, rows, extent, vec, waves, segment=0) -> np.ndarray:
+    """Softmax whose exponent sum folds segments of `segment` elements (0: the
+    whole row) by the (vec, waves) grouping, partials left-folded."""
     x = _f32(values).reshape(-1)
     out = np.empty(rows * extent, np.float32)
-    _check(lib().tiler_oracle_softmax_grouped_f32(_ptr(x), rows, extent, vec, waves, _ptr(out)),
-           "softmax_grouped")
+    _check(lib().tiler_oracle_softmax_segmented_f32(_ptr(x), rows, extent, segment, vec, waves,
+                                                    _ptr(out)), "softmax_grouped")
     return out
 
 

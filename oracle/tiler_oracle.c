@@ -644,10 +644,19 @@ int32_t tiler_oracle_rms_norm_grouped_f32(const float *x, const float *w, uint64
     return TILER_ORACLE_OK;
 }
 
-int32_t tiler_oracle_softmax_grouped_f32(const float *x, uint64_t rows, uint64_t extent,
-                                         uint32_t vec, uint32_t waves, float *y) {
+/* Softmax with a segmented exponent sum: the row's exponents are cut into
+ * segments of `segment` elements (0: one segment, the whole row); each
+ * segment's partial is the (vec, waves) grouped fold of its elements and the
+ * row total is the left fold of the partials in ascending segment order,
+ * seeded by the first.  The shift, the exponent and the final scaling are
+ * softmax.rs:237-315's: m = the governed maximum of the row, e = exp(x - m)
+ * certified, y = canon(e * (1 / d)). */
+int32_t tiler_oracle_softmax_segmented_f32(const float *x, uint64_t rows, uint64_t extent,
+                                           uint64_t segment, uint32_t vec, uint32_t waves,
+                                           float *y) {
     if (vec == 0 || waves == 0 || waves > 16) return TILER_ORACLE_INVALID_APPLICATION;
     if (extent == 0) return TILER_ORACLE_OK;
+    if (segment == 0 || segment > extent) segment = extent;
     float *e = (float *)malloc(sizeof(float) * extent);
     for (uint64_t r = 0; r < rows; ++r) {
         const float *xr = x + r * extent;
@@ -660,10 +669,20 @@ int32_t tiler_oracle_softmax_grouped_f32(const float *x, uint64_t rows, uint64_t
                 return st;
             }
         }
-        float d = row_grouped_fold(e, extent, vec, waves);
+        float d = 0.0f;
+        for (uint64_t s0 = 0; s0 < extent; s0 += segment) {
+            uint64_t len = extent - s0 < segment ? extent - s0 : segment;
+            float part = row_grouped_fold(e + s0, len, vec, waves);
+            d = s0 == 0 ? part : d + part;
+        }
         float rcp = 1.0f / d;
         for (uint64_t p = 0; p < extent; ++p) y[r * extent + p] = canon(e[p] * rcp);
     }
     free(e);
     return TILER_ORACLE_OK;
+}
+
+int32_t tiler_oracle_softmax_grouped_f32(const float *x, uint64_t rows, uint64_t extent,
+                                         uint32_t vec, uint32_t waves, float *y) {
+    return tiler_oracle_softmax_segmented_f32(x, rows, extent, 0, vec, waves, y);
 }

@@ -122,6 +122,11 @@ int32_t tiler_oracle_rms_norm_grouped_f32(const float *x, const float *w, uint64
                                           uint32_t waves, float *y);
 int32_t tiler_oracle_softmax_grouped_f32(const float *x, uint64_t rows, uint64_t extent,
                                          uint32_t vec, uint32_t waves, float *y);
+/* The same with the exponent sum folded by segments of `segment` elements
+ * (0: the whole row), partials left-folded in ascending segment order. */
+int32_t tiler_oracle_softmax_segmented_f32(const float *x, uint64_t rows, uint64_t extent,
+                                           uint64_t segment, uint32_t vec, uint32_t waves,
+                                           float *y);
 
 /* Audit of the device's binary32 exp (device_exp_audit.c): the device
  * algorithm restated bit for bit, and an exhaustive scan of every binary32

@@ -116,12 +116,15 @@ def test_pre_commit_gather_bound_names_first_position():
 
 def test_row_grouping_is_declared_device_free():
     import tiler_amd
-    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 4096) == (8, 1)
-    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 8192) == (8, 1)
-    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 8193) == (8, 16)
-    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.F32, 100000) == (4, 16)
-    assert tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, 2048) == (4, 1)
-    assert tiler_amd.row_grouping(L.ROWS_SUM, L.F32, 10) == (4, 4)
+    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 4096) == (8, 1, 0)
+    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 8192) == (8, 1, 0)
+    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, 8193) == (8, 16, 0)
+    assert tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.F32, 100000) == (4, 16, 0)
+    assert tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, 2048) == (4, 1, 0)
+    assert tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, 8192) == (4, 1, 0)
+    assert tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, 8193) == (4, 4, 8192)
+    assert tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, 131072) == (4, 4, 8192)
+    assert tiler_amd.row_grouping(L.ROWS_SUM, L.F32, 10) == (4, 4, 0)
     with pytest.raises(tiler_amd.Refusal):
         tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.BF16, 2048)
     with pytest.raises(tiler_amd.Refusal):

@@ -63,7 +63,7 @@ def test_rms_norm_bf16(ctx, case):
     xb = oracle.bf16_narrow(r.standard_normal((rows, extent)).astype(np.float32))
     wb = oracle.bf16_narrow(r.normal(1.0, 0.1, extent).astype(np.float32))
     got = families.rms_norm_bf16(xb, wb, EPS, ctx=ctx)
-    vec, waves = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, extent)
+    vec, waves, _ = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, extent)
     y = oracle.rms_norm_grouped(bf16_widen(xb), bf16_widen(wb), rows, extent, EPS, True, vec, waves)
     assert np.array_equal(got, oracle.bf16_narrow(y).reshape(rows, extent)), (rows, extent)
 
@@ -77,8 +77,8 @@ def test_softmax(ctx, case):
     if extent > 3:
         x[0, r.integers(0, extent, extent // 3)] = -np.inf
     got = families.softmax_f32((rows, extent), 1, x, ctx=ctx).reshape(rows, extent)
-    vec, waves = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
-    want = oracle.softmax_grouped(x, rows, extent, vec, waves).reshape(rows, extent)
+    vec, waves, seg = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
+    want = oracle.softmax_grouped(x, rows, extent, vec, waves, seg).reshape(rows, extent)
     assert np.array_equal(bits(got), bits(want)), (rows, extent)
 
 

@@ -1,10 +1,15 @@
 """GPU: RMSNorm and softmax rows longer than one wave holds (> 8192 elements).
 
-One 1024-thread workgroup per row, register-resident up to 1024 x 8 chunks per
-row and streamed beyond; the fold order is the declared grouping
-tiler_hip_row_grouping reports (vec, waves 16), restated by the oracle's
-grouped forms (tiler-reference/src/rms_norm.rs:405-489, softmax.rs:200-315
-with that reassociation).  Bit-exact against the oracle on the same inputs.
+RMSNorm: one 1024-thread workgroup per row, register-resident up to 1024 x 8
+chunks per row and streamed beyond.  Softmax: the exponent sum folds by
+8192-element segments, run by one 1024-thread workgroup per row with the row
+in registers (up to 4 segments) or by one workgroup per segment in three
+launches (more segments; the partials in the context workspace up to 32768
+segments, allocated beyond).  The fold order is
+the declared grouping tiler_hip_row_grouping reports, restated by the
+oracle's grouped forms (tiler-reference/src/rms_norm.rs:405-489,
+softmax.rs:200-315 with that reassociation).  Bit-exact against the oracle on
+the same inputs, whichever form runs.
 """
 from __future__ import annotations
 
@@ -48,7 +53,7 @@ def test_rms_norm_bf16_long_rows(ctx, rows, extent, broadcast, offset):
     xb = oracle.bf16_narrow(rng.standard_normal((rows, extent)).astype(np.float32))
     wshape = (extent,) if broadcast else (rows, extent)
     wb = oracle.bf16_narrow(rng.normal(1.0, 0.1, wshape).astype(np.float32))
-    vec, waves = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, extent)
+    vec, waves, _ = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.BF16, extent)
     assert (vec, waves) == (8, 16)
     got = _dev_rms(ctx, L.BF16, xb, wb, rows, extent, broadcast, offset)
     y = oracle.rms_norm_grouped(bf16_widen(xb), bf16_widen(wb), rows, extent, EPS, broadcast, vec, waves)
@@ -60,21 +65,57 @@ def test_rms_norm_f32_long_rows(ctx, rows, extent):
     rng = np.random.default_rng(extent + 7)
     x = rng.standard_normal((rows, extent)).astype(np.float32)
     w = rng.normal(1.0, 0.1, (rows, extent)).astype(np.float32)
-    vec, waves = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.F32, extent)
+    vec, waves, _ = tiler_amd.row_grouping(L.ROWS_RMS_NORM, L.F32, extent)
     got = _dev_rms(ctx, L.F32, x, w, rows, extent, False)
     want = oracle.rms_norm_grouped(x, w, rows, extent, EPS, False, vec, waves).reshape(rows, extent)
     assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("rows,extent", [(4, 8196), (2, 20000), (2, 32768), (3, 50001)])
-def test_softmax_long_rows(ctx, rows, extent):
+def _form(rows, extent):
+    nseg = -(-extent // 8192)
+    return "resident" if nseg <= 4 else "split" if rows * nseg <= 32768 else "split, allocated partials"
+
+
+# Every launch form, aligned and element-wise (extent % 4, base offset).
+@pytest.mark.parametrize("rows,extent,offset", [
+    (4, 8196, 0), (2, 20000, 0), (2, 32768, 0), (140, 20001, 0), (1, 8193, 0),   # resident
+    (3, 50001, 0), (5, 131072, 1), (131, 50000, 0), (130, 90001, 1),              # split
+])
+def test_softmax_long_rows(ctx, rows, extent, offset):
     rng = np.random.default_rng(extent + 11)
     x = (rng.standard_normal((rows, extent)) * 3).astype(np.float32)
     x[0, ::7] = -np.inf                  # masked positions
     if rows > 2:
         x[2, extent // 2] = np.nan          # a NaN poisons its row
-    vec, waves = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
-    assert (vec, waves) == (4, 16)
+    if rows > 3:
+        x[3, :min(extent, 8192)] = -np.inf  # a whole segment masked
+    vec, waves, seg = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
+    assert (vec, waves, seg) == (4, 4, 8192)
+    print(f"softmax long rows={rows} extent={extent} offset={offset} form={_form(rows, extent)}", flush=True)
+    dx, dy = ctx.alloc(x.nbytes + 16), ctx.alloc(x.nbytes + 16)
+    try:
+        vx, vy = dx.offset(offset * 4), dy.offset(offset * 4)
+        vx.upload(x)
+        ctx.softmax_f32(vx, rows, extent, vy)
+        ctx.synchronize()
+        got = vy.download(np.float32, x.shape)
+    finally:
+        dx.free(); dy.free()
+    want = oracle.softmax_grouped(x, rows, extent, vec, waves, seg).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_softmax_split_with_allocated_partials(ctx):
+    # 6600 rows of 5 segments: 33000 segment partials exceed the 32768 the
+    # workspace holds, so the call allocates them on the stream.  Rows repeat
+    # 8 distinct inputs; every row must equal the oracle's for its input
+    # (rows are independent), checked on the 8 distinct rows and by equality.
+    rows, extent, distinct = 6600, 40960, 8
+    assert _form(rows, extent) == "split, allocated partials"
+    base = (np.random.default_rng(77).standard_normal((distinct, extent)) * 3).astype(np.float32)
+    base[1, 100:9000] = -np.inf
+    x = np.tile(base, (rows // distinct, 1))
+    print(f"softmax split allocated partials rows={rows} extent={extent}", flush=True)
     dx, dy = ctx.to_device(x), ctx.alloc(x.nbytes)
     try:
         ctx.softmax_f32(dx, rows, extent, dy)
@@ -82,8 +123,11 @@ def test_softmax_long_rows(ctx, rows, extent):
         got = dy.download(np.float32, x.shape)
     finally:
         dx.free(); dy.free()
-    want = oracle.softmax_grouped(x, rows, extent, vec, waves).reshape(rows, extent)
-    assert np.array_equal(bits(got), bits(want))
+    del x
+    want = oracle.softmax_grouped(base, distinct, extent, 4, 4, 8192).reshape(distinct, extent)
+    assert np.array_equal(bits(got[:distinct]), bits(want))
+    assert np.array_equal(got.reshape(rows // distinct, distinct, extent).view(np.uint32),
+                          np.broadcast_to(want.view(np.uint32), (rows // distinct, distinct, extent)))
 
 
 def test_long_row_softmax_matches_f64_within_tolerance(ctx):

@@ -105,14 +105,14 @@ def test_rms_norm_routed(ctx, dtype, rows, extent):
                           want.view(np.uint16 if dtype == L.BF16 else np.uint32))
 
 
-@pytest.mark.parametrize("rows,extent", [(64, 2048), (5, 300), (2, 40000)])
+@pytest.mark.parametrize("rows,extent", [(64, 2048), (5, 300), (2, 40000), (150, 20001)])
 def test_softmax_routed(ctx, rows, extent):
     x = (np.random.default_rng(extent).standard_normal((rows, extent)) * 3).astype(np.float32)
     rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), ctx=ctx)
     (got,) = _routed(ctx, rz, [x], [(np.float32, (rows, extent))])
     import tiler_amd
-    vec, waves = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
-    assert np.array_equal(bits(got).reshape(-1), bits(oracle.softmax_grouped(x, rows, extent, vec, waves)))
+    vec, waves, seg = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
+    assert np.array_equal(bits(got).reshape(-1), bits(oracle.softmax_grouped(x, rows, extent, vec, waves, seg)))
 
 
 @pytest.mark.parametrize("op,n", [(L.MAP_ADD, 4096), (L.MAP_MULTIPLY, 1001), (L.MAP_SILU, 8192), (L.MAP_SILU, 77)])

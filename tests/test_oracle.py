@@ -332,6 +332,43 @@ def test_grouped_rms_and_softmax_agree_with_strict_on_exact_inputs():
     assert np.all(bits(y) == 0x3DCCCCCD)
 
 
+def test_segmented_softmax_composes_the_pinned_fold():
+    # Each segment's partial is the pinned row-grouped fold of its exponents;
+    # the row total is their left fold; the scaling is softmax.rs's.
+    rng = np.random.default_rng(17)
+    rows, extent, seg = 2, 20000, 8192
+    x = (rng.standard_normal((rows, extent)) * 3).astype(np.float32)
+    got = oracle.softmax_grouped(x, rows, extent, 4, 4, seg).reshape(rows, extent)
+    for r in range(rows):
+        m = x[r, 0]
+        for v in x[r, 1:]:
+            m = oracle.maximum_f32(m, v)
+        e = np.array([oracle.certified_exp_f32(np.float32(v - np.float32(m))) for v in x[r]], np.float32)
+        d = None
+        for s0 in range(0, extent, seg):
+            part = oracle.row_grouped_sum(e[s0:s0 + seg], 1, min(seg, extent - s0), 4, 4)[0]
+            d = part if d is None else np.float32(d + part)
+        want = e * (np.float32(1.0) / d)
+        assert np.array_equal(bits(got[r]), bits(want))
+
+
+def test_segmented_softmax_special_cases():
+    rng = np.random.default_rng(18)
+    x = (rng.standard_normal((3, 9000)) * 4).astype(np.float32)
+    whole = oracle.softmax_grouped(x, 3, 9000, 4, 4)
+    # a segment at least the row, or 0, is the unsegmented fold
+    assert np.array_equal(bits(oracle.softmax_grouped(x, 3, 9000, 4, 4, 9000)), bits(whole))
+    assert np.array_equal(bits(oracle.softmax_grouped(x, 3, 9000, 4, 4, 1 << 20)), bits(whole))
+    assert np.array_equal(bits(oracle.softmax_grouped(x, 3, 9000, 4, 4, 0)), bits(whole))
+    # and a real split changes the association (on these seeds, some bit)
+    split = oracle.softmax_grouped(x, 3, 9000, 4, 4, 4096)
+    assert not np.array_equal(bits(split), bits(whole))
+    assert np.max(np.abs(split.astype(np.float64) - whole) / whole) < 1e-5
+    # exact inputs: every grouping gives the exact quotient
+    c = np.full((2, 20000), np.float32(0.5))
+    assert np.all(bits(oracle.softmax_grouped(c, 2, 20000, 4, 4, 8192)) == bits(np.float32(1 / 20000))[()])
+
+
 # -- gather ---------------------------------------------------------------------------
 
 def _geometry(shape, axis):

@@ -66,6 +66,30 @@ def test_rms_norm_headline_and_variants():
     _check_segments(long_row)
 
 
+def test_softmax_long_rows_choose_a_launch_form():
+    # Rows of more than 4 segments: one workgroup per 8192-element segment in
+    # three launches, the partials in two scratch slots of rows * segments
+    # f32.  Up to 4 segments: one workgroup per row, the row in registers.
+    sp = realize(L.PROGRAM_SOFTMAX, (32, 131072), flags=L.REGION_ALIGNED16)
+    assert sp.symbols == ["tiler_softmax_f32_split_max_a", "tiler_softmax_f32_split_sum_a",
+                          "tiler_softmax_f32_split_out_a"]
+    assert [d.grid for d in sp.dispatches] == [(16 * 32, 1, 1)] * 3
+    assert all(d.block == (256, 1, 1) for d in sp.dispatches)
+    assert sp.slots == [(L.SLOT_INPUT, 32 * 131072 * 4), (L.SLOT_OUTPUT, 32 * 131072 * 4),
+                        (L.SLOT_SCRATCH, 32 * 16 * 4), (L.SLOT_SCRATCH, 32 * 16 * 4)]
+    assert [sorted(s for s, _ in d.bindings) for d in sp.dispatches] == [[0, 2], [0, 2, 3], [0, 1, 2, 3]]
+    _check_segments(sp)
+    assert realize(L.PROGRAM_SOFTMAX, (3, 50001)).symbols[0] == "tiler_softmax_f32_split_max_u"
+    assert realize(L.PROGRAM_SOFTMAX, (1000, 32769)).symbols[0] == "tiler_softmax_f32_split_max_u"
+    res = realize(L.PROGRAM_SOFTMAX, (2, 32768), flags=L.REGION_ALIGNED16)
+    assert res.symbols == ["tiler_softmax_f32_long_r_a"] and res.dispatches[0].grid == (2, 1, 1)
+    assert res.dispatches[0].block == (1024, 1, 1) and len(res.slots) == 2
+    _check_segments(res)
+    assert realize(L.PROGRAM_SOFTMAX, (7, 8193)).symbols == ["tiler_softmax_f32_long_r_u"]
+    big = realize(L.PROGRAM_SOFTMAX, (100000, 65536), flags=L.REGION_ALIGNED16)
+    assert big.dispatches[0].grid == (800000, 1, 1) and big.slots[2] == (L.SLOT_SCRATCH, 3200000)
+
+
 def test_softmax_and_sums():
     sm = realize(L.PROGRAM_SOFTMAX, (65536, 2048))
     assert sm.symbols == ["tiler_softmax_f32_ch8_full"] and sm.dispatches[0].grid == (16384, 1, 1)

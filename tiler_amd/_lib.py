@@ -322,7 +322,8 @@ SIGNATURES = {
     "tiler_hip_graph_destroy": (_S, [_CTX, _P]),
     "tiler_hip_sum_f32": (_S, [_CTX, _P, _U64, _U64, _P, ctypes.POINTER(SumPlan), _P]),
     "tiler_hip_sum_tree_workgroups": (_U32, [_CTX, _U64]),
-    "tiler_hip_row_grouping": (_S, [_U32, _U32, _U64, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
+    "tiler_hip_row_grouping": (_S, [_U32, _U32, _U64, ctypes.POINTER(_U32), ctypes.POINTER(_U32),
+                                    ctypes.POINTER(_U64)]),
     "tiler_hip_rms_norm": (_S, [_CTX, _U32, _P, _P, _I32, _U64, _U64, _U32, _P, _P]),
     "tiler_hip_softmax_f32": (_S, [_CTX, _P, _U64, _U64, _P, _P]),
     "tiler_hip_map": (_S, [_CTX, _U32, _U32, _P, _P, _I32, _U64, _F, _F, _P, _P]),

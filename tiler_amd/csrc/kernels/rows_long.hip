@@ -2,17 +2,19 @@
 // (tiler-reference/src/rms_norm.rs:134-195, 453-489; softmax.rs:237-315), for
 // rows longer than one wave holds in registers (8192 elements).
 //
-// One 1024-thread workgroup (16 waves) per row.  Thread t owns the 16-byte
-// chunks t, t + 1024, t + 2048, ... of the row and folds their elements in
-// ascending position; each wave combines its lanes with the xor butterfly and
-// the 16 wave results are added in ascending wave order -- the declared
-// grouping (vec = elements per chunk, waves = 16) the oracle restates.
+// RMSNorm: one 1024-thread workgroup (16 waves) per row.  Thread t owns the
+// 16-byte chunks t, t + 1024, t + 2048, ... of the row and folds their
+// elements in ascending position; each wave combines its lanes with the xor
+// butterfly and the 16 wave results are added in ascending wave order -- the
+// declared grouping (vec = elements per chunk, waves = 16) the oracle
+// restates.  CH > 0: the row's chunks stay in registers between passes (CH
+// per thread, rows up to 1024 * CH chunks), so HBM sees each byte once.
+// CH == 0: rows of any length are streamed (read twice: fold, epilogue).
 //
-// CH > 0: the row's chunks stay in registers between passes (CH per thread,
-// rows up to 1024 * CH chunks), so HBM sees each byte once.  CH == 0: rows of
-// any length are streamed -- RMSNorm reads the row twice (fold, epilogue),
-// softmax three times (maximum, exponent sum, output; the exponent is
-// recomputed bit-identically in the last pass).
+// Softmax: the exponent sum folds by 8192-element segments (described at
+// softmax_f32_seg_row), so a row can also be split across workgroups when
+// there are too few rows to fill the device.
+//
 // AL: 1 when the row base and extent keep every chunk 16-byte aligned; 0 loads
 // and stores element by element in the same order.
 #include "common.h"
@@ -244,49 +246,185 @@ __device__ __forceinline__ f32x4 scale_chunk(f32x4 e, float r) {
   return f32x4{tiler::canon(e.x * r), tiler::canon(e.y * r), tiler::canon(e.z * r), tiler::canon(e.w * r)};
 }
 
-template <int CH, int AL>
-__device__ __forceinline__ void softmax_f32_long_row(const float* __restrict__ x, float* __restrict__ y,
-                                                     uint32_t extent, float* lds, const double* tab) {
+// Softmax rows longer than 8192 elements fold their exponent sum by segments
+// of kSegElems elements: lane l of a 256-thread group folds the segment's
+// 16-byte chunks l, l + 256, ..., l + 1792 in ascending position, each wave
+// combines its lanes with the butterfly, the segment's partial is its 4 wave
+// results added in ascending order, and the row total is the left fold of the
+// partials in ascending segment order (the grouping vec 4, waves 4, segment
+// 8192 that tiler_hip_row_grouping reports).  The same fold is computed by one
+// 1024-thread workgroup per row (rows of at most 4 segments, group g of 256
+// threads takes segment g) and by the split form (one 256-thread workgroup per
+// segment, three launches), so which one runs never changes a bit.
+constexpr uint32_t kSegThreads = 256;
+constexpr uint32_t kSegChunks = 8;                                 // per lane per segment
+constexpr uint64_t kSegChunkSpan = (uint64_t)kSegThreads * kSegChunks;  // 2048 chunks
+constexpr uint64_t kSegElems = kSegChunkSpan * 4;                  // 8192 elements
+
+// Folds the four group partials into `total` (groups g < `active` hold a
+// segment) and returns it; every thread of the 1024 gets it.
+__device__ __forceinline__ float seg_round_fold(float acc, uint32_t active, float* lds, float total) {
+  acc = tiler::wave_sum_butterfly(acc);
   const uint32_t t = threadIdx.x;
+  if ((t & 63u) == 0) lds[t >> 6] = acc;
+  __syncthreads();
+  for (uint32_t g = 0; g < active; ++g) {
+    float p = lds[4 * g];
+    p = p + lds[4 * g + 1];
+    p = p + lds[4 * g + 2];
+    p = p + lds[4 * g + 3];
+    total = total + p;  // total starts at -0.0: the first add is exact
+  }
+  __syncthreads();
+  return total;
+}
+
+// One 1024-thread workgroup per row of at most 4 segments: group g keeps
+// segment g in registers between the passes, so x is read once.
+template <int AL>
+__device__ __forceinline__ void softmax_f32_seg_row(const float* __restrict__ x, float* __restrict__ y,
+                                                    uint32_t extent, float* lds, const double* tab) {
+  const uint32_t t = threadIdx.x, g = t >> 8, l = t & 255u;
   const uint64_t chunks = (extent + 3u) / 4u;
+  const uint32_t nseg = (uint32_t)((extent + kSegElems - 1) / kSegElems);  // <= 4 (the planner's choice)
   const float ninf = -__builtin_huge_valf();
-  f32x4 xv[CH > 0 ? CH : 1];
+  f32x4 xv[kSegChunks];
   float m = ninf;
-  if (CH > 0) {
 #pragma unroll
-    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
-      const uint64_t q = t + (uint64_t)c * kLongThreads;
-      xv[c] = q < chunks ? load_f32_chunk<AL>(x, q, extent, ninf) : f32x4{ninf, ninf, ninf, ninf};
-    }
-#pragma unroll
-    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) m = max_chunk(m, xv[c]);
-  } else {
-    for (uint64_t q = t; q < chunks; q += kLongThreads) m = max_chunk(m, load_f32_chunk<AL>(x, q, extent, ninf));
+  for (uint32_t c = 0; c < kSegChunks; ++c) {
+    const uint64_t q = g * kSegChunkSpan + l + c * kSegThreads;
+    xv[c] = q < chunks ? load_f32_chunk<AL>(x, q, extent, ninf) : f32x4{ninf, ninf, ninf, ninf};
+    m = max_chunk(m, xv[c]);
   }
   m = long_block_max(m, lds);
   float acc = -0.0f;
-  if (CH > 0) {
 #pragma unroll
-    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
-      const uint64_t q = t + (uint64_t)c * kLongThreads;
-      xv[c] = exp_chunk(xv[c], m, tab);
-      if (q < chunks) acc = fold_chunk(acc, xv[c], q, extent);
-    }
-  } else {
-    for (uint64_t q = t; q < chunks; q += kLongThreads)
-      acc = fold_chunk(acc, exp_chunk(load_f32_chunk<AL>(x, q, extent, ninf), m, tab), q, extent);
+  for (uint32_t c = 0; c < kSegChunks; ++c) {
+    const uint64_t q = g * kSegChunkSpan + l + c * kSegThreads;
+    xv[c] = exp_chunk(xv[c], m, tab);
+    if (q < chunks) acc = fold_chunk(acc, xv[c], q, extent);
   }
-  const float d = long_block_sum(acc, lds);
-  const float r = 1.0f / d;
-  if (CH > 0) {
+  const float total = seg_round_fold(acc, nseg < 4 ? nseg : 4u, lds, -0.0f);
+  const float r = 1.0f / total;
 #pragma unroll
-    for (int c = 0; c < (CH > 0 ? CH : 1); ++c) {
-      const uint64_t q = t + (uint64_t)c * kLongThreads;
-      if (q < chunks) store_f32_chunk<AL>(y, q, extent, scale_chunk(xv[c], r));
-    }
-  } else {
-    for (uint64_t q = t; q < chunks; q += kLongThreads)
-      store_f32_chunk<AL>(y, q, extent, scale_chunk(exp_chunk(load_f32_chunk<AL>(x, q, extent, ninf), m, tab), r));
+  for (uint32_t c = 0; c < kSegChunks; ++c) {
+    const uint64_t q = g * kSegChunkSpan + l + c * kSegThreads;
+    if (q < chunks) store_f32_chunk<AL>(y, q, extent, scale_chunk(xv[c], r));
+  }
+}
+
+// ---- split form: one 256-thread workgroup per segment -------------------------
+// Workgroup b takes segment b % nseg of row b / nseg (a flat grid, so any
+// row count launches).
+__device__ __forceinline__ float seg_block_max(float v, float* lds) {
+  v = tiler::wave_max(v);
+  const uint32_t t = threadIdx.x;
+  if ((t & 63u) == 0) lds[t >> 6] = v;
+  __syncthreads();
+  float m = lds[0];
+  m = tiler::maximum_f32(m, lds[1]);
+  m = tiler::maximum_f32(m, lds[2]);
+  m = tiler::maximum_f32(m, lds[3]);
+  __syncthreads();
+  return m;
+}
+
+// The row maximum from its segment maxima (the maximum is order-free), per
+// wave: no barrier, so the segment's loads issued before it stay in flight.
+__device__ __forceinline__ float row_max_of(const float* __restrict__ pmax, uint64_t nseg) {
+  float m = -__builtin_huge_valf();
+  for (uint64_t j = threadIdx.x & 63u; j < nseg; j += 64) m = tiler::maximum_f32(m, pmax[j]);
+  return tiler::wave_max(m);
+}
+
+// The row's exponent sum: the left fold of its segment partials in ascending
+// order, seeded by the first.  Each wave loads 64 partials at a time (one per
+// lane) and folds them in lane order.
+__device__ __forceinline__ float row_sum_of(const float* __restrict__ psum, uint64_t nseg) {
+  const uint32_t lane = threadIdx.x & 63u;
+  float d = -0.0f;  // -0.0 + p == p: the fold is seeded by the first partial
+  for (uint64_t j0 = 0; j0 < nseg; j0 += 64) {
+    const float v = j0 + lane < nseg ? psum[j0 + lane] : 0.0f;
+    const uint32_t n = nseg - j0 < 64 ? (uint32_t)(nseg - j0) : 64u;
+    for (uint32_t k = 0; k < n; ++k)
+      d = d + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+  }
+  return d;
+}
+
+template <int AL>
+__device__ __forceinline__ void load_segment(const float* __restrict__ x, uint64_t sg, uint64_t chunks,
+                                             uint32_t extent, f32x4 (&xv)[kSegChunks]) {
+  const float ninf = -__builtin_huge_valf();
+#pragma unroll
+  for (uint32_t c = 0; c < kSegChunks; ++c) {
+    const uint64_t q = sg * kSegChunkSpan + threadIdx.x + c * kSegThreads;
+    xv[c] = q < chunks ? load_f32_chunk<AL>(x, q, extent, ninf) : f32x4{ninf, ninf, ninf, ninf};
+  }
+}
+
+// Split pass 1: pmax[row * nseg + s] = the maximum of segment s.
+template <int AL>
+__device__ __forceinline__ void softmax_split_max(const float* __restrict__ x, uint32_t extent, uint64_t nseg,
+                                                  float* __restrict__ pmax) {
+  __shared__ float lds[4];
+  const uint64_t row = blockIdx.x / nseg, sg = blockIdx.x % nseg;
+  const uint64_t chunks = (extent + 3u) / 4u;
+  f32x4 xv[kSegChunks];
+  load_segment<AL>(x + row * extent, sg, chunks, extent, xv);
+  float m = -__builtin_huge_valf();
+#pragma unroll
+  for (uint32_t c = 0; c < kSegChunks; ++c) m = max_chunk(m, xv[c]);
+  m = seg_block_max(m, lds);
+  if (threadIdx.x == 0) pmax[row * nseg + sg] = m;
+}
+
+// Split pass 2: psum[row * nseg + s] = segment s's partial of the exponent sum.
+template <int AL>
+__device__ __forceinline__ void softmax_split_sum(const float* __restrict__ x, uint32_t extent, uint64_t nseg,
+                                                  const float* __restrict__ pmax, float* __restrict__ psum,
+                                                  const double* tab) {
+  __shared__ float lds[4];
+  const uint64_t row = blockIdx.x / nseg, sg = blockIdx.x % nseg;
+  const uint64_t chunks = (extent + 3u) / 4u;
+  f32x4 xv[kSegChunks];
+  load_segment<AL>(x + row * extent, sg, chunks, extent, xv);
+  const float m = row_max_of(pmax + row * nseg, nseg);
+  float acc = -0.0f;
+#pragma unroll
+  for (uint32_t c = 0; c < kSegChunks; ++c) {
+    const uint64_t q = sg * kSegChunkSpan + threadIdx.x + c * kSegThreads;
+    if (q < chunks) acc = fold_chunk(acc, exp_chunk(xv[c], m, tab), q, extent);
+  }
+  acc = tiler::wave_sum_butterfly(acc);
+  if ((threadIdx.x & 63u) == 0) lds[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float p = lds[0];
+    p = p + lds[1];
+    p = p + lds[2];
+    p = p + lds[3];
+    psum[row * nseg + sg] = p;
+  }
+}
+
+// Split pass 3: y = canon(exp(x - m) * (1 / d)), d the left fold of the row's
+// partials in ascending segment order.
+template <int AL>
+__device__ __forceinline__ void softmax_split_out(const float* __restrict__ x, float* __restrict__ y,
+                                                  uint32_t extent, uint64_t nseg, const float* __restrict__ pmax,
+                                                  const float* __restrict__ psum, const double* tab) {
+  const uint64_t row = blockIdx.x / nseg, sg = blockIdx.x % nseg;
+  const uint64_t chunks = (extent + 3u) / 4u;
+  f32x4 xv[kSegChunks];
+  load_segment<AL>(x + row * extent, sg, chunks, extent, xv);
+  const float m = row_max_of(pmax + row * nseg, nseg);
+  const float r = 1.0f / row_sum_of(psum + row * nseg, nseg);
+  float* yr = y + row * extent;
+#pragma unroll
+  for (uint32_t c = 0; c < kSegChunks; ++c) {
+    const uint64_t q = sg * kSegChunkSpan + threadIdx.x + c * kSegThreads;
+    if (q < chunks) store_f32_chunk<AL>(yr, q, extent, scale_chunk(exp_chunk(xv[c], m, tab), r));
   }
 }
 
@@ -314,18 +452,43 @@ __device__ __forceinline__ void softmax_f32_long_row(const float* __restrict__ x
     rms_f32_long_row<CH, AL>(x + row * extent, w + row * w_row_stride, y + row * extent, extent, \
                              eps, lds);                                                           \
   }
-#define TILER_SOFTMAX_F32_LONG(CH, AL, SFX)                                                     \
-  extern "C" __global__ void __launch_bounds__(1024) tiler_softmax_f32_long##CH##SFX(           \
-      const float* __restrict__ x, float* __restrict__ y, uint32_t extent) {                     \
-    __shared__ float lds[kLongWaves];                                                            \
-    __shared__ double tab[64];                                                                   \
-    if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Table64[threadIdx.x];                          \
-    __syncthreads();                                                                             \
-    const uint64_t row = blockIdx.x;                                                             \
-    softmax_f32_long_row<CH, AL>(x + row * extent, y + row * extent, extent, lds, tab);         \
-  }
 #define TILER_LONG_FAMILY(M) M(1, 1, _a) M(1, 0, _u) M(2, 1, _a) M(2, 0, _u) M(4, 1, _a) M(4, 0, _u) \
   M(8, 1, _a) M(8, 0, _u) M(0, 1, _a) M(0, 0, _u)
 TILER_LONG_FAMILY(TILER_RMS_BF16_LONG)
 TILER_LONG_FAMILY(TILER_RMS_F32_LONG)
-TILER_LONG_FAMILY(TILER_SOFTMAX_F32_LONG)
+
+// Softmax rows longer than 8192 elements (the segmented fold above).
+// tiler_softmax_f32_long_r{_a,_u}: blockIdx.x is the row, 1024 threads, rows
+// of at most 4 segments.  tiler_softmax_f32_split_{max,sum,out}{_a,_u}: a flat
+// grid of rows * nseg workgroups of 256 threads; pmax and psum hold
+// rows * nseg partials.
+#define TILER_SOFTMAX_TAB                                              \
+  __shared__ double tab[64];                                           \
+  if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Table64[threadIdx.x];  \
+  __syncthreads();
+#define TILER_SOFTMAX_F32_SEG(AL, SFX)                                                                     \
+  extern "C" __global__ void __launch_bounds__(1024) tiler_softmax_f32_long_r##SFX(                       \
+      const float* __restrict__ x, float* __restrict__ y, uint32_t extent) {                              \
+    __shared__ float lds[kLongWaves];                                                                     \
+    TILER_SOFTMAX_TAB                                                                                     \
+    const uint64_t row = blockIdx.x;                                                                      \
+    softmax_f32_seg_row<AL>(x + row * extent, y + row * extent, extent, lds, tab);                     \
+  }                                                                                                       \
+  extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_split_max##SFX(                     \
+      const float* __restrict__ x, uint32_t extent, uint64_t nseg, float* __restrict__ pmax) {            \
+    softmax_split_max<AL>(x, extent, nseg, pmax);                                                         \
+  }                                                                                                       \
+  extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_split_sum##SFX(                     \
+      const float* __restrict__ x, uint32_t extent, uint64_t nseg, const float* __restrict__ pmax,        \
+      float* __restrict__ psum) {                                                                         \
+    TILER_SOFTMAX_TAB                                                                                     \
+    softmax_split_sum<AL>(x, extent, nseg, pmax, psum, tab);                                              \
+  }                                                                                                       \
+  extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_split_out##SFX(                     \
+      const float* __restrict__ x, float* __restrict__ y, uint32_t extent, uint64_t nseg,                 \
+      const float* __restrict__ pmax, const float* __restrict__ psum) {                                   \
+    TILER_SOFTMAX_TAB                                                                                     \
+    softmax_split_out<AL>(x, y, extent, nseg, pmax, psum, tab);                                           \
+  }
+TILER_SOFTMAX_F32_SEG(1, _a)
+TILER_SOFTMAX_F32_SEG(0, _u)

@@ -25,6 +25,12 @@ constexpr uint32_t kMaxBindings = 6;
 constexpr uint32_t kMaxSlots = 6;
 constexpr uint32_t kMaxLaunches = 4;
 constexpr uint32_t kMaxSumWorkgroups = 4096;
+// Bytes of partials a context keeps in its workspace (the sum's partials, the
+// split softmax's segment maxima and sums); larger scratch is allocated.
+constexpr uint64_t kWorkspacePartialBytes = 256 * 1024;
+// Softmax rows longer than kWaveRowMax fold by segments of this many elements.
+constexpr uint64_t kWaveRowMax = 8192;
+constexpr uint64_t kSoftmaxSegment = 8192;
 
 // Slot roles, as tiler_hip_realization reports them.
 constexpr uint32_t kSlotInput = TILER_HIP_SLOT_INPUT;

@@ -120,16 +120,14 @@ const EntryRow kEntries[] = {
     {"tiler_rms_norm_f32_long8_u", "rms-norm-f32/long-row", 3},
     {"tiler_rms_norm_f32_long0_a", "rms-norm-f32/long-row", 3},
     {"tiler_rms_norm_f32_long0_u", "rms-norm-f32/long-row", 3},
-    {"tiler_softmax_f32_long1_a", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long1_u", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long2_a", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long2_u", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long4_a", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long4_u", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long8_a", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long8_u", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long0_a", "softmax-f32/long-row", 2},
-    {"tiler_softmax_f32_long0_u", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long_r_a", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_long_r_u", "softmax-f32/long-row", 2},
+    {"tiler_softmax_f32_split_max_a", "softmax-f32/split-row", 2},
+    {"tiler_softmax_f32_split_max_u", "softmax-f32/split-row", 2},
+    {"tiler_softmax_f32_split_sum_a", "softmax-f32/split-row", 3},
+    {"tiler_softmax_f32_split_sum_u", "softmax-f32/split-row", 3},
+    {"tiler_softmax_f32_split_out_a", "softmax-f32/split-row", 4},
+    {"tiler_softmax_f32_split_out_u", "softmax-f32/split-row", 4},
     {"tiler_gather_u128", "gather", 4},
     {"tiler_gather_u64", "gather", 4},
     {"tiler_gather_u32", "gather", 4},
@@ -202,7 +200,7 @@ struct tiler_hip_context {
   std::unordered_map<std::string, hipFunction_t> fns;
   std::vector<hipModule_t> routed_modules;
   std::vector<hipFunction_t> prepared;
-  // workspace: [sum partials kMaxSumWorkgroups f32][gather_bad u64 + pad]
+  // workspace: [partials kWorkspacePartialBytes][gather_bad u64 + pad]
   uint8_t* workspace = nullptr;
   float* sum_partials = nullptr;
   unsigned long long* gather_bad = nullptr;
@@ -244,9 +242,9 @@ tiler_hip_status launch(tiler_hip_context* ctx, const char* symbol, uint32_t gx,
   return TILER_HIP_OK;
 }
 
-// Rows longer than one wave holds run one workgroup per row (the grouping
-// tiler_hip_row_grouping reports).
-constexpr uint64_t kWaveRowMax = 8192;
+// Rows longer than one wave holds run one workgroup per row, softmax's by
+// segments (the grouping tiler_hip_row_grouping reports).
+using tiler_rt::kWaveRowMax;
 
 tiler_rt::Target target_of(const tiler_hip_context* ctx) {
   return tiler_rt::Target{ctx ? ctx->compute_units : kProfileComputeUnits};
@@ -645,7 +643,7 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
     }
     ctx->fns[kEntries[i].symbol] = f;
   }
-  const uint64_t ws_bytes = kMaxSumWorkgroups * 4 + 256;
+  const uint64_t ws_bytes = tiler_rt::kWorkspacePartialBytes + 256;
   if (hipMalloc(&ctx->workspace, ws_bytes) != hipSuccess) {
     copy_text(diagnostic, diagnostic_bytes, "workspace allocation failed");
     hipModuleUnload(ctx->module);
@@ -654,7 +652,7 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
     return TILER_HIP_REFUSE_CAPACITY;
   }
   ctx->sum_partials = reinterpret_cast<float*>(ctx->workspace);
-  ctx->gather_bad = reinterpret_cast<unsigned long long*>(ctx->workspace + kMaxSumWorkgroups * 4);
+  ctx->gather_bad = reinterpret_cast<unsigned long long*>(ctx->workspace + tiler_rt::kWorkspacePartialBytes);
   hipMemset(ctx->workspace, 0, ws_bytes);
   hipMemset(ctx->gather_bad, 0xff, 8);
   hipDeviceSynchronize();
@@ -1033,8 +1031,9 @@ tiler_hip_status tiler_hip_graph_destroy(tiler_hip_context* ctx, tiler_hip_graph
 
 // ---------------------------------------------------------------------------
 tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_t extent,
-                                        uint32_t* vec, uint32_t* waves) {
-  if (!vec || !waves) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+                                        uint32_t* vec, uint32_t* waves, uint64_t* segment) {
+  if (!vec || !waves || !segment) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  *segment = 0;
   switch (family) {
     case TILER_HIP_ROWS_RMS_NORM:
       if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16) return TILER_HIP_REFUSE_UNSUPPORTED;
@@ -1044,7 +1043,8 @@ tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_
     case TILER_HIP_ROWS_SOFTMAX:
       if (dtype != TILER_HIP_F32) return TILER_HIP_REFUSE_UNSUPPORTED;
       *vec = 4;
-      *waves = extent > kWaveRowMax ? 16 : 1;
+      *waves = extent > kWaveRowMax ? 4 : 1;
+      *segment = extent > kWaveRowMax ? tiler_rt::kSoftmaxSegment : 0;
       return TILER_HIP_OK;
     case TILER_HIP_ROWS_SUM:
       if (dtype != TILER_HIP_F32) return TILER_HIP_REFUSE_UNSUPPORTED;
@@ -1075,7 +1075,7 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
   // stream); only larger splits allocate, stream-ordered.
   bool own = false;
   if (p.nslots > 2 && p.nlaunches) {
-    if (p.slot_bytes[2] <= (uint64_t)kMaxSumWorkgroups * 4) {
+    if (p.slot_bytes[2] <= tiler_rt::kWorkspacePartialBytes) {
       slots[2] = ctx->sum_partials;
     } else {
       if (hipMallocAsync(&slots[2], p.slot_bytes[2], s) != hipSuccess)
@@ -1110,8 +1110,28 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
   tiler_hip_status st = tiler_rt::plan_softmax_f32(rows, extent, addr, p);
   if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
   if (p.nlaunches && (!x || !y)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipStream_t s = pick(ctx, stream);
   void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(x), y};
-  return run_program(ctx, p, slots, pick(ctx, stream));
+  // The split form's partials (segment maxima, then sums) live in the context
+  // workspace when they fit (ordered on the stream); larger ones are
+  // allocated, stream-ordered.
+  bool own = false;
+  uint8_t* part = nullptr;
+  if (p.nslots > 2) {
+    const uint64_t bytes = p.slot_bytes[2] + p.slot_bytes[3];
+    if (bytes <= tiler_rt::kWorkspacePartialBytes) {
+      part = reinterpret_cast<uint8_t*>(ctx->sum_partials);
+    } else {
+      if (hipMallocAsync(reinterpret_cast<void**>(&part), bytes, s) != hipSuccess)
+        return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "partials allocation failed");
+      own = true;
+    }
+    slots[2] = part;
+    slots[3] = part + p.slot_bytes[2];
+  }
+  st = run_program(ctx, p, slots, s);
+  if (own) hipFreeAsync(part, s);
+  return st;
 }
 
 tiler_hip_status tiler_hip_map(tiler_hip_context* ctx, uint32_t op, uint32_t dtype,

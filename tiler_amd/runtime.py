@@ -285,12 +285,13 @@ class Context:
                                                     _ptr(c), epilogue, stream), "contract_bf16")
 
 
-def row_grouping(family: int, dtype: int, extent: int) -> tuple[int, int]:
-    """The declared (vec, waves) grouping the row kernels use for `extent`."""
-    vec, waves = ctypes.c_uint32(), ctypes.c_uint32()
-    _raise(L.lib().tiler_hip_row_grouping(family, dtype, extent, ctypes.byref(vec), ctypes.byref(waves)),
-           "row_grouping")
-    return vec.value, waves.value
+def row_grouping(family: int, dtype: int, extent: int) -> tuple[int, int, int]:
+    """The declared (vec, waves, segment) grouping the row kernels use for
+    `extent` (segment 0: the row folds whole)."""
+    vec, waves, segment = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
+    _raise(L.lib().tiler_hip_row_grouping(family, dtype, extent, ctypes.byref(vec), ctypes.byref(waves),
+                                          ctypes.byref(segment)), "row_grouping")
+    return vec.value, waves.value, segment.value
 
 
 def validate_gather_index(index: np.ndarray, gathered: int, index_signed: bool):
