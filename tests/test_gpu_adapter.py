@@ -149,3 +149,45 @@ def test_graph_replay_matches_eager_on_every_replay(ctx):
     finally:
         for b in (dx, dw, dy, ds, dso):
             b.free()
+
+
+def test_graph_replay_of_split_softmax(ctx):
+    # 4 rows of 7 segments: the split form's three launches, partials in the
+    # context workspace, captured and replayed; every replay matches eager.
+    rows, extent = 4, 50001
+    x = (np.random.default_rng(64).standard_normal((rows, extent)) * 3).astype(np.float32)
+    dx, dy = ctx.to_device(x), ctx.alloc(x.nbytes)
+    try:
+        ctx.softmax_f32(dx, rows, extent, dy)
+        ctx.synchronize()
+        eager = dy.download(np.float32, x.shape)
+        assert np.array_equal(bits(eager).reshape(-1), bits(oracle.softmax_grouped(x, rows, extent, 4, 4, 8192)))
+        ctx.capture_begin()
+        ctx.softmax_f32(dx, rows, extent, dy)
+        graph = ctx.capture_end()
+        for _ in range(4):
+            ctx.fill_u32(dy, 0, x.size)
+            ctx.synchronize()
+            ctx.graph_launch(graph)
+            ctx.synchronize()
+            assert np.array_equal(bits(dy.download(np.float32, x.shape)), bits(eager))
+        ctx.graph_destroy(graph)
+    finally:
+        dx.free(); dy.free()
+
+
+def test_split_softmax_needing_allocation_refuses_under_capture(ctx):
+    # 6600 x 40960 needs 33000 segment partials, beyond the workspace: eager it
+    # allocates them on the stream; under capture it refuses before any launch
+    # (the buffers are full size all the same).
+    rows, extent = 6600, 40960
+    dx, dy = ctx.alloc(rows * extent * 4), ctx.alloc(rows * extent * 4)
+    try:
+        ctx.capture_begin()
+        with pytest.raises(tiler_amd.Refusal):
+            ctx.softmax_f32(dx, rows, extent, dy)
+        ctx.fill_u32(dy, 0, 16)
+        graph = ctx.capture_end()
+        ctx.graph_destroy(graph)
+    finally:
+        dx.free(); dy.free()

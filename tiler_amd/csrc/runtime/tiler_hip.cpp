@@ -246,6 +246,13 @@ tiler_hip_status launch(tiler_hip_context* ctx, const char* symbol, uint32_t gx,
 // segments (the grouping tiler_hip_row_grouping reports).
 using tiler_rt::kWaveRowMax;
 
+// Partials beyond the workspace are allocated on the stream; under graph
+// capture that would record an allocation node, so such calls refuse there.
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 tiler_rt::Target target_of(const tiler_hip_context* ctx) {
   return tiler_rt::Target{ctx ? ctx->compute_units : kProfileComputeUnits};
 }
@@ -1078,6 +1085,8 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
     if (p.slot_bytes[2] <= tiler_rt::kWorkspacePartialBytes) {
       slots[2] = ctx->sum_partials;
     } else {
+      if (capturing(s))
+        return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "partials exceed the workspace under graph capture");
       if (hipMallocAsync(&slots[2], p.slot_bytes[2], s) != hipSuccess)
         return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "partials allocation failed");
       own = true;
@@ -1122,6 +1131,8 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
     if (bytes <= tiler_rt::kWorkspacePartialBytes) {
       part = reinterpret_cast<uint8_t*>(ctx->sum_partials);
     } else {
+      if (capturing(s))
+        return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "partials exceed the workspace under graph capture");
       if (hipMallocAsync(reinterpret_cast<void**>(&part), bytes, s) != hipSuccess)
         return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "partials allocation failed");
       own = true;
