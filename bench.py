@@ -245,11 +245,11 @@ class Softmax(Workload):
 
 class SoftmaxDecode(Workload):
     """Few long rows: f32 [32 heads x 131072 keys] softmax over the keys (the
-    shape of decode-attention scores).  16 segments a row, so the split form
-    runs (three launches over 512 workgroups); 16 buffer sets (512 MiB)
-    keep the working set out of the 256 MB last-level cache."""
+    shape of decode-attention scores).  16 segments a row, 512 workgroups:
+    the row-synchronized form runs (one launch, x read once); 16 buffer sets
+    (512 MiB) keep the working set out of the 256 MB last-level cache."""
     name = "softmax_decode"
-    kernel = "tiler_softmax_f32_split_out_a"
+    kernel = "tiler_softmax_f32_rowsync_a"
     rows, extent = 32, 131072
     sets = 16
 

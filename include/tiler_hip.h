@@ -430,10 +430,15 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context *ctx, uint32_t dtype, cons
 /* Softmax over the last axis with the governed-maximum shift (softmax-f32@1;
  * tiler-reference/src/softmax.rs:200-315).  Rows longer than 8192 elements
  * fold their exponent sum by segments (tiler_hip_row_grouping); rows of more
- * than 4 segments run each segment in a workgroup of its own, the segment
- * partials in the context's workspace (up to 32768 segments; more are
- * allocated on the stream), so such calls on different streams of one
- * context must not run concurrently. */
+ * than 4 segments run each segment in a workgroup of its own.  Up to 2
+ * workgroups per CU they synchronize through words in the context's
+ * workspace (one launch; waits bounded by 200 us, or by the
+ * TILER_HIP_ROW_SYNC_WAIT_TICKS environment variable at bind, in 100 MHz
+ * ticks, after which a workgroup computes its row's maximum and sum from the
+ * row itself); beyond that they run three launches with the segment partials
+ * in the workspace (up to 32768 segments; more are allocated on the stream).
+ * Either way such calls on different streams of one context must not run
+ * concurrently. */
 tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context *ctx, const float *x, uint64_t rows,
                                        uint64_t extent, float *y, tiler_hip_stream stream);
 

@@ -38,7 +38,7 @@ int main() {
   std::mt19937_64 r(20261201);
   uint64_t planned = 0;
   for (int it = 0; it < 20000; ++it) {
-    const Target t{(uint32_t)(1 + r() % 512)};
+    const Target t{(uint32_t)(1 + r() % 512), 20000};
     const uintptr_t addr[kMaxSlots] = {r() % 2 ? 0u : 1u, r() % 2 ? 0u : 4u, 0, 16, 2, 0};
     const Mode mode = r() % 2 ? Mode::Direct : Mode::Realized;
     uint64_t dims[8], strides[8];
@@ -56,7 +56,7 @@ int main() {
     plan_sum_f32(t, pick(r), pick(r), sp, addr, p[0]);
     plan_rms_norm((uint32_t)(r() % 3), (int32_t)(r() % 2), pick(r), pick(r), r() % 2 ? 0x3727C5ACu : (uint32_t)r(),
                   addr, p[1]);
-    plan_softmax_f32(pick(r), pick(r), addr, p[2]);
+    plan_softmax_f32(r() % 2 ? Mode::Direct : Mode::Realized, t, pick(r), pick(r), addr, p[2]);
     plan_map(mode, (uint32_t)(r() % 5), (uint32_t)(r() % 3), (int32_t)(r() % 2), pick(r), 1.0f, 2.0f, addr, p[3]);
     plan_broadcast(pick(r), (uint32_t)(r() % 10) % 9, dims, strides, (uint32_t)(r() % 6), p[4]);
     plan_gather(mode, pick(r), pick(r), pick(r), (uint32_t)(r() % 17), pick(r), (int32_t)(r() % 2), addr, p[5]);

@@ -3,9 +3,10 @@
 RMSNorm: one 1024-thread workgroup per row, register-resident up to 1024 x 8
 chunks per row and streamed beyond.  Softmax: the exponent sum folds by
 8192-element segments, run by one 1024-thread workgroup per row with the row
-in registers (up to 4 segments) or by one workgroup per segment in three
-launches (more segments; the partials in the context workspace up to 32768
-segments, allocated beyond).  The fold order is
+in registers (up to 4 segments), or by one workgroup per segment: in one
+row-synchronized launch when rows x segments <= 2 x CUs, else in three
+launches (the partials in the context workspace up to 32768 segments,
+allocated beyond).  The fold order is
 the declared grouping tiler_hip_row_grouping reports, restated by the
 oracle's grouped forms (tiler-reference/src/rms_norm.rs:405-489,
 softmax.rs:200-315 with that reassociation).  Bit-exact against the oracle on
@@ -71,9 +72,13 @@ def test_rms_norm_f32_long_rows(ctx, rows, extent):
     assert np.array_equal(bits(got), bits(want))
 
 
-def _form(rows, extent):
+def _form(rows, extent, cus=256):
     nseg = -(-extent // 8192)
-    return "resident" if nseg <= 4 else "split" if rows * nseg <= 32768 else "split, allocated partials"
+    if nseg <= 4:
+        return "resident"
+    if rows * nseg <= min(2 * cus, 1024):
+        return "row-synchronized"
+    return "split" if rows * nseg <= 32768 else "split, allocated partials"
 
 
 # Every launch form, aligned and element-wise (extent % 4, base offset).
@@ -91,7 +96,7 @@ def test_softmax_long_rows(ctx, rows, extent, offset):
         x[3, :min(extent, 8192)] = -np.inf  # a whole segment masked
     vec, waves, seg = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
     assert (vec, waves, seg) == (4, 4, 8192)
-    print(f"softmax long rows={rows} extent={extent} offset={offset} form={_form(rows, extent)}", flush=True)
+    print(f"softmax long rows={rows} extent={extent} offset={offset} form={_form(rows, extent, ctx.observe_live_device('compute-units'))}", flush=True)
     dx, dy = ctx.alloc(x.nbytes + 16), ctx.alloc(x.nbytes + 16)
     try:
         vx, vy = dx.offset(offset * 4), dy.offset(offset * 4)
@@ -144,3 +149,33 @@ def test_long_row_softmax_matches_f64_within_tolerance(ctx):
     e = np.exp(x64 - x64.max(axis=1, keepdims=True))
     ref = e / e.sum(axis=1, keepdims=True)
     assert float((np.abs(got - ref) / ref).max()) <= 1e-5
+
+
+def test_row_synchronized_softmax_fallback_matches(ctx):
+    # With the wait bound at 0 ticks no workgroup waits for its row: each one
+    # computes the row maximum and sum from the row itself.  The result is the
+    # same segmented fold, bit for bit, as the waiting form and the oracle.
+    import os
+    rows, extent = 3, 70001
+    assert _form(rows, extent, ctx.observe_live_device("compute-units")) == "row-synchronized"
+    x = (np.random.default_rng(91).standard_normal((rows, extent)) * 3).astype(np.float32)
+    x[1, 9000:20000] = -np.inf
+    want = oracle.softmax_grouped(x, rows, extent, 4, 4, 8192).reshape(rows, extent)
+    os.environ["TILER_HIP_ROW_SYNC_WAIT_TICKS"] = "0"
+    try:
+        c0 = tiler_amd.Context(0)
+    finally:
+        del os.environ["TILER_HIP_ROW_SYNC_WAIT_TICKS"]
+    try:
+        for c in (c0, ctx):
+            dx, dy = c.to_device(x), c.alloc(x.nbytes)
+            try:
+                for _ in range(3):  # the counters return to zero after every call
+                    c.fill_u32(dy, 0, x.size)
+                    c.softmax_f32(dx, rows, extent, dy)
+                    c.synchronize()
+                    assert np.array_equal(bits(dy.download(np.float32, x.shape)), bits(want))
+            finally:
+                dx.free(); dy.free()
+    finally:
+        c0.close()

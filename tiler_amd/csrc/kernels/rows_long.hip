@@ -428,6 +428,180 @@ __device__ __forceinline__ void softmax_split_out(const float* __restrict__ x, f
   }
 }
 
+// ---- row-synchronized form: one launch -----------------------------------------
+// The split form's three passes in one kernel: each 256-thread workgroup keeps
+// its segment in registers, publishes its segment maximum, reads every
+// maximum of its row, publishes its segment partial and reads every partial
+// of its row.  A published value is one 64-bit word, (tag << 32) | bits,
+// written and polled with relaxed agent-scope atomics: a word is valid when
+// its tag is this call's, so no ordering between locations (and no cache
+// write-back) is needed.  The tag is the epoch word + 1; the last workgroup
+// of the call to publish its partial (every workgroup has read the epoch by
+// then) stores the tag as the next epoch, so earlier calls' words never
+// match.  A wait is bounded (`wait_ticks` of the 100 MHz real-time clock); a
+// workgroup whose wait runs out computes the row maximum, or the row sum with
+// the same segment fold, from the row itself, so results never depend on the
+// workgroups being resident together -- only the speed does.
+//
+// sync: u32 epoch, u32 count, pad to 256 bytes, then u64 words for the
+// maxima [rows * nseg] and the partials [rows * nseg].
+constexpr uint32_t kRowSyncHeaderBytes = 256;
+
+// Wave 0 only: the row's nseg words of this call's tag, 64 per lane group in
+// ascending order, combined into the row maximum (sum == false; order-free)
+// or the left fold of the partials in ascending segment order (sum == true).
+// Returns false when the wait bound runs out first.
+__device__ __forceinline__ bool collect_row(const uint64_t* words, uint64_t nseg, uint32_t tag,
+                                            uint64_t wait_ticks, bool sum, float* out) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint64_t t0 = wall_clock64();
+  float acc = sum ? -0.0f : -__builtin_huge_valf();  // -0.0 + p == p: seeded by the first
+  for (uint64_t j0 = 0; j0 < nseg; j0 += 64) {
+    const uint64_t j = j0 + lane;
+    uint64_t v = 0;
+    bool have = j >= nseg;
+    while (true) {
+      if (!have) {
+        v = __hip_atomic_load(&words[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        have = (uint32_t)(v >> 32) == tag;
+      }
+      if (__all(have)) break;
+      if (wall_clock64() - t0 >= wait_ticks) return false;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    const float val = __uint_as_float((uint32_t)v);
+    if (sum) {
+      const uint32_t n = nseg - j0 < 64 ? (uint32_t)(nseg - j0) : 64u;
+      for (uint32_t k = 0; k < n; ++k)
+        acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, val), k));
+    } else {
+      acc = tiler::maximum_f32(acc, tiler::wave_max(j < nseg ? val : -__builtin_huge_valf()));
+    }
+  }
+  *out = acc;
+  return true;
+}
+
+// The row maximum from the row itself (order-free), all 256 threads.
+template <int AL>
+__device__ __forceinline__ float row_max_direct(const float* __restrict__ xr, uint64_t chunks, uint32_t extent,
+                                                float* lds) {
+  const float ninf = -__builtin_huge_valf();
+  float m = ninf;
+  for (uint64_t q = threadIdx.x; q < chunks; q += kSegThreads) m = max_chunk(m, load_f32_chunk<AL>(xr, q, extent, ninf));
+  return seg_block_max(m, lds);
+}
+
+// The row's exponent sum from the row itself: every segment's partial by the
+// segment fold, left-folded in ascending order (all 256 threads get it).
+template <int AL>
+__device__ __forceinline__ float row_sum_direct(const float* __restrict__ xr, uint64_t chunks, uint32_t extent,
+                                                uint64_t nseg, float m, float* lds, const double* tab) {
+  float d = -0.0f;
+  for (uint64_t j = 0; j < nseg; ++j) {
+    f32x4 xv[kSegChunks];
+    load_segment<AL>(xr, j, chunks, extent, xv);
+    float acc = -0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < kSegChunks; ++c) {
+      const uint64_t q = j * kSegChunkSpan + threadIdx.x + c * kSegThreads;
+      if (q < chunks) acc = fold_chunk(acc, exp_chunk(xv[c], m, tab), q, extent);
+    }
+    acc = tiler::wave_sum_butterfly(acc);
+    if ((threadIdx.x & 63u) == 0) lds[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    float p = lds[0];
+    p = p + lds[1];
+    p = p + lds[2];
+    p = p + lds[3];
+    d = d + p;
+    __syncthreads();
+  }
+  return d;
+}
+
+__device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
+  return ((uint64_t)tag << 32) | __float_as_uint(v);
+}
+
+template <int AL>
+__device__ __forceinline__ void softmax_rowsync(const float* __restrict__ x, float* __restrict__ y, uint32_t extent,
+                                                uint64_t nseg, uint8_t* __restrict__ sync, uint64_t wait_ticks,
+                                                const double* tab) {
+  __shared__ float lds[4];
+  __shared__ uint32_t sh_tag, sh_ok;
+  __shared__ float sh_val;
+  const uint32_t t = threadIdx.x;
+  const uint64_t wgs = gridDim.x;
+  const uint64_t row = blockIdx.x / nseg, sg = blockIdx.x % nseg;
+  const uint64_t chunks = (extent + 3u) / 4u;
+  const float* xr = x + row * extent;
+  uint32_t* ctl = reinterpret_cast<uint32_t*>(sync);
+  uint64_t* wmax = reinterpret_cast<uint64_t*>(sync + kRowSyncHeaderBytes) + row * nseg;
+  uint64_t* wsum = reinterpret_cast<uint64_t*>(sync + kRowSyncHeaderBytes) + wgs + row * nseg;
+  if (t == 0) {
+    const uint32_t e = __hip_atomic_load(&ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_tag = e + 1u == 0u ? 1u : e + 1u;  // never 0, the workspace's initial words
+  }
+  f32x4 xv[kSegChunks];
+  load_segment<AL>(xr, sg, chunks, extent, xv);
+  float m = -__builtin_huge_valf();
+#pragma unroll
+  for (uint32_t i = 0; i < kSegChunks; ++i) m = max_chunk(m, xv[i]);
+  m = seg_block_max(m, lds);  // its barrier also publishes sh_tag
+  const uint32_t tag = sh_tag;
+  if (t < 64) {
+    if (t == 0) __hip_atomic_store(&wmax[sg], tagged(tag, m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float v;
+    const bool ok = collect_row(wmax, nseg, tag, wait_ticks, false, &v);
+    if (t == 0) {
+      sh_ok = ok ? 1u : 0u;
+      sh_val = v;
+    }
+  }
+  __syncthreads();
+  m = sh_ok ? sh_val : row_max_direct<AL>(xr, chunks, extent, lds);
+  float acc = -0.0f;
+#pragma unroll
+  for (uint32_t i = 0; i < kSegChunks; ++i) {
+    const uint64_t q = sg * kSegChunkSpan + t + i * kSegThreads;
+    xv[i] = exp_chunk(xv[i], m, tab);
+    if (q < chunks) acc = fold_chunk(acc, xv[i], q, extent);
+  }
+  acc = tiler::wave_sum_butterfly(acc);
+  __syncthreads();  // every wave is past its reads of sh_ok, sh_val and lds
+  if ((t & 63u) == 0) lds[t >> 6] = acc;
+  __syncthreads();
+  if (t < 64) {
+    if (t == 0) {
+      float p = lds[0];
+      p = p + lds[1];
+      p = p + lds[2];
+      p = p + lds[3];
+      __hip_atomic_store(&wsum[sg], tagged(tag, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__hip_atomic_fetch_add(&ctl[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)wgs - 1) {
+        __hip_atomic_store(&ctl[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&ctl[0], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    float v;
+    const bool ok = collect_row(wsum, nseg, tag, wait_ticks, true, &v);
+    if (t == 0) {
+      sh_ok = ok ? 1u : 0u;
+      sh_val = v;
+    }
+  }
+  __syncthreads();
+  const float d = sh_ok ? sh_val : row_sum_direct<AL>(xr, chunks, extent, nseg, m, lds, tab);
+  const float r = 1.0f / d;
+  float* yr = y + row * extent;
+#pragma unroll
+  for (uint32_t i = 0; i < kSegChunks; ++i) {
+    const uint64_t q = sg * kSegChunkSpan + t + i * kSegThreads;
+    if (q < chunks) store_f32_chunk<AL>(yr, q, extent, scale_chunk(xv[i], r));
+  }
+}
+
 }  // namespace
 
 // Entry points: blockIdx.x is the row; 1024 threads.  Instances CH in
@@ -459,9 +633,10 @@ TILER_LONG_FAMILY(TILER_RMS_F32_LONG)
 
 // Softmax rows longer than 8192 elements (the segmented fold above).
 // tiler_softmax_f32_long_r{_a,_u}: blockIdx.x is the row, 1024 threads, rows
-// of at most 4 segments.  tiler_softmax_f32_split_{max,sum,out}{_a,_u}: a flat
-// grid of rows * nseg workgroups of 256 threads; pmax and psum hold
-// rows * nseg partials.
+// of at most 4 segments.  tiler_softmax_f32_split_{max,sum,out}{_a,_u} and
+// tiler_softmax_f32_rowsync{_a,_u}: a flat grid of rows * nseg workgroups of
+// 256 threads; pmax and psum hold rows * nseg partials; sync is the
+// row-synchronized form's area (header and 2 * rows * nseg words).
 #define TILER_SOFTMAX_TAB                                              \
   __shared__ double tab[64];                                           \
   if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Table64[threadIdx.x];  \
@@ -489,6 +664,12 @@ TILER_LONG_FAMILY(TILER_RMS_F32_LONG)
       const float* __restrict__ pmax, const float* __restrict__ psum) {                                   \
     TILER_SOFTMAX_TAB                                                                                     \
     softmax_split_out<AL>(x, y, extent, nseg, pmax, psum, tab);                                           \
+  }                                                                                                       \
+  extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_rowsync##SFX(                       \
+      const float* __restrict__ x, float* __restrict__ y, uint32_t extent, uint64_t nseg,                 \
+      uint8_t* __restrict__ sync, uint64_t wait_ticks) {                                                  \
+    TILER_SOFTMAX_TAB                                                                                     \
+    softmax_rowsync<AL>(x, y, extent, nseg, sync, wait_ticks, tab);                                       \
   }
 TILER_SOFTMAX_F32_SEG(1, _a)
 TILER_SOFTMAX_F32_SEG(0, _u)

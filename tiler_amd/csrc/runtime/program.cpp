@@ -211,9 +211,13 @@ tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_
 // * longer rows: one 256-thread workgroup per segment in three launches
 //   (maxima, sums, output; x read three times), the partials in scratch.
 //   Measured faster than streaming each row through one workgroup at every
-//   row count tried (1 to 512 rows), up to 68x for a single row.
-tiler_hip_status plan_softmax_f32(uint64_t rows, uint64_t extent, const uintptr_t* addr,
-                                  Program& p) {
+//   row count tried (1 to 512 rows), up to 68x for a single row;
+// * longer rows, direct calls, at most two workgroups per CU: the same
+//   workgroups in one row-synchronized launch (x read once), its epoch and
+//   tagged words in the context workspace (slot 2).  The realized route keeps
+//   the three launches: its scratch does not persist between calls.
+tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
+                                  const uintptr_t* addr, Program& p) {
   const uint32_t x = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotInput);
   const uint32_t y = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotOutput);
   if (rows == 0 || extent == 0) return TILER_HIP_OK;
@@ -232,6 +236,13 @@ tiler_hip_status plan_softmax_f32(uint64_t rows, uint64_t extent, const uintptr_
     }
     const uint64_t wgs = mul_sat(rows, nseg);
     if (wgs > 0x7fffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more segments than the launch grid holds");
+    if (mode == Mode::Direct && wgs <= 2ull * t.compute_units && wgs <= kRowSyncMaxWorkgroups) {
+      const uint32_t sync = p.slot(256 + 16 * wgs, kSlotScratch);
+      std::snprintf(name, sizeof(name), "tiler_softmax_f32_rowsync%s", sfx);
+      p.add(name, (uint32_t)wgs, 1, 256)
+          .ptr(x).ptr(y).u32((uint32_t)extent).u64(nseg).ptr(sync).u64(t.row_sync_wait_ticks);
+      return TILER_HIP_OK;
+    }
     const uint32_t pmax = p.slot(wgs * 4, kSlotScratch);
     const uint32_t psum = p.slot(wgs * 4, kSlotScratch);
     std::snprintf(name, sizeof(name), "tiler_softmax_f32_split_max%s", sfx);

@@ -31,6 +31,12 @@ constexpr uint64_t kWorkspacePartialBytes = 256 * 1024;
 // Softmax rows longer than kWaveRowMax fold by segments of this many elements.
 constexpr uint64_t kWaveRowMax = 8192;
 constexpr uint64_t kSoftmaxSegment = 8192;
+// The row-synchronized softmax keeps its epoch, count and tagged words in a
+// workspace area nothing else writes (256 header bytes, then 2 words of 8
+// bytes per workgroup); it runs at most this many workgroups.
+constexpr uint64_t kRowSyncMaxWorkgroups = 1024;
+constexpr uint64_t kRowSyncBytes = 256 + 16 * kRowSyncMaxWorkgroups;
+constexpr uint64_t kRowSyncDefaultWaitTicks = 20000;  // 200 us of the 100 MHz clock
 
 // Slot roles, as tiler_hip_realization reports them.
 constexpr uint32_t kSlotInput = TILER_HIP_SLOT_INPUT;
@@ -85,6 +91,7 @@ struct Program {
 // What a planner may assume about the device.
 struct Target {
   uint32_t compute_units;
+  uint64_t row_sync_wait_ticks;  // the row-synchronized softmax's wait bound
 };
 
 // Direct: the program runs now, on known addresses (it may bind a slot at an
@@ -103,8 +110,8 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
 tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
                                Program& p);
-tiler_hip_status plan_softmax_f32(uint64_t rows, uint64_t extent, const uintptr_t* addr,
-                                  Program& p);
+tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
+                                  const uintptr_t* addr, Program& p);
 tiler_hip_status plan_map(Mode mode, uint32_t op, uint32_t dtype, int32_t x2_broadcast,
                           uint64_t n, float a, float b, const uintptr_t* addr, Program& p);
 tiler_hip_status plan_broadcast(uint64_t src_elements, uint32_t rank, const uint64_t* out_dims,

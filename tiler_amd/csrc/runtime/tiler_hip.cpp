@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -128,6 +129,8 @@ const EntryRow kEntries[] = {
     {"tiler_softmax_f32_split_sum_u", "softmax-f32/split-row", 3},
     {"tiler_softmax_f32_split_out_a", "softmax-f32/split-row", 4},
     {"tiler_softmax_f32_split_out_u", "softmax-f32/split-row", 4},
+    {"tiler_softmax_f32_rowsync_a", "softmax-f32/row-synchronized", 3},
+    {"tiler_softmax_f32_rowsync_u", "softmax-f32/row-synchronized", 3},
     {"tiler_gather_u128", "gather", 4},
     {"tiler_gather_u64", "gather", 4},
     {"tiler_gather_u32", "gather", 4},
@@ -201,9 +204,15 @@ struct tiler_hip_context {
   std::vector<hipModule_t> routed_modules;
   std::vector<hipFunction_t> prepared;
   // workspace: [partials kWorkspacePartialBytes][gather_bad u64 + pad]
+  //            [row-synchronized softmax area kRowSyncBytes: epoch, count, tagged words]
   uint8_t* workspace = nullptr;
   float* sum_partials = nullptr;
   unsigned long long* gather_bad = nullptr;
+  uint8_t* row_sync = nullptr;
+  // The row-synchronized softmax's wait bound (100 MHz ticks): the
+  // TILER_HIP_ROW_SYNC_WAIT_TICKS environment variable at bind, else 200 us.
+  // 0 makes every workgroup compute its row's maximum and sum from the row.
+  uint64_t row_sync_wait_ticks = tiler_rt::kRowSyncDefaultWaitTicks;
   uint32_t compute_units = 0;
   uint64_t lds_bytes = 0;
   uint32_t max_threads = 0;
@@ -254,7 +263,8 @@ bool capturing(hipStream_t s) {
 }
 
 tiler_rt::Target target_of(const tiler_hip_context* ctx) {
-  return tiler_rt::Target{ctx ? ctx->compute_units : kProfileComputeUnits};
+  return tiler_rt::Target{ctx ? ctx->compute_units : kProfileComputeUnits,
+                          ctx ? ctx->row_sync_wait_ticks : tiler_rt::kRowSyncDefaultWaitTicks};
 }
 
 // Runs a planned program on `s`: slot addresses (plus each binding's offset)
@@ -650,7 +660,7 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
     }
     ctx->fns[kEntries[i].symbol] = f;
   }
-  const uint64_t ws_bytes = tiler_rt::kWorkspacePartialBytes + 256;
+  const uint64_t ws_bytes = tiler_rt::kWorkspacePartialBytes + 256 + tiler_rt::kRowSyncBytes;
   if (hipMalloc(&ctx->workspace, ws_bytes) != hipSuccess) {
     copy_text(diagnostic, diagnostic_bytes, "workspace allocation failed");
     hipModuleUnload(ctx->module);
@@ -660,6 +670,8 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
   }
   ctx->sum_partials = reinterpret_cast<float*>(ctx->workspace);
   ctx->gather_bad = reinterpret_cast<unsigned long long*>(ctx->workspace + tiler_rt::kWorkspacePartialBytes);
+  ctx->row_sync = ctx->workspace + tiler_rt::kWorkspacePartialBytes + 256;
+  if (const char* w = std::getenv("TILER_HIP_ROW_SYNC_WAIT_TICKS")) ctx->row_sync_wait_ticks = std::strtoull(w, nullptr, 10);
   hipMemset(ctx->workspace, 0, ws_bytes);
   hipMemset(ctx->gather_bad, 0xff, 8);
   hipDeviceSynchronize();
@@ -1116,7 +1128,7 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   const uintptr_t addr[2] = {(uintptr_t)x, (uintptr_t)y};
-  tiler_hip_status st = tiler_rt::plan_softmax_f32(rows, extent, addr, p);
+  tiler_hip_status st = tiler_rt::plan_softmax_f32(tiler_rt::Mode::Direct, target_of(ctx), rows, extent, addr, p);
   if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
   if (p.nlaunches && (!x || !y)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipStream_t s = pick(ctx, stream);
@@ -1126,7 +1138,10 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
   // allocated, stream-ordered.
   bool own = false;
   uint8_t* part = nullptr;
-  if (p.nslots > 2) {
+  if (p.nslots == 3) {  // the row-synchronized form: its area in the workspace
+    if (p.slot_bytes[2] > tiler_rt::kRowSyncBytes) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "row-sync area");
+    slots[2] = ctx->row_sync;
+  } else if (p.nslots > 2) {
     const uint64_t bytes = p.slot_bytes[2] + p.slot_bytes[3];
     if (bytes <= tiler_rt::kWorkspacePartialBytes) {
       part = reinterpret_cast<uint8_t*>(ctx->sum_partials);
@@ -1305,7 +1320,7 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
       st = tiler_rt::plan_rms_norm(r->dtype, bc ? 1 : 0, e[0], e[1], r->scalars[0], addr, p);
       break;
     case TILER_HIP_PROGRAM_SOFTMAX:
-      st = r->dtype == TILER_HIP_F32 ? tiler_rt::plan_softmax_f32(e[0], e[1], addr, p)
+      st = r->dtype == TILER_HIP_F32 ? tiler_rt::plan_softmax_f32(tiler_rt::Mode::Realized, t, e[0], e[1], addr, p)
                                      : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "softmax is an f32 family");
       break;
     case TILER_HIP_PROGRAM_CONTRACTION:
