@@ -72,7 +72,10 @@ def test_rms_norm_bf16(ctx, case):
 def test_softmax(ctx, case):
     r = _rng(case, 4)
     rows = int(r.integers(1, 9))
-    extent = int(r.choice([int(r.integers(1, 9000)), int(r.integers(8193, 50000))]))
+    # short rows, rows of 2-4 segments (one workgroup per row) and longer
+    # rows (one workgroup per segment, synchronized in one launch)
+    extent = int(r.choice([int(r.integers(1, 9000)), int(r.integers(8193, 32769)),
+                           int(r.integers(32769, 140000))]))
     x = (r.standard_normal((rows, extent)) * 4).astype(np.float32)
     if extent > 3:
         x[0, r.integers(0, extent, extent // 3)] = -np.inf
@@ -165,7 +168,9 @@ def test_realized_plans_match_direct_calls(ctx, case):
         got, want = _route_vs_direct(ctx, rz, [x, w], (np.uint16, rows * extent),
                                      lambda: families.rms_norm_bf16(x, w, EPS, ctx=ctx))
     elif fam == 1:
-        rows, extent = int(r.integers(1, 9)), int(r.integers(1, 20000))
+        # up to 12 segments: the realized plan runs the three-launch split where
+        # the direct call synchronizes rows in one launch; the bits must agree
+        rows, extent = int(r.integers(1, 9)), int(r.integers(1, 98304))
         x = (r.standard_normal((rows, extent)) * 3).astype(np.float32)
         rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), ctx=ctx)
         got, want = _route_vs_direct(ctx, rz, [x], (np.float32, rows * extent),

@@ -67,19 +67,28 @@ def test_rms_norm_headline_and_variants():
 
 
 def test_softmax_long_rows_choose_a_launch_form():
-    # Rows of more than 4 segments: one workgroup per 8192-element segment in
-    # three launches, the partials in two scratch slots of rows * segments
-    # f32.  Up to 4 segments: one workgroup per row, the row in registers.
-    sp = realize(L.PROGRAM_SOFTMAX, (32, 131072), flags=L.REGION_ALIGNED16)
+    # Rows of more than 4 segments, at most 2 workgroups per CU (the profile's
+    # 256): one workgroup per 8192-element segment in one row-synchronized
+    # launch, its area zeroed by a fill first (a realized plan's scratch is
+    # fresh).  More workgroups: three launches, the partials in two scratch
+    # slots of rows * segments f32.  Up to 4 segments: one workgroup per row.
+    rs = realize(L.PROGRAM_SOFTMAX, (32, 131072), flags=L.REGION_ALIGNED16)
+    assert rs.symbols == ["tiler_fill_u32", "tiler_softmax_f32_rowsync_a"]
+    sync = 256 + 16 * 512
+    assert rs.slots == [(L.SLOT_INPUT, 32 * 131072 * 4), (L.SLOT_OUTPUT, 32 * 131072 * 4), (L.SLOT_SCRATCH, sync)]
+    assert rs.dispatches[1].grid == (512, 1, 1) and rs.dispatches[1].block == (256, 1, 1)
+    assert struct.unpack_from("<QI4xQ", bytes(rs.raw.entries[0].kernargs[:24])) == (0, 0, sync // 4)
+    _check_segments(rs)
+    sp = realize(L.PROGRAM_SOFTMAX, (64, 131072), flags=L.REGION_ALIGNED16)
     assert sp.symbols == ["tiler_softmax_f32_split_max_a", "tiler_softmax_f32_split_sum_a",
                           "tiler_softmax_f32_split_out_a"]
-    assert [d.grid for d in sp.dispatches] == [(16 * 32, 1, 1)] * 3
+    assert [d.grid for d in sp.dispatches] == [(16 * 64, 1, 1)] * 3
     assert all(d.block == (256, 1, 1) for d in sp.dispatches)
-    assert sp.slots == [(L.SLOT_INPUT, 32 * 131072 * 4), (L.SLOT_OUTPUT, 32 * 131072 * 4),
-                        (L.SLOT_SCRATCH, 32 * 16 * 4), (L.SLOT_SCRATCH, 32 * 16 * 4)]
+    assert sp.slots == [(L.SLOT_INPUT, 64 * 131072 * 4), (L.SLOT_OUTPUT, 64 * 131072 * 4),
+                        (L.SLOT_SCRATCH, 64 * 16 * 4), (L.SLOT_SCRATCH, 64 * 16 * 4)]
     assert [sorted(s for s, _ in d.bindings) for d in sp.dispatches] == [[0, 2], [0, 2, 3], [0, 1, 2, 3]]
     _check_segments(sp)
-    assert realize(L.PROGRAM_SOFTMAX, (3, 50001)).symbols[0] == "tiler_softmax_f32_split_max_u"
+    assert realize(L.PROGRAM_SOFTMAX, (3, 50001)).symbols == ["tiler_fill_u32", "tiler_softmax_f32_rowsync_u"]
     assert realize(L.PROGRAM_SOFTMAX, (1000, 32769)).symbols[0] == "tiler_softmax_f32_split_max_u"
     res = realize(L.PROGRAM_SOFTMAX, (2, 32768), flags=L.REGION_ALIGNED16)
     assert res.symbols == ["tiler_softmax_f32_long_r_a"] and res.dispatches[0].grid == (2, 1, 1)

@@ -212,10 +212,11 @@ tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_
 //   (maxima, sums, output; x read three times), the partials in scratch.
 //   Measured faster than streaming each row through one workgroup at every
 //   row count tried (1 to 512 rows), up to 68x for a single row;
-// * longer rows, direct calls, at most two workgroups per CU: the same
-//   workgroups in one row-synchronized launch (x read once), its epoch and
-//   tagged words in the context workspace (slot 2).  The realized route keeps
-//   the three launches: its scratch does not persist between calls.
+// * longer rows, at most two workgroups per CU: the same workgroups in one
+//   row-synchronized launch (x read once), its epoch and tagged words in
+//   slot 2 -- for direct calls the context workspace's area, which stays
+//   valid between calls; a realized plan's scratch is fresh, so its program
+//   zeroes the area with a fill kernel first.
 tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
                                   const uintptr_t* addr, Program& p) {
   const uint32_t x = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotInput);
@@ -236,8 +237,11 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
     }
     const uint64_t wgs = mul_sat(rows, nseg);
     if (wgs > 0x7fffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more segments than the launch grid holds");
-    if (mode == Mode::Direct && wgs <= 2ull * t.compute_units && wgs <= kRowSyncMaxWorkgroups) {
-      const uint32_t sync = p.slot(256 + 16 * wgs, kSlotScratch);
+    if (wgs <= 2ull * t.compute_units && wgs <= kRowSyncMaxWorkgroups) {
+      const uint64_t sync_bytes = 256 + 16 * wgs;
+      const uint32_t sync = p.slot(sync_bytes, kSlotScratch);
+      if (mode == Mode::Realized)
+        p.add("tiler_fill_u32", blocks_capped(sync_bytes / 4, 64), 1, 256).ptr(sync).u32(0).u64(sync_bytes / 4);
       std::snprintf(name, sizeof(name), "tiler_softmax_f32_rowsync%s", sfx);
       p.add(name, (uint32_t)wgs, 1, 256)
           .ptr(x).ptr(y).u32((uint32_t)extent).u64(nseg).ptr(sync).u64(t.row_sync_wait_ticks);
