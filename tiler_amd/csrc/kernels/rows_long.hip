@@ -279,24 +279,51 @@ __device__ __forceinline__ float seg_round_fold(float acc, uint32_t active, floa
   return total;
 }
 
+// Chunks q0, q0 + 256, ..., q0 + 1792 of a row into registers, -inf past the
+// row.  The padding is written before the (masked) load, never after it, so
+// the 8 loads stay in flight together: a select or a second path writing the
+// load's registers would make the compiler wait for each load in turn.  AL:
+// the planner's _a condition (extent % 4 == 0, aligned base) makes every
+// chunk below `chunks` whole.
+template <int AL>
+__device__ __forceinline__ void load_chunks(const float* __restrict__ x, uint64_t q0, uint64_t chunks,
+                                            uint32_t extent, f32x4 (&xv)[kSegChunks]) {
+  const float ninf = -__builtin_huge_valf();
+#pragma unroll
+  for (uint32_t c = 0; c < kSegChunks; ++c) {
+    const uint64_t q = q0 + c * kSegThreads;
+    xv[c] = f32x4{ninf, ninf, ninf, ninf};
+    if (q < chunks) {
+      if (AL) {
+        xv[c] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + q * 4u));
+      } else {
+        const uint64_t p0 = q * 4u;
+        if (p0 < extent) xv[c].x = x[p0];
+        if (p0 + 1 < extent) xv[c].y = x[p0 + 1];
+        if (p0 + 2 < extent) xv[c].z = x[p0 + 2];
+        if (p0 + 3 < extent) xv[c].w = x[p0 + 3];
+      }
+    }
+  }
+}
+
 // One 1024-thread workgroup per row of at most 4 segments: group g keeps
 // segment g in registers between the passes, so x is read once.
 template <int AL>
 __device__ __forceinline__ void softmax_f32_seg_row(const float* __restrict__ x, float* __restrict__ y,
-                                                    uint32_t extent, float* lds, const double* tab) {
+                                                    uint32_t extent, float* lds, double* tab) {
   const uint32_t t = threadIdx.x, g = t >> 8, l = t & 255u;
   const uint64_t chunks = (extent + 3u) / 4u;
   const uint32_t nseg = (uint32_t)((extent + kSegElems - 1) / kSegElems);  // <= 4 (the planner's choice)
   const float ninf = -__builtin_huge_valf();
   f32x4 xv[kSegChunks];
   float m = ninf;
+  load_chunks<AL>(x, g * kSegChunkSpan + l, chunks, extent, xv);
+  const double tv = kExp2Table64[t & 63u];  // the exponent table, filled after the row's loads are issued
 #pragma unroll
-  for (uint32_t c = 0; c < kSegChunks; ++c) {
-    const uint64_t q = g * kSegChunkSpan + l + c * kSegThreads;
-    xv[c] = q < chunks ? load_f32_chunk<AL>(x, q, extent, ninf) : f32x4{ninf, ninf, ninf, ninf};
-    m = max_chunk(m, xv[c]);
-  }
-  m = long_block_max(m, lds);
+  for (uint32_t c = 0; c < kSegChunks; ++c) m = max_chunk(m, xv[c]);
+  if (t < 64) tab[t] = tv;
+  m = long_block_max(m, lds);  // its barrier also publishes tab
   float acc = -0.0f;
 #pragma unroll
   for (uint32_t c = 0; c < kSegChunks; ++c) {
@@ -355,12 +382,7 @@ __device__ __forceinline__ float row_sum_of(const float* __restrict__ psum, uint
 template <int AL>
 __device__ __forceinline__ void load_segment(const float* __restrict__ x, uint64_t sg, uint64_t chunks,
                                              uint32_t extent, f32x4 (&xv)[kSegChunks]) {
-  const float ninf = -__builtin_huge_valf();
-#pragma unroll
-  for (uint32_t c = 0; c < kSegChunks; ++c) {
-    const uint64_t q = sg * kSegChunkSpan + threadIdx.x + c * kSegThreads;
-    xv[c] = q < chunks ? load_f32_chunk<AL>(x, q, extent, ninf) : f32x4{ninf, ninf, ninf, ninf};
-  }
+  load_chunks<AL>(x, sg * kSegChunkSpan + threadIdx.x, chunks, extent, xv);
 }
 
 // Split pass 1: pmax[row * nseg + s] = the maximum of segment s.
@@ -383,13 +405,16 @@ __device__ __forceinline__ void softmax_split_max(const float* __restrict__ x, u
 template <int AL>
 __device__ __forceinline__ void softmax_split_sum(const float* __restrict__ x, uint32_t extent, uint64_t nseg,
                                                   const float* __restrict__ pmax, float* __restrict__ psum,
-                                                  const double* tab) {
+                                                  double* tab) {
   __shared__ float lds[4];
   const uint64_t row = blockIdx.x / nseg, sg = blockIdx.x % nseg;
   const uint64_t chunks = (extent + 3u) / 4u;
   f32x4 xv[kSegChunks];
   load_segment<AL>(x + row * extent, sg, chunks, extent, xv);
+  const double tv = kExp2Table64[threadIdx.x & 63u];  // filled after the segment's loads are issued
   const float m = row_max_of(pmax + row * nseg, nseg);
+  if (threadIdx.x < 64) tab[threadIdx.x] = tv;
+  __syncthreads();
   float acc = -0.0f;
 #pragma unroll
   for (uint32_t c = 0; c < kSegChunks; ++c) {
@@ -413,13 +438,16 @@ __device__ __forceinline__ void softmax_split_sum(const float* __restrict__ x, u
 template <int AL>
 __device__ __forceinline__ void softmax_split_out(const float* __restrict__ x, float* __restrict__ y,
                                                   uint32_t extent, uint64_t nseg, const float* __restrict__ pmax,
-                                                  const float* __restrict__ psum, const double* tab) {
+                                                  const float* __restrict__ psum, double* tab) {
   const uint64_t row = blockIdx.x / nseg, sg = blockIdx.x % nseg;
   const uint64_t chunks = (extent + 3u) / 4u;
   f32x4 xv[kSegChunks];
   load_segment<AL>(x + row * extent, sg, chunks, extent, xv);
+  const double tv = kExp2Table64[threadIdx.x & 63u];  // filled after the segment's loads are issued
   const float m = row_max_of(pmax + row * nseg, nseg);
   const float r = 1.0f / row_sum_of(psum + row * nseg, nseg);
+  if (threadIdx.x < 64) tab[threadIdx.x] = tv;
+  __syncthreads();
   float* yr = y + row * extent;
 #pragma unroll
   for (uint32_t c = 0; c < kSegChunks; ++c) {
@@ -524,12 +552,14 @@ __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
   return ((uint64_t)tag << 32) | __float_as_uint(v);
 }
 
+// `tab` is filled here, after the segment's loads are issued, so the
+// workgroup's first memory round trips overlap instead of queueing.
 template <int AL>
 __device__ __forceinline__ void softmax_rowsync(const float* __restrict__ x, float* __restrict__ y, uint32_t extent,
                                                 uint64_t nseg, uint8_t* __restrict__ sync, uint64_t wait_ticks,
-                                                const double* tab) {
+                                                double* tab) {
   __shared__ float lds[4];
-  __shared__ uint32_t sh_tag, sh_ok;
+  __shared__ uint32_t sh_ok;
   __shared__ float sh_val;
   const uint32_t t = threadIdx.x;
   const uint64_t wgs = gridDim.x;
@@ -539,17 +569,17 @@ __device__ __forceinline__ void softmax_rowsync(const float* __restrict__ x, flo
   uint32_t* ctl = reinterpret_cast<uint32_t*>(sync);
   uint64_t* wmax = reinterpret_cast<uint64_t*>(sync + kRowSyncHeaderBytes) + row * nseg;
   uint64_t* wsum = reinterpret_cast<uint64_t*>(sync + kRowSyncHeaderBytes) + wgs + row * nseg;
-  if (t == 0) {
-    const uint32_t e = __hip_atomic_load(&ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh_tag = e + 1u == 0u ? 1u : e + 1u;  // never 0, the workspace's initial words
-  }
   f32x4 xv[kSegChunks];
   load_segment<AL>(xr, sg, chunks, extent, xv);
+  // Only wave 0 publishes and polls, so only its lanes need the epoch.
+  const uint32_t e = t < 64 ? __hip_atomic_load(&ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+  const double tv = kExp2Table64[t & 63u];
   float m = -__builtin_huge_valf();
 #pragma unroll
   for (uint32_t i = 0; i < kSegChunks; ++i) m = max_chunk(m, xv[i]);
-  m = seg_block_max(m, lds);  // its barrier also publishes sh_tag
-  const uint32_t tag = sh_tag;
+  if (t < 64) tab[t] = tv;
+  m = seg_block_max(m, lds);  // its barrier also publishes tab
+  const uint32_t tag = e + 1u == 0u ? 1u : e + 1u;  // never 0, the workspace's initial words
   if (t < 64) {
     if (t == 0) __hip_atomic_store(&wmax[sg], tagged(tag, m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float v;
@@ -637,15 +667,11 @@ TILER_LONG_FAMILY(TILER_RMS_F32_LONG)
 // tiler_softmax_f32_rowsync{_a,_u}: a flat grid of rows * nseg workgroups of
 // 256 threads; pmax and psum hold rows * nseg partials; sync is the
 // row-synchronized form's area (header and 2 * rows * nseg words).
-#define TILER_SOFTMAX_TAB                                              \
-  __shared__ double tab[64];                                           \
-  if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Table64[threadIdx.x];  \
-  __syncthreads();
 #define TILER_SOFTMAX_F32_SEG(AL, SFX)                                                                     \
   extern "C" __global__ void __launch_bounds__(1024) tiler_softmax_f32_long_r##SFX(                       \
       const float* __restrict__ x, float* __restrict__ y, uint32_t extent) {                              \
     __shared__ float lds[kLongWaves];                                                                     \
-    TILER_SOFTMAX_TAB                                                                                     \
+    __shared__ double tab[64];                                                                            \
     const uint64_t row = blockIdx.x;                                                                      \
     softmax_f32_seg_row<AL>(x + row * extent, y + row * extent, extent, lds, tab);                     \
   }                                                                                                       \
@@ -656,19 +682,19 @@ TILER_LONG_FAMILY(TILER_RMS_F32_LONG)
   extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_split_sum##SFX(                     \
       const float* __restrict__ x, uint32_t extent, uint64_t nseg, const float* __restrict__ pmax,        \
       float* __restrict__ psum) {                                                                         \
-    TILER_SOFTMAX_TAB                                                                                     \
+    __shared__ double tab[64];                                                                            \
     softmax_split_sum<AL>(x, extent, nseg, pmax, psum, tab);                                              \
   }                                                                                                       \
   extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_split_out##SFX(                     \
       const float* __restrict__ x, float* __restrict__ y, uint32_t extent, uint64_t nseg,                 \
       const float* __restrict__ pmax, const float* __restrict__ psum) {                                   \
-    TILER_SOFTMAX_TAB                                                                                     \
+    __shared__ double tab[64];                                                                            \
     softmax_split_out<AL>(x, y, extent, nseg, pmax, psum, tab);                                           \
   }                                                                                                       \
   extern "C" __global__ void __launch_bounds__(256) tiler_softmax_f32_rowsync##SFX(                       \
       const float* __restrict__ x, float* __restrict__ y, uint32_t extent, uint64_t nseg,                 \
       uint8_t* __restrict__ sync, uint64_t wait_ticks) {                                                  \
-    TILER_SOFTMAX_TAB                                                                                     \
+    __shared__ double tab[64];                                                                            \
     softmax_rowsync<AL>(x, y, extent, nseg, sync, wait_ticks, tab);                                       \
   }
 TILER_SOFTMAX_F32_SEG(1, _a)
