@@ -12,8 +12,9 @@
 // CH == 0: rows of any length are streamed (read twice: fold, epilogue).
 //
 // Softmax: the exponent sum folds by 8192-element segments (described at
-// softmax_f32_seg_row), so a row can also be split across workgroups when
-// there are too few rows to fill the device.
+// softmax_f32_seg_row), so a row can also be split across workgroups: one
+// workgroup per row up to 4 segments, one per segment beyond (one
+// row-synchronized launch, or three launches).
 //
 // AL: 1 when the row base and extent keep every chunk 16-byte aligned; 0 loads
 // and stores element by element in the same order.
