@@ -255,8 +255,9 @@ __device__ __forceinline__ f32x4 scale_chunk(f32x4 e, float r) {
 // partials in ascending segment order (the grouping vec 4, waves 4, segment
 // 8192 that tiler_hip_row_grouping reports).  The same fold is computed by one
 // 1024-thread workgroup per row (rows of at most 4 segments, group g of 256
-// threads takes segment g) and by the split form (one 256-thread workgroup per
-// segment, three launches), so which one runs never changes a bit.
+// threads takes segment g) and by one 256-thread workgroup per segment (the
+// row-synchronized launch, or the split form's three launches), so which one
+// runs never changes a bit.
 constexpr uint32_t kSegThreads = 256;
 constexpr uint32_t kSegChunks = 8;                                 // per lane per segment
 constexpr uint64_t kSegChunkSpan = (uint64_t)kSegThreads * kSegChunks;  // 2048 chunks
