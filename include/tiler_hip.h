@@ -294,6 +294,40 @@ const char *tiler_hip_last_diagnostic(const tiler_hip_context *ctx);
 tiler_hip_status tiler_hip_observe_live_device(tiler_hip_context *ctx, const char *key,
                                                uint64_t *value);
 
+/* Target environment (RuntimeAdapter::target_environment_support and
+ * observe_target_environment, tiler-runtime/src/adapter.rs:295-322; the
+ * descriptor schema contract, tiler-artifact/src/program/environment.rs:
+ * 249-400).  tiler-hip registers exactly one provider schema, so it never
+ * answers Unsupported.  Its canonical descriptor is the bound device's code
+ * object target, the one fact a gfx950 code object is compatible with:
+ *   u32 BE length, then the target ID "amdgcn-amd-amdhsa--gfx950" followed by
+ *   its features in the order the target ID grammar fixes (":sramecc+|-"
+ *   then ":xnack+|-"), then u32 BE wavefront size (64).
+ * A descriptor is canonical iff it is exactly that spelling for some feature
+ * values; every other byte run refuses with a reason. */
+typedef struct {
+    char provider[64];           /* "tiler.hip.target-environment" */
+    uint32_t provider_revision;  /* nonzero: 1 */
+    uint16_t schema_major, schema_minor; /* 1.0 */
+} tiler_hip_target_environment_schema;
+
+/* target_environment_support: fills the registered schema (device-free). */
+tiler_hip_status tiler_hip_target_environment_support(tiler_hip_target_environment_schema *out);
+/* validate_canonical_descriptor: TILER_HIP_OK for the schema's one canonical
+ * spelling, TILER_HIP_REFUSE_INVALID_ARGUMENT naming the first defect. */
+tiler_hip_status tiler_hip_validate_target_environment(const void *descriptor, uint64_t bytes,
+                                                       char *diagnostic, uint64_t diagnostic_bytes);
+/* observe_target_environment: the bound context's canonical descriptor.
+ * *observed = 1 and the bytes (up to `capacity`; *required receives the
+ * length), or *observed = 0 (TargetEnvironmentObservation::Unavailable) with
+ * the reason in `reason` -- still TILER_HIP_OK: it filters claimed cells and
+ * is not a context failure.  TILER_HIP_REFUSE_CAPACITY if the bytes do not
+ * fit. */
+tiler_hip_status tiler_hip_observe_target_environment(tiler_hip_context *ctx, uint8_t *descriptor,
+                                                      uint64_t capacity, uint64_t *required,
+                                                      uint32_t *observed, char *reason,
+                                                      uint64_t reason_bytes);
+
 typedef struct {
     const void *code;      /* code-object bytes (borrowed for the call) */
     uint64_t code_bytes;
@@ -329,6 +363,10 @@ typedef struct {
     const uint64_t *slot_bytes;     /* required bytes per storage slot */
     uint32_t entry_count;
     const tiler_hip_dispatch_entry *entries; /* in execution order */
+    /* Optional (NULL: none): per slot, host bytes (slot_bytes[i] of them) that
+     * tiler_hip_dispatch uploads into the slot before the first entry runs --
+     * a realization's CONSTANT slot.  NULL entries are left alone. */
+    const void *const *slot_contents;
 } tiler_hip_dispatch_plan;
 
 /* plan_dispatch (adapter.rs:453): sizes and checks the route against the
@@ -393,8 +431,9 @@ tiler_hip_status tiler_hip_graph_destroy(tiler_hip_context *ctx, tiler_hip_graph
 
 /* Sum over the last axis of a dense [rows, extent] f32 tensor
  * (strict-serial-sum-f32@1; tiler-reference/src/evaluate.rs:498-589). */
-#define TILER_HIP_SUM_TREE 0        /* reassociating two-level tree (declared grouping) */
-#define TILER_HIP_SUM_SERIAL 1      /* ReductionTopology::Serial, bit-exact strict_sum */
+#define TILER_HIP_SUM_SERIAL 0      /* ReductionTopology::Serial, bit-exact strict_sum; the zero
+                                       default, so an unset plan is the strict fold */
+#define TILER_HIP_SUM_TREE 1        /* reassociating two-level tree (declared grouping) */
 #define TILER_HIP_SUM_MULTIPASS 2   /* ::MultiPass, bit-exact strict_partitioned_sum
                                        (evaluate.rs:788-832) */
 #define TILER_HIP_SUM_COOPERATIVE 3 /* ::CooperativeWorkgroup, bit-exact
@@ -470,6 +509,70 @@ tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_
 tiler_hip_status tiler_hip_map(tiler_hip_context *ctx, uint32_t op, uint32_t dtype,
                                const void *x, const void *x2, int32_t x2_broadcast, uint64_t n,
                                float a, float b, void *y, tiler_hip_stream stream);
+
+/* One node of a pointwise expression (PointwiseF32Node,
+ * tiler-ir/src/schedule/pointwise.rs:74-140; PointwiseBf16Node,
+ * pointwise_bf16.rs:114-168).  Operands name earlier nodes (a DAG in
+ * topological order).  INPUT: a = access ordinal (the inputs are dense
+ * 0..n-1, each named once).  CONSTANT: a = the constant's bits (binary32, or
+ * bf16 in the low 16 bits).  ADD, MULTIPLY, DIVIDE: a = lhs, b = rhs.  EXP,
+ * RSQRT: a = argument.  bf16 expressions admit INPUT, CONSTANT, ADD and
+ * MULTIPLY only. */
+#define TILER_HIP_NODE_INPUT 0u
+#define TILER_HIP_NODE_CONSTANT 1u
+#define TILER_HIP_NODE_ADD 2u
+#define TILER_HIP_NODE_MULTIPLY 3u
+#define TILER_HIP_NODE_DIVIDE 4u
+#define TILER_HIP_NODE_EXP 5u
+#define TILER_HIP_NODE_RSQRT 6u
+#define TILER_HIP_MAX_EXPRESSION_NODES 4096u /* MAX_POINTWISE_{F32,BF16}_EXPRESSION_NODES */
+typedef struct {
+    uint32_t op;
+    uint32_t a;
+    uint32_t b;
+} tiler_hip_expression_node;
+
+/* Pointwise expression DAG (ScalarProgram::PointwiseF32 / PointwiseBf16;
+ * tiler-ir/src/schedule/pointwise.rs:74-140, pointwise_bf16.rs:114-168):
+ * y[i] = root evaluated on inputs[0..I)[i] for i < n, one fused launch.  The
+ * DAG is verified as the reference's builder does (operands defined before
+ * use, input ordinals dense and each named once, every node reachable from
+ * the root, at most TILER_HIP_MAX_EXPRESSION_NODES nodes, at most 16 inputs).
+ * dtype TILER_HIP_F32: ADD, MULTIPLY, DIVIDE round once (IEEE binary32),
+ * EXP and RSQRT are correctly rounded, every node's result is canonicalized,
+ * and the subnormal modes (TILER_HIP_SUBNORMALS_*, 0: preserve) apply at
+ * each node's operands and result (tiler-reference/src/conformance.rs:498-521).
+ * dtype TILER_HIP_BF16: bf16 storage, INPUT/CONSTANT/ADD/MULTIPLY, each node
+ * rounded once to bf16 (ADR 0091), preserve only.  The register program is
+ * uploaded on a call's first use (so a graph may capture only programs the
+ * context has already run). */
+tiler_hip_status tiler_hip_expression(tiler_hip_context *ctx, uint32_t dtype,
+                                      const tiler_hip_expression_node *nodes, uint32_t node_count,
+                                      uint32_t root, const void *const *inputs, uint64_t n, void *y,
+                                      uint32_t input_subnormals, uint32_t result_subnormals,
+                                      tiler_hip_stream stream);
+
+/* Serial fold of a dense row-major f32 tensor (dims[0..rank), rank <= 8)
+ * over the axes set in reduced_mask, one output per kept coordinate (kept
+ * axes in order): TILER_HIP_FOLD_* (see PROGRAM_FOLD below; scale and bias
+ * bits for FMA).  Bit-exact with the reference's strict fold
+ * (tiler-reference/src/evaluate.rs:498-589; tiler-ir/src/kernel/lower.rs:
+ * 1236-1305, 2485-2500). */
+tiler_hip_status tiler_hip_fold_f32(tiler_hip_context *ctx, uint32_t variant, const float *x,
+                                    uint32_t rank, const uint64_t *dims, uint64_t reduced_mask,
+                                    uint32_t scale_bits, uint32_t bias_bits, float *out,
+                                    tiler_hip_stream stream);
+
+/* Reindex move with signed strides (the mirrored reindex,
+ * tiler-metal/goldens/structural_mirrored_reindex.metal; structural.rs:75-108):
+ * out (row-major over out_dims) element reads source offset
+ * base + sum_d coord_d * strides[d].  The smallest and largest offset the
+ * geometry reaches must lie in [0, src_elements), else it refuses before any
+ * launch.  element_bytes 2 or 4. */
+tiler_hip_status tiler_hip_reindex(tiler_hip_context *ctx, const void *src, uint64_t src_elements,
+                                   uint32_t rank, const uint64_t *out_dims, const int64_t *strides,
+                                   int64_t base, uint32_t element_bytes, void *out,
+                                   tiler_hip_stream stream);
 
 /* Broadcast / reindex move (broadcast-f32@2; tiler-reference/src/structural.rs:75-108):
  * out (row-major over out_dims) element reads source offset
@@ -555,12 +658,62 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context *ctx, const uint16_t 
 #define TILER_HIP_PROGRAM_GATHER 6      /* tiler-reference/src/structural.rs:513-606 */
 #define TILER_HIP_PROGRAM_BROADCAST 7   /* tiler-reference/src/structural.rs:75-108 */
 #define TILER_HIP_PROGRAM_CONVERT 8     /* the ADR 0091 conversion families; variant: TILER_HIP_CONVERT_* */
+#define TILER_HIP_PROGRAM_EXPRESSION 9  /* ::PointwiseF32 / ::PointwiseBf16 expression DAGs (model.rs:663,
+                                           681; schedule/pointwise.rs, pointwise_bf16.rs): nodes, root */
+#define TILER_HIP_PROGRAM_FOLD 10       /* the serial folds over any reduced axis set (variant:
+                                           TILER_HIP_FOLD_*): StrictSerialSum (model.rs:698),
+                                           FusedMultiplyAddSerialSum (:709), SquaredSerialSum (:745),
+                                           StrictSerialMaximum (:920) */
+#define TILER_HIP_PROGRAM_REINDEX 11    /* structural reindex with signed strides (the mirrored reindex,
+                                           tiler-metal/goldens/structural_mirrored_reindex.metal) */
+
+/* PROGRAM_FOLD variants.  The input is dense row-major with `rank` dims in
+ * extents[]; grouping[0] is the reduced-axis mask (bit d: axis d reduced);
+ * the output is the kept axes, dense, in order.  Each output folds its
+ * contributors in lexicographic order of the reduced coordinates, seeded at
+ * the first contributor (evaluate.rs:548-585); every combine is canonical.
+ *   SUM      acc = acc + x                         empty: +0 (empty_identity_bits)
+ *   SQUARED  acc = acc + fl(x * x)                 empty: +0
+ *   FMA      acc = acc + fl(fl(x * scale) + bias)  scalars {scale, bias}; the
+ *            program's `contraction` permission (FusedMultiplyAddSerialSum::
+ *            contraction) is not consumed: the two-rounding form is the one
+ *            every contract admits                 empty: +0
+ *   MAXIMUM  NaN-propagating IEEE maximum with -0 < +0 (softmax.rs:168-186);
+ *            order-insensitive, so it spends no reassociation permission;
+ *            an empty reduced domain is refused (model.rs:880-906) */
+#define TILER_HIP_FOLD_SUM 0u
+#define TILER_HIP_FOLD_SQUARED 1u
+#define TILER_HIP_FOLD_FMA 2u
+#define TILER_HIP_FOLD_MAXIMUM 3u
 
 /* Region flags. */
 #define TILER_HIP_REGION_ALIGNED16 1u         /* precondition: every slot's base address is 16-byte aligned */
 #define TILER_HIP_REGION_OPERAND_BROADCAST 2u /* pointwise: x2 is one element; rms_norm: w is one row */
 #define TILER_HIP_REGION_INDEX_SIGNED 4u      /* gather: int32 indices */
 #define TILER_HIP_REGION_PARTICIPANT_MAJOR 8u /* cooperative sum layout */
+
+/* The plan's numerical contract as it reaches one region: the permissions
+ * its ReductionTopology carries (permits_reassociation, permits_permutation;
+ * tiler-ir/src/schedule/model.rs:1330-1340, 1409-1413, 1520-1540) and the two
+ * subnormal dimensions of the resolved contract (STRICT_F32,
+ * FLUSH_SUBNORMALS_TO_ZERO_F32, REASSOCIATE_F32, FLUSH_AND_REASSOCIATE_F32,
+ * STRICT_BF16 ...; tiler-compiler/src/session.rs:1793-1888).  All zero is the
+ * strict contract: no regrouping of any fold, subnormals preserved.
+ *   - A reassociating realization (the two-level tree sum, the multi-pass and
+ *     cooperative splits, the grouped RMSNorm and softmax row folds, the MFMA
+ *     contraction) is chosen only under PERMITS_REASSOCIATION.  Without it the
+ *     region gets the strict serial fold where this library has one (sum,
+ *     RMSNorm, softmax, contraction) and is refused otherwise.  The maximum is
+ *     order-insensitive on every binary32 input and spends no permission.
+ *   - Subnormal modes: the device preserves binary32 and bf16 subnormals.
+ *     A flushing mode is realized where the kernels implement it (pointwise
+ *     expressions) and refused before commit everywhere else.  Byte moves
+ *     (gather, broadcast) perform no arithmetic and ignore the modes. */
+#define TILER_HIP_PERMITS_REASSOCIATION 1u
+#define TILER_HIP_PERMITS_PERMUTATION 2u
+#define TILER_HIP_SUBNORMALS_PRESERVE 1u       /* 0 reads as PRESERVE */
+#define TILER_HIP_SUBNORMALS_FLUSH_SIGN 2u     /* to the zero of the operand's sign */
+#define TILER_HIP_SUBNORMALS_FLUSH_POSITIVE 3u /* to +0 */
 
 typedef struct {
     uint32_t program;      /* TILER_HIP_PROGRAM_* */
@@ -571,17 +724,30 @@ typedef struct {
                               gather, broadcast: element bytes */
     uint32_t flags;        /* TILER_HIP_REGION_* */
     uint32_t rank;         /* broadcast: output rank (<= 8) */
-    uint64_t extents[8];   /* pointwise, convert {n}; sum, rms_norm, softmax {rows, extent};
+    uint64_t extents[8];   /* pointwise, convert, expression {n}; sum, rms_norm, softmax {rows, extent};
                               contraction {m, n, k}; gather {outer, gathered, inner, index count};
-                              broadcast: the output dims */
-    uint64_t strides[8];   /* broadcast: source stride (elements) per output axis */
+                              broadcast, reindex: the output dims; fold: the input dims */
+    uint64_t strides[8];   /* broadcast: source stride (elements) per output axis;
+                              reindex: the same as int64 (two's complement, may be negative) */
     uint64_t grouping[3];  /* multi-pass sum {partitions, per partition};
                               cooperative sum {participants, per partition, rounds};
-                              broadcast {source elements} */
+                              broadcast {source elements}; reindex {source elements, base offset};
+                              fold {reduced-axis mask} */
     uint32_t scalars[2];   /* rms_norm {eps bits}; pointwise {a bits, b bits} */
+    uint32_t permissions;        /* TILER_HIP_PERMITS_*: the contract's regrouping freedoms */
+    uint32_t input_subnormals;   /* TILER_HIP_SUBNORMALS_* (0: preserve) */
+    uint32_t result_subnormals;  /* TILER_HIP_SUBNORMALS_* (0: preserve) */
+    /* PROGRAM_EXPRESSION: node_count nodes (<= TILER_HIP_MAX_EXPRESSION_NODES)
+     * and the root's index; the nodes are read during the call only. */
+    uint32_t node_count;
+    uint32_t root;
+    const tiler_hip_expression_node *nodes;
 } tiler_hip_region;
 
 /* Storage slot roles.  Slot order per program:
+ *   expression  the inputs in access order, y, program (a constant slot)
+ *   fold        x, out
+ *   reindex     src, out
  *   pointwise   x, [x2,] y       (x2 only for ADD and MULTIPLY)
  *   serial sum  x, out, [partials: scratch]
  *   rms_norm    x, w, y
@@ -595,6 +761,9 @@ typedef struct {
 #define TILER_HIP_SLOT_INPUT 0
 #define TILER_HIP_SLOT_OUTPUT 1
 #define TILER_HIP_SLOT_SCRATCH 2
+#define TILER_HIP_SLOT_CONSTANT 3 /* read-only; the route uploads the realization's `constant`
+                                     bytes into it before the first dispatch */
+#define TILER_HIP_REALIZATION_CONSTANT_BYTES 49152u /* 4096 nodes of 12 bytes */
 
 typedef struct {
     uint32_t entry;             /* payload entry index (tiler_hip_payload_entry names it) */
@@ -603,17 +772,20 @@ typedef struct {
     uint32_t kernarg_bytes;
     uint8_t kernargs[256];      /* argument segment; pointer fields are bound at dispatch */
     uint32_t binding_count;
-    uint32_t binding_slots[6];
-    uint32_t binding_offsets[6];
+    uint32_t binding_slots[18];
+    uint32_t binding_offsets[18];
 } tiler_hip_realized_entry;
 
 typedef struct {
     uint32_t slot_count;
-    uint32_t slot_roles[6];     /* TILER_HIP_SLOT_* */
-    uint64_t slot_bytes[6];
+    uint32_t slot_roles[18];    /* TILER_HIP_SLOT_* */
+    uint64_t slot_bytes[18];
     uint32_t slot_alignment;    /* precondition on every slot base: 16 with ALIGNED16, else 1 */
     uint32_t entry_count;       /* 0: zero work, nothing to dispatch */
     tiler_hip_realized_entry entries[4]; /* in execution order */
+    uint32_t constant_slot;     /* the CONSTANT slot (slot_count when there is none) */
+    uint32_t constant_bytes;    /* its contents: constant[0 .. constant_bytes) */
+    uint8_t constant[TILER_HIP_REALIZATION_CONSTANT_BYTES];
 } tiler_hip_realization;
 
 /* Refuses (pre-commit, typed) what the family entry point would refuse for

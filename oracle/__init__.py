@@ -91,6 +91,11 @@ _SIGS = {
     "tiler_oracle_rms_norm_grouped_f32": (_I32, [_P, _P, _U64, _U64, _U32, _I32, _U32, _U32, _P]),
     "tiler_oracle_softmax_grouped_f32": (_I32, [_P, _U64, _U64, _U32, _U32, _P]),
     "tiler_oracle_softmax_segmented_f32": (_I32, [_P, _U64, _U64, _U64, _U32, _U32, _P]),
+    "tiler_oracle_expression_f32": (_I32, [_P, _P, _P, _U32, _U32, _P, _U64, _P, _I32, _I32]),
+    "tiler_oracle_expression_bf16": (_I32, [_P, _P, _P, _U32, _U32, _P, _U64, _P]),
+    "tiler_oracle_bf16_exact_add": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16]),
+    "tiler_oracle_bf16_exact_multiply": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16]),
+    "tiler_oracle_fold_f32": (_I32, [_P, _U32, _P, _U64, _U32, _U32, _U32, _P, _I32, _I32]),
 }
 
 
@@ -337,3 +342,61 @@ def audit_device_exp(margin_log2: int = -48, threads: int = 8, cap: int = 1 << 1
 def device_exp_f32(s: float) -> float:
     """The device's binary32 exp, restated (see audit_device_exp)."""
     return float(lib().tiler_oracle_device_exp_f32(s))
+
+
+def _node_arrays(nodes):
+    ops = np.array([nd[0] for nd in nodes], dtype=np.uint32)
+    a = np.array([nd[1] for nd in nodes], dtype=np.uint32)
+    b = np.array([nd[2] if len(nd) > 2 else 0 for nd in nodes], dtype=np.uint32)
+    return ops, a, b
+
+
+def expression_f32(nodes, inputs, root=None, input_mode=PRESERVE, result_mode=PRESERVE) -> np.ndarray:
+    """A pointwise f32 expression DAG (pointwise.rs:74-140): `nodes` are
+    (op, a, b) triples (0 input, 1 constant, 2 add, 3 multiply, 4 divide,
+    5 exp, 6 rsqrt), `inputs` one array per access ordinal."""
+    ops, a, b = _node_arrays(nodes)
+    ins = [_f32(x).reshape(-1) for x in inputs]
+    n = ins[0].size if ins else 0
+    ptrs = (ctypes.c_void_p * max(1, len(ins)))(*[x.ctypes.data for x in ins])
+    y = np.empty(n, np.float32)
+    root = len(nodes) - 1 if root is None else root
+    _check(lib().tiler_oracle_expression_f32(_ptr(ops), _ptr(a), _ptr(b), len(nodes), root, ptrs, n, _ptr(y),
+                                             input_mode, result_mode), "expression_f32")
+    return y
+
+
+def expression_bf16(nodes, inputs, root=None) -> np.ndarray:
+    """A pointwise bf16 expression DAG (pointwise_bf16.rs): inputs and result
+    as bf16 bit patterns (uint16)."""
+    ops, a, b = _node_arrays(nodes)
+    ins = [np.ascontiguousarray(x, dtype=np.uint16).reshape(-1) for x in inputs]
+    n = ins[0].size if ins else 0
+    ptrs = (ctypes.c_void_p * max(1, len(ins)))(*[x.ctypes.data for x in ins])
+    y = np.empty(n, np.uint16)
+    root = len(nodes) - 1 if root is None else root
+    _check(lib().tiler_oracle_expression_bf16(_ptr(ops), _ptr(a), _ptr(b), len(nodes), root, ptrs, n, _ptr(y)),
+           "expression_bf16")
+    return y
+
+
+def bf16_exact_add(x: int, z: int) -> int:
+    return int(lib().tiler_oracle_bf16_exact_add(x, z))
+
+
+def bf16_exact_multiply(x: int, z: int) -> int:
+    return int(lib().tiler_oracle_bf16_exact_multiply(x, z))
+
+
+def fold_f32(values, dims, reduced_axes, op=0, scale_bits=0, bias_bits=0, input_mode=PRESERVE,
+             result_mode=PRESERVE) -> np.ndarray:
+    """The strict serial fold of a dense tensor over `reduced_axes` (op 0 sum,
+    1 squared, 2 scale-bias, 3 maximum); the kept axes in order."""
+    x = _f32(values).reshape(-1)
+    d = np.ascontiguousarray(dims, dtype=np.uint64)
+    mask = sum(1 << ax for ax in reduced_axes)
+    outputs = int(np.prod([dims[i] for i in range(len(dims)) if not (mask >> i) & 1], dtype=np.int64))
+    out = np.empty(outputs, np.float32)
+    _check(lib().tiler_oracle_fold_f32(_ptr(x), len(dims), _ptr(d), mask, op, scale_bits, bias_bits, _ptr(out),
+                                       input_mode, result_mode), "fold_f32")
+    return out

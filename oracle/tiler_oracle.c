@@ -686,3 +686,183 @@ int32_t tiler_oracle_softmax_grouped_f32(const float *x, uint64_t rows, uint64_t
                                          uint32_t vec, uint32_t waves, float *y) {
     return tiler_oracle_softmax_segmented_f32(x, rows, extent, 0, vec, waves, y);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Pointwise expression DAGs (tiler-ir/src/schedule/pointwise.rs:74-140 and
+ * pointwise_bf16.rs:114-168; the per-node statements of tiler-metal's
+ * pointwise goldens): nodes in topological order, evaluated per element.
+ * f32 nodes: ADD/MULTIPLY/DIVIDE one IEEE rounding (-ffp-contract=off),
+ * EXP and RSQRT the certified values (silu.rs:573-662, rms_norm.rs:219-293),
+ * operand and result subnormal modes (conformance.rs:498-521), then the
+ * canonical NaN.  Opcodes: 0 input (a = ordinal), 1 constant (a = bits),
+ * 2 add, 3 multiply, 4 divide (a, b), 5 exp, 6 rsqrt (a).  Status 1 for a
+ * malformed DAG (operand after its use, bad opcode). */
+int32_t tiler_oracle_expression_f32(const uint32_t *ops, const uint32_t *as, const uint32_t *bs,
+                                    uint32_t count, uint32_t root, const float *const *inputs,
+                                    uint64_t n, float *y, int32_t input_mode, int32_t result_mode) {
+    if (count == 0 || root >= count) return TILER_ORACLE_INVALID_APPLICATION;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (ops[i] > 6) return TILER_ORACLE_INVALID_APPLICATION;
+        if (ops[i] >= 2 && (as[i] >= i || (ops[i] <= 4 && bs[i] >= i)))
+            return TILER_ORACLE_INVALID_APPLICATION;
+    }
+    float *v = (float *)malloc(sizeof(float) * count);
+    if (!v) return TILER_ORACLE_INVALID_APPLICATION;
+    for (uint64_t e = 0; e < n; ++e) {
+        for (uint32_t i = 0; i < count; ++i) {
+            float r;
+            int32_t st = TILER_ORACLE_OK;
+            switch (ops[i]) {
+                case 0: r = inputs[as[i]][e]; break;
+                case 1: r = u2f(as[i]); break;
+                case 2: r = canon(RSLT(OPND(v[as[i]]) + OPND(v[bs[i]]))); break;
+                case 3: r = canon(RSLT(OPND(v[as[i]]) * OPND(v[bs[i]]))); break;
+                case 4: r = canon(RSLT(OPND(v[as[i]]) / OPND(v[bs[i]]))); break;
+                case 5: {
+                    float a = OPND(v[as[i]]);
+                    st = isnan(a) ? (r = a, TILER_ORACLE_OK) : tiler_oracle_certified_exp_f32(a, &r);
+                    r = canon(RSLT(r));
+                    break;
+                }
+                default: {
+                    float a = OPND(v[as[i]]);
+                    st = tiler_oracle_certified_rsqrt_f32(a, &r);
+                    r = canon(RSLT(r));
+                    break;
+                }
+            }
+            if (st) {
+                free(v);
+                return st;
+            }
+            v[i] = r;
+        }
+        y[e] = v[root];
+    }
+    free(v);
+    return TILER_ORACLE_OK;
+}
+
+/* ADR 0091 narrowing of an exact binary128 value to bf16: round to nearest
+ * even at the bf16 quantum of the value's binade (2^-133 below 2^-126),
+ * overflow to infinity at the inclusive midpoint above the largest finite
+ * bf16, signed zero kept.  The quantum scaling is exact in binary128. */
+static uint16_t bf16_of_q(q_t q) {
+    if (isnanq(q)) return CANONICAL_BF16_NAN_BITS;
+    const uint16_t sign = signbitq(q) ? 0x8000u : 0;
+    q_t a = fabsq(q);
+    if (a == 0) return sign;
+    int e;
+    frexpq(a, &e); /* a in [2^(e-1), 2^e) */
+    int ex = e - 1;
+    if (ex < -126) ex = -126;
+    const q_t quantum = ldexpq(1.0Q, ex - 7);
+    q_t m = rintq(a / quantum); /* default rounding: to nearest, ties to even */
+    q_t r = m * quantum;
+    if (r >= ldexpq(1.0Q, 128)) return sign | 0x7f80u;
+    float f = (float)r; /* exact: r is a bf16 value */
+    return sign | (uint16_t)(f2u(f) >> 16);
+}
+
+/* bf16 expressions (pointwise_bf16.rs: INPUT, CONSTANT, ADD, MULTIPLY; each
+ * node one rounding of the exact result to bf16, canonical NaN 0x7fc0;
+ * bf16.rs:238-787 exact_add / exact_multiply then the ADR 0091 rounding).
+ * The exact sum and product of two bf16 values are formed in binary128:
+ * products are exact (16 significant bits); a sum is exact unless the
+ * operands' exponents differ by more than ~104, and then the smaller lies
+ * far below half a bf16 quantum of the larger and binary128 keeps it as a
+ * sticky nonzero remainder, which is all the rounding reads. */
+int32_t tiler_oracle_expression_bf16(const uint32_t *ops, const uint32_t *as, const uint32_t *bs,
+                                     uint32_t count, uint32_t root, const uint16_t *const *inputs,
+                                     uint64_t n, uint16_t *y) {
+    if (count == 0 || root >= count) return TILER_ORACLE_INVALID_APPLICATION;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (ops[i] > 3) return TILER_ORACLE_INVALID_APPLICATION;
+        if (ops[i] >= 2 && (as[i] >= i || bs[i] >= i)) return TILER_ORACLE_INVALID_APPLICATION;
+        if (ops[i] == 1 && as[i] > 0xffffu) return TILER_ORACLE_INVALID_APPLICATION;
+    }
+    uint16_t *v = (uint16_t *)malloc(sizeof(uint16_t) * count);
+    if (!v) return TILER_ORACLE_INVALID_APPLICATION;
+    for (uint64_t e = 0; e < n; ++e) {
+        for (uint32_t i = 0; i < count; ++i) {
+            switch (ops[i]) {
+                case 0: v[i] = inputs[as[i]][e]; break;
+                case 1: v[i] = (uint16_t)as[i]; break;
+                default: {
+                    const q_t x = (q_t)tiler_oracle_bf16_widen(v[as[i]]);
+                    const q_t z = (q_t)tiler_oracle_bf16_widen(v[bs[i]]);
+                    v[i] = bf16_of_q(ops[i] == 2 ? x + z : x * z);
+                }
+            }
+        }
+        y[e] = v[root];
+    }
+    free(v);
+    return TILER_ORACLE_OK;
+}
+
+uint16_t tiler_oracle_bf16_exact_add(uint16_t x, uint16_t z) {
+    return bf16_of_q((q_t)tiler_oracle_bf16_widen(x) + (q_t)tiler_oracle_bf16_widen(z));
+}
+uint16_t tiler_oracle_bf16_exact_multiply(uint16_t x, uint16_t z) {
+    return bf16_of_q((q_t)tiler_oracle_bf16_widen(x) * (q_t)tiler_oracle_bf16_widen(z));
+}
+
+/* ------------------------------------------------------------------------ */
+/* evaluate.rs:498-589 strict_sum over any axis set, with the prologues and the
+ * maximum combiner of tiler-ir/src/kernel/lower.rs:1236-1305, 2485-2500:
+ * survivors in axis order give the output layout; each output folds its
+ * contributors in lexicographic order of the reduced coordinates, seeded at
+ * the first (transformed) contributor.  op 0 sum, 1 squared (canon(x*x)),
+ * 2 scale-bias (canon(canon(x*s) + b)), 3 maximum (NaN-propagating, -0 < +0).
+ * An empty sum commits +0; an empty maximum is refused (model.rs:880-906).
+ * The result is canonicalized. */
+int32_t tiler_oracle_fold_f32(const float *x, uint32_t rank, const uint64_t *dims,
+                              uint64_t reduced_mask, uint32_t op, uint32_t scale_bits,
+                              uint32_t bias_bits, float *out, int32_t input_mode,
+                              int32_t result_mode) {
+    if (rank > 8 || op > 3 || (reduced_mask >> rank)) return TILER_ORACLE_INVALID_APPLICATION;
+    uint64_t stride[8], kept[8], red[8], kept_n = 0, red_n = 0, outputs = 1, contributors = 1;
+    uint64_t total = 1;
+    for (int d = (int)rank - 1; d >= 0; --d) {
+        stride[d] = total;
+        total *= dims[d];
+    }
+    for (uint32_t d = 0; d < rank; ++d) {
+        if (reduced_mask >> d & 1) {
+            red[red_n++] = d;
+            contributors *= dims[d];
+        } else {
+            kept[kept_n++] = d;
+            outputs *= dims[d];
+        }
+    }
+    if (outputs && contributors == 0 && op == 3) return TILER_ORACLE_INVALID_APPLICATION;
+    const float s = u2f(scale_bits), b = u2f(bias_bits);
+    for (uint64_t o = 0; o < outputs; ++o) {
+        uint64_t base = 0, rem = o;
+        for (int k = (int)kept_n - 1; k >= 0; --k) {
+            base += (rem % dims[kept[k]]) * stride[kept[k]];
+            rem /= dims[kept[k]];
+        }
+        float acc = 0.0f;
+        for (uint64_t c = 0; c < contributors; ++c) {
+            uint64_t off = base, r2 = c;
+            for (int k = (int)red_n - 1; k >= 0; --k) {
+                off += (r2 % dims[red[k]]) * stride[red[k]];
+                r2 /= dims[red[k]];
+            }
+            float v = x[off], t;
+            switch (op) {
+                case 1: t = canon(RSLT(OPND(v) * OPND(v))); break;
+                case 2: t = canon(RSLT(OPND(canon(RSLT(OPND(v) * OPND(s)))) + OPND(b))); break;
+                default: t = v;
+            }
+            if (c == 0) acc = t;
+            else if (op == 3) acc = canon(tiler_oracle_maximum_f32(acc, t));
+            else acc = canon(RSLT(OPND(acc) + OPND(t)));
+        }
+        out[o] = contributors == 0 ? 0.0f : canon(acc);
+    }
+    return TILER_ORACLE_OK;
+}

@@ -128,6 +128,27 @@ int32_t tiler_oracle_softmax_segmented_f32(const float *x, uint64_t rows, uint64
                                            uint64_t segment, uint32_t vec, uint32_t waves,
                                            float *y);
 
+/* Pointwise expression DAGs (tiler-ir/src/schedule/pointwise.rs:74-140,
+ * pointwise_bf16.rs:114-168): nodes in topological order, opcodes 0 input
+ * (a = ordinal), 1 constant (a = bits), 2 add, 3 multiply, 4 divide (a, b),
+ * 5 exp, 6 rsqrt (a); y[e] = the root's value at element e.  bf16: opcodes
+ * 0-3, each node rounded once from its exact value (binary128) to bf16. */
+int32_t tiler_oracle_expression_f32(const uint32_t *ops, const uint32_t *as, const uint32_t *bs,
+                                    uint32_t count, uint32_t root, const float *const *inputs,
+                                    uint64_t n, float *y, int32_t input_mode, int32_t result_mode);
+int32_t tiler_oracle_expression_bf16(const uint32_t *ops, const uint32_t *as, const uint32_t *bs,
+                                     uint32_t count, uint32_t root, const uint16_t *const *inputs,
+                                     uint64_t n, uint16_t *y);
+uint16_t tiler_oracle_bf16_exact_add(uint16_t x, uint16_t z);
+uint16_t tiler_oracle_bf16_exact_multiply(uint16_t x, uint16_t z);
+
+/* The strict serial fold over any axis set of a dense row-major tensor:
+ * op 0 sum, 1 squared, 2 scale-bias (scale_bits, bias_bits), 3 maximum. */
+int32_t tiler_oracle_fold_f32(const float *x, uint32_t rank, const uint64_t *dims,
+                              uint64_t reduced_mask, uint32_t op, uint32_t scale_bits,
+                              uint32_t bias_bits, float *out, int32_t input_mode,
+                              int32_t result_mode);
+
 /* Audit of the device's binary32 exp (device_exp_audit.c): the device
  * algorithm restated bit for bit, and an exhaustive scan of every binary32
  * input in (-104, 89).  Inputs whose binary64 value lies within

@@ -129,13 +129,13 @@ def test_graph_replay_matches_eager_on_every_replay(ctx):
     ds, dso = ctx.to_device(sx), ctx.alloc(4)
     try:
         ctx.rms_norm(L.BF16, dx, dw, rows, extent, eps, dy)
-        ctx.sum_f32(ds, 1, sx.size, dso)
+        ctx.sum_f32(ds, 1, sx.size, dso, topology=L.SUM_TREE)
         ctx.synchronize()
         eager_y = dy.download(np.uint16, (rows, extent))
         eager_s = dso.download(np.float32, (1,))
         ctx.capture_begin()
         ctx.rms_norm(L.BF16, dx, dw, rows, extent, eps, dy)
-        ctx.sum_f32(ds, 1, sx.size, dso)
+        ctx.sum_f32(ds, 1, sx.size, dso, topology=L.SUM_TREE)
         graph = ctx.capture_end()
         for _ in range(4):
             ctx.fill_u32(dy, 0, xb.nbytes // 4)

@@ -363,14 +363,21 @@ def test_bf16_contraction_exceptional_values(ctx, m, n, k, silu):
 
 def test_bf16_contraction_full_size_config(ctx):
     """C5: bf16 A, B [4096 x 4096] ~ N(0, 1/sqrt(4096)), f32 accumulation,
-    fused SiLU, bf16 C: relative Frobenius error <= 1e-2 against the strict
-    f32 reference on a sample of 64 rows (rows are independent outputs)."""
+    fused SiLU, bf16 C: the whole 4096 x 4096 output against the strict f32
+    reference (the oracle's multithreaded fold, then silu_f32): relative
+    Frobenius error <= 1e-2 over the output and over every row, and the
+    non-finite pattern identical."""
     m = n = k = 4096
     rng = np.random.default_rng(5)
     ab = oracle.bf16_narrow((rng.standard_normal((m, k), dtype=np.float32) / np.float32(64.0)))
     bb = oracle.bf16_narrow((rng.standard_normal((n, k), dtype=np.float32) / np.float32(64.0)))
     got = families.contract_bf16(ab, bb, L.EPILOGUE_SILU, ctx=ctx)
-    rows = np.arange(0, m, m // 64)
-    ref = oracle.contract_strict_f32(bf16_widen(ab[rows]), bf16_widen(bb), rows.size, n, k)
-    ref = oracle.silu_f32(ref).reshape(rows.size, n)
-    assert _frob(got[rows], ref) <= 1e-2
+    print("[C5] device done; strict f32 oracle over the whole output", flush=True)
+    ref = oracle.contract_strict_f32(bf16_widen(ab), bf16_widen(bb), m, n, k)
+    ref = oracle.silu_f32(ref).reshape(m, n)
+    assert np.isfinite(ref).all() and np.isfinite(bf16_widen(got)).all()
+    assert _frob(got, ref) <= 1e-2
+    g = bf16_widen(got).astype(np.float64)
+    r = ref.astype(np.float64)
+    per_row = np.linalg.norm(g - r, axis=1) / np.linalg.norm(r, axis=1)
+    assert per_row.max() <= 1e-2, f"row {int(per_row.argmax())}: {per_row.max():.3e}"

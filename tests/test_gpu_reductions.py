@@ -119,7 +119,7 @@ def test_tree_sum_full_size_config(ctx):
     do = ctx.alloc(4 * 4)
     try:
         for i in range(4):
-            ctx.sum_f32(dx, 1, n, do.offset(4 * i))
+            ctx.sum_f32(dx, 1, n, do.offset(4 * i), topology=L.SUM_TREE)
         ctx.synchronize()
         got = do.download(np.float32, (4,))
     finally:

@@ -11,6 +11,7 @@ the edges: tail variants, long rows, small grids, unaligned storage.
 from __future__ import annotations
 
 import ctypes
+import functools
 import struct
 
 import pytest
@@ -20,6 +21,7 @@ from tiler_amd.realize import realize
 from tiler_amd.runtime import Refusal
 
 EPS = 0x3727C5AC
+RE = L.PERMITS_REASSOCIATION  # the REASSOCIATE_F32 contract's permission
 
 
 def _descriptor_kernarg_bytes(symbol: str) -> int:
@@ -48,7 +50,7 @@ def _check_segments(rz):
 
 def test_rms_norm_headline_and_variants():
     rz = realize(L.PROGRAM_RMS_NORM, (8192, 4096), dtype=L.BF16, scalars=(EPS,),
-                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST)
+                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, permissions=RE)
     assert rz.symbols == ["tiler_rms_norm_bf16_ch8_full"]
     assert rz.dispatches[0].grid == (2048, 1, 1) and rz.dispatches[0].block == (256, 1, 1)
     assert rz.slots == [(L.SLOT_INPUT, 8192 * 4096 * 2), (L.SLOT_INPUT, 4096 * 2),
@@ -58,28 +60,29 @@ def test_rms_norm_headline_and_variants():
     # kernel arguments: x, w, w_row_stride (0: broadcast), y, rows, extent, eps
     seg = bytes(rz.raw.entries[0].kernargs[:rz.raw.entries[0].kernarg_bytes])
     assert struct.unpack_from("<QQQQQII", seg) == (0, 0, 0, 0, 8192, 4096, EPS)
-    unaligned = realize(L.PROGRAM_RMS_NORM, (8, 4096), dtype=L.BF16, scalars=(EPS,), flags=0)
+    unaligned = realize(L.PROGRAM_RMS_NORM, (8, 4096), dtype=L.BF16, scalars=(EPS,), flags=0, permissions=RE)
     assert unaligned.symbols == ["tiler_rms_norm_bf16_ch8_u"] and unaligned.alignment == 1
-    long_row = realize(L.PROGRAM_RMS_NORM, (3, 20000), dtype=L.BF16, scalars=(EPS,))
+    long_row = realize(L.PROGRAM_RMS_NORM, (3, 20000), dtype=L.BF16, scalars=(EPS,), permissions=RE)
     assert long_row.symbols == ["tiler_rms_norm_bf16_long4_a"]
     assert long_row.dispatches[0].grid == (3, 1, 1) and long_row.dispatches[0].block == (1024, 1, 1)
     _check_segments(long_row)
 
 
 def test_softmax_long_rows_choose_a_launch_form():
+    realize_re = functools.partial(realize, permissions=RE)
     # Rows of more than 4 segments, at most 2 workgroups per CU (the profile's
     # 256): one workgroup per 8192-element segment in one row-synchronized
     # launch, its area zeroed by a fill first (a realized plan's scratch is
     # fresh).  More workgroups: three launches, the partials in two scratch
     # slots of rows * segments f32.  Up to 4 segments: one workgroup per row.
-    rs = realize(L.PROGRAM_SOFTMAX, (32, 131072), flags=L.REGION_ALIGNED16)
+    rs = realize_re(L.PROGRAM_SOFTMAX, (32, 131072), flags=L.REGION_ALIGNED16)
     assert rs.symbols == ["tiler_fill_u32", "tiler_softmax_f32_rowsync_a"]
     sync = 256 + 16 * 512
     assert rs.slots == [(L.SLOT_INPUT, 32 * 131072 * 4), (L.SLOT_OUTPUT, 32 * 131072 * 4), (L.SLOT_SCRATCH, sync)]
     assert rs.dispatches[1].grid == (512, 1, 1) and rs.dispatches[1].block == (256, 1, 1)
     assert struct.unpack_from("<QI4xQ", bytes(rs.raw.entries[0].kernargs[:24])) == (0, 0, sync // 4)
     _check_segments(rs)
-    sp = realize(L.PROGRAM_SOFTMAX, (64, 131072), flags=L.REGION_ALIGNED16)
+    sp = realize_re(L.PROGRAM_SOFTMAX, (64, 131072), flags=L.REGION_ALIGNED16)
     assert sp.symbols == ["tiler_softmax_f32_split_max_a", "tiler_softmax_f32_split_sum_a",
                           "tiler_softmax_f32_split_out_a"]
     assert [d.grid for d in sp.dispatches] == [(16 * 64, 1, 1)] * 3
@@ -88,23 +91,23 @@ def test_softmax_long_rows_choose_a_launch_form():
                         (L.SLOT_SCRATCH, 64 * 16 * 4), (L.SLOT_SCRATCH, 64 * 16 * 4)]
     assert [sorted(s for s, _ in d.bindings) for d in sp.dispatches] == [[0, 2], [0, 2, 3], [0, 1, 2, 3]]
     _check_segments(sp)
-    assert realize(L.PROGRAM_SOFTMAX, (3, 50001)).symbols == ["tiler_fill_u32", "tiler_softmax_f32_rowsync_u"]
-    assert realize(L.PROGRAM_SOFTMAX, (1000, 32769)).symbols[0] == "tiler_softmax_f32_split_max_u"
-    res = realize(L.PROGRAM_SOFTMAX, (2, 32768), flags=L.REGION_ALIGNED16)
+    assert realize_re(L.PROGRAM_SOFTMAX, (3, 50001)).symbols == ["tiler_fill_u32", "tiler_softmax_f32_rowsync_u"]
+    assert realize_re(L.PROGRAM_SOFTMAX, (1000, 32769)).symbols[0] == "tiler_softmax_f32_split_max_u"
+    res = realize_re(L.PROGRAM_SOFTMAX, (2, 32768), flags=L.REGION_ALIGNED16)
     assert res.symbols == ["tiler_softmax_f32_long_r_a"] and res.dispatches[0].grid == (2, 1, 1)
     assert res.dispatches[0].block == (1024, 1, 1) and len(res.slots) == 2
     _check_segments(res)
-    assert realize(L.PROGRAM_SOFTMAX, (7, 8193)).symbols == ["tiler_softmax_f32_long_r_u"]
-    big = realize(L.PROGRAM_SOFTMAX, (100000, 65536), flags=L.REGION_ALIGNED16)
+    assert realize_re(L.PROGRAM_SOFTMAX, (7, 8193)).symbols == ["tiler_softmax_f32_long_r_u"]
+    big = realize_re(L.PROGRAM_SOFTMAX, (100000, 65536), flags=L.REGION_ALIGNED16)
     assert big.dispatches[0].grid == (800000, 1, 1) and big.slots[2] == (L.SLOT_SCRATCH, 3200000)
 
 
 def test_softmax_and_sums():
-    sm = realize(L.PROGRAM_SOFTMAX, (65536, 2048))
+    sm = realize(L.PROGRAM_SOFTMAX, (65536, 2048), permissions=RE)
     assert sm.symbols == ["tiler_softmax_f32_ch8_full"] and sm.dispatches[0].grid == (16384, 1, 1)
     _check_segments(sm)
 
-    tree = realize(L.PROGRAM_SERIAL_SUM, (1, 1 << 24), topology=L.SUM_TREE)
+    tree = realize(L.PROGRAM_SERIAL_SUM, (1, 1 << 24), topology=L.SUM_TREE, permissions=RE)
     assert tree.symbols == ["tiler_sum_f32_grid", "tiler_sum_f32_grid_final"]
     G = L.lib().tiler_hip_sum_tree_workgroups(None, 1 << 24)
     assert tree.dispatches[0].grid == (G, 1, 1) and tree.dispatches[1].grid == (1, 1, 1)
@@ -112,17 +115,17 @@ def test_softmax_and_sums():
     assert [s for s, _ in tree.dispatches[0].bindings] == [0, 2]      # x, partials
     assert [s for s, _ in tree.dispatches[1].bindings] == [2, 1]      # partials, out
     _check_segments(tree)
-    assert realize(L.PROGRAM_SERIAL_SUM, (1, 1000), topology=L.SUM_TREE, flags=0).symbols[0] == \
+    assert realize(L.PROGRAM_SERIAL_SUM, (1, 1000), topology=L.SUM_TREE, flags=0, permissions=RE).symbols[0] == \
         "tiler_sum_f32_grid_unaligned"
-    assert realize(L.PROGRAM_SERIAL_SUM, (64, 1000), topology=L.SUM_TREE).symbols == ["tiler_sum_f32_rows"]
+    assert realize(L.PROGRAM_SERIAL_SUM, (64, 1000), topology=L.SUM_TREE, permissions=RE).symbols == ["tiler_sum_f32_rows"]
 
-    mp = realize(L.PROGRAM_SERIAL_SUM, (3, 120), topology=L.SUM_MULTIPASS, grouping=(4, 30))
+    mp = realize(L.PROGRAM_SERIAL_SUM, (3, 120), topology=L.SUM_MULTIPASS, grouping=(4, 30), permissions=RE)
     assert mp.symbols == ["tiler_sum_f32_partials", "tiler_sum_f32_serial"]
     assert mp.slots[2] == (L.SLOT_SCRATCH, 3 * 4 * 4)
     _check_segments(mp)
 
     coop = realize(L.PROGRAM_SERIAL_SUM, (5, 4 * 3 * 2), topology=L.SUM_COOPERATIVE, grouping=(4, 3, 2),
-                   flags=L.REGION_ALIGNED16 | L.REGION_PARTICIPANT_MAJOR)
+                   flags=L.REGION_ALIGNED16 | L.REGION_PARTICIPANT_MAJOR, permissions=RE)
     assert coop.symbols == ["tiler_sum_f32_cooperative"]
     assert coop.dispatches[0].grid == (5, 1, 1) and coop.dispatches[0].block == (4, 1, 1)
     seg = bytes(coop.raw.entries[0].kernargs[:coop.raw.entries[0].kernarg_bytes])
@@ -132,17 +135,17 @@ def test_softmax_and_sums():
 
 
 def test_contraction_paths():
-    c5 = realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, variant=L.EPILOGUE_SILU)
+    c5 = realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, permissions=RE, variant=L.EPILOGUE_SILU)
     assert c5.symbols == ["tiler_contract_bf16_silu_t256"]
     assert c5.dispatches[0].grid == (256, 1, 1) and c5.dispatches[0].block == (1024, 1, 1)
     _check_segments(c5)
-    assert realize(L.PROGRAM_CONTRACTION, (16, 4096, 4096), dtype=L.BF16).symbols == \
+    assert realize(L.PROGRAM_CONTRACTION, (16, 4096, 4096), dtype=L.BF16, permissions=RE).symbols == \
         ["tiler_contract_bf16_skinny1"]
-    small = realize(L.PROGRAM_CONTRACTION, (1000, 2048, 512), dtype=L.BF16)
+    small = realize(L.PROGRAM_CONTRACTION, (1000, 2048, 512), dtype=L.BF16, permissions=RE)
     assert small.symbols == ["tiler_contract_bf16_t128"] and small.dispatches[0].grid == (8 * 16, 1, 1)
-    assert realize(L.PROGRAM_CONTRACTION, (300, 130, 64), dtype=L.BF16).symbols == \
+    assert realize(L.PROGRAM_CONTRACTION, (300, 130, 64), dtype=L.BF16, permissions=RE).symbols == \
         ["tiler_contract_bf16_g128"]
-    assert realize(L.PROGRAM_CONTRACTION, (300, 128, 60), dtype=L.BF16).symbols == \
+    assert realize(L.PROGRAM_CONTRACTION, (300, 128, 60), dtype=L.BF16, permissions=RE).symbols == \
         ["tiler_contract_bf16_g128_k"]
     strict = realize(L.PROGRAM_CONTRACTION, (40, 70, 9))
     assert strict.symbols == ["tiler_contract_strict_f32"] and strict.dispatches[0].grid == (5, 3, 1)
@@ -195,8 +198,8 @@ def test_zero_work_skips_dispatch():
 
 @pytest.mark.parametrize("kwargs,status", [
     (dict(program=L.PROGRAM_RMS_NORM, extents=(4, 64), dtype=L.F32, scalars=(0,)), L.REFUSE_INVALID_ARGUMENT),
-    (dict(program=L.PROGRAM_SERIAL_SUM, extents=(2, 100), topology=L.SUM_MULTIPASS, grouping=(3, 30)),
-     L.REFUSE_INVALID_ARGUMENT),
+    (dict(program=L.PROGRAM_SERIAL_SUM, extents=(2, 100), topology=L.SUM_MULTIPASS, grouping=(3, 30),
+          permissions=RE), L.REFUSE_INVALID_ARGUMENT),
     (dict(program=L.PROGRAM_SERIAL_SUM, extents=(2, 100), dtype=L.BF16), L.REFUSE_UNSUPPORTED),
     (dict(program=L.PROGRAM_CONTRACTION, extents=(4, 4, 0), dtype=L.BF16), L.REFUSE_INVALID_ARGUMENT),
     (dict(program=L.PROGRAM_CONTRACTION, extents=(4, 4, 4), variant=L.EPILOGUE_SILU), L.REFUSE_UNSUPPORTED),

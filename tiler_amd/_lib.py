@@ -33,8 +33,8 @@ FAIL_TRANSFER = 5
 F32 = 0
 BF16 = 1
 
-SUM_TREE = 0
-SUM_SERIAL = 1
+SUM_SERIAL = 0
+SUM_TREE = 1
 SUM_MULTIPASS = 2
 SUM_COOPERATIVE = 3
 
@@ -58,6 +58,29 @@ PROGRAM_CONTRACTION = 5
 PROGRAM_GATHER = 6
 PROGRAM_BROADCAST = 7
 PROGRAM_CONVERT = 8
+PROGRAM_EXPRESSION = 9
+PROGRAM_FOLD = 10
+PROGRAM_REINDEX = 11
+
+FOLD_SUM = 0
+FOLD_SQUARED = 1
+FOLD_FMA = 2
+FOLD_MAXIMUM = 3
+
+NODE_INPUT = 0
+NODE_CONSTANT = 1
+NODE_ADD = 2
+NODE_MULTIPLY = 3
+NODE_DIVIDE = 4
+NODE_EXP = 5
+NODE_RSQRT = 6
+MAX_EXPRESSION_NODES = 4096
+
+PERMITS_REASSOCIATION = 1
+PERMITS_PERMUTATION = 2
+SUBNORMALS_PRESERVE = 1
+SUBNORMALS_FLUSH_SIGN = 2
+SUBNORMALS_FLUSH_POSITIVE = 3
 
 CONVERT_NARROW_F32_BF16 = 0
 CONVERT_WIDEN_BF16_F32 = 1
@@ -70,6 +93,9 @@ REGION_PARTICIPANT_MAJOR = 8
 SLOT_INPUT = 0
 SLOT_OUTPUT = 1
 SLOT_SCRATCH = 2
+SLOT_CONSTANT = 3
+REALIZATION_CONSTANT_BYTES = 49152
+MAX_SLOTS = 18
 
 
 class TargetProfile(ctypes.Structure):
@@ -170,6 +196,16 @@ class DispatchPlan(ctypes.Structure):
         ("slot_bytes", ctypes.POINTER(ctypes.c_uint64)),
         ("entry_count", ctypes.c_uint32),
         ("entries", ctypes.POINTER(DispatchEntry)),
+        ("slot_contents", ctypes.POINTER(ctypes.c_void_p)),
+    ]
+
+
+class TargetEnvironmentSchema(ctypes.Structure):
+    _fields_ = [
+        ("provider", ctypes.c_char * 64),
+        ("provider_revision", ctypes.c_uint32),
+        ("schema_major", ctypes.c_uint16),
+        ("schema_minor", ctypes.c_uint16),
     ]
 
 
@@ -184,6 +220,10 @@ class SumPlan(ctypes.Structure):
     ]
 
 
+class ExpressionNode(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_uint32), ("a", ctypes.c_uint32), ("b", ctypes.c_uint32)]
+
+
 class Region(ctypes.Structure):
     _fields_ = [
         ("program", ctypes.c_uint32),
@@ -196,6 +236,12 @@ class Region(ctypes.Structure):
         ("strides", ctypes.c_uint64 * 8),
         ("grouping", ctypes.c_uint64 * 3),
         ("scalars", ctypes.c_uint32 * 2),
+        ("permissions", ctypes.c_uint32),
+        ("input_subnormals", ctypes.c_uint32),
+        ("result_subnormals", ctypes.c_uint32),
+        ("node_count", ctypes.c_uint32),
+        ("root", ctypes.c_uint32),
+        ("nodes", ctypes.POINTER(ExpressionNode)),
     ]
 
 
@@ -207,19 +253,22 @@ class RealizedEntry(ctypes.Structure):
         ("kernarg_bytes", ctypes.c_uint32),
         ("kernargs", ctypes.c_uint8 * 256),
         ("binding_count", ctypes.c_uint32),
-        ("binding_slots", ctypes.c_uint32 * 6),
-        ("binding_offsets", ctypes.c_uint32 * 6),
+        ("binding_slots", ctypes.c_uint32 * MAX_SLOTS),
+        ("binding_offsets", ctypes.c_uint32 * MAX_SLOTS),
     ]
 
 
 class Realization(ctypes.Structure):
     _fields_ = [
         ("slot_count", ctypes.c_uint32),
-        ("slot_roles", ctypes.c_uint32 * 6),
-        ("slot_bytes", ctypes.c_uint64 * 6),
+        ("slot_roles", ctypes.c_uint32 * MAX_SLOTS),
+        ("slot_bytes", ctypes.c_uint64 * MAX_SLOTS),
         ("slot_alignment", ctypes.c_uint32),
         ("entry_count", ctypes.c_uint32),
         ("entries", RealizedEntry * 4),
+        ("constant_slot", ctypes.c_uint32),
+        ("constant_bytes", ctypes.c_uint32),
+        ("constant", ctypes.c_uint8 * REALIZATION_CONSTANT_BYTES),
     ]
 
 
@@ -338,6 +387,15 @@ SIGNATURES = {
     "tiler_hip_contract_bf16": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _U32, _P]),
     "tiler_hip_realize": (_S, [_CTX, ctypes.POINTER(Region), ctypes.POINTER(Realization),
                                ctypes.c_char_p, _U64]),
+    "tiler_hip_expression": (_S, [_CTX, _U32, ctypes.POINTER(ExpressionNode), _U32, _U32,
+                                  ctypes.POINTER(_P), _U64, _P, _U32, _U32, _P]),
+    "tiler_hip_fold_f32": (_S, [_CTX, _U32, _P, _U32, ctypes.POINTER(_U64), _U64, _U32, _U32, _P, _P]),
+    "tiler_hip_reindex": (_S, [_CTX, _P, _U64, _U32, ctypes.POINTER(_U64), ctypes.POINTER(ctypes.c_int64),
+                               ctypes.c_int64, _U32, _P, _P]),
+    "tiler_hip_target_environment_support": (_S, [ctypes.POINTER(TargetEnvironmentSchema)]),
+    "tiler_hip_validate_target_environment": (_S, [_P, _U64, ctypes.c_char_p, _U64]),
+    "tiler_hip_observe_target_environment": (_S, [_CTX, _P, _U64, ctypes.POINTER(_U64), ctypes.POINTER(_U32),
+                                                  ctypes.c_char_p, _U64]),
     "tiler_hip_payload_metadata": (_S, [_P, _U64, ctypes.POINTER(_U64)]),
     "tiler_hip_payload_identity": (_S, [_P]),
     "tiler_hip_digest": (_S, [_P, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64), _U32, _P, _U64, _P]),

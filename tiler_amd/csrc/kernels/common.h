@@ -146,4 +146,43 @@ __device__ __forceinline__ float silu_f32(float x) {
   return x / divisor;
 }
 
+// SiLU for a result that is narrowed to bf16 next (the contraction epilogue):
+// returns a binary32 value whose bf16 narrowing equals
+// bf16_narrow(silu_f32(x)) for every binary32 x -- the reference SiLU
+// (silu.rs:511-533), one narrowing, no second semantics.
+// * x >= 17: exp(-x) <= 4.2e-8 < 2^-24, so fl(1 + exp(-x)) = 1 and
+//   silu_f32(x) = x exactly (also +inf).
+// * -80 < x < 17: e^-x = 2^(yh + yl) with yh = fl(-x*log2e) and yl its
+//   rounding error plus the constant's (exact product split by an FMA), from
+//   the hardware 2^yh corrected to first order by yl*ln2; then x / (1 + e)
+//   by the hardware reciprocal and one residual step.  That value is within
+//   a few binary32 steps of silu_f32(x).  Only an f32 result whose low 16 bits
+//   lie within kSiluGuard steps of the bf16 midpoint 0x8000 can round to a
+//   different bf16 than silu_f32(x) does; those (and every other x: NaN,
+//   x <= -80) take silu_f32 itself.
+// The equivalence is checked on the device over all 2^32 binary32 inputs,
+// together with the largest distance between the two values.
+constexpr uint32_t kSiluGuard = 8;
+__device__ __forceinline__ float silu_fast_f32(float x) {
+  const float kLog2e = 0x1.715476p+0f;       // binary32 nearest log2(e)
+  const float kLog2eLo = 0x1.4ae0c0p-26f;    // binary32 nearest log2(e) - kLog2e
+  const float kLn2 = 0x1.62e430p-1f;
+  const float yh = x * -kLog2e;
+  const float yl = __builtin_fmaf(x, -kLog2e, -yh) + x * -kLog2eLo;
+  const float p = __builtin_amdgcn_exp2f(yh);
+  const float e = __builtin_fmaf(p, yl * kLn2, p);
+  const float d = 1.0f + e;
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float s = x * r;
+  return __builtin_fmaf(__builtin_fmaf(-s, d, x), r, s);
+}
+__device__ __forceinline__ float silu_for_bf16(float x) {
+  if (x >= 17.0f) return x;
+  if (x > -80.0f) {
+    const float s = silu_fast_f32(x);
+    if ((__float_as_uint(s) & 0xffffu) - (0x8000u - kSiluGuard) > 2u * kSiluGuard) return s;
+  }
+  return silu_f32(x);
+}
+
 }  // namespace tiler

@@ -8,7 +8,8 @@
 // * tiler_contract_bf16_{,silu_}t256 / t128 -- the cooperative bf16
 //   contraction on MFMA (v_mfma_f32_16x16x32_bf16), LDS-staged by buffer
 //   loads: bf16 operands, f32 accumulation, an optional fused SiLU epilogue on
-//   the f32 accumulator, one bf16 narrowing.  Any m; n and k multiples of 8.
+//   the f32 accumulator (the reference SiLU: bf16(silu_f32(acc)) exactly, via
+//   tiler::silu_for_bf16), one bf16 narrowing.  Any m; n and k multiples of 8.
 // * tiler_contract_bf16_{,silu_}skinny{1..4} -- m <= 64 (decode shapes): B
 //   streamed once into registers, k split over 16 waves, LDS reduction.
 // * tiler_contract_bf16_{,silu_}g128[_k] -- the guarded general form
@@ -19,18 +20,28 @@
 using tiler::canon;
 
 // ---------------------------------------------------------------------------
-extern "C" __global__ void __launch_bounds__(256)
-tiler_contract_strict_f32(const float* __restrict__ a, const float* __restrict__ b, uint32_t m,
-                          uint32_t n, uint32_t k, float* __restrict__ c) {
+// Strict contraction.  T = float: the f32 family.  T = uint16_t: bf16
+// operands widened exactly to binary32, the same fold, then (optionally) the
+// reference SiLU and one bf16 narrowing -- the realization of a bf16
+// contraction region whose contract grants no reassociation (the MFMA forms
+// below regroup the k sum).
+template <typename T, bool kSilu>
+__device__ __forceinline__ void contract_strict_body(const T* __restrict__ a, const T* __restrict__ b,
+                                                     uint32_t m, uint32_t n, uint32_t k, T* __restrict__ c) {
+  constexpr bool kBf16 = sizeof(T) == 2;
   __shared__ float as[16][17];
   __shared__ float bs[16][17];
   const uint32_t tx = threadIdx.x & 15u, ty = threadIdx.x >> 4;
   const uint32_t i0 = blockIdx.y * 16u, j0 = blockIdx.x * 16u;
+  auto widen = [](T v) -> float {
+    if constexpr (kBf16) return tiler::bf16_widen(v);
+    else return v;
+  };
   float acc = -0.0f;  // -0 + first product == first product, bit for bit
   for (uint32_t k0 = 0; k0 < k; k0 += 16) {
     uint32_t kk = k0 + tx;
-    as[ty][tx] = (i0 + ty < m && kk < k) ? a[(uint64_t)(i0 + ty) * k + kk] : 0.0f;
-    bs[ty][tx] = (j0 + ty < n && kk < k) ? b[(uint64_t)(j0 + ty) * k + kk] : 0.0f;
+    as[ty][tx] = (i0 + ty < m && kk < k) ? widen(a[(uint64_t)(i0 + ty) * k + kk]) : 0.0f;
+    bs[ty][tx] = (j0 + ty < n && kk < k) ? widen(b[(uint64_t)(j0 + ty) * k + kk]) : 0.0f;
     __syncthreads();
     const uint32_t steps = (k - k0) < 16u ? (k - k0) : 16u;
     for (uint32_t s = 0; s < steps; ++s) {
@@ -39,7 +50,28 @@ tiler_contract_strict_f32(const float* __restrict__ a, const float* __restrict__
     }
     __syncthreads();
   }
-  if (i0 + ty < m && j0 + tx < n) c[(uint64_t)(i0 + ty) * n + j0 + tx] = canon(acc);
+  if (i0 + ty < m && j0 + tx < n) {
+    float v = canon(acc);
+    if (kSilu) v = tiler::silu_f32(v);
+    if constexpr (kBf16) c[(uint64_t)(i0 + ty) * n + j0 + tx] = (uint16_t)tiler::bf16_narrow(v);
+    else c[(uint64_t)(i0 + ty) * n + j0 + tx] = v;
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_strict_f32(const float* __restrict__ a, const float* __restrict__ b, uint32_t m,
+                          uint32_t n, uint32_t k, float* __restrict__ c) {
+  contract_strict_body<float, false>(a, b, m, n, k, c);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_strict_bf16(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m,
+                           uint32_t n, uint32_t k, uint16_t* __restrict__ c) {
+  contract_strict_body<uint16_t, false>(a, b, m, n, k, c);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_strict_bf16_silu(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m,
+                                uint32_t n, uint32_t k, uint16_t* __restrict__ c) {
+  contract_strict_body<uint16_t, true>(a, b, m, n, k, c);
 }
 
 // ---------------------------------------------------------------------------
@@ -203,14 +235,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kK = 64;
 
-__device__ __forceinline__ float silu_fast(float v) {
-  // Epilogue SiLU: hardware exp2 and reciprocal (relative error ~1e-7),
-  // far inside the bf16 narrowing that follows; -inf -> NaN, +inf -> +inf,
-  // large negative -> -0 as the reference's formula gives.
-  float e = __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
-  return v * __builtin_amdgcn_rcpf(1.0f + e);
-}
-
 // Epilogue store word for a pair of adjacent output rows.  Lanes 2c and 2c+1
 // of a 16x16 MFMA block hold the same two rows (v0: row r, v1: row r+1) of
 // columns 2c and 2c+1.  Each lane narrows its (v0, v1) with
@@ -240,6 +264,10 @@ constexpr int kWaitLgkm0 = 0xC07F;    // lgkmcnt(0)
 // R = (wave * LOADS + j) * 8 .. R + 7 of the LDS tile, lane i the physical
 // chunk i % 8 of row R + i / 8.  voff[j] is that lane's byte offset in the
 // panel at k = 0 (with the chunk swizzle applied); k0_bytes moves along k.
+// The k offset is part of the per-lane offset, not the scalar one: the
+// buffer range check counts the per-lane offset only, so this way the
+// panel's record count bounds every byte read (a ragged last k-tile's
+// chunks past the panel's last row load as zeros, never past the operand).
 template <int LOADS>
 __device__ __forceinline__ void issue_operand_tile(__amdgpu_buffer_rsrc_t panel, const uint32_t* voff,
                                                    uint32_t k0_bytes, uint16_t* lds_tile,
@@ -247,7 +275,7 @@ __device__ __forceinline__ void issue_operand_tile(__amdgpu_buffer_rsrc_t panel,
 #pragma unroll
   for (int j = 0; j < LOADS; ++j)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        panel, (lds_void*)(lds_tile + (wave_s * LOADS + j) * 8u * kK), 16, voff[j], k0_bytes, 0, 0);
+        panel, (lds_void*)(lds_tile + (wave_s * LOADS + j) * 8u * kK), 16, voff[j] + k0_bytes, 0, 0, 0);
 }
 
 template <int TILE, bool kSilu>
@@ -398,8 +426,8 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
       for (int r = 0; r < 4; r += 2) {
         float v0 = acc[i][j][r], v1 = acc[i][j][r + 1];
         if (kSilu) {
-          v0 = silu_fast(v0);
-          v1 = silu_fast(v1);
+          v0 = tiler::silu_for_bf16(v0);
+          v1 = tiler::silu_for_bf16(v1);
         }
         const uint32_t row = i * 16u + grp * 4u + r + (odd ? 1u : 0u);
         const uint32_t col = j * 16u + ((lane & 15u) & ~1u);
@@ -491,7 +519,7 @@ __device__ __forceinline__ void contract_bf16_skinny_body(const uint16_t* __rest
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t row = wave * 16u + grp * 4u + i;
-      const float v = kSilu ? silu_fast(tv[i]) : tv[i];
+      const float v = kSilu ? tiler::silu_for_bf16(tv[i]) : tv[i];
       if (row < m && colg < n) c[(uint64_t)row * n + colg] = (uint16_t)tiler::bf16_narrow(v);
     }
   }

@@ -137,11 +137,15 @@ TILER_MAP_VEC(3, true, _b)
 
 // Broadcast / reindex (tiler-reference/src/structural.rs:75-108): a pure move.
 // out element o (row-major over out_dims) reads source offset
-// sum_d coord_d(o) * src_stride_d; a broadcast axis has stride 0.  Rank <= 8.
+// base + sum_d coord_d(o) * src_stride_d; a broadcast axis has stride 0, a
+// reversed axis a negative stride (two's complement: the sum wraps modulo
+// 2^64 to the in-range offset the host proved, as the mirrored reindex
+// golden's `1 - i%2` does).  Rank <= 8.
 struct BroadcastGeometry {
   uint64_t out_dims[8];
   uint64_t src_strides[8];
   uint32_t rank;
+  uint64_t base;
 };
 
 template <typename T>
@@ -149,7 +153,7 @@ __device__ __forceinline__ void broadcast_body(const T* __restrict__ src, T* __r
                                                uint64_t n, const BroadcastGeometry& g) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    uint64_t rem = i, off = 0;
+    uint64_t rem = i, off = g.base;
     for (int d = (int)g.rank - 1; d >= 0; --d) {
       uint64_t c = rem % g.out_dims[d];
       rem /= g.out_dims[d];
@@ -170,7 +174,7 @@ __device__ __forceinline__ void broadcast_rows_body(const T* __restrict__ src, T
   constexpr uint32_t kPer = 16 / sizeof(T);
   const uint64_t inner = g.out_dims[g.rank - 1], sin = g.src_strides[g.rank - 1];
   for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    uint64_t rem = r, base = 0;
+    uint64_t rem = r, base = g.base;
     for (int d = (int)g.rank - 2; d >= 0; --d) {
       const uint64_t c = rem % g.out_dims[d];
       rem /= g.out_dims[d];

@@ -4,7 +4,10 @@
 #include "reduce.hip"
 #include "rows.hip"
 #include "rows_long.hip"
+#include "rows_strict.hip"
 #include "gather.hip"
 #include "map.hip"
+#include "expr.hip"
+#include "fold.hip"
 #include "convert.hip"
 #include "contract.hip"

@@ -45,6 +45,14 @@ struct BroadcastGeometryHost {
   uint64_t out_dims[8];
   uint64_t src_strides[8];
   uint32_t rank;
+  uint64_t base;
+};
+
+// Host mirror of fold.hip's FoldGeometry.
+struct FoldGeometryHost {
+  uint64_t dims[8];
+  uint64_t strides[8];
+  uint32_t kept_rank, red_rank;
 };
 
 }  // namespace
@@ -73,6 +81,17 @@ Launch& Launch::ptr(uint32_t slot, uint64_t addend) {
   return *this;
 }
 Launch& Launch::null_ptr() { return blob(nullptr, 8, 8); }
+Launch& Launch::ptr_table(const uint32_t* slots, uint32_t count, uint32_t capacity) {
+  if (count > capacity || nbindings + count > kMaxBindings) {
+    overflow = true;
+    return *this;
+  }
+  blob(nullptr, 8 * capacity, 8);
+  if (overflow) return *this;
+  const uint32_t base = arg_offsets[nargs - 1];
+  for (uint32_t i = 0; i < count; ++i) bindings[nbindings++] = {base + 8 * i, slots[i], 0};
+  return *this;
+}
 Launch& Launch::u32(uint32_t v) { return blob(&v, 4, 4); }
 Launch& Launch::u64(uint64_t v) { return blob(&v, 8, 8); }
 Launch& Launch::f32(float v) { return blob(&v, 4, 4); }
@@ -116,6 +135,8 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
   switch (sp.topology) {
     case TILER_HIP_SUM_SERIAL:
       if (rows == 0) return TILER_HIP_OK;
+      if ((rows + 255) / 256 > 0x7fffffffull)
+        return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
       p.add("tiler_sum_f32_serial", (uint32_t)((rows + 255) / 256), 1, 256)
           .ptr(x).u64(rows).u64(extent).u64(1).ptr(out);
       return TILER_HIP_OK;
@@ -124,6 +145,8 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
       if (rows == 0) return TILER_HIP_OK;
       if (P == 0 || (c != 0 && P > UINT64_MAX / c) || P * c != extent)
         return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "partitions do not cover the axis exactly");
+      if (mul_sat(rows, P) / 256 >= 0x7fffffffull)
+        return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more partitions than the launch grid holds");
       const uint32_t part = p.slot(mul_sat(mul_sat(rows, P), 4), kSlotScratch);
       p.add("tiler_sum_f32_partials", (uint32_t)((rows * P + 255) / 256), 1, 256)
           .ptr(x).u64(rows).u64(extent).u64(P).u64(c).ptr(part);
@@ -136,6 +159,7 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
       if (rows == 0) return TILER_HIP_OK;
       if (P == 0 || P > 1024 || c == 0 || R == 0 || P * c * R != extent)
         return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "grouping does not cover the axis exactly");
+      if (rows > 0x7fffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
       p.add("tiler_sum_f32_cooperative", (uint32_t)rows, 1, (uint32_t)P)
           .ptr(x).u64(extent).u32((uint32_t)P).u64(c).u64(R).u32(sp.participant_major ? 1u : 0u).ptr(out);
       return TILER_HIP_OK;
@@ -150,6 +174,7 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
         p.add("tiler_sum_f32_grid_final", 1, 1, 256).ptr(part).u32(G).u64(extent).ptr(out);
         return TILER_HIP_OK;
       }
+      if (rows > 0x7fffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
       p.add("tiler_sum_f32_rows", (uint32_t)rows, 1, 256).ptr(x).u64(extent).ptr(out);
       return TILER_HIP_OK;
     }
@@ -162,7 +187,7 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
 // RMS normalization.  Slots: 0 x, 1 w, 2 y.
 tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
-                               Program& p) {
+                               Program& p, bool strict) {
   float eps;
   std::memcpy(&eps, &eps_bits, 4);
   // rms_norm.rs:462-466: a non-positive or non-finite eps refuses.
@@ -183,6 +208,14 @@ tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_
   const bool al = aligned16(addr[x]) && aligned16(addr[w]) && aligned16(addr[y]) && (extent * elem) % 16 == 0;
   const uint64_t wstride = weight_broadcast ? 0 : extent;
   char name[64];
+  if (strict) {  // the reference's serial fold of the squares: one wave per row
+    if ((rows + 3) / 4 > 0x7fffffffull)
+      return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+    std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict", ty);
+    p.add(name, (uint32_t)((rows + 3) / 4), 1, 256)
+        .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps);
+    return TILER_HIP_OK;
+  }
   if (extent > kWaveRowMax) {  // one workgroup per row
     if (rows > 0x7fffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
     std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_long%u%s", ty, long_row_chunks(extent, vec), al ? "_a" : "_u");
@@ -218,12 +251,19 @@ tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_
 //   valid between calls; a realized plan's scratch is fresh, so its program
 //   zeroes the area with a fill kernel first.
 tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
-                                  const uintptr_t* addr, Program& p) {
+                                  const uintptr_t* addr, Program& p, bool strict) {
   const uint32_t x = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotInput);
   const uint32_t y = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotOutput);
   if (rows == 0 || extent == 0) return TILER_HIP_OK;
   if (extent > 0xffffffffull)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
+  if (strict) {  // the reference's serial exponent sum: one wave per row
+    if ((rows + 3) / 4 > 0x7fffffffull)
+      return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+    p.add("tiler_softmax_f32_strict", (uint32_t)((rows + 3) / 4), 1, 256)
+        .ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
+    return TILER_HIP_OK;
+  }
   const bool al = aligned16(addr[x]) && aligned16(addr[y]) && extent % 4 == 0;
   const char* sfx = al ? "_a" : "_u";
   char name[64];
@@ -423,13 +463,22 @@ tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Pr
 }
 
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
-                                    uint32_t epilogue, const uintptr_t* addr, Program& p) {
+                                    uint32_t epilogue, const uintptr_t* addr, Program& p, bool strict) {
   if (epilogue > TILER_HIP_EPILOGUE_SILU) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "epilogue");
   const uint32_t a = p.slot(mul_sat(mul_sat(m, k), 2), kSlotInput);
   const uint32_t b = p.slot(mul_sat(mul_sat(n, k), 2), kSlotInput);
   const uint32_t c = p.slot(mul_sat(mul_sat(m, n), 2), kSlotOutput);
   if (k == 0) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty contracted extent");
   if (m == 0 || n == 0) return TILER_HIP_OK;
+  if (strict) {  // the strict fold on exactly widened operands (MFMA regroups the k sum)
+    if (m > 0xffffffffull || n > 0xffffffffull || k > 0xffffffffull || (m + 15) / 16 > 65535 ||
+        (n + 15) / 16 > 0x7fffffffull)
+      return p.refuse(TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
+    p.add(epilogue == TILER_HIP_EPILOGUE_SILU ? "tiler_contract_strict_bf16_silu" : "tiler_contract_strict_bf16",
+          (uint32_t)((n + 15) / 16), (uint32_t)((m + 15) / 16), 256)
+        .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n).u32((uint32_t)k).ptr(c);
+    return TILER_HIP_OK;
+  }
   if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull || (m + 127) / 128 > 65535)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
   const bool silu = epilogue == TILER_HIP_EPILOGUE_SILU;
@@ -463,6 +512,285 @@ tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uin
                           : (full ? "tiler_contract_bf16_g128" : "tiler_contract_bf16_g128_k");
   p.add(name, (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 256)
       .ptr(a).ptr(b).u32(m32).u32(n32).u32(k32).ptr(c);
+  return TILER_HIP_OK;
+}
+
+}  // namespace tiler_rt
+
+// ---------------------------------------------------------------------------
+// Pointwise expressions.
+namespace tiler_rt {
+
+namespace {
+
+void put16(std::vector<uint8_t>& v, uint32_t x) {
+  v.push_back((uint8_t)x);
+  v.push_back((uint8_t)(x >> 8));
+}
+void put32(std::vector<uint8_t>& v, uint32_t x) {
+  put16(v, x & 0xffffu);
+  put16(v, x >> 16);
+}
+
+}  // namespace
+
+tiler_hip_status compile_expression(uint32_t dtype, const tiler_hip_expression_node* nodes, uint32_t count,
+                                    uint32_t root, bool epilogue, ExpressionProgram& out, std::string& diag) {
+  auto refuse = [&](tiler_hip_status st, const std::string& what) {
+    diag = what;
+    return st;
+  };
+  if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16) return refuse(TILER_HIP_REFUSE_UNSUPPORTED, "expression dtype");
+  if (count == 0 || !nodes) return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty expression");
+  if (count > TILER_HIP_MAX_EXPRESSION_NODES)
+    return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "expression beyond the 4096-node limit");
+  if (root >= count) return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "root is not a node");
+  std::vector<int64_t> input_of(count, -1);  // node -> ordinal
+  std::vector<uint32_t> ordinals;
+  for (uint32_t i = 0; i < count; ++i) {
+    const tiler_hip_expression_node& nd = nodes[i];
+    const bool bf16_op = nd.op <= TILER_HIP_NODE_MULTIPLY;
+    if (nd.op > TILER_HIP_NODE_RSQRT || (dtype == TILER_HIP_BF16 && !bf16_op))
+      return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "node " + std::to_string(i) + ": operation outside the vocabulary");
+    switch (nd.op) {
+      case TILER_HIP_NODE_INPUT:
+        input_of[i] = nd.a;
+        ordinals.push_back(nd.a);
+        break;
+      case TILER_HIP_NODE_CONSTANT:
+        if (dtype == TILER_HIP_BF16 && nd.a > 0xffffu)
+          return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "node " + std::to_string(i) + ": a bf16 constant is 16 bits");
+        break;
+      case TILER_HIP_NODE_ADD:
+      case TILER_HIP_NODE_MULTIPLY:
+      case TILER_HIP_NODE_DIVIDE:
+        if (nd.a >= i || nd.b >= i)
+          return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "node " + std::to_string(i) + ": operand not defined before use");
+        break;
+      default:  // EXP, RSQRT
+        if (nd.a >= i)
+          return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "node " + std::to_string(i) + ": operand not defined before use");
+    }
+  }
+  // Dense ordinals 0..n-1, each named once (pointwise.rs:222-235).
+  std::vector<uint8_t> seen(ordinals.size(), 0);
+  for (uint32_t o : ordinals) {
+    if (o >= ordinals.size() || seen[o]) return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "input ordinals are not dense");
+    seen[o] = 1;
+  }
+  if (ordinals.empty()) return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "expression reads no input");
+  // Every node reachable from the root (pointwise.rs:420-428).
+  std::vector<uint8_t> live(count, 0);
+  live[root] = 1;
+  for (int64_t i = root; i >= 0; --i) {
+    if (!live[i]) continue;
+    const tiler_hip_expression_node& nd = nodes[i];
+    if (nd.op >= TILER_HIP_NODE_ADD) live[nd.a] = 1;
+    if (nd.op >= TILER_HIP_NODE_ADD && nd.op <= TILER_HIP_NODE_DIVIDE) live[nd.b] = 1;
+  }
+  for (uint32_t i = 0; i < count; ++i)
+    if (!live[i]) return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "node " + std::to_string(i) + " is unreachable from the root");
+  const uint32_t nin = (uint32_t)ordinals.size();
+  if (epilogue && (nin != 1 || nodes[root].op == TILER_HIP_NODE_INPUT))
+    return refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "an epilogue reads exactly the folded value and transforms it");
+  if (nin > kMaxExpressionInputs)
+    return refuse(TILER_HIP_REFUSE_CAPACITY, "more than 16 expression inputs");
+
+  // Execution order: the inputs by ordinal, then every other node in order.
+  std::vector<uint32_t> order;
+  order.reserve(count);
+  std::vector<uint32_t> node_of_ordinal(nin);
+  for (uint32_t i = 0; i < count; ++i)
+    if (input_of[i] >= 0) node_of_ordinal[input_of[i]] = i;
+  for (uint32_t k = 0; k < nin; ++k) order.push_back(node_of_ordinal[k]);
+  for (uint32_t i = 0; i < count; ++i)
+    if (input_of[i] < 0) order.push_back(i);
+  std::vector<uint32_t> pos(count);
+  for (uint32_t s = 0; s < count; ++s) pos[order[s]] = s;
+  std::vector<uint32_t> last(count, 0);  // execution step of the last read
+  for (uint32_t s = 0; s < count; ++s) {
+    const tiler_hip_expression_node& nd = nodes[order[s]];
+    if (nd.op >= TILER_HIP_NODE_ADD) last[nd.a] = s;
+    if (nd.op >= TILER_HIP_NODE_ADD && nd.op <= TILER_HIP_NODE_DIVIDE) last[nd.b] = s;
+  }
+  last[root] = count;  // the result stays live to the end
+  // Linear scan: the lowest free register at each definition; an operand's
+  // register is released at its last read, before the result is placed (the
+  // kernel reads both operands before it writes).
+  std::vector<uint32_t> reg(count, 0);
+  std::vector<uint8_t> used;
+  uint32_t high = 0;
+  out.code.clear();
+  out.code.reserve((size_t)count * kExpressionInstrBytes);
+  for (uint32_t s = 0; s < count; ++s) {
+    const uint32_t i = order[s];
+    const tiler_hip_expression_node& nd = nodes[i];
+    uint32_t ra = 0, rb = 0;
+    if (nd.op >= TILER_HIP_NODE_ADD) {
+      ra = reg[nd.a];
+      rb = nd.op <= TILER_HIP_NODE_DIVIDE ? reg[nd.b] : ra;
+      if (last[nd.a] == s) used[ra] = 0;
+      if (nd.op <= TILER_HIP_NODE_DIVIDE && last[nd.b] == s) used[rb] = 0;
+    }
+    uint32_t d = 0;
+    while (d < used.size() && used[d]) ++d;
+    if (d == used.size()) used.push_back(0);
+    used[d] = 1;
+    reg[i] = d;
+    if (d + 1 > high) high = d + 1;
+    put16(out.code, nd.op);
+    put16(out.code, d);
+    put16(out.code, ra);
+    put16(out.code, rb);
+    put32(out.code, nd.op == TILER_HIP_NODE_INPUT ? nd.a : nd.op == TILER_HIP_NODE_CONSTANT ? nd.a : 0);
+  }
+  out.count = count;
+  out.inputs = nin;
+  out.registers = high;
+  out.result = reg[root];
+  (void)pos;
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status plan_expression(const Target& t, uint32_t dtype, uint64_t n, const ExpressionProgram& prog,
+                                 const Contract& c, const uintptr_t* addr, Program& p) {
+  (void)t;
+  if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16) return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "expression dtype");
+  if (dtype == TILER_HIP_BF16 && c.flushes())
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "a flushing subnormal mode is realized for f32 expressions only");
+  const uint64_t eb = dtype == TILER_HIP_BF16 ? 2 : 4;
+  uint32_t in_slots[kMaxExpressionInputs];
+  for (uint32_t k = 0; k < prog.inputs; ++k) in_slots[k] = p.slot(mul_sat(n, eb), kSlotInput);
+  const uint32_t y = p.slot(mul_sat(n, eb), kSlotOutput);
+  const uint32_t code = p.slot(prog.code.size(), TILER_HIP_SLOT_CONSTANT);
+  p.constant_slot = code;
+  p.constant = prog.code;
+  if (n == 0) return TILER_HIP_OK;
+  const uint32_t in_mode = c.input_mode < 1 ? 1 : c.input_mode, out_mode = c.result_mode < 1 ? 1 : c.result_mode;
+  const char* ty = dtype == TILER_HIP_BF16 ? "bf16" : "f32";
+  char name[48];
+  if (prog.registers <= kExpressionRegisters) {
+    const uint64_t per = dtype == TILER_HIP_BF16 ? 8 : 4;
+    bool vec = n % per == 0 && aligned16(addr[prog.inputs]);
+    for (uint32_t k = 0; k < prog.inputs; ++k) vec = vec && aligned16(addr[k]);
+    const uint32_t nin = prog.inputs <= 4 ? prog.inputs : 0;
+    const uint64_t work = vec ? n / per : n;
+    std::snprintf(name, sizeof(name), "tiler_expr_%s_r16%s_i%u", ty, vec ? "" : "s", nin);
+    p.add(name, blocks_capped(work, 8192), 1, 256)
+        .ptr_table(in_slots, prog.inputs, kMaxExpressionInputs)
+        .ptr(y).ptr(code).u32(prog.count).u32(prog.result).u64(work).u32(in_mode).u32(out_mode);
+    return TILER_HIP_OK;
+  }
+  // Value store in scratch, [register][lane]: as many lanes as keep it within
+  // 256 MiB (at least one workgroup, at most 65536 lanes).
+  uint64_t lanes = (256ull << 20) / (4ull * prog.registers);
+  if (lanes > 65536) lanes = 65536;
+  lanes = lanes / 256 * 256;
+  if (lanes == 0) lanes = 256;
+  const uint64_t needed = (n + 255) / 256 * 256;
+  if (lanes > needed) lanes = needed;
+  const uint32_t store = p.slot(4ull * prog.registers * lanes, kSlotScratch);
+  std::snprintf(name, sizeof(name), "tiler_expr_%s_mem", ty);
+  p.add(name, (uint32_t)(lanes / 256), 1, 256)
+      .ptr_table(in_slots, prog.inputs, kMaxExpressionInputs)
+      .ptr(y).ptr(code).u32(prog.count).u32(prog.result).u64(n).u32(in_mode).u32(out_mode).ptr(store);
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Serial folds over any reduced-axis set.  Slots: x, out, [epilogue program].
+tiler_hip_status plan_fold(uint32_t op, uint32_t rank, const uint64_t* dims, uint64_t reduced_mask,
+                           uint32_t scale_bits, uint32_t bias_bits, const ExpressionProgram* epilogue,
+                           Program& p) {
+  if (op > TILER_HIP_FOLD_MAXIMUM) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "fold variant");
+  if (rank > 8 || (rank && !dims)) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "fold rank");
+  if (reduced_mask >> rank) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "reduced axis beyond the rank");
+  if (epilogue && op == TILER_HIP_FOLD_MAXIMUM)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the maximum fold carries no epilogue");
+  FoldGeometryHost g;
+  std::memset(&g, 0, sizeof(g));
+  uint64_t stride[8], total = 1, outputs = 1, contributors = 1;
+  for (int d = (int)rank - 1; d >= 0; --d) {
+    stride[d] = total;
+    total = mul_sat(total, dims[d]);
+  }
+  for (uint32_t d = 0; d < rank; ++d) {
+    if (reduced_mask >> d & 1) continue;
+    g.dims[g.kept_rank] = dims[d];
+    g.strides[g.kept_rank++] = stride[d];
+    outputs = mul_sat(outputs, dims[d]);
+  }
+  for (uint32_t d = 0; d < rank; ++d) {
+    if (!(reduced_mask >> d & 1)) continue;
+    g.dims[g.kept_rank + g.red_rank] = dims[d];
+    g.strides[g.kept_rank + g.red_rank++] = stride[d];
+    contributors = mul_sat(contributors, dims[d]);
+  }
+  const uint32_t x = p.slot(mul_sat(total, 4), kSlotInput);
+  const uint32_t out = p.slot(mul_sat(outputs, 4), kSlotOutput);
+  uint32_t code = kMaxSlots;
+  if (epilogue) {
+    code = p.slot(epilogue->code.size(), TILER_HIP_SLOT_CONSTANT);
+    p.constant_slot = code;
+    p.constant = epilogue->code;
+  }
+  if (outputs == 0) return TILER_HIP_OK;
+  if (total == UINT64_MAX) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "fold extents overflow");
+  // model.rs:880-906: a maximum over no contributors has no value to commit.
+  if (contributors == 0 && op == TILER_HIP_FOLD_MAXIMUM)
+    return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "an empty maximum has no identity");
+  static const char* const kNames[] = {"tiler_fold_sum_f32", "tiler_fold_squared_f32", "tiler_fold_fma_f32",
+                                       "tiler_fold_maximum_f32"};
+  float scale, bias;
+  std::memcpy(&scale, &scale_bits, 4);
+  std::memcpy(&bias, &bias_bits, 4);
+  Launch& l = p.add(kNames[op], blocks_capped(outputs, 65536), 1, 256)
+                  .ptr(x).ptr(out).u64(outputs).u64(contributors).blob(&g, sizeof(g), 8)
+                  .f32(scale).f32(bias).u32(0);
+  if (epilogue) l.ptr(code).u32(epilogue->count).u32(epilogue->result);
+  else l.null_ptr().u32(0).u32(0);
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Reindex with signed strides.  Slots: src, out.
+tiler_hip_status plan_reindex(uint64_t src_elements, uint32_t rank, const uint64_t* out_dims,
+                              const int64_t* strides, int64_t base, uint32_t element_bytes, Program& p) {
+  if (rank > 8 || (rank && (!out_dims || !strides))) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "reindex rank");
+  if (element_bytes != 2 && element_bytes != 4)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "reindex element width");
+  BroadcastGeometryHost g;
+  std::memset(&g, 0, sizeof(g));
+  g.rank = rank;
+  g.base = (uint64_t)base;
+  uint64_t n = 1;
+  __int128 lo = base, hi = base;
+  bool overflow = false;
+  for (uint32_t d = 0; d < rank; ++d) {
+    g.out_dims[d] = out_dims[d];
+    g.src_strides[d] = (uint64_t)strides[d];
+    n = mul_sat(n, out_dims[d]);
+    if (out_dims[d] == 0) continue;
+    const __int128 span = (__int128)strides[d] * (__int128)(out_dims[d] - 1);
+    if (span < 0) lo += span;
+    else hi += span;
+    if (lo < -((__int128)1 << 100) || hi > ((__int128)1 << 100)) overflow = true;
+  }
+  const uint32_t src = p.slot(mul_sat(src_elements, element_bytes), kSlotInput);
+  const uint32_t out = p.slot(mul_sat(n, element_bytes), kSlotOutput);
+  if (n == 0) return TILER_HIP_OK;
+  if (overflow || n == UINT64_MAX || lo < 0 || hi >= (__int128)src_elements)
+    return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "reindex geometry reads outside the source");
+  const uint64_t inner = rank ? out_dims[rank - 1] : 1;
+  if (rank && inner >= 256) {
+    const uint64_t rows = n / inner;
+    p.add(element_bytes == 4 ? "tiler_broadcast_rows_u32" : "tiler_broadcast_rows_u16",
+          (uint32_t)(rows < 8192 ? rows : 8192), 1, 256)
+        .ptr(src).ptr(out).u64(rows).blob(&g, sizeof(g), 8);
+    return TILER_HIP_OK;
+  }
+  p.add(element_bytes == 4 ? "tiler_broadcast_u32" : "tiler_broadcast_u16", blocks_capped(n, 8192), 1, 256)
+      .ptr(src).ptr(out).u64(n).blob(&g, sizeof(g), 8);
   return TILER_HIP_OK;
 }
 

@@ -14,6 +14,7 @@
 #include <cstdint>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "tiler_hip.h"
 
@@ -21,8 +22,13 @@ namespace tiler_rt {
 
 constexpr uint32_t kMaxKernargBytes = 256;
 constexpr uint32_t kMaxArgs = 12;
-constexpr uint32_t kMaxBindings = 6;
-constexpr uint32_t kMaxSlots = 6;
+constexpr uint32_t kMaxBindings = 18;
+constexpr uint32_t kMaxSlots = 18;
+// Pointwise expressions: at most this many distinct inputs (one pointer each
+// in the kernel's input table) and 16 registers in the register form.
+constexpr uint32_t kMaxExpressionInputs = 16;
+constexpr uint32_t kExpressionRegisters = 16;
+constexpr uint32_t kExpressionInstrBytes = 12;
 constexpr uint32_t kMaxLaunches = 4;
 constexpr uint32_t kMaxSumWorkgroups = 4096;
 // Bytes of partials a context keeps in its workspace (the sum's partials, the
@@ -69,6 +75,8 @@ struct Launch {
   Launch& u64(uint64_t v);
   Launch& f32(float v);
   Launch& blob(const void* p, uint32_t bytes, uint32_t align);
+  // A table of `count` pointers to slots (NULL past count), `capacity` wide.
+  Launch& ptr_table(const uint32_t* slots, uint32_t count, uint32_t capacity);
 };
 
 struct Program {
@@ -78,6 +86,9 @@ struct Program {
   Launch launches[kMaxLaunches];
   uint32_t nlaunches;
   std::string diag;
+  // The CONSTANT slot's contents (an expression's register program), if any.
+  uint32_t constant_slot = kMaxSlots;
+  std::vector<uint8_t> constant;
 
   Program();
   uint32_t slot(uint64_t bytes, uint32_t role);
@@ -94,6 +105,30 @@ struct Target {
   uint64_t row_sync_wait_ticks;  // the row-synchronized softmax's wait bound
 };
 
+// The plan's numerical contract as one region states it.  Zero-initialized
+// is the strict contract.
+struct Contract {
+  bool reassociate = false;     // permits_reassociation
+  uint32_t input_mode = 1;      // 1 preserve, 2 flush sign-preserving, 3 flush to +0
+  uint32_t result_mode = 1;
+  bool flushes() const { return input_mode > 1 || result_mode > 1; }
+};
+
+// A pointwise expression compiled for the interpreter kernels (expr.hip):
+// instructions in execution order (the inputs first, input k into register
+// k), the result register, and the register count the program needs.
+struct ExpressionProgram {
+  std::vector<uint8_t> code;  // 12-byte instructions
+  uint32_t count = 0, inputs = 0, registers = 0, result = 0;
+};
+
+// Checks a DAG the way the reference's verifier does
+// (tiler-ir/src/schedule/pointwise.rs:185-240: operands defined before use,
+// dense input ordinals each named once, every node reachable from the root,
+// the node limit; pointwise_bf16.rs: the bf16 vocabulary) and compiles it.
+tiler_hip_status compile_expression(uint32_t dtype, const tiler_hip_expression_node* nodes, uint32_t count,
+                                    uint32_t root, bool epilogue, ExpressionProgram& out, std::string& diag);
+
 // Direct: the program runs now, on known addresses (it may bind a slot at an
 // offset, and the gather record is armed by the context).  Realized: the
 // program is exported as a dispatch plan (no offsets; it arms its own record).
@@ -109,9 +144,9 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
                               const tiler_hip_sum_plan& sp, const uintptr_t* addr, Program& p);
 tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
-                               Program& p);
+                               Program& p, bool strict = false);
 tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
-                                  const uintptr_t* addr, Program& p);
+                                  const uintptr_t* addr, Program& p, bool strict = false);
 tiler_hip_status plan_map(Mode mode, uint32_t op, uint32_t dtype, int32_t x2_broadcast,
                           uint64_t n, float a, float b, const uintptr_t* addr, Program& p);
 tiler_hip_status plan_broadcast(uint64_t src_elements, uint32_t rank, const uint64_t* out_dims,
@@ -124,6 +159,21 @@ tiler_hip_status plan_convert(Mode mode, uint32_t direction, uint64_t n, const u
                               Program& p);
 tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p);
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
-                                    uint32_t epilogue, const uintptr_t* addr, Program& p);
+                                    uint32_t epilogue, const uintptr_t* addr, Program& p,
+                                    bool strict = false);
+// Pointwise expression over n elements: slots inputs 0..I-1, y, program
+// (CONSTANT), and -- for programs beyond the register form -- the value
+// store (SCRATCH).  `addr` covers the inputs then y.
+tiler_hip_status plan_expression(const Target& t, uint32_t dtype, uint64_t n, const ExpressionProgram& prog,
+                                 const Contract& c, const uintptr_t* addr, Program& p);
+// Serial fold of a dense row-major tensor over the axes in `reduced_mask`.
+// Slots: x, out, and the epilogue's program (CONSTANT) when one is given.
+tiler_hip_status plan_fold(uint32_t op, uint32_t rank, const uint64_t* dims, uint64_t reduced_mask,
+                           uint32_t scale_bits, uint32_t bias_bits, const ExpressionProgram* epilogue,
+                           Program& p);
+// Reindex with signed strides: out (row-major over out_dims) reads source
+// offset base + sum coord_d * strides[d].  Slots: src, out.
+tiler_hip_status plan_reindex(uint64_t src_elements, uint32_t rank, const uint64_t* out_dims,
+                              const int64_t* strides, int64_t base, uint32_t element_bytes, Program& p);
 
 }  // namespace tiler_rt

@@ -161,6 +161,25 @@ const EntryRow kEntries[] = {
     {"tiler_widen_bf16_f32_v8", "convert-bf16-to-f32/widen", 2},
     {"tiler_widen_bf16_f32", "convert-bf16-to-f32/widen", 2},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_bf16", "tensor-contraction-bf16/strict", 3},
+    {"tiler_contract_strict_bf16_silu", "tensor-contraction-bf16/strict+silu", 3},
+    {"tiler_rms_norm_f32_strict", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_bf16_strict", "rms-norm/bf16/strict", 3},
+    {"tiler_softmax_f32_strict", "softmax-f32/strict", 2},
+    {"tiler_fold_sum_f32", "strict-serial-sum-f32/serial-any-axes", 3},
+    {"tiler_fold_squared_f32", "squared-serial-sum-f32/serial", 3},
+    {"tiler_fold_fma_f32", "fused-multiply-add-serial-sum-f32/serial", 3},
+    {"tiler_fold_maximum_f32", "strict-serial-maximum-f32/serial", 3},
+#define TILER_EXPR_ROWS(TY, FAM)                                                                  \
+  {"tiler_expr_" TY "_r16_i0", FAM, 18}, {"tiler_expr_" TY "_r16_i1", FAM, 18},                     \
+      {"tiler_expr_" TY "_r16_i2", FAM, 18}, {"tiler_expr_" TY "_r16_i3", FAM, 18},                 \
+      {"tiler_expr_" TY "_r16_i4", FAM, 18}, {"tiler_expr_" TY "_r16s_i0", FAM, 18},                \
+      {"tiler_expr_" TY "_r16s_i1", FAM, 18}, {"tiler_expr_" TY "_r16s_i2", FAM, 18},               \
+      {"tiler_expr_" TY "_r16s_i3", FAM, 18}, {"tiler_expr_" TY "_r16s_i4", FAM, 18},               \
+      {"tiler_expr_" TY "_mem", FAM, 19}
+    TILER_EXPR_ROWS("f32", "pointwise-f32-expression"),
+    TILER_EXPR_ROWS("bf16", "pointwise-bf16-expression"),
+#undef TILER_EXPR_ROWS
     {"tiler_contract_bf16_g128", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_g128", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_g128_k", "tensor-contraction-bf16/cooperative", 3},
@@ -221,6 +240,9 @@ struct tiler_hip_context {
   int32_t input_subnormals = -1, result_subnormals = -1;  // measured on first query
   std::string arch;
   std::string diag;
+  // Device copies of the expression register programs direct calls ran,
+  // keyed by their bytes (freed at release).
+  std::unordered_map<std::string, void*> expression_programs;
 };
 
 namespace {
@@ -704,6 +726,7 @@ void tiler_hip_release(tiler_hip_context* ctx) {
   hipSetDevice(ctx->device);
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   for (hipModule_t m : ctx->routed_modules) hipModuleUnload(m);
+  for (auto& kv : ctx->expression_programs) hipFree(kv.second);
   if (ctx->module) hipModuleUnload(ctx->module);
   if (ctx->workspace) hipFree(ctx->workspace);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
@@ -843,7 +866,8 @@ tiler_hip_status tiler_hip_plan_dispatch(tiler_hip_context* ctx,
     hipFuncGetAttribute(&maxt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, ctx->prepared[e.prepared]);
     if (threads == 0 || threads > (uint64_t)maxt)
       return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "entry " + std::to_string(i) + " workgroup wider than its pipeline admits");
-    if (e.grid[0] == 0 || e.grid[1] == 0 || e.grid[2] == 0 || e.grid[1] > 65535 || e.grid[2] > 65535)
+    if (e.grid[0] == 0 || e.grid[1] == 0 || e.grid[2] == 0 || e.grid[0] > 0x7fffffffu || e.grid[1] > 65535 ||
+        e.grid[2] > 65535)
       return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "entry " + std::to_string(i) + " grid outside the profile");
     int slds = 0;
     hipFuncGetAttribute(&slds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, ctx->prepared[e.prepared]);
@@ -881,6 +905,17 @@ tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_disp
                                     void* const* slot_pointers) {
   if (!ctx || !plan) return TILER_HIP_FAIL_LAUNCH;
   hipSetDevice(ctx->device);
+  // Constant slots first (an expression's register program), ordered on the
+  // stream before every entry; the host bytes are the caller's for the call.
+  if (plan->slot_contents) {
+    for (uint32_t s = 0; s < plan->slot_count; ++s) {
+      if (!plan->slot_contents[s] || !plan->slot_bytes[s]) continue;
+      if (!slot_pointers[s]) return fail(ctx, TILER_HIP_FAIL_TRANSFER, "constant slot " + std::to_string(s) + " unbound");
+      hipError_t err = hipMemcpyAsync(slot_pointers[s], plan->slot_contents[s], plan->slot_bytes[s],
+                                      hipMemcpyHostToDevice, ctx->stream);
+      if (err != hipSuccess) return fail(ctx, TILER_HIP_FAIL_TRANSFER, hipGetErrorString(err));
+    }
+  }
   std::vector<uint8_t> args;
   for (uint32_t i = 0; i < plan->entry_count; ++i) {
     const tiler_hip_dispatch_entry& e = plan->entries[i];
@@ -1273,7 +1308,196 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t*
 }
 
 // ---------------------------------------------------------------------------
+tiler_hip_status tiler_hip_expression(tiler_hip_context* ctx, uint32_t dtype,
+                                      const tiler_hip_expression_node* nodes, uint32_t node_count,
+                                      uint32_t root, const void* const* inputs, uint64_t n, void* y,
+                                      uint32_t input_subnormals, uint32_t result_subnormals,
+                                      tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::ExpressionProgram prog;
+  std::string diag;
+  tiler_hip_status st = tiler_rt::compile_expression(dtype, nodes, node_count, root, false, prog, diag);
+  if (st != TILER_HIP_OK) return fail(ctx, st, diag);
+  if (n && (!y || (prog.inputs && !inputs))) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  for (uint32_t k = 0; n && k < prog.inputs; ++k)
+    if (!inputs[k]) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Contract c;
+  c.input_mode = input_subnormals ? input_subnormals : 1;
+  c.result_mode = result_subnormals ? result_subnormals : 1;
+  if (c.input_mode > 3 || c.result_mode > 3) return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "unknown subnormal mode");
+  uintptr_t addr[tiler_rt::kMaxSlots] = {};
+  for (uint32_t k = 0; k < prog.inputs; ++k) addr[k] = inputs ? (uintptr_t)inputs[k] : 0;
+  addr[prog.inputs] = (uintptr_t)y;
+  tiler_rt::Program p;
+  st = tiler_rt::plan_expression(target_of(ctx), dtype, n, prog, c, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (!p.nlaunches) return TILER_HIP_OK;
+  hipStream_t s = pick(ctx, stream);
+  // The register program lives on the device once per distinct program (a
+  // synchronous upload on first use; under graph capture an uncached program
+  // refuses, so capture after one eager call).
+  std::string key(p.constant.begin(), p.constant.end());
+  auto it = ctx->expression_programs.find(key);
+  if (it == ctx->expression_programs.end()) {
+    if (capturing(s)) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "expression program not yet resident under graph capture");
+    if (ctx->expression_programs.size() >= 4096) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "too many resident expression programs");
+    void* dev = nullptr;
+    if (hipMalloc(&dev, p.constant.size()) != hipSuccess) return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "expression program");
+    if (hipMemcpy(dev, p.constant.data(), p.constant.size(), hipMemcpyHostToDevice) != hipSuccess) {
+      hipFree(dev);
+      return fail(ctx, TILER_HIP_FAIL_TRANSFER, "expression program upload");
+    }
+    it = ctx->expression_programs.emplace(key, dev).first;
+  }
+  void* slots[tiler_rt::kMaxSlots] = {};
+  for (uint32_t k = 0; k < prog.inputs; ++k) slots[k] = const_cast<void*>(inputs[k]);
+  slots[prog.inputs] = y;
+  slots[prog.inputs + 1] = it->second;
+  bool own = false;
+  if (p.nslots > prog.inputs + 2) {  // the value store
+    if (capturing(s)) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "value store allocation under graph capture");
+    if (hipMallocAsync(&slots[prog.inputs + 2], p.slot_bytes[prog.inputs + 2], s) != hipSuccess)
+      return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "value store allocation failed");
+    own = true;
+  }
+  st = run_program(ctx, p, slots, s);
+  if (own) hipFreeAsync(slots[prog.inputs + 2], s);
+  return st;
+}
+
+tiler_hip_status tiler_hip_fold_f32(tiler_hip_context* ctx, uint32_t variant, const float* x, uint32_t rank,
+                                    const uint64_t* dims, uint64_t reduced_mask, uint32_t scale_bits,
+                                    uint32_t bias_bits, float* out, tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  tiler_hip_status st = tiler_rt::plan_fold(variant, rank, dims, reduced_mask, scale_bits, bias_bits, nullptr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!x || !out)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(x), out};
+  return run_program(ctx, p, slots, pick(ctx, stream));
+}
+
+tiler_hip_status tiler_hip_reindex(tiler_hip_context* ctx, const void* src, uint64_t src_elements, uint32_t rank,
+                                   const uint64_t* out_dims, const int64_t* strides, int64_t base,
+                                   uint32_t element_bytes, void* out, tiler_hip_stream stream) {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  tiler_hip_status st = tiler_rt::plan_reindex(src_elements, rank, out_dims, strides, base, element_bytes, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!src || !out)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(src), out};
+  return run_program(ctx, p, slots, pick(ctx, stream));
+}
+
+// ---------------------------------------------------------------------------
+// Target environment (adapter.rs:295-322; environment.rs:249-400).
+namespace {
+
+constexpr const char* kEnvironmentProvider = "tiler.hip.target-environment";
+constexpr const char* kTargetIdPrefix = "amdgcn-amd-amdhsa--gfx950";
+
+void put_u32_be(std::vector<uint8_t>& v, uint32_t x) {
+  for (int i = 3; i >= 0; --i) v.push_back((uint8_t)(x >> (8 * i)));
+}
+uint32_t get_u32_be(const uint8_t* p) {
+  return (uint32_t)p[0] << 24 | (uint32_t)p[1] << 16 | (uint32_t)p[2] << 8 | p[3];
+}
+
+// The canonical descriptor for a target ID's feature settings.
+std::vector<uint8_t> environment_descriptor(bool sramecc, bool xnack) {
+  std::string id = std::string(kTargetIdPrefix) + ":sramecc" + (sramecc ? "+" : "-") + ":xnack" + (xnack ? "+" : "-");
+  std::vector<uint8_t> v;
+  put_u32_be(v, (uint32_t)id.size());
+  v.insert(v.end(), id.begin(), id.end());
+  put_u32_be(v, 64);
+  return v;
+}
+
+}  // namespace
+
+tiler_hip_status tiler_hip_target_environment_support(tiler_hip_target_environment_schema* out) {
+  if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  std::memset(out, 0, sizeof(*out));
+  copy_text(out->provider, sizeof(out->provider), kEnvironmentProvider);
+  out->provider_revision = 1;
+  out->schema_major = 1;
+  out->schema_minor = 0;
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_validate_target_environment(const void* descriptor, uint64_t bytes, char* diagnostic,
+                                                       uint64_t diagnostic_bytes) {
+  if (!descriptor && bytes) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  const uint8_t* d = static_cast<const uint8_t*>(descriptor);
+  auto refuse = [&](const char* what) {
+    copy_text(diagnostic, diagnostic_bytes, what);
+    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  };
+  if (bytes < 8) return refuse("descriptor shorter than its framing");
+  const uint32_t len = get_u32_be(d);
+  if ((uint64_t)len + 8 != bytes) return refuse("descriptor length does not frame the bytes exactly");
+  const std::string id(reinterpret_cast<const char*>(d + 4), len);
+  if (get_u32_be(d + 4 + len) != 64) return refuse("wavefront size is not 64");
+  for (bool sramecc : {false, true})
+    for (bool xnack : {false, true}) {
+      const std::vector<uint8_t> canonical = environment_descriptor(sramecc, xnack);
+      if (canonical.size() == bytes && std::memcmp(canonical.data(), d, bytes) == 0) {
+        copy_text(diagnostic, diagnostic_bytes, "");
+        return TILER_HIP_OK;
+      }
+    }
+  if (id.rfind(kTargetIdPrefix, 0) != 0) return refuse("target ID is not amdgcn-amd-amdhsa--gfx950");
+  return refuse("target ID features are not the canonical :sramecc(+|-):xnack(+|-) spelling");
+}
+
+tiler_hip_status tiler_hip_observe_target_environment(tiler_hip_context* ctx, uint8_t* descriptor,
+                                                      uint64_t capacity, uint64_t* required, uint32_t* observed,
+                                                      char* reason, uint64_t reason_bytes) {
+  if (!ctx || !observed) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  *observed = 0;
+  if (required) *required = 0;
+  // The runtime's gcnArchName spells the bound device's target ID features
+  // (e.g. "gfx950:sramecc+:xnack-"); without both, nothing is asserted.
+  const std::string& arch = ctx->arch;
+  const auto feature = [&](const char* name) -> int {
+    const std::string on = std::string(":") + name + "+", off = std::string(":") + name + "-";
+    if (arch.find(on) != std::string::npos) return 1;
+    if (arch.find(off) != std::string::npos) return 0;
+    return -1;
+  };
+  const int sramecc = feature("sramecc"), xnack = feature("xnack");
+  if (arch.rfind("gfx950", 0) != 0 || sramecc < 0 || xnack < 0) {
+    copy_text(reason, reason_bytes, "the runtime's architecture name (" + arch + ") does not state both target features");
+    return TILER_HIP_OK;
+  }
+  const std::vector<uint8_t> v = environment_descriptor(sramecc == 1, xnack == 1);
+  if (required) *required = v.size();
+  if (!descriptor || capacity < v.size()) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "descriptor buffer too small");
+  std::memcpy(descriptor, v.data(), v.size());
+  *observed = 1;
+  copy_text(reason, reason_bytes, "");
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Realization recognizer.
+namespace {
+
+tiler_rt::Contract contract_of(const tiler_hip_region* r) {
+  tiler_rt::Contract c;
+  c.reassociate = (r->permissions & TILER_HIP_PERMITS_REASSOCIATION) != 0;
+  c.input_mode = r->input_subnormals ? r->input_subnormals : TILER_HIP_SUBNORMALS_PRESERVE;
+  c.result_mode = r->result_subnormals ? r->result_subnormals : TILER_HIP_SUBNORMALS_PRESERVE;
+  return c;
+}
+
+bool arithmetic(uint32_t program) {
+  return program != TILER_HIP_PROGRAM_GATHER && program != TILER_HIP_PROGRAM_BROADCAST &&
+         program != TILER_HIP_PROGRAM_REINDEX;
+}
+
+}  // namespace
+
 tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip_region* r,
                                    tiler_hip_realization* out, char* diagnostic,
                                    uint64_t diagnostic_bytes) {
@@ -1282,12 +1506,31 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
   const bool al = (r->flags & TILER_HIP_REGION_ALIGNED16) != 0;
   const bool bc = (r->flags & TILER_HIP_REGION_OPERAND_BROADCAST) != 0;
   // A stand-in address per slot: 0 is 16-byte aligned, 1 is not.
-  const uintptr_t addr[tiler_rt::kMaxSlots] = {al ? 0u : 1u, al ? 0u : 1u, al ? 0u : 1u,
-                                               al ? 0u : 1u, al ? 0u : 1u, al ? 0u : 1u};
+  uintptr_t addr[tiler_rt::kMaxSlots];
+  for (uint32_t i = 0; i < tiler_rt::kMaxSlots; ++i) addr[i] = al ? 0u : 1u;
   const uint64_t* e = r->extents;
   const tiler_rt::Target t = target_of(ctx);
+  const tiler_rt::Contract c = contract_of(r);
   tiler_rt::Program p;
   tiler_hip_status st;
+  if (c.input_mode > TILER_HIP_SUBNORMALS_FLUSH_POSITIVE || c.result_mode > TILER_HIP_SUBNORMALS_FLUSH_POSITIVE) {
+    copy_text(diagnostic, diagnostic_bytes, "unknown subnormal mode");
+    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  }
+  // The device preserves subnormals; a flushing contract is realized only
+  // where the kernel implements the modes (f32 expressions).  Byte moves do
+  // no arithmetic.
+  if (c.flushes() && arithmetic(r->program) &&
+      !(r->program == TILER_HIP_PROGRAM_EXPRESSION && r->dtype == TILER_HIP_F32)) {
+    copy_text(diagnostic, diagnostic_bytes,
+              "a flushing subnormal mode is not realized for this program (the device preserves subnormals)");
+    return TILER_HIP_REFUSE_UNSUPPORTED;
+  }
+  auto needs_reassociation = [&](const char* what) {
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                    (std::string(what) + " regroups the fold; the contract grants no reassociation").c_str());
+  };
+  tiler_rt::ExpressionProgram prog;
   switch (r->program) {
     case TILER_HIP_PROGRAM_POINTWISE: {
       float a, b;
@@ -1296,9 +1539,20 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
       st = tiler_rt::plan_map(tiler_rt::Mode::Realized, r->variant, r->dtype, bc ? 1 : 0, e[0], a, b, addr, p);
       break;
     }
+    case TILER_HIP_PROGRAM_EXPRESSION: {
+      st = tiler_rt::compile_expression(r->dtype, r->nodes, r->node_count, r->root, false, prog, p.diag);
+      if (st == TILER_HIP_OK) st = tiler_rt::plan_expression(t, r->dtype, e[0], prog, c, addr, p);
+      break;
+    }
     case TILER_HIP_PROGRAM_SERIAL_SUM: {
       if (r->dtype != TILER_HIP_F32) {
         st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the serial sum is an f32 family");
+        break;
+      }
+      // Tree, multi-pass and cooperative all regroup the contributor sequence
+      // (model.rs:1381-1392, 1520-1531): they need permits_reassociation.
+      if (r->topology != TILER_HIP_SUM_SERIAL && !c.reassociate) {
+        st = needs_reassociation("a split or tree sum");
         break;
       }
       tiler_hip_sum_plan sp;
@@ -1316,12 +1570,29 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
       st = tiler_rt::plan_sum_f32(t, e[0], e[1], sp, addr, p);
       break;
     }
+    case TILER_HIP_PROGRAM_FOLD: {
+      if (r->dtype != TILER_HIP_F32) {
+        st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the folds are f32 families");
+        break;
+      }
+      const bool epi = r->node_count != 0;
+      if (epi) {
+        st = tiler_rt::compile_expression(TILER_HIP_F32, r->nodes, r->node_count, r->root, true, prog, p.diag);
+        if (st != TILER_HIP_OK) break;
+      }
+      st = tiler_rt::plan_fold(r->variant, r->rank, r->extents, r->grouping[0], r->scalars[0], r->scalars[1],
+                               epi ? &prog : nullptr, p);
+      break;
+    }
     case TILER_HIP_PROGRAM_RMS_NORM:
-      st = tiler_rt::plan_rms_norm(r->dtype, bc ? 1 : 0, e[0], e[1], r->scalars[0], addr, p);
+      // Without permits_reassociation the serial fold of the reference runs;
+      // with it, the grouped row fold (the declared grouping).
+      st = tiler_rt::plan_rms_norm(r->dtype, bc ? 1 : 0, e[0], e[1], r->scalars[0], addr, p, !c.reassociate);
       break;
     case TILER_HIP_PROGRAM_SOFTMAX:
-      st = r->dtype == TILER_HIP_F32 ? tiler_rt::plan_softmax_f32(tiler_rt::Mode::Realized, t, e[0], e[1], addr, p)
-                                     : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "softmax is an f32 family");
+      st = r->dtype == TILER_HIP_F32
+               ? tiler_rt::plan_softmax_f32(tiler_rt::Mode::Realized, t, e[0], e[1], addr, p, !c.reassociate)
+               : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "softmax is an f32 family");
       break;
     case TILER_HIP_PROGRAM_CONTRACTION:
       if (r->dtype == TILER_HIP_F32)
@@ -1329,7 +1600,7 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
                  ? tiler_rt::plan_contract_strict_f32(e[0], e[1], e[2], p)
                  : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the strict f32 contraction has no epilogue");
       else if (r->dtype == TILER_HIP_BF16)
-        st = tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p);
+        st = tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p, !c.reassociate);
       else
         st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "contraction dtype");
       break;
@@ -1340,6 +1611,13 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
     case TILER_HIP_PROGRAM_BROADCAST:
       st = tiler_rt::plan_broadcast(r->grouping[0], r->rank, r->extents, r->strides, r->variant, p);
       break;
+    case TILER_HIP_PROGRAM_REINDEX: {
+      int64_t strides[8];
+      for (uint32_t d = 0; d < 8; ++d) strides[d] = (int64_t)r->strides[d];
+      st = tiler_rt::plan_reindex(r->grouping[0], r->rank, r->extents, strides, (int64_t)r->grouping[1],
+                                  r->variant, p);
+      break;
+    }
     case TILER_HIP_PROGRAM_CONVERT:
       st = tiler_rt::plan_convert(tiler_rt::Mode::Realized, r->variant, e[0], addr, p);
       break;
@@ -1350,12 +1628,20 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
     copy_text(diagnostic, diagnostic_bytes, p.diag);
     return st;
   }
+  if (p.constant.size() > TILER_HIP_REALIZATION_CONSTANT_BYTES) {
+    copy_text(diagnostic, diagnostic_bytes, "the program's constant slot exceeds the realization's capacity");
+    std::memset(out, 0, sizeof(*out));
+    return TILER_HIP_REFUSE_CAPACITY;
+  }
   out->slot_count = p.nslots;
   for (uint32_t i = 0; i < p.nslots; ++i) {
     out->slot_roles[i] = p.slot_roles[i];
     out->slot_bytes[i] = p.slot_bytes[i];
   }
   out->slot_alignment = al ? 16 : 1;
+  out->constant_slot = p.constant_slot < p.nslots ? p.constant_slot : p.nslots;
+  out->constant_bytes = (uint32_t)p.constant.size();
+  if (!p.constant.empty()) std::memcpy(out->constant, p.constant.data(), p.constant.size());
   for (uint32_t i = 0; i < p.nlaunches; ++i) {
     const tiler_rt::Launch& l = p.launches[i];
     tiler_hip_realized_entry& d = out->entries[i];

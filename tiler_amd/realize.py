@@ -61,22 +61,35 @@ def _entry_info(index: int):
     return info.symbol.decode(), info.family.decode()
 
 
-def realize(program: int, extents, *, dtype: int = L.F32, topology: int = 0, variant: int = 0,
+def realize(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_SERIAL, variant: int = 0,
             flags: int = L.REGION_ALIGNED16, rank: int = 0, strides=(), grouping=(), scalars=(),
-            ctx=None) -> Realization:
+            permissions: int = 0, input_subnormals: int = 0, result_subnormals: int = 0,
+            nodes=(), root: int | None = None, ctx=None) -> Realization:
     """Realizes one region.  `ctx` (a runtime.Context) lets the bound device's
     CU count decide tile sizes and groupings; without it the declared
-    profile's does (the call is then device-free)."""
+    profile's does (the call is then device-free).
+
+    The contract: `permissions` (L.PERMITS_*) and the two subnormal modes
+    (L.SUBNORMALS_*, 0 preserve) are the plan's numerical contract for this
+    region; the defaults are the strict contract.  `nodes` (op, a, b) and
+    `root` (default: the last node) give an expression's DAG, or a fold's
+    epilogue."""
     r = L.Region()
     r.program, r.topology, r.dtype, r.variant, r.flags, r.rank = program, topology, dtype, variant, flags, rank
     for i, v in enumerate(extents):
         r.extents[i] = int(v)
     for i, v in enumerate(strides):
-        r.strides[i] = int(v)
+        r.strides[i] = int(v) & 0xFFFFFFFFFFFFFFFF
     for i, v in enumerate(grouping):
-        r.grouping[i] = int(v)
+        r.grouping[i] = int(v) & 0xFFFFFFFFFFFFFFFF
     for i, v in enumerate(scalars):
         r.scalars[i] = int(v)
+    r.permissions, r.input_subnormals, r.result_subnormals = permissions, input_subnormals, result_subnormals
+    node_array = (L.ExpressionNode * max(1, len(nodes)))(*[L.ExpressionNode(*nd) for nd in nodes])
+    if len(nodes):
+        r.node_count = len(nodes)
+        r.root = len(nodes) - 1 if root is None else root
+        r.nodes = node_array
     out = L.Realization()
     diag = ctypes.create_string_buffer(256)
     st = L.lib().tiler_hip_realize(ctx.handle if ctx is not None else None, ctypes.byref(r), ctypes.byref(out),
@@ -152,7 +165,7 @@ def route(ctx, realization: Realization, storage, payload=None) -> None:
         return  # zero work: the dispatch is skipped
     for i, ((role, nbytes), buf) in enumerate(zip(rz.slots, storage)):
         if buf is None:
-            if role != L.SLOT_SCRATCH:
+            if role not in (L.SLOT_SCRATCH, L.SLOT_CONSTANT):
                 raise Refusal(L.REFUSE_BINDING_MISMATCH, "route", f"slot {i} needs caller storage")
             continue
         cap = _capacity(buf)
@@ -174,7 +187,15 @@ def route(ctx, realization: Realization, storage, payload=None) -> None:
                                      ctypes.cast(kernargs, ctypes.c_void_p), e.kernarg_bytes,
                                      e.binding_count, slots, offs)
     slot_bytes = (ctypes.c_uint64 * len(rz.slots))(*[b for _, b in rz.slots])
-    plan = L.DispatchPlan(len(rz.slots), slot_bytes, n, entries)
+    # The CONSTANT slot's contents (an expression's register program) travel
+    # with the plan; dispatch uploads them before the first entry.
+    contents = (ctypes.c_void_p * len(rz.slots))()
+    if rz.raw.constant_slot < len(rz.slots):
+        constant = ctypes.create_string_buffer(bytes(rz.raw.constant[:rz.raw.constant_bytes]),
+                                               max(1, rz.raw.constant_bytes))
+        keep.append(constant)
+        contents[rz.raw.constant_slot] = ctypes.cast(constant, ctypes.c_void_p)
+    plan = L.DispatchPlan(len(rz.slots), slot_bytes, n, entries, contents)
     h = ctx.handle
     _raise(L.lib().tiler_hip_plan_dispatch(h, ctypes.byref(plan)), "plan_dispatch", ctx.diagnostic())
     ptrs = (ctypes.c_void_p * len(rz.slots))(*[_address(b) or None for b in storage])

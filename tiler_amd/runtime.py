@@ -218,7 +218,7 @@ class Context:
         return v.value
 
     # -- realization families (device storage, asynchronous) ------------------
-    def sum_f32(self, x, rows: int, extent: int, out, topology: int = L.SUM_TREE,
+    def sum_f32(self, x, rows: int, extent: int, out, topology: int = L.SUM_SERIAL,
                 partitions: int = 0, participants: int = 0, per_partition: int = 0,
                 rounds: int = 0, participant_major: bool = False, stream=None):
         plan = L.SumPlan(topology, 1 if participant_major else 0, partitions, participants,
@@ -283,6 +283,66 @@ class Context:
                       stream=None):
         self._check(L.lib().tiler_hip_contract_bf16(self.handle, _ptr(a), _ptr(b), m, n, k,
                                                     _ptr(c), epilogue, stream), "contract_bf16")
+
+    def expression(self, dtype: int, nodes, inputs, n: int, y, root: int | None = None,
+                   input_subnormals: int = 0, result_subnormals: int = 0, stream=None):
+        """A pointwise expression DAG: `nodes` are (op, a, b) triples (L.NODE_*),
+        `inputs` one device buffer per access ordinal."""
+        arr = (L.ExpressionNode * max(1, len(nodes)))(*[L.ExpressionNode(*nd) for nd in nodes])
+        ptrs = (ctypes.c_void_p * max(1, len(inputs)))(*[_ptr(b) for b in inputs])
+        self._check(L.lib().tiler_hip_expression(self.handle, dtype, arr, len(nodes),
+                                                 len(nodes) - 1 if root is None else root, ptrs, n, _ptr(y),
+                                                 input_subnormals, result_subnormals, stream), "expression")
+
+    def fold_f32(self, variant: int, x, dims, reduced_axes, out, scale_bits: int = 0, bias_bits: int = 0,
+                 stream=None):
+        """Serial fold (L.FOLD_*) of a dense f32 tensor over `reduced_axes`."""
+        rank = len(dims)
+        d = (ctypes.c_uint64 * max(rank, 1))(*dims)
+        mask = sum(1 << a for a in reduced_axes)
+        self._check(L.lib().tiler_hip_fold_f32(self.handle, variant, _ptr(x), rank, d, mask, scale_bits,
+                                               bias_bits, _ptr(out), stream), "fold_f32")
+
+    def reindex(self, src, src_elements: int, out_dims, strides, base: int, element_bytes: int, out,
+                stream=None):
+        rank = len(out_dims)
+        d = (ctypes.c_uint64 * max(rank, 1))(*out_dims)
+        s = (ctypes.c_int64 * max(rank, 1))(*strides)
+        self._check(L.lib().tiler_hip_reindex(self.handle, _ptr(src), src_elements, rank, d, s, base,
+                                              element_bytes, _ptr(out), stream), "reindex")
+
+    # -- target environment (adapter.rs:295-322) ------------------------------
+    def observe_target_environment(self):
+        """(descriptor bytes, None) when observed, (None, reason) when
+        Unavailable (which filters claimed cells, never fails the route)."""
+        buf = ctypes.create_string_buffer(256)
+        need, observed = ctypes.c_uint64(), ctypes.c_uint32()
+        reason = ctypes.create_string_buffer(256)
+        self._check(L.lib().tiler_hip_observe_target_environment(self.handle, buf, 256, ctypes.byref(need),
+                                                                 ctypes.byref(observed), reason, 256),
+                    "observe_target_environment")
+        if not observed.value:
+            return None, reason.value.decode()
+        return buf.raw[:need.value], None
+
+
+def target_environment_support() -> dict:
+    """The one target-environment descriptor schema tiler-hip registers."""
+    s = L.TargetEnvironmentSchema()
+    _raise(L.lib().tiler_hip_target_environment_support(ctypes.byref(s)), "target_environment_support")
+    return {"provider": s.provider.decode(), "revision": s.provider_revision,
+            "schema": (s.schema_major, s.schema_minor)}
+
+
+def validate_target_environment(descriptor: bytes) -> str | None:
+    """None when `descriptor` is the schema's canonical spelling, else the reason."""
+    diag = ctypes.create_string_buffer(256)
+    st = L.lib().tiler_hip_validate_target_environment(descriptor, len(descriptor), diag, 256)
+    if st == L.OK:
+        return None
+    if st != L.REFUSE_INVALID_ARGUMENT:
+        _raise(st, "validate_target_environment")
+    return diag.value.decode()
 
 
 def row_grouping(family: int, dtype: int, extent: int) -> tuple[int, int, int]:
