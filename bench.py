@@ -179,7 +179,10 @@ class Sum(Workload):
                                      "condition_number": float(np.sum(np.abs(x), dtype=np.float64)) / abs(exact)}
             self.xs.append(self._keep(self.ctx.to_device(x)))
         self.out = self._keep(self.ctx.alloc(4))
-        self.ctx.sum_f32(self.xs[0], 1, self.n, self.out, topology=L.SUM_TREE)
+        from tiler_amd import _lib as L
+        # the reassociating tree: the sum under a REASSOCIATE_F32 contract
+        self.topology = L.SUM_TREE
+        self.ctx.sum_f32(self.xs[0], 1, self.n, self.out, topology=self.topology)
         got = float(self.out.download(np.float32, (1,))[0])
         exact = self.conditioning["sum_f64"]
         self.conditioning["device_sum"] = got
@@ -187,7 +190,7 @@ class Sum(Workload):
         return self.sets
 
     def launch(self, i):
-        self.ctx.sum_f32(self.xs[i % self.sets], 1, self.n, self.out, topology=L.SUM_TREE)
+        self.ctx.sum_f32(self.xs[i % self.sets], 1, self.n, self.out, topology=self.topology)
 
     def cpu_baseline(self, budget_s):
         import oracle

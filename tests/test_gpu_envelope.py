@@ -81,7 +81,7 @@ def test_rms_norm_through_the_carried_payload(ctx, carried):
     x = oracle.bf16_narrow(rng.standard_normal((rows, extent)).astype(np.float32))
     w = oracle.bf16_narrow(rng.normal(1.0, 0.1, extent).astype(np.float32))
     rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=L.BF16, scalars=(EPS,),
-                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=ctx)
+                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     (got,) = _routed(ctx, rz, [x, w], [(np.uint16, (rows, extent))], carried)
     dx, dw, dy = ctx.to_device(x), ctx.to_device(w), ctx.alloc(x.nbytes)
     try:
@@ -96,7 +96,7 @@ def test_tree_sum_through_the_carried_payload(ctx, carried):
     print("envelope route: tree sum 3 x 2^20+5", flush=True)
     rows, extent = 3, (1 << 20) + 5
     x = np.random.default_rng(6).uniform(-1, 1, (rows, extent)).astype(np.float32)
-    rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_TREE, ctx=ctx)
+    rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_TREE, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     (got,) = _routed(ctx, rz, [x], [(np.float32, (rows,))], carried)
     want = families.tree_sum(x, (rows, extent), 1, ctx=ctx)
     assert np.array_equal(got.view(np.uint32), np.asarray(want, np.float32).reshape(-1).view(np.uint32))
@@ -108,7 +108,7 @@ def test_bf16_contraction_through_the_carried_payload(ctx, carried):
     rng = np.random.default_rng(7)
     a = oracle.bf16_narrow((rng.standard_normal((m, k)) / 16).astype(np.float32))
     b = oracle.bf16_narrow((rng.standard_normal((n, k)) / 16).astype(np.float32))
-    rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=L.EPILOGUE_SILU, ctx=ctx)
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=L.EPILOGUE_SILU, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     (got,) = _routed(ctx, rz, [a, b], [(np.uint16, (m, n))], carried)
     assert np.array_equal(got, families.contract_bf16(a, b, L.EPILOGUE_SILU, ctx=ctx))
 
@@ -118,7 +118,7 @@ def test_a_symbol_the_payload_does_not_map_is_refused(ctx):
     only = F.payload_metadata(entries=[(b"tiler_map_f32", "tiler_map_f32", [0, 1, 2])])
     data = F.Artifact(payloads=[F.Payload(metadata=only, code=code)]).encode()
     chosen = E.select_payload(E.read_envelope(data))
-    rz = realize(L.PROGRAM_SOFTMAX, (4, 256), ctx=ctx)
+    rz = realize(L.PROGRAM_SOFTMAX, (4, 256), permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     x, y = ctx.alloc(4 * 256 * 4), ctx.alloc(4 * 256 * 4)
     try:
         with pytest.raises(Refusal) as r:

@@ -164,7 +164,7 @@ def test_realized_plans_match_direct_calls(ctx, case):
         x = oracle.bf16_narrow(r.standard_normal((rows, extent)).astype(np.float32))
         w = oracle.bf16_narrow(r.normal(1.0, 0.1, extent).astype(np.float32))
         rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=L.BF16, scalars=(EPS,),
-                     flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=ctx)
+                     flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
         got, want = _route_vs_direct(ctx, rz, [x, w], (np.uint16, rows * extent),
                                      lambda: families.rms_norm_bf16(x, w, EPS, ctx=ctx))
     elif fam == 1:
@@ -172,13 +172,13 @@ def test_realized_plans_match_direct_calls(ctx, case):
         # the direct call synchronizes rows in one launch; the bits must agree
         rows, extent = int(r.integers(1, 9)), int(r.integers(1, 98304))
         x = (r.standard_normal((rows, extent)) * 3).astype(np.float32)
-        rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), ctx=ctx)
+        rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
         got, want = _route_vs_direct(ctx, rz, [x], (np.float32, rows * extent),
                                      lambda: families.softmax_f32((rows, extent), 1, x, ctx=ctx))
     elif fam == 2:
         rows, extent = int(r.integers(1, 40)), int(r.integers(1, 5000))
         x = r.uniform(-1, 1, (rows, extent)).astype(np.float32)
-        rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_TREE, ctx=ctx)
+        rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_TREE, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
         got, want = _route_vs_direct(ctx, rz, [x], (np.float32, rows),
                                      lambda: families.tree_sum(x, (rows, extent), 1, ctx=ctx))
     elif fam == 3:
@@ -186,7 +186,7 @@ def test_realized_plans_match_direct_calls(ctx, case):
         n, k = 8 * max(1, n // 8), 8 * max(1, k // 8)
         a = oracle.bf16_narrow((r.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32))
         b = oracle.bf16_narrow((r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
-        rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=L.EPILOGUE_SILU, ctx=ctx)
+        rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=L.EPILOGUE_SILU, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
         got, want = _route_vs_direct(ctx, rz, [a, b], (np.uint16, m * n),
                                      lambda: families.contract_bf16(a, b, L.EPILOGUE_SILU, ctx=ctx))
     elif fam == 4:

@@ -198,7 +198,10 @@ def test_f32_expression_subnormal_modes(ctx, modes):
     x0 = (rng.standard_normal(n) * 1e-38).astype(np.float32)   # many subnormal operands
     x1 = (rng.standard_normal(n) * 1e-3).astype(np.float32)
     x0[:4] = [-1e-45, 1e-45, -0.0, 5e-39]
-    nodes = [(0, 0, 0), (0, 1, 0), (3, 0, 1), (2, 2, 0), (4, 3, 1), (6, 0, 0), (2, 4, 5)]
+    # x0*0.5 + (x0 / rsqrt(x1*x1)) * x1: subnormal operands (x0) and
+    # subnormal results (x0*0.5, x0*|x1|, ...) on most elements, every node kind
+    nodes = [(0, 0, 0), (0, 1, 0), (3, 1, 1), (6, 2, 0), (4, 0, 3), (3, 4, 1), (1, 0x3F000000, 0), (3, 0, 6),
+             (2, 7, 5)]
     want = oracle.expression_f32(nodes, [x0, x1], input_mode=_O_MODE[modes[0]], result_mode=_O_MODE[modes[1]])
     preserve = oracle.expression_f32(nodes, [x0, x1])
     assert not np.array_equal(bits(want), bits(preserve))  # the modes are observable here

@@ -53,7 +53,7 @@ def _routed(ctx, rz, inputs, outputs):
 def test_serial_sum_routed(ctx):
     rows, extent = 1000, 37
     x = np.random.default_rng(71).standard_normal((rows, extent)).astype(np.float32)
-    rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_SERIAL, ctx=ctx)
+    rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_SERIAL, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     assert rz.symbols == ["tiler_sum_f32_serial"]
     (got,) = _routed(ctx, rz, [x], [(np.float32, (rows,))])
     assert np.array_equal(bits(got), bits(oracle.strict_sum(x, (rows, extent), 1)))
@@ -68,7 +68,7 @@ def test_serial_sum_routed(ctx):
 ])
 def test_grouped_sums_routed(ctx, topology, rows, extent, grouping, flags):
     x = np.random.default_rng(rows + extent).uniform(-1, 1, (rows, extent)).astype(np.float32)
-    rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=topology, grouping=grouping, flags=flags, ctx=ctx)
+    rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=topology, grouping=grouping, flags=flags, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     (got,) = _routed(ctx, rz, [x], [(np.float32, (rows,))])
     from tiler_amd import families
     if topology == L.SUM_MULTIPASS:
@@ -93,7 +93,7 @@ def test_rms_norm_routed(ctx, dtype, rows, extent):
         w = rng.normal(1.0, 0.1, extent).astype(np.float32)
         out_t = np.float32
     rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=dtype, scalars=(EPS,),
-                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=ctx)
+                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     (got,) = _routed(ctx, rz, [x, w], [(out_t, (rows, extent))])
     dx, dw, dy = ctx.to_device(x), ctx.to_device(w), ctx.alloc(x.nbytes)
     try:
@@ -108,7 +108,7 @@ def test_rms_norm_routed(ctx, dtype, rows, extent):
 @pytest.mark.parametrize("rows,extent", [(64, 2048), (5, 300), (2, 40000), (150, 20001)])
 def test_softmax_routed(ctx, rows, extent):
     x = (np.random.default_rng(extent).standard_normal((rows, extent)) * 3).astype(np.float32)
-    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), ctx=ctx)
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     (got,) = _routed(ctx, rz, [x], [(np.float32, (rows, extent))])
     import tiler_amd
     vec, waves, seg = tiler_amd.row_grouping(L.ROWS_SOFTMAX, L.F32, extent)
@@ -165,7 +165,7 @@ def test_bf16_contraction_routed(ctx, m, n, k, silu):
     a = oracle.bf16_narrow((rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32))
     b = oracle.bf16_narrow((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
     ep = L.EPILOGUE_SILU if silu else L.EPILOGUE_NONE
-    rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=ep, ctx=ctx)
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=ep, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     (got,) = _routed(ctx, rz, [a, b], [(np.uint16, (m, n))])
     from tiler_amd import families
     assert np.array_equal(got, families.contract_bf16(a, b, ep, ctx=ctx))
@@ -175,13 +175,13 @@ def test_strict_contraction_routed(ctx):
     rng = np.random.default_rng(73)
     a = rng.standard_normal((40, 9)).astype(np.float32)
     b = rng.standard_normal((70, 9)).astype(np.float32)
-    rz = realize(L.PROGRAM_CONTRACTION, (40, 70, 9), ctx=ctx)
+    rz = realize(L.PROGRAM_CONTRACTION, (40, 70, 9), permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     (got,) = _routed(ctx, rz, [a, b], [(np.float32, (40, 70))])
     assert np.array_equal(bits(got).reshape(-1), bits(oracle.contract_strict_f32(a, b, 40, 70, 9)).reshape(-1))
 
 
 def test_route_refuses_before_commit(ctx):
-    rz = realize(L.PROGRAM_SOFTMAX, (4, 256), ctx=ctx)
+    rz = realize(L.PROGRAM_SOFTMAX, (4, 256), permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
     x = ctx.alloc(4 * 256 * 4)
     small = ctx.alloc(64)
     try:

@@ -151,7 +151,7 @@ __device__ __forceinline__ float silu_f32(float x) {
 // bf16_narrow(silu_f32(x)) for every binary32 x -- the reference SiLU
 // (silu.rs:511-533), one narrowing, no second semantics.
 // * x >= 17: exp(-x) <= 4.2e-8 < 2^-24, so fl(1 + exp(-x)) = 1 and
-//   silu_f32(x) = x exactly (also +inf).
+//   silu_f32(x) = x exactly (also +inf).  x = +-0: +-0.
 // * -80 < x < 17: e^-x = 2^(yh + yl) with yh = fl(-x*log2e) and yl its
 //   rounding error plus the constant's (exact product split by an FMA), from
 //   the hardware 2^yh corrected to first order by yl*ln2; then x / (1 + e)
@@ -178,6 +178,8 @@ __device__ __forceinline__ float silu_fast_f32(float x) {
 }
 __device__ __forceinline__ float silu_for_bf16(float x) {
   if (x >= 17.0f) return x;
+  // silu(+-0) = +-0 / 2; the residual step would lose the sign of a zero.
+  if (x == 0.0f) return x;
   if (x > -80.0f) {
     const float s = silu_fast_f32(x);
     if ((__float_as_uint(s) & 0xffffu) - (0x8000u - kSiluGuard) > 2u * kSiluGuard) return s;

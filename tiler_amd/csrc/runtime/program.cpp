@@ -707,6 +707,9 @@ tiler_hip_status plan_fold(uint32_t op, uint32_t rank, const uint64_t* dims, uin
   if (reduced_mask >> rank) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "reduced axis beyond the rank");
   if (epilogue && op == TILER_HIP_FOLD_MAXIMUM)
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the maximum fold carries no epilogue");
+  // The fold kernel evaluates its epilogue in a 16-register file.
+  if (epilogue && epilogue->registers > kExpressionRegisters)
+    return p.refuse(TILER_HIP_REFUSE_CAPACITY, "epilogue needs more than 16 live values");
   FoldGeometryHost g;
   std::memset(&g, 0, sizeof(g));
   uint64_t stride[8], total = 1, outputs = 1, contributors = 1;
