@@ -450,6 +450,19 @@ typedef struct {
 tiler_hip_status tiler_hip_sum_f32(tiler_hip_context *ctx, const float *x, uint64_t rows,
                                    uint64_t extent, float *out, const tiler_hip_sum_plan *plan,
                                    tiler_hip_stream stream);
+/* tiler_hip_sum_f32 without any allocation, for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference: it exists for
+ * those callers only.  Same plan, same kernels and the same bits as
+ * tiler_hip_sum_f32; the partials (the tree's workgroup partials, the
+ * multi-pass split's) live in a static device array of 8 MiB that each GPU
+ * holds until the process ends, resolved per device at tiler_hip_bind.  A
+ * plan whose partials exceed 8 MiB refuses with TILER_HIP_REFUSE_CAPACITY.
+ * Calls on one GPU share that array: calls that overlap (other streams,
+ * other contexts of the same device) race. */
+tiler_hip_status tiler_hip_sum_f32_noalloc(tiler_hip_context *ctx, const float *x, uint64_t rows,
+                                           uint64_t extent, float *out, const tiler_hip_sum_plan *plan,
+                                           tiler_hip_stream stream);
 /* Workgroups the single-output tree uses for n contributors (its grouping). */
 uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context *ctx, uint64_t n);
 

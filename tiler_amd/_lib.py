@@ -370,6 +370,7 @@ SIGNATURES = {
     "tiler_hip_graph_launch": (_S, [_CTX, _P, _P]),
     "tiler_hip_graph_destroy": (_S, [_CTX, _P]),
     "tiler_hip_sum_f32": (_S, [_CTX, _P, _U64, _U64, _P, ctypes.POINTER(SumPlan), _P]),
+    "tiler_hip_sum_f32_noalloc": (_S, [_CTX, _P, _U64, _U64, _P, ctypes.POINTER(SumPlan), _P]),
     "tiler_hip_sum_tree_workgroups": (_U32, [_CTX, _U64]),
     "tiler_hip_row_grouping": (_S, [_U32, _U32, _U64, ctypes.POINTER(_U32), ctypes.POINTER(_U32),
                                     ctypes.POINTER(_U64)]),

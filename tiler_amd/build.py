@@ -60,6 +60,13 @@ def build(verbose: bool = False) -> str:
         fh.write(source_bundle())
     os.replace(bundle + ".tmp", bundle)
 
+    # The no-allocation entry point's static device array: one small HIP
+    # translation unit compiled by hipcc for gfx950, so the runtime registers
+    # the array and hipGetSymbolAddress can resolve it per device.
+    noalloc_obj = os.path.join(BUILD, "noalloc.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-x", "hip", "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC",
+          "-c", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{ROOT}/include",
+          "-o", noalloc_obj, os.path.join(CSRC, "runtime", "noalloc.hip")], stderr=subprocess.DEVNULL)
     payload_obj = os.path.join(BUILD, "payload.o")
     _run(["gcc", "-c", f'-DTILER_HSACO_PATH="{HSACO}"', f'-DTILER_SOURCE_BUNDLE_PATH="{bundle}"', "-o", payload_obj,
           os.path.join(CSRC, "runtime", "payload.S")])
@@ -72,7 +79,7 @@ def build(verbose: bool = False) -> str:
           os.path.join(CSRC, "runtime", "digest.cpp"),
           os.path.join(CSRC, "runtime", "envelope.cpp"),
           os.path.join(CSRC, "runtime", "code_object.cpp"),
-          payload_obj,
+          payload_obj, noalloc_obj,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])
     os.replace(tmp_lib, LIB)
     if verbose:

@@ -20,6 +20,7 @@
 #include "code_object.h"
 #include "digest.h"
 #include "envelope.h"
+#include "noalloc.h"
 #include "program.h"
 
 extern "C" const uint8_t tiler_hip_code_object[];
@@ -243,6 +244,11 @@ struct tiler_hip_context {
   // Device copies of the expression register programs direct calls ran,
   // keyed by their bytes (freed at release).
   std::unordered_map<std::string, void*> expression_programs;
+  // This device's copy of the no-allocation entry point's static scratch
+  // array (noalloc.hip), resolved at bind; null if resolution failed
+  // (noalloc_error holds the HIP error).
+  void* noalloc_scratch = nullptr;
+  int noalloc_error = 0;
 };
 
 namespace {
@@ -697,6 +703,10 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
   hipMemset(ctx->workspace, 0, ws_bytes);
   hipMemset(ctx->gather_bad, 0xff, 8);
   hipDeviceSynchronize();
+  // The no-allocation entry point's scratch: this device's address of the
+  // static array, resolved once here with the device current.
+  ctx->noalloc_error = tiler_hip_noalloc_scratch_address(&ctx->noalloc_scratch);
+  if (ctx->noalloc_error != 0) ctx->noalloc_scratch = nullptr;
   if (env) {
     std::memset(env, 0, sizeof(*env));
     env->device_ordinal = ordinal;
@@ -1142,6 +1152,32 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
   st = run_program(ctx, p, slots, s);
   if (own) hipFreeAsync(slots[2], s);
   return st;
+}
+
+tiler_hip_status tiler_hip_sum_f32_noalloc(tiler_hip_context* ctx, const float* x, uint64_t rows,
+                                           uint64_t extent, float* out, const tiler_hip_sum_plan* plan,
+                                           tiler_hip_stream stream) {
+  if (!ctx || !plan || (rows && !out) || (rows && extent && !x))
+    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  const uintptr_t addr[3] = {(uintptr_t)x, (uintptr_t)out, 0};
+  tiler_hip_status st = tiler_rt::plan_sum_f32(target_of(ctx), rows, extent, *plan, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(x), out, nullptr};
+  if (p.nslots > 2 && p.nlaunches) {
+    // The partials go to this device's static scratch array, through the
+    // address bind resolved: nothing is allocated.  Every stage-1 launch
+    // writes all the partials its second launch reads, so nothing needs
+    // clearing; overlapping calls on one GPU share the array and race.
+    if (!ctx->noalloc_scratch)
+      return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED,
+                  "the static scratch array could not be resolved at bind (HIP error " +
+                      std::to_string(ctx->noalloc_error) + ")");
+    if (p.slot_bytes[2] > TILER_HIP_NOALLOC_SCRATCH_BYTES)
+      return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "partials exceed the 8 MiB static scratch array");
+    slots[2] = ctx->noalloc_scratch;
+  }
+  return run_program(ctx, p, slots, pick(ctx, stream));
 }
 
 tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, const void* x,
