@@ -5,9 +5,9 @@
 // SiLU (tiler-reference/src/silu.rs:511-533) narrowed once.
 //
 // result[0] mismatching inputs          result[1] lowest mismatching pattern
-// result[2] fast-domain inputs that fell back to silu_f32
+// result[2] fast-domain inputs marked for silu_f32 (near a bf16 midpoint)
 // result[3] largest distance, in binary32 steps, between silu_fast_f32(x)
-//           and silu_f32(x) over the fast domain (-80 < x < 17)
+//           and silu_f32(x) over the fast domain (-80 < x < 2^127)
 // result[4] inputs in the fast domain
 //
 // Test infrastructure: compiled into its own code object by the test build
@@ -46,14 +46,14 @@ tiler_audit_silu_for_bf16(uint64_t first, uint64_t count, unsigned long long* re
       ++mis;
       if (bits < low) low = bits;
     }
-    if (x > -80.0f && x < 17.0f) {
+    if (x > -80.0f && x < 0x1.0p127f) {
       ++fast;
-      const float s = tiler::silu_fast_f32(x);
+      bool marked;
+      const float s = tiler::silu_bf16_candidate(x, marked);
       const int64_t d = ordered(s) - ordered(exact);
       const unsigned long long ad = (unsigned long long)(d < 0 ? -d : d);
       if (ad > dist) dist = ad;
-      const uint32_t lo16 = __float_as_uint(s) & 0xffffu;
-      if (lo16 - (0x8000u - tiler::kSiluGuard) <= 2u * tiler::kSiluGuard) ++fall;
+      if (marked) ++fall;
     }
   }
   atomicAdd(&s_mis, mis);

@@ -147,19 +147,21 @@ __device__ __forceinline__ float silu_f32(float x) {
 }
 
 // SiLU for a result that is narrowed to bf16 next (the contraction epilogue):
-// returns a binary32 value whose bf16 narrowing equals
+// silu_for_bf16 returns a binary32 value whose bf16 narrowing equals
 // bf16_narrow(silu_f32(x)) for every binary32 x -- the reference SiLU
 // (silu.rs:511-533), one narrowing, no second semantics.
-// * x >= 17: exp(-x) <= 4.2e-8 < 2^-24, so fl(1 + exp(-x)) = 1 and
-//   silu_f32(x) = x exactly (also +inf).  x = +-0: +-0.
-// * -80 < x < 17: e^-x = 2^(yh + yl) with yh = fl(-x*log2e) and yl its
-//   rounding error plus the constant's (exact product split by an FMA), from
-//   the hardware 2^yh corrected to first order by yl*ln2; then x / (1 + e)
-//   by the hardware reciprocal and one residual step.  That value is within
-//   a few binary32 steps of silu_f32(x).  Only an f32 result whose low 16 bits
-//   lie within kSiluGuard steps of the bf16 midpoint 0x8000 can round to a
-//   different bf16 than silu_f32(x) does; those (and every other x: NaN,
-//   x <= -80) take silu_f32 itself.
+// * The fast value (silu_fast_f32), nine operations: e^-x = 2^(yh + yl) with
+//   yh = fl(-x*log2e) and yl its rounding error (exact, by an FMA) plus the
+//   constant's own, from the hardware 2^yh corrected to first order by
+//   yl*ln2; then x times the hardware reciprocal of fl(1 + e).  For
+//   -80 < x < 2^127 it is within a few binary32 steps of silu_f32(x).  It is
+//   x itself for x >= 17 (e <= e^-17 < 2^-24, so fl(1 + e) = 1), and keeps
+//   the sign of a zero (x * 0.5).
+// * Only a value whose low 16 bits lie within kSiluGuard steps of the bf16
+//   midpoint 0x8000 can round to a different bf16 than silu_f32(x) does;
+//   those, and every x outside (-80, 2^127) (NaN, +-inf, x <= -80, the
+//   largest finite x), are marked exact (silu_bf16_candidate) and take
+//   silu_f32 itself.
 // The equivalence is checked on the device over all 2^32 binary32 inputs,
 // together with the largest distance between the two values.
 constexpr uint32_t kSiluGuard = 8;
@@ -168,23 +170,23 @@ __device__ __forceinline__ float silu_fast_f32(float x) {
   const float kLog2eLo = 0x1.4ae0c0p-26f;    // binary32 nearest log2(e) - kLog2e
   const float kLn2 = 0x1.62e430p-1f;
   const float yh = x * -kLog2e;
-  const float yl = __builtin_fmaf(x, -kLog2e, -yh) + x * -kLog2eLo;
+  const float yl = __builtin_fmaf(x, -kLog2eLo, __builtin_fmaf(x, -kLog2e, -yh));
   const float p = __builtin_amdgcn_exp2f(yh);
   const float e = __builtin_fmaf(p, yl * kLn2, p);
-  const float d = 1.0f + e;
-  const float r = __builtin_amdgcn_rcpf(d);
-  const float s = x * r;
-  return __builtin_fmaf(__builtin_fmaf(-s, d, x), r, s);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+// The fast value, branch free, and whether only silu_f32(x) is known to
+// narrow right.
+__device__ __forceinline__ float silu_bf16_candidate(float x, bool& exact) {
+  const float v = silu_fast_f32(x);
+  const bool near_midpoint = (__float_as_uint(v) & 0xffffu) - (0x8000u - kSiluGuard) <= 2u * kSiluGuard;
+  exact = !(x > -80.0f && x < 0x1.0p127f) || near_midpoint;
+  return v;
 }
 __device__ __forceinline__ float silu_for_bf16(float x) {
-  if (x >= 17.0f) return x;
-  // silu(+-0) = +-0 / 2; the residual step would lose the sign of a zero.
-  if (x == 0.0f) return x;
-  if (x > -80.0f) {
-    const float s = silu_fast_f32(x);
-    if ((__float_as_uint(s) & 0xffffu) - (0x8000u - kSiluGuard) > 2u * kSiluGuard) return s;
-  }
-  return silu_f32(x);
+  bool exact;
+  const float v = silu_bf16_candidate(x, exact);
+  return exact ? silu_f32(x) : v;
 }
 
 }  // namespace tiler

@@ -254,6 +254,38 @@ __device__ __forceinline__ uint32_t pack_row_pair(float v0, float v1, uint32_t s
   return __builtin_amdgcn_perm(q, p, sel);
 }
 
+// One value's bf16 bits, narrowed as pack_row_pair narrows.
+__device__ __forceinline__ uint16_t narrow_one(float v) {
+  const float qnan = __uint_as_float(0x7fc00000u);
+  const f32x2v f = {v != v ? qnan : v, 0.0f};
+  return (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2v));
+}
+
+// Row pair p = 8i + 2j + r/2 of a wave's 4 x 4 MFMA blocks (accumulators
+// r, r+1 of block (i, j)), p wave-uniform: a scalar branch per case, which
+// needs neither indexed registers nor private memory.
+__device__ __forceinline__ void accumulator_pair(const f32x4 (&acc)[4][4], uint32_t p, float& x0, float& x1) {
+  switch (p) {
+#define TILER_PAIR_CASE(t)                         \
+  case t:                                          \
+    x0 = acc[(t) >> 3][((t) >> 1) & 3][((t)&1) * 2]; \
+    x1 = acc[(t) >> 3][((t) >> 1) & 3][((t)&1) * 2 + 1]; \
+    return;
+    TILER_PAIR_CASE(0) TILER_PAIR_CASE(1) TILER_PAIR_CASE(2) TILER_PAIR_CASE(3)
+    TILER_PAIR_CASE(4) TILER_PAIR_CASE(5) TILER_PAIR_CASE(6) TILER_PAIR_CASE(7)
+    TILER_PAIR_CASE(8) TILER_PAIR_CASE(9) TILER_PAIR_CASE(10) TILER_PAIR_CASE(11)
+    TILER_PAIR_CASE(12) TILER_PAIR_CASE(13) TILER_PAIR_CASE(14) TILER_PAIR_CASE(15)
+    TILER_PAIR_CASE(16) TILER_PAIR_CASE(17) TILER_PAIR_CASE(18) TILER_PAIR_CASE(19)
+    TILER_PAIR_CASE(20) TILER_PAIR_CASE(21) TILER_PAIR_CASE(22) TILER_PAIR_CASE(23)
+    TILER_PAIR_CASE(24) TILER_PAIR_CASE(25) TILER_PAIR_CASE(26) TILER_PAIR_CASE(27)
+    TILER_PAIR_CASE(28) TILER_PAIR_CASE(29) TILER_PAIR_CASE(30)
+#undef TILER_PAIR_CASE
+    default:
+      x0 = acc[3][3][2];
+      x1 = acc[3][3][3];
+  }
+}
+
 // s_waitcnt immediates (gfx9 layout: vmcnt [3:0] and [15:14], expcnt [6:4],
 // lgkmcnt [11:8]); a field at its maximum does not wait.
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
@@ -411,6 +443,9 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmLgkm0);
   __syncthreads();  // every wave is done with the operand stages
+  // Keep the epilogue out of the last tile's schedule: interleaved, its
+  // temporaries meet the fragments and the accumulators and spill.
+  __builtin_amdgcn_sched_barrier(0);
 
   // Epilogue: wave-private 64 x 64 bf16 region (8 KiB) with 128-B rows, chunk
   // q of row r at q ^ (r & 7).  Lanes 2c and 2c+1 hold adjacent columns of
@@ -418,6 +453,13 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
   uint16_t* cst = smem + wave * (64u * 64u);
   const bool odd = lane & 1u;
   const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+  // SiLU in two passes, so the hot code stays one straight line: pass 1
+  // stores every element's fast value and marks in the wave-uniform `redo`
+  // (bit p = 8i + 2j + r/2) the row pairs where some lane's value only
+  // silu_f32 narrows right; pass 2 takes the marked pairs one at a time
+  // through one shared copy of the reference code and overwrites those
+  // lanes' bf16 (LDS writes of one wave land in issue order).
+  uint32_t redo = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -426,17 +468,38 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
       for (int r = 0; r < 4; r += 2) {
         float v0 = acc[i][j][r], v1 = acc[i][j][r + 1];
         if (kSilu) {
-          v0 = tiler::silu_for_bf16(v0);
-          v1 = tiler::silu_for_bf16(v1);
+          bool x0, x1;
+          v0 = tiler::silu_bf16_candidate(v0, x0);
+          v1 = tiler::silu_bf16_candidate(v1, x1);
+          redo |= (uint32_t)(__builtin_amdgcn_ballot_w64(x0 || x1) != 0) << (i * 8 + j * 2 + r / 2);
         }
         const uint32_t row = i * 16u + grp * 4u + r + (odd ? 1u : 0u);
         const uint32_t col = j * 16u + ((lane & 15u) & ~1u);
         const uint32_t q = (col >> 3) ^ (row & 7u);
         *reinterpret_cast<uint32_t*>(cst + row * 64u + q * 8u + (col & 7u)) = pack_row_pair(v0, v1, sel);
       }
+  if (kSilu) {
+    while (redo != 0) {
+      const uint32_t p = (uint32_t)__builtin_ctz(redo);
+      redo &= redo - 1u;
+      float xs[2];
+      accumulator_pair(acc, p, xs[0], xs[1]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        bool exact;
+        (void)tiler::silu_bf16_candidate(xs[h], exact);
+        if (exact) {
+          const uint32_t row = (p >> 3) * 16u + grp * 4u + (p & 1u) * 2u + (uint32_t)h;
+          const uint32_t col = ((p >> 1) & 3u) * 16u + (lane & 15u);
+          cst[row * 64u + (((col >> 3) ^ (row & 7u)) * 8u) + (col & 7u)] = narrow_one(tiler::silu_f32(xs[h]));
+        }
+      }
+    }
+  }
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   __builtin_amdgcn_wave_barrier();
-  const uint32_t grow0 = m0 + wm * 64u, gcol0 = n0 + wn * 64u;
+  // from the scalar wave index: a vector copy would be live (or spilled) across the whole loop
+  const uint32_t grow0 = m0 + (wave_s / kGrid) * 64u, gcol0 = n0 + (wave_s % kGrid) * 64u;
 #pragma unroll 4
   for (int it = 0; it < 64 * 8 / 64; ++it) {
     const uint32_t qid = it * 64u + lane;
