@@ -468,7 +468,51 @@ class Convert(Workload):
                 "sample": f"{done} elements of the oracle's narrowing in {el:.1f} s, single thread"}
 
 
-WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, SoftmaxDecode, Gather, Contract, Convert)}
+class Expression(Workload):
+    """A pointwise f32 expression DAG (ScalarProgram::PointwiseF32) over three
+    inputs of f32[2^26]: y = (x0 * x1 + x2) * 0.5, one rounding per node, one
+    fused launch.  Not a BASELINE config, measured as a family of its own."""
+    name = "expression"
+    kernel = "tiler_expr_f32_r16_i3"
+    n = 1 << 26
+    sets = 2  # 2 x 1 GiB touched per sweep
+    nodes = [(0, 0, 0), (0, 1, 0), (0, 2, 0), (3, 0, 1), (2, 3, 2), (1, 0x3F000000, 0), (3, 4, 5)]
+
+    def config(self):
+        return {"workload": "f32 expression y = (x0 * x1 + x2) * 0.5 over 3 x f32[2^26] ~N(0,1)",
+                "nodes": len(self.nodes), "inputs": 3, "buffer_sets": self.sets}
+
+    def work(self):  # algorithmic bytes per launch: three inputs read, one output written
+        return self.n * 4 * 4
+
+    def setup(self):
+        from tiler_amd import _lib as L
+        self.L = L
+        rng = np.random.default_rng(8)
+        self.sets_ = []
+        for _ in range(self.sets):
+            ins = [self._keep(self.ctx.to_device(rng.standard_normal(self.n, dtype=np.float32))) for _ in range(3)]
+            self.sets_.append((ins, self._keep(self.ctx.alloc(self.n * 4))))
+        return self.sets
+
+    def launch(self, i):
+        ins, y = self.sets_[i % self.sets]
+        self.ctx.expression(self.L.F32, self.nodes, ins, self.n, y)
+
+    def cpu_baseline(self, budget_s):
+        import oracle
+        rng = np.random.default_rng(8)
+        xs = [rng.standard_normal(1 << 20, dtype=np.float32) for _ in range(3)]
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s:
+            oracle.expression_f32(self.nodes, xs)
+            done += xs[0].size
+        el = time.perf_counter() - t0
+        return {"value": done * 16 / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done} elements of the oracle's expression evaluator in {el:.1f} s, single thread"}
+
+
+WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, SoftmaxDecode, Gather, Contract, Convert, Expression)}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_all_families.md")

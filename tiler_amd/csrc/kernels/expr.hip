@@ -99,8 +99,19 @@ __device__ __forceinline__ void expr_r16_body(ExprInputs in, void* __restrict__ 
                                               uint32_t result, uint64_t chunks, uint32_t in_mode,
                                               uint32_t out_mode) {
   constexpr int E = kVec ? (kBf16 ? 8 : 4) : 1;
+  constexpr bool kPipelined = kVec && NIN > 0;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t q = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; q < chunks; q += stride) {
+  // Pipelined form: the next chunk's NIN input loads are issued before this
+  // chunk's program runs, so a wave keeps its loads in flight while it
+  // interprets.
+  u32x4 next[NIN > 0 ? NIN : 1];
+  const uint64_t q0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (kPipelined && q0 < chunks) {
+#pragma unroll
+    for (int k = 0; k < NIN; ++k)
+      next[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(in.p[k]) + q0);
+  }
+  for (uint64_t q = q0; q < chunks; q += stride) {
     // One 16-register file per vector element, as vector values indexed by
     // the (uniform) register number: no stack array, so the files live in
     // VGPRs and a read or write is one indexed register move.
@@ -125,8 +136,12 @@ __device__ __forceinline__ void expr_r16_body(ExprInputs in, void* __restrict__ 
       if (kVec) {
         u32x4 raw[NIN > 0 ? NIN : 1];
 #pragma unroll
-        for (int k = 0; k < NIN; ++k)
-          raw[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(in.p[k]) + q);
+        for (int k = 0; k < NIN; ++k) raw[k] = next[k];
+        if (q + stride < chunks) {
+#pragma unroll
+          for (int k = 0; k < NIN; ++k)
+            next[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(in.p[k]) + q + stride);
+        }
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
           float v[E];
