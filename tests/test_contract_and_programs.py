@@ -97,6 +97,11 @@ def test_flushing_modes_where_implemented_or_irrelevant():
                  result_subnormals=L.SUBNORMALS_FLUSH_POSITIVE)
     seg = bytes(rz.raw.entries[0].kernargs[:rz.raw.entries[0].kernarg_bytes])
     assert struct.unpack_from("<II", seg, len(seg) - 8) == (2, 3)  # the modes reach the kernel
+    # the vector form reads the modes only in its _r16f_ copy; the preserve copy compiles them out
+    assert rz.symbols == ["tiler_expr_f32_r16f_i2"]
+    assert realize(L.PROGRAM_EXPRESSION, (64,), nodes=nodes).symbols == ["tiler_expr_f32_r16_i2"]
+    assert realize(L.PROGRAM_EXPRESSION, (64,), nodes=nodes, flags=0, input_subnormals=L.SUBNORMALS_FLUSH_SIGN
+                   ).symbols == ["tiler_expr_f32_r16s_i2"]
     # byte moves perform no arithmetic
     assert realize(L.PROGRAM_GATHER, (1, 10, 4, 3), variant=4, input_subnormals=2).raw.entry_count == 2
     assert realize(L.PROGRAM_BROADCAST, (8, 4), variant=4, rank=2, strides=(0, 1), grouping=(4,),

@@ -206,8 +206,10 @@ def test_f32_expression_subnormal_modes(ctx, modes):
     preserve = oracle.expression_f32(nodes, [x0, x1])
     assert not np.array_equal(bits(want), bits(preserve))  # the modes are observable here
     assert np.array_equal(bits(_run_direct(ctx, L.F32, nodes, [x0, x1], modes)), bits(want))
-    got, _ = _run_routed(ctx, L.F32, nodes, [x0, x1], modes)
-    assert np.array_equal(bits(got), bits(want))
+    got, symbols = _run_routed(ctx, L.F32, nodes, [x0, x1], modes)
+    assert symbols == ["tiler_expr_f32_r16f_i2"] and np.array_equal(bits(got), bits(want))
+    got, symbols = _run_routed(ctx, L.F32, nodes, [x0, x1], modes, flags=0)
+    assert symbols == ["tiler_expr_f32_r16s_i2"] and np.array_equal(bits(got), bits(want))
 
 
 def test_expression_forms_agree_on_unaligned_storage(ctx):

@@ -675,7 +675,9 @@ tiler_hip_status plan_expression(const Target& t, uint32_t dtype, uint64_t n, co
     for (uint32_t k = 0; k < prog.inputs; ++k) vec = vec && aligned16(addr[k]);
     const uint32_t nin = prog.inputs <= 4 ? prog.inputs : 0;
     const uint64_t work = vec ? n / per : n;
-    std::snprintf(name, sizeof(name), "tiler_expr_%s_r16%s_i%u", ty, vec ? "" : "s", nin);
+    // the vector f32 form has a copy with the mode code compiled out
+    const char* form = !vec ? "s" : (dtype == TILER_HIP_F32 && c.flushes()) ? "f" : "";
+    std::snprintf(name, sizeof(name), "tiler_expr_%s_r16%s_i%u", ty, form, nin);
     p.add(name, blocks_capped(work, 8192), 1, 256)
         .ptr_table(in_slots, prog.inputs, kMaxExpressionInputs)
         .ptr(y).ptr(code).u32(prog.count).u32(prog.result).u64(work).u32(in_mode).u32(out_mode);

@@ -180,6 +180,11 @@ const EntryRow kEntries[] = {
       {"tiler_expr_" TY "_mem", FAM, 19}
     TILER_EXPR_ROWS("f32", "pointwise-f32-expression"),
     TILER_EXPR_ROWS("bf16", "pointwise-bf16-expression"),
+    {"tiler_expr_f32_r16f_i0", "pointwise-f32-expression", 18},
+    {"tiler_expr_f32_r16f_i1", "pointwise-f32-expression", 18},
+    {"tiler_expr_f32_r16f_i2", "pointwise-f32-expression", 18},
+    {"tiler_expr_f32_r16f_i3", "pointwise-f32-expression", 18},
+    {"tiler_expr_f32_r16f_i4", "pointwise-f32-expression", 18},
 #undef TILER_EXPR_ROWS
     {"tiler_contract_bf16_g128", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_g128", "tensor-contraction-bf16/cooperative+silu", 3},
