@@ -644,6 +644,48 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context *ctx, const uint16_t 
                                          uint16_t *c, uint32_t epilogue,
                                          tiler_hip_stream stream);
 
+/* Contraction over any admitted binary index structure (ADR 0087: the
+ * reference's ContractionIndexStructure, tiler-ir/src/semantic/contraction.rs:
+ * 482-660, evaluated by tiler-reference/src/contraction.rs:346-715).  Each
+ * operand is dense row-major with operand_rank[s] axes, axis a labelled
+ * operand_indices[s][a] (any uint32) and sized operand_dims[s][a]; the result
+ * is dense row-major over output_indices.  Refused (INVALID_ARGUMENT) unless
+ * the five structural rules hold (an index repeats within no tuple, every
+ * output index names an operand axis, every summed index names an axis of
+ * both operands; contraction.rs:804-900), at least one index is summed, the
+ * extents of one index agree, and the summed domain is not empty
+ * (contraction.rs:420-428).  The contracted set is every operand index absent
+ * from the output, ascending by label; its row-major odometer is the
+ * contributor sequence.
+ *   strict (no PERMITS_REASSOCIATION): the reference fold per output --
+ *     seeded at the first product, fl(a*b) and fl(acc + p), no FMA; f32
+ *     bit-exact; bf16 operands widened exactly, the f32 fold, optional SiLU,
+ *     one bf16 narrowing.
+ *   PERMITS_REASSOCIATION, bf16: structures of the form
+ *     left [batch.., m, k] x right [batch.., n, k] or [batch.., k, n] ->
+ *     out [batch.., m, n] (one summed index; batch axes in any order, each in
+ *     either operand or both -- the attention score and value contractions)
+ *     run on the MFMA kernels above with batch strides, a right operand
+ *     stored [k, n] first transposed into a workspace; other structures take
+ *     the strict fold. */
+#define TILER_HIP_MAX_CONTRACTION_RANK 8
+typedef struct {
+    uint32_t operand_rank[2];         /* left, right */
+    uint32_t output_rank;
+    uint32_t reserved;                /* 0 */
+    uint32_t operand_indices[2][8];
+    uint32_t output_indices[8];
+    uint64_t operand_dims[2][8];
+} tiler_hip_contraction_structure;
+/* dtype TILER_HIP_F32 (epilogue NONE) or TILER_HIP_BF16; permissions
+ * TILER_HIP_PERMITS_*.  The workspace a [k, n] right operand needs is
+ * allocated on the stream (refused under graph capture); the strict form's
+ * geometry is uploaded once per distinct structure and kept by the context. */
+tiler_hip_status tiler_hip_contract(tiler_hip_context *ctx, uint32_t dtype,
+                                    const tiler_hip_contraction_structure *structure,
+                                    uint32_t epilogue, uint32_t permissions, const void *left,
+                                    const void *right, void *out, tiler_hip_stream stream);
+
 /* ------------------------------------------------------------------------
  * Realization recognizer: one scheduled region -> the dispatches that realize
  * it on this library's entry points.  It takes the role of tiler-metal's
@@ -755,6 +797,9 @@ typedef struct {
     uint32_t node_count;
     uint32_t root;
     const tiler_hip_expression_node *nodes;
+    /* PROGRAM_CONTRACTION: NULL is td,od->to over extents {m, n, k}; else the
+     * index structure (read during the call only), extents unused. */
+    const tiler_hip_contraction_structure *structure;
 } tiler_hip_region;
 
 /* Storage slot roles.  Slot order per program:
@@ -765,7 +810,8 @@ typedef struct {
  *   serial sum  x, out, [partials: scratch]
  *   rms_norm    x, w, y
  *   softmax     x, y
- *   contraction a [m, k], b [n, k], c [m, n]
+ *   contraction a [m, k], b [n, k], c [m, n]; with a structure: left, right,
+ *               out, [the transposed right operand: scratch]
  *   gather      source, index, out, record (scratch: u64, all ones unless an index was
  *               out of range; then the lowest such position).  The program arms the
  *               record itself; validate host indices first (tiler_hip_validate_gather_index).

@@ -86,6 +86,8 @@ _SIGS = {
     "tiler_oracle_rms_norm_f32": (_I32, [_P, _P, _U64, _U64, _U64, _U32, _P, _I32, _I32]),
     "tiler_oracle_gather": (_I32, [_P, _U64, _U64, _U64, _U32, _P, _U64, _I32, _P, _P, _P]),
     "tiler_oracle_contract_strict_f32": (_I32, [_P, _P, _U64, _U64, _U64, _P, _U64, _U64, _U32]),
+    "tiler_oracle_contract_general": (_I32, [_U32, _I32, _U32, _P, _P, _U32, _P, _P, _U32, _P, _P, _P, _P,
+                                             _U32]),
     "tiler_oracle_row_grouped_sum_f32": (_I32, [_P, _U64, _U64, _U32, _U32, _P]),
     "tiler_oracle_grid_tree_sum_f32": (_I32, [_P, _U64, _U32, _P]),
     "tiler_oracle_rms_norm_grouped_f32": (_I32, [_P, _P, _U64, _U64, _U32, _I32, _U32, _U32, _P]),
@@ -282,6 +284,32 @@ def contract_strict_f32(a, b, m, n, k, row_begin=0, row_end=None, threads=None) 
     _check(lib().tiler_oracle_contract_strict_f32(_ptr(a), _ptr(b), m, n, k, _ptr(c), row_begin,
                                                   row_end, threads), "contract_strict_f32")
     return c.reshape(m, n)
+
+
+def contract_general(left, left_idx, right, right_idx, out_idx, silu=False, threads=None) -> np.ndarray:
+    """A binary contraction by index labels (ADR 0087), e.g. attention scores
+    ``contract_general(q, "bhqd", k, "bkd", "bhqk")``: labels are strings of
+    single characters or sequences of ints.  f32 operands give an f32 result;
+    uint16 (bf16 bit patterns) operands give bf16 bits, optionally through
+    the reference SiLU.  Shapes come from the operand arrays."""
+    def labels(x):
+        return np.array([ord(c) for c in x] if isinstance(x, str) else list(x), np.uint32)
+    bf16 = left.dtype == np.uint16
+    left = np.ascontiguousarray(left, np.uint16 if bf16 else np.float32)
+    right = np.ascontiguousarray(right, np.uint16 if bf16 else np.float32)
+    li, ri, oi = labels(left_idx), labels(right_idx), labels(out_idx)
+    ld = np.array(left.shape, np.uint64)
+    rd = np.array(right.shape, np.uint64)
+    extent = {}
+    for lab, d in list(zip(li, left.shape)) + list(zip(ri, right.shape)):
+        extent.setdefault(int(lab), d)
+    shape = tuple(extent.get(int(lab), 0) for lab in oi)
+    out = np.zeros(shape, np.uint16 if bf16 else np.float32)
+    threads = threads or max(1, min(os.cpu_count() or 1, 16))
+    _check(lib().tiler_oracle_contract_general(1 if bf16 else 0, 1 if silu else 0, li.size, _ptr(li), _ptr(ld),
+                                               ri.size, _ptr(ri), _ptr(rd), oi.size, _ptr(oi), _ptr(left),
+                                               _ptr(right), _ptr(out), threads), "contract_general")
+    return out
 
 
 def row_grouped_sum(contributors, rows, extent, vec, waves) -> np.ndarray:

@@ -533,6 +533,179 @@ int32_t tiler_oracle_contract_strict_f32(const float *a, const float *b, uint64_
 }
 
 /* ------------------------------------------------------------------------ */
+/* General contraction (see header). */
+typedef struct {
+    uint32_t dtype;
+    int32_t silu;
+    const void *left, *right;
+    void *out;
+    uint32_t out_rank, con_rank;
+    uint64_t out_dims[8], con_dims[8];
+    uint64_t l_out[8], r_out[8], l_con[8], r_con[8]; /* operand strides per output / contracted axis */
+    uint64_t con_count, begin, end;
+    int32_t status;
+} general_job;
+
+static float general_operand(const general_job *j, int right, uint64_t off) {
+    if (j->dtype == 0) return ((const float *)(right ? j->right : j->left))[off];
+    uint16_t h = ((const uint16_t *)(right ? j->right : j->left))[off];
+    return u2f((uint32_t)h << 16);
+}
+
+static void *general_worker(void *arg) {
+    general_job *j = (general_job *)arg;
+    for (uint64_t o = j->begin; o < j->end; ++o) {
+        /* the output coordinate, row-major (contraction.rs:580-585) */
+        uint64_t lbase = 0, rbase = 0, rem = o;
+        for (int32_t d = (int32_t)j->out_rank - 1; d >= 0; --d) {
+            uint64_t c = rem % j->out_dims[d];
+            rem /= j->out_dims[d];
+            lbase += c * j->l_out[d];
+            rbase += c * j->r_out[d];
+        }
+        uint64_t coord[8] = {0};
+        uint64_t lo = 0, ro = 0;
+        float acc = 0.0f;
+        for (uint64_t step = 0; step < j->con_count; ++step) {
+            float p = canon(general_operand(j, 0, lbase + lo) * general_operand(j, 1, rbase + ro));
+            acc = step == 0 ? p : canon(acc + p); /* contraction.rs:635-652 */
+            /* next contracted coordinate, ascending lexicographic */
+            for (int32_t d = (int32_t)j->con_rank - 1; d >= 0; --d) {
+                lo += j->l_con[d];
+                ro += j->r_con[d];
+                if (++coord[d] < j->con_dims[d]) break;
+                lo -= coord[d] * j->l_con[d];
+                ro -= coord[d] * j->r_con[d];
+                coord[d] = 0;
+            }
+        }
+        acc = canon(acc);
+        if (j->dtype == 0) {
+            ((float *)j->out)[o] = acc;
+        } else {
+            float v = acc;
+            if (j->silu && tiler_oracle_silu_f32(&acc, 1, &v, 0, 0) != TILER_ORACLE_OK) {
+                j->status = TILER_ORACLE_UNDECIDED;
+                return NULL;
+            }
+            ((uint16_t *)j->out)[o] = tiler_oracle_bf16_narrow(v);
+        }
+    }
+    return NULL;
+}
+
+int32_t tiler_oracle_contract_general(uint32_t dtype, int32_t silu, uint32_t left_rank,
+                                      const uint32_t *left_idx, const uint64_t *left_dims,
+                                      uint32_t right_rank, const uint32_t *right_idx,
+                                      const uint64_t *right_dims, uint32_t out_rank,
+                                      const uint32_t *out_idx, const void *left, const void *right,
+                                      void *out, uint32_t threads) {
+    if (dtype > 1 || (dtype == 0 && silu)) return TILER_ORACLE_INVALID_APPLICATION;
+    if (left_rank > 8 || right_rank > 8 || out_rank > 8) return TILER_ORACLE_INVALID_APPLICATION;
+    const uint32_t rank[2] = {left_rank, right_rank};
+    const uint32_t *idx[2] = {left_idx, right_idx};
+    const uint64_t *dims[2] = {left_dims, right_dims};
+    /* rule: an index repeats within no operand, nor within the output */
+    for (int s = 0; s < 2; ++s)
+        for (uint32_t a = 0; a < rank[s]; ++a)
+            for (uint32_t b = a + 1; b < rank[s]; ++b)
+                if (idx[s][a] == idx[s][b]) return TILER_ORACLE_INVALID_APPLICATION;
+    for (uint32_t a = 0; a < out_rank; ++a)
+        for (uint32_t b = a + 1; b < out_rank; ++b)
+            if (out_idx[a] == out_idx[b]) return TILER_ORACLE_INVALID_APPLICATION;
+    /* extent per index, agreeing everywhere (contraction.rs:386-399) */
+    uint32_t labels[16];
+    uint64_t extent[16];
+    uint32_t nl = 0;
+    for (int s = 0; s < 2; ++s)
+        for (uint32_t a = 0; a < rank[s]; ++a) {
+            uint32_t i = 0;
+            while (i < nl && labels[i] != idx[s][a]) ++i;
+            if (i == nl) {
+                labels[nl] = idx[s][a];
+                extent[nl++] = dims[s][a];
+            } else if (extent[i] != dims[s][a]) {
+                return TILER_ORACLE_INVALID_APPLICATION;
+            }
+        }
+    /* every output index names an operand index */
+    general_job base;
+    memset(&base, 0, sizeof base);
+    base.dtype = dtype;
+    base.silu = silu;
+    base.left = left;
+    base.right = right;
+    base.out = out;
+    base.out_rank = out_rank;
+    uint64_t outputs = 1;
+    for (uint32_t d = 0; d < out_rank; ++d) {
+        uint32_t i = 0;
+        while (i < nl && labels[i] != out_idx[d]) ++i;
+        if (i == nl) return TILER_ORACLE_INVALID_APPLICATION;
+        base.out_dims[d] = extent[i];
+        outputs *= extent[i];
+    }
+    /* the contracted set: operand indices absent from the output, ascending;
+     * each must name an axis of both operands */
+    uint32_t con[16];
+    uint32_t nc = 0;
+    for (uint32_t i = 0; i < nl; ++i) {
+        int in_out = 0;
+        for (uint32_t d = 0; d < out_rank; ++d) in_out |= out_idx[d] == labels[i];
+        if (in_out) continue;
+        int in[2] = {0, 0};
+        for (int s = 0; s < 2; ++s)
+            for (uint32_t a = 0; a < rank[s]; ++a) in[s] |= idx[s][a] == labels[i];
+        if (!in[0] || !in[1]) return TILER_ORACLE_INVALID_APPLICATION;
+        uint32_t at = nc++;
+        while (at > 0 && con[at - 1] > labels[i]) {
+            con[at] = con[at - 1];
+            --at;
+        }
+        con[at] = labels[i];
+    }
+    if (nc == 0 || nc > 8) return TILER_ORACLE_INVALID_APPLICATION;
+    base.con_rank = nc;
+    base.con_count = 1;
+    for (uint32_t c = 0; c < nc; ++c) {
+        uint32_t i = 0;
+        while (labels[i] != con[c]) ++i;
+        base.con_dims[c] = extent[i];
+        base.con_count *= extent[i];
+    }
+    /* contraction.rs:420-428: an empty contracted domain has no result */
+    if (base.con_count == 0) return TILER_ORACLE_INVALID_APPLICATION;
+    /* per operand axis: the stride it contributes to an output or contracted axis */
+    for (int s = 0; s < 2; ++s) {
+        uint64_t stride = 1;
+        for (int32_t a = (int32_t)rank[s] - 1; a >= 0; --a) {
+            for (uint32_t d = 0; d < out_rank; ++d)
+                if (out_idx[d] == idx[s][a]) (s ? base.r_out : base.l_out)[d] = stride;
+            for (uint32_t c = 0; c < nc; ++c)
+                if (con[c] == idx[s][a]) (s ? base.r_con : base.l_con)[c] = stride;
+            stride *= dims[s][a];
+        }
+    }
+    if (threads == 0) threads = 1;
+    if (threads > 64) threads = 64;
+    if (threads > outputs) threads = outputs ? (uint32_t)outputs : 1;
+    pthread_t tid[64];
+    general_job jobs[64];
+    for (uint32_t t = 0; t < threads; ++t) {
+        jobs[t] = base;
+        jobs[t].begin = outputs * t / threads;
+        jobs[t].end = outputs * (t + 1) / threads;
+        pthread_create(&tid[t], NULL, general_worker, &jobs[t]);
+    }
+    int32_t st = TILER_ORACLE_OK;
+    for (uint32_t t = 0; t < threads; ++t) {
+        pthread_join(tid[t], NULL);
+        if (jobs[t].status) st = jobs[t].status;
+    }
+    return st;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Declared groupings of the tiler-hip reassociating kernels (see header). */
 
 /* One row under grouping (vec, waves): returns the committed sum. */

@@ -96,6 +96,25 @@ int32_t tiler_oracle_contract_strict_f32(const float *a, const float *b, uint64_
                                          uint64_t k, float *c, uint64_t row_begin,
                                          uint64_t row_end, uint32_t threads);
 
+/* Contraction over a general binary index structure (ADR 0087):
+ * tiler-reference/src/contraction.rs:346-715 (ContractionFold::plan and
+ * evaluate_outputs) under the preserve conformance.  Each operand is dense
+ * row-major with `*_rank` axes labelled by `*_idx` (any uint32 labels) and
+ * sized by `*_dims`; the output is dense row-major over `out_idx`.  The five
+ * structural rules (tiler-ir/src/semantic/contraction.rs:804-900) and extent
+ * agreement are checked; the contracted set is every operand index absent
+ * from the output, ascending by label, and its row-major odometer is the
+ * contributor sequence: seeded at the first product, fl(a*b) and
+ * fl(acc + p) each canonicalized, no FMA.  dtype 0: f32 operands and
+ * result; dtype 1: bf16 operands widened exactly, the same f32 fold, then
+ * (silu != 0) the reference SiLU and one bf16 narrowing. */
+int32_t tiler_oracle_contract_general(uint32_t dtype, int32_t silu, uint32_t left_rank,
+                                      const uint32_t *left_idx, const uint64_t *left_dims,
+                                      uint32_t right_rank, const uint32_t *right_idx,
+                                      const uint64_t *right_dims, uint32_t out_rank,
+                                      const uint32_t *out_idx, const void *left, const void *right,
+                                      void *out, uint32_t threads);
+
 /* ---- Declared groupings of the tiler-hip reassociating kernels ----------
  * These restate the exact addition order each HIP kernel performs, so the
  * device result can be compared bit for bit; they are the analogue of

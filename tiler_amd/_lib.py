@@ -224,6 +224,35 @@ class ExpressionNode(ctypes.Structure):
     _fields_ = [("op", ctypes.c_uint32), ("a", ctypes.c_uint32), ("b", ctypes.c_uint32)]
 
 
+class ContractionStructure(ctypes.Structure):
+    _fields_ = [
+        ("operand_rank", ctypes.c_uint32 * 2),
+        ("output_rank", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+        ("operand_indices", (ctypes.c_uint32 * 8) * 2),
+        ("output_indices", ctypes.c_uint32 * 8),
+        ("operand_dims", (ctypes.c_uint64 * 8) * 2),
+    ]
+
+
+def contraction_structure(left_idx, left_dims, right_idx, right_dims, out_idx) -> ContractionStructure:
+    """Labels are strings of single characters or sequences of ints."""
+    def labels(x):
+        return [ord(c) for c in x] if isinstance(x, str) else [int(v) for v in x]
+    s = ContractionStructure()
+    for side, (idx, dims) in enumerate(((left_idx, left_dims), (right_idx, right_dims))):
+        lab = labels(idx)
+        s.operand_rank[side] = len(lab)
+        for a, (v, d) in enumerate(zip(lab, dims)):
+            s.operand_indices[side][a] = v
+            s.operand_dims[side][a] = int(d)
+    out = labels(out_idx)
+    s.output_rank = len(out)
+    for a, v in enumerate(out):
+        s.output_indices[a] = v
+    return s
+
+
 class Region(ctypes.Structure):
     _fields_ = [
         ("program", ctypes.c_uint32),
@@ -242,6 +271,7 @@ class Region(ctypes.Structure):
         ("node_count", ctypes.c_uint32),
         ("root", ctypes.c_uint32),
         ("nodes", ctypes.POINTER(ExpressionNode)),
+        ("structure", ctypes.POINTER(ContractionStructure)),
     ]
 
 
@@ -386,6 +416,7 @@ SIGNATURES = {
                                              ctypes.POINTER(ctypes.c_int64)]),
     "tiler_hip_contract_strict_f32": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _P]),
     "tiler_hip_contract_bf16": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _U32, _P]),
+    "tiler_hip_contract": (_S, [_CTX, _U32, ctypes.POINTER(ContractionStructure), _U32, _U32, _P, _P, _P, _P]),
     "tiler_hip_realize": (_S, [_CTX, ctypes.POINTER(Region), ctypes.POINTER(Realization),
                                ctypes.c_char_p, _U64]),
     "tiler_hip_expression": (_S, [_CTX, _U32, ctypes.POINTER(ExpressionNode), _U32, _U32,

@@ -16,6 +16,7 @@
 //   (v_mfma_f32_32x32x16_bf16, register-staged) for any n and k: out-of-range
 //   operand elements are zero-filled, out-of-range outputs are not stored.
 #include "common.h"
+#include "contract_geometry.h"
 
 using tiler::canon;
 
@@ -125,11 +126,11 @@ template <bool kFullK, bool kSilu>
 __device__ __forceinline__ void contract_bf16_body(const uint16_t* __restrict__ a,
                                                    const uint16_t* __restrict__ b, uint32_t m,
                                                    uint32_t n, uint32_t k,
-                                                   uint16_t* __restrict__ c) {
+                                                   uint16_t* __restrict__ c, uint32_t m_tile) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBM * kLdsRow];  // [buf][A|B]
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t wm = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;  // wave's 64x64 sub-tile
-  const uint32_t m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const uint32_t m0 = m_tile * kBM, n0 = blockIdx.x * kBN;
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -611,9 +612,78 @@ TILER_CONTRACT_SKINNY(4)
   extern "C" __global__ void __launch_bounds__(256)                                            \
       NAME(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m,         \
            uint32_t n, uint32_t k, uint16_t* __restrict__ c) {                                  \
-    contract_bf16_body<FULLK, SILU>(a, b, m, n, k, c);                                          \
+    contract_bf16_body<FULLK, SILU>(a, b, m, n, k, c, blockIdx.y);                              \
   }
 TILER_CONTRACT_BF16(tiler_contract_bf16_g128, true, false)
 TILER_CONTRACT_BF16(tiler_contract_bf16_silu_g128, true, true)
 TILER_CONTRACT_BF16(tiler_contract_bf16_g128_k, false, false)
 TILER_CONTRACT_BF16(tiler_contract_bf16_silu_g128_k, false, true)
+
+// ---------------------------------------------------------------------------
+// Batched forms (*_b): the kernels above over a batch of independent
+// [m, k] x [n, k] -> [m, n] problems, each operand moved by the batch
+// coordinate's strides (a stride of 0 shares an operand across that axis:
+// one K for every head).  Batch b is blockIdx.y (staged, skinny) or
+// blockIdx.y / m_tiles (g128, whose m tile is blockIdx.y % m_tiles).  The
+// planner checks every moved base keeps the alignment the form assumes.
+namespace {
+
+__device__ __forceinline__ void batch_offsets(const tiler_geom::BatchGeometry& g, uint32_t batch, uint64_t& oa,
+                                              uint64_t& ob, uint64_t& oc) {
+  oa = ob = oc = 0;
+  uint64_t rem = batch;
+#pragma unroll
+  for (int d = tiler_geom::kBatchAxes - 1; d >= 0; --d)
+    if ((uint32_t)d < g.rank) {
+      const uint64_t coord = rem % g.dims[d];
+      rem /= g.dims[d];
+      oa += coord * g.a_stride[d];
+      ob += coord * g.b_stride[d];
+      oc += coord * g.c_stride[d];
+    }
+}
+
+}  // namespace
+
+#define TILER_CONTRACT_BATCHED_STAGED(TILE, WAVES, SILU, NAME)                                      \
+  extern "C" __global__ void __launch_bounds__(64 * WAVES)                                          \
+      NAME(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m, uint32_t n,  \
+           uint32_t k, uint16_t* __restrict__ c, tiler_geom::BatchGeometry g) {                    \
+    uint64_t oa, ob, oc;                                                                            \
+    batch_offsets(g, blockIdx.y, oa, ob, oc);                                                       \
+    contract_bf16_staged_body<TILE, SILU>(a + oa, b + ob, m, n, k, c + oc);                         \
+  }
+TILER_CONTRACT_BATCHED_STAGED(256, 16, false, tiler_contract_bf16_t256_b)
+TILER_CONTRACT_BATCHED_STAGED(256, 16, true, tiler_contract_bf16_silu_t256_b)
+TILER_CONTRACT_BATCHED_STAGED(128, 4, false, tiler_contract_bf16_t128_b)
+TILER_CONTRACT_BATCHED_STAGED(128, 4, true, tiler_contract_bf16_silu_t128_b)
+
+#define TILER_CONTRACT_BATCHED_SKINNY(MB, SILU, NAME)                                               \
+  extern "C" __global__ void __launch_bounds__(1024)                                                \
+      NAME(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m, uint32_t n,  \
+           uint32_t k, uint16_t* __restrict__ c, tiler_geom::BatchGeometry g) {                    \
+    uint64_t oa, ob, oc;                                                                            \
+    batch_offsets(g, blockIdx.y, oa, ob, oc);                                                       \
+    contract_bf16_skinny_body<MB, SILU>(a + oa, b + ob, m, n, k, c + oc);                           \
+  }
+TILER_CONTRACT_BATCHED_SKINNY(1, false, tiler_contract_bf16_skinny1_b)
+TILER_CONTRACT_BATCHED_SKINNY(2, false, tiler_contract_bf16_skinny2_b)
+TILER_CONTRACT_BATCHED_SKINNY(3, false, tiler_contract_bf16_skinny3_b)
+TILER_CONTRACT_BATCHED_SKINNY(4, false, tiler_contract_bf16_skinny4_b)
+TILER_CONTRACT_BATCHED_SKINNY(1, true, tiler_contract_bf16_silu_skinny1_b)
+TILER_CONTRACT_BATCHED_SKINNY(2, true, tiler_contract_bf16_silu_skinny2_b)
+TILER_CONTRACT_BATCHED_SKINNY(3, true, tiler_contract_bf16_silu_skinny3_b)
+TILER_CONTRACT_BATCHED_SKINNY(4, true, tiler_contract_bf16_silu_skinny4_b)
+
+#define TILER_CONTRACT_BATCHED_G128(NAME, FULLK, SILU)                                              \
+  extern "C" __global__ void __launch_bounds__(256)                                                 \
+      NAME(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m, uint32_t n,  \
+           uint32_t k, uint16_t* __restrict__ c, uint32_t m_tiles, tiler_geom::BatchGeometry g) {  \
+    uint64_t oa, ob, oc;                                                                            \
+    batch_offsets(g, blockIdx.y / m_tiles, oa, ob, oc);                                             \
+    contract_bf16_body<FULLK, SILU>(a + oa, b + ob, m, n, k, c + oc, blockIdx.y % m_tiles);         \
+  }
+TILER_CONTRACT_BATCHED_G128(tiler_contract_bf16_g128_b, true, false)
+TILER_CONTRACT_BATCHED_G128(tiler_contract_bf16_silu_g128_b, true, true)
+TILER_CONTRACT_BATCHED_G128(tiler_contract_bf16_g128_k_b, false, false)
+TILER_CONTRACT_BATCHED_G128(tiler_contract_bf16_silu_g128_k_b, false, true)

@@ -11,3 +11,4 @@
 #include "fold.hip"
 #include "convert.hip"
 #include "contract.hip"
+#include "contract_general.hip"

@@ -3,6 +3,8 @@
 // points of include/tiler_hip.h document.
 #include "program.h"
 
+#include "../kernels/contract_geometry.h"
+
 #include <cmath>
 #include <cstdio>
 
@@ -512,6 +514,226 @@ tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uin
                           : (full ? "tiler_contract_bf16_g128" : "tiler_contract_bf16_g128_k");
   p.add(name, (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 256)
       .ptr(a).ptr(b).u32(m32).u32(n32).u32(k32).ptr(c);
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Contraction over a general binary index structure.  Slots: 0 left, 1 right,
+// 2 out; then the strict form's geometry (CONSTANT) or the MFMA form's
+// transposed right operand (scratch).
+namespace {
+
+struct Axis {
+  uint32_t label;
+  uint64_t extent;
+};
+
+// Row-major element stride of the axis labelled `label` in an operand, or 0
+// (and false) when the operand has no such axis.
+bool stride_of(const tiler_hip_contraction_structure& s, int side, uint32_t label, uint64_t& stride) {
+  uint64_t st = 1;
+  for (int32_t a = (int32_t)s.operand_rank[side] - 1; a >= 0; --a) {
+    if (s.operand_indices[side][a] == label) {
+      stride = st;
+      return true;
+    }
+    st = mul_sat(st, s.operand_dims[side][a]);
+  }
+  stride = 0;
+  return false;
+}
+
+}  // namespace
+
+tiler_hip_status plan_contract_general(const Target& t, uint32_t dtype, const tiler_hip_contraction_structure& s,
+                                       uint32_t epilogue, bool strict, const uintptr_t* addr, Program& p) {
+  using tiler_geom::kAxes;
+  if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16) return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "contraction dtype");
+  if (epilogue > TILER_HIP_EPILOGUE_SILU) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "epilogue");
+  if (dtype == TILER_HIP_F32 && epilogue != TILER_HIP_EPILOGUE_NONE)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the strict f32 contraction has no epilogue");
+  if (s.reserved != 0) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "reserved structure field");
+  if (s.operand_rank[0] > kAxes || s.operand_rank[1] > kAxes || s.output_rank > kAxes)
+    return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "more than 8 indices in one tuple");
+  const uint64_t eb = dtype == TILER_HIP_BF16 ? 2 : 4;
+  // The five structural rules (tiler-ir/src/semantic/contraction.rs:804-900)
+  // and one extent per index (tiler-reference/src/contraction.rs:386-399).
+  for (int side = 0; side < 2; ++side)
+    for (uint32_t a = 0; a < s.operand_rank[side]; ++a)
+      for (uint32_t b = a + 1; b < s.operand_rank[side]; ++b)
+        if (s.operand_indices[side][a] == s.operand_indices[side][b])
+          return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "an index repeated within an operand");
+  for (uint32_t a = 0; a < s.output_rank; ++a)
+    for (uint32_t b = a + 1; b < s.output_rank; ++b)
+      if (s.output_indices[a] == s.output_indices[b])
+        return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "a duplicate output index");
+  Axis seen[2 * kAxes];
+  uint32_t nseen = 0;
+  for (int side = 0; side < 2; ++side)
+    for (uint32_t a = 0; a < s.operand_rank[side]; ++a) {
+      uint32_t i = 0;
+      while (i < nseen && seen[i].label != s.operand_indices[side][a]) ++i;
+      if (i == nseen) {
+        seen[nseen++] = {s.operand_indices[side][a], s.operand_dims[side][a]};
+      } else if (seen[i].extent != s.operand_dims[side][a]) {
+        return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "one index with two extents");
+      }
+    }
+  auto extent_of = [&](uint32_t label, uint64_t& e) {
+    for (uint32_t i = 0; i < nseen; ++i)
+      if (seen[i].label == label) {
+        e = seen[i].extent;
+        return true;
+      }
+    return false;
+  };
+  uint64_t out_dims[kAxes] = {};
+  uint64_t outputs = 1;
+  for (uint32_t d = 0; d < s.output_rank; ++d) {
+    if (!extent_of(s.output_indices[d], out_dims[d]))
+      return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "an output index in no operand");
+    outputs = mul_sat(outputs, out_dims[d]);
+  }
+  uint32_t con[2 * kAxes];
+  uint32_t ncon = 0;
+  for (uint32_t i = 0; i < nseen; ++i) {
+    bool in_out = false;
+    for (uint32_t d = 0; d < s.output_rank; ++d) in_out |= s.output_indices[d] == seen[i].label;
+    if (in_out) continue;
+    uint64_t unused;
+    if (!stride_of(s, 0, seen[i].label, unused) || !stride_of(s, 1, seen[i].label, unused))
+      return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "a summed index in one operand");
+    uint32_t at = ncon++;
+    while (at > 0 && con[at - 1] > seen[i].label) {
+      con[at] = con[at - 1];
+      --at;
+    }
+    con[at] = seen[i].label;
+  }
+  if (ncon == 0) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "no summed index (an outer product)");
+  uint64_t left_elems = 1, right_elems = 1;
+  for (uint32_t a = 0; a < s.operand_rank[0]; ++a) left_elems = mul_sat(left_elems, s.operand_dims[0][a]);
+  for (uint32_t a = 0; a < s.operand_rank[1]; ++a) right_elems = mul_sat(right_elems, s.operand_dims[1][a]);
+  const uint32_t l = p.slot(mul_sat(left_elems, eb), kSlotInput);
+  const uint32_t r = p.slot(mul_sat(right_elems, eb), kSlotInput);
+  const uint32_t o = p.slot(mul_sat(outputs, eb), kSlotOutput);
+  uint64_t con_dims[kAxes] = {};
+  uint64_t contracted = 1;
+  for (uint32_t c = 0; c < ncon; ++c) {
+    extent_of(con[c], con_dims[c]);
+    contracted = mul_sat(contracted, con_dims[c]);
+  }
+  // contraction.rs:420-428: an empty contracted domain has no unseeded result.
+  if (contracted == 0) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty contracted domain");
+  if (left_elems == UINT64_MAX || right_elems == UINT64_MAX || outputs == UINT64_MAX)
+    return p.refuse(TILER_HIP_REFUSE_CAPACITY, "operand or result extents overflow");
+  if (outputs == 0) return TILER_HIP_OK;
+  const bool silu = epilogue == TILER_HIP_EPILOGUE_SILU;
+
+  // MFMA: one summed index k, out [batch.., m, n], left [.., m, k],
+  // right [.., n, k] or [.., k, n].
+  if (!strict && dtype == TILER_HIP_BF16 && ncon == 1 && s.output_rank >= 2) {
+    const uint32_t ki = con[0], mi = s.output_indices[s.output_rank - 2], ni = s.output_indices[s.output_rank - 1];
+    const uint32_t lr = s.operand_rank[0], rr = s.operand_rank[1];
+    uint64_t st;
+    const bool left_ok = lr >= 2 && s.operand_indices[0][lr - 1] == ki && s.operand_indices[0][lr - 2] == mi &&
+                         !stride_of(s, 1, mi, st);
+    const bool right_nk = rr >= 2 && s.operand_indices[1][rr - 1] == ki && s.operand_indices[1][rr - 2] == ni;
+    const bool right_kn = rr >= 2 && s.operand_indices[1][rr - 1] == ni && s.operand_indices[1][rr - 2] == ki;
+    const bool ni_ok = !stride_of(s, 0, ni, st);
+    const uint32_t nbatch = s.output_rank - 2;
+    uint64_t m = 0, n = 0, k = con_dims[0];
+    extent_of(mi, m);
+    extent_of(ni, n);
+    uint64_t batches = 1;
+    for (uint32_t d = 0; d < nbatch; ++d) batches = mul_sat(batches, out_dims[d]);
+    if (left_ok && ni_ok && (right_nk || right_kn) && nbatch <= (uint32_t)tiler_geom::kBatchAxes &&
+        batches <= 65535 && m <= 0x7fffffffull && n <= 0x7fffffffull && k <= 0x7fffffffull) {
+      tiler_geom::BatchGeometry g{};
+      g.rank = nbatch;
+      // The right operand as the kernels read it: its own layout, or (stored
+      // [.., k, n]) transposed into scratch as [.., n, k], dense.
+      uint64_t rbatch = 1;
+      for (uint32_t a = 0; a + 2 < rr; ++a) rbatch = mul_sat(rbatch, s.operand_dims[1][a]);
+      bool strides8 = true;
+      uint64_t ostride = mul_sat(m, n);
+      for (int32_t d = (int32_t)nbatch - 1; d >= 0; --d) {
+        g.dims[d] = out_dims[d];
+        g.c_stride[d] = ostride;
+        ostride = mul_sat(ostride, out_dims[d]);
+        stride_of(s, 0, s.output_indices[d], g.a_stride[d]);
+        stride_of(s, 1, s.output_indices[d], g.b_stride[d]);  // the transposed layout keeps batch strides
+        strides8 = strides8 && g.a_stride[d] % 8 == 0 && g.b_stride[d] % 8 == 0 && g.c_stride[d] % 8 == 0;
+      }
+      uint32_t right_slot = r;
+      if (right_kn) {
+        if (k > 0xffffffffull || n > 0xffffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "transpose extents");
+        right_slot = p.slot(mul_sat(right_elems, 2), kSlotScratch);
+        const uint64_t row_tiles = (k + 63) / 64, work = mul_sat(rbatch, row_tiles);
+        p.add("tiler_transpose_bf16", (uint32_t)((n + 63) / 64), (uint32_t)(work < 65535 ? work : 65535), 256)
+            .ptr(r).ptr(right_slot).u64(rbatch).u32((uint32_t)k).u32((uint32_t)n);
+      }
+      const uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
+      const bool ab_al = aligned16(addr[l]) && (right_kn || aligned16(addr[r])) && strides8;
+      char name[48];
+      if (m <= 64 && k % 8 == 0 && ab_al) {
+        std::snprintf(name, sizeof(name), "tiler_contract_bf16_%sskinny%u_b", silu ? "silu_" : "", (uint32_t)((m + 15) / 16));
+        p.add(name, (uint32_t)((n + 15) / 16), (uint32_t)batches, 1024)
+            .ptr(l).ptr(right_slot).u32(m32).u32(n32).u32(k32).ptr(o).blob(&g, sizeof g, 8);
+        return TILER_HIP_OK;
+      }
+      if (n % 8 == 0 && k % 8 == 0 && k * 512ull < (1ull << 31) && ab_al && aligned16(addr[o])) {
+        const uint64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
+        const uint64_t t128 = ((m + 127) / 128) * ((n + 127) / 128);
+        // 256-tiles only where a problem spans them (a head dimension of 128
+        // would leave half of each idle) and they fill every CU
+        const bool big = m >= 256 && n >= 256 && mul_sat(t256, batches) >= t.compute_units;
+        const uint64_t tiles = big ? t256 : t128;
+        if (tiles <= 0x7fffffffull) {
+          std::snprintf(name, sizeof(name), "tiler_contract_bf16_%st%u_b", silu ? "silu_" : "", big ? 256u : 128u);
+          p.add(name, (uint32_t)tiles, (uint32_t)batches, big ? 1024 : 256)
+              .ptr(l).ptr(right_slot).u32(m32).u32(n32).u32(k32).ptr(o).blob(&g, sizeof g, 8);
+          return TILER_HIP_OK;
+        }
+      }
+      const uint64_t m_tiles = (m + 127) / 128;
+      if (mul_sat(m_tiles, batches) <= 65535) {
+        const bool full = k % 8 == 0 && ab_al;
+        std::snprintf(name, sizeof(name), "tiler_contract_bf16_%sg128%s_b", silu ? "silu_" : "", full ? "" : "_k");
+        p.add(name, (uint32_t)((n + 127) / 128), (uint32_t)(m_tiles * batches), 256)
+            .ptr(l).ptr(right_slot).u32(m32).u32(n32).u32(k32).ptr(o).u32((uint32_t)m_tiles).blob(&g, sizeof g, 8);
+        return TILER_HIP_OK;
+      }
+      // no MFMA launch fits: the strict fold below (drop the scratch slot)
+      if (right_kn) {
+        p.nslots = 3;
+        p.nlaunches = 0;
+      }
+    }
+  }
+
+  // The strict fold, the geometry in a constant slot.
+  tiler_geom::GeneralGeometry g{};
+  g.out_rank = s.output_rank;
+  g.con_rank = ncon;
+  g.outputs = outputs;
+  for (uint32_t d = 0; d < s.output_rank; ++d) {
+    g.out_dims[d] = out_dims[d];
+    stride_of(s, 0, s.output_indices[d], g.l_out[d]);
+    stride_of(s, 1, s.output_indices[d], g.r_out[d]);
+  }
+  for (uint32_t c = 0; c < ncon; ++c) {
+    g.con_dims[c] = con_dims[c];
+    stride_of(s, 0, con[c], g.l_con[c]);
+    stride_of(s, 1, con[c], g.r_con[c]);
+  }
+  const uint32_t geo = p.slot(sizeof g, TILER_HIP_SLOT_CONSTANT);
+  p.constant_slot = geo;
+  p.constant.assign(reinterpret_cast<const uint8_t*>(&g), reinterpret_cast<const uint8_t*>(&g) + sizeof g);
+  const char* name = dtype == TILER_HIP_F32 ? "tiler_contract_general_f32"
+                     : silu                 ? "tiler_contract_general_bf16_silu"
+                                            : "tiler_contract_general_bf16";
+  p.add(name, blocks_capped(outputs, 65536), 1, 256).ptr(l).ptr(r).ptr(o).ptr(geo);
   return TILER_HIP_OK;
 }
 

@@ -158,6 +158,11 @@ tiler_hip_status plan_gather(Mode mode, uint64_t outer, uint64_t gathered, uint6
 tiler_hip_status plan_convert(Mode mode, uint32_t direction, uint64_t n, const uintptr_t* addr,
                               Program& p);
 tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p);
+// Any admitted binary index structure: the strict fold (f32, or bf16 without
+// reassociation), or under it the batched MFMA forms where the structure is
+// [batch.., m, k] x [batch.., n, k | k, n] -> [batch.., m, n].
+tiler_hip_status plan_contract_general(const Target& t, uint32_t dtype, const tiler_hip_contraction_structure& s,
+                                       uint32_t epilogue, bool strict, const uintptr_t* addr, Program& p);
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
                                     uint32_t epilogue, const uintptr_t* addr, Program& p,
                                     bool strict = false);

@@ -202,6 +202,19 @@ const EntryRow kEntries[] = {
     {"tiler_contract_bf16_silu_t128", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_t256", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_t256", "tensor-contraction-bf16/cooperative+silu", 3},
+    // general index structures: the strict fold (geometry in a constant slot),
+    // the batched MFMA forms and the right-operand transpose ahead of them
+    {"tiler_contract_general_f32", "tensor-contraction-f32/strict-general", 4},
+    {"tiler_contract_general_bf16", "tensor-contraction-bf16/strict-general", 4},
+    {"tiler_contract_general_bf16_silu", "tensor-contraction-bf16/strict-general+silu", 4},
+    {"tiler_transpose_bf16", "tensor-contraction-bf16/transpose", 2},
+#define TILER_BATCHED_ROWS(K)                                                                        \
+  {"tiler_contract_bf16_" K "_b", "tensor-contraction-bf16/cooperative-batched", 3},                  \
+      {"tiler_contract_bf16_silu_" K "_b", "tensor-contraction-bf16/cooperative-batched+silu", 3}
+    TILER_BATCHED_ROWS("t256"), TILER_BATCHED_ROWS("t128"), TILER_BATCHED_ROWS("skinny1"),
+    TILER_BATCHED_ROWS("skinny2"), TILER_BATCHED_ROWS("skinny3"), TILER_BATCHED_ROWS("skinny4"),
+    TILER_BATCHED_ROWS("g128"), TILER_BATCHED_ROWS("g128_k"),
+#undef TILER_BATCHED_ROWS
 };
 constexpr uint32_t kEntryCount = sizeof(kEntries) / sizeof(kEntries[0]);
 
@@ -1348,6 +1361,61 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t*
   return run_program(ctx, p, slots, pick(ctx, stream));
 }
 
+// A program's CONSTANT slot contents (an expression's register program, a
+// contraction's geometry) live on the device once per distinct contents: a
+// synchronous upload on first use; under graph capture uncached contents
+// refuse, so capture after one eager call.
+tiler_hip_status resident_constant(tiler_hip_context* ctx, const tiler_rt::Program& p, hipStream_t s, void** out) {
+  std::string key(p.constant.begin(), p.constant.end());
+  auto it = ctx->expression_programs.find(key);
+  if (it == ctx->expression_programs.end()) {
+    if (capturing(s)) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "constant slot contents not yet resident under graph capture");
+    if (ctx->expression_programs.size() >= 4096) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "too many resident constant slots");
+    void* dev = nullptr;
+    if (hipMalloc(&dev, p.constant.size()) != hipSuccess) return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "constant slot");
+    if (hipMemcpy(dev, p.constant.data(), p.constant.size(), hipMemcpyHostToDevice) != hipSuccess) {
+      hipFree(dev);
+      return fail(ctx, TILER_HIP_FAIL_TRANSFER, "constant slot upload");
+    }
+    it = ctx->expression_programs.emplace(key, dev).first;
+  }
+  *out = it->second;
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_contract(tiler_hip_context* ctx, uint32_t dtype,
+                                    const tiler_hip_contraction_structure* structure, uint32_t epilogue,
+                                    uint32_t permissions, const void* left, const void* right, void* out,
+                                    tiler_hip_stream stream) {
+  if (!ctx || !structure) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (permissions & ~(uint32_t)(TILER_HIP_PERMITS_REASSOCIATION | TILER_HIP_PERMITS_PERMUTATION))
+    return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "unknown permission bits");
+  tiler_rt::Program p;
+  const uintptr_t addr[4] = {(uintptr_t)left, (uintptr_t)right, (uintptr_t)out, 0};
+  tiler_hip_status st = tiler_rt::plan_contract_general(target_of(ctx), dtype, *structure, epilogue,
+                                                        !(permissions & TILER_HIP_PERMITS_REASSOCIATION), addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (!p.nlaunches) return TILER_HIP_OK;
+  if (!left || !right || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  hipStream_t s = pick(ctx, stream);
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(left), const_cast<void*>(right), out};
+  bool own = false;
+  if (p.nslots > 3) {
+    if (p.slot_roles[3] == TILER_HIP_SLOT_CONSTANT) {
+      st = resident_constant(ctx, p, s, &slots[3]);
+      if (st != TILER_HIP_OK) return st;
+    } else {  // the transposed right operand
+      if (capturing(s)) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "transpose workspace allocation under graph capture");
+      if (hipMallocAsync(&slots[3], p.slot_bytes[3], s) != hipSuccess)
+        return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "transpose workspace allocation failed");
+      own = true;
+    }
+  }
+  st = run_program(ctx, p, slots, s);
+  if (own) hipFreeAsync(slots[3], s);
+  return st;
+}
+
 // ---------------------------------------------------------------------------
 tiler_hip_status tiler_hip_expression(tiler_hip_context* ctx, uint32_t dtype,
                                       const tiler_hip_expression_node* nodes, uint32_t node_count,
@@ -1374,26 +1442,11 @@ tiler_hip_status tiler_hip_expression(tiler_hip_context* ctx, uint32_t dtype,
   if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
   if (!p.nlaunches) return TILER_HIP_OK;
   hipStream_t s = pick(ctx, stream);
-  // The register program lives on the device once per distinct program (a
-  // synchronous upload on first use; under graph capture an uncached program
-  // refuses, so capture after one eager call).
-  std::string key(p.constant.begin(), p.constant.end());
-  auto it = ctx->expression_programs.find(key);
-  if (it == ctx->expression_programs.end()) {
-    if (capturing(s)) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "expression program not yet resident under graph capture");
-    if (ctx->expression_programs.size() >= 4096) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "too many resident expression programs");
-    void* dev = nullptr;
-    if (hipMalloc(&dev, p.constant.size()) != hipSuccess) return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "expression program");
-    if (hipMemcpy(dev, p.constant.data(), p.constant.size(), hipMemcpyHostToDevice) != hipSuccess) {
-      hipFree(dev);
-      return fail(ctx, TILER_HIP_FAIL_TRANSFER, "expression program upload");
-    }
-    it = ctx->expression_programs.emplace(key, dev).first;
-  }
   void* slots[tiler_rt::kMaxSlots] = {};
+  st = resident_constant(ctx, p, s, &slots[prog.inputs + 1]);
+  if (st != TILER_HIP_OK) return st;
   for (uint32_t k = 0; k < prog.inputs; ++k) slots[k] = const_cast<void*>(inputs[k]);
   slots[prog.inputs] = y;
-  slots[prog.inputs + 1] = it->second;
   bool own = false;
   if (p.nslots > prog.inputs + 2) {  // the value store
     if (capturing(s)) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "value store allocation under graph capture");
@@ -1636,7 +1689,9 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
                : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "softmax is an f32 family");
       break;
     case TILER_HIP_PROGRAM_CONTRACTION:
-      if (r->dtype == TILER_HIP_F32)
+      if (r->structure)
+        st = tiler_rt::plan_contract_general(t, r->dtype, *r->structure, r->variant, !c.reassociate, addr, p);
+      else if (r->dtype == TILER_HIP_F32)
         st = r->variant == TILER_HIP_EPILOGUE_NONE
                  ? tiler_rt::plan_contract_strict_f32(e[0], e[1], e[2], p)
                  : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the strict f32 contraction has no epilogue");

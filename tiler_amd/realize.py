@@ -64,7 +64,7 @@ def _entry_info(index: int):
 def realize(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_SERIAL, variant: int = 0,
             flags: int = L.REGION_ALIGNED16, rank: int = 0, strides=(), grouping=(), scalars=(),
             permissions: int = 0, input_subnormals: int = 0, result_subnormals: int = 0,
-            nodes=(), root: int | None = None, ctx=None) -> Realization:
+            nodes=(), root: int | None = None, structure=None, ctx=None) -> Realization:
     """Realizes one region.  `ctx` (a runtime.Context) lets the bound device's
     CU count decide tile sizes and groupings; without it the declared
     profile's does (the call is then device-free).
@@ -73,7 +73,8 @@ def realize(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_
     (L.SUBNORMALS_*, 0 preserve) are the plan's numerical contract for this
     region; the defaults are the strict contract.  `nodes` (op, a, b) and
     `root` (default: the last node) give an expression's DAG, or a fold's
-    epilogue."""
+    epilogue.  `structure` (an L.ContractionStructure, see
+    L.contraction_structure) makes a contraction region general."""
     r = L.Region()
     r.program, r.topology, r.dtype, r.variant, r.flags, r.rank = program, topology, dtype, variant, flags, rank
     for i, v in enumerate(extents):
@@ -90,6 +91,8 @@ def realize(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_
         r.node_count = len(nodes)
         r.root = len(nodes) - 1 if root is None else root
         r.nodes = node_array
+    if structure is not None:
+        r.structure = ctypes.pointer(structure)
     out = L.Realization()
     diag = ctypes.create_string_buffer(256)
     st = L.lib().tiler_hip_realize(ctx.handle if ctx is not None else None, ctypes.byref(r), ctypes.byref(out),

@@ -284,6 +284,13 @@ class Context:
         self._check(L.lib().tiler_hip_contract_bf16(self.handle, _ptr(a), _ptr(b), m, n, k,
                                                     _ptr(c), epilogue, stream), "contract_bf16")
 
+    def contract(self, dtype: int, structure, left, right, out, epilogue: int = L.EPILOGUE_NONE,
+                 permissions: int = 0, stream=None):
+        """A contraction over an index structure (L.contraction_structure):
+        the strict fold unless `permissions` grants reassociation (bf16)."""
+        self._check(L.lib().tiler_hip_contract(self.handle, dtype, ctypes.byref(structure), epilogue, permissions,
+                                               _ptr(left), _ptr(right), _ptr(out), stream), "contract")
+
     def expression(self, dtype: int, nodes, inputs, n: int, y, root: int | None = None,
                    input_subnormals: int = 0, result_subnormals: int = 0, stream=None):
         """A pointwise expression DAG: `nodes` are (op, a, b) triples (L.NODE_*),
