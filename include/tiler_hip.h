@@ -84,7 +84,14 @@ typedef struct {
     double mfma_fp8_dense_flops;      /* 5.0e15 */
     double vector_f32_flops;          /* 157.3e12 */
     double vector_f64_flops;          /* 78.6e12 */
-    uint32_t parallel_threads;        /* measured-cost row: concurrent threads */
+    /* The measured cost row (the reference's saturated-parallel-fold-steps,
+     * tiler-compiler/src/target/builder.rs:1369; consumed by
+     * tiler-compiler/src/measured_cost.rs): the fold steps the device retires
+     * at once when saturated, fitted on an MI355X by the work-span sweep of
+     * the sum family's three realizations (tiler_amd.calibrate); where and how
+     * it was measured is in cost_row_source. */
+    uint64_t saturated_parallel_fold_steps;
+    char cost_row_source[192];
 } tiler_hip_target_profile;
 
 tiler_hip_status tiler_hip_profile_declare(tiler_hip_target_profile *out);

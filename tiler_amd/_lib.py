@@ -121,7 +121,8 @@ class TargetProfile(ctypes.Structure):
         ("mfma_fp8_dense_flops", ctypes.c_double),
         ("vector_f32_flops", ctypes.c_double),
         ("vector_f64_flops", ctypes.c_double),
-        ("parallel_threads", ctypes.c_uint32),
+        ("saturated_parallel_fold_steps", ctypes.c_uint64),
+        ("cost_row_source", ctypes.c_char * 192),
     ]
 
 
