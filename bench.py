@@ -341,7 +341,7 @@ class Gather(Workload):
 class Contract(Workload):
     """bf16 4096^3 contraction with fused SiLU."""
     name = "contract"
-    kernel = "tiler_contract_bf16_silu_t256"
+    kernel = "tiler_contract_bf16_silu_t256_kf"
     bound = "mfma"
     unit = "TFLOP/s"
     m = n = k = 4096

@@ -72,7 +72,7 @@ def test_strict_contract_selects_the_serial_row_and_contraction_kernels():
     # the same regions under REASSOCIATE_F32 get the grouped forms
     assert realize(L.PROGRAM_SOFTMAX, (32, 131072), permissions=RE).symbols[-1] == "tiler_softmax_f32_rowsync_a"
     assert realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, variant=L.EPILOGUE_SILU,
-                   permissions=RE).symbols == ["tiler_contract_bf16_silu_t256"]
+                   permissions=RE).symbols == ["tiler_contract_bf16_silu_t256_kf"]
 
 
 @pytest.mark.parametrize("program,extents,kw", [

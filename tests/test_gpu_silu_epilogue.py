@@ -97,13 +97,15 @@ def _values(rng, count):
     return v
 
 
-@pytest.mark.parametrize("m,n,path", [
-    (4096, 4096, "t256"),   # 256 tiles of 256 fill every CU
-    (300, 264, "t128"),
-    (48, 200, "skinny"),
-    (130, 100, "g128"),     # n off the 8-element grid: the general form
+@pytest.mark.parametrize("m,n,pad,path", [
+    (4096, 4096, 0, "t256_kf"),  # 256 tiles of 256 fill every CU; k a multiple of 64
+    (4096, 4096, 8, "t256"),     # the same with a ragged last k tile
+    (300, 264, 0, "t128_kf"),
+    (300, 264, 8, "t128"),
+    (48, 200, 0, "skinny"),
+    (130, 100, 0, "g128"),       # n off the 8-element grid: the general form
 ])
-def test_fused_silu_is_reference_silu_on_each_path(ctx, m, n, path):
+def test_fused_silu_is_reference_silu_on_each_path(ctx, m, n, pad, path):
     rng = np.random.default_rng(m + 7 * n)
     groups = 64 if n >= 64 else n
     vals = _values(rng, m * groups)
@@ -114,7 +116,7 @@ def test_fused_silu_is_reference_silu_on_each_path(ctx, m, n, path):
         hi, lo, lo2, ok = _split3(vals)
     vals = vals.reshape(m, groups)
     k = 3 * groups
-    k_pad = (k + 7) // 8 * 8
+    k_pad = (k + 7) // 8 * 8 + pad  # zero columns past k change no accumulator
     a = np.zeros((m, k_pad), np.uint16)
     a[:, 0:k:3], a[:, 1:k:3], a[:, 2:k:3] = (x.reshape(m, groups) for x in (hi, lo, lo2))
     b = np.zeros((n, k_pad), np.uint16)

@@ -136,13 +136,15 @@ def test_softmax_and_sums():
 
 def test_contraction_paths():
     c5 = realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, permissions=RE, variant=L.EPILOGUE_SILU)
-    assert c5.symbols == ["tiler_contract_bf16_silu_t256"]
+    assert c5.symbols == ["tiler_contract_bf16_silu_t256_kf"]  # k a multiple of 64: no last-tile masking
     assert c5.dispatches[0].grid == (256, 1, 1) and c5.dispatches[0].block == (1024, 1, 1)
     _check_segments(c5)
     assert realize(L.PROGRAM_CONTRACTION, (16, 4096, 4096), dtype=L.BF16, permissions=RE).symbols == \
         ["tiler_contract_bf16_skinny1"]
     small = realize(L.PROGRAM_CONTRACTION, (1000, 2048, 512), dtype=L.BF16, permissions=RE)
-    assert small.symbols == ["tiler_contract_bf16_t128"] and small.dispatches[0].grid == (8 * 16, 1, 1)
+    assert small.symbols == ["tiler_contract_bf16_t128_kf"] and small.dispatches[0].grid == (8 * 16, 1, 1)
+    assert realize(L.PROGRAM_CONTRACTION, (1000, 2048, 520), dtype=L.BF16, permissions=RE).symbols == \
+        ["tiler_contract_bf16_t128"]
     assert realize(L.PROGRAM_CONTRACTION, (300, 130, 64), dtype=L.BF16, permissions=RE).symbols == \
         ["tiler_contract_bf16_g128"]
     assert realize(L.PROGRAM_CONTRACTION, (300, 128, 60), dtype=L.BF16, permissions=RE).symbols == \

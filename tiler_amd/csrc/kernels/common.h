@@ -136,14 +136,33 @@ __device__ __forceinline__ float exp_f32_cr(float s, const double* table = kExp2
 }
 
 // Reference SiLU, tiler-reference/src/silu.rs:511-533: x / fl(1 + exp(-x)),
-// NaN -> NaN, +inf -> +inf, -inf -> NaN.
-__device__ __forceinline__ float silu_f32(float x) {
+// NaN -> NaN, +inf -> +inf, -inf -> NaN.  `table` as exp_f32_cr takes it.
+__device__ __forceinline__ float silu_f32(float x, const double* table = kExp2Table64) {
   if (x != x) return x;
   if (x == __builtin_huge_valf()) return x;
   if (x == -__builtin_huge_valf()) return __uint_as_float(TILER_CANONICAL_F32_NAN);
-  float e = exp_f32_cr(-x);
+  float e = exp_f32_cr(-x, table);
   float divisor = 1.0f + e;
   return x / divisor;
+}
+
+// silu_f32 as one straight line (selects instead of early returns), so that
+// several evaluations interleave: the same arithmetic on every path that is
+// selected, hence the same value for every binary32 x.  The guards' lanes
+// compute a discarded core value (NaN or out-of-range arguments are harmless
+// to the conversions involved).
+__device__ __forceinline__ float silu_f32_straight(float x, const double* table = kExp2Table64) {
+  const float s = -x;
+  int m;
+  // the core on an argument clamped into its domain (every out-of-domain or
+  // NaN lane's value is selected away below)
+  double core = exp_f64_core((double)__builtin_fminf(__builtin_fmaxf(s, -104.0f), 89.0f), m, table);
+  const float ecore = (float)__builtin_ldexp(core, m);
+  float e = s >= 89.0f ? __builtin_huge_valf() : (s <= -104.0f ? 0.0f : ecore);
+  e = s != s ? s : e;
+  const float r = x / (1.0f + e);
+  const float special = x == -__builtin_huge_valf() ? __uint_as_float(TILER_CANONICAL_F32_NAN) : x;
+  return (x != x || x == __builtin_huge_valf() || x == -__builtin_huge_valf()) ? special : r;
 }
 
 // SiLU for a result that is narrowed to bf16 next (the contraction epilogue):
@@ -183,10 +202,20 @@ __device__ __forceinline__ float silu_bf16_candidate(float x, bool& exact) {
   exact = !(x > -80.0f && x < 0x1.0p127f) || near_midpoint;
   return v;
 }
+// The same fast value, with the wave's lanes that must take silu_f32 (the
+// lanes silu_bf16_candidate marks exact) as a ballot of the three raw
+// compares: the mask stays in scalar registers.
+__device__ __forceinline__ float silu_bf16_fast_marked(float x, uint64_t& mask) {
+  const float v = silu_fast_f32(x);
+  const uint32_t key = (__float_as_uint(v) & 0xffffu) - (0x8000u - kSiluGuard);
+  mask = __builtin_amdgcn_ballot_w64(key <= 2u * kSiluGuard) | __builtin_amdgcn_ballot_w64(!(x > -80.0f)) |
+         __builtin_amdgcn_ballot_w64(!(x < 0x1.0p127f));
+  return v;
+}
 __device__ __forceinline__ float silu_for_bf16(float x) {
   bool exact;
   const float v = silu_bf16_candidate(x, exact);
-  return exact ? silu_f32(x) : v;
+  return exact ? silu_f32_straight(x) : v;
 }
 
 }  // namespace tiler

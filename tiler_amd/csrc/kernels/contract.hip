@@ -241,15 +241,17 @@ constexpr int kK = 64;
 // columns 2c and 2c+1.  Each lane narrows its (v0, v1) with
 // v_cvt_pk_bf16_f32, which rounds to nearest even exactly like the ADR 0091
 // narrowing for every non-NaN input (NaNs are made canonical first, since
-// the instruction keeps a NaN's sign and payload); a DPP quad_perm [1,0,3,2]
+// the instruction keeps a NaN's sign and payload; kCanon = false skips that
+// where every NaN lane is rewritten afterwards); a DPP quad_perm [1,0,3,2]
 // swaps the packed words between the two lanes, and v_perm_b32 forms the
 // 32-bit column pair: row r of columns 2c, 2c+1 on the even lane, row r+1 on
 // the odd one.  sel is 0x05040100 on even lanes, 0x03020706 on odd lanes.
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 typedef float f32x2v __attribute__((ext_vector_type(2)));
+template <bool kCanon = true>
 __device__ __forceinline__ uint32_t pack_row_pair(float v0, float v1, uint32_t sel) {
   const float qnan = __uint_as_float(0x7fc00000u);
-  const f32x2v f = {v0 != v0 ? qnan : v0, v1 != v1 ? qnan : v1};
+  const f32x2v f = {kCanon && v0 != v0 ? qnan : v0, kCanon && v1 != v1 ? qnan : v1};
   const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2v));
   const uint32_t q = (uint32_t)__builtin_amdgcn_mov_dpp((int)p, 0xB1, 0xF, 0xF, true);
   return __builtin_amdgcn_perm(q, p, sel);
@@ -311,7 +313,10 @@ __device__ __forceinline__ void issue_operand_tile(__amdgpu_buffer_rsrc_t panel,
         panel, (lds_void*)(lds_tile + (wave_s * LOADS + j) * 8u * kK), 16, voff[j] + k0_bytes, 0, 0, 0);
 }
 
-template <int TILE, bool kSilu>
+// kRaggedK = false: k is a multiple of 64 (the planner's guarantee), so the
+// last tile needs no masking -- and without that code the SiLU form fits its
+// registers without spilling in the last tile.
+template <int TILE, bool kSilu, bool kRaggedK = true>
 __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __restrict__ a,
                                                           const uint16_t* __restrict__ b,
                                                           uint32_t m, uint32_t n, uint32_t k,
@@ -320,10 +325,21 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
   constexpr int kWaves = kGrid * kGrid;
   constexpr int kLoads = TILE / 8 / kWaves;           // 8-row loads per wave per operand tile
   constexpr uint32_t kStageElems = 2u * TILE * kK;    // A tile then B tile, bf16 elements
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * kStageElems];
+  // The operand stages, then (SiLU) the exponent table of the epilogue's
+  // exact path: a divergent lookup in LDS costs an LDS round trip, not a
+  // global one, on the path every wave with a marked element waits for at
+  // the end.  One array on purpose: with a second LDS object the compiler
+  // can no longer tell the fragment reads from the in-flight LDS-DMA refill
+  // and drains the refill (vmcnt(0)) before every tile.
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * kStageElems + (kSilu ? 256 : 0)];
+  double* const silu_table = reinterpret_cast<double*>(smem + 2 * kStageElems);
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t wm = wave / kGrid, wn = wave % kGrid;
+  // wave 0's table entry, loaded ahead of the operand tiles (loads retire in
+  // order, so waiting for it later waits for nothing issued after it)
+  double table_entry = 0.0;
+  if (kSilu && wave_s == 0) table_entry = kExp2Table64[lane];
 
   // XCD-aware tile order: workgroup id -> (xcd, slot); xcd picks a 4x8 block
   // of the tile grid, slot a tile inside it.  Row-major when the grid is not a
@@ -412,6 +428,8 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   asm volatile("s_barrier" ::: "memory");
+  // read after the final barrier, past every ds_write the loop waits for
+  if (kSilu && wave_s == 0) silu_table[lane] = table_entry;
   for (uint32_t kt = 0; kt + 1 < ktiles; ++kt) {
     const uint16_t* la = smem + (kt & 1u) * kStageElems;
     read_step(la, 0);
@@ -433,13 +451,14 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
       issue_operand_tile<kLoads>(pb, voff, (kt + 2) * kK * 2u, st + TILE * kK, wave_s);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
   {  // the last tile, masked past k when k is not a multiple of 64
     const uint16_t* la = smem + ((ktiles - 1) & 1u) * kStageElems;
     read_step(la, 0);
-    if (k_last != (uint32_t)kK) mask_step(0);
+    if (kRaggedK && k_last != (uint32_t)kK) mask_step(0);
     mfma_step();
     read_step(la, 1);
-    if (k_last != (uint32_t)kK) mask_step(1);
+    if (kRaggedK && k_last != (uint32_t)kK) mask_step(1);
     mfma_step();
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmLgkm0);
@@ -451,8 +470,14 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
   // Epilogue: wave-private 64 x 64 bf16 region (8 KiB) with 128-B rows, chunk
   // q of row r at q ^ (r & 7).  Lanes 2c and 2c+1 hold adjacent columns of
   // rows r and r+1; one exchange lets each write a 32-bit column pair.
-  uint16_t* cst = smem + wave * (64u * 64u);
-  const bool odd = lane & 1u;
+  // Lane-derived values come from an opaque copy of the lane index, so none
+  // is computed before the loop ends (in the last tile every register holds
+  // an accumulator or a fragment); the region base from the scalar wave index.
+  uint32_t elane = lane;
+  asm volatile("" : "+v"(elane));
+  const uint32_t egrp = elane >> 4;
+  uint16_t* cst = smem + wave_s * (64u * 64u);
+  const bool odd = elane & 1u;
   const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
   // SiLU in two passes, so the hot code stays one straight line: pass 1
   // stores every element's fast value and marks in the wave-uniform `redo`
@@ -469,15 +494,17 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
       for (int r = 0; r < 4; r += 2) {
         float v0 = acc[i][j][r], v1 = acc[i][j][r + 1];
         if (kSilu) {
-          bool x0, x1;
-          v0 = tiler::silu_bf16_candidate(v0, x0);
-          v1 = tiler::silu_bf16_candidate(v1, x1);
-          redo |= (uint32_t)(__builtin_amdgcn_ballot_w64(x0 || x1) != 0) << (i * 8 + j * 2 + r / 2);
+          uint64_t m0, m1;
+          v0 = tiler::silu_bf16_fast_marked(v0, m0);
+          v1 = tiler::silu_bf16_fast_marked(v1, m1);
+          redo |= (uint32_t)((m0 | m1) != 0) << (i * 8 + j * 2 + r / 2);
         }
-        const uint32_t row = i * 16u + grp * 4u + r + (odd ? 1u : 0u);
-        const uint32_t col = j * 16u + ((lane & 15u) & ~1u);
+        const uint32_t row = i * 16u + egrp * 4u + r + (odd ? 1u : 0u);
+        const uint32_t col = j * 16u + ((elane & 15u) & ~1u);
         const uint32_t q = (col >> 3) ^ (row & 7u);
-        *reinterpret_cast<uint32_t*>(cst + row * 64u + q * 8u + (col & 7u)) = pack_row_pair(v0, v1, sel);
+        // Under SiLU a NaN fast value comes only from a marked input (NaN,
+        // +-inf, beyond the fast domain), which pass 2 rewrites canonically.
+        *reinterpret_cast<uint32_t*>(cst + row * 64u + q * 8u + (col & 7u)) = pack_row_pair<!kSilu>(v0, v1, sel);
       }
   if (kSilu) {
     while (redo != 0) {
@@ -490,9 +517,9 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
         bool exact;
         (void)tiler::silu_bf16_candidate(xs[h], exact);
         if (exact) {
-          const uint32_t row = (p >> 3) * 16u + grp * 4u + (p & 1u) * 2u + (uint32_t)h;
-          const uint32_t col = ((p >> 1) & 3u) * 16u + (lane & 15u);
-          cst[row * 64u + (((col >> 3) ^ (row & 7u)) * 8u) + (col & 7u)] = narrow_one(tiler::silu_f32(xs[h]));
+          const uint32_t row = (p >> 3) * 16u + egrp * 4u + (p & 1u) * 2u + (uint32_t)h;
+          const uint32_t col = ((p >> 1) & 3u) * 16u + (elane & 15u);
+          cst[row * 64u + (((col >> 3) ^ (row & 7u)) * 8u) + (col & 7u)] = narrow_one(tiler::silu_f32(xs[h], silu_table));
         }
       }
     }
@@ -503,7 +530,7 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
   const uint32_t grow0 = m0 + (wave_s / kGrid) * 64u, gcol0 = n0 + (wave_s % kGrid) * 64u;
 #pragma unroll 4
   for (int it = 0; it < 64 * 8 / 64; ++it) {
-    const uint32_t qid = it * 64u + lane;
+    const uint32_t qid = it * 64u + elane;
     const uint32_t row = qid >> 3, q = qid & 7u;
     if (grow0 + row < m && gcol0 + q * 8u < n) {
       u32x4 v = *reinterpret_cast<const u32x4*>(cst + row * 64u + ((q ^ (row & 7u)) * 8u));
@@ -528,6 +555,22 @@ __device__ __forceinline__ void contract_bf16_staged_body(const uint16_t* __rest
   }
 TILER_CONTRACT_STAGED(256, 16)
 TILER_CONTRACT_STAGED(128, 4)
+
+// The same with k a multiple of 64 (no last-tile masking): *_kf.
+#define TILER_CONTRACT_STAGED_KF(TILE, WAVES)                                                       \
+  extern "C" __global__ void __launch_bounds__(64 * WAVES)                                          \
+      tiler_contract_bf16_t##TILE##_kf(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, \
+                                       uint32_t m, uint32_t n, uint32_t k, uint16_t* __restrict__ c) { \
+    contract_bf16_staged_body<TILE, false, false>(a, b, m, n, k, c);                                \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(64 * WAVES)                                          \
+      tiler_contract_bf16_silu_t##TILE##_kf(const uint16_t* __restrict__ a,                         \
+                                            const uint16_t* __restrict__ b, uint32_t m, uint32_t n, \
+                                            uint32_t k, uint16_t* __restrict__ c) {                 \
+    contract_bf16_staged_body<TILE, true, false>(a, b, m, n, k, c);                                 \
+  }
+TILER_CONTRACT_STAGED_KF(256, 16)
+TILER_CONTRACT_STAGED_KF(128, 4)
 
 // ---------------------------------------------------------------------------
 // Skinny bf16 contraction (m <= 64: decode-shaped), bandwidth-bound on B.

@@ -503,8 +503,10 @@ tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uin
     const bool big = t256 >= t.compute_units;
     const uint64_t tiles = big ? t256 : t128;
     if (tiles <= 0x7fffffffull) {
-      const char* name = big ? (silu ? "tiler_contract_bf16_silu_t256" : "tiler_contract_bf16_t256")
-                             : (silu ? "tiler_contract_bf16_silu_t128" : "tiler_contract_bf16_t128");
+      // k a multiple of 64: the forms without last-tile masking (_kf)
+      char name[48];
+      std::snprintf(name, sizeof(name), "tiler_contract_bf16_%st%u%s", silu ? "silu_" : "", big ? 256u : 128u,
+                    k % 64 == 0 ? "_kf" : "");
       p.add(name, (uint32_t)tiles, 1, big ? 1024 : 256).ptr(a).ptr(b).u32(m32).u32(n32).u32(k32).ptr(c);
       return TILER_HIP_OK;
     }

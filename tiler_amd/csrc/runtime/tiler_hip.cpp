@@ -202,6 +202,10 @@ const EntryRow kEntries[] = {
     {"tiler_contract_bf16_silu_t128", "tensor-contraction-bf16/cooperative+silu", 3},
     {"tiler_contract_bf16_t256", "tensor-contraction-bf16/cooperative", 3},
     {"tiler_contract_bf16_silu_t256", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_t128_kf", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_t128_kf", "tensor-contraction-bf16/cooperative+silu", 3},
+    {"tiler_contract_bf16_t256_kf", "tensor-contraction-bf16/cooperative", 3},
+    {"tiler_contract_bf16_silu_t256_kf", "tensor-contraction-bf16/cooperative+silu", 3},
     // general index structures: the strict fold (geometry in a constant slot),
     // the batched MFMA forms and the right-operand transpose ahead of them
     {"tiler_contract_general_f32", "tensor-contraction-f32/strict-general", 4},
