@@ -5,7 +5,10 @@ Builds tests/native/planner_sanitize.cpp against the runtime's own
 program.cpp and digest.cpp with g++ -fsanitize=address,undefined (no device
 code, no HIP runtime). It runs every planner over random and edge-case
 requests (zero, huge and overflowing extents, unaligned addresses, invalid
-enums) and the digest over random splits. The run must finish clean: no
+enums), the expression compiler over random and malformed node arrays (then
+the expression and fold-epilogue planners over what compiles), folds and
+signed-stride reindexes over random axis sets, general contractions over
+random index structures, and the digest over random splits. The run must finish clean: no
 sanitizer report, no argument segment overflow, every binding inside its
 segment and naming a declared slot.
 
