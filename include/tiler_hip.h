@@ -807,7 +807,23 @@ typedef struct {
     /* PROGRAM_CONTRACTION: NULL is td,od->to over extents {m, n, k}; else the
      * index structure (read during the call only), extents unused. */
     const tiler_hip_contraction_structure *structure;
+    /* TILER_HIP_FORM_*: 0 lets the library choose the realization; a proposal
+     * of tiler_hip_propose names the form it offered.  A form the program
+     * does not have, or one the request's shape does not admit, refuses. */
+    uint32_t form;
+    uint32_t reserved;     /* 0 */
 } tiler_hip_region;
+
+/* Forms a region may name (tiler_hip_region.form).  The contraction forms
+ * apply to td,od->to bf16 under PERMITS_REASSOCIATION; the softmax forms to
+ * rows of more than four 8192-element segments under PERMITS_REASSOCIATION. */
+#define TILER_HIP_FORM_AUTO 0u
+#define TILER_HIP_FORM_CONTRACT_SKINNY 1u     /* m <= 64: B streamed once, 16 columns per workgroup */
+#define TILER_HIP_FORM_CONTRACT_STAGED_256 2u /* 256x256 tiles, 16 waves, LDS-DMA double buffer */
+#define TILER_HIP_FORM_CONTRACT_STAGED_128 3u /* 128x128 tiles, 4 waves, the same schedule */
+#define TILER_HIP_FORM_CONTRACT_GENERAL_128 4u /* register-staged 128x128 tiles, any n and k */
+#define TILER_HIP_FORM_SOFTMAX_SPLIT 5u       /* three launches over segment partials in scratch */
+#define TILER_HIP_FORM_SOFTMAX_ROW_SYNC 6u    /* one row-synchronized launch (at most two workgroups per CU) */
 
 /* Storage slot roles.  Slot order per program:
  *   expression  the inputs in access order, y, program (a constant slot)
@@ -859,6 +875,71 @@ typedef struct {
  * dtype this library does not realize. */
 tiler_hip_status tiler_hip_realize(const tiler_hip_context *ctx, const tiler_hip_region *region,
                                    tiler_hip_realization *out, char *diagnostic,
+                                   uint64_t diagnostic_bytes);
+
+/* ------------------------------------------------------------------------
+ * Physical-implementation provider (PhysicalImplementationProvider::propose,
+ * tiler-compiler/src/frontier.rs:1507-1527; ProviderOffer :1466-1495).
+ * Everything this library can run for one region, so that its gfx950 tile
+ * widths, workgroup sizes and dispatch counts are visible to a planner: every
+ * strategy it has for the region's program, each either proposed -- with the
+ * region to realize for it, its launch geometry and its structural cost -- or
+ * declined with the cause the reference's StrategyDeclineCause names
+ * (frontier.rs:1311-1384).  An empty offer is not an error.  The offer
+ * depends only on its inputs (deterministic, no device access; ctx may be
+ * NULL, as for tiler_hip_realize).
+ *
+ * Strategy keys: the reference's own where the strategy is the reference's
+ * ("tiler.region.serial-baseline", "tiler.reduction.multi-pass-split",
+ * "tiler.reduction.single-workgroup-tree"; physical.rs:551,3241,3570), and
+ * "gfx950." keys for this library's own forms. */
+#define TILER_HIP_MAX_PROPOSALS 6
+#define TILER_HIP_DECLINE_NUMERICAL_PERMISSION_REFUSED 1u /* subject: the dimension key ("numerics.reassociation") */
+#define TILER_HIP_DECLINE_NO_ADMISSIBLE_SHAPE 2u          /* subject: the rule; extent: the extent that admitted none */
+#define TILER_HIP_DECLINE_UNREPRESENTABLE 3u              /* subject: the rule (the planner's refusal) */
+
+typedef struct {
+    char strategy[64];
+    tiler_hip_region region;       /* the request with this strategy's choices (form, topology, grouping):
+                                      tiler_hip_realize on it gives exactly this implementation */
+    /* PhysicalCostEstimate::structural (frontier.rs:351-400; model tiler.cost.structural.v1) */
+    uint32_t dispatch_count;
+    uint64_t launched_threads;
+    uint64_t temporary_bytes;      /* scratch slots */
+    /* The launches, in order: kernel, workgroups (x * y) and threads per workgroup. */
+    char symbols[4][48];
+    uint64_t workgroups[4];
+    uint32_t workgroup_threads[4];
+    /* The measured cost row's selector (tiler-compiler/src/measured_cost.rs:60-110;
+     * key tiler.cost.measured-fold-steps.v1): sum over stages of max(work, depth * P)
+     * with P the profile's saturated_parallel_fold_steps.  Assessed for the
+     * sum's strategies, where the row was fitted; 0 elsewhere. */
+    uint64_t measured_fold_steps;
+} tiler_hip_proposal;
+
+typedef struct {
+    char strategy[64];
+    uint32_t cause;                /* TILER_HIP_DECLINE_* */
+    char subject[64];
+    uint64_t extent;
+} tiler_hip_declined_strategy;
+
+typedef struct {
+    char provider[64];             /* provenance */
+    uint32_t proposal_count;
+    uint32_t declined_count;
+    uint32_t chosen;               /* the proposal tiler_hip_realize picks with form AUTO (its index), or
+                                      the measured row's least fold steps among the sum's proposals */
+    tiler_hip_proposal proposals[TILER_HIP_MAX_PROPOSALS];
+    tiler_hip_declined_strategy declined[TILER_HIP_MAX_PROPOSALS];
+} tiler_hip_provider_offer;
+
+/* Refuses only what no strategy could read: a NULL region or offer, an
+ * unknown program, a malformed request every strategy refuses the same way
+ * (then the diagnostic names it).  A region that names a form is proposed as
+ * if it named none. */
+tiler_hip_status tiler_hip_propose(const tiler_hip_context *ctx, const tiler_hip_region *region,
+                                   tiler_hip_provider_offer *offer, char *diagnostic,
                                    uint64_t diagnostic_bytes);
 
 #ifdef __cplusplus

@@ -85,6 +85,19 @@ SUBNORMALS_FLUSH_POSITIVE = 3
 CONVERT_NARROW_F32_BF16 = 0
 CONVERT_WIDEN_BF16_F32 = 1
 
+FORM_AUTO = 0
+FORM_CONTRACT_SKINNY = 1
+FORM_CONTRACT_STAGED_256 = 2
+FORM_CONTRACT_STAGED_128 = 3
+FORM_CONTRACT_GENERAL_128 = 4
+FORM_SOFTMAX_SPLIT = 5
+FORM_SOFTMAX_ROW_SYNC = 6
+
+MAX_PROPOSALS = 6
+DECLINE_NUMERICAL_PERMISSION_REFUSED = 1
+DECLINE_NO_ADMISSIBLE_SHAPE = 2
+DECLINE_UNREPRESENTABLE = 3
+
 REGION_ALIGNED16 = 1
 REGION_OPERAND_BROADCAST = 2
 REGION_INDEX_SIGNED = 4
@@ -273,6 +286,42 @@ class Region(ctypes.Structure):
         ("root", ctypes.c_uint32),
         ("nodes", ctypes.POINTER(ExpressionNode)),
         ("structure", ctypes.POINTER(ContractionStructure)),
+        ("form", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+class Proposal(ctypes.Structure):
+    _fields_ = [
+        ("strategy", ctypes.c_char * 64),
+        ("region", Region),
+        ("dispatch_count", ctypes.c_uint32),
+        ("launched_threads", ctypes.c_uint64),
+        ("temporary_bytes", ctypes.c_uint64),
+        ("symbols", (ctypes.c_char * 48) * 4),
+        ("workgroups", ctypes.c_uint64 * 4),
+        ("workgroup_threads", ctypes.c_uint32 * 4),
+        ("measured_fold_steps", ctypes.c_uint64),
+    ]
+
+
+class DeclinedStrategy(ctypes.Structure):
+    _fields_ = [
+        ("strategy", ctypes.c_char * 64),
+        ("cause", ctypes.c_uint32),
+        ("subject", ctypes.c_char * 64),
+        ("extent", ctypes.c_uint64),
+    ]
+
+
+class ProviderOffer(ctypes.Structure):
+    _fields_ = [
+        ("provider", ctypes.c_char * 64),
+        ("proposal_count", ctypes.c_uint32),
+        ("declined_count", ctypes.c_uint32),
+        ("chosen", ctypes.c_uint32),
+        ("proposals", Proposal * MAX_PROPOSALS),
+        ("declined", DeclinedStrategy * MAX_PROPOSALS),
     ]
 
 
@@ -419,6 +468,8 @@ SIGNATURES = {
     "tiler_hip_contract_bf16": (_S, [_CTX, _P, _P, _U64, _U64, _U64, _P, _U32, _P]),
     "tiler_hip_contract": (_S, [_CTX, _U32, ctypes.POINTER(ContractionStructure), _U32, _U32, _P, _P, _P, _P]),
     "tiler_hip_realize": (_S, [_CTX, ctypes.POINTER(Region), ctypes.POINTER(Realization),
+                               ctypes.c_char_p, _U64]),
+    "tiler_hip_propose": (_S, [_CTX, ctypes.POINTER(Region), ctypes.POINTER(ProviderOffer),
                                ctypes.c_char_p, _U64]),
     "tiler_hip_expression": (_S, [_CTX, _U32, ctypes.POINTER(ExpressionNode), _U32, _U32,
                                   ctypes.POINTER(_P), _U64, _P, _U32, _U32, _P]),

@@ -253,9 +253,16 @@ tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_
 //   valid between calls; a realized plan's scratch is fresh, so its program
 //   zeroes the area with a fill kernel first.
 tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
-                                  const uintptr_t* addr, Program& p, bool strict) {
+                                  const uintptr_t* addr, Program& p, bool strict, uint32_t form) {
   const uint32_t x = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotInput);
   const uint32_t y = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotOutput);
+  if (form != TILER_HIP_FORM_AUTO) {
+    if (strict || (form != TILER_HIP_FORM_SOFTMAX_SPLIT && form != TILER_HIP_FORM_SOFTMAX_ROW_SYNC))
+      return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "form: not a form of this softmax");
+    if ((extent + kSoftmaxSegment - 1) / kSoftmaxSegment <= 4)
+      return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                      "segmented-rows: the split and row-synchronized forms take rows of more than four segments");
+  }
   if (rows == 0 || extent == 0) return TILER_HIP_OK;
   if (extent > 0xffffffffull)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
@@ -279,7 +286,12 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
     }
     const uint64_t wgs = mul_sat(rows, nseg);
     if (wgs > 0x7fffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more segments than the launch grid holds");
-    if (wgs <= 2ull * t.compute_units && wgs <= kRowSyncMaxWorkgroups) {
+    const bool sync_fits = wgs <= 2ull * t.compute_units && wgs <= kRowSyncMaxWorkgroups;
+    if (form == TILER_HIP_FORM_SOFTMAX_ROW_SYNC && !sync_fits)
+      return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                      "row-sync-residency: the row-synchronized form needs every segment's workgroup resident "
+                      "(at most two per CU)");
+    if (sync_fits && form != TILER_HIP_FORM_SOFTMAX_SPLIT) {
       const uint64_t sync_bytes = 256 + 16 * wgs;
       const uint32_t sync = p.slot(sync_bytes, kSlotScratch);
       if (mode == Mode::Realized)
@@ -465,8 +477,12 @@ tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Pr
 }
 
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
-                                    uint32_t epilogue, const uintptr_t* addr, Program& p, bool strict) {
+                                    uint32_t epilogue, const uintptr_t* addr, Program& p, bool strict,
+                                    uint32_t form) {
   if (epilogue > TILER_HIP_EPILOGUE_SILU) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "epilogue");
+  if (form != TILER_HIP_FORM_AUTO &&
+      (strict || form < TILER_HIP_FORM_CONTRACT_SKINNY || form > TILER_HIP_FORM_CONTRACT_GENERAL_128))
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "form: not a form of this contraction");
   const uint32_t a = p.slot(mul_sat(mul_sat(m, k), 2), kSlotInput);
   const uint32_t b = p.slot(mul_sat(mul_sat(n, k), 2), kSlotInput);
   const uint32_t c = p.slot(mul_sat(mul_sat(m, n), 2), kSlotOutput);
@@ -485,8 +501,14 @@ tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uin
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
   const bool silu = epilogue == TILER_HIP_EPILOGUE_SILU;
   const uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
+  const bool pick = form == TILER_HIP_FORM_AUTO;
   // m <= 64 (decode shapes): B streamed once, one workgroup per 16 columns.
-  if (m <= 64 && k % 8 == 0 && aligned16(addr[a]) && aligned16(addr[b]) && (n + 15) / 16 <= 0x7fffffffull) {
+  const bool skinny_ok = m <= 64 && k % 8 == 0 && aligned16(addr[a]) && aligned16(addr[b]) &&
+                         (n + 15) / 16 <= 0x7fffffffull;
+  if (form == TILER_HIP_FORM_CONTRACT_SKINNY && !skinny_ok)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                    "skinny-rows: the skinny form takes m <= 64 and k a multiple of 8, aligned operands");
+  if (skinny_ok && (pick || form == TILER_HIP_FORM_CONTRACT_SKINNY)) {
     char name[48];
     std::snprintf(name, sizeof(name), "tiler_contract_bf16_%sskinny%u", silu ? "silu_" : "", (uint32_t)((m + 15) / 16));
     p.add(name, (uint32_t)((n + 15) / 16), 1, 1024).ptr(a).ptr(b).u32(m32).u32(n32).u32(k32).ptr(c);
@@ -496,12 +518,18 @@ tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uin
   // buffer resource with 32-bit offsets (256 * k * 2 bytes must stay below
   // 2^31) and moves 16-byte rows: n and k multiples of 8, aligned operands.
   // 256-tiles when they fill every CU, 128-tiles (four times as many) when not.
-  if (n % 8 == 0 && k % 8 == 0 && k * 512ull < (1ull << 31) && aligned16(addr[a]) && aligned16(addr[b]) &&
-      aligned16(addr[c])) {
+  const bool staged_ok = n % 8 == 0 && k % 8 == 0 && k * 512ull < (1ull << 31) && aligned16(addr[a]) &&
+                         aligned16(addr[b]) && aligned16(addr[c]);
+  if ((form == TILER_HIP_FORM_CONTRACT_STAGED_256 || form == TILER_HIP_FORM_CONTRACT_STAGED_128) && !staged_ok)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                    "staged-rows: the staged forms take n and k multiples of 8 (k below 2^22), aligned operands");
+  if (staged_ok && form != TILER_HIP_FORM_CONTRACT_SKINNY && form != TILER_HIP_FORM_CONTRACT_GENERAL_128) {
     const uint64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
     const uint64_t t128 = ((m + 127) / 128) * ((n + 127) / 128);
-    const bool big = t256 >= t.compute_units;
+    const bool big = pick ? t256 >= t.compute_units : form == TILER_HIP_FORM_CONTRACT_STAGED_256;
     const uint64_t tiles = big ? t256 : t128;
+    if (!pick && tiles > 0x7fffffffull)
+      return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more tiles than the launch grid holds");
     if (tiles <= 0x7fffffffull) {
       // k a multiple of 64: the forms without last-tile masking (_kf)
       char name[48];

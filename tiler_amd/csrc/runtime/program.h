@@ -145,8 +145,11 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
 tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
                                Program& p, bool strict = false);
+// `form` (TILER_HIP_FORM_SOFTMAX_*) forces the split or the row-synchronized
+// launch for rows of more than four segments.
 tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
-                                  const uintptr_t* addr, Program& p, bool strict = false);
+                                  const uintptr_t* addr, Program& p, bool strict = false,
+                                  uint32_t form = TILER_HIP_FORM_AUTO);
 tiler_hip_status plan_map(Mode mode, uint32_t op, uint32_t dtype, int32_t x2_broadcast,
                           uint64_t n, float a, float b, const uintptr_t* addr, Program& p);
 tiler_hip_status plan_broadcast(uint64_t src_elements, uint32_t rank, const uint64_t* out_dims,
@@ -163,9 +166,11 @@ tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Pr
 // [batch.., m, k] x [batch.., n, k | k, n] -> [batch.., m, n].
 tiler_hip_status plan_contract_general(const Target& t, uint32_t dtype, const tiler_hip_contraction_structure& s,
                                        uint32_t epilogue, bool strict, const uintptr_t* addr, Program& p);
+// `form` (TILER_HIP_FORM_CONTRACT_*) forces one MFMA form, refusing when the
+// request does not admit it; TILER_HIP_FORM_AUTO lets the planner choose.
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
                                     uint32_t epilogue, const uintptr_t* addr, Program& p,
-                                    bool strict = false);
+                                    bool strict = false, uint32_t form = TILER_HIP_FORM_AUTO);
 // Pointwise expression over n elements: slots inputs 0..I-1, y, program
 // (CONSTANT), and -- for programs beyond the register form -- the value
 // store (SCRATCH).  `addr` covers the inputs then y.

@@ -222,6 +222,13 @@ const EntryRow kEntries[] = {
 };
 constexpr uint32_t kEntryCount = sizeof(kEntries) / sizeof(kEntries[0]);
 
+// The payload entry named `symbol`, or kEntryCount.
+uint32_t entry_index(const char* symbol) {
+  for (uint32_t k = 0; k < kEntryCount; ++k)
+    if (std::strcmp(kEntries[k].symbol, symbol) == 0) return k;
+  return kEntryCount;
+}
+
 constexpr uint32_t kMaxSumWorkgroups = tiler_rt::kMaxSumWorkgroups;
 constexpr uint32_t kProfileComputeUnits = 256;
 
@@ -1602,11 +1609,9 @@ bool arithmetic(uint32_t program) {
 
 }  // namespace
 
-tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip_region* r,
-                                   tiler_hip_realization* out, char* diagnostic,
-                                   uint64_t diagnostic_bytes) {
-  if (!r || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  std::memset(out, 0, sizeof(*out));
+// The program a region realizes as (the planners' own output), or the
+// refusal with its diagnostic in p.diag.
+static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hip_region* r, tiler_rt::Program& p) {
   const bool al = (r->flags & TILER_HIP_REGION_ALIGNED16) != 0;
   const bool bc = (r->flags & TILER_HIP_REGION_OPERAND_BROADCAST) != 0;
   // A stand-in address per slot: 0 is 16-byte aligned, 1 is not.
@@ -1615,21 +1620,21 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
   const uint64_t* e = r->extents;
   const tiler_rt::Target t = target_of(ctx);
   const tiler_rt::Contract c = contract_of(r);
-  tiler_rt::Program p;
   tiler_hip_status st;
-  if (c.input_mode > TILER_HIP_SUBNORMALS_FLUSH_POSITIVE || c.result_mode > TILER_HIP_SUBNORMALS_FLUSH_POSITIVE) {
-    copy_text(diagnostic, diagnostic_bytes, "unknown subnormal mode");
-    return TILER_HIP_REFUSE_INVALID_ARGUMENT;
-  }
+  if (c.input_mode > TILER_HIP_SUBNORMALS_FLUSH_POSITIVE || c.result_mode > TILER_HIP_SUBNORMALS_FLUSH_POSITIVE)
+    return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "unknown subnormal mode");
+  if (r->reserved != 0) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "reserved region field is not 0");
   // The device preserves subnormals; a flushing contract is realized only
   // where the kernel implements the modes (f32 expressions).  Byte moves do
   // no arithmetic.
   if (c.flushes() && arithmetic(r->program) &&
-      !(r->program == TILER_HIP_PROGRAM_EXPRESSION && r->dtype == TILER_HIP_F32)) {
-    copy_text(diagnostic, diagnostic_bytes,
-              "a flushing subnormal mode is not realized for this program (the device preserves subnormals)");
-    return TILER_HIP_REFUSE_UNSUPPORTED;
-  }
+      !(r->program == TILER_HIP_PROGRAM_EXPRESSION && r->dtype == TILER_HIP_F32))
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                    "a flushing subnormal mode is not realized for this program (the device preserves subnormals)");
+  // Forms belong to the softmax and the td,od->to bf16 contraction.
+  if (r->form != TILER_HIP_FORM_AUTO && r->program != TILER_HIP_PROGRAM_SOFTMAX &&
+      !(r->program == TILER_HIP_PROGRAM_CONTRACTION && !r->structure && r->dtype == TILER_HIP_BF16))
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "form: this program has one form");
   auto needs_reassociation = [&](const char* what) {
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
                     (std::string(what) + " regroups the fold; the contract grants no reassociation").c_str());
@@ -1695,7 +1700,7 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
       break;
     case TILER_HIP_PROGRAM_SOFTMAX:
       st = r->dtype == TILER_HIP_F32
-               ? tiler_rt::plan_softmax_f32(tiler_rt::Mode::Realized, t, e[0], e[1], addr, p, !c.reassociate)
+               ? tiler_rt::plan_softmax_f32(tiler_rt::Mode::Realized, t, e[0], e[1], addr, p, !c.reassociate, r->form)
                : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "softmax is an f32 family");
       break;
     case TILER_HIP_PROGRAM_CONTRACTION:
@@ -1706,7 +1711,7 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
                  ? tiler_rt::plan_contract_strict_f32(e[0], e[1], e[2], p)
                  : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the strict f32 contraction has no epilogue");
       else if (r->dtype == TILER_HIP_BF16)
-        st = tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p, !c.reassociate);
+        st = tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p, !c.reassociate, r->form);
       else
         st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "contraction dtype");
       break;
@@ -1730,15 +1735,29 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
     default:
       st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "no realization for this scalar program");
   }
+  if (st != TILER_HIP_OK) return st;
+  if (p.constant.size() > TILER_HIP_REALIZATION_CONSTANT_BYTES)
+    return p.refuse(TILER_HIP_REFUSE_CAPACITY, "the program's constant slot exceeds the realization's capacity");
+  for (uint32_t i = 0; i < p.nlaunches; ++i) {
+    if (p.launches[i].overflow) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "argument segment overflow");
+    if (entry_index(p.launches[i].symbol) == kEntryCount)
+      return p.refuse(TILER_HIP_REFUSE_ABSENT_SYMBOL, (std::string("no payload entry for ") + p.launches[i].symbol).c_str());
+  }
+  return TILER_HIP_OK;
+}
+
+tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip_region* r,
+                                   tiler_hip_realization* out, char* diagnostic,
+                                   uint64_t diagnostic_bytes) {
+  if (!r || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  std::memset(out, 0, sizeof(*out));
+  tiler_rt::Program p;
+  const tiler_hip_status st = plan_region(ctx, r, p);
   if (st != TILER_HIP_OK) {
     copy_text(diagnostic, diagnostic_bytes, p.diag);
     return st;
   }
-  if (p.constant.size() > TILER_HIP_REALIZATION_CONSTANT_BYTES) {
-    copy_text(diagnostic, diagnostic_bytes, "the program's constant slot exceeds the realization's capacity");
-    std::memset(out, 0, sizeof(*out));
-    return TILER_HIP_REFUSE_CAPACITY;
-  }
+  const bool al = (r->flags & TILER_HIP_REGION_ALIGNED16) != 0;
   out->slot_count = p.nslots;
   for (uint32_t i = 0; i < p.nslots; ++i) {
     out->slot_roles[i] = p.slot_roles[i];
@@ -1751,15 +1770,7 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
   for (uint32_t i = 0; i < p.nlaunches; ++i) {
     const tiler_rt::Launch& l = p.launches[i];
     tiler_hip_realized_entry& d = out->entries[i];
-    uint32_t idx = kEntryCount;
-    for (uint32_t k = 0; k < kEntryCount; ++k)
-      if (std::strcmp(kEntries[k].symbol, l.symbol) == 0) idx = k;
-    if (idx == kEntryCount || l.overflow) {
-      copy_text(diagnostic, diagnostic_bytes, std::string("no payload entry for ") + l.symbol);
-      std::memset(out, 0, sizeof(*out));
-      return TILER_HIP_REFUSE_ABSENT_SYMBOL;
-    }
-    d.entry = idx;
+    d.entry = entry_index(l.symbol);
     d.grid[0] = l.grid[0];
     d.grid[1] = l.grid[1];
     d.grid[2] = 1;
@@ -1774,6 +1785,275 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
     }
   }
   out->entry_count = p.nlaunches;
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Physical-implementation provider.
+namespace {
+
+constexpr uint64_t kSaturatedParallelFoldSteps = 142900;  // the profile's measured cost row
+constexpr uint64_t kCombineSteps = 6 + 4;                 // a workgroup's butterfly and wave partials
+constexpr uint64_t kCombineWork = 256 * 6 + 4;
+constexpr char kSerialBaseline[] = "tiler.region.serial-baseline";
+constexpr char kMultiPassSplit[] = "tiler.reduction.multi-pass-split";
+constexpr char kWorkgroupTree[] = "tiler.reduction.single-workgroup-tree";
+constexpr char kReassociation[] = "numerics.reassociation";
+
+uint64_t sat_add(uint64_t a, uint64_t b) { return a > UINT64_MAX - b ? UINT64_MAX : a + b; }
+uint64_t sat_mul(uint64_t a, uint64_t b) { return a && b > UINT64_MAX / a ? UINT64_MAX : a * b; }
+
+uint64_t isqrt(uint64_t n) {
+  uint64_t r = (uint64_t)std::sqrt((double)n);
+  while (r > 0 && (r > n / r)) --r;
+  while ((r + 1) <= n / (r + 1)) ++r;
+  return r;
+}
+
+// The reference's split partition (tiler-compiler/src/physical.rs:2780-2798):
+// the largest divisor c <= isqrt(n) leaving at least two partitions of c.
+bool governed_partition(uint64_t n, uint64_t& partitions, uint64_t& per) {
+  if (n < 4) return false;
+  for (uint64_t c = isqrt(n); c >= 2; --c)
+    if (n % c == 0 && n / c >= 2) {
+      partitions = n / c;
+      per = c;
+      return true;
+    }
+  return false;
+}
+
+struct Stage {
+  uint64_t work, depth;
+};
+
+// Fold steps of each stage of a sum strategy: work summed over every
+// invocation, depth the longest sequential path (the same accounting the
+// calibration sweep fits the row with).
+std::vector<Stage> sum_stages(const tiler_rt::Target& t, const tiler_hip_region& r) {
+  const uint64_t rows = r.extents[0], extent = r.extents[1], n = sat_mul(rows, extent);
+  switch (r.topology) {
+    case TILER_HIP_SUM_SERIAL:
+      return {{n, extent}};
+    case TILER_HIP_SUM_MULTIPASS:
+      return {{n, r.grouping[1]}, {sat_mul(rows, r.grouping[0]), r.grouping[0]}};
+    case TILER_HIP_SUM_COOPERATIVE: {
+      const uint64_t P = r.grouping[0], c = r.grouping[1], R = r.grouping[2];
+      return {{sat_add(n, sat_mul(rows, sat_mul(R, P))), sat_mul(R, sat_add(c, P))}};
+    }
+    default:
+      if (rows == 1) {
+        const uint64_t g = tiler_rt::tree_workgroups(t, n);
+        return {{sat_add(n, g * kCombineWork), (n + 256 * g - 1) / (256 * g) + kCombineSteps},
+                {g + kCombineWork, (g + 255) / 256 + kCombineSteps}};
+      }
+      return {{sat_mul(rows, sat_add(extent, kCombineWork)), (extent + 255) / 256 + kCombineSteps}};
+  }
+}
+
+uint64_t measured_fold_steps(const std::vector<Stage>& st) {
+  uint64_t total = 0;
+  for (const Stage& s : st) {
+    const uint64_t span = sat_mul(s.depth, kSaturatedParallelFoldSteps);
+    total = sat_add(total, s.work > span ? s.work : span);
+  }
+  return total;
+}
+
+struct Offer {
+  tiler_hip_provider_offer* out;
+  tiler_hip_status invalid = TILER_HIP_OK;  // an INVALID_ARGUMENT refusal, if one came back
+  std::string invalid_diag;
+
+  void decline(const char* strategy, uint32_t cause, const std::string& subject, uint64_t extent) {
+    if (out->declined_count >= TILER_HIP_MAX_PROPOSALS) return;
+    tiler_hip_declined_strategy& d = out->declined[out->declined_count++];
+    copy_text(d.strategy, sizeof(d.strategy), strategy);
+    d.cause = cause;
+    copy_text(d.subject, sizeof(d.subject), subject);
+    d.extent = extent;
+  }
+
+  // Plans `region` for `strategy`: a proposal, or a decline named from the
+  // planner's refusal (a "rule: ..." diagnostic is a shape the strategy does
+  // not admit at `extent`).
+  int propose(const tiler_hip_context* ctx, const char* strategy, const tiler_hip_region& region, uint64_t extent,
+              bool fold_steps) {
+    tiler_rt::Program p;
+    const tiler_hip_status st = plan_region(ctx, &region, p);
+    if (st != TILER_HIP_OK) {
+      if (st == TILER_HIP_REFUSE_INVALID_ARGUMENT && invalid == TILER_HIP_OK) {
+        invalid = st;
+        invalid_diag = p.diag;
+      }
+      const std::string diag = p.diag;
+      const size_t colon = diag.find(':');
+      if (st == TILER_HIP_REFUSE_UNSUPPORTED && colon != std::string::npos && diag.find(' ') > colon)
+        decline(strategy, TILER_HIP_DECLINE_NO_ADMISSIBLE_SHAPE, diag.substr(0, colon), extent);
+      else
+        decline(strategy, TILER_HIP_DECLINE_UNREPRESENTABLE, diag, extent);
+      return -1;
+    }
+    if (out->proposal_count >= TILER_HIP_MAX_PROPOSALS) return -1;
+    tiler_hip_proposal& q = out->proposals[out->proposal_count];
+    copy_text(q.strategy, sizeof(q.strategy), strategy);
+    q.region = region;
+    q.dispatch_count = p.nlaunches;
+    for (uint32_t i = 0; i < p.nlaunches; ++i) {
+      const tiler_rt::Launch& l = p.launches[i];
+      copy_text(q.symbols[i], sizeof(q.symbols[i]), l.symbol);
+      q.workgroups[i] = (uint64_t)l.grid[0] * l.grid[1];
+      q.workgroup_threads[i] = l.block;
+      q.launched_threads = sat_add(q.launched_threads, sat_mul(q.workgroups[i], l.block));
+    }
+    for (uint32_t i = 0; i < p.nslots; ++i)
+      if (p.slot_roles[i] == tiler_rt::kSlotScratch) q.temporary_bytes = sat_add(q.temporary_bytes, p.slot_bytes[i]);
+    q.measured_fold_steps = fold_steps ? measured_fold_steps(sum_stages(target_of(ctx), region)) : 0;
+    return (int)out->proposal_count++;
+  }
+};
+
+}  // namespace
+
+tiler_hip_status tiler_hip_propose(const tiler_hip_context* ctx, const tiler_hip_region* r,
+                                   tiler_hip_provider_offer* out, char* diagnostic, uint64_t diagnostic_bytes) {
+  if (!r || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  std::memset(out, 0, sizeof(*out));
+  copy_text(out->provider, sizeof(out->provider), "tiler.hip.gfx950-physical-provider");
+  Offer o{out};
+  tiler_hip_region base = *r;
+  base.form = TILER_HIP_FORM_AUTO;
+  const bool reassociate = (r->permissions & TILER_HIP_PERMITS_REASSOCIATION) != 0;
+  tiler_hip_region strict = base;
+  strict.permissions &= ~TILER_HIP_PERMITS_REASSOCIATION;
+  // A reassociating strategy: proposed under the permission, else declined for it.
+  auto regrouping = [&](const char* strategy, const tiler_hip_region& region, uint64_t extent, bool steps) {
+    if (!reassociate) {
+      o.decline(strategy, TILER_HIP_DECLINE_NUMERICAL_PERMISSION_REFUSED, kReassociation, 0);
+      return -1;
+    }
+    return o.propose(ctx, strategy, region, extent, steps);
+  };
+  int chosen = -1;
+  const uint64_t* e = r->extents;
+  switch (r->program) {
+    case TILER_HIP_PROGRAM_SERIAL_SUM: {
+      tiler_hip_region v = strict;
+      v.topology = TILER_HIP_SUM_SERIAL;
+      o.propose(ctx, kSerialBaseline, v, e[1], true);
+      uint64_t parts = 0, per = 0;
+      if (!reassociate) {
+        o.decline(kMultiPassSplit, TILER_HIP_DECLINE_NUMERICAL_PERMISSION_REFUSED, kReassociation, 0);
+      } else if (!governed_partition(e[1], parts, per)) {
+        o.decline(kMultiPassSplit, TILER_HIP_DECLINE_NO_ADMISSIBLE_SHAPE, "no-admissible-partition", e[1]);
+      } else {
+        v = base;
+        v.topology = TILER_HIP_SUM_MULTIPASS;
+        v.grouping[0] = parts;
+        v.grouping[1] = per;
+        v.grouping[2] = 0;
+        o.propose(ctx, kMultiPassSplit, v, e[1], true);
+      }
+      v = base;
+      v.topology = TILER_HIP_SUM_TREE;
+      v.grouping[0] = v.grouping[1] = v.grouping[2] = 0;
+      regrouping(e[0] == 1 ? "gfx950.reduction.grid-tree" : kWorkgroupTree, v, e[1], true);
+      if (!reassociate) {
+        o.decline("gfx950.reduction.cooperative-workgroup", TILER_HIP_DECLINE_NUMERICAL_PERMISSION_REFUSED,
+                  kReassociation, 0);
+      } else if (e[1] == 0 || e[1] % 256 != 0) {
+        o.decline("gfx950.reduction.cooperative-workgroup", TILER_HIP_DECLINE_NO_ADMISSIBLE_SHAPE,
+                  "no-admissible-participant-count", e[1]);
+      } else {
+        v = base;
+        v.topology = TILER_HIP_SUM_COOPERATIVE;
+        v.flags &= ~TILER_HIP_REGION_PARTICIPANT_MAJOR;
+        v.grouping[0] = 256;
+        v.grouping[1] = e[1] / 256;
+        v.grouping[2] = 1;
+        o.propose(ctx, "gfx950.reduction.cooperative-workgroup", v, e[1], true);
+      }
+      // The measured cost row's selector: the least fold steps.
+      for (uint32_t i = 0; i < out->proposal_count; ++i)
+        if (chosen < 0 || out->proposals[i].measured_fold_steps < out->proposals[chosen].measured_fold_steps)
+          chosen = (int)i;
+      break;
+    }
+    case TILER_HIP_PROGRAM_RMS_NORM:
+    case TILER_HIP_PROGRAM_SOFTMAX: {
+      const int s0 = o.propose(ctx, kSerialBaseline, strict, e[1], false);
+      const uint64_t nseg = (e[1] + tiler_rt::kSoftmaxSegment - 1) / tiler_rt::kSoftmaxSegment;
+      int g = -1;
+      if (r->program == TILER_HIP_PROGRAM_SOFTMAX && nseg > 4) {
+        tiler_hip_region v = base;
+        v.form = TILER_HIP_FORM_SOFTMAX_ROW_SYNC;
+        const int sync = regrouping("gfx950.softmax.row-synchronized", v, sat_mul(e[0], nseg), false);
+        v.form = TILER_HIP_FORM_SOFTMAX_SPLIT;
+        const int split = regrouping("gfx950.softmax.split", v, sat_mul(e[0], nseg), false);
+        g = sync >= 0 ? sync : split;
+      } else {
+        g = regrouping("gfx950.rows.grouped-fold", base, e[1], false);
+      }
+      chosen = reassociate && g >= 0 ? g : s0;
+      break;
+    }
+    case TILER_HIP_PROGRAM_CONTRACTION: {
+      const int s0 = o.propose(ctx, kSerialBaseline, strict, r->structure ? 0 : e[2], false);
+      if (r->dtype != TILER_HIP_BF16) {
+        chosen = s0;
+        break;
+      }
+      if (r->structure) {
+        if (!reassociate) {
+          o.decline("gfx950.contraction.mfma-batched", TILER_HIP_DECLINE_NUMERICAL_PERMISSION_REFUSED,
+                    kReassociation, 0);
+          chosen = s0;
+          break;
+        }
+        tiler_rt::Program p;
+        if (plan_region(ctx, &base, p) == TILER_HIP_OK && p.nlaunches &&
+            std::strncmp(p.launches[p.nlaunches - 1].symbol, "tiler_contract_general", 22) == 0) {
+          o.decline("gfx950.contraction.mfma-batched", TILER_HIP_DECLINE_NO_ADMISSIBLE_SHAPE,
+                    "batched-operand-layout", 0);
+          chosen = s0;
+        } else {
+          const int b = o.propose(ctx, "gfx950.contraction.mfma-batched", base, 0, false);
+          chosen = b >= 0 ? b : s0;
+        }
+        break;
+      }
+      static const struct {
+        const char* strategy;
+        uint32_t form;
+      } forms[] = {{"gfx950.contraction.mfma-skinny", TILER_HIP_FORM_CONTRACT_SKINNY},
+                   {"gfx950.contraction.mfma-staged-256", TILER_HIP_FORM_CONTRACT_STAGED_256},
+                   {"gfx950.contraction.mfma-staged-128", TILER_HIP_FORM_CONTRACT_STAGED_128},
+                   {"gfx950.contraction.mfma-general-128", TILER_HIP_FORM_CONTRACT_GENERAL_128}};
+      tiler_rt::Program autop;
+      const bool auto_ok = reassociate && plan_region(ctx, &base, autop) == TILER_HIP_OK;
+      chosen = s0;
+      for (const auto& f : forms) {
+        tiler_hip_region v = base;
+        v.form = f.form;
+        const uint64_t extent = f.form == TILER_HIP_FORM_CONTRACT_SKINNY ? e[0] : e[1] % 8 ? e[1] : e[2];
+        const int i = regrouping(f.strategy, v, extent, false);
+        if (i >= 0 && auto_ok && autop.nlaunches && out->proposals[i].dispatch_count == autop.nlaunches &&
+            std::strcmp(out->proposals[i].symbols[0], autop.launches[0].symbol) == 0)
+          chosen = i;
+      }
+      break;
+    }
+    default:
+      chosen = o.propose(ctx, kSerialBaseline, base, 0, false);
+  }
+  if (out->proposal_count == 0 && o.invalid != TILER_HIP_OK) {
+    const std::string why = o.invalid_diag;
+    std::memset(out, 0, sizeof(*out));
+    copy_text(diagnostic, diagnostic_bytes, why);
+    return o.invalid;
+  }
+  out->chosen = chosen >= 0 ? (uint32_t)chosen : 0;
+  copy_text(diagnostic, diagnostic_bytes, "");
   return TILER_HIP_OK;
 }
 

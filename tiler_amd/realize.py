@@ -61,20 +61,11 @@ def _entry_info(index: int):
     return info.symbol.decode(), info.family.decode()
 
 
-def realize(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_SERIAL, variant: int = 0,
+def _region(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_SERIAL, variant: int = 0,
             flags: int = L.REGION_ALIGNED16, rank: int = 0, strides=(), grouping=(), scalars=(),
             permissions: int = 0, input_subnormals: int = 0, result_subnormals: int = 0,
-            nodes=(), root: int | None = None, structure=None, ctx=None) -> Realization:
-    """Realizes one region.  `ctx` (a runtime.Context) lets the bound device's
-    CU count decide tile sizes and groupings; without it the declared
-    profile's does (the call is then device-free).
-
-    The contract: `permissions` (L.PERMITS_*) and the two subnormal modes
-    (L.SUBNORMALS_*, 0 preserve) are the plan's numerical contract for this
-    region; the defaults are the strict contract.  `nodes` (op, a, b) and
-    `root` (default: the last node) give an expression's DAG, or a fold's
-    epilogue.  `structure` (an L.ContractionStructure, see
-    L.contraction_structure) makes a contraction region general."""
+            nodes=(), root: int | None = None, structure=None, form: int = L.FORM_AUTO):
+    """An L.Region and the objects its pointers reference (kept alive with it)."""
     r = L.Region()
     r.program, r.topology, r.dtype, r.variant, r.flags, r.rank = program, topology, dtype, variant, flags, rank
     for i, v in enumerate(extents):
@@ -86,6 +77,7 @@ def realize(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_
     for i, v in enumerate(scalars):
         r.scalars[i] = int(v)
     r.permissions, r.input_subnormals, r.result_subnormals = permissions, input_subnormals, result_subnormals
+    r.form = form
     node_array = (L.ExpressionNode * max(1, len(nodes)))(*[L.ExpressionNode(*nd) for nd in nodes])
     if len(nodes):
         r.node_count = len(nodes)
@@ -93,6 +85,30 @@ def realize(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_
         r.nodes = node_array
     if structure is not None:
         r.structure = ctypes.pointer(structure)
+    return r, (node_array, structure)
+
+
+def realize(program: int, extents, *, ctx=None, **kw) -> Realization:
+    """Realizes one region.  `ctx` (a runtime.Context) lets the bound device's
+    CU count decide tile sizes and groupings; without it the declared
+    profile's does (the call is then device-free).
+
+    Keywords (the tiler_hip_region fields): dtype, topology, variant, flags,
+    rank, strides, grouping, scalars.  The contract: `permissions`
+    (L.PERMITS_*) and the two subnormal modes `input_subnormals` /
+    `result_subnormals` (L.SUBNORMALS_*, 0 preserve) are the plan's numerical
+    contract for this region; the defaults are the strict contract.  `nodes`
+    (op, a, b) and `root` (default: the last node) give an expression's DAG,
+    or a fold's epilogue.  `structure` (an L.ContractionStructure, see
+    L.contraction_structure) makes a contraction region general.  `form`
+    (L.FORM_*) names one form a proposal offered (default: the library's
+    choice)."""
+    r, keep = _region(program, **dict(kw, extents=extents))
+    return _realize_region(r, ctx)
+
+
+def _realize_region(r, ctx) -> Realization:
+    program = r.program
     out = L.Realization()
     diag = ctypes.create_string_buffer(256)
     st = L.lib().tiler_hip_realize(ctx.handle if ctx is not None else None, ctypes.byref(r), ctypes.byref(out),
@@ -107,6 +123,71 @@ def realize(program: int, extents, *, dtype: int = L.F32, topology: int = L.SUM_
             symbol, family, tuple(e.grid), tuple(e.block),
             [(e.binding_slots[b], e.binding_offsets[b]) for b in range(e.binding_count)]))
     return res
+
+
+@dataclass
+class Proposal:
+    """One implementation tiler_hip_propose offered: its strategy key, the
+    launches (kernel, workgroups, threads per workgroup), its structural cost
+    (dispatches, launched threads, temporary bytes) and, for the sum, the
+    measured row's fold steps."""
+    strategy: str
+    symbols: list
+    workgroups: list
+    workgroup_threads: list
+    dispatch_count: int
+    launched_threads: int
+    temporary_bytes: int
+    measured_fold_steps: int
+    region: L.Region
+    _keep: tuple = ()
+
+    def realize(self, ctx=None) -> Realization:
+        """The realization of exactly this proposal."""
+        return _realize_region(self.region, ctx)
+
+
+@dataclass
+class Declined:
+    strategy: str
+    cause: int  # L.DECLINE_*
+    subject: str  # the numerical dimension key, or the rule
+    extent: int
+
+
+@dataclass
+class Offer:
+    provider: str
+    proposals: list
+    declined: list
+    chosen: int  # index into proposals
+
+    def strategies(self) -> list:
+        return [p.strategy for p in self.proposals]
+
+
+def propose(program: int, extents, *, ctx=None, **kw) -> Offer:
+    """Every implementation the library has for one region
+    (PhysicalImplementationProvider::propose, tiler-compiler/src/frontier.rs:1507-1527),
+    proposed or declined with its cause.  Keywords as for realize."""
+    r, keep = _region(program, **dict(kw, extents=extents))
+    offer = L.ProviderOffer()
+    diag = ctypes.create_string_buffer(256)
+    st = L.lib().tiler_hip_propose(ctx.handle if ctx is not None else None, ctypes.byref(r), ctypes.byref(offer),
+                                   diag, 256)
+    _raise(st, "propose", diag.value.decode())
+    props = []
+    for i in range(offer.proposal_count):
+        q = offer.proposals[i]
+        n = q.dispatch_count
+        region = L.Region()
+        ctypes.pointer(region)[0] = q.region
+        props.append(Proposal(q.strategy.decode(), [q.symbols[j].value.decode() for j in range(n)],
+                              list(q.workgroups[:n]), list(q.workgroup_threads[:n]), n, q.launched_threads,
+                              q.temporary_bytes, q.measured_fold_steps, region, keep))
+    declined = [Declined(d.strategy.decode(), d.cause, d.subject.decode(), d.extent)
+                for d in offer.declined[:offer.declined_count]]
+    return Offer(offer.provider.decode(), props, declined, offer.chosen)
 
 
 def _payload_code():
