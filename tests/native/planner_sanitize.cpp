@@ -158,13 +158,15 @@ int main() {
     plan_sum_f32(t, pick(r), pick(r), sp, addr, p[0]);
     plan_rms_norm((uint32_t)(r() % 3), (int32_t)(r() % 2), pick(r), pick(r), r() % 2 ? 0x3727C5ACu : (uint32_t)r(),
                   addr, p[1]);
-    plan_softmax_f32(r() % 2 ? Mode::Direct : Mode::Realized, t, pick(r), pick(r), addr, p[2]);
+    plan_softmax_f32(r() % 2 ? Mode::Direct : Mode::Realized, t, pick(r), pick(r), addr, p[2], r() % 4 == 0,
+                     (uint32_t)(r() % 8));
     plan_map(mode, (uint32_t)(r() % 5), (uint32_t)(r() % 3), (int32_t)(r() % 2), pick(r), 1.0f, 2.0f, addr, p[3]);
     plan_broadcast(pick(r), (uint32_t)(r() % 10) % 9, dims, strides, (uint32_t)(r() % 6), p[4]);
     plan_gather(mode, pick(r), pick(r), pick(r), (uint32_t)(r() % 17), pick(r), (int32_t)(r() % 2), addr, p[5]);
     plan_convert(mode, (uint32_t)(r() % 3), pick(r), addr, p[6]);
     plan_contract_strict_f32(pick(r), pick(r), pick(r), p[7]);
-    plan_contract_bf16(t, pick(r), pick(r), pick(r), (uint32_t)(r() % 3), addr, p[8]);
+    plan_contract_bf16(t, pick(r), pick(r), pick(r), (uint32_t)(r() % 3), addr, p[8], r() % 4 == 0,
+                       (uint32_t)(r() % 6));
     for (int i = 0; i < 9; ++i) {
       check(p[i]);
       planned += p[i].nlaunches;
