@@ -111,11 +111,17 @@ def test_sum_strategies(rows, extent):
 
 
 def test_sum_split_declined_without_a_partition():
-    for extent in (3, 1009):  # below four contributors; a prime
+    for extent in (3, 1009, (1 << 61) - 1):  # below four contributors; primes
         o = propose(L.PROGRAM_SERIAL_SUM, (2, extent), permissions=RE)
         (d,) = [d for d in o.declined if d.strategy == "tiler.reduction.multi-pass-split"]
-        assert d.cause == L.DECLINE_NO_ADMISSIBLE_SHAPE and d.subject == "no-admissible-partition"
+        if extent < 1 << 48:
+            assert d.cause == L.DECLINE_NO_ADMISSIBLE_SHAPE and d.subject == "no-admissible-partition"
+        else:  # beyond any device's memory: the partition search is not run
+            assert d.cause == L.DECLINE_UNREPRESENTABLE and d.subject == "split-extent-unrepresentable"
         assert d.extent == extent
+    # the largest extents saturate the fold-step counts instead of wrapping
+    o = propose(L.PROGRAM_SERIAL_SUM, (1, (1 << 64) - 1), permissions=RE)
+    assert all(p.measured_fold_steps > 0 for p in o.proposals)
 
 
 def test_the_measured_row_prefers_the_tree_for_one_long_row_and_serial_for_many_short():

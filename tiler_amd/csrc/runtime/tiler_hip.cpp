@@ -1802,6 +1802,10 @@ constexpr char kReassociation[] = "numerics.reassociation";
 
 uint64_t sat_add(uint64_t a, uint64_t b) { return a > UINT64_MAX - b ? UINT64_MAX : a + b; }
 uint64_t sat_mul(uint64_t a, uint64_t b) { return a && b > UINT64_MAX / a ? UINT64_MAX : a * b; }
+uint64_t ceil_div(uint64_t a, uint64_t b) { return a / b + (a % b != 0); }
+// Contributor counts beyond this hold more than a petabyte of f32: the split's
+// partition search (a walk down from the square root) is not run for them.
+constexpr uint64_t kMaxPartitionedExtent = 1ull << 48;
 
 uint64_t isqrt(uint64_t n) {
   uint64_t r = (uint64_t)std::sqrt((double)n);
@@ -1844,10 +1848,10 @@ std::vector<Stage> sum_stages(const tiler_rt::Target& t, const tiler_hip_region&
     default:
       if (rows == 1) {
         const uint64_t g = tiler_rt::tree_workgroups(t, n);
-        return {{sat_add(n, g * kCombineWork), (n + 256 * g - 1) / (256 * g) + kCombineSteps},
-                {g + kCombineWork, (g + 255) / 256 + kCombineSteps}};
+        return {{sat_add(n, g * kCombineWork), ceil_div(n, 256 * g) + kCombineSteps},
+                {g + kCombineWork, ceil_div(g, 256) + kCombineSteps}};
       }
-      return {{sat_mul(rows, sat_add(extent, kCombineWork)), (extent + 255) / 256 + kCombineSteps}};
+      return {{sat_mul(rows, sat_add(extent, kCombineWork)), ceil_div(extent, 256) + kCombineSteps}};
   }
 }
 
@@ -1944,6 +1948,8 @@ tiler_hip_status tiler_hip_propose(const tiler_hip_context* ctx, const tiler_hip
       uint64_t parts = 0, per = 0;
       if (!reassociate) {
         o.decline(kMultiPassSplit, TILER_HIP_DECLINE_NUMERICAL_PERMISSION_REFUSED, kReassociation, 0);
+      } else if (e[1] > kMaxPartitionedExtent) {
+        o.decline(kMultiPassSplit, TILER_HIP_DECLINE_UNREPRESENTABLE, "split-extent-unrepresentable", e[1]);
       } else if (!governed_partition(e[1], parts, per)) {
         o.decline(kMultiPassSplit, TILER_HIP_DECLINE_NO_ADMISSIBLE_SHAPE, "no-admissible-partition", e[1]);
       } else {
