@@ -170,7 +170,7 @@ def test_row_synchronized_softmax_fallback_matches(ctx):
         for c in (c0, ctx):
             dx, dy = c.to_device(x), c.alloc(x.nbytes)
             try:
-                for _ in range(3):  # the counters return to zero after every call
+                for _ in range(3):  # every call raises the epoch past its own tag
                     c.fill_u32(dy, 0, x.size)
                     c.softmax_f32(dx, rows, extent, dy)
                     c.synchronize()
@@ -179,3 +179,25 @@ def test_row_synchronized_softmax_fallback_matches(ctx):
                 dx.free(); dy.free()
     finally:
         c0.close()
+
+
+def test_row_synchronized_softmax_calls_of_changing_shapes(ctx):
+    # Calls of different shapes share the context's epoch and word area: a
+    # call's segment positions hold an earlier call's words (of other rows,
+    # other values) under earlier tags, which must never be taken for its own.
+    cus = ctx.observe_live_device("compute-units")
+    shapes = [(32, 131072), (5, 50001), (31, 90000), (2, 70001), (32, 131072), (5, 50001)]
+    rng = np.random.default_rng(17)
+    for i, (rows, extent) in enumerate(shapes * 2):
+        assert _form(rows, extent, cus) == "row-synchronized"
+        x = (rng.standard_normal((rows, extent)) * (1 + i)).astype(np.float32)
+        print(f"[row-sync call {i}] {rows}x{extent}", flush=True)
+        dx, dy = ctx.to_device(x), ctx.alloc(x.nbytes)
+        try:
+            ctx.softmax_f32(dx, rows, extent, dy)
+            ctx.synchronize()
+            got = dy.download(np.float32, x.shape)
+        finally:
+            dx.free(); dy.free()
+        want = oracle.softmax_grouped(x, rows, extent, 4, 4, 8192).reshape(rows, extent)
+        assert np.array_equal(bits(got), bits(want)), (rows, extent)

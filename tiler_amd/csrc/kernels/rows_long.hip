@@ -465,16 +465,27 @@ __device__ __forceinline__ void softmax_split_out(const float* __restrict__ x, f
 // of its row.  A published value is one 64-bit word, (tag << 32) | bits,
 // written and polled with relaxed agent-scope atomics: a word is valid when
 // its tag is this call's, so no ordering between locations (and no cache
-// write-back) is needed.  The tag is the epoch word + 1; the last workgroup
-// of the call to publish its partial (every workgroup has read the epoch by
-// then) stores the tag as the next epoch, so earlier calls' words never
-// match.  A wait is bounded (`wait_ticks` of the 100 MHz real-time clock); a
+// write-back) is needed.
+// The epoch is a 64-bit word; a workgroup reads it (e) first and takes the
+// call number c = e + 1, or e + 2 when the low 32 bits of e + 1 are zero;
+// the tag is the low 32 bits of c, never 0 (the workspace's initial words).
+// At its end a workgroup raises the epoch to c by an atomic maximum that
+// nobody waits on -- segment 0 of each row, and any workgroup whose wait ran
+// out.  Every tag a call publishes under is then at most the next call's
+// epoch: a row whose workgroups agree on the tag has its segment 0 raise the
+// epoch to it, and in a row whose workgroups read different epochs (one
+// started after another workgroup of the call ended) no wait can complete,
+// so every one of them raises the epoch to its own.  Tags so only repeat
+// after 2^32 - 1 calls.  (A counter of arrivals that picks the last
+// workgroup would serialize every workgroup on one address and put that on
+// the kernel's critical path: 3.5 us of 20.5 at 32 x 131072.)
+// A wait is bounded (`wait_ticks` of the 100 MHz real-time clock); a
 // workgroup whose wait runs out computes the row maximum, or the row sum with
 // the same segment fold, from the row itself, so results never depend on the
 // workgroups being resident together -- only the speed does.
 //
-// sync: u32 epoch, u32 count, pad to 256 bytes, then u64 words for the
-// maxima [rows * nseg] and the partials [rows * nseg].
+// sync: u64 epoch, pad to 256 bytes, then u64 words for the maxima
+// [rows * nseg] and the partials [rows * nseg].
 constexpr uint32_t kRowSyncHeaderBytes = 256;
 
 // Wave 0 only: the row's nseg words of this call's tag, 64 per lane group in
@@ -561,33 +572,36 @@ __device__ __forceinline__ void softmax_rowsync(const float* __restrict__ x, flo
                                                 uint64_t nseg, uint8_t* __restrict__ sync, uint64_t wait_ticks,
                                                 double* tab) {
   __shared__ float lds[4];
-  __shared__ uint32_t sh_ok;
+  __shared__ uint32_t sh_ok, sh_late;
   __shared__ float sh_val;
   const uint32_t t = threadIdx.x;
   const uint64_t wgs = gridDim.x;
   const uint64_t row = blockIdx.x / nseg, sg = blockIdx.x % nseg;
   const uint64_t chunks = (extent + 3u) / 4u;
   const float* xr = x + row * extent;
-  uint32_t* ctl = reinterpret_cast<uint32_t*>(sync);
+  uint64_t* epoch = reinterpret_cast<uint64_t*>(sync);
   uint64_t* wmax = reinterpret_cast<uint64_t*>(sync + kRowSyncHeaderBytes) + row * nseg;
   uint64_t* wsum = reinterpret_cast<uint64_t*>(sync + kRowSyncHeaderBytes) + wgs + row * nseg;
   f32x4 xv[kSegChunks];
   load_segment<AL>(xr, sg, chunks, extent, xv);
   // Only wave 0 publishes and polls, so only its lanes need the epoch.
-  const uint32_t e = t < 64 ? __hip_atomic_load(&ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+  const uint64_t e = t < 64 ? __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
   const double tv = kExp2Table64[t & 63u];
   float m = -__builtin_huge_valf();
 #pragma unroll
   for (uint32_t i = 0; i < kSegChunks; ++i) m = max_chunk(m, xv[i]);
   if (t < 64) tab[t] = tv;
-  m = seg_block_max(m, lds);  // its barrier also publishes tab
-  const uint32_t tag = e + 1u == 0u ? 1u : e + 1u;  // never 0, the workspace's initial words
+  if (t == 0) sh_late = 0;
+  m = seg_block_max(m, lds);  // its barrier also publishes tab and sh_late
+  const uint64_t call = (uint32_t)(e + 1) == 0u ? e + 2 : e + 1;
+  const uint32_t tag = (uint32_t)call;
   if (t < 64) {
     if (t == 0) __hip_atomic_store(&wmax[sg], tagged(tag, m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float v;
     const bool ok = collect_row(wmax, nseg, tag, wait_ticks, false, &v);
     if (t == 0) {
       sh_ok = ok ? 1u : 0u;
+      sh_late |= ok ? 0u : 1u;
       sh_val = v;
     }
   }
@@ -611,15 +625,12 @@ __device__ __forceinline__ void softmax_rowsync(const float* __restrict__ x, flo
       p = p + lds[2];
       p = p + lds[3];
       __hip_atomic_store(&wsum[sg], tagged(tag, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (__hip_atomic_fetch_add(&ctl[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)wgs - 1) {
-        __hip_atomic_store(&ctl[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&ctl[0], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
     }
     float v;
     const bool ok = collect_row(wsum, nseg, tag, wait_ticks, true, &v);
     if (t == 0) {
       sh_ok = ok ? 1u : 0u;
+      sh_late |= ok ? 0u : 1u;
       sh_val = v;
     }
   }
@@ -632,6 +643,7 @@ __device__ __forceinline__ void softmax_rowsync(const float* __restrict__ x, flo
     const uint64_t q = sg * kSegChunkSpan + t + i * kSegThreads;
     if (q < chunks) store_f32_chunk<AL>(yr, q, extent, scale_chunk(xv[i], r));
   }
+  if (t == 0 && (sg == 0 || sh_late)) __hip_atomic_fetch_max(epoch, call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace

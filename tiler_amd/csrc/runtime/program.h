@@ -37,7 +37,7 @@ constexpr uint64_t kWorkspacePartialBytes = 256 * 1024;
 // Softmax rows longer than kWaveRowMax fold by segments of this many elements.
 constexpr uint64_t kWaveRowMax = 8192;
 constexpr uint64_t kSoftmaxSegment = 8192;
-// The row-synchronized softmax keeps its epoch, count and tagged words in a
+// The row-synchronized softmax keeps its 64-bit epoch and tagged words in a
 // workspace area nothing else writes (256 header bytes, then 2 words of 8
 // bytes per workgroup); it runs at most this many workgroups.
 constexpr uint64_t kRowSyncMaxWorkgroups = 1024;

@@ -253,7 +253,7 @@ struct tiler_hip_context {
   std::vector<hipModule_t> routed_modules;
   std::vector<hipFunction_t> prepared;
   // workspace: [partials kWorkspacePartialBytes][gather_bad u64 + pad]
-  //            [row-synchronized softmax area kRowSyncBytes: epoch, count, tagged words]
+  //            [row-synchronized softmax area kRowSyncBytes: epoch, tagged words]
   uint8_t* workspace = nullptr;
   float* sum_partials = nullptr;
   unsigned long long* gather_bad = nullptr;
