@@ -857,8 +857,6 @@ tiler_hip_status compile_expression(uint32_t dtype, const tiler_hip_expression_n
   for (uint32_t k = 0; k < nin; ++k) order.push_back(node_of_ordinal[k]);
   for (uint32_t i = 0; i < count; ++i)
     if (input_of[i] < 0) order.push_back(i);
-  std::vector<uint32_t> pos(count);
-  for (uint32_t s = 0; s < count; ++s) pos[order[s]] = s;
   std::vector<uint32_t> last(count, 0);  // execution step of the last read
   for (uint32_t s = 0; s < count; ++s) {
     const tiler_hip_expression_node& nd = nodes[order[s]];
@@ -900,7 +898,6 @@ tiler_hip_status compile_expression(uint32_t dtype, const tiler_hip_expression_n
   out.inputs = nin;
   out.registers = high;
   out.result = reg[root];
-  (void)pos;
   return TILER_HIP_OK;
 }
 
