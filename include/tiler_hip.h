@@ -46,6 +46,7 @@ typedef int32_t tiler_hip_status;
 #define TILER_HIP_REFUSE_GATHER_INDEX_OUT_OF_BOUNDS (-9)
 #define TILER_HIP_REFUSE_UNRECOGNIZED_KEY (-10)
 #define TILER_HIP_REFUSE_NOT_PREPARED (-11)
+#define TILER_HIP_REFUSE_PAYLOAD_MISMATCH (-12) /* a payload's metadata names another compilation */
 /* Failures (post-commit; RuntimeAdapter::Failure). */
 #define TILER_HIP_FAIL_ALLOCATION 1
 #define TILER_HIP_FAIL_LAUNCH 2
@@ -240,6 +241,19 @@ tiler_hip_status tiler_hip_read_payload_metadata(const void *bytes, uint64_t byt
                                                  tiler_hip_payload_mapping *mappings,
                                                  uint32_t capacity, char *diagnostic,
                                                  uint64_t diagnostic_bytes);
+
+/* The producer's correspondence check (tiler-build/src/payload_cache.rs:522-526
+ * takes it; the reference's backends spell it at
+ * tiler-build/tests/custom_backend/backend.rs:545-574): does a PayloadMetadata
+ * record -- a carried or cached payload's -- describe this library's own
+ * compilation (tiler_hip_payload_metadata)?  The facts are read in order:
+ * "source-representation", "source", "toolchain", "target", "components",
+ * "flags", "entries".  TILER_HIP_OK and "" in `fact` when all agree;
+ * TILER_HIP_REFUSE_PAYLOAD_MISMATCH with the first disagreeing fact in `fact`;
+ * TILER_HIP_REFUSE_MALFORMED_PAYLOAD (and decode.rs's refusal in `fact`) when
+ * the record does not decode. */
+tiler_hip_status tiler_hip_payload_correspondence(const void *metadata, uint64_t byte_count, char *fact,
+                                                  uint64_t fact_bytes);
 
 /* The carried payload this backend executes (the role tiler-metal-aot's
  * loader plays for its own payloads): backend "tiler.hip", representation

@@ -179,3 +179,58 @@ def test_digest_refuses_missing_pointers():
     out = (ctypes.c_uint8 * 32)()
     assert L.lib().tiler_hip_digest(None, 4, None, None, 0, b"x", 1, out) == L.REFUSE_INVALID_ARGUMENT
     assert L.lib().tiler_hip_digest(b"d", 1, None, None, 1, b"x", 1, out) == L.REFUSE_INVALID_ARGUMENT
+
+
+def _own_fields() -> dict:
+    """This library's PayloadMetadata decoded into the test-side encoder's
+    keywords (tests/envelope_fixture.payload_metadata)."""
+    c = _Cursor(_metadata())
+    c.take(len(b"tiler.artifact-envelope.payload-metadata.v1\0"))
+    f = {"schema": (c.u(2), c.u(2)), "source_representation": c.text(), "source": c.run(), "toolchain": c.text(),
+         "target": c.text(), "family": c.text(), "language": c.text(), "deployment": (c.u(2), c.u(2))}
+    f["components"] = tuple((c.text(), c.text()) for _ in range(c.u(8)))
+    f["sdk"] = (c.text(), c.text(), c.text())
+    f["flags"] = tuple(c.text() for _ in range(c.u(8)))
+    f["link_flags"] = tuple(c.text() for _ in range(c.u(8)))
+    entries = []
+    for _ in range(c.u(8)):
+        key, sym = c.run(), c.text()
+        entries.append((key, sym, tuple(c.u(4) for _ in range(c.u(8)))))
+    f["entries"] = tuple(entries)
+    f["obligations"] = tuple((c.text(), c.text()) for _ in range(c.u(8)))
+    f["platform_tag"] = c.take(1)
+    assert c.i == len(c.b)
+    return f
+
+
+def _correspondence(md: bytes):
+    fact = ctypes.create_string_buffer(256)
+    st = L.lib().tiler_hip_payload_correspondence(md, len(md), fact, 256)
+    return st, fact.value.decode()
+
+
+def test_payload_correspondence_names_the_first_disagreeing_fact():
+    import envelope_fixture as F
+    own = _own_fields()
+    assert F.payload_metadata(**own) == _metadata()   # the test-side encoder reproduces the record exactly
+    assert _correspondence(_metadata()) == (L.OK, "")
+    variants = [
+        ("source-representation", {"source_representation": "tiler.hip.source-bundle.v2"}),
+        ("source", {"source": own["source"] + b" "}),
+        ("toolchain", {"toolchain": "tiler.hip.other-clang"}),
+        ("target", {"target": "amdgcn-amd-amdhsa--gfx942"}),
+        ("components", {"components": (("compiler", "another clang"),)}),
+        ("flags", {"flags": own["flags"][:-1]}),
+        ("flags", {"link_flags": ("-shared",)}),
+        ("entries", {"entries": own["entries"][:-1]}),
+    ]
+    for fact, change in variants:
+        assert _correspondence(F.payload_metadata(**dict(own, **change))) == (L.REFUSE_PAYLOAD_MISMATCH, fact)
+    # the order is the contract: of two disagreements the earlier fact is named
+    both = dict(own, toolchain="tiler.hip.other-clang", entries=own["entries"][:-1])
+    assert _correspondence(F.payload_metadata(**both)) == (L.REFUSE_PAYLOAD_MISMATCH, "toolchain")
+    # facts outside the correspondence (family, language, obligations) do not move it
+    assert _correspondence(F.payload_metadata(**dict(own, obligations=()))) == (L.OK, "")
+    # a record that does not decode is malformed, with decode.rs's refusal
+    st, why = _correspondence(_metadata()[:-3])
+    assert st == L.REFUSE_MALFORMED_PAYLOAD and why

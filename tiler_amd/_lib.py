@@ -24,6 +24,7 @@ REFUSE_UNSUPPORTED = -8
 REFUSE_GATHER_INDEX_OUT_OF_BOUNDS = -9
 REFUSE_UNRECOGNIZED_KEY = -10
 REFUSE_NOT_PREPARED = -11
+REFUSE_PAYLOAD_MISMATCH = -12
 FAIL_ALLOCATION = 1
 FAIL_LAUNCH = 2
 FAIL_DEVICE = 3
@@ -482,6 +483,7 @@ SIGNATURES = {
                                                   ctypes.c_char_p, _U64]),
     "tiler_hip_payload_metadata": (_S, [_P, _U64, ctypes.POINTER(_U64)]),
     "tiler_hip_payload_identity": (_S, [_P]),
+    "tiler_hip_payload_correspondence": (_S, [_P, _U64, ctypes.c_char_p, _U64]),
     "tiler_hip_digest": (_S, [_P, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64), _U32, _P, _U64, _P]),
     "tiler_hip_read_envelope": (_S, [_P, _U64, ctypes.POINTER(Envelope), ctypes.c_char_p, _U64]),
     "tiler_hip_read_payload_metadata": (_S, [_P, _U64, ctypes.POINTER(PayloadSubject),

@@ -564,6 +564,7 @@ void metadata_or_throw(const uint8_t* bytes, uint64_t n, PayloadSubject& m, Payl
   m.language = c.text();
   m.deployment_major = c.u16();
   m.deployment_minor = c.u16();
+  const uint64_t components_at = c.position();
   m.component_count = c.count(kMaxProvenanceComponents, "ProvenanceComponents");
   // Each collection is read whole before its order is checked, as
   // Cursor::vec then require_canonical do.
@@ -582,14 +583,18 @@ void metadata_or_throw(const uint8_t* bytes, uint64_t n, PayloadSubject& m, Payl
     prev_version = version;
   }
   if (order >= 0) require_ordered(order, "ProvenanceComponent");
+  m.components = Span{c.at(components_at), c.position() - components_at};
   m.sdk_name = c.text();
   m.sdk_version = c.text();
   m.sdk_build = c.text();
+  const uint64_t flags_at = c.position();
   m.compile_flag_count = c.count(kMaxProvenanceFlags, "ProvenanceFlags");
   for (uint64_t i = 0; i < m.compile_flag_count; ++i) c.text();
   m.link_flag_count = c.count(kMaxProvenanceFlags, "ProvenanceFlags");
   for (uint64_t i = 0; i < m.link_flag_count; ++i) c.text();
+  m.flags = Span{c.at(flags_at), c.position() - flags_at};
 
+  const uint64_t entries_at = c.position();
   m.entry_count = c.count(kMaxPayloadEntryMappings, "PayloadEntryMappings");
   Span prev_key{};
   order = -1;
@@ -604,6 +609,7 @@ void metadata_or_throw(const uint8_t* bytes, uint64_t n, PayloadSubject& m, Payl
     if (i < capacity && out) out[i] = e;
   }
   if (order >= 0) require_ordered(order, "PayloadEntryMapping");
+  m.entries = Span{c.at(entries_at), c.position() - entries_at};
 
   m.obligation_count = c.count(kMaxTargetObligations, "TargetObligations");
   Span prev_ok{}, prev_ov{};
@@ -665,6 +671,18 @@ std::string read_envelope(const uint8_t* bytes, uint64_t n, Envelope& out) {
   } catch (...) {  // allocation failure: nothing crosses the C ABI
     return "AllocationFailure";
   }
+}
+
+const char* first_disagreeing_fact(const PayloadSubject& expected, const PayloadSubject& actual) {
+  auto same = [](Span a, Span b) { return a.n == b.n && (a.n == 0 || std::memcmp(a.p, b.p, a.n) == 0); };
+  if (!same(expected.source_representation, actual.source_representation)) return "source-representation";
+  if (!same(expected.source, actual.source)) return "source";
+  if (!same(expected.toolchain, actual.toolchain)) return "toolchain";
+  if (!same(expected.target, actual.target)) return "target";
+  if (!same(expected.components, actual.components)) return "components";
+  if (!same(expected.flags, actual.flags)) return "flags";
+  if (!same(expected.entries, actual.entries)) return "entries";
+  return "";
 }
 
 std::string read_payload_metadata(const uint8_t* bytes, uint64_t n, PayloadSubject& out,

@@ -84,6 +84,9 @@ struct PayloadSubject {
   uint64_t component_count = 0, compile_flag_count = 0, link_flag_count = 0;
   uint64_t entry_count = 0, obligation_count = 0;
   bool unversioned = false;
+  // The encoded lists as they lie in the record (counts included): the
+  // ordered tool components, the compile and link flags, the entry mappings.
+  Span components, flags, entries;
 };
 
 // decode_metadata (codec/payload.rs:589-660) with check_provenance
@@ -91,5 +94,13 @@ struct PayloadSubject {
 // `mappings` (which may be null when capacity is 0).
 std::string read_payload_metadata(const uint8_t* bytes, uint64_t n, PayloadSubject& out,
                                   PayloadMapping* mappings, uint64_t capacity);
+
+// The first fact on which two decoded PayloadMetadata records disagree, in
+// the order a payload's correspondence check reads them
+// (tiler-build/tests/custom_backend/backend.rs:545-574,
+// tiler-build/examples/identity_join_producer.rs:978-1003):
+// "source-representation", "source", "toolchain", "target", "components",
+// "flags", "entries"; "" when every one agrees.
+const char* first_disagreeing_fact(const PayloadSubject& expected, const PayloadSubject& actual);
 
 }  // namespace tiler_rt

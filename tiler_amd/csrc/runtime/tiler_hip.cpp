@@ -483,6 +483,26 @@ tiler_hip_status tiler_hip_payload_metadata(uint8_t* out, uint64_t capacity, uin
   return TILER_HIP_OK;
 }
 
+tiler_hip_status tiler_hip_payload_correspondence(const void* metadata, uint64_t byte_count, char* fact,
+                                                  uint64_t fact_bytes) {
+  if (byte_count && !metadata) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  const std::vector<uint8_t>& own = payload_metadata_bytes();
+  tiler_rt::PayloadSubject expected, actual;
+  std::string why = tiler_rt::read_payload_metadata(own.data(), own.size(), expected, nullptr, 0);
+  if (!why.empty()) {  // this library's own record always decodes; say so if it ever does not
+    copy_text(fact, fact_bytes, "own metadata: " + why);
+    return TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+  }
+  why = tiler_rt::read_payload_metadata(static_cast<const uint8_t*>(metadata), byte_count, actual, nullptr, 0);
+  if (!why.empty()) {
+    copy_text(fact, fact_bytes, why);
+    return TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+  }
+  const char* first = tiler_rt::first_disagreeing_fact(expected, actual);
+  copy_text(fact, fact_bytes, first);
+  return first[0] ? TILER_HIP_REFUSE_PAYLOAD_MISMATCH : TILER_HIP_OK;
+}
+
 tiler_hip_status tiler_hip_payload_identity(uint8_t* out) {
   if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   const std::vector<uint8_t>& m = payload_metadata_bytes();
