@@ -356,7 +356,7 @@ tiler_hip_status run_program(tiler_hip_context* ctx, const tiler_rt::Program& p,
 extern "C" {
 
 // ---------------------------------------------------------------------------
-tiler_hip_status tiler_hip_profile_declare(tiler_hip_target_profile* out) {
+tiler_hip_status tiler_hip_profile_declare(tiler_hip_target_profile* out) try {
   if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   std::memset(out, 0, sizeof(*out));
   copy_text(out->profile_key, sizeof(out->profile_key), kProfileKey);
@@ -390,10 +390,12 @@ tiler_hip_status tiler_hip_profile_declare(tiler_hip_target_profile* out) {
             "measured: AMD Instinct MI355X gfx950:sramecc+:xnack- (256 CUs), ROCm 7.2, 2026-12-02; "
             "python -m tiler_amd.calibrate (profiles/saturated_parallel_fold_steps.md)");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // ---------------------------------------------------------------------------
-tiler_hip_status tiler_hip_payload(tiler_hip_payload_view* out) {
+tiler_hip_status tiler_hip_payload(tiler_hip_payload_view* out) try {
   if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   out->backend = kBackend;
   out->representation = kRepresentation;
@@ -407,6 +409,8 @@ tiler_hip_status tiler_hip_payload(tiler_hip_payload_view* out) {
   out->source = tiler_hip_source_bundle;
   out->source_bytes = (uint64_t)(tiler_hip_source_bundle_end - tiler_hip_source_bundle);
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // The payload's compilation subject in the artifact layer's canonical
@@ -474,17 +478,19 @@ const std::vector<uint8_t>& payload_metadata_bytes() {
 
 }  // namespace
 
-tiler_hip_status tiler_hip_payload_metadata(uint8_t* out, uint64_t capacity, uint64_t* required) {
+tiler_hip_status tiler_hip_payload_metadata(uint8_t* out, uint64_t capacity, uint64_t* required) try {
   const std::vector<uint8_t>& m = payload_metadata_bytes();
   if (required) *required = m.size();
   if (!out) return required ? TILER_HIP_OK : TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (capacity < m.size()) return TILER_HIP_REFUSE_CAPACITY;
   std::memcpy(out, m.data(), m.size());
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_payload_correspondence(const void* metadata, uint64_t byte_count, char* fact,
-                                                  uint64_t fact_bytes) {
+                                                  uint64_t fact_bytes) try {
   if (byte_count && !metadata) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   const std::vector<uint8_t>& own = payload_metadata_bytes();
   tiler_rt::PayloadSubject expected, actual;
@@ -501,19 +507,23 @@ tiler_hip_status tiler_hip_payload_correspondence(const void* metadata, uint64_t
   const char* first = tiler_rt::first_disagreeing_fact(expected, actual);
   copy_text(fact, fact_bytes, first);
   return first[0] ? TILER_HIP_REFUSE_PAYLOAD_MISMATCH : TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
-tiler_hip_status tiler_hip_payload_identity(uint8_t* out) {
+tiler_hip_status tiler_hip_payload_identity(uint8_t* out) try {
   if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   const std::vector<uint8_t>& m = payload_metadata_bytes();
   tiler_rt::governed_digest(kPayloadIdentityDomain, sizeof(kPayloadIdentityDomain) - 1, nullptr, nullptr, 0,
                             m.data(), m.size(), out);
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_digest(const void* domain, uint64_t domain_bytes, const void* const* qualifiers,
                                   const uint64_t* qualifier_bytes, uint32_t qualifier_count,
-                                  const void* bytes, uint64_t byte_count, uint8_t* out) {
+                                  const void* bytes, uint64_t byte_count, uint8_t* out) try {
   if (!out || (domain_bytes && !domain) || (byte_count && !bytes) ||
       (qualifier_count && (!qualifiers || !qualifier_bytes)))
     return TILER_HIP_REFUSE_INVALID_ARGUMENT;
@@ -522,9 +532,11 @@ tiler_hip_status tiler_hip_digest(const void* domain, uint64_t domain_bytes, con
   tiler_rt::governed_digest(domain, domain_bytes, qualifiers, qualifier_bytes, qualifier_count, bytes,
                             byte_count, out);
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
-tiler_hip_status tiler_hip_payload_entry(uint32_t index, tiler_hip_entry_info* out) {
+tiler_hip_status tiler_hip_payload_entry(uint32_t index, tiler_hip_entry_info* out) try {
   if (!out || index >= kEntryCount) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_hip::KernelDescriptorFacts facts;
   bool absent = false;
@@ -536,11 +548,13 @@ tiler_hip_status tiler_hip_payload_entry(uint32_t index, tiler_hip_entry_info* o
   out->buffer_bindings = kEntries[index].buffers;
   out->kernarg_bytes = facts.kernarg_bytes;
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_validate_payload(const void* code, uint64_t code_bytes,
                                             const char* symbol, uint32_t kernarg_bytes,
-                                            char* diagnostic, uint64_t diagnostic_bytes) {
+                                            char* diagnostic, uint64_t diagnostic_bytes) try {
   tiler_hip::KernelDescriptorFacts facts;
   bool absent = false;
   std::string why = tiler_hip::inspect_code_object(code, code_bytes, symbol, &facts, &absent);
@@ -556,10 +570,12 @@ tiler_hip_status tiler_hip_validate_payload(const void* code, uint64_t code_byte
   }
   copy_text(diagnostic, diagnostic_bytes, "");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_read_envelope(const void* bytes, uint64_t byte_count, tiler_hip_envelope* out,
-                                         char* diagnostic, uint64_t diagnostic_bytes) {
+                                         char* diagnostic, uint64_t diagnostic_bytes) try {
   if (!out || (byte_count && !bytes)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   static_assert(tiler_rt::kMaxEnvelopeSections == sizeof(out->section_purpose), "section table width");
   static_assert(tiler_rt::kMaxEnvelopePayloads == sizeof(out->payloads) / sizeof(out->payloads[0]),
@@ -600,12 +616,14 @@ tiler_hip_status tiler_hip_read_envelope(const void* bytes, uint64_t byte_count,
   }
   delete e;
   return why.empty() ? TILER_HIP_OK : TILER_HIP_REFUSE_MALFORMED_PAYLOAD;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_read_payload_metadata(const void* bytes, uint64_t byte_count,
                                                  tiler_hip_payload_subject* out,
                                                  tiler_hip_payload_mapping* mappings, uint32_t capacity,
-                                                 char* diagnostic, uint64_t diagnostic_bytes) {
+                                                 char* diagnostic, uint64_t diagnostic_bytes) try {
   if (!out || (byte_count && !bytes) || (capacity && !mappings)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   std::memset(out, 0, sizeof(*out));
   tiler_rt::PayloadSubject s;
@@ -641,6 +659,8 @@ tiler_hip_status tiler_hip_read_payload_metadata(const void* bytes, uint64_t byt
     mappings[i].transports = m[i].transports.p;
   }
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 namespace {
@@ -649,12 +669,14 @@ tiler_hip_status select_payload(const tiler_hip_envelope* envelope, uint32_t* in
 }  // namespace
 
 tiler_hip_status tiler_hip_select_payload(const tiler_hip_envelope* envelope, uint32_t* index,
-                                          char* diagnostic, uint64_t diagnostic_bytes) {
+                                          char* diagnostic, uint64_t diagnostic_bytes) try {
   try {
     return select_payload(envelope, index, diagnostic, diagnostic_bytes);
   } catch (...) {  // allocation failure: nothing crosses the C ABI
     return TILER_HIP_REFUSE_CAPACITY;
   }
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 namespace {
@@ -690,7 +712,7 @@ tiler_hip_status select_payload(const tiler_hip_envelope* envelope, uint32_t* in
 // ---------------------------------------------------------------------------
 tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
                                 tiler_hip_execution_environment* env, char* diagnostic,
-                                uint64_t diagnostic_bytes) {
+                                uint64_t diagnostic_bytes) try {
   if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   *out = nullptr;
   int count = 0;
@@ -784,6 +806,8 @@ tiler_hip_status tiler_hip_bind(int32_t ordinal, tiler_hip_context** out,
   copy_text(diagnostic, diagnostic_bytes, "");
   *out = ctx;
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 void tiler_hip_release(tiler_hip_context* ctx) {
@@ -841,7 +865,7 @@ tiler_hip_status measure_subnormals(tiler_hip_context* ctx) {
 }  // namespace
 
 tiler_hip_status tiler_hip_observe_live_device(tiler_hip_context* ctx, const char* key,
-                                               uint64_t* value) {
+                                               uint64_t* value) try {
   if (!ctx || !key || !value) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   std::string k = key;
   if (k == "f32-input-subnormals" || k == "f32-result-subnormals") {
@@ -862,11 +886,13 @@ tiler_hip_status tiler_hip_observe_live_device(tiler_hip_context* ctx, const cha
   else if (k == "device-address-bits") *value = 64;
   else return fail(ctx, TILER_HIP_REFUSE_UNRECOGNIZED_KEY, "unrecognized live-device key " + k);
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_prepare_entries(tiler_hip_context* ctx,
                                            const tiler_hip_routed_entry* entries, uint32_t count,
-                                           uint32_t* first_index) {
+                                           uint32_t* first_index) try {
   if (!ctx || (count && !entries)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipSetDevice(ctx->device);
   std::vector<hipModule_t> loaded;
@@ -893,10 +919,12 @@ tiler_hip_status tiler_hip_prepare_entries(tiler_hip_context* ctx,
   ctx->routed_modules.insert(ctx->routed_modules.end(), loaded.begin(), loaded.end());
   ctx->prepared.insert(ctx->prepared.end(), fns.begin(), fns.end());
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_observe_prepared_entry(tiler_hip_context* ctx, uint32_t prepared,
-                                                  const char* key, uint64_t* value) {
+                                                  const char* key, uint64_t* value) try {
   if (!ctx || !key || !value) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (prepared >= ctx->prepared.size())
     return fail(ctx, TILER_HIP_REFUSE_NOT_PREPARED, "entry not prepared");
@@ -912,10 +940,12 @@ tiler_hip_status tiler_hip_observe_prepared_entry(tiler_hip_context* ctx, uint32
     return fail(ctx, TILER_HIP_REFUSE_NOT_PREPARED, "hipFuncGetAttribute failed");
   *value = (uint64_t)v;
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_plan_dispatch(tiler_hip_context* ctx,
-                                         const tiler_hip_dispatch_plan* plan) {
+                                         const tiler_hip_dispatch_plan* plan) try {
   if (!ctx || !plan || (plan->entry_count && !plan->entries) ||
       (plan->slot_count && !plan->slot_bytes))
     return TILER_HIP_REFUSE_INVALID_ARGUMENT;
@@ -948,11 +978,13 @@ tiler_hip_status tiler_hip_plan_dispatch(tiler_hip_context* ctx,
     }
   }
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_allocate_dispatch(tiler_hip_context* ctx,
                                              const tiler_hip_dispatch_plan* plan,
-                                             void** slot_pointers) {
+                                             void** slot_pointers) try {
   if (!ctx || !plan || (plan->slot_count && !slot_pointers)) return TILER_HIP_FAIL_ALLOCATION;
   hipSetDevice(ctx->device);
   for (uint32_t s = 0; s < plan->slot_count; ++s) {
@@ -964,10 +996,12 @@ tiler_hip_status tiler_hip_allocate_dispatch(tiler_hip_context* ctx,
     slot_pointers[s] = p;
   }
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_dispatch_plan* plan,
-                                    void* const* slot_pointers) {
+                                    void* const* slot_pointers) try {
   if (!ctx || !plan) return TILER_HIP_FAIL_LAUNCH;
   hipSetDevice(ctx->device);
   // Constant slots first (an expression's register program), ordered on the
@@ -1001,11 +1035,13 @@ tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_disp
   hipError_t err = hipStreamSynchronize(ctx->stream);
   if (err != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, hipGetErrorString(err));
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_FAIL_ALLOCATION;
 }
 
 tiler_hip_status tiler_hip_release_dispatch(tiler_hip_context* ctx,
                                             const tiler_hip_dispatch_plan* plan,
-                                            void** slot_pointers, const void** caller_owned) {
+                                            void** slot_pointers, const void** caller_owned) try {
   if (!ctx || !plan) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipSetDevice(ctx->device);
   for (uint32_t s = 0; s < plan->slot_count; ++s) {
@@ -1014,25 +1050,31 @@ tiler_hip_status tiler_hip_release_dispatch(tiler_hip_context* ctx,
     slot_pointers[s] = nullptr;
   }
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // ---------------------------------------------------------------------------
-tiler_hip_status tiler_hip_buffer_alloc(tiler_hip_context* ctx, uint64_t bytes, void** out) {
+tiler_hip_status tiler_hip_buffer_alloc(tiler_hip_context* ctx, uint64_t bytes, void** out) try {
   if (!ctx || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipSetDevice(ctx->device);
   *out = nullptr;
   if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess)
     return fail(ctx, TILER_HIP_FAIL_ALLOCATION, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
-tiler_hip_status tiler_hip_buffer_free(tiler_hip_context* ctx, void* ptr) {
+tiler_hip_status tiler_hip_buffer_free(tiler_hip_context* ctx, void* ptr) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipSetDevice(ctx->device);
   if (ptr && hipFree(ptr) != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, "hipFree failed");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_status tiler_hip_upload(tiler_hip_context* ctx, void* dst, const void* src,
-                                  uint64_t bytes) {
+                                  uint64_t bytes) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (bytes == 0) return TILER_HIP_OK;
   hipSetDevice(ctx->device);
@@ -1040,9 +1082,11 @@ tiler_hip_status tiler_hip_upload(tiler_hip_context* ctx, void* dst, const void*
       hipStreamSynchronize(ctx->stream) != hipSuccess)
     return fail(ctx, TILER_HIP_FAIL_TRANSFER, "host-to-device copy failed");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_status tiler_hip_download(tiler_hip_context* ctx, void* dst, const void* src,
-                                    uint64_t bytes) {
+                                    uint64_t bytes) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (bytes == 0) return TILER_HIP_OK;
   hipSetDevice(ctx->device);
@@ -1050,59 +1094,75 @@ tiler_hip_status tiler_hip_download(tiler_hip_context* ctx, void* dst, const voi
       hipStreamSynchronize(ctx->stream) != hipSuccess)
     return fail(ctx, TILER_HIP_FAIL_TRANSFER, "device-to-host copy failed");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_status tiler_hip_fill_u32(tiler_hip_context* ctx, void* dst, uint32_t value,
-                                    uint64_t words, tiler_hip_stream stream) {
+                                    uint64_t words, tiler_hip_stream stream) try {
   if (!ctx || (words && !dst)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (words == 0) return TILER_HIP_OK;
   uint64_t groups = (words + 255) / 256;
   if (groups > 4096) groups = 4096;
   void* args[] = {&dst, &value, &words};
   return launch(ctx, "tiler_fill_u32", (uint32_t)groups, 1, 256, pick(ctx, stream), args);
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_status tiler_hip_copy(tiler_hip_context* ctx, void* dst, const void* src, uint64_t bytes,
-                                tiler_hip_stream stream) {
+                                tiler_hip_stream stream) try {
   if (!ctx || (bytes && (!dst || !src))) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (bytes == 0) return TILER_HIP_OK;
   if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, pick(ctx, stream)) != hipSuccess)
     return fail(ctx, TILER_HIP_FAIL_TRANSFER, "device-to-device copy failed");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
-tiler_hip_status tiler_hip_synchronize(tiler_hip_context* ctx) {
+tiler_hip_status tiler_hip_synchronize(tiler_hip_context* ctx) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, hipGetErrorString(e));
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_stream tiler_hip_context_stream(tiler_hip_context* ctx) {
   return ctx ? static_cast<tiler_hip_stream>(ctx->stream) : nullptr;
 }
-tiler_hip_status tiler_hip_event_create(tiler_hip_context* ctx, tiler_hip_event* out) {
+tiler_hip_status tiler_hip_event_create(tiler_hip_context* ctx, tiler_hip_event* out) try {
   if (!ctx || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipEvent_t e = nullptr;
   if (hipEventCreate(&e) != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, "hipEventCreate failed");
   *out = e;
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_status tiler_hip_event_record(tiler_hip_context* ctx, tiler_hip_event ev,
-                                        tiler_hip_stream stream) {
+                                        tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (hipEventRecord(static_cast<hipEvent_t>(ev), pick(ctx, stream)) != hipSuccess)
     return fail(ctx, TILER_HIP_FAIL_DEVICE, "hipEventRecord failed");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_status tiler_hip_event_elapsed_ms(tiler_hip_context* ctx, tiler_hip_event start,
-                                            tiler_hip_event stop, float* ms) {
+                                            tiler_hip_event stop, float* ms) try {
   if (!ctx || !ms) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (hipEventSynchronize(static_cast<hipEvent_t>(stop)) != hipSuccess ||
       hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)) != hipSuccess)
     return fail(ctx, TILER_HIP_FAIL_DEVICE, "hipEventElapsedTime failed");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
-tiler_hip_status tiler_hip_event_destroy(tiler_hip_context* ctx, tiler_hip_event ev) {
+tiler_hip_status tiler_hip_event_destroy(tiler_hip_context* ctx, tiler_hip_event ev) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipEventDestroy(static_cast<hipEvent_t>(ev));
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 struct GraphHandle {
@@ -1110,14 +1170,16 @@ struct GraphHandle {
   hipGraphExec_t exec = nullptr;
 };
 
-tiler_hip_status tiler_hip_capture_begin(tiler_hip_context* ctx, tiler_hip_stream stream) {
+tiler_hip_status tiler_hip_capture_begin(tiler_hip_context* ctx, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipError_t e = hipStreamBeginCapture(pick(ctx, stream), hipStreamCaptureModeThreadLocal);
   if (e != hipSuccess) return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED, std::string("capture: ") + hipGetErrorString(e));
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_status tiler_hip_capture_end(tiler_hip_context* ctx, tiler_hip_stream stream,
-                                       tiler_hip_graph* out) {
+                                       tiler_hip_graph* out) try {
   if (!ctx || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   auto* g = new GraphHandle();
   hipError_t e = hipStreamEndCapture(pick(ctx, stream), &g->graph);
@@ -1129,15 +1191,19 @@ tiler_hip_status tiler_hip_capture_end(tiler_hip_context* ctx, tiler_hip_stream 
   }
   *out = g;
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 tiler_hip_status tiler_hip_graph_launch(tiler_hip_context* ctx, tiler_hip_graph graph,
-                                        tiler_hip_stream stream) {
+                                        tiler_hip_stream stream) try {
   if (!ctx || !graph) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipError_t e = hipGraphLaunch(static_cast<GraphHandle*>(graph)->exec, pick(ctx, stream));
   if (e != hipSuccess) return fail(ctx, TILER_HIP_FAIL_LAUNCH, std::string("graph launch: ") + hipGetErrorString(e));
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
-tiler_hip_status tiler_hip_graph_destroy(tiler_hip_context* ctx, tiler_hip_graph graph) {
+tiler_hip_status tiler_hip_graph_destroy(tiler_hip_context* ctx, tiler_hip_graph graph) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   auto* g = static_cast<GraphHandle*>(graph);
   if (g) {
@@ -1146,11 +1212,13 @@ tiler_hip_status tiler_hip_graph_destroy(tiler_hip_context* ctx, tiler_hip_graph
     delete g;
   }
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // ---------------------------------------------------------------------------
 tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_t extent,
-                                        uint32_t* vec, uint32_t* waves, uint64_t* segment) {
+                                        uint32_t* vec, uint32_t* waves, uint64_t* segment) try {
   if (!vec || !waves || !segment) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   *segment = 0;
   switch (family) {
@@ -1173,6 +1241,8 @@ tiler_hip_status tiler_hip_row_grouping(uint32_t family, uint32_t dtype, uint64_
     default:
       return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   }
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context* ctx, uint64_t n) {
@@ -1181,7 +1251,7 @@ uint32_t tiler_hip_sum_tree_workgroups(const tiler_hip_context* ctx, uint64_t n)
 
 tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint64_t rows,
                                    uint64_t extent, float* out, const tiler_hip_sum_plan* plan,
-                                   tiler_hip_stream stream) {
+                                   tiler_hip_stream stream) try {
   if (!ctx || !plan || (rows && !out) || (rows && extent && !x))
     return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
@@ -1207,11 +1277,13 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
   st = run_program(ctx, p, slots, s);
   if (own) hipFreeAsync(slots[2], s);
   return st;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_sum_f32_noalloc(tiler_hip_context* ctx, const float* x, uint64_t rows,
                                            uint64_t extent, float* out, const tiler_hip_sum_plan* plan,
-                                           tiler_hip_stream stream) {
+                                           tiler_hip_stream stream) try {
   if (!ctx || !plan || (rows && !out) || (rows && extent && !x))
     return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
@@ -1233,12 +1305,14 @@ tiler_hip_status tiler_hip_sum_f32_noalloc(tiler_hip_context* ctx, const float* 
     slots[2] = ctx->noalloc_scratch;
   }
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, const void* x,
                                     const void* w, int32_t weight_broadcast, uint64_t rows,
                                     uint64_t extent, uint32_t eps_bits, void* y,
-                                    tiler_hip_stream stream) {
+                                    tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   const uintptr_t addr[3] = {(uintptr_t)x, (uintptr_t)w, (uintptr_t)y};
@@ -1247,10 +1321,12 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, cons
   if (p.nlaunches && (!x || !w || !y)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(x), const_cast<void*>(w), y};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, uint64_t rows,
-                                       uint64_t extent, float* y, tiler_hip_stream stream) {
+                                       uint64_t extent, float* y, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   const uintptr_t addr[2] = {(uintptr_t)x, (uintptr_t)y};
@@ -1284,11 +1360,13 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
   st = run_program(ctx, p, slots, s);
   if (own) hipFreeAsync(part, s);
   return st;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_map(tiler_hip_context* ctx, uint32_t op, uint32_t dtype,
                                const void* x, const void* x2, int32_t x2_broadcast, uint64_t n,
-                               float a, float b, void* y, tiler_hip_stream stream) {
+                               float a, float b, void* y, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   const bool binary = op == TILER_HIP_MAP_ADD || op == TILER_HIP_MAP_MULTIPLY;
   tiler_rt::Program p;
@@ -1298,12 +1376,14 @@ tiler_hip_status tiler_hip_map(tiler_hip_context* ctx, uint32_t op, uint32_t dty
   if (p.nlaunches && (!x || !y || (binary && !x2))) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(x), binary ? const_cast<void*>(x2) : y, y};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_broadcast(tiler_hip_context* ctx, const void* src, uint64_t src_elements,
                                      uint32_t rank, const uint64_t* out_dims,
                                      const uint64_t* src_strides, uint32_t element_bytes, void* out,
-                                     tiler_hip_stream stream) {
+                                     tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   tiler_hip_status st = tiler_rt::plan_broadcast(src_elements, rank, out_dims, src_strides, element_bytes, p);
@@ -1311,10 +1391,12 @@ tiler_hip_status tiler_hip_broadcast(tiler_hip_context* ctx, const void* src, ui
   if (p.nlaunches && (!src || !out)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(src), out};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_convert(tiler_hip_context* ctx, uint32_t direction, const void* src,
-                                   uint64_t n, void* dst, tiler_hip_stream stream) {
+                                   uint64_t n, void* dst, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   const uintptr_t addr[2] = {(uintptr_t)src, (uintptr_t)dst};
@@ -1323,11 +1405,13 @@ tiler_hip_status tiler_hip_convert(tiler_hip_context* ctx, uint32_t direction, c
   if (p.nlaunches && (!src || !dst)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(src), dst};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_validate_gather_index(const uint32_t* index, uint64_t count,
                                                  int32_t index_signed, uint64_t gathered,
-                                                 uint64_t* bad_position, int64_t* bad_value) {
+                                                 uint64_t* bad_position, int64_t* bad_value) try {
   if (count && !index) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   for (uint64_t i = 0; i < count; ++i) {
     int64_t v = index_signed ? (int64_t)(int32_t)index[i] : (int64_t)index[i];
@@ -1338,12 +1422,14 @@ tiler_hip_status tiler_hip_validate_gather_index(const uint32_t* index, uint64_t
     }
   }
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_gather(tiler_hip_context* ctx, const void* source, uint64_t outer,
                                   uint64_t gathered, uint64_t inner, uint32_t element_bytes,
                                   const uint32_t* index, uint64_t count, int32_t index_signed,
-                                  void* out, tiler_hip_stream stream) {
+                                  void* out, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   const uintptr_t addr[4] = {(uintptr_t)source, (uintptr_t)index, (uintptr_t)out, 0};
@@ -1354,10 +1440,12 @@ tiler_hip_status tiler_hip_gather(tiler_hip_context* ctx, const void* source, ui
   void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(source), const_cast<uint32_t*>(index), out,
                                       ctx->gather_bad};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_gather_status(tiler_hip_context* ctx, tiler_hip_stream stream,
-                                         uint64_t* bad_position) {
+                                         uint64_t* bad_position) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   hipStream_t s = pick(ctx, stream);
   unsigned long long v = 0;
@@ -1370,11 +1458,13 @@ tiler_hip_status tiler_hip_gather_status(tiler_hip_context* ctx, tiler_hip_strea
   hipStreamSynchronize(s);
   return fail(ctx, TILER_HIP_FAIL_GATHER_INDEX_OUT_OF_BOUNDS,
               "gather index out of bounds at position " + std::to_string(v));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_contract_strict_f32(tiler_hip_context* ctx, const float* a,
                                                const float* b, uint64_t m, uint64_t n,
-                                               uint64_t k, float* c, tiler_hip_stream stream) {
+                                               uint64_t k, float* c, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   tiler_hip_status st = tiler_rt::plan_contract_strict_f32(m, n, k, p);
@@ -1382,12 +1472,14 @@ tiler_hip_status tiler_hip_contract_strict_f32(tiler_hip_context* ctx, const flo
   if (p.nlaunches && (!a || !b || !c)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(a), const_cast<float*>(b), c};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t* a,
                                          const uint16_t* b, uint64_t m, uint64_t n, uint64_t k,
                                          uint16_t* c, uint32_t epilogue,
-                                         tiler_hip_stream stream) {
+                                         tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   const uintptr_t addr[3] = {(uintptr_t)a, (uintptr_t)b, (uintptr_t)c};
@@ -1396,6 +1488,8 @@ tiler_hip_status tiler_hip_contract_bf16(tiler_hip_context* ctx, const uint16_t*
   if (p.nlaunches && (!a || !b || !c)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<uint16_t*>(a), const_cast<uint16_t*>(b), c};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // A program's CONSTANT slot contents (an expression's register program, a
@@ -1423,7 +1517,7 @@ tiler_hip_status resident_constant(tiler_hip_context* ctx, const tiler_rt::Progr
 tiler_hip_status tiler_hip_contract(tiler_hip_context* ctx, uint32_t dtype,
                                     const tiler_hip_contraction_structure* structure, uint32_t epilogue,
                                     uint32_t permissions, const void* left, const void* right, void* out,
-                                    tiler_hip_stream stream) {
+                                    tiler_hip_stream stream) try {
   if (!ctx || !structure) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   if (permissions & ~(uint32_t)(TILER_HIP_PERMITS_REASSOCIATION | TILER_HIP_PERMITS_PERMUTATION))
     return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "unknown permission bits");
@@ -1451,6 +1545,8 @@ tiler_hip_status tiler_hip_contract(tiler_hip_context* ctx, uint32_t dtype,
   st = run_program(ctx, p, slots, s);
   if (own) hipFreeAsync(slots[3], s);
   return st;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -1458,7 +1554,7 @@ tiler_hip_status tiler_hip_expression(tiler_hip_context* ctx, uint32_t dtype,
                                       const tiler_hip_expression_node* nodes, uint32_t node_count,
                                       uint32_t root, const void* const* inputs, uint64_t n, void* y,
                                       uint32_t input_subnormals, uint32_t result_subnormals,
-                                      tiler_hip_stream stream) {
+                                      tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::ExpressionProgram prog;
   std::string diag;
@@ -1494,11 +1590,13 @@ tiler_hip_status tiler_hip_expression(tiler_hip_context* ctx, uint32_t dtype,
   st = run_program(ctx, p, slots, s);
   if (own) hipFreeAsync(slots[prog.inputs + 2], s);
   return st;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_fold_f32(tiler_hip_context* ctx, uint32_t variant, const float* x, uint32_t rank,
                                     const uint64_t* dims, uint64_t reduced_mask, uint32_t scale_bits,
-                                    uint32_t bias_bits, float* out, tiler_hip_stream stream) {
+                                    uint32_t bias_bits, float* out, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   tiler_hip_status st = tiler_rt::plan_fold(variant, rank, dims, reduced_mask, scale_bits, bias_bits, nullptr, p);
@@ -1506,11 +1604,13 @@ tiler_hip_status tiler_hip_fold_f32(tiler_hip_context* ctx, uint32_t variant, co
   if (p.nlaunches && (!x || !out)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(x), out};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_reindex(tiler_hip_context* ctx, const void* src, uint64_t src_elements, uint32_t rank,
                                    const uint64_t* out_dims, const int64_t* strides, int64_t base,
-                                   uint32_t element_bytes, void* out, tiler_hip_stream stream) {
+                                   uint32_t element_bytes, void* out, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   tiler_hip_status st = tiler_rt::plan_reindex(src_elements, rank, out_dims, strides, base, element_bytes, p);
@@ -1518,6 +1618,8 @@ tiler_hip_status tiler_hip_reindex(tiler_hip_context* ctx, const void* src, uint
   if (p.nlaunches && (!src || !out)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(src), out};
   return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -1546,7 +1648,7 @@ std::vector<uint8_t> environment_descriptor(bool sramecc, bool xnack) {
 
 }  // namespace
 
-tiler_hip_status tiler_hip_target_environment_support(tiler_hip_target_environment_schema* out) {
+tiler_hip_status tiler_hip_target_environment_support(tiler_hip_target_environment_schema* out) try {
   if (!out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   std::memset(out, 0, sizeof(*out));
   copy_text(out->provider, sizeof(out->provider), kEnvironmentProvider);
@@ -1554,10 +1656,12 @@ tiler_hip_status tiler_hip_target_environment_support(tiler_hip_target_environme
   out->schema_major = 1;
   out->schema_minor = 0;
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_validate_target_environment(const void* descriptor, uint64_t bytes, char* diagnostic,
-                                                       uint64_t diagnostic_bytes) {
+                                                       uint64_t diagnostic_bytes) try {
   if (!descriptor && bytes) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   const uint8_t* d = static_cast<const uint8_t*>(descriptor);
   auto refuse = [&](const char* what) {
@@ -1579,11 +1683,13 @@ tiler_hip_status tiler_hip_validate_target_environment(const void* descriptor, u
     }
   if (id.rfind(kTargetIdPrefix, 0) != 0) return refuse("target ID is not amdgcn-amd-amdhsa--gfx950");
   return refuse("target ID features are not the canonical :sramecc(+|-):xnack(+|-) spelling");
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 tiler_hip_status tiler_hip_observe_target_environment(tiler_hip_context* ctx, uint8_t* descriptor,
                                                       uint64_t capacity, uint64_t* required, uint32_t* observed,
-                                                      char* reason, uint64_t reason_bytes) {
+                                                      char* reason, uint64_t reason_bytes) try {
   if (!ctx || !observed) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   *observed = 0;
   if (required) *required = 0;
@@ -1608,6 +1714,8 @@ tiler_hip_status tiler_hip_observe_target_environment(tiler_hip_context* ctx, ui
   *observed = 1;
   copy_text(reason, reason_bytes, "");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -1768,7 +1876,7 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
 
 tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip_region* r,
                                    tiler_hip_realization* out, char* diagnostic,
-                                   uint64_t diagnostic_bytes) {
+                                   uint64_t diagnostic_bytes) try {
   if (!r || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   std::memset(out, 0, sizeof(*out));
   tiler_rt::Program p;
@@ -1806,6 +1914,8 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
   }
   out->entry_count = p.nlaunches;
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -1940,7 +2050,7 @@ struct Offer {
 }  // namespace
 
 tiler_hip_status tiler_hip_propose(const tiler_hip_context* ctx, const tiler_hip_region* r,
-                                   tiler_hip_provider_offer* out, char* diagnostic, uint64_t diagnostic_bytes) {
+                                   tiler_hip_provider_offer* out, char* diagnostic, uint64_t diagnostic_bytes) try {
   if (!r || !out) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   std::memset(out, 0, sizeof(*out));
   copy_text(out->provider, sizeof(out->provider), "tiler.hip.gfx950-physical-provider");
@@ -2081,6 +2191,8 @@ tiler_hip_status tiler_hip_propose(const tiler_hip_context* ctx, const tiler_hip
   out->chosen = chosen >= 0 ? (uint32_t)chosen : 0;
   copy_text(diagnostic, diagnostic_bytes, "");
   return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
 }
 
 }  // extern "C"
