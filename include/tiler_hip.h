@@ -377,7 +377,22 @@ typedef struct {
     uint32_t binding_count;    /* buffer bindings patched into kernargs */
     const uint32_t *binding_slots;   /* slot of each binding */
     const uint32_t *binding_offsets; /* byte offset of its pointer in kernargs */
+    uint32_t extent_count;     /* live extents patched into kernargs (32-bit fields) */
+    const uint32_t *extent_ids;      /* which of the plan's live extents */
+    const uint32_t *extent_offsets;  /* byte offset of its field in kernargs */
 } tiler_hip_dispatch_entry;
+
+/* One live input-axis extent a realization reads at dispatch
+ * (InputExtentParameter, tiler-ir/src/kernel/model.rs:375-390; the
+ * LiveContraction topology's contracted trip count, schedule/model.rs:1429-1450):
+ * the extent of axis `axis` of input access `access`, which must lie in
+ * [minimum, bound] -- `bound` is what the realization's slot sizes hold. */
+typedef struct {
+    uint32_t access;
+    uint32_t axis;
+    uint64_t minimum;
+    uint64_t bound;
+} tiler_hip_live_extent;
 
 typedef struct {
     uint32_t slot_count;
@@ -388,6 +403,11 @@ typedef struct {
      * tiler_hip_dispatch uploads into the slot before the first entry runs --
      * a realization's CONSTANT slot.  NULL entries are left alone. */
     const void *const *slot_contents;
+    /* The live extents' values for this dispatch (NULL with count 0: none),
+     * and optionally (NULL: unchecked) the range each must lie in. */
+    uint32_t extent_count;
+    const uint64_t *extents;
+    const tiler_hip_live_extent *extent_ranges;
 } tiler_hip_dispatch_plan;
 
 /* plan_dispatch (adapter.rs:453): sizes and checks the route against the
@@ -767,6 +787,9 @@ tiler_hip_status tiler_hip_contract(tiler_hip_context *ctx, uint32_t dtype,
 #define TILER_HIP_REGION_OPERAND_BROADCAST 2u /* pointwise: x2 is one element; rms_norm: w is one row */
 #define TILER_HIP_REGION_INDEX_SIGNED 4u      /* gather: int32 indices */
 #define TILER_HIP_REGION_PARTICIPANT_MAJOR 8u /* cooperative sum layout */
+#define TILER_HIP_REGION_LIVE_EXTENT 16u      /* contraction td,od->to: k is live (LiveContraction), read at
+                                                 dispatch as the realization's live extent 0 (input 0, axis 1);
+                                                 extents[2] is its bound */
 
 /* The plan's numerical contract as it reaches one region: the permissions
  * its ReductionTopology carries (permits_reassociation, permits_permutation;
@@ -870,6 +893,9 @@ typedef struct {
     uint32_t binding_count;
     uint32_t binding_slots[18];
     uint32_t binding_offsets[18];
+    uint32_t extent_count;      /* live extents this entry reads (tiler_hip_dispatch_entry) */
+    uint32_t extent_ids[2];
+    uint32_t extent_offsets[2];
 } tiler_hip_realized_entry;
 
 typedef struct {
@@ -882,6 +908,8 @@ typedef struct {
     uint32_t constant_slot;     /* the CONSTANT slot (slot_count when there is none) */
     uint32_t constant_bytes;    /* its contents: constant[0 .. constant_bytes) */
     uint8_t constant[TILER_HIP_REALIZATION_CONSTANT_BYTES];
+    uint32_t live_extent_count; /* REGION_LIVE_EXTENT: the extents the dispatch supplies, by id */
+    tiler_hip_live_extent live_extents[2];
 } tiler_hip_realization;
 
 /* Refuses (pre-commit, typed) what the family entry point would refuse for

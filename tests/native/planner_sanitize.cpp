@@ -133,7 +133,17 @@ static void check(const Program& p) {
         std::printf("bad binding in %s\n", l.symbol);
         std::exit(1);
       }
+    for (uint32_t x = 0; x < l.nextents; ++x)
+      if (l.extents[x].id >= p.nlive || l.extents[x].offset + 4 > l.kernarg_bytes || l.extents[x].offset % 4) {
+        std::printf("bad live extent in %s\n", l.symbol);
+        std::exit(1);
+      }
   }
+  for (uint32_t x = 0; x < p.nlive; ++x)
+    if (p.live[x].minimum < 1 || p.live[x].minimum > p.live[x].bound) {
+      std::printf("empty live extent range\n");
+      std::exit(1);
+    }
 }
 
 int main() {
@@ -164,9 +174,9 @@ int main() {
     plan_broadcast(pick(r), (uint32_t)(r() % 10) % 9, dims, strides, (uint32_t)(r() % 6), p[4]);
     plan_gather(mode, pick(r), pick(r), pick(r), (uint32_t)(r() % 17), pick(r), (int32_t)(r() % 2), addr, p[5]);
     plan_convert(mode, (uint32_t)(r() % 3), pick(r), addr, p[6]);
-    plan_contract_strict_f32(pick(r), pick(r), pick(r), p[7]);
+    plan_contract_strict_f32(pick(r), pick(r), pick(r), p[7], r() % 2 == 0);
     plan_contract_bf16(t, pick(r), pick(r), pick(r), (uint32_t)(r() % 3), addr, p[8], r() % 4 == 0,
-                       (uint32_t)(r() % 6));
+                       (uint32_t)(r() % 6), r() % 3 == 0);
     for (int i = 0; i < 9; ++i) {
       check(p[i]);
       planned += p[i].nlaunches;

@@ -195,3 +195,76 @@ def test_route_refuses_before_commit(ctx):
             route(ctx, rz, [x])                         # one binding per slot
     finally:
         x.free(); small.free()
+
+
+LIVE = L.REGION_ALIGNED16 | L.REGION_LIVE_EXTENT
+
+
+def _route_live(ctx, rz, bufs, a, b, k, out_dtype, m, n):
+    """Routes one live-k realization with A [m, k] and B [n, k] packed at the
+    start of bound-sized slots; returns C [m, n]."""
+    bufs[0].upload(np.ascontiguousarray(a))
+    bufs[1].upload(np.ascontiguousarray(b))
+    print(f"[live k] {rz.symbols} m={m} n={n} k={k}", flush=True)
+    route(ctx, rz, bufs, extents=(k,))
+    return bufs[2].download(out_dtype, (m, n))
+
+
+@pytest.mark.parametrize("dtype,variant,permissions", [
+    (L.F32, L.EPILOGUE_NONE, 0),                                   # the strict f32 fold
+    (L.BF16, L.EPILOGUE_SILU, 0),                                  # strict bf16 fold, then SiLU
+    (L.BF16, L.EPILOGUE_SILU, L.PERMITS_REASSOCIATION),            # the general MFMA form
+    (L.BF16, L.EPILOGUE_NONE, L.PERMITS_REASSOCIATION),
+])
+def test_live_contracted_extent_routes_every_value(ctx, dtype, variant, permissions):
+    """One realization (LiveContraction: k read at dispatch) routed at several
+    k up to the bound it was sized for, each result against the oracle at
+    that k: the strict folds bit for bit, the MFMA form within 1e-2 relative
+    Frobenius of the f64 contraction of the widened operands."""
+    m, n, bound = 300, 264, 200
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, bound), dtype=dtype, variant=variant, permissions=permissions,
+                 flags=LIVE, ctx=ctx)
+    assert rz.live_extents == [(0, 1, 1, bound)]
+    bufs = [ctx.alloc(nbytes) for _, nbytes in rz.slots]
+    try:
+        for k in (1, 7, 64, 131, bound):
+            rng = np.random.default_rng(k)
+            a = rng.standard_normal((m, k)).astype(np.float32)
+            b = rng.standard_normal((n, k)).astype(np.float32)
+            if dtype == L.F32:
+                got = _route_live(ctx, rz, bufs, a, b, k, np.float32, m, n)
+                assert np.array_equal(bits(got).reshape(-1), bits(oracle.contract_strict_f32(a, b, m, n, k)).reshape(-1)), k
+                continue
+            a16, b16 = oracle.bf16_narrow(a), oracle.bf16_narrow(b)
+            got = _route_live(ctx, rz, bufs, a16, b16, k, np.uint16, m, n)
+            if not permissions:
+                want = oracle.contract_general(a16, "mk", b16, "nk", "mn", silu=variant == L.EPILOGUE_SILU)
+                assert np.array_equal(got, want), k
+                continue
+            wide = bf16_widen(a16).astype(np.float64) @ bf16_widen(b16).astype(np.float64).T
+            if variant == L.EPILOGUE_SILU:
+                wide = oracle.silu_f32(wide.astype(np.float32).reshape(-1)).reshape(m, n).astype(np.float64)
+            g = bf16_widen(got).astype(np.float64)
+            assert np.linalg.norm(g - wide) / np.linalg.norm(wide) <= 1e-2, k
+    finally:
+        for x in bufs:
+            x.free()
+
+
+def test_live_extent_outside_its_range_is_refused_before_commit(ctx):
+    m, n, bound = 40, 70, 64
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, bound), flags=LIVE, ctx=ctx)
+    bufs = [ctx.alloc(nbytes) for _, nbytes in rz.slots]
+    try:
+        for k in (0, bound + 1, 1 << 32):
+            with pytest.raises(Refusal) as e:
+                route(ctx, rz, bufs, extents=(k,))
+            assert e.value.status == L.REFUSE_CAPACITY, k
+        with pytest.raises(Refusal) as e:
+            route(ctx, rz, bufs)                        # the live extent's value is not supplied
+        assert e.value.status == L.REFUSE_BINDING_MISMATCH
+        with pytest.raises(Refusal):
+            route(ctx, realize(L.PROGRAM_CONTRACTION, (m, n, bound), ctx=ctx), bufs, extents=(3,))
+    finally:
+        for x in bufs:
+            x.free()

@@ -154,6 +154,80 @@ def test_contraction_paths():
     _check_segments(strict)
 
 
+LIVE = L.REGION_ALIGNED16 | L.REGION_LIVE_EXTENT
+
+
+def test_live_contracted_extent():
+    """LiveContraction (tiler-ir/src/schedule/model.rs:1429-1450): k is an
+    input-axis extent read at dispatch (InputExtentParameter, kernel/model.rs:
+    375-390).  The realization sizes its slots for the bound, declares live
+    extent 0 as input 0's axis 1 in [1, bound], and leaves the k field of the
+    argument segment for the dispatch to patch."""
+    m, n, bound = 40, 70, 512
+    f = realize(L.PROGRAM_CONTRACTION, (m, n, bound), flags=LIVE)
+    assert f.symbols == ["tiler_contract_strict_f32"]
+    assert f.live_extents == [(0, 1, 1, bound)]
+    assert [s for s, _ in f.slots] == [L.SLOT_INPUT, L.SLOT_INPUT, L.SLOT_OUTPUT]
+    assert [b for _, b in f.slots] == [m * bound * 4, n * bound * 4, m * n * 4]
+    # a, b, m, n, k, c: the k field follows the two pointers and m, n
+    assert f.dispatches[0].extents == [(0, 24)]
+    assert bytes(f.raw.entries[0].kernargs[16:28]) == struct.pack("<III", m, n, 0)
+    _check_segments(f)
+    assert realize(L.PROGRAM_CONTRACTION, (m, n, bound)).live_extents == []
+    # bf16: the MFMA path takes the general form, whatever the bound's alignment
+    for variant, symbol in ((L.EPILOGUE_NONE, "tiler_contract_bf16_g128_k"),
+                            (L.EPILOGUE_SILU, "tiler_contract_bf16_silu_g128_k")):
+        b = realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, permissions=RE, variant=variant,
+                    flags=LIVE)
+        assert b.symbols == [symbol] and b.live_extents == [(0, 1, 1, 4096)]
+        assert b.dispatches[0].extents == [(0, 24)]
+        _check_segments(b)
+    g = realize(L.PROGRAM_CONTRACTION, (300, 264, 192), dtype=L.BF16, permissions=RE, flags=LIVE,
+                form=L.FORM_CONTRACT_GENERAL_128)
+    assert g.symbols == ["tiler_contract_bf16_g128_k"]
+    s = realize(L.PROGRAM_CONTRACTION, (300, 264, 192), dtype=L.BF16, variant=L.EPILOGUE_SILU, flags=LIVE)
+    assert s.symbols == ["tiler_contract_strict_bf16_silu"] and s.dispatches[0].extents == [(0, 24)]
+    # zero work still declares the extent (the route supplies it and skips the dispatch)
+    z = realize(L.PROGRAM_CONTRACTION, (0, 64, 64), dtype=L.BF16, flags=LIVE)
+    assert z.raw.entry_count == 0 and z.live_extents == [(0, 1, 1, 64)]
+
+
+@pytest.mark.parametrize("kwargs,status,rule", [
+    (dict(program=L.PROGRAM_CONTRACTION, extents=(300, 264, 192), dtype=L.BF16, permissions=RE,
+          form=L.FORM_CONTRACT_STAGED_256), L.REFUSE_UNSUPPORTED, "live-extent"),
+    (dict(program=L.PROGRAM_CONTRACTION, extents=(16, 264, 192), dtype=L.BF16, permissions=RE,
+          form=L.FORM_CONTRACT_SKINNY), L.REFUSE_UNSUPPORTED, "live-extent"),
+    (dict(program=L.PROGRAM_CONTRACTION, extents=(), dtype=L.F32,
+          structure=L.contraction_structure("bhqd", (2, 2, 3, 4), "bkd", (2, 5, 4), "bhqk")),
+     L.REFUSE_UNSUPPORTED, "live-extent"),
+    (dict(program=L.PROGRAM_SOFTMAX, extents=(4, 64)), L.REFUSE_UNSUPPORTED, "live-extent"),
+    (dict(program=L.PROGRAM_CONTRACTION, extents=(4, 4, 0)), L.REFUSE_INVALID_ARGUMENT, None),
+])
+def test_live_extent_refusals(kwargs, status, rule):
+    program, extents = kwargs.pop("program"), kwargs.pop("extents")
+    with pytest.raises(Refusal) as e:
+        realize(program, extents, flags=LIVE, **kwargs)
+    assert e.value.status == status
+    if rule is not None:
+        assert e.value.diagnostic.startswith(rule + ":"), e.value.diagnostic
+
+
+def test_live_extent_provider_offer():
+    """With k live only the general MFMA form runs: the provider declines the
+    skinny and staged forms by that rule and chooses the general form."""
+    from tiler_amd.realize import propose
+    offer = propose(L.PROGRAM_CONTRACTION, (300, 264, 192), dtype=L.BF16, variant=L.EPILOGUE_SILU,
+                    permissions=RE, flags=LIVE)
+    assert offer.strategies() == ["tiler.region.serial-baseline", "gfx950.contraction.mfma-general-128"]
+    assert {(d.strategy, d.subject) for d in offer.declined} == {
+        ("gfx950.contraction.mfma-skinny", "live-extent"),
+        ("gfx950.contraction.mfma-staged-256", "live-extent"),
+        ("gfx950.contraction.mfma-staged-128", "live-extent")}
+    assert offer.chosen == 1
+    for p in offer.proposals:
+        assert p.realize().live_extents == [(0, 1, 1, 192)]
+
+
 def test_moves_and_maps():
     g = realize(L.PROGRAM_GATHER, (1, 128256, 4096, 16384), variant=2)
     assert g.symbols == ["tiler_fill_u32", "tiler_gather_u128"]

@@ -103,6 +103,7 @@ REGION_ALIGNED16 = 1
 REGION_OPERAND_BROADCAST = 2
 REGION_INDEX_SIGNED = 4
 REGION_PARTICIPANT_MAJOR = 8
+REGION_LIVE_EXTENT = 16
 
 SLOT_INPUT = 0
 SLOT_OUTPUT = 1
@@ -110,6 +111,7 @@ SLOT_SCRATCH = 2
 SLOT_CONSTANT = 3
 REALIZATION_CONSTANT_BYTES = 49152
 MAX_SLOTS = 18
+MAX_LIVE_EXTENTS = 2
 
 
 class TargetProfile(ctypes.Structure):
@@ -202,6 +204,18 @@ class DispatchEntry(ctypes.Structure):
         ("binding_count", ctypes.c_uint32),
         ("binding_slots", ctypes.POINTER(ctypes.c_uint32)),
         ("binding_offsets", ctypes.POINTER(ctypes.c_uint32)),
+        ("extent_count", ctypes.c_uint32),
+        ("extent_ids", ctypes.POINTER(ctypes.c_uint32)),
+        ("extent_offsets", ctypes.POINTER(ctypes.c_uint32)),
+    ]
+
+
+class LiveExtent(ctypes.Structure):
+    _fields_ = [
+        ("access", ctypes.c_uint32),
+        ("axis", ctypes.c_uint32),
+        ("minimum", ctypes.c_uint64),
+        ("bound", ctypes.c_uint64),
     ]
 
 
@@ -212,6 +226,9 @@ class DispatchPlan(ctypes.Structure):
         ("entry_count", ctypes.c_uint32),
         ("entries", ctypes.POINTER(DispatchEntry)),
         ("slot_contents", ctypes.POINTER(ctypes.c_void_p)),
+        ("extent_count", ctypes.c_uint32),
+        ("extents", ctypes.POINTER(ctypes.c_uint64)),
+        ("extent_ranges", ctypes.POINTER(LiveExtent)),
     ]
 
 
@@ -336,6 +353,9 @@ class RealizedEntry(ctypes.Structure):
         ("binding_count", ctypes.c_uint32),
         ("binding_slots", ctypes.c_uint32 * MAX_SLOTS),
         ("binding_offsets", ctypes.c_uint32 * MAX_SLOTS),
+        ("extent_count", ctypes.c_uint32),
+        ("extent_ids", ctypes.c_uint32 * MAX_LIVE_EXTENTS),
+        ("extent_offsets", ctypes.c_uint32 * MAX_LIVE_EXTENTS),
     ]
 
 
@@ -350,6 +370,8 @@ class Realization(ctypes.Structure):
         ("constant_slot", ctypes.c_uint32),
         ("constant_bytes", ctypes.c_uint32),
         ("constant", ctypes.c_uint8 * REALIZATION_CONSTANT_BYTES),
+        ("live_extent_count", ctypes.c_uint32),
+        ("live_extents", LiveExtent * MAX_LIVE_EXTENTS),
     ]
 
 

@@ -95,6 +95,15 @@ Launch& Launch::ptr_table(const uint32_t* slots, uint32_t count, uint32_t capaci
   return *this;
 }
 Launch& Launch::u32(uint32_t v) { return blob(&v, 4, 4); }
+Launch& Launch::live_u32(uint32_t id) {
+  if (nextents >= kMaxLiveExtents) {
+    overflow = true;
+    return *this;
+  }
+  blob(nullptr, 4, 4);
+  if (!overflow) extents[nextents++] = {arg_offsets[nargs - 1], id};
+  return *this;
+}
 Launch& Launch::u64(uint64_t v) { return blob(&v, 8, 8); }
 Launch& Launch::f32(float v) { return blob(&v, 4, 4); }
 
@@ -115,6 +124,7 @@ Launch& Program::add(const char* symbol, uint32_t gx, uint32_t gy, uint32_t bloc
   l.kernarg_bytes = 0;
   l.nargs = 0;
   l.nbindings = 0;
+  l.nextents = 0;
   l.overflow = false;
   return l;
 }
@@ -462,45 +472,67 @@ tiler_hip_status plan_convert(Mode mode, uint32_t direction, uint64_t n, const u
 
 // ---------------------------------------------------------------------------
 // Contractions.  Slots: 0 a [m, k], 1 b [n, k], 2 c [m, n].
-tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p) {
+// The live contracted extent: read at dispatch from input 0 (A[m][k]), axis 1,
+// at least 1 (an empty contracted domain has no unseeded result) and at most
+// the bound the slots were sized for.
+static void declare_live_k(Program& p, uint64_t bound) {
+  p.live[0] = LiveExtent{0, 1, 1, bound};
+  p.nlive = 1;
+}
+
+tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p, bool live_k) {
   const uint32_t a = p.slot(mul_sat(mul_sat(m, k), 4), kSlotInput);
   const uint32_t b = p.slot(mul_sat(mul_sat(n, k), 4), kSlotInput);
   const uint32_t c = p.slot(mul_sat(mul_sat(m, n), 4), kSlotOutput);
   // contraction.rs:420-428: an empty contracted domain has no unseeded result.
   if (k == 0) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty contracted extent");
+  if (live_k) declare_live_k(p, k);
   if (m == 0 || n == 0) return TILER_HIP_OK;
   if (m > 0xffffffffull || n > 0xffffffffull || k > 0xffffffffull || (m + 15) / 16 > 65535)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
-  p.add("tiler_contract_strict_f32", (uint32_t)((n + 15) / 16), (uint32_t)((m + 15) / 16), 256)
-      .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n).u32((uint32_t)k).ptr(c);
+  Launch& l = p.add("tiler_contract_strict_f32", (uint32_t)((n + 15) / 16), (uint32_t)((m + 15) / 16), 256)
+                  .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n);
+  (live_k ? l.live_u32(0) : l.u32((uint32_t)k)).ptr(c);
   return TILER_HIP_OK;
 }
 
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
                                     uint32_t epilogue, const uintptr_t* addr, Program& p, bool strict,
-                                    uint32_t form) {
+                                    uint32_t form, bool live_k) {
   if (epilogue > TILER_HIP_EPILOGUE_SILU) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "epilogue");
   if (form != TILER_HIP_FORM_AUTO &&
       (strict || form < TILER_HIP_FORM_CONTRACT_SKINNY || form > TILER_HIP_FORM_CONTRACT_GENERAL_128))
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "form: not a form of this contraction");
+  if (live_k && form != TILER_HIP_FORM_AUTO && form != TILER_HIP_FORM_CONTRACT_GENERAL_128)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                    "live-extent: with a live k only the general form (any k) runs");
   const uint32_t a = p.slot(mul_sat(mul_sat(m, k), 2), kSlotInput);
   const uint32_t b = p.slot(mul_sat(mul_sat(n, k), 2), kSlotInput);
   const uint32_t c = p.slot(mul_sat(mul_sat(m, n), 2), kSlotOutput);
   if (k == 0) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "empty contracted extent");
+  if (live_k) declare_live_k(p, k);
   if (m == 0 || n == 0) return TILER_HIP_OK;
   if (strict) {  // the strict fold on exactly widened operands (MFMA regroups the k sum)
     if (m > 0xffffffffull || n > 0xffffffffull || k > 0xffffffffull || (m + 15) / 16 > 65535 ||
         (n + 15) / 16 > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
-    p.add(epilogue == TILER_HIP_EPILOGUE_SILU ? "tiler_contract_strict_bf16_silu" : "tiler_contract_strict_bf16",
-          (uint32_t)((n + 15) / 16), (uint32_t)((m + 15) / 16), 256)
-        .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n).u32((uint32_t)k).ptr(c);
+    Launch& l = p.add(epilogue == TILER_HIP_EPILOGUE_SILU ? "tiler_contract_strict_bf16_silu" : "tiler_contract_strict_bf16",
+                      (uint32_t)((n + 15) / 16), (uint32_t)((m + 15) / 16), 256)
+                    .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n);
+    (live_k ? l.live_u32(0) : l.u32((uint32_t)k)).ptr(c);
     return TILER_HIP_OK;
   }
   if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull || (m + 127) / 128 > 65535)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
   const bool silu = epilogue == TILER_HIP_EPILOGUE_SILU;
   const uint32_t m32 = (uint32_t)m, n32 = (uint32_t)n, k32 = (uint32_t)k;
+  if (live_k) {  // any k up to the bound: the general form, which takes k not a multiple of 8
+    Launch& l = p.add(silu ? "tiler_contract_bf16_silu_g128_k" : "tiler_contract_bf16_g128_k",
+                      (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 256)
+                    .ptr(a).ptr(b).u32(m32).u32(n32);
+    l.live_u32(0).ptr(c);
+    return TILER_HIP_OK;
+  }
   const bool pick = form == TILER_HIP_FORM_AUTO;
   // m <= 64 (decode shapes): B streamed once, one workgroup per 16 columns.
   const bool skinny_ok = m <= 64 && k % 8 == 0 && aligned16(addr[a]) && aligned16(addr[b]) &&

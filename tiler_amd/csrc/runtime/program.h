@@ -55,6 +55,19 @@ struct Binding {
   uint64_t addend;  // bytes past the slot base (direct execution only)
 };
 
+struct ExtentBinding {
+  uint32_t offset;  // byte offset of the 32-bit field in the kernarg segment
+  uint32_t id;      // the program's live extent
+};
+
+// A live extent (the program reads it at dispatch): input access, axis, and
+// the range its value must lie in.
+struct LiveExtent {
+  uint32_t access, axis;
+  uint64_t minimum, bound;
+};
+constexpr uint32_t kMaxLiveExtents = 2;
+
 struct Launch {
   char symbol[64];
   uint32_t grid[2];
@@ -65,6 +78,8 @@ struct Launch {
   uint32_t nargs;
   Binding bindings[kMaxBindings];
   uint32_t nbindings;
+  ExtentBinding extents[kMaxLiveExtents];
+  uint32_t nextents;
   bool overflow;  // an argument did not fit (a planner bug; refused)
 
   // Kernel arguments in declaration order, each at its natural alignment
@@ -74,6 +89,7 @@ struct Launch {
   Launch& u32(uint32_t v);
   Launch& u64(uint64_t v);
   Launch& f32(float v);
+  Launch& live_u32(uint32_t id);  // a 32-bit field the dispatch fills with live extent `id`
   Launch& blob(const void* p, uint32_t bytes, uint32_t align);
   // A table of `count` pointers to slots (NULL past count), `capacity` wide.
   Launch& ptr_table(const uint32_t* slots, uint32_t count, uint32_t capacity);
@@ -89,6 +105,8 @@ struct Program {
   // The CONSTANT slot's contents (an expression's register program), if any.
   uint32_t constant_slot = kMaxSlots;
   std::vector<uint8_t> constant;
+  LiveExtent live[kMaxLiveExtents];
+  uint32_t nlive = 0;
 
   Program();
   uint32_t slot(uint64_t bytes, uint32_t role);
@@ -160,7 +178,9 @@ tiler_hip_status plan_gather(Mode mode, uint64_t outer, uint64_t gathered, uint6
                              const uintptr_t* addr, Program& p);
 tiler_hip_status plan_convert(Mode mode, uint32_t direction, uint64_t n, const uintptr_t* addr,
                               Program& p);
-tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p);
+// live_k: k is read at dispatch (live extent 0, input 0 axis 1, in [1, k]);
+// the slots hold operands of the bound k.
+tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p, bool live_k = false);
 // Any admitted binary index structure: the strict fold (f32, or bf16 without
 // reassociation), or under it the batched MFMA forms where the structure is
 // [batch.., m, k] x [batch.., n, k | k, n] -> [batch.., m, n].
@@ -170,7 +190,8 @@ tiler_hip_status plan_contract_general(const Target& t, uint32_t dtype, const ti
 // request does not admit it; TILER_HIP_FORM_AUTO lets the planner choose.
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,
                                     uint32_t epilogue, const uintptr_t* addr, Program& p,
-                                    bool strict = false, uint32_t form = TILER_HIP_FORM_AUTO);
+                                    bool strict = false, uint32_t form = TILER_HIP_FORM_AUTO,
+                                    bool live_k = false);
 // Pointwise expression over n elements: slots inputs 0..I-1, y, program
 // (CONSTANT), and -- for programs beyond the register form -- the value
 // store (SCRATCH).  `addr` covers the inputs then y.

@@ -976,6 +976,26 @@ tiler_hip_status tiler_hip_plan_dispatch(tiler_hip_context* ctx,
       if ((uint64_t)e.binding_offsets[b] + 8 > e.kernarg_bytes)
         return fail(ctx, TILER_HIP_REFUSE_BINDING_MISMATCH, "binding pointer outside the kernarg segment");
     }
+    if (e.extent_count && (!e.extent_ids || !e.extent_offsets)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+    for (uint32_t x = 0; x < e.extent_count; ++x) {
+      if (e.extent_ids[x] >= plan->extent_count)
+        return fail(ctx, TILER_HIP_REFUSE_BINDING_MISMATCH, "entry reads a live extent the plan does not supply");
+      if ((uint64_t)e.extent_offsets[x] + 4 > e.kernarg_bytes)
+        return fail(ctx, TILER_HIP_REFUSE_BINDING_MISMATCH, "live extent field outside the kernarg segment");
+    }
+  }
+  if (plan->extent_count && !plan->extents) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  for (uint32_t x = 0; x < plan->extent_count; ++x) {
+    // Every live extent is a 32-bit launch field; a range, when given, is
+    // what the realization's slots were sized for.
+    const uint64_t v = plan->extents[x];
+    const bool in_range = plan->extent_ranges
+                              ? v >= plan->extent_ranges[x].minimum && v <= plan->extent_ranges[x].bound
+                              : true;
+    if (v > 0xffffffffull || !in_range)
+      return fail(ctx, TILER_HIP_REFUSE_CAPACITY,
+                  "live extent " + std::to_string(x) + " = " + std::to_string(v) +
+                      " outside the range the realization was sized for");
   }
   return TILER_HIP_OK;
 } catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
@@ -1022,6 +1042,12 @@ tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_disp
     for (uint32_t b = 0; b < e.binding_count; ++b) {
       void* p = slot_pointers[e.binding_slots[b]];
       std::memcpy(args.data() + e.binding_offsets[b], &p, sizeof(p));
+    }
+    for (uint32_t x = 0; x < e.extent_count; ++x) {
+      if (e.extent_ids[x] >= plan->extent_count || plan->extents[e.extent_ids[x]] > 0xffffffffull)
+        return fail(ctx, TILER_HIP_FAIL_LAUNCH, "entry " + std::to_string(i) + ": live extent not supplied");
+      const uint32_t v = (uint32_t)plan->extents[e.extent_ids[x]];
+      std::memcpy(args.data() + e.extent_offsets[x], &v, sizeof(v));
     }
     size_t size = args.size();
     void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE,
@@ -1742,6 +1768,7 @@ bool arithmetic(uint32_t program) {
 static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hip_region* r, tiler_rt::Program& p) {
   const bool al = (r->flags & TILER_HIP_REGION_ALIGNED16) != 0;
   const bool bc = (r->flags & TILER_HIP_REGION_OPERAND_BROADCAST) != 0;
+  const bool live = (r->flags & TILER_HIP_REGION_LIVE_EXTENT) != 0;
   // A stand-in address per slot: 0 is 16-byte aligned, 1 is not.
   uintptr_t addr[tiler_rt::kMaxSlots];
   for (uint32_t i = 0; i < tiler_rt::kMaxSlots; ++i) addr[i] = al ? 0u : 1u;
@@ -1763,6 +1790,9 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
   if (r->form != TILER_HIP_FORM_AUTO && r->program != TILER_HIP_PROGRAM_SOFTMAX &&
       !(r->program == TILER_HIP_PROGRAM_CONTRACTION && !r->structure && r->dtype == TILER_HIP_BF16))
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "form: this program has one form");
+  // A live extent belongs to the contraction (LiveContraction, schedule/model.rs:1429-1450).
+  if (live && r->program != TILER_HIP_PROGRAM_CONTRACTION)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "live-extent: only the contraction's k is live");
   auto needs_reassociation = [&](const char* what) {
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
                     (std::string(what) + " regroups the fold; the contract grants no reassociation").c_str());
@@ -1833,13 +1863,14 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
       break;
     case TILER_HIP_PROGRAM_CONTRACTION:
       if (r->structure)
-        st = tiler_rt::plan_contract_general(t, r->dtype, *r->structure, r->variant, !c.reassociate, addr, p);
+        st = live ? p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "live-extent: a structured contraction's extents are fixed")
+                  : tiler_rt::plan_contract_general(t, r->dtype, *r->structure, r->variant, !c.reassociate, addr, p);
       else if (r->dtype == TILER_HIP_F32)
         st = r->variant == TILER_HIP_EPILOGUE_NONE
-                 ? tiler_rt::plan_contract_strict_f32(e[0], e[1], e[2], p)
+                 ? tiler_rt::plan_contract_strict_f32(e[0], e[1], e[2], p, live)
                  : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the strict f32 contraction has no epilogue");
       else if (r->dtype == TILER_HIP_BF16)
-        st = tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p, !c.reassociate, r->form);
+        st = tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p, !c.reassociate, r->form, live);
       else
         st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "contraction dtype");
       break;
@@ -1911,8 +1942,16 @@ tiler_hip_status tiler_hip_realize(const tiler_hip_context* ctx, const tiler_hip
       d.binding_slots[b] = l.bindings[b].slot;
       d.binding_offsets[b] = l.bindings[b].offset;
     }
+    d.extent_count = l.nextents;
+    for (uint32_t x = 0; x < l.nextents; ++x) {
+      d.extent_ids[x] = l.extents[x].id;
+      d.extent_offsets[x] = l.extents[x].offset;
+    }
   }
   out->entry_count = p.nlaunches;
+  out->live_extent_count = p.nlive;
+  for (uint32_t x = 0; x < p.nlive; ++x)
+    out->live_extents[x] = {p.live[x].access, p.live[x].axis, p.live[x].minimum, p.live[x].bound};
   return TILER_HIP_OK;
 } catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
   return TILER_HIP_REFUSE_CAPACITY;

@@ -40,6 +40,7 @@ class RealizedDispatch:
     grid: tuple
     block: tuple
     bindings: list  # (slot, byte offset of the pointer field)
+    extents: list = field(default_factory=list)  # (live extent id, byte offset of its u32 field)
 
 
 @dataclass
@@ -49,6 +50,9 @@ class Realization:
     slots: list = field(default_factory=list)  # (role, bytes)
     alignment: int = 1
     dispatches: list = field(default_factory=list)
+    # (input access, axis, minimum, bound) per live extent: route(extents=...)
+    # supplies their values, each in [minimum, bound]
+    live_extents: list = field(default_factory=list)
 
     @property
     def symbols(self) -> list:
@@ -121,7 +125,10 @@ def _realize_region(r, ctx) -> Realization:
         symbol, family = _entry_info(e.entry)
         res.dispatches.append(RealizedDispatch(
             symbol, family, tuple(e.grid), tuple(e.block),
-            [(e.binding_slots[b], e.binding_offsets[b]) for b in range(e.binding_count)]))
+            [(e.binding_slots[b], e.binding_offsets[b]) for b in range(e.binding_count)],
+            [(e.extent_ids[x], e.extent_offsets[x]) for x in range(e.extent_count)]))
+    res.live_extents = [(x.access, x.axis, x.minimum, x.bound)
+                        for x in out.live_extents[:out.live_extent_count]]
     return res
 
 
@@ -228,14 +235,20 @@ def _capacity(buf):
     return getattr(buf, "nbytes", None)
 
 
-def route(ctx, realization: Realization, storage, payload=None) -> None:
+def route(ctx, realization: Realization, storage, payload=None, extents=()) -> None:
     """Executes `realization` on `ctx`'s stream and waits for it.  `storage`
     lists one device buffer (or address) per slot, in the realization's slot
     order; scratch slots may be None (allocated here, released after).
     `payload` (from `tiler_amd.envelope.select_payload`) routes through a
     carried code object instead of the library's own: every symbol dispatched
-    must be one of its PayloadEntryMappings."""
+    must be one of its PayloadEntryMappings.  `extents` gives this dispatch's
+    value of each live extent (realization.live_extents, in order); the slots
+    still hold the bound, and an input whose axis is live is packed at the
+    value given."""
     rz = realization
+    if len(extents) != len(rz.live_extents):
+        raise Refusal(L.REFUSE_BINDING_MISMATCH, "route",
+                      f"{len(extents)} live extent values for {len(rz.live_extents)} live extents")
     if payload is not None:
         mapped = set(payload.subject.symbols) if payload.subject is not None else set()
         for d in rz.dispatches:
@@ -266,10 +279,12 @@ def route(ctx, realization: Realization, storage, payload=None) -> None:
         slots = (ctypes.c_uint32 * max(1, e.binding_count))(*e.binding_slots[:e.binding_count])
         offs = (ctypes.c_uint32 * max(1, e.binding_count))(*e.binding_offsets[:e.binding_count])
         kernargs = ctypes.create_string_buffer(bytes(e.kernargs[:e.kernarg_bytes]), max(1, e.kernarg_bytes))
-        keep += [slots, offs, kernargs]
+        ids = (ctypes.c_uint32 * max(1, e.extent_count))(*e.extent_ids[:e.extent_count])
+        xoffs = (ctypes.c_uint32 * max(1, e.extent_count))(*e.extent_offsets[:e.extent_count])
+        keep += [slots, offs, kernargs, ids, xoffs]
         entries[i] = L.DispatchEntry(_prepared(ctx, rz.dispatches[i].symbol, payload), e.grid, e.block, 0,
                                      ctypes.cast(kernargs, ctypes.c_void_p), e.kernarg_bytes,
-                                     e.binding_count, slots, offs)
+                                     e.binding_count, slots, offs, e.extent_count, ids, xoffs)
     slot_bytes = (ctypes.c_uint64 * len(rz.slots))(*[b for _, b in rz.slots])
     # The CONSTANT slot's contents (an expression's register program) travel
     # with the plan; dispatch uploads them before the first entry.
@@ -279,7 +294,10 @@ def route(ctx, realization: Realization, storage, payload=None) -> None:
                                                max(1, rz.raw.constant_bytes))
         keep.append(constant)
         contents[rz.raw.constant_slot] = ctypes.cast(constant, ctypes.c_void_p)
-    plan = L.DispatchPlan(len(rz.slots), slot_bytes, n, entries, contents)
+    live = len(rz.live_extents)
+    values = (ctypes.c_uint64 * max(1, live))(*[int(v) for v in extents])
+    ranges = (L.LiveExtent * max(1, live))(*rz.raw.live_extents[:live])
+    plan = L.DispatchPlan(len(rz.slots), slot_bytes, n, entries, contents, live, values, ranges)
     h = ctx.handle
     _raise(L.lib().tiler_hip_plan_dispatch(h, ctypes.byref(plan)), "plan_dispatch", ctx.diagnostic())
     ptrs = (ctypes.c_void_p * len(rz.slots))(*[_address(b) or None for b in storage])
