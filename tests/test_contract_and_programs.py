@@ -47,7 +47,10 @@ def test_zeroed_region_is_the_strict_serial_sum():
     assert L.lib().tiler_hip_realize(None, ctypes.byref(r), ctypes.byref(out), None, 0) == L.OK
     info = L.EntryInfo()
     assert L.lib().tiler_hip_payload_entry(out.entries[0].entry, ctypes.byref(info)) == L.OK
-    assert out.entry_count == 1 and info.symbol == b"tiler_sum_f32_serial"
+    # the strict serial fold (rows of 100 are staged through LDS, one row per
+    # workgroup for 4 rows; the stand-in address is unaligned without ALIGNED16)
+    assert out.entry_count == 1 and info.symbol == b"tiler_sum_f32_staged_r1_u"
+    assert info.family == b"strict-serial-sum-f32/serial"
     assert L.SUM_SERIAL == 0
 
 

@@ -52,6 +52,53 @@ def test_serial_sum_golden_sets_and_random(ctx):
     assert np.array_equal(bits(got), bits(oracle.strict_sum(x, (37, 1001), 1)))
 
 
+def _order_sensitive(rng, rows, extent):
+    """Values over 80 binades, so that any other order of the fold gives
+    other bits; row 0 all -0.0 (the fold's -0.0 total), row 1 with a NaN,
+    row 2 with +inf and -inf (NaN), row 3 with one +inf."""
+    x = (rng.standard_normal((rows, extent)) * np.exp2(rng.integers(-40, 40, (rows, extent)))).astype(np.float32)
+    if rows >= 4:
+        x[0] = -0.0
+        x[1, extent // 2] = np.nan
+        x[2, 0], x[2, -1] = np.inf, -np.inf
+        x[3, extent - 1] = np.inf
+    return x
+
+
+@pytest.mark.parametrize("rows,extent,offset", [
+    (3, 10000, 0),     # one row per workgroup, 16-byte loads, a ragged last stage
+    (5, 9999, 0),      # rows off the 16-byte grid: 4-byte loads
+    (4, 3000, 4),      # an unaligned base
+    (700, 1500, 0),    # four rows per workgroup (one per wave), a ragged last workgroup
+    (2000, 300, 0),    # sixteen rows per workgroup
+    (3000, 259, 0),    # sixteen rows, 4-byte loads
+    (5000, 129, 0),    # sixty-four rows per workgroup, 4-byte loads
+    (20000, 64, 0),    # sixty-four rows per workgroup, one stage
+    (17000, 65, 0),    # sixty-four rows, a second stage of one element
+    (1, 70000, 0),     # one long row
+])
+def test_serial_sum_staged_rows_are_the_strict_fold(ctx, rows, extent, offset):
+    """Rows of 64 or more elements are folded from LDS stages
+    (tiler_sum_f32_staged_r*); the fold is still evaluate.rs:555-585's, bit
+    for bit."""
+    x = _order_sensitive(np.random.default_rng(rows * 7 + extent), rows, extent)
+    dx = ctx.alloc(x.nbytes + offset)
+    do = ctx.alloc(rows * 4)
+    try:
+        src = dx.offset(offset)
+        src.upload(x)
+        ctx.sum_f32(src, rows, extent, do, topology=L.SUM_SERIAL)
+        got = do.download(np.float32, (rows,))
+    finally:
+        dx.free()
+        do.free()
+    want = oracle.strict_sum(x, (rows, extent), 1)
+    assert np.array_equal(bits(got), bits(want))
+    if rows >= 4:
+        assert bits(got)[0] == 0x80000000 and bits(got)[1] == bits(got)[2] == 0x7FC00000
+        assert got[3] == np.inf
+
+
 def test_multipass_sum_matches_strict_partitioned_sum(ctx):
     s = G["serial_sum"]
     sep = f32(s["separating_operands"])

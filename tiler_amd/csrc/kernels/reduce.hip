@@ -17,6 +17,8 @@
 //                                launch combining the workgroup partials.
 // The first three are bit-exact with the reference; the tree's exact order is
 // its declared grouping, restated by the oracle's grid/row grouped sums.
+#include <type_traits>
+
 #include "common.h"
 
 using tiler::canon;
@@ -37,6 +39,138 @@ tiler_sum_f32_serial(const float* __restrict__ x, uint64_t outer, uint64_t exten
   for (uint64_t p = 0; p < extent; ++p) acc = acc + base[p * inner];
   out[id] = extent == 0 ? 0.0f : canon(acc);
 }
+
+// Serial over contiguous rows, staged through LDS: out[v] = the same strict
+// fold of x[v*length .. +length), ascending from a -0.0 seed, as
+// tiler_sum_f32_serial computes.  A lane that folds its own row straight from
+// global memory waits a memory latency per load (each load of a wave touches
+// 64 rows); here a 256-thread workgroup serves R rows.  Stage s holds
+// C = 4096/R elements of each row.  All four waves load stage s+1 into
+// registers (coalesced: consecutive lanes read consecutive elements of one
+// row), the folding lanes fold stage s from LDS, and then stage s+1 is stored
+// to the other buffer.  Row r is folded by lane r/4 of wave r%4 (R = 1: lane 0
+// of wave 0), so a workgroup's chains sit on its four waves' SIMDs rather
+// than sharing one.  The chain of adds bounds a long row, and the loads hide
+// behind it.  kVec: 16-byte loads (aligned x, length a multiple of 4).
+template <int R, bool kVec>
+__device__ __forceinline__ void sum_staged_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
+                                                float* __restrict__ out) {
+  constexpr uint32_t C = 4096 / R;               // elements of a row per stage
+  constexpr uint32_t kStride = C + 4;            // LDS row stride in floats (16-byte aligned, staggered banks)
+  constexpr uint32_t W = kVec ? 4 : 1;           // elements per load
+  constexpr uint32_t kRowPieces = C / W;         // loads per row per stage
+  constexpr uint32_t kPer = 4096 / W / 256;      // loads per thread per stage
+  __shared__ __align__(16) float stage[2][R * kStride];
+  const uint32_t t = threadIdx.x;
+  const uint64_t row0 = (uint64_t)blockIdx.x * R;
+  const uint64_t stages = (length + C - 1) / C;
+  typedef typename std::conditional<kVec, f32x4, float>::type piece;
+  piece reg[kPer];
+  auto load = [&](uint64_t s) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      const uint64_t e = s * C + (uint64_t)(q % kRowPieces) * W;
+      if (row0 + r < nrows && e < length) {
+        const float* src = x + (row0 + r) * length + e;
+        if constexpr (kVec) reg[i] = *reinterpret_cast<const f32x4*>(src);
+        else reg[i] = *src;
+      } else {
+        reg[i] = piece{};  // never folded: past the row or past the last row
+      }
+    }
+  };
+  auto store = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      *reinterpret_cast<piece*>(&stage[buf][r * kStride + (q % kRowPieces) * W]) = reg[i];
+    }
+  };
+  const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
+  const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < nrows;
+  float acc = -0.0f;
+  if (stages > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (uint64_t s = 0; s < stages; ++s) {
+    const bool more = s + 1 < stages;
+    if (more) load(s + 1);
+    if (folds) {
+      const float* row = &stage[s & 1][fr * kStride];
+      const uint32_t count = (uint32_t)(length - s * C < C ? length - s * C : C);
+      if (count == C) {
+        // A whole stage: batches of kBatch 16-byte reads, the next batch's
+        // reads in flight while the current one is added, so the chain of
+        // adds does not wait out an LDS latency per read.
+        // Two register sets in turn (no copies between them); long rows run
+        // one workgroup per CU, with registers for batches of 16 reads.
+        constexpr uint32_t kBatch = C / 4 < (R <= 4 ? 16u : 8u) ? C / 4 : (R <= 4 ? 16u : 8u);
+        constexpr uint32_t kBatches = C / 4 / kBatch;
+        const f32x4* rv = reinterpret_cast<const f32x4*>(row);
+        f32x4 ba[kBatch], bb[kBatch];
+        auto add_batch = [&](const f32x4* v) {
+#pragma unroll
+          for (uint32_t j = 0; j < kBatch; ++j) {
+            acc = acc + v[j].x;
+            acc = acc + v[j].y;
+            acc = acc + v[j].z;
+            acc = acc + v[j].w;
+          }
+        };
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) ba[j] = rv[j];
+        for (uint32_t b = 0; b < kBatches; b += 2) {
+          if (b + 1 < kBatches) {
+#pragma unroll
+            for (uint32_t j = 0; j < kBatch; ++j) bb[j] = rv[(b + 1) * kBatch + j];
+          }
+          add_batch(ba);
+          if (b + 1 < kBatches) {
+            if (b + 2 < kBatches) {
+#pragma unroll
+              for (uint32_t j = 0; j < kBatch; ++j) ba[j] = rv[(b + 2) * kBatch + j];
+            }
+            add_batch(bb);
+          }
+        }
+      } else {
+        // The last stage: only elements below `length` are folded (a padded
+        // +0.0 would turn a -0.0 total into +0.0).
+        uint32_t c = 0;
+        for (; c + 4 <= count; c += 4) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(row + c);
+          acc = acc + v.x;
+          acc = acc + v.y;
+          acc = acc + v.z;
+          acc = acc + v.w;
+        }
+        for (; c < count; ++c) acc = acc + row[c];
+      }
+    }
+    if (more) store((uint32_t)((s + 1) & 1));
+    __syncthreads();
+  }
+  if (folds) out[row0 + fr] = length == 0 ? 0.0f : canon(acc);
+}
+
+#define TILER_SUM_STAGED(R)                                                                            \
+  extern "C" __global__ void __launch_bounds__(256)                                                    \
+      tiler_sum_f32_staged_r##R(const float* __restrict__ x, uint64_t nrows, uint64_t length,          \
+                                float* __restrict__ out) {                                             \
+    sum_staged_body<R, true>(x, nrows, length, out);                                                   \
+  }                                                                                                    \
+  extern "C" __global__ void __launch_bounds__(256)                                                    \
+      tiler_sum_f32_staged_r##R##_u(const float* __restrict__ x, uint64_t nrows, uint64_t length,      \
+                                    float* __restrict__ out) {                                         \
+    sum_staged_body<R, false>(x, nrows, length, out);                                                  \
+  }
+TILER_SUM_STAGED(1)
+TILER_SUM_STAGED(4)
+TILER_SUM_STAGED(16)
+TILER_SUM_STAGED(64)
 
 // MultiPass pass 1: partials[r*P + p] = strict fold of
 // x[r*extent + p*chunk .. +chunk]; an empty partition commits +0.0.

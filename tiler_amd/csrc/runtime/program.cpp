@@ -140,6 +140,27 @@ uint32_t tree_workgroups(const Target& t, uint64_t n) {
 // ---------------------------------------------------------------------------
 // Sum over the last axis of [rows, extent] f32.  Slots: 0 x, 1 out,
 // 2 partials (multi-pass and the single-output tree).
+// The strict serial fold of `nrows` contiguous rows of `length` elements
+// (slot `src`, row v at v * length) into `dst`.  Rows of 64 or more elements
+// are staged through LDS, R rows per workgroup with R the smallest of
+// 1, 4, 16, 64 that keeps to one workgroup per CU (64 beyond), so that the
+// folding chains of few long rows get a SIMD each; shorter rows take one lane
+// per row, whose loads are already near one another.
+static void add_serial_fold(const Target& t, uint32_t src, bool src_aligned, uint64_t nrows, uint64_t length,
+                            uint32_t dst, Program& p) {
+  if (length >= 64) {
+    const uint64_t cus = t.compute_units;
+    const uint32_t R = nrows <= cus ? 1 : nrows <= 4 * cus ? 4 : nrows <= 16 * cus ? 16 : 64;
+    const bool vec = src_aligned && length % 4 == 0;
+    char name[40];
+    std::snprintf(name, sizeof(name), "tiler_sum_f32_staged_r%u%s", R, vec ? "" : "_u");
+    p.add(name, (uint32_t)((nrows + R - 1) / R), 1, 256).ptr(src).u64(nrows).u64(length).ptr(dst);
+    return;
+  }
+  p.add("tiler_sum_f32_serial", (uint32_t)((nrows + 255) / 256), 1, 256)
+      .ptr(src).u64(nrows).u64(length).u64(1).ptr(dst);
+}
+
 tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
                               const tiler_hip_sum_plan& sp, const uintptr_t* addr, Program& p) {
   const uint32_t x = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotInput);
@@ -147,23 +168,27 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
   switch (sp.topology) {
     case TILER_HIP_SUM_SERIAL:
       if (rows == 0) return TILER_HIP_OK;
-      if ((rows + 255) / 256 > 0x7fffffffull)
+      if ((rows + 255) / 256 > 0x7fffffffull || (extent >= 64 && rows > 0x7fffffffull))
         return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-      p.add("tiler_sum_f32_serial", (uint32_t)((rows + 255) / 256), 1, 256)
-          .ptr(x).u64(rows).u64(extent).u64(1).ptr(out);
+      add_serial_fold(t, x, aligned16(addr[x]), rows, extent, out, p);
       return TILER_HIP_OK;
     case TILER_HIP_SUM_MULTIPASS: {
       const uint64_t P = sp.partitions, c = sp.per_partition;
       if (rows == 0) return TILER_HIP_OK;
       if (P == 0 || (c != 0 && P > UINT64_MAX / c) || P * c != extent)
         return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "partitions do not cover the axis exactly");
-      if (mul_sat(rows, P) / 256 >= 0x7fffffffull)
+      if (mul_sat(rows, P) / 256 >= 0x7fffffffull || (c >= 64 && mul_sat(rows, P) > 0x7fffffffull))
         return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more partitions than the launch grid holds");
       const uint32_t part = p.slot(mul_sat(mul_sat(rows, P), 4), kSlotScratch);
-      p.add("tiler_sum_f32_partials", (uint32_t)((rows * P + 255) / 256), 1, 256)
-          .ptr(x).u64(rows).u64(extent).u64(P).u64(c).ptr(part);
-      p.add("tiler_sum_f32_serial", (uint32_t)((rows + 255) / 256), 1, 256)
-          .ptr(part).u64(rows).u64(P).u64(1).ptr(out);
+      // With exact coverage partition p of row r is the contiguous run
+      // (r*P + p) * c: pass 1 is the serial fold of rows*P rows of c.
+      if (c >= 64)
+        add_serial_fold(t, x, aligned16(addr[x]), rows * P, c, part, p);
+      else
+        p.add("tiler_sum_f32_partials", (uint32_t)((rows * P + 255) / 256), 1, 256)
+            .ptr(x).u64(rows).u64(extent).u64(P).u64(c).ptr(part);
+      // the partials are the planner's own scratch, 16-byte aligned
+      add_serial_fold(t, part, true, rows, P, out, p);
       return TILER_HIP_OK;
     }
     case TILER_HIP_SUM_COOPERATIVE: {

@@ -45,6 +45,14 @@ struct EntryRow {
 // Every kernel the payload carries, in a fixed order (the entry mapping).
 const EntryRow kEntries[] = {
     {"tiler_sum_f32_serial", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_staged_r1", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_staged_r1_u", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_staged_r4", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_staged_r4_u", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_staged_r16", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_staged_r16_u", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_staged_r64", "strict-serial-sum-f32/serial", 2},
+    {"tiler_sum_f32_staged_r64_u", "strict-serial-sum-f32/serial", 2},
     {"tiler_sum_f32_partials", "strict-serial-sum-f32/multipass", 2},
     {"tiler_sum_f32_cooperative", "strict-serial-sum-f32/cooperative-workgroup", 2},
     {"tiler_sum_f32_grid", "strict-serial-sum-f32/tree", 2},
