@@ -18,7 +18,11 @@ single-threaded, on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                        [--no-families] [--no-cpu-baseline] [--calibration-copy]
-                       [--vendor-gemm]
+                       [--vendor-gemm] [--no-reference-cells]
+
+"reference_cells" times this library on the reference's own published
+benchmark cells (its strict f32 contraction cells and its reduction dispatch
+crossover cells), each beside the reference's Apple-GPU figure.
 """
 from __future__ import annotations
 
@@ -612,6 +616,125 @@ def measure(ctx, wl, steps, warmup):
     }
 
 
+# The reference's own published device timings, Apple GPUs (context: other
+# hardware, other memory system; not targets).  Strict f32 contraction cells
+# of spikes/scheduling/metal_contraction_vertical/results/2026-07-31-timing-
+# apple9-f32-msl4-macos26-m3pro-metal32023.883/timing-summary.tsv, realization
+# `tiled` (the strict first-product fold): (cell, m, n, k, settled min us,
+# GFLOP/s, line).
+REFERENCE_CONTRACTION_CELLS = [
+    ("w_decode_kv", 1, 1024, 1024, 60.500, 34.7, 3),
+    ("w_prefill_q", 10, 2048, 1024, 148.958, 281.6, 9),
+    ("w_prefill_mlp_in", 128, 3072, 1024, 1601.833, 502.7, 15),
+    ("w_prefill_mlp_out", 128, 1024, 3072, 1599.459, 503.5, 21),
+    ("w_prefill_o", 128, 1024, 2048, 1051.458, 510.6, 27),
+    ("w_vocab_slice", 1, 8192, 1024, 523.500, 32.0, 33),
+    ("t_vocab_full", 1, 151936, 1024, 9668.583, 32.2, 39),
+    ("t_prefill_mlp_512", 512, 3072, 1024, 6395.375, 503.7, 45),
+]
+# Reduction dispatch crossover at 2^24 elements, Apple M4 Max, amortized p50 us
+# (spikes/program-planning/reduction-dispatch-crossover/results/2026-08-07-
+# apple-m4-max-macos27.0-26A5388g/sweep.tsv): (rows, extent, strategy, us, line).
+REFERENCE_REDUCTION_CELLS = [
+    (1024, 16384, "serial-fold", 1493.1444, 208),
+    (1024, 16384, "single-workgroup-tree", 891.5083, 209),
+    (1024, 16384, "multi-pass-split", 891.0139, 210),
+    (4096, 4096, "serial-fold", 865.2778, 235),
+    (4096, 4096, "single-workgroup-tree", 851.6889, 236),
+    (4096, 4096, "multi-pass-split", 852.9639, 237),
+    (65536, 256, "serial-fold", 860.7167, 274),
+    (65536, 256, "single-workgroup-tree", 830.7334, 275),
+    (65536, 256, "multi-pass-split", 836.9389, 276),
+]
+
+
+def time_launches(ctx, launch, steps, warmup, graph=True):
+    """Mean ms per launch of `launch(i)`: W eager warm-ups, then K launches
+    captured into a graph, replayed once untimed and once between events
+    (graph=False: K eager launches between events, for a family that
+    allocates per call and so refuses capture)."""
+    for i in range(warmup):
+        launch(i)
+    ctx.synchronize()
+    g = None
+    if graph:
+        ctx.capture_begin()
+        try:
+            for i in range(steps):
+                launch(warmup + i)
+        finally:
+            g = ctx.capture_end()
+        ctx.graph_launch(g)
+        ctx.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    if g is not None:
+        ctx.graph_launch(g)
+    else:
+        for i in range(steps):
+            launch(warmup + i)
+    ctx.record(e1)
+    ctx.synchronize()
+    ms = ctx.elapsed_ms(e0, e1) / steps
+    for e in (e0, e1):
+        ctx.destroy_event(e)
+    if g is not None:
+        ctx.graph_destroy(g)
+    return ms
+
+
+def reference_cells(ctx, steps, warmup):
+    """This library on the reference's own published benchmark cells, with the
+    same semantics: the strict f32 contraction (tiler_contract_strict_f32, the
+    first-product fold bit for bit) and the three reduction strategies of the
+    dispatch crossover (the strict serial fold; the workgroup tree and the
+    multi-pass split, as under the sweep's FLUSH_AND_REASSOCIATE_F32 contract).
+    Reduction inputs rotate over 5 sets of 64 MiB (more than the Infinity
+    Cache holds)."""
+    from tiler_amd import _lib as L
+    from tiler_amd.calibrate import split_partitions
+    out = {"contraction": [], "reduction": [],
+           "reference_hardware": {"contraction": "Apple M3 Pro", "reduction": "Apple M4 Max"}}
+    rng = np.random.default_rng(3)
+    for cell, m, n, k, ref_us, ref_gflops, line in REFERENCE_CONTRACTION_CELLS:
+        a = ctx.to_device(rng.standard_normal((m, k)).astype(np.float32))
+        b = ctx.to_device(rng.standard_normal((n, k)).astype(np.float32))
+        c = ctx.alloc(m * n * 4)
+        try:
+            ms = time_launches(ctx, lambda i: ctx.contract_strict_f32(a, b, m, n, k, c), max(5, steps // 4), warmup)
+        finally:
+            for x in (a, b, c):
+                x.free()
+        gflops = 2.0 * m * n * k / (ms * 1e-3) / 1e9
+        out["contraction"].append({"cell": cell, "m": m, "n": n, "k": k, "us": ms * 1e3, "gflop_per_s": gflops,
+                                   "reference_us": ref_us, "reference_gflop_per_s": ref_gflops,
+                                   "reference_line": line})
+        log(f"reference cell {cell} {m}x{n}x{k}: {ms * 1e3:.1f} us ({gflops:.0f} GFLOP/s; reference {ref_us} us)")
+    n_elem = 1 << 24
+    xs = [ctx.to_device(rng.uniform(-1, 1, n_elem).astype(np.float32)) for _ in range(5)]
+    o = ctx.alloc(65536 * 4)
+    try:
+        for rows, extent, strategy, ref_us, line in REFERENCE_REDUCTION_CELLS:
+            if strategy == "serial-fold":
+                kw = dict(topology=L.SUM_SERIAL)
+            elif strategy == "single-workgroup-tree":
+                kw = dict(topology=L.SUM_TREE)
+            else:
+                p = split_partitions(extent)
+                kw = dict(topology=L.SUM_MULTIPASS, partitions=p, per_partition=extent // p)
+            # a split whose partials outgrow the context workspace allocates
+            # per call, which capture refuses: those cells run eagerly
+            ms = time_launches(ctx, lambda i: ctx.sum_f32(xs[i % 5], rows, extent, o, **kw), max(10, steps // 4),
+                               warmup, graph=strategy != "multi-pass-split")
+            out["reduction"].append({"rows": rows, "extent": extent, "strategy": strategy, "us": ms * 1e3,
+                                     "reference_us": ref_us, "reference_line": line})
+            log(f"reference cell {rows}x{extent} {strategy}: {ms * 1e3:.1f} us (reference {ref_us} us)")
+    finally:
+        for x in xs + [o]:
+            x.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -620,6 +743,8 @@ def main():
     ap.add_argument("--workload", default="rms_norm", choices=sorted(WORKLOADS))
     ap.add_argument("--no-families", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-reference-cells", action="store_true",
+                    help="skip timing the reference's own published benchmark cells")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time the vendor bf16 GEMM (torch.matmul) on the contraction operands")
@@ -668,6 +793,10 @@ def main():
             families[name] = {k: r[k] for k in ("value", "unit", "ms_per_step", "median_ms", "roofline", "config")}
             log(f"{name}: {r['value']:.1f} {r['unit']} ({100 * r['roofline']['frac']:.1f}% of peak)")
 
+    cells = None
+    if not args.no_reference_cells:
+        cells = reference_cells(ctx, args.steps, args.warmup)
+
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline ({args.workload}), ~{args.cpu_seconds:.0f} s")
@@ -693,6 +822,7 @@ def main():
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "families": families,
+        **({"reference_cells": cells} if cells else {}),
         **({"vendor_gemm": vendor} if vendor else {}),
         "device": {k: ctx.environment[k] for k in ("device_name", "gcn_arch_name", "compute_units")},
     }
