@@ -174,7 +174,7 @@ int main() {
     plan_broadcast(pick(r), (uint32_t)(r() % 10) % 9, dims, strides, (uint32_t)(r() % 6), p[4]);
     plan_gather(mode, pick(r), pick(r), pick(r), (uint32_t)(r() % 17), pick(r), (int32_t)(r() % 2), addr, p[5]);
     plan_convert(mode, (uint32_t)(r() % 3), pick(r), addr, p[6]);
-    plan_contract_strict_f32(pick(r), pick(r), pick(r), p[7], r() % 2 == 0);
+    plan_contract_strict_f32(t, pick(r), pick(r), pick(r), addr, p[7], r() % 2 == 0);
     plan_contract_bf16(t, pick(r), pick(r), pick(r), (uint32_t)(r() % 3), addr, p[8], r() % 4 == 0,
                        (uint32_t)(r() % 6), r() % 3 == 0);
     for (int i = 0; i < 9; ++i) {

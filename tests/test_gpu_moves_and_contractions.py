@@ -281,6 +281,46 @@ def test_strict_contraction_tails_and_signed_zero(ctx):
     assert bits(z)[0, 0] == 0x80000000
 
 
+@pytest.mark.parametrize("m,n,k,offset", [
+    (1, 200, 1000, 0),   # one output column per workgroup, 16-byte loads
+    (3, 300, 999, 0),    # four columns per workgroup, 4-byte loads, a ragged last stage
+    (16, 200, 300, 0),   # sixteen columns per workgroup
+    (5, 4000, 130, 0),   # sixty-four columns per workgroup, 4-byte loads
+    (2, 3000, 64, 0),    # sixty-four columns, exactly one stage
+    (1, 70, 4099, 0),    # one column per workgroup over two stages
+    (4, 100, 512, 4),    # unaligned operands: 4-byte loads
+])
+def test_strict_contraction_few_rows_is_the_first_product_fold(ctx, m, n, k, offset):
+    """m <= 16 runs the staged fold of products (tiler_contract_strict_f32_s*):
+    still contraction.rs:558-630's fold, bit for bit, with values over 60
+    binades so any other order shows; row 0 of A all -0.0 against positive B
+    (a -0.0 total), a NaN in row 1, an inf against a zero in row 2."""
+    rng = np.random.default_rng(m * 1000 + n + k)
+    a = (rng.standard_normal((m, k)) * np.exp2(rng.integers(-30, 30, (m, k)))).astype(np.float32)
+    b = (rng.standard_normal((n, k)) * np.exp2(rng.integers(-30, 30, (n, k)))).astype(np.float32)
+    if m >= 3:
+        a[0] = -0.0
+        b[0] = np.abs(b[0])
+        a[1, k // 3] = np.nan
+        a[2, 5], b[:, 5] = np.inf, 0.0
+    da, db = ctx.alloc(a.nbytes + offset), ctx.alloc(b.nbytes + offset)
+    dc = ctx.alloc(m * n * 4)
+    try:
+        da.offset(offset).upload(a)
+        db.offset(offset).upload(b)
+        print(f"[strict few rows] m={m} n={n} k={k} offset={offset}", flush=True)
+        ctx.contract_strict_f32(da.offset(offset), db.offset(offset), m, n, k, dc)
+        got = dc.download(np.float32, (m, n))
+    finally:
+        for x in (da, db, dc):
+            x.free()
+    want = oracle.contract_strict_f32(a, b, m, n, k).reshape(m, n)
+    assert np.array_equal(bits(got), bits(want))
+    if m >= 3:
+        assert bits(got)[0, 0] == 0x80000000
+        assert (bits(got)[1] == 0x7FC00000).all() and (bits(got)[2] == 0x7FC00000).all()
+
+
 def _frob(got_bits, ref32):
     g = bf16_widen(got_bits).astype(np.float64)
     r = np.asarray(ref32, np.float64)

@@ -52,20 +52,27 @@ tiler_sum_f32_serial(const float* __restrict__ x, uint64_t outer, uint64_t exten
 // of wave 0), so a workgroup's chains sit on its four waves' SIMDs rather
 // than sharing one.  The chain of adds bounds a long row, and the loads hide
 // behind it.  kVec: 16-byte loads (aligned x, length a multiple of 4).
-template <int R, bool kVec>
-__device__ __forceinline__ void sum_staged_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
-                                                float* __restrict__ out) {
+//
+// kDot: the fold of products instead, out[v] = fold over e of fl(a[e] *
+// x[v*length + e]) -- one output row of the strict contraction, with x the
+// right operand's rows and `a` the left operand's row, staged beside them.
+template <int R, bool kVec, bool kDot>
+__device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
+                                                 const float* __restrict__ a, float* __restrict__ out) {
   constexpr uint32_t C = 4096 / R;               // elements of a row per stage
   constexpr uint32_t kStride = C + 4;            // LDS row stride in floats (16-byte aligned, staggered banks)
   constexpr uint32_t W = kVec ? 4 : 1;           // elements per load
   constexpr uint32_t kRowPieces = C / W;         // loads per row per stage
   constexpr uint32_t kPer = 4096 / W / 256;      // loads per thread per stage
+  constexpr uint32_t kAPer = kDot ? (kRowPieces + 255) / 256 : 0;  // loads of the left row per thread
   __shared__ __align__(16) float stage[2][R * kStride];
+  __shared__ __align__(16) float astage[kDot ? 2 : 1][kDot ? C : 4];
   const uint32_t t = threadIdx.x;
   const uint64_t row0 = (uint64_t)blockIdx.x * R;
   const uint64_t stages = (length + C - 1) / C;
   typedef typename std::conditional<kVec, f32x4, float>::type piece;
   piece reg[kPer];
+  piece areg[kAPer > 0 ? kAPer : 1];
   auto load = [&](uint64_t s) {
 #pragma unroll
     for (uint32_t i = 0; i < kPer; ++i) {
@@ -79,12 +86,28 @@ __device__ __forceinline__ void sum_staged_body(const float* __restrict__ x, uin
         reg[i] = piece{};  // never folded: past the row or past the last row
       }
     }
+#pragma unroll
+    for (uint32_t i = 0; i < kAPer; ++i) {
+      const uint32_t q = t + 256u * i;
+      const uint64_t e = s * C + (uint64_t)q * W;
+      if (q < kRowPieces && e < length) {
+        if constexpr (kVec) areg[i] = *reinterpret_cast<const f32x4*>(a + e);
+        else areg[i] = a[e];
+      } else {
+        areg[i] = piece{};
+      }
+    }
   };
   auto store = [&](uint32_t buf) {
 #pragma unroll
     for (uint32_t i = 0; i < kPer; ++i) {
       const uint32_t q = t + 256u * i, r = q / kRowPieces;
       *reinterpret_cast<piece*>(&stage[buf][r * kStride + (q % kRowPieces) * W]) = reg[i];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kAPer; ++i) {
+      const uint32_t q = t + 256u * i;
+      if (q < kRowPieces) *reinterpret_cast<piece*>(&astage[buf][q * W]) = areg[i];
     }
   };
   const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
@@ -100,25 +123,36 @@ __device__ __forceinline__ void sum_staged_body(const float* __restrict__ x, uin
     if (more) load(s + 1);
     if (folds) {
       const float* row = &stage[s & 1][fr * kStride];
+      const float* arow = &astage[kDot ? (s & 1) : 0][0];
       const uint32_t count = (uint32_t)(length - s * C < C ? length - s * C : C);
+      // one fold step: the element, or under kDot its product with the left
+      // row's element (two roundings: no FMA)
+      auto step4 = [&](const f32x4 v, uint32_t c) {
+        if constexpr (kDot) {
+          const f32x4 w = *reinterpret_cast<const f32x4*>(arow + c);
+          acc = acc + w.x * v.x;
+          acc = acc + w.y * v.y;
+          acc = acc + w.z * v.z;
+          acc = acc + w.w * v.w;
+        } else {
+          acc = acc + v.x;
+          acc = acc + v.y;
+          acc = acc + v.z;
+          acc = acc + v.w;
+        }
+      };
       if (count == C) {
-        // A whole stage: batches of kBatch 16-byte reads, the next batch's
+        // A whole stage: ping-pong batches of 16-byte reads, the next batch's
         // reads in flight while the current one is added, so the chain of
-        // adds does not wait out an LDS latency per read.
-        // Two register sets in turn (no copies between them); long rows run
-        // one workgroup per CU, with registers for batches of 16 reads.
+        // adds does not wait out an LDS latency per read; long rows run one
+        // workgroup per CU, with registers for batches of 16 reads.
         constexpr uint32_t kBatch = C / 4 < (R <= 4 ? 16u : 8u) ? C / 4 : (R <= 4 ? 16u : 8u);
         constexpr uint32_t kBatches = C / 4 / kBatch;
         const f32x4* rv = reinterpret_cast<const f32x4*>(row);
         f32x4 ba[kBatch], bb[kBatch];
-        auto add_batch = [&](const f32x4* v) {
+        auto add_batch = [&](const f32x4* v, uint32_t first) {
 #pragma unroll
-          for (uint32_t j = 0; j < kBatch; ++j) {
-            acc = acc + v[j].x;
-            acc = acc + v[j].y;
-            acc = acc + v[j].z;
-            acc = acc + v[j].w;
-          }
+          for (uint32_t j = 0; j < kBatch; ++j) step4(v[j], (first + j) * 4u);
         };
 #pragma unroll
         for (uint32_t j = 0; j < kBatch; ++j) ba[j] = rv[j];
@@ -127,27 +161,24 @@ __device__ __forceinline__ void sum_staged_body(const float* __restrict__ x, uin
 #pragma unroll
             for (uint32_t j = 0; j < kBatch; ++j) bb[j] = rv[(b + 1) * kBatch + j];
           }
-          add_batch(ba);
+          add_batch(ba, b * kBatch);
           if (b + 1 < kBatches) {
             if (b + 2 < kBatches) {
 #pragma unroll
               for (uint32_t j = 0; j < kBatch; ++j) ba[j] = rv[(b + 2) * kBatch + j];
             }
-            add_batch(bb);
+            add_batch(bb, (b + 1) * kBatch);
           }
         }
       } else {
         // The last stage: only elements below `length` are folded (a padded
         // +0.0 would turn a -0.0 total into +0.0).
         uint32_t c = 0;
-        for (; c + 4 <= count; c += 4) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(row + c);
-          acc = acc + v.x;
-          acc = acc + v.y;
-          acc = acc + v.z;
-          acc = acc + v.w;
+        for (; c + 4 <= count; c += 4) step4(*reinterpret_cast<const f32x4*>(row + c), c);
+        for (; c < count; ++c) {
+          if constexpr (kDot) acc = acc + arow[c] * row[c];
+          else acc = acc + row[c];
         }
-        for (; c < count; ++c) acc = acc + row[c];
       }
     }
     if (more) store((uint32_t)((s + 1) & 1));
@@ -160,12 +191,12 @@ __device__ __forceinline__ void sum_staged_body(const float* __restrict__ x, uin
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_sum_f32_staged_r##R(const float* __restrict__ x, uint64_t nrows, uint64_t length,          \
                                 float* __restrict__ out) {                                             \
-    sum_staged_body<R, true>(x, nrows, length, out);                                                   \
+    staged_fold_body<R, true, false>(x, nrows, length, nullptr, out);                                                   \
   }                                                                                                    \
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_sum_f32_staged_r##R##_u(const float* __restrict__ x, uint64_t nrows, uint64_t length,      \
                                     float* __restrict__ out) {                                         \
-    sum_staged_body<R, false>(x, nrows, length, out);                                                  \
+    staged_fold_body<R, false, false>(x, nrows, length, nullptr, out);                                                  \
   }
 TILER_SUM_STAGED(1)
 TILER_SUM_STAGED(4)

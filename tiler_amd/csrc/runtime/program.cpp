@@ -505,7 +505,8 @@ static void declare_live_k(Program& p, uint64_t bound) {
   p.nlive = 1;
 }
 
-tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Program& p, bool live_k) {
+tiler_hip_status plan_contract_strict_f32(const Target& t, uint64_t m, uint64_t n, uint64_t k, const uintptr_t* addr,
+                                          Program& p, bool live_k) {
   const uint32_t a = p.slot(mul_sat(mul_sat(m, k), 4), kSlotInput);
   const uint32_t b = p.slot(mul_sat(mul_sat(n, k), 4), kSlotInput);
   const uint32_t c = p.slot(mul_sat(mul_sat(m, n), 4), kSlotOutput);
@@ -515,6 +516,21 @@ tiler_hip_status plan_contract_strict_f32(uint64_t m, uint64_t n, uint64_t k, Pr
   if (m == 0 || n == 0) return TILER_HIP_OK;
   if (m > 0xffffffffull || n > 0xffffffffull || k > 0xffffffffull || (m + 15) / 16 > 65535)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
+  if (m <= 16 && k >= 64) {
+    // Few output rows (decode shapes): each output is the staged fold of the
+    // products along one row of B (contiguous in k), one workgroup row per
+    // output row, R output columns per workgroup chosen as for the serial
+    // fold by the output count.  With k live the 4-byte-load form takes any k.
+    const uint64_t outputs = m * n, cus = t.compute_units;
+    const uint32_t R = outputs <= cus ? 1 : outputs <= 4 * cus ? 4 : outputs <= 16 * cus ? 16 : 64;
+    const bool vec = !live_k && k % 4 == 0 && aligned16(addr[a]) && aligned16(addr[b]);
+    char name[40];
+    std::snprintf(name, sizeof(name), "tiler_contract_strict_f32_s%u%s", R, vec ? "" : "_u");
+    Launch& l = p.add(name, (uint32_t)((n + R - 1) / R), (uint32_t)m, 256)
+                    .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n);
+    (live_k ? l.live_u32(0) : l.u32((uint32_t)k)).ptr(c);
+    return TILER_HIP_OK;
+  }
   Launch& l = p.add("tiler_contract_strict_f32", (uint32_t)((n + 15) / 16), (uint32_t)((m + 15) / 16), 256)
                   .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n);
   (live_k ? l.live_u32(0) : l.u32((uint32_t)k)).ptr(c);

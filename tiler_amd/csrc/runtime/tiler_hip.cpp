@@ -170,6 +170,14 @@ const EntryRow kEntries[] = {
     {"tiler_widen_bf16_f32_v8", "convert-bf16-to-f32/widen", 2},
     {"tiler_widen_bf16_f32", "convert-bf16-to-f32/widen", 2},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_s1", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_s1_u", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_s4", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_s4_u", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_s16", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_s16_u", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_s64", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_s64_u", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_strict_bf16", "tensor-contraction-bf16/strict", 3},
     {"tiler_contract_strict_bf16_silu", "tensor-contraction-bf16/strict+silu", 3},
     {"tiler_rms_norm_f32_strict", "rms-norm-f32/strict", 3},
@@ -1501,7 +1509,8 @@ tiler_hip_status tiler_hip_contract_strict_f32(tiler_hip_context* ctx, const flo
                                                uint64_t k, float* c, tiler_hip_stream stream) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
-  tiler_hip_status st = tiler_rt::plan_contract_strict_f32(m, n, k, p);
+  const uintptr_t addr[3] = {(uintptr_t)a, (uintptr_t)b, (uintptr_t)c};
+  tiler_hip_status st = tiler_rt::plan_contract_strict_f32(target_of(ctx), m, n, k, addr, p);
   if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
   if (p.nlaunches && (!a || !b || !c)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<float*>(a), const_cast<float*>(b), c};
@@ -1875,7 +1884,7 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
                   : tiler_rt::plan_contract_general(t, r->dtype, *r->structure, r->variant, !c.reassociate, addr, p);
       else if (r->dtype == TILER_HIP_F32)
         st = r->variant == TILER_HIP_EPILOGUE_NONE
-                 ? tiler_rt::plan_contract_strict_f32(e[0], e[1], e[2], p, live)
+                 ? tiler_rt::plan_contract_strict_f32(t, e[0], e[1], e[2], addr, p, live)
                  : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the strict f32 contraction has no epilogue");
       else if (r->dtype == TILER_HIP_BF16)
         st = tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p, !c.reassociate, r->form, live);
