@@ -289,12 +289,18 @@ def test_strict_contraction_tails_and_signed_zero(ctx):
     (2, 3000, 64, 0),    # sixty-four columns, exactly one stage
     (1, 70, 4099, 0),    # one column per workgroup over two stages
     (4, 100, 512, 4),    # unaligned operands: 4-byte loads
+    (40, 70, 100, 0),    # m > 16: 16 x 16 blocked tiles, ragged edges and k tile
+    (33, 65, 77, 4),     # the same, unaligned
+    (512, 1000, 96, 0),  # 32 x 32 tiles (2 x 2 per thread), a ragged n edge
+    (2048, 2040, 70, 0), # 64 x 64 tiles (4 x 4 per thread), a ragged n edge and k tile
 ])
-def test_strict_contraction_few_rows_is_the_first_product_fold(ctx, m, n, k, offset):
-    """m <= 16 runs the staged fold of products (tiler_contract_strict_f32_s*):
-    still contraction.rs:558-630's fold, bit for bit, with values over 60
-    binades so any other order shows; row 0 of A all -0.0 against positive B
-    (a -0.0 total), a NaN in row 1, an inf against a zero in row 2."""
+def test_strict_contraction_staged_and_blocked_are_the_first_product_fold(ctx, m, n, k, offset):
+    """k >= 64 runs the staged fold of products for m <= 16
+    (tiler_contract_strict_f32_s*) and register-blocked tiles above
+    (tiler_contract_strict_f32_b16/_b32/_b64): still contraction.rs:558-630's fold,
+    bit for bit, with values over 60 binades so any other order shows; row 0
+    of A all -0.0 against positive B (a -0.0 total), a NaN in row 1, an inf
+    against a zero in row 2."""
     rng = np.random.default_rng(m * 1000 + n + k)
     a = (rng.standard_normal((m, k)) * np.exp2(rng.integers(-30, 30, (m, k)))).astype(np.float32)
     b = (rng.standard_normal((n, k)) * np.exp2(rng.integers(-30, 30, (n, k)))).astype(np.float32)

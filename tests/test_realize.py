@@ -152,6 +152,16 @@ def test_contraction_paths():
     strict = realize(L.PROGRAM_CONTRACTION, (40, 70, 9))
     assert strict.symbols == ["tiler_contract_strict_f32"] and strict.dispatches[0].grid == (5, 3, 1)
     _check_segments(strict)
+    # k >= 64: register-blocked tiles of 16, 32 or 64 by the work on the busiest CU; m <= 16: staged rows
+    assert realize(L.PROGRAM_CONTRACTION, (128, 1024, 3072)).symbols == ["tiler_contract_strict_f32_b16"]
+    blocked = realize(L.PROGRAM_CONTRACTION, (512, 3072, 1024))
+    assert blocked.symbols == ["tiler_contract_strict_f32_b32"] and blocked.dispatches[0].grid == (96, 16, 1)
+    big = realize(L.PROGRAM_CONTRACTION, (2048, 2040, 70))
+    assert big.symbols == ["tiler_contract_strict_f32_b64"] and big.dispatches[0].grid == (32, 32, 1)
+    few = realize(L.PROGRAM_CONTRACTION, (1, 1024, 1024))
+    assert few.symbols == ["tiler_contract_strict_f32_s4"] and few.dispatches[0].grid == (256, 1, 1)
+    for rz in (blocked, big, few):
+        _check_segments(rz)
 
 
 LIVE = L.REGION_ALIGNED16 | L.REGION_LIVE_EXTENT
@@ -165,7 +175,7 @@ def test_live_contracted_extent():
     argument segment for the dispatch to patch."""
     m, n, bound = 40, 70, 512
     f = realize(L.PROGRAM_CONTRACTION, (m, n, bound), flags=LIVE)
-    assert f.symbols == ["tiler_contract_strict_f32"]
+    assert f.symbols == ["tiler_contract_strict_f32_b16"]
     assert f.live_extents == [(0, 1, 1, bound)]
     assert [s for s, _ in f.slots] == [L.SLOT_INPUT, L.SLOT_INPUT, L.SLOT_OUTPUT]
     assert [b for _, b in f.slots] == [m * bound * 4, n * bound * 4, m * n * 4]

@@ -75,6 +75,105 @@ tiler_contract_strict_bf16_silu(const uint16_t* __restrict__ a, const uint16_t* 
   contract_strict_body<uint16_t, true>(a, b, m, n, k, c);
 }
 
+// Register-blocked: a workgroup of 16 x 16 threads owns a (16 TM) x (16 TN)
+// output tile and each thread TM x TN outputs (rows ty*TM.., columns
+// tx*TN..), every one of them the same ascending first-product fold; the
+// TM*TN chains of a thread interleave, so the dependent adds do not wait on
+// one another.  A and B k-tiles of 16 are loaded into registers one tile
+// ahead (coalesced along k) and stored transposed (k-major) into the other
+// LDS buffer, so each k step reads TM values of A and TN of B per thread for
+// TM*TN products.  Only k steps below k are folded: the zeros loaded past k
+// never enter a chain (a +0.0 product would turn a -0.0 total into +0.0).
+template <int TM, int TN>
+__device__ __forceinline__ void contract_strict_blocked_body(const float* __restrict__ a,
+                                                             const float* __restrict__ b, uint32_t m,
+                                                             uint32_t n, uint32_t k,
+                                                             float* __restrict__ c) {
+  constexpr uint32_t BM = 16 * TM, BN = 16 * TN, BK = 16;
+  __shared__ __align__(16) float as[2][BK][BM + 4];
+  __shared__ __align__(16) float bs[2][BK][BN + 4];
+  const uint32_t t = threadIdx.x, tx = t & 15u, ty = t >> 4;
+  const uint32_t i0 = blockIdx.y * BM, j0 = blockIdx.x * BN;
+  float ra[TM], rb[TN];  // this thread's share of the next k-tile: element t + 256 q
+  auto load = [&](uint32_t k0) {
+#pragma unroll
+    for (uint32_t q = 0; q < TM; ++q) {
+      const uint32_t e = t + 256u * q, r = e / BK, kk = k0 + e % BK;
+      ra[q] = (i0 + r < m && kk < k) ? a[(uint64_t)(i0 + r) * k + kk] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < TN; ++q) {
+      const uint32_t e = t + 256u * q, r = e / BK, kk = k0 + e % BK;
+      rb[q] = (j0 + r < n && kk < k) ? b[(uint64_t)(j0 + r) * k + kk] : 0.0f;
+    }
+  };
+  auto store = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t q = 0; q < TM; ++q) {
+      const uint32_t e = t + 256u * q;
+      as[buf][e % BK][e / BK] = ra[q];
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < TN; ++q) {
+      const uint32_t e = t + 256u * q;
+      bs[buf][e % BK][e / BK] = rb[q];
+    }
+  };
+  float acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = -0.0f;  // -0 + first product == first product
+  const uint32_t tiles = (k + BK - 1) / BK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (uint32_t kt = 0; kt < tiles; ++kt) {
+    const uint32_t buf = kt & 1u;
+    if (kt + 1 < tiles) load((kt + 1) * BK);
+    const uint32_t steps = k - kt * BK < BK ? k - kt * BK : BK;
+    for (uint32_t s = 0; s < steps; ++s) {
+      float fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = as[buf][s][ty * TM + i];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = bs[buf][s][tx * TN + j];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = acc[i][j] + fa[i] * fb[j];
+    }
+    if (kt + 1 < tiles) store(buf ^ 1u);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const uint32_t row = i0 + ty * TM + i;
+    if (row >= m) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint32_t col = j0 + tx * TN + j;
+      if (col < n) c[(uint64_t)row * n + col] = canon(acc[i][j]);
+    }
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_strict_f32_b16(const float* __restrict__ a, const float* __restrict__ b, uint32_t m, uint32_t n,
+                              uint32_t k, float* __restrict__ c) {
+  contract_strict_blocked_body<1, 1>(a, b, m, n, k, c);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_strict_f32_b32(const float* __restrict__ a, const float* __restrict__ b, uint32_t m, uint32_t n,
+                              uint32_t k, float* __restrict__ c) {
+  contract_strict_blocked_body<2, 2>(a, b, m, n, k, c);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_strict_f32_b64(const float* __restrict__ a, const float* __restrict__ b, uint32_t m, uint32_t n,
+                              uint32_t k, float* __restrict__ c) {
+  contract_strict_blocked_body<4, 4>(a, b, m, n, k, c);
+}
+
 // Few output rows: output row i = blockIdx.y is the staged strict fold
 // (tiler_sum_f32_staged_r*, reduce.hip) of the products of A's row i with B's
 // rows, which are contiguous in k -- the same first-product fold, ascending k,

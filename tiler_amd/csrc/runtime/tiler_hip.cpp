@@ -170,6 +170,9 @@ const EntryRow kEntries[] = {
     {"tiler_widen_bf16_f32_v8", "convert-bf16-to-f32/widen", 2},
     {"tiler_widen_bf16_f32", "convert-bf16-to-f32/widen", 2},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_b16", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_b32", "tensor-contraction-f32/strict", 3},
+    {"tiler_contract_strict_f32_b64", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_strict_f32_s1", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_strict_f32_s1_u", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_strict_f32_s4", "tensor-contraction-f32/strict", 3},
