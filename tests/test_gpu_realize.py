@@ -50,11 +50,13 @@ def _routed(ctx, rz, inputs, outputs):
             b.free()
 
 
-def test_serial_sum_routed(ctx):
-    rows, extent = 1000, 37
+@pytest.mark.parametrize("rows,extent,symbol", [(1000, 37, "tiler_sum_f32_staged_r256_u"),
+                                               (1000, 9, "tiler_sum_f32_serial"),
+                                               (3, 5000, "tiler_sum_f32_staged_r1")])
+def test_serial_sum_routed(ctx, rows, extent, symbol):
     x = np.random.default_rng(71).standard_normal((rows, extent)).astype(np.float32)
     rz = realize(L.PROGRAM_SERIAL_SUM, (rows, extent), topology=L.SUM_SERIAL, permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
-    assert rz.symbols == ["tiler_sum_f32_serial"]
+    assert rz.symbols == [symbol]
     (got,) = _routed(ctx, rz, [x], [(np.float32, (rows,))])
     assert np.array_equal(bits(got), bits(oracle.strict_sum(x, (rows, extent), 1)))
 

@@ -76,6 +76,9 @@ def _order_sensitive(rng, rows, extent):
     (20000, 64, 0),    # sixty-four rows per workgroup, one stage
     (17000, 65, 0),    # sixty-four rows, a second stage of one element
     (1, 70000, 0),     # one long row
+    (5000, 20, 0),     # rows of 16..63: 256 rows per workgroup, stages of 16
+    (300, 63, 0),      # the same, 4-byte loads, a ragged last stage
+    (257, 16, 4),      # one stage, an unaligned base, a second workgroup of one row
 ])
 def test_serial_sum_staged_rows_are_the_strict_fold(ctx, rows, extent, offset):
     """Rows of 64 or more elements are folded from LDS stages
@@ -110,6 +113,10 @@ def test_multipass_sum_matches_strict_partitioned_sum(ctx):
     x = (rng.standard_normal((9, 4096)) * 10).astype(np.float32)
     got = _sum_dev(ctx, x, 9, 4096, topology=L.SUM_MULTIPASS, partitions=64, per_partition=64)
     assert np.array_equal(bits(got), bits(oracle.strict_partitioned_sum(x, 9, 4096, 64, 64)))
+    # partitions of 16..63: the staged fold with 256 rows per workgroup
+    z = (rng.standard_normal((33, 1024)) * 10).astype(np.float32)
+    got = _sum_dev(ctx, z, 33, 1024, topology=L.SUM_MULTIPASS, partitions=32, per_partition=32)
+    assert np.array_equal(bits(got), bits(oracle.strict_partitioned_sum(z, 33, 1024, 32, 32)))
     # 70 x 64 partials exceed the context workspace: the stream-ordered allocation path
     y = (rng.standard_normal((70, 1024)) * 10).astype(np.float32)
     got = _sum_dev(ctx, y, 70, 1024, topology=L.SUM_MULTIPASS, partitions=64, per_partition=16)
@@ -147,6 +154,25 @@ def test_tree_sum_exact_sets_and_special_values(ctx):
     nan = np.ones(3000, np.float32)
     nan[1234] = f32(["0x7fc01234"])[0]
     assert bits(_sum_dev(ctx, nan, 1, 3000, topology=L.SUM_TREE))[0] == 0x7FC00000
+
+
+@pytest.mark.parametrize("rows,extent,offset", [(1000, 256, 0), (37, 255, 0), (4096, 64, 0), (5, 1, 0),
+                                                (9, 200, 4)])
+def test_tree_sum_short_rows_one_wave_each(ctx, rows, extent, offset):
+    """Rows of at most 256 run one wave per row (tiler_sum_f32_rows_w): the
+    same declared grouping as the 256-thread form, bit for bit."""
+    x = np.random.default_rng(rows + extent).uniform(-1, 1, (rows, extent)).astype(np.float32)
+    x[0, 0] = np.float32(2.0 ** 30)  # large enough that the grouping shows in the bits
+    dx = ctx.alloc(x.nbytes + offset)
+    do = ctx.alloc(rows * 4)
+    try:
+        dx.offset(offset).upload(x)
+        ctx.sum_f32(dx.offset(offset), rows, extent, do, topology=L.SUM_TREE)
+        got = do.download(np.float32, (rows,))
+    finally:
+        dx.free()
+        do.free()
+    assert np.array_equal(bits(got), bits(oracle.row_grouped_sum(x, rows, extent, 4, 4)))
 
 
 def test_tree_sum_rows_declared_grouping(ctx):

@@ -28,7 +28,7 @@ from tiler_amd.realize import propose, realize
 from tiler_amd.runtime import Refusal
 
 RE = L.PERMITS_REASSOCIATION
-P_ROW = 6317  # the profile's saturated_parallel_fold_steps
+P_ROW = 17870  # the profile's saturated_parallel_fold_steps
 
 
 def _check_proposals(offer):

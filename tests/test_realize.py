@@ -120,7 +120,12 @@ def test_softmax_and_sums():
     assert realize(L.PROGRAM_SERIAL_SUM, (64, 1000), topology=L.SUM_TREE, permissions=RE).symbols == ["tiler_sum_f32_rows"]
 
     mp = realize(L.PROGRAM_SERIAL_SUM, (3, 120), topology=L.SUM_MULTIPASS, grouping=(4, 30), permissions=RE)
-    assert mp.symbols == ["tiler_sum_f32_partials", "tiler_sum_f32_serial"]
+    # partitions of 30: pass 1 is the staged fold over 3 x 4 rows of 30 (stages of 16)
+    assert mp.symbols == ["tiler_sum_f32_staged_r256_u", "tiler_sum_f32_serial"]
+    assert realize(L.PROGRAM_SERIAL_SUM, (3, 120), topology=L.SUM_MULTIPASS, grouping=(12, 10),
+                   permissions=RE).symbols == ["tiler_sum_f32_partials", "tiler_sum_f32_serial"]
+    assert realize(L.PROGRAM_SERIAL_SUM, (9, 256), topology=L.SUM_TREE, permissions=RE).symbols == \
+        ["tiler_sum_f32_rows_w"]
     assert mp.slots[2] == (L.SLOT_SCRATCH, 3 * 4 * 4)
     _check_segments(mp)
 

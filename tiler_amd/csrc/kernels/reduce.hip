@@ -202,6 +202,7 @@ TILER_SUM_STAGED(1)
 TILER_SUM_STAGED(4)
 TILER_SUM_STAGED(16)
 TILER_SUM_STAGED(64)
+TILER_SUM_STAGED(256)  // rows of 16..63: stages of 16 elements, every lane folding a row
 
 // MultiPass pass 1: partials[r*P + p] = strict fold of
 // x[r*extent + p*chunk .. +chunk]; an empty partition commits +0.0.
@@ -323,6 +324,47 @@ tiler_sum_f32_grid_final(const float* __restrict__ partials, uint32_t G, uint64_
   for (uint32_t i = threadIdx.x; i < G; i += 256) acc = acc + partials[i];
   float total = block_sum256(acc, lds4);
   if (threadIdx.x == 0) out[0] = n == 0 ? 0.0f : canon(total);
+}
+
+// Rows of at most 256: the same grouping, one wave per row.  Thread t of the
+// 256-thread form folds elements 4t..4t+3, so for extent <= 256 only wave 0
+// holds contributors; waves 1-3 fold nothing and their butterflies give
+// -0.0, which the ascending fold of the four wave sums adds exactly
+// (w + -0.0 == w for every w).  The row's value is therefore wave 0's
+// butterfly alone, computed here by each wave for its own row (4 rows per
+// workgroup).  kVec: 16-byte loads (aligned x, extent a multiple of 4).
+template <bool kVec>
+__device__ __forceinline__ void sum_rows_wave_body(const float* __restrict__ x, uint64_t rows, uint32_t extent,
+                                                   float* __restrict__ out) {
+  const uint32_t l = threadIdx.x & 63u;
+  const uint64_t row = (uint64_t)blockIdx.x * 4u + (threadIdx.x >> 6);
+  if (row >= rows) return;  // a whole wave: no barrier below
+  const float* r = x + row * extent;
+  float acc = -0.0f;
+  const uint32_t p = 4u * l;
+  if (kVec) {
+    if (p < extent) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(r + p);
+      acc = acc + v.x;
+      acc = acc + v.y;
+      acc = acc + v.z;
+      acc = acc + v.w;
+    }
+  } else {
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e)
+      if (p + e < extent) acc = acc + r[p + e];
+  }
+  const float s = tiler::wave_sum_butterfly(acc);
+  if (l == 0) out[row] = canon(s);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_sum_f32_rows_w(const float* __restrict__ x, uint64_t rows, uint32_t extent, float* __restrict__ out) {
+  sum_rows_wave_body<true>(x, rows, extent, out);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_sum_f32_rows_w_u(const float* __restrict__ x, uint64_t rows, uint32_t extent, float* __restrict__ out) {
+  sum_rows_wave_body<false>(x, rows, extent, out);
 }
 
 // Many outputs: one 256-thread workgroup per row of `extent` contributors,

@@ -144,8 +144,9 @@ uint32_t tree_workgroups(const Target& t, uint64_t n) {
 // (slot `src`, row v at v * length) into `dst`.  Rows of 64 or more elements
 // are staged through LDS, R rows per workgroup with R the smallest of
 // 1, 4, 16, 64 that keeps to one workgroup per CU (64 beyond), so that the
-// folding chains of few long rows get a SIMD each; shorter rows take one lane
-// per row, whose loads are already near one another.
+// folding chains of few long rows get a SIMD each; rows of 16..63 in stages
+// of 16, 256 rows per workgroup; shorter rows take one lane per row, whose
+// loads are already near one another.
 static void add_serial_fold(const Target& t, uint32_t src, bool src_aligned, uint64_t nrows, uint64_t length,
                             uint32_t dst, Program& p) {
   if (length >= 64) {
@@ -155,6 +156,12 @@ static void add_serial_fold(const Target& t, uint32_t src, bool src_aligned, uin
     char name[40];
     std::snprintf(name, sizeof(name), "tiler_sum_f32_staged_r%u%s", R, vec ? "" : "_u");
     p.add(name, (uint32_t)((nrows + R - 1) / R), 1, 256).ptr(src).u64(nrows).u64(length).ptr(dst);
+    return;
+  }
+  if (length >= 16) {  // stages of 16 elements, 256 rows per workgroup, every lane folding
+    const bool vec = src_aligned && length % 4 == 0;
+    p.add(vec ? "tiler_sum_f32_staged_r256" : "tiler_sum_f32_staged_r256_u", (uint32_t)((nrows + 255) / 256), 1, 256)
+        .ptr(src).u64(nrows).u64(length).ptr(dst);
     return;
   }
   p.add("tiler_sum_f32_serial", (uint32_t)((nrows + 255) / 256), 1, 256)
@@ -168,7 +175,7 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
   switch (sp.topology) {
     case TILER_HIP_SUM_SERIAL:
       if (rows == 0) return TILER_HIP_OK;
-      if ((rows + 255) / 256 > 0x7fffffffull || (extent >= 64 && rows > 0x7fffffffull))
+      if ((rows + 255) / 256 > 0x7fffffffull || (extent >= 16 && rows > 0x7fffffffull))
         return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
       add_serial_fold(t, x, aligned16(addr[x]), rows, extent, out, p);
       return TILER_HIP_OK;
@@ -177,12 +184,12 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
       if (rows == 0) return TILER_HIP_OK;
       if (P == 0 || (c != 0 && P > UINT64_MAX / c) || P * c != extent)
         return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "partitions do not cover the axis exactly");
-      if (mul_sat(rows, P) / 256 >= 0x7fffffffull || (c >= 64 && mul_sat(rows, P) > 0x7fffffffull))
+      if (mul_sat(rows, P) / 256 >= 0x7fffffffull || (c >= 16 && mul_sat(rows, P) > 0x7fffffffull))
         return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more partitions than the launch grid holds");
       const uint32_t part = p.slot(mul_sat(mul_sat(rows, P), 4), kSlotScratch);
       // With exact coverage partition p of row r is the contiguous run
       // (r*P + p) * c: pass 1 is the serial fold of rows*P rows of c.
-      if (c >= 64)
+      if (c >= 16)
         add_serial_fold(t, x, aligned16(addr[x]), rows * P, c, part, p);
       else
         p.add("tiler_sum_f32_partials", (uint32_t)((rows * P + 255) / 256), 1, 256)
@@ -212,6 +219,12 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
         return TILER_HIP_OK;
       }
       if (rows > 0x7fffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+      if (extent >= 1 && extent <= 256) {  // the same grouping, one wave per row
+        p.add(aligned16(addr[x]) && extent % 4 == 0 ? "tiler_sum_f32_rows_w" : "tiler_sum_f32_rows_w_u",
+              (uint32_t)((rows + 3) / 4), 1, 256)
+            .ptr(x).u64(rows).u32((uint32_t)extent).ptr(out);
+        return TILER_HIP_OK;
+      }
       p.add("tiler_sum_f32_rows", (uint32_t)rows, 1, 256).ptr(x).u64(extent).ptr(out);
       return TILER_HIP_OK;
     }
