@@ -70,7 +70,7 @@ def test_strict_contract_selects_the_serial_row_and_contraction_kernels():
     assert realize(L.PROGRAM_RMS_NORM, (5, 20000), scalars=(EPS,)).symbols == ["tiler_rms_norm_f32_strict"]
     assert realize(L.PROGRAM_SOFTMAX, (32, 131072)).symbols == ["tiler_softmax_f32_strict"]
     c = realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, variant=L.EPILOGUE_SILU)
-    assert c.symbols == ["tiler_contract_strict_bf16_silu"] and c.dispatches[0].grid == (256, 256, 1)
+    assert c.symbols == ["tiler_contract_strict_bf16_silu_b64"] and c.dispatches[0].grid == (64, 64, 1)
     assert realize(L.PROGRAM_CONTRACTION, (40, 70, 9), dtype=L.BF16).symbols == ["tiler_contract_strict_bf16"]
     # the same regions under REASSOCIATE_F32 get the grouped forms
     assert realize(L.PROGRAM_SOFTMAX, (32, 131072), permissions=RE).symbols[-1] == "tiler_softmax_f32_rowsync_a"

@@ -341,10 +341,15 @@ def test_strict_softmax_is_the_reference_fold(ctx):
         assert np.array_equal(bits(got).reshape(-1), bits(want).reshape(-1)), (rows, extent)
 
 
+@pytest.mark.parametrize("m,n,k,form", [(70, 90, 300, "b16"), (512, 1000, 96, "b32"), (2048, 2040, 70, "b64"),
+                                        (40, 70, 9, "")])
 @pytest.mark.parametrize("silu", [False, True])
-def test_strict_bf16_contraction(ctx, silu):
-    rng = np.random.default_rng(23)
-    m, n, k = 70, 90, 300
+def test_strict_bf16_contraction(ctx, silu, m, n, k, form):
+    """The strict bf16 contraction (no reassociation): register-blocked tiles
+    of 16/32/64 for k >= 64, one output per thread below; the first-product
+    fold on exactly widened operands, then (SiLU) the reference SiLU, one
+    narrowing -- bit for bit."""
+    rng = np.random.default_rng(23 + m)
     a = oracle.bf16_narrow(rng.standard_normal((m, k)).astype(np.float32)).reshape(m, k)
     b = oracle.bf16_narrow(rng.standard_normal((n, k)).astype(np.float32)).reshape(n, k)
     ref = oracle.contract_strict_f32(bf16_widen(a), bf16_widen(b), m, n, k)
@@ -353,7 +358,8 @@ def test_strict_bf16_contraction(ctx, silu):
     want = oracle.bf16_narrow(ref).reshape(m, n)
     rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16,
                  variant=L.EPILOGUE_SILU if silu else L.EPILOGUE_NONE, ctx=ctx)
-    assert rz.symbols[0].startswith("tiler_contract_strict_bf16")
+    assert rz.symbols[0].startswith("tiler_contract_strict_bf16") and rz.symbols[0].endswith(form)
+    print(f"[strict bf16] {rz.symbols[0]} m={m} n={n} k={k}", flush=True)
     bufs = [ctx.to_device(a), ctx.to_device(b), ctx.alloc(m * n * 2)]
     try:
         route(ctx, rz, bufs)

@@ -117,10 +117,14 @@ def test_multipass_sum_matches_strict_partitioned_sum(ctx):
     z = (rng.standard_normal((33, 1024)) * 10).astype(np.float32)
     got = _sum_dev(ctx, z, 33, 1024, topology=L.SUM_MULTIPASS, partitions=32, per_partition=32)
     assert np.array_equal(bits(got), bits(oracle.strict_partitioned_sum(z, 33, 1024, 32, 32)))
-    # 70 x 64 partials exceed the context workspace: the stream-ordered allocation path
     y = (rng.standard_normal((70, 1024)) * 10).astype(np.float32)
     got = _sum_dev(ctx, y, 70, 1024, topology=L.SUM_MULTIPASS, partitions=64, per_partition=16)
     assert np.array_equal(bits(got), bits(oracle.strict_partitioned_sum(y, 70, 1024, 64, 16)))
+    # 2100 x 512 partials (4.3 MB) exceed the context's 256 KiB partials
+    # workspace: the stream-ordered allocation path
+    w = (rng.standard_normal((2100, 1024)) * 10).astype(np.float32)
+    got = _sum_dev(ctx, w, 2100, 1024, topology=L.SUM_MULTIPASS, partitions=512, per_partition=2)
+    assert np.array_equal(bits(got), bits(oracle.strict_partitioned_sum(w, 2100, 1024, 512, 2)))
 
 
 @pytest.mark.parametrize("major", [False, True])

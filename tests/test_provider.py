@@ -137,7 +137,7 @@ def test_contraction_forms():
     _check_proposals(o)
     assert o.strategies() == ["tiler.region.serial-baseline", "gfx950.contraction.mfma-staged-256",
                               "gfx950.contraction.mfma-staged-128", "gfx950.contraction.mfma-general-128"]
-    assert o.proposals[0].symbols == ["tiler_contract_strict_bf16_silu"]
+    assert o.proposals[0].symbols == ["tiler_contract_strict_bf16_silu_b64"]
     by = {p.strategy: p for p in o.proposals}
     assert by["gfx950.contraction.mfma-staged-256"].workgroups == [256]
     assert by["gfx950.contraction.mfma-staged-256"].workgroup_threads == [1024]

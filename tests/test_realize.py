@@ -201,7 +201,7 @@ def test_live_contracted_extent():
                 form=L.FORM_CONTRACT_GENERAL_128)
     assert g.symbols == ["tiler_contract_bf16_g128_k"]
     s = realize(L.PROGRAM_CONTRACTION, (300, 264, 192), dtype=L.BF16, variant=L.EPILOGUE_SILU, flags=LIVE)
-    assert s.symbols == ["tiler_contract_strict_bf16_silu"] and s.dispatches[0].extents == [(0, 24)]
+    assert s.symbols == ["tiler_contract_strict_bf16_silu_b16"] and s.dispatches[0].extents == [(0, 24)]
     # zero work still declares the extent (the route supplies it and skips the dispatch)
     z = realize(L.PROGRAM_CONTRACTION, (0, 64, 64), dtype=L.BF16, flags=LIVE)
     assert z.raw.entry_count == 0 and z.live_extents == [(0, 1, 1, 64)]

@@ -84,11 +84,18 @@ tiler_contract_strict_bf16_silu(const uint16_t* __restrict__ a, const uint16_t* 
 // LDS buffer, so each k step reads TM values of A and TN of B per thread for
 // TM*TN products.  Only k steps below k are folded: the zeros loaded past k
 // never enter a chain (a +0.0 product would turn a -0.0 total into +0.0).
-template <int TM, int TN>
-__device__ __forceinline__ void contract_strict_blocked_body(const float* __restrict__ a,
-                                                             const float* __restrict__ b, uint32_t m,
-                                                             uint32_t n, uint32_t k,
-                                                             float* __restrict__ c) {
+//
+// T = uint16_t: bf16 operands widened exactly on load, then (kSilu) the
+// reference SiLU and one bf16 narrowing on commit -- the strict bf16 form.
+template <int TM, int TN, typename T = float, bool kSilu = false>
+__device__ __forceinline__ void contract_strict_blocked_body(const T* __restrict__ a, const T* __restrict__ b,
+                                                             uint32_t m, uint32_t n, uint32_t k,
+                                                             T* __restrict__ c) {
+  constexpr bool kBf16 = sizeof(T) == 2;
+  auto widen = [](T v) -> float {
+    if constexpr (kBf16) return tiler::bf16_widen(v);
+    else return v;
+  };
   constexpr uint32_t BM = 16 * TM, BN = 16 * TN, BK = 16;
   __shared__ __align__(16) float as[2][BK][BM + 4];
   __shared__ __align__(16) float bs[2][BK][BN + 4];
@@ -99,12 +106,12 @@ __device__ __forceinline__ void contract_strict_blocked_body(const float* __rest
 #pragma unroll
     for (uint32_t q = 0; q < TM; ++q) {
       const uint32_t e = t + 256u * q, r = e / BK, kk = k0 + e % BK;
-      ra[q] = (i0 + r < m && kk < k) ? a[(uint64_t)(i0 + r) * k + kk] : 0.0f;
+      ra[q] = (i0 + r < m && kk < k) ? widen(a[(uint64_t)(i0 + r) * k + kk]) : 0.0f;
     }
 #pragma unroll
     for (uint32_t q = 0; q < TN; ++q) {
       const uint32_t e = t + 256u * q, r = e / BK, kk = k0 + e % BK;
-      rb[q] = (j0 + r < n && kk < k) ? b[(uint64_t)(j0 + r) * k + kk] : 0.0f;
+      rb[q] = (j0 + r < n && kk < k) ? widen(b[(uint64_t)(j0 + r) * k + kk]) : 0.0f;
     }
   };
   auto store = [&](uint32_t buf) {
@@ -153,7 +160,11 @@ __device__ __forceinline__ void contract_strict_blocked_body(const float* __rest
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const uint32_t col = j0 + tx * TN + j;
-      if (col < n) c[(uint64_t)row * n + col] = canon(acc[i][j]);
+      if (col >= n) continue;
+      float v = canon(acc[i][j]);
+      if (kSilu) v = tiler::silu_f32(v);
+      if constexpr (kBf16) c[(uint64_t)row * n + col] = (uint16_t)tiler::bf16_narrow(v);
+      else c[(uint64_t)row * n + col] = v;
     }
   }
 }
@@ -168,6 +179,22 @@ tiler_contract_strict_f32_b32(const float* __restrict__ a, const float* __restri
                               uint32_t k, float* __restrict__ c) {
   contract_strict_blocked_body<2, 2>(a, b, m, n, k, c);
 }
+#define TILER_CONTRACT_STRICT_BF16_BLOCKED(EDGE, T)                                                    \
+  extern "C" __global__ void __launch_bounds__(256)                                                    \
+      tiler_contract_strict_bf16_b##EDGE(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,\
+                                         uint32_t m, uint32_t n, uint32_t k, uint16_t* __restrict__ c) {\
+    contract_strict_blocked_body<T, T, uint16_t, false>(a, b, m, n, k, c);                            \
+  }                                                                                                    \
+  extern "C" __global__ void __launch_bounds__(256)                                                    \
+      tiler_contract_strict_bf16_silu_b##EDGE(const uint16_t* __restrict__ a,                          \
+                                              const uint16_t* __restrict__ b, uint32_t m, uint32_t n,  \
+                                              uint32_t k, uint16_t* __restrict__ c) {                  \
+    contract_strict_blocked_body<T, T, uint16_t, true>(a, b, m, n, k, c);                             \
+  }
+TILER_CONTRACT_STRICT_BF16_BLOCKED(16, 1)
+TILER_CONTRACT_STRICT_BF16_BLOCKED(32, 2)
+TILER_CONTRACT_STRICT_BF16_BLOCKED(64, 4)
+
 extern "C" __global__ void __launch_bounds__(256)
 tiler_contract_strict_f32_b64(const float* __restrict__ a, const float* __restrict__ b, uint32_t m, uint32_t n,
                               uint32_t k, float* __restrict__ c) {

@@ -518,6 +518,26 @@ static void declare_live_k(Program& p, uint64_t bound) {
   p.nlive = 1;
 }
 
+// Register-blocked strict tiles of 16·T x 16·T, T x T outputs per thread,
+// T in {1, 2, 4}: the one with the least work on the busiest CU -- rounds of
+// tiles over the CUs x outputs per tile x the time per output step, relative
+// weights 31 : 20 : 18 (T = 1 measured 1.4-1.7 x T = 2 per output step on the
+// 128 x 1024 x 3072 and 128 x 3072 x 1024 cells; T = 4 taken a tenth below
+// T = 2).  Returns T.
+static uint32_t strict_tile(const Target& t, uint64_t m, uint64_t n) {
+  const uint64_t cus = t.compute_units;
+  uint32_t best = 1;
+  uint64_t best_cost = UINT64_MAX;
+  for (uint32_t T : {1u, 2u, 4u}) {
+    const uint64_t edge = 16ull * T;
+    const uint64_t tiles = ((m + edge - 1) / edge) * ((n + edge - 1) / edge);
+    const uint64_t weight = T == 1 ? 31 : T == 2 ? 20 : 18;
+    const uint64_t cost = mul_sat(mul_sat((tiles + cus - 1) / cus, edge * edge), weight);
+    if (cost < best_cost) best_cost = cost, best = T;
+  }
+  return best;
+}
+
 tiler_hip_status plan_contract_strict_f32(const Target& t, uint64_t m, uint64_t n, uint64_t k, const uintptr_t* addr,
                                           Program& p, bool live_k) {
   const uint32_t a = p.slot(mul_sat(mul_sat(m, k), 4), kSlotInput);
@@ -545,22 +565,7 @@ tiler_hip_status plan_contract_strict_f32(const Target& t, uint64_t m, uint64_t 
     return TILER_HIP_OK;
   }
   if (k >= 64) {
-    // Register-blocked tiles of 16·T x 16·T, T x T outputs per thread,
-    // T in {1, 2, 4}: the one with the least work on the busiest CU -- rounds
-    // of tiles over the CUs x outputs per tile x the time per output step,
-    // relative weights 31 : 20 : 18 (T = 1 measured 1.4-1.7 x T = 2 per
-    // output step on the 128 x 1024 x 3072 and 128 x 3072 x 1024 cells; T = 4
-    // taken a tenth below T = 2).
-    const uint64_t cus = t.compute_units;
-    uint32_t best = 0;
-    uint64_t best_cost = UINT64_MAX;
-    for (uint32_t T : {1u, 2u, 4u}) {
-      const uint64_t edge = 16ull * T;
-      const uint64_t tiles = ((m + edge - 1) / edge) * ((n + edge - 1) / edge);
-      const uint64_t weight = T == 1 ? 31 : T == 2 ? 20 : 18;
-      const uint64_t cost = mul_sat(mul_sat((tiles + cus - 1) / cus, edge * edge), weight);
-      if (cost < best_cost) best_cost = cost, best = T;
-    }
+    const uint32_t best = strict_tile(t, m, n);
     const uint32_t tile = 16 * best;
     static const char* const names[] = {nullptr, "tiler_contract_strict_f32_b16", "tiler_contract_strict_f32_b32",
                                         nullptr, "tiler_contract_strict_f32_b64"};
@@ -597,7 +602,17 @@ tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uin
     if (m > 0xffffffffull || n > 0xffffffffull || k > 0xffffffffull || (m + 15) / 16 > 65535 ||
         (n + 15) / 16 > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "contraction extents beyond the launch profile");
-    Launch& l = p.add(epilogue == TILER_HIP_EPILOGUE_SILU ? "tiler_contract_strict_bf16_silu" : "tiler_contract_strict_bf16",
+    const bool silu = epilogue == TILER_HIP_EPILOGUE_SILU;
+    if (k >= 64) {  // register-blocked tiles, chosen as for the f32 form
+      const uint32_t T = strict_tile(t, m, n), tile = 16 * T;
+      char name[48];
+      std::snprintf(name, sizeof(name), "tiler_contract_strict_bf16_%sb%u", silu ? "silu_" : "", tile);
+      Launch& l = p.add(name, (uint32_t)((n + tile - 1) / tile), (uint32_t)((m + tile - 1) / tile), 256)
+                      .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n);
+      (live_k ? l.live_u32(0) : l.u32((uint32_t)k)).ptr(c);
+      return TILER_HIP_OK;
+    }
+    Launch& l = p.add(silu ? "tiler_contract_strict_bf16_silu" : "tiler_contract_strict_bf16",
                       (uint32_t)((n + 15) / 16), (uint32_t)((m + 15) / 16), 256)
                     .ptr(a).ptr(b).u32((uint32_t)m).u32((uint32_t)n);
     (live_k ? l.live_u32(0) : l.u32((uint32_t)k)).ptr(c);

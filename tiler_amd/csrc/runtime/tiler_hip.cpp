@@ -187,6 +187,12 @@ const EntryRow kEntries[] = {
     {"tiler_contract_strict_f32_s64_u", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_strict_bf16", "tensor-contraction-bf16/strict", 3},
     {"tiler_contract_strict_bf16_silu", "tensor-contraction-bf16/strict+silu", 3},
+    {"tiler_contract_strict_bf16_b16", "tensor-contraction-bf16/strict", 3},
+    {"tiler_contract_strict_bf16_b32", "tensor-contraction-bf16/strict", 3},
+    {"tiler_contract_strict_bf16_b64", "tensor-contraction-bf16/strict", 3},
+    {"tiler_contract_strict_bf16_silu_b16", "tensor-contraction-bf16/strict+silu", 3},
+    {"tiler_contract_strict_bf16_silu_b32", "tensor-contraction-bf16/strict+silu", 3},
+    {"tiler_contract_strict_bf16_silu_b64", "tensor-contraction-bf16/strict+silu", 3},
     {"tiler_rms_norm_f32_strict", "rms-norm-f32/strict", 3},
     {"tiler_rms_norm_bf16_strict", "rms-norm/bf16/strict", 3},
     {"tiler_softmax_f32_strict", "softmax-f32/strict", 2},
