@@ -369,14 +369,33 @@ tiler_sum_f32_rows_w_u(const float* __restrict__ x, uint64_t rows, uint32_t exte
 
 // Many outputs: one 256-thread workgroup per row of `extent` contributors,
 // grouping (vec 4, waves 4): thread t folds elements p with (p/4)%256 == t in
-// ascending p, then block_sum256.
+// ascending p, then block_sum256.  On a 16-byte-aligned row the whole
+// 1024-element tiles go four at a time, their loads issued before their adds
+// (a workgroup per row is otherwise latency-bound: one load in flight per
+// thread); the adds keep the order.
 extern "C" __global__ void __launch_bounds__(256)
 tiler_sum_f32_rows(const float* __restrict__ x, uint64_t extent, float* __restrict__ out) {
   __shared__ float lds4[4];
   const uint32_t t = threadIdx.x;
   const float* row = x + (uint64_t)blockIdx.x * extent;
   float acc = -0.0f;
-  for (uint64_t base = 0; base < extent; base += 1024) {
+  uint64_t base = 0;
+  if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {  // uniform across the workgroup
+    const f32x4* r4 = reinterpret_cast<const f32x4*>(row);
+    for (; base + 4096 <= extent; base += 4096) {
+      f32x4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = __builtin_nontemporal_load(&r4[(base >> 2) + 256u * j + t]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc = acc + v[j].x;
+        acc = acc + v[j].y;
+        acc = acc + v[j].z;
+        acc = acc + v[j].w;
+      }
+    }
+  }
+  for (; base < extent; base += 1024) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       uint64_t p = base + 4ull * t + e;
