@@ -166,8 +166,8 @@ int main() {
     sp.rounds = pick(r);
     Program p[10];
     plan_sum_f32(t, pick(r), pick(r), sp, addr, p[0]);
-    plan_rms_norm((uint32_t)(r() % 3), (int32_t)(r() % 2), pick(r), pick(r), r() % 2 ? 0x3727C5ACu : (uint32_t)r(),
-                  addr, p[1]);
+    plan_rms_norm(t, (uint32_t)(r() % 3), (int32_t)(r() % 2), pick(r), pick(r), r() % 2 ? 0x3727C5ACu : (uint32_t)r(),
+                  addr, p[1], r() % 3 == 0);
     plan_softmax_f32(r() % 2 ? Mode::Direct : Mode::Realized, t, pick(r), pick(r), addr, p[2], r() % 4 == 0,
                      (uint32_t)(r() % 8));
     plan_map(mode, (uint32_t)(r() % 5), (uint32_t)(r() % 3), (int32_t)(r() % 2), pick(r), 1.0f, 2.0f, addr, p[3]);

@@ -296,7 +296,7 @@ def _route_rows(ctx, program, x, w=None, dtype=L.F32, eps=0, broadcast=True):
     rows, extent = x.shape
     flags = L.REGION_ALIGNED16 | (L.REGION_OPERAND_BROADCAST if broadcast else 0)
     rz = realize(program, (rows, extent), dtype=dtype, scalars=(eps,), flags=flags, ctx=ctx)
-    assert rz.symbols[-1].endswith("_strict"), rz.symbols
+    assert "_strict" in rz.symbols[-1], rz.symbols
     bufs = [ctx.to_device(x)] + ([ctx.to_device(w)] if w is not None else []) + [ctx.alloc(x.nbytes)]
     try:
         route(ctx, rz, bufs)
@@ -325,6 +325,47 @@ def test_strict_rms_norm_is_the_reference_fold(ctx):
                                 0x3727C5AC)
     got = _route_rows(ctx, L.PROGRAM_RMS_NORM, xb, wb, dtype=L.BF16, eps=0x3727C5AC)
     assert np.array_equal(got.reshape(-1), oracle.bf16_narrow(wantf).reshape(-1))
+
+
+@pytest.mark.parametrize("rows,extent,dtype,broadcast,form", [
+    (8192, 4096, L.BF16, True, "_strict_r16"),  # the C2 configuration
+    (1500, 300, L.F32, True, "_strict_r4"),
+    (20000, 64, L.BF16, True, "_strict_r64"),   # one stage
+    (700, 1001, L.F32, False, "_strict_r1_u"),  # 4-byte loads, a weight row per row, a ragged stage
+    (300, 1030, L.BF16, True, "_strict_r1_u"),
+])
+def test_strict_rms_norm_staged_rows(ctx, rows, extent, dtype, broadcast, form):
+    """Rows of >= 64 run the staged strict fold (tiler_rms_norm_*_strict_r*):
+    the reference's serial fold of the squares, then its division, eps and
+    certified rsqrt, bit for bit against the oracle (bf16: on exactly widened
+    values, one narrowing).  Row 0 is all zeros (0 / N + eps), row 1 holds a
+    NaN and row 2 an infinity."""
+    rng = np.random.default_rng(rows + extent)
+    x = rng.standard_normal((rows, extent)).astype(np.float32) * np.float32(3.0)
+    x[0] = 0.0
+    x[1, extent // 2] = np.nan
+    x[2, 0] = np.inf
+    w = rng.normal(1.0, 0.1, extent if broadcast else (rows, extent)).astype(np.float32)
+    if dtype == L.BF16:
+        x, w = oracle.bf16_narrow(x).reshape(x.shape), oracle.bf16_narrow(w).reshape(w.shape)
+        xf, wf = bf16_widen(x), bf16_widen(w)
+    else:
+        xf, wf = x, w
+    flags = L.REGION_ALIGNED16 | (L.REGION_OPERAND_BROADCAST if broadcast else 0)
+    rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=dtype, scalars=(0x3727C5AC,), flags=flags, ctx=ctx)
+    assert rz.symbols[-1].endswith(form), rz.symbols
+    print(f"[strict rms] {rz.symbols[-1]} rows={rows} extent={extent}", flush=True)
+    bufs = [ctx.to_device(x), ctx.to_device(w), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[-1].download(x.dtype, x.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    want = oracle.rms_norm_f32(xf, np.broadcast_to(wf, xf.shape).copy(), xf.shape, 1, 0x3727C5AC).reshape(rows, extent)
+    if dtype == L.BF16:
+        want = oracle.bf16_narrow(want).reshape(rows, extent)
+    assert np.array_equal(bits(got) if dtype == L.F32 else got, bits(want) if dtype == L.F32 else want)
 
 
 def test_strict_softmax_is_the_reference_fold(ctx):

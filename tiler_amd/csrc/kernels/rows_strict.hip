@@ -14,6 +14,8 @@
 // (model.rs:906-912), so the wave computes it with a butterfly.  The
 // epilogue (scale or reciprocal multiply, weight, narrowing) runs on every
 // lane and re-reads the row.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -116,7 +118,187 @@ __device__ __forceinline__ void softmax_strict_body(const float* __restrict__ x,
   for (uint32_t i = lane; i < extent; i += 64) yr[i] = tiler::canon(tiler::exp_f32_cr(xr[i] - m) * r);
 }
 
+// Strict RMSNorm over many rows, staged like the strict serial sum
+// (reduce.hip, tiler_sum_f32_staged_r*).
+// * Each 256-thread workgroup serves R rows. Stage s holds C = 4096/R
+//   elements of each row.
+// * All threads load stage s+1, coalesced (16-byte loads: kVec), and store
+//   the squares fl(x*x) of the exactly widened elements into the other LDS
+//   buffer.
+// * Lane r/4 of wave r%4 folds row r's squares in ascending order, with the
+//   next batch of LDS reads in flight. One wave instruction advances R/4
+//   rows' chains, where one wave per row spent a whole instruction slot on
+//   one lane's add.
+// * The fold starts from -0.0. A square is never -0.0, so -0.0 plus the
+//   first square is the first square.
+// * Then, per row, rms_norm.rs:177-187: the division by N, + eps, the
+//   certified rsqrt. All threads write y = canon(w * fl(x * s)), re-reading x.
+template <typename T, int R, bool kVec>
+__device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, const T* __restrict__ w,
+                                                       uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,
+                                                       uint32_t extent, float eps) {
+  constexpr bool kBf16 = sizeof(T) == 2;
+  constexpr uint32_t C = 4096 / R;
+  constexpr uint32_t kStride = C + 4;
+  constexpr uint32_t W = kVec ? 16 / sizeof(T) : 1;  // elements per load
+  constexpr uint32_t kRowPieces = C / W;
+  constexpr uint32_t kPer = 4096 / W / 256;
+  typedef typename std::conditional<kVec, u32x4, T>::type raw;
+  __shared__ __align__(16) float stage[2][R * kStride];
+  __shared__ float scale[R];
+  const uint32_t t = threadIdx.x;
+  const uint64_t row0 = (uint64_t)blockIdx.x * R;
+  const uint32_t stages = (extent + C - 1) / C;
+  auto widen = [](uint32_t bits) -> float {
+    if constexpr (kBf16) return tiler::bf16_widen(bits);
+    else return __uint_as_float(bits);
+  };
+  raw reg[kPer];
+  auto load = [&](uint32_t s) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      const uint32_t e = s * C + (q % kRowPieces) * W;
+      if (row0 + r < rows && e < extent) reg[i] = *reinterpret_cast<const raw*>(x + (row0 + r) * extent + e);
+      else reg[i] = raw{};
+    }
+  };
+  auto store = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      float* dst = &stage[buf][r * kStride + (q % kRowPieces) * W];
+      if constexpr (!kVec) {
+        const float v = kBf16 ? tiler::bf16_widen(reg[i]) : (float)reg[i];
+        *dst = v * v;
+      } else if constexpr (kBf16) {  // 8 bf16 -> 8 squares
+        const u32x4 u = reg[i];
+        f32x4 lo, hi;
+        lo.x = widen(u.x & 0xffffu); lo.y = widen(u.x >> 16); lo.z = widen(u.y & 0xffffu); lo.w = widen(u.y >> 16);
+        hi.x = widen(u.z & 0xffffu); hi.y = widen(u.z >> 16); hi.z = widen(u.w & 0xffffu); hi.w = widen(u.w >> 16);
+        *reinterpret_cast<f32x4*>(dst) = lo * lo;
+        *reinterpret_cast<f32x4*>(dst + 4) = hi * hi;
+      } else {
+        const u32x4 u = reg[i];
+        f32x4 v;
+        v.x = widen(u.x); v.y = widen(u.y); v.z = widen(u.z); v.w = widen(u.w);
+        *reinterpret_cast<f32x4*>(dst) = v * v;
+      }
+    }
+  };
+  const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
+  const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < rows;
+  float acc = -0.0f;
+  if (stages > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (uint32_t s = 0; s < stages; ++s) {
+    const bool more = s + 1 < stages;
+    if (more) load(s + 1);
+    if (folds) {
+      const float* row = &stage[s & 1][fr * kStride];
+      const uint32_t count = extent - s * C < C ? extent - s * C : C;
+      if (count == C) {
+        constexpr uint32_t kBatch = C / 4 < 8 ? C / 4 : 8;
+        constexpr uint32_t kBatches = C / 4 / kBatch;
+        const f32x4* rv = reinterpret_cast<const f32x4*>(row);
+        f32x4 ba[kBatch], bb[kBatch];
+        auto add_batch = [&](const f32x4* v) {
+#pragma unroll
+          for (uint32_t j = 0; j < kBatch; ++j) {
+            acc = acc + v[j].x;
+            acc = acc + v[j].y;
+            acc = acc + v[j].z;
+            acc = acc + v[j].w;
+          }
+        };
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) ba[j] = rv[j];
+        for (uint32_t b = 0; b < kBatches; b += 2) {
+          if (b + 1 < kBatches) {
+#pragma unroll
+            for (uint32_t j = 0; j < kBatch; ++j) bb[j] = rv[(b + 1) * kBatch + j];
+          }
+          add_batch(ba);
+          if (b + 1 < kBatches) {
+            if (b + 2 < kBatches) {
+#pragma unroll
+              for (uint32_t j = 0; j < kBatch; ++j) ba[j] = rv[(b + 2) * kBatch + j];
+            }
+            add_batch(bb);
+          }
+        }
+      } else {
+        for (uint32_t c = 0; c < count; ++c) acc = acc + row[c];
+      }
+    }
+    if (more) store((s + 1) & 1u);
+    __syncthreads();
+  }
+  if (folds) scale[fr] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
+  __syncthreads();
+  for (uint32_t r = 0; r < (uint32_t)R; ++r) {
+    if (row0 + r >= rows) break;
+    const float sc = scale[r];
+    const uint64_t base = (row0 + r) * extent, wbase = (row0 + r) * w_row_stride;
+    if constexpr (kVec) {
+      for (uint32_t e = t * W; e < extent; e += 256u * W) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(x + base + e);
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(w + wbase + e);
+        u32x4 out;
+        if constexpr (kBf16) {
+          auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
+            return tiler::bf16_narrow(tiler::canon(widen(wb) * (widen(xb) * sc)));
+          };
+          out.x = one(xv.x & 0xffffu, wv.x & 0xffffu) | (one(xv.x >> 16, wv.x >> 16) << 16);
+          out.y = one(xv.y & 0xffffu, wv.y & 0xffffu) | (one(xv.y >> 16, wv.y >> 16) << 16);
+          out.z = one(xv.z & 0xffffu, wv.z & 0xffffu) | (one(xv.z >> 16, wv.z >> 16) << 16);
+          out.w = one(xv.w & 0xffffu, wv.w & 0xffffu) | (one(xv.w >> 16, wv.w >> 16) << 16);
+        } else {
+          auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
+            return __float_as_uint(tiler::canon(widen(wb) * (widen(xb) * sc)));
+          };
+          out.x = one(xv.x, wv.x);
+          out.y = one(xv.y, wv.y);
+          out.z = one(xv.z, wv.z);
+          out.w = one(xv.w, wv.w);
+        }
+        *reinterpret_cast<u32x4*>(y + base + e) = out;
+      }
+    } else {
+      for (uint32_t e = t; e < extent; e += 256u) {
+        const float normalized = load_elem<kBf16>(x, base + e) * sc;
+        store_elem<kBf16>(y, base + e, tiler::canon(load_elem<kBf16>(w, wbase + e) * normalized));
+      }
+    }
+  }
+}
+
 }  // namespace
+
+#define TILER_RMS_STRICT_STAGED(TY, T, R)                                                             \
+  extern "C" __global__ void __launch_bounds__(256)                                                   \
+      tiler_rms_norm_##TY##_strict_r##R(const T* __restrict__ x, const T* __restrict__ w,             \
+                                        uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,      \
+                                        uint32_t extent, float eps) {                                 \
+    rms_strict_staged_body<T, R, true>(x, w, w_row_stride, y, rows, extent, eps);                     \
+  }                                                                                                   \
+  extern "C" __global__ void __launch_bounds__(256)                                                   \
+      tiler_rms_norm_##TY##_strict_r##R##_u(const T* __restrict__ x, const T* __restrict__ w,         \
+                                            uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,  \
+                                            uint32_t extent, float eps) {                             \
+    rms_strict_staged_body<T, R, false>(x, w, w_row_stride, y, rows, extent, eps);                    \
+  }
+TILER_RMS_STRICT_STAGED(f32, float, 1)
+TILER_RMS_STRICT_STAGED(f32, float, 4)
+TILER_RMS_STRICT_STAGED(f32, float, 16)
+TILER_RMS_STRICT_STAGED(f32, float, 64)
+TILER_RMS_STRICT_STAGED(bf16, uint16_t, 1)
+TILER_RMS_STRICT_STAGED(bf16, uint16_t, 4)
+TILER_RMS_STRICT_STAGED(bf16, uint16_t, 16)
+TILER_RMS_STRICT_STAGED(bf16, uint16_t, 64)
 
 extern "C" __global__ void __launch_bounds__(256)
 tiler_rms_norm_f32_strict(const float* __restrict__ x, const float* __restrict__ w, uint64_t w_row_stride,

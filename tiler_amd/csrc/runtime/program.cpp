@@ -235,7 +235,7 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
 
 // ---------------------------------------------------------------------------
 // RMS normalization.  Slots: 0 x, 1 w, 2 y.
-tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
+tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
                                Program& p, bool strict) {
   float eps;
@@ -258,7 +258,20 @@ tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_
   const bool al = aligned16(addr[x]) && aligned16(addr[w]) && aligned16(addr[y]) && (extent * elem) % 16 == 0;
   const uint64_t wstride = weight_broadcast ? 0 : extent;
   char name[64];
-  if (strict) {  // the reference's serial fold of the squares: one wave per row
+  if (strict && extent >= 64) {
+    // The reference's serial fold of the squares, staged: R rows per
+    // workgroup, the largest of 64, 16, 4 that still gives every CU a
+    // workgroup (else 1), a folding lane per row.
+    const uint64_t cus = t.compute_units;
+    const uint32_t R = rows >= 64 * cus ? 64 : rows >= 16 * cus ? 16 : rows >= 4 * cus ? 4 : 1;
+    if ((rows + R - 1) / R > 0x7fffffffull)
+      return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+    std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict_r%u%s", ty, R, al ? "" : "_u");
+    p.add(name, (uint32_t)((rows + R - 1) / R), 1, 256)
+        .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps);
+    return TILER_HIP_OK;
+  }
+  if (strict) {  // short rows: the reference's serial fold of the squares, one wave per row
     if ((rows + 3) / 4 > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
     std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict", ty);

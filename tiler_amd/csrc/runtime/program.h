@@ -160,7 +160,7 @@ uint32_t tree_workgroups(const Target& t, uint64_t n);
 // carry the alignment a realization may assume.
 tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
                               const tiler_hip_sum_plan& sp, const uintptr_t* addr, Program& p);
-tiler_hip_status plan_rms_norm(uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
+tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
                                Program& p, bool strict = false);
 // `form` (TILER_HIP_FORM_SOFTMAX_*) forces the split or the row-synchronized

@@ -195,6 +195,22 @@ const EntryRow kEntries[] = {
     {"tiler_contract_strict_bf16_silu_b64", "tensor-contraction-bf16/strict+silu", 3},
     {"tiler_rms_norm_f32_strict", "rms-norm-f32/strict", 3},
     {"tiler_rms_norm_bf16_strict", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_f32_strict_r1", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r1_u", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r4", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r4_u", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r16", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r16_u", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r64", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r64_u", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r1", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r1_u", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r4", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r4_u", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r16", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r16_u", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r64", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r64_u", "rms-norm/bf16/strict", 3},
     {"tiler_softmax_f32_strict", "softmax-f32/strict", 2},
     {"tiler_fold_sum_f32", "strict-serial-sum-f32/serial-any-axes", 3},
     {"tiler_fold_squared_f32", "squared-serial-sum-f32/serial", 3},
@@ -1372,7 +1388,7 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context* ctx, uint32_t dtype, cons
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   tiler_rt::Program p;
   const uintptr_t addr[3] = {(uintptr_t)x, (uintptr_t)w, (uintptr_t)y};
-  tiler_hip_status st = tiler_rt::plan_rms_norm(dtype, weight_broadcast, rows, extent, eps_bits, addr, p);
+  tiler_hip_status st = tiler_rt::plan_rms_norm(target_of(ctx), dtype, weight_broadcast, rows, extent, eps_bits, addr, p);
   if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
   if (p.nlaunches && (!x || !w || !y)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(x), const_cast<void*>(w), y};
@@ -1885,7 +1901,7 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
     case TILER_HIP_PROGRAM_RMS_NORM:
       // Without permits_reassociation the serial fold of the reference runs;
       // with it, the grouped row fold (the declared grouping).
-      st = tiler_rt::plan_rms_norm(r->dtype, bc ? 1 : 0, e[0], e[1], r->scalars[0], addr, p, !c.reassociate);
+      st = tiler_rt::plan_rms_norm(t, r->dtype, bc ? 1 : 0, e[0], e[1], r->scalars[0], addr, p, !c.reassociate);
       break;
     case TILER_HIP_PROGRAM_SOFTMAX:
       st = r->dtype == TILER_HIP_F32
