@@ -70,7 +70,9 @@ def test_strict_contract_selects_the_serial_row_and_contraction_kernels():
     assert s.symbols == ["tiler_rms_norm_bf16_strict_r16"] and s.dispatches[0].grid == (512, 1, 1)
     assert realize(L.PROGRAM_RMS_NORM, (5, 20000), scalars=(EPS,)).symbols == ["tiler_rms_norm_f32_strict_r1"]
     assert realize(L.PROGRAM_RMS_NORM, (5, 40), scalars=(EPS,)).symbols == ["tiler_rms_norm_f32_strict"]
-    assert realize(L.PROGRAM_SOFTMAX, (32, 131072)).symbols == ["tiler_softmax_f32_strict"]
+    assert realize(L.PROGRAM_SOFTMAX, (32, 131072)).symbols == ["tiler_softmax_f32_strict_r1"]
+    assert realize(L.PROGRAM_SOFTMAX, (65536, 2048)).symbols == ["tiler_softmax_f32_strict_r16"]
+    assert realize(L.PROGRAM_SOFTMAX, (9, 40)).symbols == ["tiler_softmax_f32_strict"]
     c = realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, variant=L.EPILOGUE_SILU)
     assert c.symbols == ["tiler_contract_strict_bf16_silu_b64"] and c.dispatches[0].grid == (64, 64, 1)
     assert realize(L.PROGRAM_CONTRACTION, (40, 70, 9), dtype=L.BF16).symbols == ["tiler_contract_strict_bf16"]

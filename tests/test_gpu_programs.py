@@ -382,6 +382,40 @@ def test_strict_softmax_is_the_reference_fold(ctx):
         assert np.array_equal(bits(got).reshape(-1), bits(want).reshape(-1)), (rows, extent)
 
 
+@pytest.mark.parametrize("rows,extent,form", [
+    (16384, 64, "_strict_r16"),    # one partial stage (the oracle's certified exp keeps these small)
+    (4500, 530, "_strict_r16_u"),  # 4-byte loads, three stages, a ragged last workgroup
+    (4096, 200, "_strict_r16"),
+    (1500, 301, "_strict_r4_u"),   # 4-byte loads, a ragged last stage
+    (300, 72, "_strict_r1"),
+])
+def test_strict_softmax_staged_rows(ctx, rows, extent, form):
+    """Rows of >= 64 run the staged strict softmax (tiler_softmax_f32_strict_r*):
+    the maximum, the exponent sum folded in order, the reciprocal multiply --
+    bit for bit against the oracle.  Row 0 all -inf, row 1 with a NaN, row 2
+    with a +inf, row 3 with -0.0 and +0.0 as its only large values."""
+    rng = np.random.default_rng(rows * 3 + extent)
+    x = (rng.standard_normal((rows, extent)) * 3).astype(np.float32)
+    x[0] = -np.inf
+    x[1, extent // 3] = np.nan
+    x[2, extent - 1] = np.inf
+    x[3] = -np.abs(x[3]) - 1
+    x[3, 0], x[3, 1] = -0.0, 0.0
+    flags = L.REGION_ALIGNED16
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), flags=flags, ctx=ctx)
+    assert rz.symbols[-1].endswith(form), rz.symbols
+    print(f"[strict softmax] {rz.symbols[-1]} rows={rows} extent={extent}", flush=True)
+    bufs = [ctx.to_device(x), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[-1].download(np.float32, x.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    want = oracle.softmax_f32(x, x.shape, 1).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want))
+
+
 @pytest.mark.parametrize("m,n,k,form", [(70, 90, 300, "b16"), (512, 1000, 96, "b32"), (2048, 2040, 70, "b64"),
                                         (40, 70, 9, "")])
 @pytest.mark.parametrize("silu", [False, True])

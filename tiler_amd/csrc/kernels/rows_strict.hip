@@ -276,7 +276,172 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
   }
 }
 
+// Strict softmax over many rows, staged the same way (R rows per workgroup,
+// stages of C = 4096/R elements of each row), in three streamed passes over
+// each row (softmax.rs:237-315):
+// * The maximum. It is order-insensitive (model.rs:906-912), so each thread
+//   keeps the running maximum of its own pieces and the pieces of a row are
+//   combined from LDS afterwards.
+// * The exponents e = certified exp(fl(x - m)), stored into LDS stage by
+//   stage. Lane r/4 of wave r%4 folds row r's exponents in ascending order
+//   from -0.0 (an exponent is never -0.0, so -0.0 plus the first is the first).
+// * y = canon(fl(exp(fl(x - m)) * fl(1 / d))): the reciprocal, then a
+//   multiply, the exponent recomputed (the same correctly rounded value).
+template <int R, bool kVec>
+__device__ __forceinline__ void softmax_strict_staged_body(const float* __restrict__ x, float* __restrict__ y,
+                                                           uint64_t rows, uint32_t extent) {
+  constexpr uint32_t C = 4096 / R;
+  constexpr uint32_t kStride = C + 4;
+  constexpr uint32_t W = kVec ? 4 : 1;
+  constexpr uint32_t kRowPieces = C / W;
+  constexpr uint32_t kPer = 4096 / W / 256;
+  typedef typename std::conditional<kVec, f32x4, float>::type piece;
+  __shared__ __align__(16) float stage[2][R * kStride];
+  __shared__ float rowmax[R];
+  __shared__ float recip[R];
+  __shared__ double tab[64];
+  const uint32_t t = threadIdx.x;
+  if (t < 64) tab[t] = kExp2Table64[t];
+  const uint64_t row0 = (uint64_t)blockIdx.x * R;
+  const uint32_t stages = (extent + C - 1) / C;
+  auto valid = [&](uint32_t i, uint32_t s, uint32_t& r, uint32_t& e) {
+    const uint32_t q = t + 256u * i;
+    r = q / kRowPieces;
+    e = s * C + (q % kRowPieces) * W;
+    return row0 + r < rows && e < extent;
+  };
+  // Pass 1: the maximum.  Piece i of this thread always belongs to the same
+  // row and column of the stage, so its running maximum is one per piece.
+  float pm[kPer];
+#pragma unroll
+  for (uint32_t i = 0; i < kPer; ++i) pm[i] = -__builtin_huge_valf();  // the maximum's two-sided identity
+#pragma unroll 2
+  for (uint32_t s = 0; s < stages; ++s) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      uint32_t r, e;
+      if (!valid(i, s, r, e)) continue;
+      const float* src = x + (row0 + r) * extent + e;
+      if constexpr (kVec) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src);
+        pm[i] = tiler::maximum_f32(tiler::maximum_f32(tiler::maximum_f32(tiler::maximum_f32(pm[i], v.x), v.y), v.z),
+                                   v.w);
+      } else {
+        pm[i] = tiler::maximum_f32(pm[i], *src);
+      }
+    }
+  }
+  // Combine: stage buffer 0 holds every piece's maximum at [row][column].
+#pragma unroll
+  for (uint32_t i = 0; i < kPer; ++i) {
+    const uint32_t q = t + 256u * i;
+    stage[0][(q / kRowPieces) * kStride + q % kRowPieces] = pm[i];
+  }
+  __syncthreads();
+  const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
+  const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < rows;
+  if (folds) {
+    float m = -__builtin_huge_valf();
+    for (uint32_t c = 0; c < kRowPieces; ++c) m = tiler::maximum_f32(m, stage[0][fr * kStride + c]);
+    rowmax[fr] = m;
+  }
+  __syncthreads();
+  // Pass 2: the exponents, folded in order.
+  piece reg[kPer];
+  auto load = [&](uint32_t s) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      uint32_t r, e;
+      if (valid(i, s, r, e)) reg[i] = *reinterpret_cast<const piece*>(x + (row0 + r) * extent + e);
+      else reg[i] = piece{};
+    }
+  };
+  auto store = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      const float m = rowmax[r < R ? r : 0];
+      float* dst = &stage[buf][r * kStride + (q % kRowPieces) * W];
+      if constexpr (kVec) {
+        f32x4 ev;
+        ev.x = tiler::exp_f32_cr(reg[i].x - m, tab);
+        ev.y = tiler::exp_f32_cr(reg[i].y - m, tab);
+        ev.z = tiler::exp_f32_cr(reg[i].z - m, tab);
+        ev.w = tiler::exp_f32_cr(reg[i].w - m, tab);
+        *reinterpret_cast<f32x4*>(dst) = ev;
+      } else {
+        *dst = tiler::exp_f32_cr(reg[i] - m, tab);
+      }
+    }
+  };
+  float acc = -0.0f;
+  if (stages > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (uint32_t s = 0; s < stages; ++s) {
+    const bool more = s + 1 < stages;
+    if (more) load(s + 1);
+    if (folds) {
+      const float* row = &stage[s & 1][fr * kStride];
+      const uint32_t count = extent - s * C < C ? extent - s * C : C;
+      uint32_t c = 0;
+      for (; c + 4 <= count; c += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(row + c);
+        acc = acc + v.x;
+        acc = acc + v.y;
+        acc = acc + v.z;
+        acc = acc + v.w;
+      }
+      for (; c < count; ++c) acc = acc + row[c];
+    }
+    if (more) store((s + 1) & 1u);
+    __syncthreads();
+  }
+  if (folds) recip[fr] = 1.0f / acc;  // softmax.rs:302-313: the reciprocal, then a multiply
+  __syncthreads();
+  // Pass 3: y, over the workgroup's rows as one flat run of pieces (the
+  // iterations are independent, so several loads are in flight per thread).
+  const uint64_t nrows = rows - row0 < (uint64_t)R ? rows - row0 : (uint64_t)R;
+  const uint64_t per_row = (extent + W - 1) / W, pieces = nrows * per_row;
+#pragma unroll 4
+  for (uint64_t idx = t; idx < pieces; idx += 256u) {
+    const uint32_t r = (uint32_t)(idx / per_row);
+    const uint32_t e = (uint32_t)(idx - (uint64_t)r * per_row) * W;
+    const float m = rowmax[r], rc = recip[r];
+    const uint64_t at = (row0 + r) * extent + e;
+    if constexpr (kVec) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(x + at);
+      f32x4 o;
+      o.x = tiler::canon(tiler::exp_f32_cr(v.x - m, tab) * rc);
+      o.y = tiler::canon(tiler::exp_f32_cr(v.y - m, tab) * rc);
+      o.z = tiler::canon(tiler::exp_f32_cr(v.z - m, tab) * rc);
+      o.w = tiler::canon(tiler::exp_f32_cr(v.w - m, tab) * rc);
+      *reinterpret_cast<f32x4*>(y + at) = o;
+    } else {
+      y[at] = tiler::canon(tiler::exp_f32_cr(x[at] - m, tab) * rc);
+    }
+  }
+}
+
 }  // namespace
+
+#define TILER_SOFTMAX_STRICT_STAGED(R)                                                                \
+  extern "C" __global__ void __launch_bounds__(256)                                                   \
+      tiler_softmax_f32_strict_r##R(const float* __restrict__ x, float* __restrict__ y, uint64_t rows, \
+                                    uint32_t extent) {                                                \
+    softmax_strict_staged_body<R, true>(x, y, rows, extent);                                          \
+  }                                                                                                   \
+  extern "C" __global__ void __launch_bounds__(256)                                                   \
+      tiler_softmax_f32_strict_r##R##_u(const float* __restrict__ x, float* __restrict__ y,           \
+                                        uint64_t rows, uint32_t extent) {                             \
+    softmax_strict_staged_body<R, false>(x, y, rows, extent);                                         \
+  }
+TILER_SOFTMAX_STRICT_STAGED(1)
+TILER_SOFTMAX_STRICT_STAGED(4)
+TILER_SOFTMAX_STRICT_STAGED(16)
+TILER_SOFTMAX_STRICT_STAGED(64)
 
 #define TILER_RMS_STRICT_STAGED(TY, T, R)                                                             \
   extern "C" __global__ void __launch_bounds__(256)                                                   \

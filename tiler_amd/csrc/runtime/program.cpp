@@ -327,7 +327,22 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
   if (rows == 0 || extent == 0) return TILER_HIP_OK;
   if (extent > 0xffffffffull)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
-  if (strict) {  // the reference's serial exponent sum: one wave per row
+  if (strict && extent >= 64 && extent <= 0xffffffffull) {
+    // The reference's serial exponent sum, staged: R rows per workgroup as
+    // for the strict RMSNorm but at most 16 (stages of at least 256
+    // elements, so a stage's fold covers the next stage's loads), three
+    // streamed passes (maximum, exponents folded in order, output).
+    const uint64_t cus = t.compute_units;
+    const uint32_t R = rows >= 16 * cus ? 16 : rows >= 4 * cus ? 4 : 1;
+    if ((rows + R - 1) / R > 0x7fffffffull)
+      return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+    const bool vec = aligned16(addr[x]) && aligned16(addr[y]) && extent % 4 == 0;
+    char sname[48];
+    std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_r%u%s", R, vec ? "" : "_u");
+    p.add(sname, (uint32_t)((rows + R - 1) / R), 1, 256).ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
+    return TILER_HIP_OK;
+  }
+  if (strict) {  // short rows: the reference's serial exponent sum, one wave per row
     if ((rows + 3) / 4 > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
     p.add("tiler_softmax_f32_strict", (uint32_t)((rows + 3) / 4), 1, 256)
