@@ -127,9 +127,21 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
       const uint32_t count = (uint32_t)(length - s * C < C ? length - s * C : C);
       // one fold step: the element, or under kDot its product with the left
       // row's element (two roundings: no FMA)
+      // The left row's elements are the same for every folding lane: they
+      // are read from global memory at a wave-uniform address (the scalar
+      // cache serves them), not from LDS.
+      const float* aglob = a + s * C;
       auto step4 = [&](const f32x4 v, uint32_t c) {
         if constexpr (kDot) {
-          const f32x4 w = *reinterpret_cast<const f32x4*>(arow + c);
+          f32x4 w;
+          if constexpr (kVec) {
+            w = *reinterpret_cast<const f32x4*>(aglob + c);
+          } else {
+            w.x = aglob[c];
+            w.y = aglob[c + 1];
+            w.z = aglob[c + 2];
+            w.w = aglob[c + 3];
+          }
           acc = acc + w.x * v.x;
           acc = acc + w.y * v.y;
           acc = acc + w.z * v.z;
