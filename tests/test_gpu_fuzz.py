@@ -46,6 +46,83 @@ def test_sums(ctx, case):
     assert np.array_equal(bits(got).reshape(-1), bits(want).reshape(-1))
 
 
+def _staged_shape(r, max_elements):
+    """(rows, extent) spread over every staged form: rows from 1 to 20000,
+    extents from 16 to 20000, at most `max_elements` in all."""
+    rows = int(np.exp(r.uniform(0, np.log(20000))))
+    extent = int(np.exp(r.uniform(np.log(16), np.log(20000))))
+    while rows * extent > max_elements:
+        rows = max(1, rows // 2)
+        extent = max(16, extent * 3 // 4)
+    return rows, extent
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_staged_folds(ctx, case):
+    """Random rows and extents, an aligned or unaligned base: the strict
+    serial fold (staged for rows of >= 16), the multi-pass split at the
+    reference's partition, the workgroup tree over rows, each bit for bit."""
+    from tiler_amd.calibrate import split_partitions
+    r = _rng(case, 9)
+    rows, extent = _staged_shape(r, 2_000_000)
+    offset = int(r.choice([0, 4]))
+    x = (r.standard_normal((rows, extent)) * np.exp2(r.integers(-30, 30, (rows, extent)))).astype(np.float32)
+    if rows > 1:
+        x[0] = -0.0
+    dx, do = ctx.alloc(x.nbytes + offset), ctx.alloc(rows * 4)
+    try:
+        src = dx.offset(offset)
+        src.upload(x)
+        print(f"[staged folds] case {case}: rows={rows} extent={extent} offset={offset}", flush=True)
+        ctx.sum_f32(src, rows, extent, do, topology=L.SUM_SERIAL)
+        assert np.array_equal(bits(do.download(np.float32, (rows,))), bits(oracle.strict_sum(x, (rows, extent), 1)))
+        p = split_partitions(extent)
+        if extent % p == 0:
+            ctx.sum_f32(src, rows, extent, do, topology=L.SUM_MULTIPASS, partitions=p, per_partition=extent // p)
+            want = oracle.strict_partitioned_sum(x, rows, extent, p, extent // p)
+            assert np.array_equal(bits(do.download(np.float32, (rows,))), bits(want))
+        if rows > 1:
+            ctx.sum_f32(src, rows, extent, do, topology=L.SUM_TREE)
+            want = oracle.row_grouped_sum(x, rows, extent, 4, 4)
+            assert np.array_equal(bits(do.download(np.float32, (rows,))), bits(want))
+    finally:
+        dx.free()
+        do.free()
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_strict_rows(ctx, case):
+    """Random shapes through the strict (no reassociation) RMSNorm and
+    softmax realizations, staged for rows of >= 64: bit for bit."""
+    from tiler_amd.realize import realize, route
+    r = _rng(case, 10)
+    rows, extent = _staged_shape(r, 300_000)
+    x = (r.standard_normal((rows, extent)) * 3).astype(np.float32)
+    w = r.normal(1.0, 0.1, extent).astype(np.float32)
+    print(f"[strict rows] case {case}: rows={rows} extent={extent}", flush=True)
+    rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), scalars=(EPS,),
+                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=ctx)
+    bufs = [ctx.to_device(x), ctx.to_device(w), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[2].download(np.float32, x.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    want = oracle.rms_norm_f32(x, np.broadcast_to(w, x.shape).copy(), x.shape, 1, EPS).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want)), rz.symbols
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), flags=L.REGION_ALIGNED16, ctx=ctx)
+    bufs = [ctx.to_device(x), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[1].download(np.float32, x.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    want = oracle.softmax_f32(x, x.shape, 1).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want)), rz.symbols
+
+
 @pytest.mark.parametrize("case", range(CASES))
 def test_tree_sum(ctx, case):
     r = _rng(case, 2)
