@@ -356,12 +356,15 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
       else reg[i] = piece{};
     }
   };
-  auto store = [&](uint32_t buf) {
+  auto store = [&](uint32_t buf, uint32_t sbuf) {
 #pragma unroll
     for (uint32_t i = 0; i < kPer; ++i) {
       const uint32_t q = t + 256u * i, r = q / kRowPieces;
       const float m = rowmax[r < R ? r : 0];
       float* dst = &stage[buf][r * kStride + (q % kRowPieces) * W];
+      // The exponents also go to y, where the output pass scales them.
+      const uint32_t e = sbuf * C + (q % kRowPieces) * W;
+      const bool in = row0 + r < rows && e < extent;
       if constexpr (kVec) {
         f32x4 ev;
         ev.x = tiler::exp_f32_cr(reg[i].x - m, tab);
@@ -369,15 +372,18 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
         ev.z = tiler::exp_f32_cr(reg[i].z - m, tab);
         ev.w = tiler::exp_f32_cr(reg[i].w - m, tab);
         *reinterpret_cast<f32x4*>(dst) = ev;
+        if (in) *reinterpret_cast<f32x4*>(y + (row0 + r) * extent + e) = ev;
       } else {
-        *dst = tiler::exp_f32_cr(reg[i] - m, tab);
+        const float ev = tiler::exp_f32_cr(reg[i] - m, tab);
+        *dst = ev;
+        if (in) y[(row0 + r) * extent + e] = ev;
       }
     }
   };
   float acc = -0.0f;
   if (stages > 0) {
     load(0);
-    store(0);
+    store(0, 0);
   }
   __syncthreads();
   for (uint32_t s = 0; s < stages; ++s) {
@@ -396,7 +402,7 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
       }
       for (; c < count; ++c) acc = acc + row[c];
     }
-    if (more) store((s + 1) & 1u);
+    if (more) store((s + 1) & 1u, s + 1);
     __syncthreads();
   }
   if (folds) recip[fr] = 1.0f / acc;  // softmax.rs:302-313: the reciprocal, then a multiply
@@ -409,18 +415,18 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
   for (uint64_t idx = t; idx < pieces; idx += 256u) {
     const uint32_t r = (uint32_t)(idx / per_row);
     const uint32_t e = (uint32_t)(idx - (uint64_t)r * per_row) * W;
-    const float m = rowmax[r], rc = recip[r];
+    const float rc = recip[r];
     const uint64_t at = (row0 + r) * extent + e;
     if constexpr (kVec) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(x + at);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(y + at);  // the exponents pass 2 wrote
       f32x4 o;
-      o.x = tiler::canon(tiler::exp_f32_cr(v.x - m, tab) * rc);
-      o.y = tiler::canon(tiler::exp_f32_cr(v.y - m, tab) * rc);
-      o.z = tiler::canon(tiler::exp_f32_cr(v.z - m, tab) * rc);
-      o.w = tiler::canon(tiler::exp_f32_cr(v.w - m, tab) * rc);
+      o.x = tiler::canon(v.x * rc);
+      o.y = tiler::canon(v.y * rc);
+      o.z = tiler::canon(v.z * rc);
+      o.w = tiler::canon(v.w * rc);
       *reinterpret_cast<f32x4*>(y + at) = o;
     } else {
-      y[at] = tiler::canon(tiler::exp_f32_cr(x[at] - m, tab) * rc);
+      y[at] = tiler::canon(y[at] * rc);
     }
   }
 }
