@@ -338,13 +338,26 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
     stage[0][(q / kRowPieces) * kStride + q % kRowPieces] = pm[i];
   }
   __syncthreads();
+  // Each row's piece maxima are combined by the 256 / R threads of its
+  // group: a strided pass, then a butterfly within the group (and, for
+  // R = 1, across the four waves through LDS).
+  {
+    constexpr uint32_t kTPR = 256 / R;  // threads per row
+    const uint32_t cr = t / kTPR, cl = t % kTPR;
+    float m = -__builtin_huge_valf();
+    for (uint32_t c = cl; c < kRowPieces; c += kTPR) m = tiler::maximum_f32(m, stage[0][cr * kStride + c]);
+#pragma unroll
+    for (uint32_t o = (kTPR < 64 ? kTPR : 64) / 2; o >= 1; o >>= 1) m = tiler::maximum_f32(m, __shfl_xor(m, o, 64));
+    if constexpr (kTPR == 256) {
+      __shared__ float wm[4];
+      if ((t & 63u) == 0) wm[t >> 6] = m;
+      __syncthreads();
+      m = tiler::maximum_f32(tiler::maximum_f32(wm[0], wm[1]), tiler::maximum_f32(wm[2], wm[3]));
+    }
+    if (cl == 0) rowmax[cr] = m;
+  }
   const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
   const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < rows;
-  if (folds) {
-    float m = -__builtin_huge_valf();
-    for (uint32_t c = 0; c < kRowPieces; ++c) m = tiler::maximum_f32(m, stage[0][fr * kStride + c]);
-    rowmax[fr] = m;
-  }
   __syncthreads();
   // Pass 2: the exponents, folded in order.
   piece reg[kPer];
