@@ -460,7 +460,6 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
 TILER_SOFTMAX_STRICT_STAGED(1)
 TILER_SOFTMAX_STRICT_STAGED(4)
 TILER_SOFTMAX_STRICT_STAGED(16)
-TILER_SOFTMAX_STRICT_STAGED(64)
 
 #define TILER_RMS_STRICT_STAGED(TY, T, R)                                                             \
   extern "C" __global__ void __launch_bounds__(256)                                                   \

@@ -218,8 +218,6 @@ const EntryRow kEntries[] = {
     {"tiler_softmax_f32_strict_r4_u", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_r16", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_r16_u", "softmax-f32/strict", 2},
-    {"tiler_softmax_f32_strict_r64", "softmax-f32/strict", 2},
-    {"tiler_softmax_f32_strict_r64_u", "softmax-f32/strict", 2},
     {"tiler_fold_sum_f32", "strict-serial-sum-f32/serial-any-axes", 3},
     {"tiler_fold_squared_f32", "squared-serial-sum-f32/serial", 3},
     {"tiler_fold_fma_f32", "fused-multiply-add-serial-sum-f32/serial", 3},
