@@ -369,7 +369,7 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
       else reg[i] = piece{};
     }
   };
-  auto store = [&](uint32_t buf, uint32_t sbuf) {
+  auto store_some = [&](uint32_t buf, uint32_t sbuf, auto guard) {
 #pragma unroll
     for (uint32_t i = 0; i < kPer; ++i) {
       const uint32_t q = t + 256u * i, r = q / kRowPieces;
@@ -377,7 +377,8 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
       float* dst = &stage[buf][r * kStride + (q % kRowPieces) * W];
       // The exponents also go to y, where the output pass scales them.
       const uint32_t e = sbuf * C + (q % kRowPieces) * W;
-      const bool in = row0 + r < rows && e < extent;
+      // Slots past the row's end or the last row are never folded.
+      if (decltype(guard)::value && !(row0 + r < rows && e < extent)) continue;
       if constexpr (kVec) {
         f32x4 ev;
         ev.x = tiler::exp_f32_cr(reg[i].x - m, tab);
@@ -385,13 +386,19 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
         ev.z = tiler::exp_f32_cr(reg[i].z - m, tab);
         ev.w = tiler::exp_f32_cr(reg[i].w - m, tab);
         *reinterpret_cast<f32x4*>(dst) = ev;
-        if (in) *reinterpret_cast<f32x4*>(y + (row0 + r) * extent + e) = ev;
+        *reinterpret_cast<f32x4*>(y + (row0 + r) * extent + e) = ev;
       } else {
         const float ev = tiler::exp_f32_cr(reg[i] - m, tab);
         *dst = ev;
-        if (in) y[(row0 + r) * extent + e] = ev;
+        y[(row0 + r) * extent + e] = ev;
       }
     }
+  };
+  // Whole stages (every slot a row's element) take the unguarded form, so the
+  // pieces' exponents interleave; only a workgroup's edge stages test slots.
+  auto store = [&](uint32_t buf, uint32_t sbuf) {
+    if (row0 + R <= rows && (uint64_t)(sbuf + 1) * C <= extent) store_some(buf, sbuf, std::false_type{});
+    else store_some(buf, sbuf, std::true_type{});
   };
   float acc = -0.0f;
   if (stages > 0) {

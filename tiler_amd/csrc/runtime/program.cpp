@@ -331,8 +331,9 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
     // The reference's serial exponent sum, staged: R rows per workgroup as
     // for the strict RMSNorm but at most 16 (stages of at least 256
     // elements, so a stage's fold covers the next stage's loads; 64 rows of
-    // 64-element stages ran the 65536 x 2048 case in 611 us, 16 in 524), three
-    // streamed passes (maximum, exponents folded in order, output).
+    // 64-element stages ran the 65536 x 2048 case in 611 us, 16 in 524 on the
+    // same build), three streamed passes (maximum, exponents folded in order,
+    // output).
     const uint64_t cus = t.compute_units;
     const uint32_t R = rows >= 16 * cus ? 16 : rows >= 4 * cus ? 4 : 1;
     if ((rows + R - 1) / R > 0x7fffffffull)
