@@ -8,7 +8,11 @@
  * exceptions cross the boundary, and all state lives in a tiler_hip_context
  * (the adapter's `Self`).  One context = one device and one ordered stream,
  * the reference's single-device profile (docs/decisions/0090-...md:152):
- * calls on one context must not overlap from several threads.
+ * calls on one context must not overlap from several threads.  Calls that
+ * bind the context's device workspace (the tree and multi-pass sums'
+ * partials, the split and row-synchronized softmax, the gather record) run
+ * on the context's own stream only: given any other stream they refuse with
+ * TILER_HIP_REFUSE_UNSUPPORTED before anything is enqueued.
  *
  * Status convention (tiler-runtime/src/adapter.rs:222-231, ADR 0051):
  *   0                 success
@@ -404,7 +408,10 @@ typedef struct {
      * a realization's CONSTANT slot.  NULL entries are left alone. */
     const void *const *slot_contents;
     /* The live extents' values for this dispatch (NULL with count 0: none),
-     * and optionally (NULL: unchecked) the range each must lie in. */
+     * and the range each must lie in (the realization's live_extents, in
+     * order): required whenever extent_count > 0.  Both plan_dispatch
+     * (refusal) and dispatch (failure, before any entry is launched) check
+     * every value against its range. */
     uint32_t extent_count;
     const uint64_t *extents;
     const tiler_hip_live_extent *extent_ranges;
@@ -488,6 +495,10 @@ typedef struct {
     uint64_t rounds;            /* cooperative */
 } tiler_hip_sum_plan;
 
+/* The tree's and the multi-pass split's partials live in the context
+ * workspace when they fit (256 KiB): such a call takes NULL or the context's
+ * own stream, and refuses any other (TILER_HIP_REFUSE_UNSUPPORTED).  Larger
+ * partials are allocated on the given stream. */
 tiler_hip_status tiler_hip_sum_f32(tiler_hip_context *ctx, const float *x, uint64_t rows,
                                    uint64_t extent, float *out, const tiler_hip_sum_plan *plan,
                                    tiler_hip_stream stream);
@@ -530,8 +541,9 @@ tiler_hip_status tiler_hip_rms_norm(tiler_hip_context *ctx, uint32_t dtype, cons
  * ticks, after which a workgroup computes its row's maximum and sum from the
  * row itself); beyond that they run three launches with the segment partials
  * in the workspace (up to 32768 segments; more are allocated on the stream).
- * Either way such calls on different streams of one context must not run
- * concurrently. */
+ * A call that binds the workspace takes NULL or the context's own stream and
+ * refuses any other (TILER_HIP_REFUSE_UNSUPPORTED), so two such calls never
+ * overlap. */
 tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context *ctx, const float *x, uint64_t rows,
                                        uint64_t extent, float *y, tiler_hip_stream stream);
 
@@ -643,14 +655,17 @@ tiler_hip_status tiler_hip_broadcast(tiler_hip_context *ctx, const void *src, ui
  * element_bytes elements, 32-bit index (index_signed: int32, else uint32),
  * output [outer, index_count, inner].  Byte moves only.  An out-of-range index
  * is never clamped or wrapped: its run is not written and the lowest offending
- * position is recorded for tiler_hip_gather_status. */
+ * position is recorded for tiler_hip_gather_status.  The record is the
+ * context's: the call takes NULL or the context's own stream and refuses any
+ * other (TILER_HIP_REFUSE_UNSUPPORTED). */
 tiler_hip_status tiler_hip_gather(tiler_hip_context *ctx, const void *source, uint64_t outer,
                                   uint64_t gathered, uint64_t inner, uint32_t element_bytes,
                                   const uint32_t *index, uint64_t index_count,
                                   int32_t index_signed, void *out, tiler_hip_stream stream);
 /* Waits for the stream and reports the gathers since the last call:
  * TILER_HIP_OK, or TILER_HIP_FAIL_GATHER_INDEX_OUT_OF_BOUNDS with the lowest
- * offending position.  Re-arms the record. */
+ * offending position.  Re-arms the record.  NULL or the context's own stream
+ * only (TILER_HIP_REFUSE_UNSUPPORTED otherwise). */
 tiler_hip_status tiler_hip_gather_status(tiler_hip_context *ctx, tiler_hip_stream stream,
                                          uint64_t *bad_position);
 /* Pre-commit form of the same bound rule for host-resident indices:

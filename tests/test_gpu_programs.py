@@ -388,6 +388,8 @@ def test_strict_softmax_is_the_reference_fold(ctx):
     (4096, 200, "_strict_r16"),
     (1500, 301, "_strict_r4_u"),   # 4-byte loads, a ragged last stage
     (300, 72, "_strict_r1"),
+    (4096, 512, "_strict_r16"),    # 16-byte loads, whole stages only (the C3 kernel's store path)
+    (1024, 2048, "_strict_r4"),    # 16-byte loads, whole stages, four rows per workgroup
 ])
 def test_strict_softmax_staged_rows(ctx, rows, extent, form):
     """Rows of >= 64 run the staged strict softmax (tiler_softmax_f32_strict_r*):
@@ -414,6 +416,95 @@ def test_strict_softmax_staged_rows(ctx, rows, extent, form):
             b.free()
     want = oracle.softmax_f32(x, x.shape, 1).reshape(rows, extent)
     assert np.array_equal(bits(got), bits(want))
+
+
+def _sampled_rows(rng, rows, per_group, groups_sampled):
+    """Rows covering every residue mod `per_group` (the rows one workgroup
+    holds): the first and last workgroup whole, plus `groups_sampled` - 2
+    other workgroups, each contributing one row per residue."""
+    groups = rows // per_group
+    picked = set(range(per_group)) | set(range(rows - per_group, rows))
+    others = rng.choice(np.arange(1, groups - 1), size=groups_sampled - 2, replace=False)
+    for r in range(per_group):
+        for g in others:
+            picked.add(int(g) * per_group + r)
+    return np.array(sorted(picked))
+
+
+def test_strict_softmax_c3_shape_sampled_rows(ctx):
+    """The strict softmax at the C3 configuration (f32 [32 x 2048 x 2048],
+    65536 rows of 2048; tiler_softmax_f32_strict_r16, 16 rows per workgroup,
+    16-byte loads, whole stages) routed under the strict contract (no
+    PERMITS_REASSOCIATION) -- 512 rows compared bit for bit with the oracle's
+    softmax_f32 (softmax.rs:237-315): the first and last workgroup whole and
+    one row of every residue mod 16 from 30 other workgroups.  Planted rows:
+    all -inf, a NaN, a +inf, -0.0 and +0.0 as the only large values, and a
+    row of one repeated value."""
+    rows, extent = 65536, 2048
+    rng = np.random.default_rng(65536)
+    x = rng.standard_normal((rows, extent), dtype=np.float32) * np.float32(3)
+    sample = _sampled_rows(rng, rows, 16, 32)
+    planted = {int(sample[0]): "ninf", int(sample[17]): "nan", int(sample[40]): "pinf",
+               int(sample[-1]): "zeros", int(sample[-6]): "flat", int(sample[100]): "nan"}
+    for r, kind in planted.items():
+        if kind == "ninf":
+            x[r] = -np.inf
+        elif kind == "nan":
+            x[r, (r * 7) % extent] = np.nan
+        elif kind == "pinf":
+            x[r, extent - 1 - r % 16] = np.inf
+        elif kind == "zeros":
+            x[r] = -np.abs(x[r]) - 1
+            x[r, 0], x[r, extent - 1] = -0.0, 0.0
+        else:
+            x[r] = np.float32(0.75)
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), flags=L.REGION_ALIGNED16, ctx=ctx)
+    assert rz.symbols == ["tiler_softmax_f32_strict_r16"], rz.symbols
+    print(f"[strict softmax C3] {rz.symbols} rows={rows} extent={extent} sampled={len(sample)}", flush=True)
+    bufs = [ctx.to_device(x), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[-1].download(np.float32, x.shape)[sample]
+    finally:
+        for b in bufs:
+            b.free()
+    xs = np.ascontiguousarray(x[sample])
+    del x
+    want = oracle.softmax_f32(xs, xs.shape, 1).reshape(xs.shape)
+    diff = np.argwhere(bits(got) != bits(want))
+    assert diff.size == 0, f"{len(diff)} elements differ, first in row {sample[diff[0][0]]} at {diff[0][1]}"
+
+
+def test_strict_bf16_silu_contraction_c5_shape_sampled_rows(ctx):
+    """The strict bf16 contraction with the SiLU epilogue at the C5
+    configuration (A, B bf16 [4096 x 4096] ~N(0, 1/64), C = bf16(silu(A.B^T)))
+    routed under the strict contract: tiler_contract_strict_bf16_silu_b64,
+    64 x 64 outputs per workgroup.  192 whole output rows -- the first and
+    last row tile whole, and one row of every residue mod 64, each from
+    another tile --
+    bit for bit with bf16_narrow(silu_f32(contract_strict_f32(widened))),
+    the reference's fold (contraction.rs:558-630) and SiLU (silu.rs:511-533)
+    on exactly widened operands."""
+    m = n = k = 4096
+    rng = np.random.default_rng(4096)
+    a = oracle.bf16_narrow(rng.standard_normal((m, k), dtype=np.float32) / np.float32(64)).reshape(m, k)
+    b = oracle.bf16_narrow(rng.standard_normal((n, k), dtype=np.float32) / np.float32(64)).reshape(n, k)
+    sample = np.array(sorted(set(range(64)) | set(range(m - 64, m)) |
+                             {int(g) * 64 + r for r, g in enumerate(rng.integers(1, m // 64 - 1, 64))}))
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=L.EPILOGUE_SILU, ctx=ctx)
+    assert rz.symbols == ["tiler_contract_strict_bf16_silu_b64"], rz.symbols
+    print(f"[strict bf16 silu C5] {rz.symbols} {m}x{n}x{k} sampled rows={len(sample)}", flush=True)
+    bufs = [ctx.to_device(a), ctx.to_device(b), ctx.alloc(m * n * 2)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[2].download(np.uint16, (m, n))[sample]
+    finally:
+        for x in bufs:
+            x.free()
+    ref = oracle.contract_strict_f32(bf16_widen(a[sample]), bf16_widen(b), len(sample), n, k)
+    want = oracle.bf16_narrow(oracle.silu_f32(ref)).reshape(len(sample), n)
+    diff = np.argwhere(got != want)
+    assert diff.size == 0, f"{len(diff)} outputs differ, first at row {sample[diff[0][0]]} column {diff[0][1]}"
 
 
 @pytest.mark.parametrize("m,n,k,form", [(70, 90, 300, "b16"), (512, 1000, 96, "b32"), (2048, 2040, 70, "b64"),

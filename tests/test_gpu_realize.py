@@ -15,6 +15,9 @@ arrive before anything is committed.
 """
 from __future__ import annotations
 
+import ctypes
+import re
+
 import numpy as np
 import pytest
 
@@ -270,3 +273,112 @@ def test_live_extent_outside_its_range_is_refused_before_commit(ctx):
     finally:
         for x in bufs:
             x.free()
+
+
+@pytest.mark.parametrize("dtype", [L.F32, L.BF16])
+def test_live_contracted_extent_decode_shape(ctx, dtype):
+    """A decode-shaped LiveContraction (m = 8 rows, n = 1000, k bound 5000):
+    the f32 region runs the staged strict fold along B's rows
+    (tiler_contract_strict_f32_s*_u, whose rows per workgroup and stages were
+    sized from the bound), the bf16 region the register-blocked strict tiles.
+    Routed at k far below the bound, at k not a multiple of 4 and at the
+    bound, each bit for bit with the strict fold at that k."""
+    m, n, bound = 8, 1000, 5000
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, bound), dtype=dtype, flags=LIVE, ctx=ctx)
+    if dtype == L.F32:
+        assert re.fullmatch(r"tiler_contract_strict_f32_s\d+_u", rz.symbols[0]), rz.symbols
+    else:
+        assert rz.symbols[0].startswith("tiler_contract_strict_bf16"), rz.symbols
+    bufs = [ctx.alloc(nbytes) for _, nbytes in rz.slots]
+    try:
+        for k in (1, 7, 130, 4999, bound):
+            rng = np.random.default_rng(k + 1)
+            a = rng.standard_normal((m, k)).astype(np.float32)
+            b = rng.standard_normal((n, k)).astype(np.float32)
+            if dtype == L.F32:
+                got = _route_live(ctx, rz, bufs, a, b, k, np.float32, m, n)
+                want = oracle.contract_strict_f32(a, b, m, n, k)
+                assert np.array_equal(bits(got).reshape(-1), bits(want).reshape(-1)), k
+            else:
+                a16, b16 = oracle.bf16_narrow(a).reshape(m, k), oracle.bf16_narrow(b).reshape(n, k)
+                got = _route_live(ctx, rz, bufs, a16, b16, k, np.uint16, m, n)
+                assert np.array_equal(got, oracle.contract_general(a16, "mk", b16, "nk", "mn")), k
+    finally:
+        for x in bufs:
+            x.free()
+
+
+def test_dispatch_rechecks_live_extents_and_requires_ranges(ctx):
+    """A plan whose live extent lies outside its range, or that carries
+    values without ranges, is refused at plan_dispatch and fails at dispatch
+    before any entry is launched (the output slot keeps its contents)."""
+    from tiler_amd.realize import _prepared
+    m, n, bound = 40, 70, 64
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, bound), flags=LIVE, ctx=ctx)
+    e = rz.raw.entries[0]
+    count = e.binding_count
+    slots = (ctypes.c_uint32 * count)(*e.binding_slots[:count])
+    offs = (ctypes.c_uint32 * count)(*e.binding_offsets[:count])
+    ids = (ctypes.c_uint32 * e.extent_count)(*e.extent_ids[:e.extent_count])
+    xoffs = (ctypes.c_uint32 * e.extent_count)(*e.extent_offsets[:e.extent_count])
+    ka = ctypes.create_string_buffer(bytes(e.kernargs[:e.kernarg_bytes]), e.kernarg_bytes)
+    de = L.DispatchEntry(_prepared(ctx, rz.symbols[0]), (ctypes.c_uint32 * 3)(*e.grid), (ctypes.c_uint32 * 3)(*e.block),
+                         0, ctypes.cast(ka, ctypes.c_void_p), e.kernarg_bytes, count, slots, offs,
+                         e.extent_count, ids, xoffs)
+    sb = (ctypes.c_uint64 * len(rz.slots))(*[b for _, b in rz.slots])
+    bufs = [ctx.alloc(b) for _, b in rz.slots]
+    ptrs = (ctypes.c_void_p * len(bufs))(*[x.ptr for x in bufs])
+    ranges = (L.LiveExtent * 1)(*rz.raw.live_extents[:1])
+    try:
+        ctx.fill_u32(bufs[2], 0x7FC00001, m * n)
+        ctx.synchronize()
+        too_big = (ctypes.c_uint64 * 1)(bound + 1)
+        plan = L.DispatchPlan(len(rz.slots), sb, 1, ctypes.pointer(de), None, 1, too_big, ranges)
+        assert L.lib().tiler_hip_plan_dispatch(ctx.handle, ctypes.byref(plan)) == L.REFUSE_CAPACITY
+        assert L.lib().tiler_hip_dispatch(ctx.handle, ctypes.byref(plan), ptrs) == L.FAIL_LAUNCH
+        ok = (ctypes.c_uint64 * 1)(bound)
+        bare = L.DispatchPlan(len(rz.slots), sb, 1, ctypes.pointer(de), None, 1, ok, None)
+        assert L.lib().tiler_hip_plan_dispatch(ctx.handle, ctypes.byref(bare)) == L.REFUSE_INVALID_ARGUMENT
+        assert L.lib().tiler_hip_dispatch(ctx.handle, ctypes.byref(bare), ptrs) == L.FAIL_LAUNCH
+        assert (bufs[2].download(np.uint32, (m * n,)) == 0x7FC00001).all()  # nothing ran
+    finally:
+        for x in bufs:
+            x.free()
+
+
+def test_workspace_calls_refuse_a_foreign_stream(ctx):
+    """The tree sum's partials, the split softmax's partials and the gather
+    record live in the context workspace, ordered by the context's stream
+    only: given another stream (here a second context's) those calls refuse
+    before anything is enqueued; calls that bind no workspace (RMSNorm) run
+    on any stream; the context's own stream, given explicitly, is accepted."""
+    import tiler_amd
+    other = tiler_amd.Context(0)
+    x = np.ones((1, 1 << 20), np.float32)
+    dx, dout = ctx.to_device(x), ctx.alloc(4)
+    dy = ctx.alloc(x.nbytes)
+    idx = ctx.to_device(np.zeros(4, np.uint32))
+    try:
+        foreign = other.stream
+        with pytest.raises(Refusal) as e:
+            ctx.sum_f32(dx, 1, 1 << 20, dout, topology=L.SUM_TREE, stream=foreign)
+        assert e.value.status == L.REFUSE_UNSUPPORTED
+        with pytest.raises(Refusal) as e:
+            ctx.softmax_f32(dx, 1, 1 << 20, dy, stream=foreign)
+        assert e.value.status == L.REFUSE_UNSUPPORTED
+        with pytest.raises(Refusal) as e:
+            ctx.gather(dx, 1, 1 << 20, 1, 4, idx, 4, dy, stream=foreign)
+        assert e.value.status == L.REFUSE_UNSUPPORTED
+        ctx.sum_f32(dx, 1, 1 << 20, dout, topology=L.SUM_TREE, stream=ctx.stream)
+        ctx.synchronize()
+        assert dout.download(np.float32, (1,))[0] == np.float32(1 << 20)
+        w = ctx.to_device(np.ones(1 << 10, np.float32))
+        try:
+            ctx.rms_norm(L.F32, dx, w, 1 << 10, 1 << 10, 0x3727C5AC, dy, stream=foreign)
+            other.synchronize()
+        finally:
+            w.free()
+    finally:
+        for b in (dx, dout, dy, idx):
+            b.free()
+        other.close()

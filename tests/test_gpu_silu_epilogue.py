@@ -19,6 +19,7 @@ guarded general form).  Two checks:
 from __future__ import annotations
 
 import os
+import re
 import struct
 
 import numpy as np
@@ -28,7 +29,7 @@ import oracle
 from device_launch import launch
 from helpers import bits, bf16_widen
 from tiler_amd import _lib as L
-from tiler_amd import families
+from tiler_amd.realize import realize, route
 
 pytestmark = pytest.mark.gpu
 
@@ -101,6 +102,26 @@ def _values(rng, count):
     return v
 
 
+def _contract_on_path(ctx, a, b, epilogue, path):
+    """C = A.B^T (bf16 bits) realized under PERMITS_REASSOCIATION; the
+    realization must dispatch the kernel form `path` names (its symbol ends in
+    _<path>, a skinny form's row count after it), so every case below runs the
+    epilogue it is labelled with."""
+    m, k = a.shape
+    n = b.shape[0]
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=epilogue,
+                 permissions=L.PERMITS_REASSOCIATION, ctx=ctx)
+    assert len(rz.symbols) == 1 and re.search(rf"_{path}\d*$", rz.symbols[0]), (path, rz.symbols)
+    print(f"[silu path] {path}: {rz.symbols[0]} m={m} n={n} k={k}", flush=True)
+    bufs = [ctx.to_device(a), ctx.to_device(b), ctx.alloc(m * n * 2)]
+    try:
+        route(ctx, rz, bufs)
+        return bufs[2].download(np.uint16, (m, n))
+    finally:
+        for x in bufs:
+            x.free()
+
+
 @pytest.mark.parametrize("m,n,pad,path", [
     (4096, 4096, 0, "t256_kf"),  # 256 tiles of 256 fill every CU; k a multiple of 64
     (4096, 4096, 8, "t256"),     # the same with a ragged last k tile
@@ -127,10 +148,10 @@ def test_fused_silu_is_reference_silu_on_each_path(ctx, m, n, pad, path):
     g = np.arange(n) % groups
     for t in range(3):
         b[np.arange(n), 3 * g + t] = 0x3F80  # bf16 1.0
-    got = families.contract_bf16(a, b, L.EPILOGUE_SILU, ctx=ctx)
+    got = _contract_on_path(ctx, a, b, L.EPILOGUE_SILU, path)
     acc = vals[:, g]  # C[i, j] = v[i, j % groups] exactly
     want = oracle.bf16_narrow(oracle.silu_f32(vals))[:, g]  # each distinct accumulator once
-    plain = families.contract_bf16(a, b, L.EPILOGUE_NONE, ctx=ctx)
+    plain = _contract_on_path(ctx, a, b, L.EPILOGUE_NONE, path)
     assert np.array_equal(plain, oracle.bf16_narrow(acc).reshape(m, n)), "accumulators are not exact"
     diff = np.argwhere(got != want)
     assert diff.size == 0, (f"{path}: {len(diff)} outputs differ, first at {tuple(diff[0])}: "

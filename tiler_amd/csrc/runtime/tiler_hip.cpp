@@ -342,6 +342,19 @@ hipStream_t pick(tiler_hip_context* ctx, tiler_hip_stream s) {
   return s ? static_cast<hipStream_t>(s) : ctx->stream;
 }
 
+// The context workspace (the tree and split partials, the row-synchronized
+// softmax's words, the gather record) is ordered by the context's own stream
+// only.  A call that would bind it on another stream could overlap a call on
+// the context stream and corrupt both with no status, so it refuses before
+// anything is enqueued (the single ordered stream of
+// docs/decisions/0090-...md:152-154, where every unsupported case is refused).
+tiler_hip_status workspace_stream(tiler_hip_context* ctx, tiler_hip_stream s, const char* what) {
+  if (s && static_cast<hipStream_t>(s) != ctx->stream)
+    return fail(ctx, TILER_HIP_REFUSE_UNSUPPORTED,
+                std::string(what) + " binds the context workspace, which only the context's own stream orders");
+  return TILER_HIP_OK;
+}
+
 hipFunction_t fn(tiler_hip_context* ctx, const char* symbol) {
   auto it = ctx->fns.find(symbol);
   return it == ctx->fns.end() ? nullptr : it->second;
@@ -362,6 +375,13 @@ tiler_hip_status launch(tiler_hip_context* ctx, const char* symbol, uint32_t gx,
 // Rows longer than one wave holds run one workgroup per row, softmax's by
 // segments (the grouping tiler_hip_row_grouping reports).
 using tiler_rt::kWaveRowMax;
+
+// Every live extent is a 32-bit launch field inside the range its
+// realization's slots were sized for (callers check extent_ranges first).
+bool live_extent_in_range(const tiler_hip_dispatch_plan* plan, uint32_t x) {
+  const uint64_t v = plan->extents[x];
+  return v <= 0xffffffffull && v >= plan->extent_ranges[x].minimum && v <= plan->extent_ranges[x].bound;
+}
 
 // Partials beyond the workspace are allocated on the stream; under graph
 // capture that would record an allocation node, so such calls refuse there.
@@ -1037,16 +1057,14 @@ tiler_hip_status tiler_hip_plan_dispatch(tiler_hip_context* ctx,
     }
   }
   if (plan->extent_count && !plan->extents) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  // The ranges are what the realization's slots were sized for; without them
+  // a value could not be told from one that reads past its operands.
+  if (plan->extent_count && !plan->extent_ranges)
+    return fail(ctx, TILER_HIP_REFUSE_INVALID_ARGUMENT, "live extents without the ranges they were sized for");
   for (uint32_t x = 0; x < plan->extent_count; ++x) {
-    // Every live extent is a 32-bit launch field; a range, when given, is
-    // what the realization's slots were sized for.
-    const uint64_t v = plan->extents[x];
-    const bool in_range = plan->extent_ranges
-                              ? v >= plan->extent_ranges[x].minimum && v <= plan->extent_ranges[x].bound
-                              : true;
-    if (v > 0xffffffffull || !in_range)
+    if (!live_extent_in_range(plan, x))
       return fail(ctx, TILER_HIP_REFUSE_CAPACITY,
-                  "live extent " + std::to_string(x) + " = " + std::to_string(v) +
+                  "live extent " + std::to_string(x) + " = " + std::to_string(plan->extents[x]) +
                       " outside the range the realization was sized for");
   }
   return TILER_HIP_OK;
@@ -1076,6 +1094,16 @@ tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_disp
                                     void* const* slot_pointers) try {
   if (!ctx || !plan) return TILER_HIP_FAIL_LAUNCH;
   hipSetDevice(ctx->device);
+  // The live extents again, before anything is launched: the plan that was
+  // checked may not be the one dispatched, and a value past its bound would
+  // make the kernels read past operands sized for the bound.
+  if (plan->extent_count && (!plan->extents || !plan->extent_ranges))
+    return fail(ctx, TILER_HIP_FAIL_LAUNCH, "live extents without their values or ranges");
+  for (uint32_t x = 0; x < plan->extent_count; ++x)
+    if (!live_extent_in_range(plan, x))
+      return fail(ctx, TILER_HIP_FAIL_LAUNCH,
+                  "live extent " + std::to_string(x) + " = " + std::to_string(plan->extents[x]) +
+                      " outside the range the realization was sized for; nothing launched");
   // Constant slots first (an expression's register program), ordered on the
   // stream before every entry; the host bytes are the caller's for the call.
   if (plan->slot_contents) {
@@ -1343,6 +1371,7 @@ tiler_hip_status tiler_hip_sum_f32(tiler_hip_context* ctx, const float* x, uint6
   bool own = false;
   if (p.nslots > 2 && p.nlaunches) {
     if (p.slot_bytes[2] <= tiler_rt::kWorkspacePartialBytes) {
+      if ((st = workspace_stream(ctx, stream, "this sum's partials")) != TILER_HIP_OK) return st;
       slots[2] = ctx->sum_partials;
     } else {
       if (capturing(s))
@@ -1420,10 +1449,12 @@ tiler_hip_status tiler_hip_softmax_f32(tiler_hip_context* ctx, const float* x, u
   uint8_t* part = nullptr;
   if (p.nslots == 3) {  // the row-synchronized form: its area in the workspace
     if (p.slot_bytes[2] > tiler_rt::kRowSyncBytes) return fail(ctx, TILER_HIP_REFUSE_CAPACITY, "row-sync area");
+    if ((st = workspace_stream(ctx, stream, "the row-synchronized softmax")) != TILER_HIP_OK) return st;
     slots[2] = ctx->row_sync;
   } else if (p.nslots > 2) {
     const uint64_t bytes = p.slot_bytes[2] + p.slot_bytes[3];
     if (bytes <= tiler_rt::kWorkspacePartialBytes) {
+      if ((st = workspace_stream(ctx, stream, "the split softmax's partials")) != TILER_HIP_OK) return st;
       part = reinterpret_cast<uint8_t*>(ctx->sum_partials);
     } else {
       if (capturing(s))
@@ -1515,6 +1546,8 @@ tiler_hip_status tiler_hip_gather(tiler_hip_context* ctx, const void* source, ui
                                               count, index_signed, addr, p);
   if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
   if (p.nlaunches && (!source || !index || !out)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (p.nlaunches && (st = workspace_stream(ctx, stream, "the gather's out-of-range record")) != TILER_HIP_OK)
+    return st;
   void* slots[tiler_rt::kMaxSlots] = {const_cast<void*>(source), const_cast<uint32_t*>(index), out,
                                       ctx->gather_bad};
   return run_program(ctx, p, slots, pick(ctx, stream));
@@ -1525,6 +1558,8 @@ tiler_hip_status tiler_hip_gather(tiler_hip_context* ctx, const void* source, ui
 tiler_hip_status tiler_hip_gather_status(tiler_hip_context* ctx, tiler_hip_stream stream,
                                          uint64_t* bad_position) try {
   if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  if (tiler_hip_status st = workspace_stream(ctx, stream, "the gather record's read"); st != TILER_HIP_OK)
+    return st;
   hipStream_t s = pick(ctx, stream);
   unsigned long long v = 0;
   if (hipMemcpyAsync(&v, ctx->gather_bad, 8, hipMemcpyDeviceToHost, s) != hipSuccess ||
