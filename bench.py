@@ -516,7 +516,48 @@ class Expression(Workload):
                 "sample": f"{done} elements of the oracle's expression evaluator in {el:.1f} s, single thread"}
 
 
-WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, SoftmaxDecode, Gather, Contract, Convert, Expression)}
+class Dequantize(Workload):
+    """Strict-affine U4 -> f32 dequantization (ScalarProgram::
+    StrictAffineU4Dequantize) of 2^28 codes packed LSB-first: 0.5 B read and
+    4 B written per element.  Not a BASELINE config, measured as a family of
+    its own."""
+    name = "dequantize"
+    kernel = "tiler_dequantize_u4_f32_v4"
+    n = 1 << 28
+    scale_bits, zero_point = 0x3C23D70A, 8  # 0.01, zero point 8
+    sets = 2  # 2 x 1.125 GiB touched per sweep
+
+    def config(self):
+        return {"workload": "dequantize strict-affine U4[2^28] (packed LSB-first, uniform codes) -> f32, "
+                            "scale 0.01, zero point 8", "buffer_sets": self.sets}
+
+    def work(self):  # algorithmic bytes per launch
+        return self.n // 2 + self.n * 4
+
+    def setup(self):
+        rng = np.random.default_rng(9)
+        self.sets_ = [self._keep(self.ctx.to_device(rng.integers(0, 256, self.n // 2, dtype=np.uint8)),
+                                 self.ctx.alloc(self.n * 4)) for _ in range(self.sets)]
+        return self.sets
+
+    def launch(self, i):
+        codes, y = self.sets_[i % self.sets]
+        self.ctx.dequantize_u4(codes, self.n, self.scale_bits, self.zero_point, y)
+
+    def cpu_baseline(self, budget_s):
+        import oracle
+        packed = np.random.default_rng(9).integers(0, 256, 1 << 21, dtype=np.uint8)
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s:
+            oracle.dequantize_u4(packed, packed.size * 2, self.scale_bits, self.zero_point)
+            done += packed.size * 2
+        el = time.perf_counter() - t0
+        return {"value": done * 4.5 / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done} elements of the oracle's dequantization in {el:.1f} s, single thread"}
+
+
+WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, SoftmaxDecode, Gather, Contract, Convert, Expression,
+                                 Dequantize)}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_all_families.md")

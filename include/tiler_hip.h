@@ -57,6 +57,7 @@ typedef int32_t tiler_hip_status;
 #define TILER_HIP_FAIL_DEVICE 3
 #define TILER_HIP_FAIL_GATHER_INDEX_OUT_OF_BOUNDS 4
 #define TILER_HIP_FAIL_TRANSFER 5
+#define TILER_HIP_FAIL_VALUE_DOMAIN 6 /* a bound value outside its type's domain, found on the device */
 
 typedef struct tiler_hip_context tiler_hip_context;
 typedef void *tiler_hip_stream; /* hipStream_t */
@@ -668,6 +669,18 @@ tiler_hip_status tiler_hip_gather(tiler_hip_context *ctx, const void *source, ui
  * only (TILER_HIP_REFUSE_UNSUPPORTED otherwise). */
 tiler_hip_status tiler_hip_gather_status(tiler_hip_context *ctx, tiler_hip_stream stream,
                                          uint64_t *bad_position);
+/* Strict per-tensor affine U4 -> f32 dequantization
+ * (dequantize-strict-affine; tiler-reference/src/quantization.rs:218-246 and
+ * :409-419, ScalarProgram::StrictAffineU4Dequantize, tiler-ir/src/schedule/
+ * model.rs:682-696): n codes packed U4 LSB-first in (n + 1) / 2 U8 carriers
+ * with a zero tail; y[i] = (code_i - zero_point) * scale as binary32, +0.0
+ * where code_i == zero_point.  scale_bits must be a positive normal binary32
+ * and zero_point at most 15 (the value contract, quantization.rs:318-370):
+ * otherwise TILER_HIP_REFUSE_INVALID_ARGUMENT before anything is enqueued. */
+tiler_hip_status tiler_hip_dequantize_u4(tiler_hip_context *ctx, const uint8_t *codes, uint64_t n,
+                                        uint32_t scale_bits, uint32_t zero_point, float *y,
+                                        tiler_hip_stream stream);
+
 /* Pre-commit form of the same bound rule for host-resident indices:
  * TILER_HIP_REFUSE_GATHER_INDEX_OUT_OF_BOUNDS naming the first position. */
 tiler_hip_status tiler_hip_validate_gather_index(const uint32_t *index, uint64_t index_count,
@@ -777,6 +790,10 @@ tiler_hip_status tiler_hip_contract(tiler_hip_context *ctx, uint32_t dtype,
                                            StrictSerialMaximum (:920) */
 #define TILER_HIP_PROGRAM_REINDEX 11    /* structural reindex with signed strides (the mirrored reindex,
                                            tiler-metal/goldens/structural_mirrored_reindex.metal) */
+#define TILER_HIP_PROGRAM_DEQUANTIZE_U4 12 /* ::StrictAffineU4Dequantize (model.rs:682-696): slots codes,
+                                              scale, zero point, y, and a 4-byte scratch slot where the
+                                              kernel records the operands' domain verdict (0 in domain,
+                                              1 scale, 2 zero point); extents[0] = element count */
 
 /* PROGRAM_FOLD variants.  The input is dense row-major with `rank` dims in
  * extents[]; grouping[0] is the reduced-axis mask (bit d: axis d reduced);

@@ -85,6 +85,8 @@ _SIGS = {
     "tiler_oracle_softmax_f32": (_I32, [_P, _U64, _U64, _U64, _P, _I32, _I32]),
     "tiler_oracle_rms_norm_f32": (_I32, [_P, _P, _U64, _U64, _U64, _U32, _P, _I32, _I32]),
     "tiler_oracle_gather": (_I32, [_P, _U64, _U64, _U64, _U32, _P, _U64, _I32, _P, _P, _P]),
+    "tiler_oracle_dequantize_u4": (_I32, [_P, _U64, _U32, ctypes.c_uint8, _P]),
+    "tiler_oracle_strict_affine_domain": (_I32, [_U32, ctypes.c_uint8]),
     "tiler_oracle_contract_strict_f32": (_I32, [_P, _P, _U64, _U64, _U64, _P, _U64, _U64, _U32]),
     "tiler_oracle_contract_general": (_I32, [_U32, _I32, _U32, _P, _P, _U32, _P, _P, _U32, _P, _P, _P, _P,
                                              _U32]),
@@ -252,6 +254,35 @@ def rms_norm_f32(values, weights, shape, axis, eps_bits, input_mode=PRESERVE,
     _check(lib().tiler_oracle_rms_norm_f32(_ptr(x), _ptr(w), outer, extent, inner, eps_bits,
                                            _ptr(out), input_mode, result_mode), "rms_norm_f32")
     return out
+
+
+def pack_u4(codes) -> np.ndarray:
+    """U4 codes (values 0..15) packed LSB-first into U8 carriers with a zero
+    tail (schedule/model.rs:682-696): element i is nibble i % 2 of byte i / 2."""
+    c = np.asarray(codes, dtype=np.uint8).reshape(-1)
+    if c.size and int(c.max()) > 15:
+        raise ValueError("a U4 code above 15")
+    padded = np.zeros(c.size + (c.size & 1), np.uint8)
+    padded[:c.size] = c
+    return (padded[0::2] | (padded[1::2] << 4)).astype(np.uint8)
+
+
+def dequantize_u4(packed, n: int, scale_bits: int, zero_point: int) -> np.ndarray:
+    """quantization.rs:218-246, :409-419 over n packed U4 codes; raises
+    ValueError for a scale outside positive-normal-f32 or a zero point above
+    15 (the value contract, quantization.rs:318-370)."""
+    p = np.ascontiguousarray(np.asarray(packed, dtype=np.uint8))
+    if p.size < (n + 1) // 2:
+        raise ValueError("fewer carriers than codes")
+    out = np.empty(n, np.float32)
+    if lib().tiler_oracle_dequantize_u4(_ptr(p), n, scale_bits & 0xFFFFFFFF, zero_point & 0xFF, _ptr(out)) != OK:
+        raise ValueError("strict-affine value outside its domain")
+    return out
+
+
+def strict_affine_domain(scale_bits: int, zero_point: int) -> int:
+    """0 valid, 1 scale outside positive-normal-f32, 2 zero point above 15."""
+    return lib().tiler_oracle_strict_affine_domain(scale_bits & 0xFFFFFFFF, zero_point & 0xFF)
 
 
 def gather(source: np.ndarray, outer: int, gathered: int, inner: int, index,

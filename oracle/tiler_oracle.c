@@ -17,6 +17,9 @@
  *   rms_norm / softmax / silu -- every worked example and boundary row of
  *     rms_norm/tests.rs:253-420, softmax/tests.rs:362-651, silu/tests.rs:35-91;
  *   gather -- gather_conformance.rs:181-398 rows;
+ *   strict-affine U4 dequantize -- the dequantize_one and scale-domain rows of
+ *     quantization.rs:638-703 and every (code, zero point) pair against exact
+ *     integer arithmetic (tests/test_oracle.py);
  *   strict contraction -- the six SHA-256 digests of
  *     tiler-reference/tests/contraction_profile_cells.rs:148-200;
  *   bf16 narrowing -- closed form (ADR 0091 decision 2) checked exhaustively
@@ -457,6 +460,40 @@ int32_t tiler_oracle_gather(const void *source, uint64_t outer, uint64_t gathere
             uint64_t sel = index_signed ? (uint64_t)(int64_t)(int32_t)index[i] : index[i];
             memcpy(dst + (o * index_count + i) * run, src + (o * gathered + sel) * run, run);
         }
+    }
+    return TILER_ORACLE_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* quantization.rs:318-345 read_scale_value: the scale domain is
+ * positive-normal-f32 (f32::is_normal and not negative), and :347-370
+ * read_zero_point_value: a U4 code, 0..=15. */
+int32_t tiler_oracle_strict_affine_domain(uint32_t scale_bits, uint8_t zero_point) {
+    const float scale = u2f(scale_bits);
+    if (fpclassify(scale) != FP_NORMAL || signbit(scale)) return 1;
+    if (zero_point > 15) return 2;
+    return 0;
+}
+
+/* quantization.rs:218-246 dequantize over a dense code tensor, each element
+ * by :409-419 dequantize_one: the zero point's own code is +0.0; otherwise
+ * the difference of the two codes, exact in binary32, times the scale (one
+ * rounding).  The codes arrive packed as the schedule's ScalarProgram reads
+ * them (model.rs:682-696: U4 LSB-first in U8 carriers, zero tail), the
+ * nibble the Metal emitter extracts as (carrier >> ((i & 1) * 4)) & 0x0f
+ * (tiler-metal/src/emit.rs:2047). */
+int32_t tiler_oracle_dequantize_u4(const uint8_t *codes, uint64_t n, uint32_t scale_bits,
+                                   uint8_t zero_point, float *out) {
+    if (tiler_oracle_strict_affine_domain(scale_bits, zero_point) != 0) return TILER_ORACLE_INVALID_APPLICATION;
+    const float scale = u2f(scale_bits);
+    for (uint64_t i = 0; i < n; ++i) {
+        const int32_t code = (codes[i / 2] >> ((i & 1) * 4)) & 0x0f;
+        if (code == (int32_t)zero_point) {
+            out[i] = 0.0f;
+            continue;
+        }
+        const float difference = (float)(code - (int32_t)zero_point);
+        out[i] = difference * scale;
     }
     return TILER_ORACLE_OK;
 }

@@ -183,6 +183,19 @@ int32_t tiler_oracle_audit_device_exp(int32_t margin_log2, int32_t planted_log2,
                                       uint64_t *checked, uint64_t *mismatches,
                                       float *first_mismatch);
 
+/* Strict per-tensor affine U4 -> f32 dequantization
+ * (tiler-reference/src/quantization.rs:218-246 dequantize, :409-419
+ * dequantize_one; codes packed U4 LSB-first with a zero tail,
+ * tiler-ir/src/schedule/model.rs:682-696).  Element i is nibble i % 2 (low
+ * first) of byte i / 2.  scale must be a positive normal binary32
+ * (quantization.rs:318-345) and the zero point lie in 0..=15 (:347-370), else
+ * TILER_ORACLE_INVALID_APPLICATION with nothing written.  A code equal to the
+ * zero point decodes to +0.0; any other to fl((code - zero_point) * scale). */
+int32_t tiler_oracle_dequantize_u4(const uint8_t *codes, uint64_t n, uint32_t scale_bits,
+                                   uint8_t zero_point, float *out);
+/* The same domain rules alone: 0 ok, 1 scale, 2 zero point. */
+int32_t tiler_oracle_strict_affine_domain(uint32_t scale_bits, uint8_t zero_point);
+
 #ifdef __cplusplus
 }
 #endif

@@ -485,3 +485,69 @@ def test_bf16_narrowing_matches_exact_rounding():
     for p, v, g in zip(pats, vals, got):
         assert int(g) == _rne_bf16_exact(float(v)), hex(int(p))
     assert np.array_equal(bits(oracle.bf16_widen(got)), np.asarray([int(g) << 16 for g in got], np.uint32))
+
+
+# --- strict-affine U4 dequantization ------------------------------------------
+
+def test_dequantize_u4_reference_rows():
+    g = golden()["strict_affine_u4"]
+    for row in g["dequantize_one"]:
+        packed = oracle.pack_u4([row["code"]])
+        got = oracle.dequantize_u4(packed, 1, int(row["scale_bits"], 16), row["zero_point"])
+        assert int(bits(got)[0]) == hexbits(row["value_bits"]), row["source"]
+
+
+def test_dequantize_u4_scale_and_zero_point_domain():
+    g = golden()["strict_affine_u4"]
+    packed = oracle.pack_u4([7, 8])
+    for b in g["invalid_scale_bits"]["bits"]:
+        assert oracle.strict_affine_domain(int(b, 16), 8) == 1, b
+        with pytest.raises(ValueError):
+            oracle.dequantize_u4(packed, 2, int(b, 16), 8)
+    assert oracle.strict_affine_domain(int(g["smallest_normal_scale_bits"]["bits"], 16), 8) == 0
+    assert oracle.strict_affine_domain(0x3F000000, 15) == 0
+    assert oracle.strict_affine_domain(0x3F000000, 16) == 2
+    assert oracle.strict_affine_domain(0x7F7FFFFF, 0) == 0  # the largest finite scale is normal
+
+
+def test_dequantize_u4_packing_is_lsb_first_with_a_zero_tail():
+    g = golden()["strict_affine_u4"]["packing"]
+    carriers = np.array([int(c, 16) for c in g["carriers"]], np.uint8)
+    assert np.array_equal(oracle.pack_u4(g["codes"]), carriers)
+    got = oracle.dequantize_u4(carriers, 3, 0x3F800000, 0)
+    assert got.tolist() == [float(c) for c in g["codes"]]
+
+
+@pytest.mark.parametrize("scale_bits", [0x00800000, 0x3F000000, 0x3DCCCCCD, 0x7F7FFFFF, 0x7E800001, 0x0E5A3C11])
+def test_dequantize_u4_every_code_and_zero_point_is_one_rounding(scale_bits):
+    """All 16 codes x 16 zero points: the difference is an exact integer, its
+    product with the scale is exact in binary64 (5 + 24 significant bits), so
+    one rounding of that product to binary32 is the IEEE product; the zero
+    point's own code is +0.0; at the smallest normal scale every value is +0.0
+    or normal (quantization.rs:687-703)."""
+    scale = np.uint32(scale_bits).view(np.float32)
+    codes = np.tile(np.arange(16, dtype=np.uint8), 1)
+    for zp in range(16):
+        got = oracle.dequantize_u4(oracle.pack_u4(codes), 16, scale_bits, zp)
+        diff = codes.astype(np.int64) - zp
+        with np.errstate(over="ignore"):
+            want = (diff.astype(np.float64) * np.float64(scale)).astype(np.float32)
+        want[diff == 0] = np.float32(0.0)  # +0.0, never -0.0
+        assert np.array_equal(bits(got), bits(want)), (hex(scale_bits), zp)
+        if scale_bits == 0x00800000:
+            assert all(v == 0 or (np.isfinite(v) and abs(v) >= np.finfo(np.float32).tiny) for v in got)
+
+
+def test_dequantize_u4_a_planted_mistake_fails_the_exhaustive_check():
+    """The independent formula of the exhaustive check separates the
+    reference's decode from two plausible mistakes: the high nibble taken
+    first, and (zero point - code) for (code - zero point)."""
+    codes = np.arange(16, dtype=np.uint8)
+    packed = oracle.pack_u4(codes)
+    got = oracle.dequantize_u4(packed, 16, 0x3F800000, 3)
+    high_first = np.concatenate([[(p >> 4) & 15, p & 15] for p in packed]).astype(np.float32) - 3
+    negated = (3 - codes.astype(np.int64)).astype(np.float32)
+    want = (codes.astype(np.int64) - 3).astype(np.float32)
+    assert np.array_equal(bits(got), bits(want))
+    assert not np.array_equal(bits(got), bits(high_first))
+    assert not np.array_equal(bits(got), bits(negated))

@@ -281,6 +281,28 @@ def test_conversion_families():
         realize(L.PROGRAM_CONVERT, (8,), variant=7)
 
 
+def test_strict_affine_u4_dequantize():
+    """StrictAffineU4Dequantize (model.rs:682-696): slots [codes, scale, zero
+    point, y, domain record]; the vector form for aligned whole 4-element
+    groups, else the scalar form over everything; a flushing contract is
+    realized as the strict one (no operand or product is subnormal)."""
+    rz = realize(L.PROGRAM_DEQUANTIZE_U4, (4096,))
+    assert rz.symbols == ["tiler_dequantize_u4_f32_v4_slots"]
+    assert rz.slots == [(L.SLOT_INPUT, 2048), (L.SLOT_INPUT, 4), (L.SLOT_INPUT, 1), (L.SLOT_OUTPUT, 16384),
+                        (L.SLOT_SCRATCH, 4)]
+    assert rz.dispatches[0].bindings == [(0, 0), (1, 16), (2, 24), (3, 32), (4, 40)]
+    assert realize(L.PROGRAM_DEQUANTIZE_U4, (4097,)).symbols == ["tiler_dequantize_u4_f32_slots"]
+    assert realize(L.PROGRAM_DEQUANTIZE_U4, (4096,), flags=0).symbols == ["tiler_dequantize_u4_f32_slots"]
+    assert realize(L.PROGRAM_DEQUANTIZE_U4, (5,)).slots[0] == (L.SLOT_INPUT, 3)  # zero-tail carrier
+    flushed = realize(L.PROGRAM_DEQUANTIZE_U4, (4096,), input_subnormals=L.SUBNORMALS_FLUSH_SIGN,
+                      result_subnormals=L.SUBNORMALS_FLUSH_POSITIVE)
+    assert flushed.symbols == rz.symbols
+    with pytest.raises(Refusal) as e:
+        realize(L.PROGRAM_DEQUANTIZE_U4, (64,), dtype=L.BF16)
+    assert e.value.status == L.REFUSE_UNSUPPORTED
+    assert realize(L.PROGRAM_DEQUANTIZE_U4, (0,)).raw.entry_count == 0
+
+
 def test_zero_work_skips_dispatch():
     assert realize(L.PROGRAM_SOFTMAX, (0, 2048)).raw.entry_count == 0
     assert realize(L.PROGRAM_CONTRACTION, (0, 64, 64), dtype=L.BF16).raw.entry_count == 0

@@ -30,6 +30,7 @@ FAIL_LAUNCH = 2
 FAIL_DEVICE = 3
 FAIL_GATHER_INDEX_OUT_OF_BOUNDS = 4
 FAIL_TRANSFER = 5
+FAIL_VALUE_DOMAIN = 6
 
 F32 = 0
 BF16 = 1
@@ -62,6 +63,7 @@ PROGRAM_CONVERT = 8
 PROGRAM_EXPRESSION = 9
 PROGRAM_FOLD = 10
 PROGRAM_REINDEX = 11
+PROGRAM_DEQUANTIZE_U4 = 12
 
 FOLD_SUM = 0
 FOLD_SQUARED = 1
@@ -484,6 +486,7 @@ SIGNATURES = {
                                  _U32, _P, _P]),
     "tiler_hip_gather": (_S, [_CTX, _P, _U64, _U64, _U64, _U32, _P, _U64, _I32, _P, _P]),
     "tiler_hip_convert": (_S, [_CTX, _U32, _P, _U64, _P, _P]),
+    "tiler_hip_dequantize_u4": (_S, [_CTX, _P, _U64, _U32, _U32, _P, _P]),
     "tiler_hip_gather_status": (_S, [_CTX, _P, ctypes.POINTER(_U64)]),
     "tiler_hip_validate_gather_index": (_S, [_P, _U64, _I32, _U64, ctypes.POINTER(_U64),
                                              ctypes.POINTER(ctypes.c_int64)]),

@@ -12,3 +12,4 @@
 #include "convert.hip"
 #include "contract.hip"
 #include "contract_general.hip"
+#include "dequantize.hip"

@@ -539,6 +539,52 @@ tiler_hip_status plan_convert(Mode mode, uint32_t direction, uint64_t n, const u
 }
 
 // ---------------------------------------------------------------------------
+// Strict-affine U4 dequantization (quantization.rs:218-246, :409-419).
+// Direct: slots 0 codes (packed U4, (n + 1) / 2 carriers), 1 y f32 [n]; the
+// host checked the scale and zero point, which travel as launch values.
+// Realized: slots 0 codes, 1 scale (f32 scalar), 2 zero point (U8 scalar),
+// 3 y, 4 the domain verdict the kernel records (scratch, 4 bytes).
+tiler_hip_status plan_dequantize_u4(Mode mode, uint64_t n, uint32_t scale_bits, uint32_t zero_point,
+                                    const uintptr_t* addr, Program& p) {
+  const bool realized = mode == Mode::Realized;
+  const uint32_t codes = p.slot(n / 2 + (n & 1), kSlotInput);
+  uint32_t scale = 0, zero = 0;
+  if (realized) {
+    scale = p.slot(4, kSlotInput);
+    zero = p.slot(1, kSlotInput);
+  }
+  const uint32_t y = p.slot(mul_sat(n, 4), kSlotOutput);
+  const uint32_t record = realized ? p.slot(4, kSlotScratch) : 0;
+  if (!realized) {
+    const float sc = __builtin_bit_cast(float, scale_bits);
+    if (!std::isnormal(sc) || sc < 0.0f)
+      return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT,
+                      "scale outside positive-normal-f32 (the strict-affine value contract)");
+    if (zero_point > 15) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "zero point outside the U4 code domain 0..=15");
+  }
+  if (n == 0) return TILER_HIP_OK;
+  uint64_t head = aligned16(addr[codes]) && aligned16(addr[y]) ? n / 4 * 4 : 0;
+  if (realized && head != n) head = 0;  // a plan binds slot bases: one kernel over all of it
+  if (head) {
+    Launch& l = p.add(realized ? "tiler_dequantize_u4_f32_v4_slots" : "tiler_dequantize_u4_f32_v4",
+                      blocks_capped((head / 4 + 1) / 2, 1u << 30), 1, 256)
+                    .ptr(codes)
+                    .u64(head / 4);
+    if (realized) l.ptr(scale).ptr(zero).ptr(y).ptr(record);
+    else l.u32(scale_bits).u32(zero_point).ptr(y);
+    if (head == n) return TILER_HIP_OK;
+  }
+  if (realized) {
+    p.add("tiler_dequantize_u4_f32_slots", blocks_capped(n, 8192), 1, 256)
+        .ptr(codes).u64(n).ptr(scale).ptr(zero).ptr(y).ptr(record);
+  } else {
+    p.add("tiler_dequantize_u4_f32", blocks_capped(n - head, 8192), 1, 256)
+        .ptr(codes).u64(head).u64(n - head).u32(scale_bits).u32(zero_point).ptr(y);
+  }
+  return TILER_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Contractions.  Slots: 0 a [m, k], 1 b [n, k], 2 c [m, n].
 // The live contracted extent: read at dispatch from input 0 (A[m][k]), axis 1,
 // at least 1 (an empty contracted domain has no unseeded result) and at most

@@ -180,6 +180,8 @@ tiler_hip_status plan_convert(Mode mode, uint32_t direction, uint64_t n, const u
                               Program& p);
 // live_k: k is read at dispatch (live extent 0, input 0 axis 1, in [1, k]);
 // the slots hold operands of the bound k.
+tiler_hip_status plan_dequantize_u4(Mode mode, uint64_t n, uint32_t scale_bits, uint32_t zero_point,
+                                    const uintptr_t* addr, Program& p);
 tiler_hip_status plan_contract_strict_f32(const Target& t, uint64_t m, uint64_t n, uint64_t k, const uintptr_t* addr,
                                           Program& p, bool live_k = false);
 // Any admitted binary index structure: the strict fold (f32, or bf16 without

@@ -173,6 +173,10 @@ const EntryRow kEntries[] = {
     {"tiler_narrow_f32_bf16", "convert-f32-to-bf16/narrow", 2},
     {"tiler_widen_bf16_f32_v8", "convert-bf16-to-f32/widen", 2},
     {"tiler_widen_bf16_f32", "convert-bf16-to-f32/widen", 2},
+    {"tiler_dequantize_u4_f32_v4", "dequantize-strict-affine-u4", 2},
+    {"tiler_dequantize_u4_f32", "dequantize-strict-affine-u4", 2},
+    {"tiler_dequantize_u4_f32_v4_slots", "dequantize-strict-affine-u4", 5},
+    {"tiler_dequantize_u4_f32_slots", "dequantize-strict-affine-u4", 5},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_strict_f32_b16", "tensor-contraction-f32/strict", 3},
     {"tiler_contract_strict_f32_b32", "tensor-contraction-f32/strict", 3},
@@ -1518,6 +1522,21 @@ tiler_hip_status tiler_hip_convert(tiler_hip_context* ctx, uint32_t direction, c
   return TILER_HIP_REFUSE_CAPACITY;
 }
 
+tiler_hip_status tiler_hip_dequantize_u4(tiler_hip_context* ctx, const uint8_t* codes, uint64_t n,
+                                        uint32_t scale_bits, uint32_t zero_point, float* y,
+                                        tiler_hip_stream stream) try {
+  if (!ctx) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  tiler_rt::Program p;
+  const uintptr_t addr[2] = {(uintptr_t)codes, (uintptr_t)y};
+  tiler_hip_status st = tiler_rt::plan_dequantize_u4(tiler_rt::Mode::Direct, n, scale_bits, zero_point, addr, p);
+  if (st != TILER_HIP_OK) return fail(ctx, st, p.diag);
+  if (p.nlaunches && (!codes || !y)) return TILER_HIP_REFUSE_INVALID_ARGUMENT;
+  void* slots[tiler_rt::kMaxSlots] = {const_cast<uint8_t*>(codes), y};
+  return run_program(ctx, p, slots, pick(ctx, stream));
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_REFUSE_CAPACITY;
+}
+
 tiler_hip_status tiler_hip_validate_gather_index(const uint32_t* index, uint64_t count,
                                                  int32_t index_signed, uint64_t gathered,
                                                  uint64_t* bad_position, int64_t* bad_value) try {
@@ -1844,9 +1863,14 @@ tiler_rt::Contract contract_of(const tiler_hip_region* r) {
   return c;
 }
 
+// Programs whose arithmetic a flushing subnormal mode could change.  The
+// strict-affine decode is not one: its scale is a positive normal and its
+// code difference an integer of magnitude 0 or at least 1, so every operand
+// and product lies outside the subnormal range and both modes have nothing to
+// act on (quantization.rs:1-15, :400-408); the reference applies neither.
 bool arithmetic(uint32_t program) {
   return program != TILER_HIP_PROGRAM_GATHER && program != TILER_HIP_PROGRAM_BROADCAST &&
-         program != TILER_HIP_PROGRAM_REINDEX;
+         program != TILER_HIP_PROGRAM_REINDEX && program != TILER_HIP_PROGRAM_DEQUANTIZE_U4;
 }
 
 }  // namespace
@@ -1978,6 +2002,13 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
     }
     case TILER_HIP_PROGRAM_CONVERT:
       st = tiler_rt::plan_convert(tiler_rt::Mode::Realized, r->variant, e[0], addr, p);
+      break;
+    case TILER_HIP_PROGRAM_DEQUANTIZE_U4:
+      // ScalarProgram::StrictAffineU4Dequantize reads [U8 codes, F32 scale,
+      // U8 zero point] (model.rs:682-696); binary32 output only.
+      st = r->dtype == TILER_HIP_F32
+               ? tiler_rt::plan_dequantize_u4(tiler_rt::Mode::Realized, e[0], 0, 0, addr, p)
+               : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the strict-affine U4 decode produces f32");
       break;
     default:
       st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "no realization for this scalar program");

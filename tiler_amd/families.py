@@ -239,8 +239,26 @@ def contract_bf16(a_bits: np.ndarray, b_bits: np.ndarray, epilogue: int = L.EPIL
         dc.free()
 
 
+def dequantize_u4(packed: np.ndarray, n: int, scale_bits: int, zero_point: int, ctx=None) -> np.ndarray:
+    """Strict-affine U4 -> f32 on the device (quantization.rs:218-246):
+    `packed` holds n U4 codes LSB-first in (n + 1) // 2 U8 carriers."""
+    p = np.ascontiguousarray(np.asarray(packed, dtype=np.uint8))
+    if p.size < (n + 1) // 2:
+        raise Refusal(L.REFUSE_INVALID_ARGUMENT, "dequantize_u4", "fewer carriers than codes")
+    ctx = _ctx(ctx)
+    dc = ctx.to_device(p) if p.size else ctx.alloc(1)
+    dy = ctx.alloc(max(4 * n, 1))
+    try:
+        ctx.dequantize_u4(dc, n, scale_bits, zero_point, dy)
+        ctx.synchronize()
+        return dy.download(np.float32, (n,))
+    finally:
+        dc.free()
+        dy.free()
+
+
 __all__ = [
     "strict_sum", "strict_partitioned_sum", "cooperative_grouped_sum", "tree_sum",
     "rms_norm_f32", "rms_norm_bf16", "softmax_f32", "silu_f32", "gather",
-    "contract_strict_f32", "contract_bf16", "default_context", "GatherIndexOutOfBounds",
+    "contract_strict_f32", "contract_bf16", "dequantize_u4", "default_context", "GatherIndexOutOfBounds",
 ]

@@ -30,7 +30,7 @@ import ctypes
 from dataclasses import dataclass, field
 
 from . import _lib as L
-from .runtime import GatherIndexOutOfBounds, Refusal, _raise
+from .runtime import Failure, GatherIndexOutOfBounds, Refusal, _raise
 
 
 @dataclass
@@ -311,5 +311,14 @@ def route(ctx, realization: Realization, storage, payload=None, extents=()) -> N
             _raise(L.lib().tiler_hip_download(h, ctypes.byref(rec), ptrs[3], 8), "read gather record")
             if rec.value != 0xFFFFFFFFFFFFFFFF:
                 raise GatherIndexOutOfBounds(L.FAIL_GATHER_INDEX_OUT_OF_BOUNDS, rec.value)
+        elif rz.program == L.PROGRAM_DEQUANTIZE_U4:
+            # the kernel's verdict on the scale and zero point it read
+            # (quantization.rs:318-370): the output was not written
+            rec = ctypes.c_uint32()
+            _raise(L.lib().tiler_hip_download(h, ctypes.byref(rec), ptrs[4], 4), "read domain record")
+            if rec.value:
+                raise Failure(L.FAIL_VALUE_DOMAIN, "dispatch",
+                              "scale outside positive-normal-f32" if rec.value == 1
+                              else "zero point outside the U4 code domain 0..=15")
     finally:
         L.lib().tiler_hip_release_dispatch(h, ctypes.byref(plan), ptrs, owned)

@@ -259,6 +259,13 @@ class Context:
         self._check(L.lib().tiler_hip_convert(self.handle, direction, _ptr(src), n, _ptr(dst), stream),
                     "convert")
 
+    def dequantize_u4(self, codes, n: int, scale_bits: int, zero_point: int, y, stream=None):
+        """Strict-affine U4 -> f32 (quantization.rs:218-246): n codes packed
+        LSB-first in (n + 1) // 2 carriers; refuses a scale outside
+        positive-normal-f32 or a zero point above 15 before commit."""
+        self._check(L.lib().tiler_hip_dequantize_u4(self.handle, _ptr(codes), n, scale_bits & 0xFFFFFFFF,
+                                                     zero_point, _ptr(y), stream), "dequantize_u4")
+
     def gather(self, source, outer: int, gathered: int, inner: int, element_bytes: int, index,
                index_count: int, out, index_signed: bool = False, stream=None):
         self._check(L.lib().tiler_hip_gather(self.handle, _ptr(source), outer, gathered, inner,
