@@ -808,7 +808,16 @@ tiler_hip_status tiler_hip_contract(tiler_hip_context *ctx, uint32_t dtype,
  *            every contract admits                 empty: +0
  *   MAXIMUM  NaN-propagating IEEE maximum with -0 < +0 (softmax.rs:168-186);
  *            order-insensitive, so it spends no reassociation permission;
- *            an empty reduced domain is refused (model.rs:880-906) */
+ *            an empty reduced domain is refused (model.rs:880-906)
+ * The sums take the region's topology: SERIAL (any axes), or, under
+ * PERMITS_REASSOCIATION and over the trailing axis only, MULTIPASS
+ * (grouping[1] partitions of grouping[2]) and COOPERATIVE (grouping[1]
+ * participants, grouping[2] contributors per cell, RoundMajor unless
+ * TILER_HIP_REGION_PARTICIPANT_MAJOR, the rounds that cover the axis).
+ * Under a flushing contract every arithmetic site of the prologue and of
+ * each combine applies the declared modes, every fold seeded at its first
+ * contributor (evaluate.rs:575-583, 612-832, 845-1158); the maximum takes no
+ * mode.  An epilogue is realized serially under the preserving modes only. */
 #define TILER_HIP_FOLD_SUM 0u
 #define TILER_HIP_FOLD_SQUARED 1u
 #define TILER_HIP_FOLD_FMA 2u
@@ -863,7 +872,8 @@ typedef struct {
     uint64_t grouping[3];  /* multi-pass sum {partitions, per partition};
                               cooperative sum {participants, per partition, rounds};
                               broadcast {source elements}; reindex {source elements, base offset};
-                              fold {reduced-axis mask} */
+                              fold {reduced-axis mask, then the split's or the
+                              workgroup's two grouping fields} */
     uint32_t scalars[2];   /* rms_norm {eps bits}; pointwise {a bits, b bits} */
     uint32_t permissions;        /* TILER_HIP_PERMITS_*: the contract's regrouping freedoms */
     uint32_t input_subnormals;   /* TILER_HIP_SUBNORMALS_* (0: preserve) */

@@ -96,7 +96,7 @@ _SIGS = {
     "tiler_oracle_softmax_grouped_f32": (_I32, [_P, _U64, _U64, _U32, _U32, _P]),
     "tiler_oracle_softmax_segmented_f32": (_I32, [_P, _U64, _U64, _U64, _U32, _U32, _P]),
     "tiler_oracle_expression_f32": (_I32, [_P, _P, _P, _U32, _U32, _P, _U64, _P, _I32, _I32]),
-    "tiler_oracle_expression_bf16": (_I32, [_P, _P, _P, _U32, _U32, _P, _U64, _P]),
+    "tiler_oracle_expression_bf16": (_I32, [_P, _P, _P, _U32, _U32, _P, _U64, _P, _I32, _I32]),
     "tiler_oracle_bf16_exact_add": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16]),
     "tiler_oracle_bf16_exact_multiply": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16]),
     "tiler_oracle_fold_f32": (_I32, [_P, _U32, _P, _U64, _U32, _U32, _U32, _P, _I32, _I32]),
@@ -425,17 +425,18 @@ def expression_f32(nodes, inputs, root=None, input_mode=PRESERVE, result_mode=PR
     return y
 
 
-def expression_bf16(nodes, inputs, root=None) -> np.ndarray:
+def expression_bf16(nodes, inputs, root=None, input_mode=PRESERVE, result_mode=PRESERVE) -> np.ndarray:
     """A pointwise bf16 expression DAG (pointwise_bf16.rs): inputs and result
-    as bf16 bit patterns (uint16)."""
+    as bf16 bit patterns (uint16); the subnormal modes act on operand and
+    rounded-result encodings (bf16.rs:517-533)."""
     ops, a, b = _node_arrays(nodes)
     ins = [np.ascontiguousarray(x, dtype=np.uint16).reshape(-1) for x in inputs]
     n = ins[0].size if ins else 0
     ptrs = (ctypes.c_void_p * max(1, len(ins)))(*[x.ctypes.data for x in ins])
     y = np.empty(n, np.uint16)
     root = len(nodes) - 1 if root is None else root
-    _check(lib().tiler_oracle_expression_bf16(_ptr(ops), _ptr(a), _ptr(b), len(nodes), root, ptrs, n, _ptr(y)),
-           "expression_bf16")
+    _check(lib().tiler_oracle_expression_bf16(_ptr(ops), _ptr(a), _ptr(b), len(nodes), root, ptrs, n, _ptr(y),
+                                              input_mode, result_mode), "expression_bf16")
     return y
 
 

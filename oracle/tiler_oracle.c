@@ -982,9 +982,19 @@ static uint16_t bf16_of_q(q_t q) {
  * operands' exponents differ by more than ~104, and then the smaller lies
  * far below half a bf16 quantum of the larger and binary128 keeps it as a
  * sticky nonzero remainder, which is all the rounding reads. */
+/* bf16.rs:517-533 under a Bf16SubnormalRealization: accept_operand replaces a
+ * subnormal operand ENCODING by the input mode before it is decoded, commit
+ * replaces a subnormal ROUNDED result by the result mode.  A bf16 encoding is
+ * subnormal when its exponent field is zero and its significand is not. */
+static uint16_t bf16_subnormal_mode(int32_t mode, uint16_t bits) {
+    if (mode == TILER_ORACLE_PRESERVE) return bits;
+    if ((bits & 0x7f80u) != 0 || (bits & 0x007fu) == 0) return bits;
+    return mode == TILER_ORACLE_FLUSH_SIGN_PRESERVING ? (uint16_t)(bits & 0x8000u) : 0;
+}
+
 int32_t tiler_oracle_expression_bf16(const uint32_t *ops, const uint32_t *as, const uint32_t *bs,
                                      uint32_t count, uint32_t root, const uint16_t *const *inputs,
-                                     uint64_t n, uint16_t *y) {
+                                     uint64_t n, uint16_t *y, int32_t input_mode, int32_t result_mode) {
     if (count == 0 || root >= count) return TILER_ORACLE_INVALID_APPLICATION;
     for (uint32_t i = 0; i < count; ++i) {
         if (ops[i] > 3) return TILER_ORACLE_INVALID_APPLICATION;
@@ -999,9 +1009,9 @@ int32_t tiler_oracle_expression_bf16(const uint32_t *ops, const uint32_t *as, co
                 case 0: v[i] = inputs[as[i]][e]; break;
                 case 1: v[i] = (uint16_t)as[i]; break;
                 default: {
-                    const q_t x = (q_t)tiler_oracle_bf16_widen(v[as[i]]);
-                    const q_t z = (q_t)tiler_oracle_bf16_widen(v[bs[i]]);
-                    v[i] = bf16_of_q(ops[i] == 2 ? x + z : x * z);
+                    const q_t x = (q_t)tiler_oracle_bf16_widen(bf16_subnormal_mode(input_mode, v[as[i]]));
+                    const q_t z = (q_t)tiler_oracle_bf16_widen(bf16_subnormal_mode(input_mode, v[bs[i]]));
+                    v[i] = bf16_subnormal_mode(result_mode, bf16_of_q(ops[i] == 2 ? x + z : x * z));
                 }
             }
         }

@@ -157,7 +157,7 @@ int32_t tiler_oracle_expression_f32(const uint32_t *ops, const uint32_t *as, con
                                     uint64_t n, float *y, int32_t input_mode, int32_t result_mode);
 int32_t tiler_oracle_expression_bf16(const uint32_t *ops, const uint32_t *as, const uint32_t *bs,
                                      uint32_t count, uint32_t root, const uint16_t *const *inputs,
-                                     uint64_t n, uint16_t *y);
+                                     uint64_t n, uint16_t *y, int32_t input_mode, int32_t result_mode);
 uint16_t tiler_oracle_bf16_exact_add(uint16_t x, uint16_t z);
 uint16_t tiler_oracle_bf16_exact_multiply(uint16_t x, uint16_t z);
 

@@ -6,8 +6,8 @@ GPU -- each pinned by something other than a restatement of itself.
 Contract (tiler-ir/src/schedule/model.rs:1330-1340, 1381-1392, 1520-1531;
 tiler-compiler/src/session.rs:1793-1888): a zeroed region is the strict
 contract, so it must get the strict serial fold or refuse; a reassociating
-realization needs permits_reassociation; a flushing subnormal mode is refused
-wherever the kernels do not implement it.
+realization needs permits_reassociation; a flushing subnormal mode is realized
+where the kernels apply it and refused elsewhere.
 """
 from __future__ import annotations
 
@@ -83,13 +83,9 @@ def test_strict_contract_selects_the_serial_row_and_contraction_kernels():
 
 
 @pytest.mark.parametrize("program,extents,kw", [
-    (L.PROGRAM_SERIAL_SUM, (2, 100), {}),
-    (L.PROGRAM_RMS_NORM, (2, 100), dict(scalars=(EPS,))),
-    (L.PROGRAM_SOFTMAX, (2, 100), {}),
     (L.PROGRAM_CONTRACTION, (4, 4, 4), {}),
+    (L.PROGRAM_CONTRACTION, (4, 4, 64), dict(dtype=L.BF16, permissions=RE)),
     (L.PROGRAM_CONVERT, (64,), {}),
-    (L.PROGRAM_FOLD, (4, 4), dict(rank=2, grouping=(2,))),
-    (L.PROGRAM_EXPRESSION, (64,), dict(dtype=L.BF16, nodes=[(0, 0, 0), (2, 0, 0)])),
 ])
 @pytest.mark.parametrize("modes", [(L.SUBNORMALS_FLUSH_SIGN, 0), (0, L.SUBNORMALS_FLUSH_POSITIVE)])
 def test_flushing_modes_refuse_where_not_implemented(program, extents, kw, modes):
@@ -114,6 +110,58 @@ def test_flushing_modes_where_implemented_or_irrelevant():
     assert realize(L.PROGRAM_BROADCAST, (8, 4), variant=4, rank=2, strides=(0, 1), grouping=(4,),
                    result_subnormals=3).raw.entry_count == 1
     _refuses(L.REFUSE_INVALID_ARGUMENT, L.PROGRAM_EXPRESSION, (64,), nodes=nodes, input_subnormals=4)
+
+
+FS, FP = L.SUBNORMALS_FLUSH_SIGN, L.SUBNORMALS_FLUSH_POSITIVE
+
+
+@pytest.mark.parametrize("program,extents,kw,symbols", [
+    # sums and folds: the rule-driven kernels (first-contributor seeds, modes at every combine)
+    (L.PROGRAM_SERIAL_SUM, (2, 100), {}, ["tiler_sum_f32_staged_r1_m"]),
+    (L.PROGRAM_SERIAL_SUM, (4096, 40), {}, ["tiler_sum_f32_staged_r256_m"]),
+    (L.PROGRAM_SERIAL_SUM, (9, 7), {}, ["tiler_fold_f32_m"]),
+    (L.PROGRAM_SERIAL_SUM, (4, 100), dict(topology=L.SUM_MULTIPASS, grouping=(10, 10), permissions=RE),
+     ["tiler_sum_f32_partials_m", "tiler_fold_f32_m"]),
+    (L.PROGRAM_SERIAL_SUM, (4, 6400), dict(topology=L.SUM_MULTIPASS, grouping=(80, 80), permissions=RE),
+     ["tiler_sum_f32_staged_r4_m", "tiler_sum_f32_staged_r1_m"]),
+    (L.PROGRAM_SERIAL_SUM, (4, 100), dict(topology=L.SUM_COOPERATIVE, grouping=(10, 5, 2), permissions=RE),
+     ["tiler_sum_f32_cooperative_m"]),
+    (L.PROGRAM_FOLD, (64, 16384), dict(rank=2, grouping=(2,), variant=L.FOLD_FMA, scalars=(0x3F800000, 0)),
+     ["tiler_sum_f32_staged_r1_m"]),
+    (L.PROGRAM_FOLD, (64, 16384), dict(rank=2, grouping=(2, 256, 64), variant=L.FOLD_FMA, scalars=(0x3F800000, 0),
+                                       topology=L.SUM_COOPERATIVE, permissions=RE), ["tiler_sum_f32_cooperative_m"]),
+    (L.PROGRAM_FOLD, (4, 5, 6), dict(rank=3, grouping=(5,), variant=L.FOLD_SQUARED), ["tiler_fold_f32_m"]),
+    (L.PROGRAM_FOLD, (4, 5, 6), dict(rank=3, grouping=(5,), variant=L.FOLD_MAXIMUM), ["tiler_fold_maximum_f32"]),
+    # rows: the serial forms that take the modes, whatever the permissions
+    (L.PROGRAM_RMS_NORM, (8192, 4096), dict(scalars=(EPS,), dtype=L.BF16, permissions=RE),
+     ["tiler_rms_norm_bf16_strict"]),
+    (L.PROGRAM_SOFTMAX, (2, 100), {}, ["tiler_softmax_f32_strict"]),
+    # maps: the scalar forms with the modes; bf16 expressions: the one-element form
+    (L.PROGRAM_POINTWISE, (1024,), dict(variant=L.MAP_SILU), ["tiler_map_f32_m"]),
+    (L.PROGRAM_POINTWISE, (1024,), dict(variant=L.MAP_ADD, dtype=L.BF16), ["tiler_map_bf16_m"]),
+    (L.PROGRAM_EXPRESSION, (64,), dict(dtype=L.BF16, nodes=[(0, 0, 0), (2, 0, 0)]), ["tiler_expr_bf16_r16s_i1"]),
+])
+def test_flushing_modes_are_realized(program, extents, kw, symbols):
+    """A flushing contract realizes where the kernels apply the modes; the
+    modes travel in the argument segment (the last words, or the FoldRule's)."""
+    rz = realize(program, extents, input_subnormals=FS, result_subnormals=FP, **kw)
+    assert rz.symbols == symbols
+    if program == L.PROGRAM_FOLD and kw.get("variant") == L.FOLD_MAXIMUM:
+        return  # the maximum takes no mode
+    seg = bytes(rz.raw.entries[0].kernargs[:rz.raw.entries[0].kernarg_bytes])
+    words = struct.unpack_from(f"<{len(seg) // 4}I", seg)
+    assert any(words[i:i + 2] == (FS, FP) for i in range(len(words) - 1)), words
+
+
+def test_two_level_tree_refuses_a_flushing_contract():
+    e = _refuses(L.REFUSE_UNSUPPORTED, L.PROGRAM_SERIAL_SUM, (4, 100), topology=L.SUM_TREE, permissions=RE,
+                 input_subnormals=FS, result_subnormals=FS)
+    assert "cooperative" in e.diagnostic
+    # a split or workgroup fold needs the reassociation permission, and the trailing axis
+    _refuses(L.REFUSE_UNSUPPORTED, L.PROGRAM_FOLD, (64, 256), rank=2, grouping=(2, 16, 16),
+             topology=L.SUM_MULTIPASS)
+    _refuses(L.REFUSE_UNSUPPORTED, L.PROGRAM_FOLD, (64, 256), rank=2, grouping=(1, 8, 8),
+             topology=L.SUM_MULTIPASS, permissions=RE)
 
 
 @pytest.mark.parametrize("topology,grouping", [(L.SUM_TREE, ()), (L.SUM_COOPERATIVE, (1, 1, 1))])

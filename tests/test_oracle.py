@@ -551,3 +551,71 @@ def test_dequantize_u4_a_planted_mistake_fails_the_exhaustive_check():
     assert np.array_equal(bits(got), bits(want))
     assert not np.array_equal(bits(got), bits(high_first))
     assert not np.array_equal(bits(got), bits(negated))
+
+
+# --- the declared subnormal modes ----------------------------------------------
+
+READINGS = [(oracle.PRESERVE, oracle.PRESERVE), (oracle.FLUSH_SIGN_PRESERVING, oracle.PRESERVE),
+            (oracle.PRESERVE, oracle.FLUSH_SIGN_PRESERVING),
+            (oracle.FLUSH_SIGN_PRESERVING, oracle.FLUSH_SIGN_PRESERVING)]
+NODE_OP = {"add": 2, "multiply": 3}
+
+
+def test_f32_sites_under_each_reading():
+    """The evaluator's five occurrences (tests.rs:786-859) as one-node
+    expressions: each reading lands where the reference says."""
+    for case in G["subnormal_modes"]["f32_sites"]["cases"]:
+        l, r = f32([case["left"]]), f32([case["right"]])
+        nodes = [(0, 0, 0), (0, 1, 0), (NODE_OP[case["op"]], 0, 1)]
+        for (im, rm), want in zip(READINGS, case["readings"]):
+            got = oracle.expression_f32(nodes, [l, r], input_mode=im, result_mode=rm)
+            assert int(bits(got)[0]) == hexbits(want), (case["name"], im, rm)
+
+
+def test_split_and_modes_are_answered_independently():
+    for row in G["subnormal_modes"]["f32_split"]["rows"]:
+        x = f32(row["contributors"])
+        for (im, rm), want in zip(READINGS, row["readings"]):
+            part = oracle.strict_partial_sums(x, 1, 4, 2, 2, input_mode=im, result_mode=rm)
+            assert [int(v) for v in bits(part)] == [hexbits(v) for v in want["partials_2x2"]], (row["name"], im, rm)
+            t22 = oracle.strict_partitioned_sum(x, 1, 4, 2, 2, input_mode=im, result_mode=rm)
+            t41 = oracle.strict_partitioned_sum(x, 1, 4, 4, 1, input_mode=im, result_mode=rm)
+            assert int(bits(t22)[0]) == hexbits(want["total_2x2"]), (row["name"], im, rm)
+            assert int(bits(t41)[0]) == hexbits(want["total_4x1"]), (row["name"], im, rm)
+            # a one-contributor partition transports its operand under every reading
+            assert [int(v) for v in bits(oracle.strict_partial_sums(x, 1, 4, 4, 1, input_mode=im, result_mode=rm))] \
+                == [hexbits(v) for v in row["contributors"]]
+
+
+def test_bf16_counterexamples_under_each_reading():
+    """bf16.rs's seven counterexamples, each reading: the input mode replaces
+    operand encodings, the result mode the rounded encoding; under the
+    always-positive flush the negated rows give +0 on both dimensions."""
+    g = G["subnormal_modes"]["bf16_counterexamples"]
+    for case in g["cases"]:
+        l = np.array([hexbits(case["left"])], np.uint16)
+        r = np.array([hexbits(case["right"])], np.uint16)
+        nodes = [(0, 0, 0), (0, 1, 0), (NODE_OP[case["op"]], 0, 1)]
+        for (im, rm), want in zip(READINGS, case["readings"]):
+            got = oracle.expression_bf16(nodes, [l, r], input_mode=im, result_mode=rm)
+            assert int(got[0]) == hexbits(want), (case, im, rm)
+    pos = oracle.FLUSH_POSITIVE_ZERO
+    for left, right in (("0x8040", "0x4000"), ("0x8080", "0x3f00")):
+        got = oracle.expression_bf16([(0, 0, 0), (0, 1, 0), (3, 0, 1)],
+                                     [np.array([hexbits(left)], np.uint16), np.array([hexbits(right)], np.uint16)],
+                                     input_mode=pos, result_mode=pos)
+        assert int(got[0]) == 0x0000, (left, right)
+
+
+def test_fold_under_modes_seeds_at_the_first_contributor():
+    """A lone subnormal contributor is transported (no addition happens), and
+    with a flushing result mode two subnormals summing to a normal keep it
+    (an identity-seeded fold would flush the first one)."""
+    x = f32(["0x00400000"])
+    for im, rm in READINGS:
+        assert int(bits(oracle.strict_sum(x, (1, 1), 1, input_mode=im, result_mode=rm))[0]) == 0x00400000
+    y = f32(["0x00400000", "0x00400000"])
+    got = oracle.strict_sum(y, (1, 2), 1, input_mode=oracle.PRESERVE, result_mode=oracle.FLUSH_SIGN_PRESERVING)
+    assert int(bits(got)[0]) == 0x00800000
+    fold = oracle.fold_f32(y, (1, 2), (1,), input_mode=oracle.PRESERVE, result_mode=oracle.FLUSH_SIGN_PRESERVING)
+    assert int(bits(fold)[0]) == 0x00800000

@@ -29,6 +29,48 @@ __device__ __forceinline__ float canon(float v) {
   return v != v ? __uint_as_float(TILER_CANONICAL_F32_NAN) : v;
 }
 
+// Declared subnormal modes (tiler-reference/src/conformance.rs:498-521),
+// numbered as tiler_hip_region's: 0 and 1 preserve, 2 flush a subnormal to
+// the zero of its own sign, 3 flush it to +0.  Zeros, normals, infinities and
+// NaNs pass unchanged.  A bf16 value widened to binary32 is subnormal exactly
+// when its bf16 encoding is, so the same test serves bf16 encodings
+// (bf16.rs:517-533 accept_operand / commit).
+__device__ __forceinline__ float subnormal(uint32_t mode, float v) {
+  if (mode <= 1u) return v;
+  const uint32_t b = __float_as_uint(v);
+  if ((b & 0x7f800000u) != 0 || (b & 0x007fffffu) == 0) return v;  // not subnormal
+  return mode == 2u ? __uint_as_float(b & 0x80000000u) : 0.0f;
+}
+
+// The per-contributor rule of a serial sum under a declared contract: the
+// prologue (none; the square, SquaredSerialSum; x * scale + bias,
+// FusedMultiplyAddSerialSum, schedule/model.rs:709-760), the two subnormal
+// modes at every arithmetic site, and the combine
+// apply_to_result(canon(apply_to_operand(acc) + apply_to_operand(t)))
+// (evaluate.rs:575-583).  The fold is seeded at the first contributor's value,
+// never at an identity: under a flushing result mode an identity add would
+// flush a lone subnormal contributor the reference transports unchanged.
+enum : uint32_t { kPrologueNone = 0, kPrologueSquared = 1, kPrologueFma = 2 };
+struct FoldRule {
+  uint32_t prologue;
+  float scale, bias;
+  uint32_t in_mode, out_mode;
+};
+__device__ __forceinline__ float fold_contributor(const FoldRule& r, float v) {
+  if (r.prologue == kPrologueSquared) {
+    const float o = subnormal(r.in_mode, v);
+    return canon(subnormal(r.out_mode, o * o));
+  }
+  if (r.prologue == kPrologueFma) {
+    const float p = canon(subnormal(r.out_mode, subnormal(r.in_mode, v) * subnormal(r.in_mode, r.scale)));
+    return canon(subnormal(r.out_mode, subnormal(r.in_mode, p) + subnormal(r.in_mode, r.bias)));
+  }
+  return v;
+}
+__device__ __forceinline__ float fold_combine(const FoldRule& r, float acc, float t) {
+  return canon(subnormal(r.out_mode, subnormal(r.in_mode, acc) + subnormal(r.in_mode, t)));
+}
+
 // bf16 <-> f32 (ADR 0091 decision 2): widening is exact; narrowing is
 // round-to-nearest-even on the upper half, every NaN to 0x7fc0, signed zero
 // kept, gradual underflow, overflow to infinity at the inclusive midpoint.

@@ -62,12 +62,7 @@ typedef float f32x16v __attribute__((ext_vector_type(16)));
 
 // Subnormal modes: 1 preserve (0 reads as 1), 2 flush to the zero of the
 // same sign, 3 flush to +0 (conformance.rs:498-521).
-__device__ __forceinline__ float apply_mode(uint32_t mode, float v) {
-  if (mode <= 1u) return v;
-  const uint32_t b = __float_as_uint(v);
-  if ((b & 0x7f800000u) != 0 || (b & 0x007fffffu) == 0) return v;  // not subnormal
-  return mode == 2u ? __uint_as_float(b & 0x80000000u) : 0.0f;
-}
+__device__ __forceinline__ float apply_mode(uint32_t mode, float v) { return tiler::subnormal(mode, v); }
 
 __device__ __forceinline__ float f32_node(uint32_t op, float x, float y, uint32_t in_mode,
                                           uint32_t out_mode) {
@@ -84,9 +79,16 @@ __device__ __forceinline__ float f32_node(uint32_t op, float x, float y, uint32_
   return tiler::canon(apply_mode(out_mode, r));
 }
 
-__device__ __forceinline__ float bf16_node(uint32_t op, float x, float y) {
+// bf16 under the modes (bf16.rs:517-533): a subnormal operand encoding is
+// replaced before the operation reads it, a subnormal rounded result after
+// its one rounding (a widened bf16 value is subnormal exactly when its
+// encoding is).
+__device__ __forceinline__ float bf16_node(uint32_t op, float x, float y, uint32_t in_mode = 1u,
+                                           uint32_t out_mode = 1u) {
+  x = tiler::subnormal(in_mode, x);
+  y = tiler::subnormal(in_mode, y);
   const float r = op == kAdd ? x + y : x * y;
-  return tiler::bf16_widen(tiler::bf16_narrow(r));
+  return tiler::subnormal(out_mode, tiler::bf16_widen(tiler::bf16_narrow(r)));
 }
 
 // ---------------------------------------------------------------------------
@@ -176,7 +178,7 @@ __device__ __forceinline__ void expr_r16_body(ExprInputs in, void* __restrict__ 
       } else {
 #pragma unroll
         for (int e = 0; e < E; ++e)
-          v[e] = kBf16    ? bf16_node(op, r[e][a], r[e][b])
+          v[e] = kBf16    ? (kModes ? bf16_node(op, r[e][a], r[e][b], in_mode, out_mode) : bf16_node(op, r[e][a], r[e][b]))
                  : kModes ? f32_node(op, r[e][a], r[e][b], in_mode, out_mode)
                           : f32_node(op, r[e][a], r[e][b], 1u, 1u);
       }
@@ -245,7 +247,7 @@ __device__ __forceinline__ void expr_mem_body(ExprInputs in, void* __restrict__ 
         v = kBf16 ? tiler::bf16_widen(imm & 0xffffu) : __uint_as_float(imm);
       } else {
         const float x = store[(uint64_t)a * lanes + lane], z = store[(uint64_t)b * lanes + lane];
-        v = kBf16 ? bf16_node(op, x, z) : f32_node(op, x, z, in_mode, out_mode);
+        v = kBf16 ? bf16_node(op, x, z, in_mode, out_mode) : f32_node(op, x, z, in_mode, out_mode);
       }
       store[(uint64_t)dst * lanes + lane] = v;
     }

@@ -73,7 +73,45 @@ __device__ __forceinline__ void fold_body(const float* __restrict__ x, float* __
   }
 }
 
+// The sums under a FoldRule: its prologue and the declared subnormal modes at
+// every arithmetic site, seeded at the first contributor (the form a flushing
+// contract realizes as; the maximum compares and takes no mode).
+__device__ __forceinline__ void fold_rule_body(const float* __restrict__ x, float* __restrict__ out,
+                                               uint64_t outputs, uint64_t contributors, const FoldGeometry& g,
+                                               const tiler::FoldRule& rule, uint32_t empty_bits) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; id < outputs; id += stride) {
+    uint64_t rem = id, base = 0;
+    for (int d = (int)g.kept_rank - 1; d >= 0; --d) {
+      const uint64_t c = rem % g.dims[d];
+      rem /= g.dims[d];
+      base += c * g.strides[d];
+    }
+    float acc = 0.0f;
+    uint64_t coord[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t off = base;
+    const uint32_t r0 = g.kept_rank, rn = g.kept_rank + g.red_rank;
+    for (uint64_t p = 0; p < contributors; ++p) {
+      const float t = tiler::fold_contributor(rule, x[off]);
+      acc = p == 0 ? t : tiler::fold_combine(rule, acc, t);
+      for (int d = (int)rn - 1; d >= (int)r0; --d) {
+        off += g.strides[d];
+        if (++coord[d] < g.dims[d]) break;
+        off -= g.strides[d] * g.dims[d];
+        coord[d] = 0;
+      }
+    }
+    out[id] = contributors == 0 ? __uint_as_float(empty_bits) : tiler::canon(acc);
+  }
+}
+
 }  // namespace
+
+extern "C" __global__ void __launch_bounds__(256)
+tiler_fold_f32_m(const float* __restrict__ x, float* __restrict__ out, uint64_t outputs, uint64_t contributors,
+                 FoldGeometry g, tiler::FoldRule rule, uint32_t empty_bits) {
+  fold_rule_body(x, out, outputs, contributors, g, rule, empty_bits);
+}
 
 #define TILER_FOLD(NAME, OP)                                                                         \
   extern "C" __global__ void __launch_bounds__(256) NAME(                                            \

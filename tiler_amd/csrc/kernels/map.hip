@@ -52,7 +52,78 @@ __device__ __forceinline__ float map_op_bf16(uint32_t op, float x, float x2, flo
   }
 }
 
+// The same operations under the declared subnormal modes, at every site as
+// evaluate.rs:448-485 `binary` applies them (apply_to_result(canon(op(
+// apply_to_operand(l), apply_to_operand(r))))), and the SiLU as
+// silu.rs:511-533 silu_f32_under.
+__device__ __forceinline__ float map_op_modes(uint32_t op, float x, float x2, float a, float b, uint32_t im,
+                                              uint32_t rm) {
+  using tiler::subnormal;
+  switch (op) {
+    case 0: {
+      const float t = canon(subnormal(rm, subnormal(im, x) * subnormal(im, a)));
+      return canon(subnormal(rm, subnormal(im, t) + subnormal(im, b)));
+    }
+    case 1: {
+      if (x != x) return canon(x);
+      if (x == __builtin_huge_valf()) return x;
+      if (x == -__builtin_huge_valf()) return __uint_as_float(TILER_CANONICAL_F32_NAN);
+      const float v = subnormal(im, x);
+      const float e = subnormal(rm, tiler::exp_f32_cr(subnormal(im, -v)));
+      const float divisor = subnormal(rm, 1.0f + subnormal(im, e));
+      return canon(subnormal(rm, subnormal(im, v) / subnormal(im, divisor)));
+    }
+    case 2:
+      return canon(subnormal(rm, subnormal(im, x) + subnormal(im, x2)));
+    default:
+      return canon(subnormal(rm, subnormal(im, x) * subnormal(im, x2)));
+  }
+}
+
+// bf16 under the modes (bf16.rs:517-533): the input dimension replaces a
+// subnormal operand encoding before it is read, the result dimension a
+// subnormal rounded result; each operation rounds once to bf16.
+__device__ __forceinline__ float bf16_commit(float r, uint32_t rm) {
+  return tiler::subnormal(rm, tiler::bf16_widen(tiler::bf16_narrow(r)));
+}
+__device__ __forceinline__ float map_op_bf16_modes(uint32_t op, float x, float x2, float a, float b, uint32_t im,
+                                                   uint32_t rm) {
+  using tiler::subnormal;
+  switch (op) {
+    case 0: {
+      const float t = bf16_commit(subnormal(im, x) * subnormal(im, a), rm);
+      return bf16_commit(subnormal(im, t) + subnormal(im, b), rm);
+    }
+    case 2:
+      return bf16_commit(subnormal(im, x) + subnormal(im, x2), rm);
+    default:
+      return bf16_commit(subnormal(im, x) * subnormal(im, x2), rm);
+  }
+}
+
 }  // namespace
+
+// Scalar forms under the declared subnormal modes (a flushing contract).
+extern "C" __global__ void __launch_bounds__(256)
+tiler_map_f32_m(const float* __restrict__ x, const float* __restrict__ x2, uint64_t x2_stride, uint64_t n,
+                uint32_t op, float a, float b, float* __restrict__ y, uint32_t in_mode, uint32_t out_mode) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float s2 = x2 ? x2[i * x2_stride] : 0.0f;
+    y[i] = map_op_modes(op, x[i], s2, a, b, in_mode, out_mode);
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+tiler_map_bf16_m(const uint16_t* __restrict__ x, const uint16_t* __restrict__ x2, uint64_t x2_stride, uint64_t n,
+                 uint32_t op, float a, float b, uint16_t* __restrict__ y, uint32_t in_mode, uint32_t out_mode) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float s2 = x2 ? tiler::bf16_widen(x2[i * x2_stride]) : 0.0f;
+    y[i] = (uint16_t)tiler::bf16_narrow(
+        map_op_bf16_modes(op, tiler::bf16_widen(x[i]), s2, a, b, in_mode, out_mode));
+  }
+}
 
 extern "C" __global__ void __launch_bounds__(256)
 tiler_map_f32(const float* __restrict__ x, const float* __restrict__ x2, uint64_t x2_stride,

@@ -56,9 +56,14 @@ tiler_sum_f32_serial(const float* __restrict__ x, uint64_t outer, uint64_t exten
 // kDot: the fold of products instead, out[v] = fold over e of fl(a[e] *
 // x[v*length + e]) -- one output row of the strict contraction, with x the
 // right operand's rows and `a` the left operand's row, staged beside them.
-template <int R, bool kVec, bool kDot>
+//
+// kRule: each element is the FoldRule's contributor (a prologue, the declared
+// subnormal modes) and the fold is seeded at the first one -- the general
+// form a flushing contract or a fused prologue realizes as.
+template <int R, bool kVec, bool kDot, bool kRule = false>
 __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
-                                                 const float* __restrict__ a, float* __restrict__ out) {
+                                                 const float* __restrict__ a, float* __restrict__ out,
+                                                 tiler::FoldRule rule = tiler::FoldRule{}) {
   constexpr uint32_t C = 4096 / R;               // elements of a row per stage
   constexpr uint32_t kStride = C + 4;            // LDS row stride in floats (16-byte aligned, staggered banks)
   constexpr uint32_t W = kVec ? 4 : 1;           // elements per load
@@ -113,6 +118,16 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
   const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
   const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < nrows;
   float acc = -0.0f;
+  bool seeded = false;  // kRule: the fold starts at its first contributor
+  auto add1 = [&](float v) {
+    if constexpr (kRule) {
+      const float t = tiler::fold_contributor(rule, v);
+      acc = seeded ? tiler::fold_combine(rule, acc, t) : t;
+      seeded = true;
+    } else {
+      acc = acc + v;
+    }
+  };
   if (stages > 0) {
     load(0);
     store(0);
@@ -147,10 +162,10 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
           acc = acc + w.z * v.z;
           acc = acc + w.w * v.w;
         } else {
-          acc = acc + v.x;
-          acc = acc + v.y;
-          acc = acc + v.z;
-          acc = acc + v.w;
+          add1(v.x);
+          add1(v.y);
+          add1(v.z);
+          add1(v.w);
         }
       };
       if (count == C) {
@@ -189,7 +204,7 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
         for (; c + 4 <= count; c += 4) step4(*reinterpret_cast<const f32x4*>(row + c), c);
         for (; c < count; ++c) {
           if constexpr (kDot) acc = acc + arow[c] * row[c];
-          else acc = acc + row[c];
+          else add1(row[c]);
         }
       }
     }
@@ -216,6 +231,25 @@ TILER_SUM_STAGED(16)
 TILER_SUM_STAGED(64)
 TILER_SUM_STAGED(256)  // rows of 16..63: stages of 16 elements, every lane folding a row
 
+// The same stages under a FoldRule: a flushing contract's serial fold, and the
+// fused prologues (squared, scale-bias) over a trailing axis.
+#define TILER_SUM_STAGED_RULE(R)                                                                       \
+  extern "C" __global__ void __launch_bounds__(256)                                                    \
+      tiler_sum_f32_staged_r##R##_m(const float* __restrict__ x, uint64_t nrows, uint64_t length,      \
+                                    float* __restrict__ out, tiler::FoldRule rule) {                   \
+    staged_fold_body<R, true, false, true>(x, nrows, length, nullptr, out, rule);                      \
+  }                                                                                                    \
+  extern "C" __global__ void __launch_bounds__(256)                                                    \
+      tiler_sum_f32_staged_r##R##_u_m(const float* __restrict__ x, uint64_t nrows, uint64_t length,    \
+                                      float* __restrict__ out, tiler::FoldRule rule) {                 \
+    staged_fold_body<R, false, false, true>(x, nrows, length, nullptr, out, rule);                     \
+  }
+TILER_SUM_STAGED_RULE(1)
+TILER_SUM_STAGED_RULE(4)
+TILER_SUM_STAGED_RULE(16)
+TILER_SUM_STAGED_RULE(64)
+TILER_SUM_STAGED_RULE(256)
+
 // MultiPass pass 1: partials[r*P + p] = strict fold of
 // x[r*extent + p*chunk .. +chunk]; an empty partition commits +0.0.
 extern "C" __global__ void __launch_bounds__(256)
@@ -227,6 +261,24 @@ tiler_sum_f32_partials(const float* __restrict__ x, uint64_t rows, uint64_t exte
   const float* base = x + r * extent + p * chunk;
   float acc = -0.0f;
   for (uint64_t w = 0; w < chunk; ++w) acc = acc + base[w];
+  partials[id] = chunk == 0 ? 0.0f : canon(acc);
+}
+
+// The same under a FoldRule (evaluate.rs:612-776 strict_partial_sums_under):
+// each partition seeded at its first contributor, so a one-contributor
+// partition transports its value unchanged under every mode.
+extern "C" __global__ void __launch_bounds__(256)
+tiler_sum_f32_partials_m(const float* __restrict__ x, uint64_t rows, uint64_t extent, uint64_t partitions,
+                         uint64_t chunk, float* __restrict__ partials, tiler::FoldRule rule) {
+  uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= rows * partitions) return;
+  uint64_t r = id / partitions, p = id - r * partitions;
+  const float* base = x + r * extent + p * chunk;
+  float acc = 0.0f;
+  for (uint64_t w = 0; w < chunk; ++w) {
+    const float t = tiler::fold_contributor(rule, base[w]);
+    acc = w == 0 ? t : tiler::fold_combine(rule, acc, t);
+  }
   partials[id] = chunk == 0 ? 0.0f : canon(acc);
 }
 
@@ -254,6 +306,34 @@ tiler_sum_f32_cooperative(const float* __restrict__ x, uint64_t extent, uint32_t
       float s = -0.0f;
       for (uint32_t q = 0; q < participants; ++q) s = s + staged[q];
       total = total + s;
+    }
+    __syncthreads();
+  }
+  if (p == 0) out[blockIdx.x] = canon(total);
+}
+
+// The same under a FoldRule (evaluate.rs:845-1158 cooperative_grouped_sum_under):
+// every cell, the staged partials and the round totals seeded at their first
+// value.
+extern "C" __global__ void __launch_bounds__(1024)
+tiler_sum_f32_cooperative_m(const float* __restrict__ x, uint64_t extent, uint32_t participants,
+                            uint64_t chunk, uint64_t rounds, uint32_t participant_major,
+                            float* __restrict__ out, tiler::FoldRule rule) {
+  __shared__ float staged[1024];
+  const uint32_t p = threadIdx.x;
+  const float* row = x + (uint64_t)blockIdx.x * extent;
+  float total = 0.0f;
+  for (uint64_t r = 0; r < rounds; ++r) {
+    uint64_t cell = participant_major ? (uint64_t)p * rounds + r : r * participants + p;
+    const float* range = row + cell * chunk;
+    float partial = tiler::fold_contributor(rule, range[0]);
+    for (uint64_t w = 1; w < chunk; ++w) partial = tiler::fold_combine(rule, partial, tiler::fold_contributor(rule, range[w]));
+    staged[p] = partial;
+    __syncthreads();
+    if (p == 0) {
+      float s = staged[0];
+      for (uint32_t q = 1; q < participants; ++q) s = tiler::fold_combine(rule, s, staged[q]);
+      total = r == 0 ? s : tiler::fold_combine(rule, total, s);
     }
     __syncthreads();
   }

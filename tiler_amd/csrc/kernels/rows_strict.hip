@@ -55,10 +55,27 @@ __device__ __forceinline__ float fold_segment(const float* seg, uint32_t len, fl
   return acc;
 }
 
+// The same fold with the declared subnormal modes at each combine:
+// apply_to_result(apply_to_operand(acc) + apply_to_operand(c)).
+__device__ __forceinline__ float fold_segment_modes(const float* seg, uint32_t len, float acc, bool& seeded,
+                                                    uint32_t im, uint32_t rm) {
+  for (uint32_t i = 0; i < len; ++i) {
+    acc = seeded ? tiler::subnormal(rm, tiler::subnormal(im, acc) + tiler::subnormal(im, seg[i])) : seg[i];
+    seeded = true;
+  }
+  return acc;
+}
+
+// in_mode / out_mode: the declared subnormal modes (tiler::subnormal), applied
+// at every arithmetic site as rms_norm.rs:405-489 and softmax.rs:200-315 apply
+// them under a conformance (operands flushed before, results after); 1 and 1
+// preserve, which is the strict reading.
 template <bool kBf16>
 __device__ __forceinline__ void rms_strict_body(const void* __restrict__ x, const void* __restrict__ w,
                                                 uint64_t w_row_stride, void* __restrict__ y, uint64_t rows,
-                                                uint32_t extent, float eps) {
+                                                uint32_t extent, float eps, uint32_t im, uint32_t rm) {
+  using tiler::subnormal;
+  const bool modes = im > 1u || rm > 1u;
   __shared__ __attribute__((aligned(16))) float seg[kStrictWaves][kStrictSeg];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint64_t row = (uint64_t)blockIdx.x * kStrictWaves + wave;
@@ -69,30 +86,39 @@ __device__ __forceinline__ void rms_strict_body(const void* __restrict__ x, cons
   for (uint32_t s0 = 0; s0 < extent; s0 += kStrictSeg) {
     const uint32_t len = extent - s0 < kStrictSeg ? extent - s0 : kStrictSeg;
     for (uint32_t i = lane; i < len; i += 64) {
-      const float v = load_elem<kBf16>(x, base + s0 + i);
-      seg[wave][i] = v * v;
+      const float v = subnormal(im, load_elem<kBf16>(x, base + s0 + i));
+      seg[wave][i] = subnormal(rm, v * v);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes landed
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0) acc = fold_segment(seg[wave], len, acc, seeded);
+    if (lane == 0)
+      acc = modes ? fold_segment_modes(seg[wave], len, acc, seeded, im, rm) : fold_segment(seg[wave], len, acc, seeded);
     __builtin_amdgcn_wave_barrier();
   }
   // rms_norm.rs:177-187: a division by N, then + eps, then the certified rsqrt.
   float s = 0.0f;
   if (lane == 0) {
-    const float mean = acc / (float)extent;
-    s = tiler::rsqrt_f32_cr(mean + eps);
+    const float mean = subnormal(rm, subnormal(im, acc) / subnormal(im, (float)extent));
+    s = subnormal(rm, tiler::rsqrt_f32_cr(subnormal(im, subnormal(rm, subnormal(im, mean) + subnormal(im, eps)))));
   }
   s = __shfl(s, 0, 64);
   const uint64_t wbase = row * w_row_stride;
   for (uint32_t i = lane; i < extent; i += 64) {
-    const float normalized = load_elem<kBf16>(x, base + i) * s;
-    store_elem<kBf16>(y, base + i, tiler::canon(load_elem<kBf16>(w, wbase + i) * normalized));
+    const float normalized = subnormal(rm, subnormal(im, load_elem<kBf16>(x, base + i)) * subnormal(im, s));
+    store_elem<kBf16>(y, base + i,
+                      tiler::canon(subnormal(rm, subnormal(im, load_elem<kBf16>(w, wbase + i)) * subnormal(im, normalized))));
   }
 }
 
 __device__ __forceinline__ void softmax_strict_body(const float* __restrict__ x, float* __restrict__ y,
-                                                    uint64_t rows, uint32_t extent) {
+                                                    uint64_t rows, uint32_t extent, uint32_t im, uint32_t rm) {
+  using tiler::subnormal;
+  const bool modes = im > 1u || rm > 1u;
+  // e_i = apply_to_result(exp(apply_to_operand(fl(x_i - m) under the modes)))
+  auto expo = [&](float v, float m) {
+    const float shifted = subnormal(rm, subnormal(im, v) - subnormal(im, m));
+    return subnormal(rm, tiler::exp_f32_cr(subnormal(im, shifted)));
+  };
   __shared__ __attribute__((aligned(16))) float seg[kStrictWaves][kStrictSeg];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint64_t row = (uint64_t)blockIdx.x * kStrictWaves + wave;
@@ -106,16 +132,18 @@ __device__ __forceinline__ void softmax_strict_body(const float* __restrict__ x,
   bool seeded = false;
   for (uint32_t s0 = 0; s0 < extent; s0 += kStrictSeg) {
     const uint32_t len = extent - s0 < kStrictSeg ? extent - s0 : kStrictSeg;
-    for (uint32_t i = lane; i < len; i += 64) seg[wave][i] = tiler::exp_f32_cr(xr[s0 + i] - m);
+    for (uint32_t i = lane; i < len; i += 64) seg[wave][i] = expo(xr[s0 + i], m);
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0) d = fold_segment(seg[wave], len, d, seeded);
+    if (lane == 0)
+      d = modes ? fold_segment_modes(seg[wave], len, d, seeded, im, rm) : fold_segment(seg[wave], len, d, seeded);
     __builtin_amdgcn_wave_barrier();
   }
   float r = 0.0f;
-  if (lane == 0) r = 1.0f / d;  // softmax.rs:302-313: the reciprocal, then a multiply
+  if (lane == 0) r = subnormal(rm, 1.0f / subnormal(im, d));  // softmax.rs:302-313: the reciprocal, then a multiply
   r = __shfl(r, 0, 64);
-  for (uint32_t i = lane; i < extent; i += 64) yr[i] = tiler::canon(tiler::exp_f32_cr(xr[i] - m) * r);
+  for (uint32_t i = lane; i < extent; i += 64)
+    yr[i] = tiler::canon(subnormal(rm, subnormal(im, expo(xr[i], m)) * subnormal(im, r)));
 }
 
 // Strict RMSNorm over many rows, staged like the strict serial sum
@@ -492,16 +520,18 @@ TILER_RMS_STRICT_STAGED(bf16, uint16_t, 64)
 
 extern "C" __global__ void __launch_bounds__(256)
 tiler_rms_norm_f32_strict(const float* __restrict__ x, const float* __restrict__ w, uint64_t w_row_stride,
-                          float* __restrict__ y, uint64_t rows, uint32_t extent, float eps) {
-  rms_strict_body<false>(x, w, w_row_stride, y, rows, extent, eps);
+                          float* __restrict__ y, uint64_t rows, uint32_t extent, float eps, uint32_t in_mode,
+                          uint32_t out_mode) {
+  rms_strict_body<false>(x, w, w_row_stride, y, rows, extent, eps, in_mode, out_mode);
 }
 extern "C" __global__ void __launch_bounds__(256)
 tiler_rms_norm_bf16_strict(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                            uint64_t w_row_stride, uint16_t* __restrict__ y, uint64_t rows, uint32_t extent,
-                           float eps) {
-  rms_strict_body<true>(x, w, w_row_stride, y, rows, extent, eps);
+                           float eps, uint32_t in_mode, uint32_t out_mode) {
+  rms_strict_body<true>(x, w, w_row_stride, y, rows, extent, eps, in_mode, out_mode);
 }
 extern "C" __global__ void __launch_bounds__(256)
-tiler_softmax_f32_strict(const float* __restrict__ x, float* __restrict__ y, uint64_t rows, uint32_t extent) {
-  softmax_strict_body(x, y, rows, extent);
+tiler_softmax_f32_strict(const float* __restrict__ x, float* __restrict__ y, uint64_t rows, uint32_t extent,
+                         uint32_t in_mode, uint32_t out_mode) {
+  softmax_strict_body(x, y, rows, extent, in_mode, out_mode);
 }

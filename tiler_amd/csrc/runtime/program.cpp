@@ -147,8 +147,40 @@ uint32_t tree_workgroups(const Target& t, uint64_t n) {
 // folding chains of few long rows get a SIMD each; rows of 16..63 in stages
 // of 16, 256 rows per workgroup; shorter rows take one lane per row, whose
 // loads are already near one another.
+// The rule-driven forms (a flushing contract, a fused prologue): the same
+// stages with the rule's contributor and combine, seeded at the first
+// contributor; rows under 16 take one lane per row (the general fold over the
+// trailing axis of [nrows, length]).
+static void add_rule_fold(const Target& t, uint32_t src, bool src_aligned, uint64_t nrows, uint64_t length,
+                          uint32_t dst, const FoldRuleHost& rule, Program& p) {
+  const bool vec = src_aligned && length % 4 == 0;
+  char name[48];
+  if (length >= 16) {
+    const uint64_t cus = t.compute_units;
+    const uint32_t R = length < 64 ? 256 : nrows <= cus ? 1 : nrows <= 4 * cus ? 4 : nrows <= 16 * cus ? 16 : 64;
+    std::snprintf(name, sizeof(name), "tiler_sum_f32_staged_r%u%s_m", R, vec ? "" : "_u");
+    p.add(name, (uint32_t)((nrows + R - 1) / R), 1, 256)
+        .ptr(src).u64(nrows).u64(length).ptr(dst).blob(&rule, sizeof(rule), 4);
+    return;
+  }
+  FoldGeometryHost g;
+  std::memset(&g, 0, sizeof(g));
+  g.dims[0] = nrows;
+  g.strides[0] = length;
+  g.dims[1] = length;
+  g.strides[1] = 1;
+  g.kept_rank = 1;
+  g.red_rank = 1;
+  p.add("tiler_fold_f32_m", blocks_capped(nrows, 65536), 1, 256)
+      .ptr(src).ptr(dst).u64(nrows).u64(length).blob(&g, sizeof(g), 8).blob(&rule, sizeof(rule), 4).u32(0);
+}
+
 static void add_serial_fold(const Target& t, uint32_t src, bool src_aligned, uint64_t nrows, uint64_t length,
-                            uint32_t dst, Program& p) {
+                            uint32_t dst, Program& p, const FoldRuleHost* rule = nullptr) {
+  if (rule) {
+    add_rule_fold(t, src, src_aligned, nrows, length, dst, *rule, p);
+    return;
+  }
   if (length >= 64) {
     const uint64_t cus = t.compute_units;
     const uint32_t R = nrows <= cus ? 1 : nrows <= 4 * cus ? 4 : nrows <= 16 * cus ? 16 : 64;
@@ -169,15 +201,23 @@ static void add_serial_fold(const Target& t, uint32_t src, bool src_aligned, uin
 }
 
 tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
-                              const tiler_hip_sum_plan& sp, const uintptr_t* addr, Program& p) {
+                              const tiler_hip_sum_plan& sp, const uintptr_t* addr, Program& p,
+                              const FoldRuleHost* rule) {
   const uint32_t x = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotInput);
   const uint32_t out = p.slot(mul_sat(rows, 4), kSlotOutput);
+  // The partials' fold takes the modes but not the prologue: it sums values
+  // the first pass already produced (evaluate.rs:788-832).
+  FoldRuleHost second;
+  if (rule) {
+    second = *rule;
+    second.prologue = 0;
+  }
   switch (sp.topology) {
     case TILER_HIP_SUM_SERIAL:
       if (rows == 0) return TILER_HIP_OK;
       if ((rows + 255) / 256 > 0x7fffffffull || (extent >= 16 && rows > 0x7fffffffull))
         return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-      add_serial_fold(t, x, aligned16(addr[x]), rows, extent, out, p);
+      add_serial_fold(t, x, aligned16(addr[x]), rows, extent, out, p, rule);
       return TILER_HIP_OK;
     case TILER_HIP_SUM_MULTIPASS: {
       const uint64_t P = sp.partitions, c = sp.per_partition;
@@ -190,12 +230,15 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
       // With exact coverage partition p of row r is the contiguous run
       // (r*P + p) * c: pass 1 is the serial fold of rows*P rows of c.
       if (c >= 16)
-        add_serial_fold(t, x, aligned16(addr[x]), rows * P, c, part, p);
+        add_serial_fold(t, x, aligned16(addr[x]), rows * P, c, part, p, rule);
+      else if (rule)
+        p.add("tiler_sum_f32_partials_m", (uint32_t)((rows * P + 255) / 256), 1, 256)
+            .ptr(x).u64(rows).u64(extent).u64(P).u64(c).ptr(part).blob(rule, sizeof(*rule), 4);
       else
         p.add("tiler_sum_f32_partials", (uint32_t)((rows * P + 255) / 256), 1, 256)
             .ptr(x).u64(rows).u64(extent).u64(P).u64(c).ptr(part);
       // the partials are the planner's own scratch, 16-byte aligned
-      add_serial_fold(t, part, true, rows, P, out, p);
+      add_serial_fold(t, part, true, rows, P, out, p, rule ? &second : nullptr);
       return TILER_HIP_OK;
     }
     case TILER_HIP_SUM_COOPERATIVE: {
@@ -204,11 +247,21 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
       if (P == 0 || P > 1024 || c == 0 || R == 0 || P * c * R != extent)
         return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "grouping does not cover the axis exactly");
       if (rows > 0x7fffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-      p.add("tiler_sum_f32_cooperative", (uint32_t)rows, 1, (uint32_t)P)
-          .ptr(x).u64(extent).u32((uint32_t)P).u64(c).u64(R).u32(sp.participant_major ? 1u : 0u).ptr(out);
+      Launch& l = p.add(rule ? "tiler_sum_f32_cooperative_m" : "tiler_sum_f32_cooperative", (uint32_t)rows, 1, (uint32_t)P)
+                      .ptr(x).u64(extent).u32((uint32_t)P).u64(c).u64(R).u32(sp.participant_major ? 1u : 0u).ptr(out);
+      if (rule) l.blob(rule, sizeof(*rule), 4);
       return TILER_HIP_OK;
     }
     case TILER_HIP_SUM_TREE: {
+      // The tree's lanes start from the additive identity, which a flushing
+      // result mode would make observable (a lone subnormal partial flushed
+      // by an add the reference never performs), and its kernels take no
+      // prologue: the reference's own groupings (the split, the cooperative
+      // workgroup) realize those.
+      if (rule)
+        return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                        "the two-level tree realizes neither a flushing contract nor a fused prologue; the multi-pass "
+                        "split and the cooperative workgroup do");
       if (rows == 0) return TILER_HIP_OK;
       if (rows == 1) {
         const uint32_t G = tree_workgroups(t, extent);
@@ -237,7 +290,11 @@ tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
 // RMS normalization.  Slots: 0 x, 1 w, 2 y.
 tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
-                               Program& p, bool strict) {
+                               Program& p, bool strict, uint32_t in_mode, uint32_t out_mode) {
+  // A flushing contract: the serial fold with the modes at every site (the
+  // one-wave-per-row strict kernel, which takes them), whatever the topology.
+  const bool modes = in_mode > 1 || out_mode > 1;
+  if (modes) strict = true;
   float eps;
   std::memcpy(&eps, &eps_bits, 4);
   // rms_norm.rs:462-466: a non-positive or non-finite eps refuses.
@@ -258,7 +315,7 @@ tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_b
   const bool al = aligned16(addr[x]) && aligned16(addr[w]) && aligned16(addr[y]) && (extent * elem) % 16 == 0;
   const uint64_t wstride = weight_broadcast ? 0 : extent;
   char name[64];
-  if (strict && extent >= 64) {
+  if (strict && extent >= 64 && !modes) {
     // The reference's serial fold of the squares, staged: R rows per
     // workgroup, the largest of 64, 16, 4 that still gives every CU a
     // workgroup (else 1), a folding lane per row.
@@ -276,7 +333,7 @@ tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_b
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
     std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict", ty);
     p.add(name, (uint32_t)((rows + 3) / 4), 1, 256)
-        .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps);
+        .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps).u32(in_mode).u32(out_mode);
     return TILER_HIP_OK;
   }
   if (extent > kWaveRowMax) {  // one workgroup per row
@@ -314,9 +371,16 @@ tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_b
 //   valid between calls; a realized plan's scratch is fresh, so its program
 //   zeroes the area with a fill kernel first.
 tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
-                                  const uintptr_t* addr, Program& p, bool strict, uint32_t form) {
+                                  const uintptr_t* addr, Program& p, bool strict, uint32_t form,
+                                  uint32_t in_mode, uint32_t out_mode) {
   const uint32_t x = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotInput);
   const uint32_t y = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotOutput);
+  // A flushing contract: the serial exponent sum with the modes at every site
+  // (the one-wave-per-row strict kernel, which takes them).
+  const bool modes = in_mode > 1 || out_mode > 1;
+  if (modes && form != TILER_HIP_FORM_AUTO)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "form: a flushing contract has the serial form only");
+  if (modes) strict = true;
   if (form != TILER_HIP_FORM_AUTO) {
     if (strict || (form != TILER_HIP_FORM_SOFTMAX_SPLIT && form != TILER_HIP_FORM_SOFTMAX_ROW_SYNC))
       return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "form: not a form of this softmax");
@@ -327,7 +391,7 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
   if (rows == 0 || extent == 0) return TILER_HIP_OK;
   if (extent > 0xffffffffull)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
-  if (strict && extent >= 64 && extent <= 0xffffffffull) {
+  if (strict && extent >= 64 && extent <= 0xffffffffull && !modes) {
     // The reference's serial exponent sum, staged: R rows per workgroup as
     // for the strict RMSNorm but at most 16 (stages of at least 256
     // elements, so a stage's fold covers the next stage's loads; 64 rows of
@@ -348,7 +412,7 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
     if ((rows + 3) / 4 > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
     p.add("tiler_softmax_f32_strict", (uint32_t)((rows + 3) / 4), 1, 256)
-        .ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
+        .ptr(x).ptr(y).u64(rows).u32((uint32_t)extent).u32(in_mode).u32(out_mode);
     return TILER_HIP_OK;
   }
   const bool al = aligned16(addr[x]) && aligned16(addr[y]) && extent % 4 == 0;
@@ -405,7 +469,8 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
 // rest.  Realized (no slot offsets): the vector kernel when it covers all n,
 // the scalar kernel otherwise; both compute each element identically.
 tiler_hip_status plan_map(Mode mode, uint32_t op, uint32_t dtype, int32_t x2_broadcast,
-                          uint64_t n, float a, float b, const uintptr_t* addr, Program& p) {
+                          uint64_t n, float a, float b, const uintptr_t* addr, Program& p,
+                          uint32_t in_mode, uint32_t out_mode) {
   if (op > TILER_HIP_MAP_MULTIPLY) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "map op");
   if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16)
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "map dtype");
@@ -417,6 +482,14 @@ tiler_hip_status plan_map(Mode mode, uint32_t op, uint32_t dtype, int32_t x2_bro
   const uint32_t x2 = binary ? p.slot(x2_broadcast ? eb : mul_sat(n, eb), kSlotInput) : UINT32_MAX;
   const uint32_t y = p.slot(mul_sat(n, eb), kSlotOutput);
   if (n == 0) return TILER_HIP_OK;
+  if (in_mode > 1 || out_mode > 1) {  // a flushing contract: the scalar form with the modes
+    Launch& l = p.add(dtype == TILER_HIP_BF16 ? "tiler_map_bf16_m" : "tiler_map_f32_m", blocks_capped(n, 8192), 1, 256)
+                    .ptr(x);
+    if (binary) l.ptr(x2);
+    else l.null_ptr();
+    l.u64(x2_broadcast ? 0 : 1).u64(n).u32(op).f32(a).f32(b).ptr(y).u32(in_mode).u32(out_mode);
+    return TILER_HIP_OK;
+  }
   const uint64_t per = dtype == TILER_HIP_BF16 ? 8 : 4;  // elements per 16-byte chunk
   const bool vec_ok = aligned16(addr[x]) && aligned16(addr[y]) && (!binary || x2_broadcast || aligned16(addr[x2]));
   uint64_t head = vec_ok ? n / per * per : 0;  // elements the vector kernel covers
@@ -1109,8 +1182,6 @@ tiler_hip_status plan_expression(const Target& t, uint32_t dtype, uint64_t n, co
                                  const Contract& c, const uintptr_t* addr, Program& p) {
   (void)t;
   if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16) return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "expression dtype");
-  if (dtype == TILER_HIP_BF16 && c.flushes())
-    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "a flushing subnormal mode is realized for f32 expressions only");
   const uint64_t eb = dtype == TILER_HIP_BF16 ? 2 : 4;
   uint32_t in_slots[kMaxExpressionInputs];
   for (uint32_t k = 0; k < prog.inputs; ++k) in_slots[k] = p.slot(mul_sat(n, eb), kSlotInput);
@@ -1127,9 +1198,12 @@ tiler_hip_status plan_expression(const Target& t, uint32_t dtype, uint64_t n, co
     bool vec = n % per == 0 && aligned16(addr[prog.inputs]);
     for (uint32_t k = 0; k < prog.inputs; ++k) vec = vec && aligned16(addr[k]);
     const uint32_t nin = prog.inputs <= 4 ? prog.inputs : 0;
-    const uint64_t work = vec ? n / per : n;
-    // the vector f32 form has a copy with the mode code compiled out
+    // the vector f32 form has a copy with the mode code compiled out; bf16
+    // under a flushing contract takes the one-element form, which applies
+    // the modes
+    if (dtype == TILER_HIP_BF16 && c.flushes()) vec = false;
     const char* form = !vec ? "s" : (dtype == TILER_HIP_F32 && c.flushes()) ? "f" : "";
+    const uint64_t work = vec ? n / per : n;
     std::snprintf(name, sizeof(name), "tiler_expr_%s_r16%s_i%u", ty, form, nin);
     p.add(name, blocks_capped(work, 8192), 1, 256)
         .ptr_table(in_slots, prog.inputs, kMaxExpressionInputs)
@@ -1156,12 +1230,67 @@ tiler_hip_status plan_expression(const Target& t, uint32_t dtype, uint64_t n, co
 // Serial folds over any reduced-axis set.  Slots: x, out, [epilogue program].
 tiler_hip_status plan_fold(uint32_t op, uint32_t rank, const uint64_t* dims, uint64_t reduced_mask,
                            uint32_t scale_bits, uint32_t bias_bits, const ExpressionProgram* epilogue,
-                           Program& p) {
+                           Program& p, const Contract& c, const Target* t, const tiler_hip_sum_plan* sp,
+                           const uintptr_t* addr) {
   if (op > TILER_HIP_FOLD_MAXIMUM) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "fold variant");
   if (rank > 8 || (rank && !dims)) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "fold rank");
   if (reduced_mask >> rank) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "reduced axis beyond the rank");
   if (epilogue && op == TILER_HIP_FOLD_MAXIMUM)
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the maximum fold carries no epilogue");
+  const uint32_t topology = sp ? sp->topology : TILER_HIP_SUM_SERIAL;
+  // The maximum compares and is under no subnormal mode (softmax.rs:168-186);
+  // its one realization is the serial fold.
+  if (op == TILER_HIP_FOLD_MAXIMUM && topology != TILER_HIP_SUM_SERIAL)
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "the maximum fold has one realization, the serial fold");
+  const bool sums = op != TILER_HIP_FOLD_MAXIMUM;
+  if (epilogue && (c.flushes() || topology != TILER_HIP_SUM_SERIAL))
+    return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
+                    "a fold's epilogue is realized serially and under the preserving modes only");
+  // A sum over the trailing axis under a flushing contract, or split by a
+  // reassociating topology: the rule-driven sums (the prologue and the modes
+  // in every combine), over the [rows, extent] view of the dense input.
+  const bool trailing = rank >= 1 && reduced_mask == (1ull << (rank - 1));
+  if (sums && !epilogue && (c.flushes() || topology != TILER_HIP_SUM_SERIAL)) {
+    FoldRuleHost rule;
+    rule.prologue = op == TILER_HIP_FOLD_SQUARED ? 1u : op == TILER_HIP_FOLD_FMA ? 2u : 0u;
+    std::memcpy(&rule.scale, &scale_bits, 4);
+    std::memcpy(&rule.bias, &bias_bits, 4);
+    rule.in_mode = c.input_mode;
+    rule.out_mode = c.result_mode;
+    if (trailing && t && sp && addr) {
+      uint64_t rows = 1;
+      for (uint32_t d = 0; d + 1 < rank; ++d) rows = mul_sat(rows, dims[d]);
+      return plan_sum_f32(*t, rows, dims[rank - 1], *sp, addr, p, &rule);
+    }
+    if (topology != TILER_HIP_SUM_SERIAL)
+      return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "a split or workgroup fold reduces the trailing axis only");
+    FoldGeometryHost g;
+    std::memset(&g, 0, sizeof(g));
+    uint64_t stride[8], total = 1, outputs = 1, contributors = 1;
+    for (int d = (int)rank - 1; d >= 0; --d) {
+      stride[d] = total;
+      total = mul_sat(total, dims[d]);
+    }
+    for (uint32_t d = 0; d < rank; ++d)
+      if (!(reduced_mask >> d & 1)) {
+        g.dims[g.kept_rank] = dims[d];
+        g.strides[g.kept_rank++] = stride[d];
+        outputs = mul_sat(outputs, dims[d]);
+      }
+    for (uint32_t d = 0; d < rank; ++d)
+      if (reduced_mask >> d & 1) {
+        g.dims[g.kept_rank + g.red_rank] = dims[d];
+        g.strides[g.kept_rank + g.red_rank++] = stride[d];
+        contributors = mul_sat(contributors, dims[d]);
+      }
+    const uint32_t x = p.slot(mul_sat(total, 4), kSlotInput);
+    const uint32_t out = p.slot(mul_sat(outputs, 4), kSlotOutput);
+    if (outputs == 0) return TILER_HIP_OK;
+    if (total == UINT64_MAX) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "fold extents overflow");
+    p.add("tiler_fold_f32_m", blocks_capped(outputs, 65536), 1, 256)
+        .ptr(x).ptr(out).u64(outputs).u64(contributors).blob(&g, sizeof(g), 8).blob(&rule, sizeof(rule), 4).u32(0);
+    return TILER_HIP_OK;
+  }
   // The fold kernel evaluates its epilogue in a 16-register file.
   if (epilogue && epilogue->registers > kExpressionRegisters)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "epilogue needs more than 16 live values");

@@ -132,6 +132,14 @@ struct Contract {
   bool flushes() const { return input_mode > 1 || result_mode > 1; }
 };
 
+// Host mirror of the kernels' tiler::FoldRule (common.h): a serial sum's
+// per-contributor prologue and the two subnormal modes at every site.
+struct FoldRuleHost {
+  uint32_t prologue = 0;  // 0 none, 1 squared, 2 scale-bias
+  float scale = 1.0f, bias = 0.0f;
+  uint32_t in_mode = 1, out_mode = 1;
+};
+
 // A pointwise expression compiled for the interpreter kernels (expr.hip):
 // instructions in execution order (the inputs first, input k into register
 // k), the result register, and the register count the program needs.
@@ -158,18 +166,23 @@ uint32_t tree_workgroups(const Target& t, uint64_t n);
 // Planners.  Slot order is part of each contract (tiler_hip_realize documents
 // it); `addr` holds each slot's base address, or a stand-in whose low bits
 // carry the alignment a realization may assume.
+// rule (NULL: the plain strict fold under the preserving modes) selects the
+// rule-driven kernels: a flushing contract, or a fused prologue.
 tiler_hip_status plan_sum_f32(const Target& t, uint64_t rows, uint64_t extent,
-                              const tiler_hip_sum_plan& sp, const uintptr_t* addr, Program& p);
+                              const tiler_hip_sum_plan& sp, const uintptr_t* addr, Program& p,
+                              const FoldRuleHost* rule = nullptr);
 tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_broadcast, uint64_t rows,
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
-                               Program& p, bool strict = false);
+                               Program& p, bool strict = false, uint32_t in_mode = 1, uint32_t out_mode = 1);
 // `form` (TILER_HIP_FORM_SOFTMAX_*) forces the split or the row-synchronized
 // launch for rows of more than four segments.
 tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uint64_t extent,
                                   const uintptr_t* addr, Program& p, bool strict = false,
-                                  uint32_t form = TILER_HIP_FORM_AUTO);
+                                  uint32_t form = TILER_HIP_FORM_AUTO, uint32_t in_mode = 1,
+                                  uint32_t out_mode = 1);
 tiler_hip_status plan_map(Mode mode, uint32_t op, uint32_t dtype, int32_t x2_broadcast,
-                          uint64_t n, float a, float b, const uintptr_t* addr, Program& p);
+                          uint64_t n, float a, float b, const uintptr_t* addr, Program& p,
+                          uint32_t in_mode = 1, uint32_t out_mode = 1);
 tiler_hip_status plan_broadcast(uint64_t src_elements, uint32_t rank, const uint64_t* out_dims,
                                 const uint64_t* src_strides, uint32_t element_bytes,
                                 Program& p);
@@ -204,7 +217,8 @@ tiler_hip_status plan_expression(const Target& t, uint32_t dtype, uint64_t n, co
 // Slots: x, out, and the epilogue's program (CONSTANT) when one is given.
 tiler_hip_status plan_fold(uint32_t op, uint32_t rank, const uint64_t* dims, uint64_t reduced_mask,
                            uint32_t scale_bits, uint32_t bias_bits, const ExpressionProgram* epilogue,
-                           Program& p);
+                           Program& p, const Contract& c = Contract{}, const Target* t = nullptr,
+                           const tiler_hip_sum_plan* sp = nullptr, const uintptr_t* addr = nullptr);
 // Reindex with signed strides: out (row-major over out_dims) reads source
 // offset base + sum coord_d * strides[d].  Slots: src, out.
 tiler_hip_status plan_reindex(uint64_t src_elements, uint32_t rank, const uint64_t* out_dims,

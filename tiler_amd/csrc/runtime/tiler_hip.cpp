@@ -57,6 +57,22 @@ const EntryRow kEntries[] = {
     {"tiler_sum_f32_staged_r256_u", "strict-serial-sum-f32/serial", 2},
     {"tiler_sum_f32_partials", "strict-serial-sum-f32/multipass", 2},
     {"tiler_sum_f32_cooperative", "strict-serial-sum-f32/cooperative-workgroup", 2},
+    // the same folds under a rule: a flushing contract, or a fused prologue
+    {"tiler_sum_f32_staged_r1_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r1_u_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r4_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r4_u_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r16_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r16_u_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r64_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r64_u_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r256_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_staged_r256_u_m", "serial-sum-f32/serial+rule", 2},
+    {"tiler_sum_f32_partials_m", "serial-sum-f32/multipass+rule", 2},
+    {"tiler_sum_f32_cooperative_m", "serial-sum-f32/cooperative-workgroup+rule", 2},
+    {"tiler_fold_f32_m", "serial-sum-f32/serial-any-axes+rule", 2},
+    {"tiler_map_f32_m", "pointwise-f32+modes", 3},
+    {"tiler_map_bf16_m", "pointwise-bf16+modes", 3},
     {"tiler_sum_f32_grid", "strict-serial-sum-f32/tree", 2},
     {"tiler_sum_f32_grid_unaligned", "strict-serial-sum-f32/tree", 2},
     {"tiler_sum_f32_grid_final", "strict-serial-sum-f32/tree", 2},
@@ -1873,6 +1889,13 @@ bool arithmetic(uint32_t program) {
          program != TILER_HIP_PROGRAM_REINDEX && program != TILER_HIP_PROGRAM_DEQUANTIZE_U4;
 }
 
+// Arithmetic programs whose realizations apply the declared subnormal modes.
+bool realizes_modes(uint32_t program) {
+  return program == TILER_HIP_PROGRAM_SERIAL_SUM || program == TILER_HIP_PROGRAM_FOLD ||
+         program == TILER_HIP_PROGRAM_RMS_NORM || program == TILER_HIP_PROGRAM_SOFTMAX ||
+         program == TILER_HIP_PROGRAM_POINTWISE || program == TILER_HIP_PROGRAM_EXPRESSION;
+}
+
 }  // namespace
 
 // The program a region realizes as (the planners' own output), or the
@@ -1891,11 +1914,12 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
   if (c.input_mode > TILER_HIP_SUBNORMALS_FLUSH_POSITIVE || c.result_mode > TILER_HIP_SUBNORMALS_FLUSH_POSITIVE)
     return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "unknown subnormal mode");
   if (r->reserved != 0) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "reserved region field is not 0");
-  // The device preserves subnormals; a flushing contract is realized only
-  // where the kernel implements the modes (f32 expressions).  Byte moves do
-  // no arithmetic.
-  if (c.flushes() && arithmetic(r->program) &&
-      !(r->program == TILER_HIP_PROGRAM_EXPRESSION && r->dtype == TILER_HIP_F32))
+  // The device preserves subnormals; a flushing contract is realized where
+  // the kernels apply the declared modes at every arithmetic site (the sums
+  // and folds, RMSNorm, softmax, the maps and the expressions, f32 and bf16).
+  // Byte moves and the strict-affine decode have no site a mode could reach;
+  // the conversions and the contractions refuse it.
+  if (c.flushes() && arithmetic(r->program) && !realizes_modes(r->program))
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
                     "a flushing subnormal mode is not realized for this program (the device preserves subnormals)");
   // Forms belong to the softmax and the td,od->to bf16 contraction.
@@ -1915,7 +1939,8 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
       float a, b;
       std::memcpy(&a, &r->scalars[0], 4);
       std::memcpy(&b, &r->scalars[1], 4);
-      st = tiler_rt::plan_map(tiler_rt::Mode::Realized, r->variant, r->dtype, bc ? 1 : 0, e[0], a, b, addr, p);
+      st = tiler_rt::plan_map(tiler_rt::Mode::Realized, r->variant, r->dtype, bc ? 1 : 0, e[0], a, b, addr, p,
+                              c.input_mode, c.result_mode);
       break;
     }
     case TILER_HIP_PROGRAM_EXPRESSION: {
@@ -1946,7 +1971,14 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
         sp.per_partition = r->grouping[1];
         sp.rounds = r->grouping[2];
       }
-      st = tiler_rt::plan_sum_f32(t, e[0], e[1], sp, addr, p);
+      if (c.flushes()) {
+        tiler_rt::FoldRuleHost rule;
+        rule.in_mode = c.input_mode;
+        rule.out_mode = c.result_mode;
+        st = tiler_rt::plan_sum_f32(t, e[0], e[1], sp, addr, p, &rule);
+      } else {
+        st = tiler_rt::plan_sum_f32(t, e[0], e[1], sp, addr, p);
+      }
       break;
     }
     case TILER_HIP_PROGRAM_FOLD: {
@@ -1959,18 +1991,40 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
         st = tiler_rt::compile_expression(TILER_HIP_F32, r->nodes, r->node_count, r->root, true, prog, p.diag);
         if (st != TILER_HIP_OK) break;
       }
+      // A split or workgroup topology regroups the contributor sequence:
+      // permits_reassociation required, as for the sum program.
+      if (r->topology != TILER_HIP_SUM_SERIAL && !c.reassociate) {
+        st = needs_reassociation("a split or workgroup fold");
+        break;
+      }
+      tiler_hip_sum_plan sp;
+      std::memset(&sp, 0, sizeof(sp));
+      sp.topology = r->topology;
+      sp.participant_major = (r->flags & TILER_HIP_REGION_PARTICIPANT_MAJOR) ? 1u : 0u;
+      if (r->topology == TILER_HIP_SUM_MULTIPASS) {
+        sp.partitions = r->grouping[1];
+        sp.per_partition = r->grouping[2];
+      } else if (r->topology == TILER_HIP_SUM_COOPERATIVE && r->rank >= 1) {
+        // The rounds follow from exact coverage of the trailing axis.
+        sp.participants = r->grouping[1];
+        sp.per_partition = r->grouping[2];
+        const uint64_t per_round = sp.participants * sp.per_partition;
+        sp.rounds = per_round && r->extents[r->rank - 1] % per_round == 0 ? r->extents[r->rank - 1] / per_round : 0;
+      }
       st = tiler_rt::plan_fold(r->variant, r->rank, r->extents, r->grouping[0], r->scalars[0], r->scalars[1],
-                               epi ? &prog : nullptr, p);
+                               epi ? &prog : nullptr, p, c, &t, &sp, addr);
       break;
     }
     case TILER_HIP_PROGRAM_RMS_NORM:
       // Without permits_reassociation the serial fold of the reference runs;
       // with it, the grouped row fold (the declared grouping).
-      st = tiler_rt::plan_rms_norm(t, r->dtype, bc ? 1 : 0, e[0], e[1], r->scalars[0], addr, p, !c.reassociate);
+      st = tiler_rt::plan_rms_norm(t, r->dtype, bc ? 1 : 0, e[0], e[1], r->scalars[0], addr, p, !c.reassociate,
+                                   c.input_mode, c.result_mode);
       break;
     case TILER_HIP_PROGRAM_SOFTMAX:
       st = r->dtype == TILER_HIP_F32
-               ? tiler_rt::plan_softmax_f32(tiler_rt::Mode::Realized, t, e[0], e[1], addr, p, !c.reassociate, r->form)
+               ? tiler_rt::plan_softmax_f32(tiler_rt::Mode::Realized, t, e[0], e[1], addr, p, !c.reassociate, r->form,
+                                            c.input_mode, c.result_mode)
                : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "softmax is an f32 family");
       break;
     case TILER_HIP_PROGRAM_CONTRACTION:
