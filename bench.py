@@ -726,16 +726,28 @@ def time_launches(ctx, launch, steps, warmup, graph=True):
 
 def reference_cells(ctx, steps, warmup):
     """This library on the reference's own published benchmark cells, with the
-    same semantics: the strict f32 contraction (tiler_contract_strict_f32, the
-    first-product fold bit for bit) and the three reduction strategies of the
-    dispatch crossover (the strict serial fold; the workgroup tree and the
-    multi-pass split, as under the sweep's FLUSH_AND_REASSOCIATE_F32 contract).
-    Reduction inputs rotate over 5 sets of 64 MiB (more than the Infinity
-    Cache holds)."""
+    same semantics.
+    * The strict f32 contraction cells (tiler_contract_strict_f32, the
+      first-product fold bit for bit).
+    * The dispatch crossover's reduction cells with the reference's own
+      program (reduction-dispatch-crossover/src/main.rs:999-1028): x * 1.0 +
+      0.0 into a sum over the trailing axis, FusedMultiplyAddSerialSum, under
+      FLUSH_AND_REASSOCIATE_F32 (permits_reassociation, both subnormal modes
+      flushing to the signed zero), realized through tiler_hip_realize and run
+      through the RuntimeAdapter stages: the serial fold, the single-workgroup
+      tree (the cooperative workgroup at the balanced partition the
+      2026-08-07 sweep dispatched) and the multi-pass split (the same
+      partition).  Operands are all ones, as in the sweep, so every grouping
+      gives the contributor count exactly; each cell's every output is
+      checked against it before it is timed.  Inputs rotate over 5 sets of
+      64 MiB (more than the Infinity Cache holds)."""
     from tiler_amd import _lib as L
     from tiler_amd.calibrate import split_partitions
+    from tiler_amd.realize import prepare_route, realize
     out = {"contraction": [], "reduction": [],
-           "reference_hardware": {"contraction": "Apple M3 Pro", "reduction": "Apple M4 Max"}}
+           "reference_hardware": {"contraction": "Apple M3 Pro", "reduction": "Apple M4 Max"},
+           "reduction_program": "FusedMultiplyAddSerialSum x*1.0+0.0 over the trailing axis, "
+                                "FLUSH_AND_REASSOCIATE_F32, all-ones operands, via tiler_hip_realize"}
     rng = np.random.default_rng(3)
     for cell, m, n, k, ref_us, ref_gflops, line in REFERENCE_CONTRACTION_CELLS:
         a = ctx.to_device(rng.standard_normal((m, k)).astype(np.float32))
@@ -752,24 +764,35 @@ def reference_cells(ctx, steps, warmup):
                                    "reference_line": line})
         log(f"reference cell {cell} {m}x{n}x{k}: {ms * 1e3:.1f} us ({gflops:.0f} GFLOP/s; reference {ref_us} us)")
     n_elem = 1 << 24
-    xs = [ctx.to_device(rng.uniform(-1, 1, n_elem).astype(np.float32)) for _ in range(5)]
+    ones = np.ones(n_elem, np.float32)
+    xs = [ctx.to_device(ones) for _ in range(5)]
     o = ctx.alloc(65536 * 4)
+    contract = dict(permissions=L.PERMITS_REASSOCIATION, input_subnormals=L.SUBNORMALS_FLUSH_SIGN,
+                    result_subnormals=L.SUBNORMALS_FLUSH_SIGN, variant=L.FOLD_FMA, rank=2,
+                    scalars=(0x3F800000, 0x00000000), flags=L.REGION_ALIGNED16)
     try:
         for rows, extent, strategy, ref_us, line in REFERENCE_REDUCTION_CELLS:
+            p = split_partitions(extent)
             if strategy == "serial-fold":
-                kw = dict(topology=L.SUM_SERIAL)
+                kw = dict(topology=L.SUM_SERIAL, grouping=(2,))
             elif strategy == "single-workgroup-tree":
-                kw = dict(topology=L.SUM_TREE)
+                kw = dict(topology=L.SUM_COOPERATIVE, grouping=(2, p, extent // p))
             else:
-                p = split_partitions(extent)
-                kw = dict(topology=L.SUM_MULTIPASS, partitions=p, per_partition=extent // p)
-            # a split whose partials outgrow the context workspace allocates
-            # per call, which capture refuses: those cells run eagerly
-            ms = time_launches(ctx, lambda i: ctx.sum_f32(xs[i % 5], rows, extent, o, **kw), max(10, steps // 4),
-                               warmup, graph=strategy != "multi-pass-split")
+                kw = dict(topology=L.SUM_MULTIPASS, grouping=(2, p, extent // p))
+            rz = realize(L.PROGRAM_FOLD, (rows, extent), ctx=ctx, **kw, **contract)
+            plans = [prepare_route(ctx, rz, [x, o] + [None] * (len(rz.slots) - 2)) for x in xs]
+            try:
+                plans[0].dispatch()
+                got = o.download(np.float32, (rows,))
+                if not (got == np.float32(extent)).all():
+                    raise RuntimeError(f"reduction cell {rows}x{extent} {strategy}: outputs differ from {extent}")
+                ms = time_launches(ctx, lambda i: plans[i % 5].enqueue(), max(10, steps // 4), warmup)
+            finally:
+                for pl in plans:
+                    pl.release()
             out["reduction"].append({"rows": rows, "extent": extent, "strategy": strategy, "us": ms * 1e3,
-                                     "reference_us": ref_us, "reference_line": line})
-            log(f"reference cell {rows}x{extent} {strategy}: {ms * 1e3:.1f} us (reference {ref_us} us)")
+                                     "kernels": rz.symbols, "reference_us": ref_us, "reference_line": line})
+            log(f"reference cell {rows}x{extent} {strategy} {rz.symbols}: {ms * 1e3:.1f} us (reference {ref_us} us)")
     finally:
         for x in xs + [o]:
             x.free()

@@ -431,6 +431,15 @@ tiler_hip_status tiler_hip_allocate_dispatch(tiler_hip_context *ctx,
  * stream, submits, and waits for terminal success. */
 tiler_hip_status tiler_hip_dispatch(tiler_hip_context *ctx, const tiler_hip_dispatch_plan *plan,
                                     void *const *slot_pointers);
+/* The same encoding on `stream` (NULL: the context's) without the wait, for
+ * callers that order or capture the work themselves (a HIP graph, a serving
+ * loop).  No counterpart in the reference, whose dispatch always waits.  A
+ * plan with constant-slot contents refuses to enqueue under graph capture
+ * (upload the slot first); a failed entry is reported, but errors the device
+ * raises later surface at the caller's own synchronization.  The live
+ * extents are checked as tiler_hip_dispatch checks them. */
+tiler_hip_status tiler_hip_enqueue_dispatch(tiler_hip_context *ctx, const tiler_hip_dispatch_plan *plan,
+                                            void *const *slot_pointers, tiler_hip_stream stream);
 /* Releases the storage tiler_hip_allocate_dispatch acquired for the plan. */
 tiler_hip_status tiler_hip_release_dispatch(tiler_hip_context *ctx,
                                             const tiler_hip_dispatch_plan *plan,

@@ -456,6 +456,7 @@ SIGNATURES = {
     "tiler_hip_plan_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan)]),
     "tiler_hip_allocate_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan), ctypes.POINTER(_P)]),
     "tiler_hip_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan), ctypes.POINTER(_P)]),
+    "tiler_hip_enqueue_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan), ctypes.POINTER(_P), _P]),
     "tiler_hip_release_dispatch": (_S, [_CTX, ctypes.POINTER(DispatchPlan), ctypes.POINTER(_P),
                                         ctypes.POINTER(_P)]),
     "tiler_hip_buffer_alloc": (_S, [_CTX, _U64, ctypes.POINTER(_P)]),

@@ -56,14 +56,9 @@ tiler_sum_f32_serial(const float* __restrict__ x, uint64_t outer, uint64_t exten
 // kDot: the fold of products instead, out[v] = fold over e of fl(a[e] *
 // x[v*length + e]) -- one output row of the strict contraction, with x the
 // right operand's rows and `a` the left operand's row, staged beside them.
-//
-// kRule: each element is the FoldRule's contributor (a prologue, the declared
-// subnormal modes) and the fold is seeded at the first one -- the general
-// form a flushing contract or a fused prologue realizes as.
-template <int R, bool kVec, bool kDot, bool kRule = false>
+template <int R, bool kVec, bool kDot>
 __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
-                                                 const float* __restrict__ a, float* __restrict__ out,
-                                                 tiler::FoldRule rule = tiler::FoldRule{}) {
+                                                 const float* __restrict__ a, float* __restrict__ out) {
   constexpr uint32_t C = 4096 / R;               // elements of a row per stage
   constexpr uint32_t kStride = C + 4;            // LDS row stride in floats (16-byte aligned, staggered banks)
   constexpr uint32_t W = kVec ? 4 : 1;           // elements per load
@@ -118,16 +113,6 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
   const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
   const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < nrows;
   float acc = -0.0f;
-  bool seeded = false;  // kRule: the fold starts at its first contributor
-  auto add1 = [&](float v) {
-    if constexpr (kRule) {
-      const float t = tiler::fold_contributor(rule, v);
-      acc = seeded ? tiler::fold_combine(rule, acc, t) : t;
-      seeded = true;
-    } else {
-      acc = acc + v;
-    }
-  };
   if (stages > 0) {
     load(0);
     store(0);
@@ -162,10 +147,10 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
           acc = acc + w.z * v.z;
           acc = acc + w.w * v.w;
         } else {
-          add1(v.x);
-          add1(v.y);
-          add1(v.z);
-          add1(v.w);
+          acc = acc + v.x;
+          acc = acc + v.y;
+          acc = acc + v.z;
+          acc = acc + v.w;
         }
       };
       if (count == C) {
@@ -204,7 +189,7 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
         for (; c + 4 <= count; c += 4) step4(*reinterpret_cast<const f32x4*>(row + c), c);
         for (; c < count; ++c) {
           if constexpr (kDot) acc = acc + arow[c] * row[c];
-          else add1(row[c]);
+          else acc = acc + row[c];
         }
       }
     }
@@ -212,6 +197,110 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
     __syncthreads();
   }
   if (folds) out[row0 + fr] = length == 0 ? 0.0f : canon(acc);
+}
+
+// The same stages under a FoldRule (a flushing contract, a fused prologue),
+// rows of at least 16.  Every thread turns the values it stages into
+// apply_to_operand(contributor(x)) as it stores them to LDS (the prologue and
+// the input mode are elementwise, so they run on all 256 lanes); the folding
+// lane's chain is then only acc = R(O(acc) + t) per element, seeded at the
+// first contributor (peeled: an identity seed would meet the result mode).
+// kIn / kOut: whether the input / result mode flushes; with kOut the sum
+// that leaves R is never subnormal, so O(acc) is acc itself.  A subnormal is
+// found by v_cmp_class (the subnormal classes of both signs), which leaves
+// zeros alone, and replaced by its own sign bit (mode 2) or +0 (mode 3).
+template <int R>
+constexpr uint32_t kRuleStageFloats = 2u * R * (4096u / R + 4u);  // both buffers of R rows
+
+template <int R, bool kVec, bool kIn, bool kOut>
+__device__ __forceinline__ void staged_rule_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
+                                                 float* __restrict__ out, const tiler::FoldRule& rule,
+                                                 float* __restrict__ lds) {
+  constexpr uint32_t C = 4096 / R;
+  constexpr uint32_t kStride = C + 4;
+  constexpr uint32_t W = kVec ? 4 : 1;
+  constexpr uint32_t kRowPieces = C / W;
+  constexpr uint32_t kPer = 4096 / W / 256;
+  float(*stage)[R * kStride] = reinterpret_cast<float(*)[R * kStride]>(lds);
+  const uint32_t t = threadIdx.x;
+  const uint64_t row0 = (uint64_t)blockIdx.x * R;
+  const uint64_t stages = (length + C - 1) / C;
+  typedef typename std::conditional<kVec, f32x4, float>::type piece;
+  piece reg[kPer];
+  const uint32_t imask = rule.in_mode == 2u ? 0x80000000u : 0u;
+  const uint32_t rmask = rule.out_mode == 2u ? 0x80000000u : 0u;
+  auto flush = [](float v, uint32_t mask) {
+    return __builtin_amdgcn_classf(v, 0x90) ? __uint_as_float(__float_as_uint(v) & mask) : v;
+  };
+  auto operand = [&](float v) {  // apply_to_operand(contributor(v))
+    const float c = tiler::fold_contributor(rule, v);
+    return kIn ? flush(c, imask) : c;
+  };
+  auto load = [&](uint64_t s) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      const uint64_t e = s * C + (uint64_t)(q % kRowPieces) * W;
+      if (row0 + r < nrows && e < length) {
+        const float* src = x + (row0 + r) * length + e;
+        if constexpr (kVec) reg[i] = *reinterpret_cast<const f32x4*>(src);
+        else reg[i] = *src;
+      } else {
+        reg[i] = piece{};  // never folded: past the row or past the last row
+      }
+    }
+  };
+  auto store = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      piece v = reg[i];
+      if constexpr (kVec) {
+        v = f32x4{operand(v.x), operand(v.y), operand(v.z), operand(v.w)};
+      } else {
+        v = operand(v);
+      }
+      *reinterpret_cast<piece*>(&stage[buf][r * kStride + (q % kRowPieces) * W]) = v;
+    }
+  };
+  const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);
+  const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < nrows;
+  float acc = 0.0f, acc_o = 0.0f;  // R's last result, and O of it
+  auto step = [&](float to) {
+    const float sum = acc_o + to;
+    acc = kOut ? flush(sum, rmask) : sum;
+    acc_o = (kIn && !kOut) ? flush(acc, imask) : acc;
+  };
+  if (stages > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (uint64_t s = 0; s < stages; ++s) {
+    const bool more = s + 1 < stages;
+    if (more) load(s + 1);
+    if (folds) {
+      const float* row = &stage[s & 1][fr * kStride];
+      const uint32_t count = (uint32_t)(length - s * C < C ? length - s * C : C);
+      uint32_t c = 0;
+      if (s == 0) {  // the seed: the first contributor (as an operand of the first combine)
+        acc = acc_o = row[0];
+        c = 1;
+        for (; c < 4 && c < count; ++c) step(row[c]);
+      }
+      for (; c + 4 <= count; c += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(row + c);
+        step(v.x);
+        step(v.y);
+        step(v.z);
+        step(v.w);
+      }
+      for (; c < count; ++c) step(row[c]);
+    }
+    if (more) store((uint32_t)((s + 1) & 1));
+    __syncthreads();
+  }
+  if (folds) out[row0 + fr] = tiler::canon(acc);
 }
 
 #define TILER_SUM_STAGED(R)                                                                            \
@@ -232,17 +321,28 @@ TILER_SUM_STAGED(64)
 TILER_SUM_STAGED(256)  // rows of 16..63: stages of 16 elements, every lane folding a row
 
 // The same stages under a FoldRule: a flushing contract's serial fold, and the
-// fused prologues (squared, scale-bias) over a trailing axis.
+// fused prologues (squared, scale-bias) over a trailing axis; one body per
+// pair of flushing dimensions, chosen by a uniform branch.
+template <int R, bool kVec>
+__device__ __forceinline__ void staged_rule_dispatch(const float* __restrict__ x, uint64_t nrows, uint64_t length,
+                                                     float* __restrict__ out, const tiler::FoldRule& rule) {
+  __shared__ __align__(16) float lds[kRuleStageFloats<R>];
+  const bool in = rule.in_mode > 1u, res = rule.out_mode > 1u;
+  if (in && res) staged_rule_body<R, kVec, true, true>(x, nrows, length, out, rule, lds);
+  else if (in) staged_rule_body<R, kVec, true, false>(x, nrows, length, out, rule, lds);
+  else if (res) staged_rule_body<R, kVec, false, true>(x, nrows, length, out, rule, lds);
+  else staged_rule_body<R, kVec, false, false>(x, nrows, length, out, rule, lds);
+}
 #define TILER_SUM_STAGED_RULE(R)                                                                       \
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_sum_f32_staged_r##R##_m(const float* __restrict__ x, uint64_t nrows, uint64_t length,      \
                                     float* __restrict__ out, tiler::FoldRule rule) {                   \
-    staged_fold_body<R, true, false, true>(x, nrows, length, nullptr, out, rule);                      \
+    staged_rule_dispatch<R, true>(x, nrows, length, out, rule);                                        \
   }                                                                                                    \
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_sum_f32_staged_r##R##_u_m(const float* __restrict__ x, uint64_t nrows, uint64_t length,    \
                                       float* __restrict__ out, tiler::FoldRule rule) {                 \
-    staged_fold_body<R, false, false, true>(x, nrows, length, nullptr, out, rule);                     \
+    staged_rule_dispatch<R, false>(x, nrows, length, out, rule);                                       \
   }
 TILER_SUM_STAGED_RULE(1)
 TILER_SUM_STAGED_RULE(4)

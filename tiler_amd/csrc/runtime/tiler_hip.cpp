@@ -1110,10 +1110,43 @@ tiler_hip_status tiler_hip_allocate_dispatch(tiler_hip_context* ctx,
   return TILER_HIP_REFUSE_CAPACITY;
 }
 
+namespace {
+// The entries of a planned dispatch, in order, on `s`; nothing waits.
+tiler_hip_status enqueue_plan(tiler_hip_context* ctx, const tiler_hip_dispatch_plan* plan,
+                              void* const* slot_pointers, hipStream_t s);
+}  // namespace
+
+tiler_hip_status tiler_hip_enqueue_dispatch(tiler_hip_context* ctx, const tiler_hip_dispatch_plan* plan,
+                                            void* const* slot_pointers, tiler_hip_stream stream) try {
+  if (!ctx || !plan) return TILER_HIP_FAIL_LAUNCH;
+  hipSetDevice(ctx->device);
+  const hipStream_t s = pick(ctx, stream);
+  // A constant slot's upload from host memory has no place in captured work.
+  if (plan->slot_contents && capturing(s))
+    for (uint32_t i = 0; i < plan->slot_count; ++i)
+      if (plan->slot_contents[i] && plan->slot_bytes[i])
+        return fail(ctx, TILER_HIP_FAIL_LAUNCH, "a constant slot's upload under graph capture; upload it first");
+  return enqueue_plan(ctx, plan, slot_pointers, s);
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_FAIL_ALLOCATION;
+}
+
 tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_dispatch_plan* plan,
                                     void* const* slot_pointers) try {
   if (!ctx || !plan) return TILER_HIP_FAIL_LAUNCH;
   hipSetDevice(ctx->device);
+  tiler_hip_status st = enqueue_plan(ctx, plan, slot_pointers, ctx->stream);
+  if (st != TILER_HIP_OK) return st;
+  hipError_t err = hipStreamSynchronize(ctx->stream);
+  if (err != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, hipGetErrorString(err));
+  return TILER_HIP_OK;
+} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
+  return TILER_HIP_FAIL_ALLOCATION;
+}
+
+namespace {
+tiler_hip_status enqueue_plan(tiler_hip_context* ctx, const tiler_hip_dispatch_plan* plan,
+                              void* const* slot_pointers, hipStream_t stream) {
   // The live extents again, before anything is launched: the plan that was
   // checked may not be the one dispatched, and a value past its bound would
   // make the kernels read past operands sized for the bound.
@@ -1127,11 +1160,11 @@ tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_disp
   // Constant slots first (an expression's register program), ordered on the
   // stream before every entry; the host bytes are the caller's for the call.
   if (plan->slot_contents) {
-    for (uint32_t s = 0; s < plan->slot_count; ++s) {
-      if (!plan->slot_contents[s] || !plan->slot_bytes[s]) continue;
-      if (!slot_pointers[s]) return fail(ctx, TILER_HIP_FAIL_TRANSFER, "constant slot " + std::to_string(s) + " unbound");
-      hipError_t err = hipMemcpyAsync(slot_pointers[s], plan->slot_contents[s], plan->slot_bytes[s],
-                                      hipMemcpyHostToDevice, ctx->stream);
+    for (uint32_t k = 0; k < plan->slot_count; ++k) {
+      if (!plan->slot_contents[k] || !plan->slot_bytes[k]) continue;
+      if (!slot_pointers[k]) return fail(ctx, TILER_HIP_FAIL_TRANSFER, "constant slot " + std::to_string(k) + " unbound");
+      hipError_t err = hipMemcpyAsync(slot_pointers[k], plan->slot_contents[k], plan->slot_bytes[k],
+                                      hipMemcpyHostToDevice, stream);
       if (err != hipSuccess) return fail(ctx, TILER_HIP_FAIL_TRANSFER, hipGetErrorString(err));
     }
   }
@@ -1154,16 +1187,13 @@ tiler_hip_status tiler_hip_dispatch(tiler_hip_context* ctx, const tiler_hip_disp
                       &size, HIP_LAUNCH_PARAM_END};
     hipError_t err = hipModuleLaunchKernel(ctx->prepared[e.prepared], e.grid[0], e.grid[1],
                                            e.grid[2], e.block[0], e.block[1], e.block[2],
-                                           e.dynamic_lds_bytes, ctx->stream, nullptr, config);
+                                           e.dynamic_lds_bytes, stream, nullptr, config);
     if (err != hipSuccess)
       return fail(ctx, TILER_HIP_FAIL_LAUNCH, "entry " + std::to_string(i) + ": " + hipGetErrorString(err));
   }
-  hipError_t err = hipStreamSynchronize(ctx->stream);
-  if (err != hipSuccess) return fail(ctx, TILER_HIP_FAIL_DEVICE, hipGetErrorString(err));
   return TILER_HIP_OK;
-} catch (...) {  // host memory exhausted: nothing unwinds through the C ABI
-  return TILER_HIP_FAIL_ALLOCATION;
 }
+}  // namespace
 
 tiler_hip_status tiler_hip_release_dispatch(tiler_hip_context* ctx,
                                             const tiler_hip_dispatch_plan* plan,

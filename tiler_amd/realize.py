@@ -235,16 +235,52 @@ def _capacity(buf):
     return getattr(buf, "nbytes", None)
 
 
-def route(ctx, realization: Realization, storage, payload=None, extents=()) -> None:
-    """Executes `realization` on `ctx`'s stream and waits for it.  `storage`
-    lists one device buffer (or address) per slot, in the realization's slot
-    order; scratch slots may be None (allocated here, released after).
-    `payload` (from `tiler_amd.envelope.select_payload`) routes through a
-    carried code object instead of the library's own: every symbol dispatched
-    must be one of its PayloadEntryMappings.  `extents` gives this dispatch's
-    value of each live extent (realization.live_extents, in order); the slots
-    still hold the bound, and an input whose axis is live is packed at the
-    value given."""
+class RoutedPlan:
+    """A realization committed to its storage: planned (plan_dispatch, which
+    acquires nothing), its scratch slots allocated (allocate_dispatch), ready
+    to run.  `dispatch()` runs it and waits (the adapter's dispatch);
+    `enqueue(stream)` only encodes it (tiler_hip_enqueue_dispatch), for a
+    caller that captures it into a HIP graph or orders it itself; `release()`
+    frees the scratch it allocated.  Built by `prepare_route`."""
+
+    def __init__(self, ctx, rz, plan, ptrs, owned, keep):
+        self.ctx, self.rz, self.plan, self.ptrs, self.owned, self._keep = ctx, rz, plan, ptrs, owned, keep
+
+    def dispatch(self):
+        h = self.ctx.handle
+        _raise(L.lib().tiler_hip_dispatch(h, ctypes.byref(self.plan), self.ptrs), "dispatch", self.ctx.diagnostic())
+        self._check_records()
+
+    def enqueue(self, stream=None):
+        _raise(L.lib().tiler_hip_enqueue_dispatch(self.ctx.handle, ctypes.byref(self.plan), self.ptrs, stream),
+               "enqueue_dispatch", self.ctx.diagnostic())
+
+    def _check_records(self):
+        h, rz, ptrs = self.ctx.handle, self.rz, self.ptrs
+        if rz.program == L.PROGRAM_GATHER:
+            rec = ctypes.c_uint64()
+            _raise(L.lib().tiler_hip_download(h, ctypes.byref(rec), ptrs[3], 8), "read gather record")
+            if rec.value != 0xFFFFFFFFFFFFFFFF:
+                raise GatherIndexOutOfBounds(L.FAIL_GATHER_INDEX_OUT_OF_BOUNDS, rec.value)
+        elif rz.program == L.PROGRAM_DEQUANTIZE_U4:
+            # the kernel's verdict on the scale and zero point it read
+            # (quantization.rs:318-370): the output was not written
+            rec = ctypes.c_uint32()
+            _raise(L.lib().tiler_hip_download(h, ctypes.byref(rec), ptrs[4], 4), "read domain record")
+            if rec.value:
+                raise Failure(L.FAIL_VALUE_DOMAIN, "dispatch",
+                              "scale outside positive-normal-f32" if rec.value == 1
+                              else "zero point outside the U4 code domain 0..=15")
+
+    def release(self):
+        if self.plan is not None:
+            L.lib().tiler_hip_release_dispatch(self.ctx.handle, ctypes.byref(self.plan), self.ptrs, self.owned)
+            self.plan = None
+
+
+def prepare_route(ctx, realization: Realization, storage, payload=None, extents=()) -> "RoutedPlan | None":
+    """The route's steps up to dispatch (see `route`): refusals raise before
+    anything is committed.  Returns None for zero work (nothing to dispatch)."""
     rz = realization
     if len(extents) != len(rz.live_extents):
         raise Refusal(L.REFUSE_BINDING_MISMATCH, "route",
@@ -259,7 +295,7 @@ def route(ctx, realization: Realization, storage, payload=None, extents=()) -> N
         raise Refusal(L.REFUSE_BINDING_MISMATCH, "route",
                       f"{len(storage)} storage bindings for {len(rz.slots)} slots")
     if rz.raw.entry_count == 0:
-        return  # zero work: the dispatch is skipped
+        return None  # zero work: the dispatch is skipped
     for i, ((role, nbytes), buf) in enumerate(zip(rz.slots, storage)):
         if buf is None:
             if role not in (L.SLOT_SCRATCH, L.SLOT_CONSTANT):
@@ -297,6 +333,7 @@ def route(ctx, realization: Realization, storage, payload=None, extents=()) -> N
     live = len(rz.live_extents)
     values = (ctypes.c_uint64 * max(1, live))(*[int(v) for v in extents])
     ranges = (L.LiveExtent * max(1, live))(*rz.raw.live_extents[:live])
+    keep += [entries, slot_bytes, contents, values, ranges]
     plan = L.DispatchPlan(len(rz.slots), slot_bytes, n, entries, contents, live, values, ranges)
     h = ctx.handle
     _raise(L.lib().tiler_hip_plan_dispatch(h, ctypes.byref(plan)), "plan_dispatch", ctx.diagnostic())
@@ -304,21 +341,23 @@ def route(ctx, realization: Realization, storage, payload=None, extents=()) -> N
     owned = (ctypes.c_void_p * len(rz.slots))(*[None if b is None else 1 for b in storage])
     _raise(L.lib().tiler_hip_allocate_dispatch(h, ctypes.byref(plan), ptrs), "allocate_dispatch",
            ctx.diagnostic())
+    return RoutedPlan(ctx, rz, plan, ptrs, owned, keep)
+
+
+def route(ctx, realization: Realization, storage, payload=None, extents=()) -> None:
+    """Executes `realization` on `ctx`'s stream and waits for it.  `storage`
+    lists one device buffer (or address) per slot, in the realization's slot
+    order; scratch slots may be None (allocated here, released after).
+    `payload` (from `tiler_amd.envelope.select_payload`) routes through a
+    carried code object instead of the library's own: every symbol dispatched
+    must be one of its PayloadEntryMappings.  `extents` gives this dispatch's
+    value of each live extent (realization.live_extents, in order); the slots
+    still hold the bound, and an input whose axis is live is packed at the
+    value given."""
+    routed = prepare_route(ctx, realization, storage, payload, extents)
+    if routed is None:
+        return
     try:
-        _raise(L.lib().tiler_hip_dispatch(h, ctypes.byref(plan), ptrs), "dispatch", ctx.diagnostic())
-        if rz.program == L.PROGRAM_GATHER:
-            rec = ctypes.c_uint64()
-            _raise(L.lib().tiler_hip_download(h, ctypes.byref(rec), ptrs[3], 8), "read gather record")
-            if rec.value != 0xFFFFFFFFFFFFFFFF:
-                raise GatherIndexOutOfBounds(L.FAIL_GATHER_INDEX_OUT_OF_BOUNDS, rec.value)
-        elif rz.program == L.PROGRAM_DEQUANTIZE_U4:
-            # the kernel's verdict on the scale and zero point it read
-            # (quantization.rs:318-370): the output was not written
-            rec = ctypes.c_uint32()
-            _raise(L.lib().tiler_hip_download(h, ctypes.byref(rec), ptrs[4], 4), "read domain record")
-            if rec.value:
-                raise Failure(L.FAIL_VALUE_DOMAIN, "dispatch",
-                              "scale outside positive-normal-f32" if rec.value == 1
-                              else "zero point outside the U4 code domain 0..=15")
+        routed.dispatch()
     finally:
-        L.lib().tiler_hip_release_dispatch(h, ctypes.byref(plan), ptrs, owned)
+        routed.release()
