@@ -89,7 +89,7 @@ _SIGS = {
     "tiler_oracle_strict_affine_domain": (_I32, [_U32, ctypes.c_uint8]),
     "tiler_oracle_contract_strict_f32": (_I32, [_P, _P, _U64, _U64, _U64, _P, _U64, _U64, _U32]),
     "tiler_oracle_contract_general": (_I32, [_U32, _I32, _U32, _P, _P, _U32, _P, _P, _U32, _P, _P, _P, _P,
-                                             _U32]),
+                                             _U32, _I32, _I32]),
     "tiler_oracle_row_grouped_sum_f32": (_I32, [_P, _U64, _U64, _U32, _U32, _P]),
     "tiler_oracle_grid_tree_sum_f32": (_I32, [_P, _U64, _U32, _P]),
     "tiler_oracle_rms_norm_grouped_f32": (_I32, [_P, _P, _U64, _U64, _U32, _I32, _U32, _U32, _P]),
@@ -317,7 +317,8 @@ def contract_strict_f32(a, b, m, n, k, row_begin=0, row_end=None, threads=None) 
     return c.reshape(m, n)
 
 
-def contract_general(left, left_idx, right, right_idx, out_idx, silu=False, threads=None) -> np.ndarray:
+def contract_general(left, left_idx, right, right_idx, out_idx, silu=False, threads=None, input_mode=PRESERVE,
+                     result_mode=PRESERVE) -> np.ndarray:
     """A binary contraction by index labels (ADR 0087), e.g. attention scores
     ``contract_general(q, "bhqd", k, "bkd", "bhqk")``: labels are strings of
     single characters or sequences of ints.  f32 operands give an f32 result;
@@ -339,7 +340,8 @@ def contract_general(left, left_idx, right, right_idx, out_idx, silu=False, thre
     threads = threads or max(1, min(os.cpu_count() or 1, 16))
     _check(lib().tiler_oracle_contract_general(1 if bf16 else 0, 1 if silu else 0, li.size, _ptr(li), _ptr(ld),
                                                ri.size, _ptr(ri), _ptr(rd), oi.size, _ptr(oi), _ptr(left),
-                                               _ptr(right), _ptr(out), threads), "contract_general")
+                                               _ptr(right), _ptr(out), threads, input_mode, result_mode),
+           "contract_general")
     return out
 
 

@@ -574,6 +574,7 @@ int32_t tiler_oracle_contract_strict_f32(const float *a, const float *b, uint64_
 typedef struct {
     uint32_t dtype;
     int32_t silu;
+    int32_t input_mode, result_mode;
     const void *left, *right;
     void *out;
     uint32_t out_rank, con_rank;
@@ -591,6 +592,7 @@ static float general_operand(const general_job *j, int right, uint64_t off) {
 
 static void *general_worker(void *arg) {
     general_job *j = (general_job *)arg;
+    const int32_t input_mode = j->input_mode, result_mode = j->result_mode; /* OPND / RSLT */
     for (uint64_t o = j->begin; o < j->end; ++o) {
         /* the output coordinate, row-major (contraction.rs:580-585) */
         uint64_t lbase = 0, rbase = 0, rem = o;
@@ -604,8 +606,10 @@ static void *general_worker(void *arg) {
         uint64_t lo = 0, ro = 0;
         float acc = 0.0f;
         for (uint64_t step = 0; step < j->con_count; ++step) {
-            float p = canon(general_operand(j, 0, lbase + lo) * general_operand(j, 1, rbase + ro));
-            acc = step == 0 ? p : canon(acc + p); /* contraction.rs:635-652 */
+            /* contraction.rs:600-625: each factor as an operand, the product and
+             * every accumulation as results, the accumulator as an operand */
+            float p = RSLT(canon(OPND(general_operand(j, 0, lbase + lo)) * OPND(general_operand(j, 1, rbase + ro))));
+            acc = step == 0 ? p : RSLT(canon(OPND(acc) + OPND(p))); /* contraction.rs:635-652 */
             /* next contracted coordinate, ascending lexicographic */
             for (int32_t d = (int32_t)j->con_rank - 1; d >= 0; --d) {
                 lo += j->l_con[d];
@@ -621,7 +625,7 @@ static void *general_worker(void *arg) {
             ((float *)j->out)[o] = acc;
         } else {
             float v = acc;
-            if (j->silu && tiler_oracle_silu_f32(&acc, 1, &v, 0, 0) != TILER_ORACLE_OK) {
+            if (j->silu && tiler_oracle_silu_f32(&acc, 1, &v, input_mode, result_mode) != TILER_ORACLE_OK) {
                 j->status = TILER_ORACLE_UNDECIDED;
                 return NULL;
             }
@@ -636,7 +640,8 @@ int32_t tiler_oracle_contract_general(uint32_t dtype, int32_t silu, uint32_t lef
                                       uint32_t right_rank, const uint32_t *right_idx,
                                       const uint64_t *right_dims, uint32_t out_rank,
                                       const uint32_t *out_idx, const void *left, const void *right,
-                                      void *out, uint32_t threads) {
+                                      void *out, uint32_t threads, int32_t input_mode,
+                                      int32_t result_mode) {
     if (dtype > 1 || (dtype == 0 && silu)) return TILER_ORACLE_INVALID_APPLICATION;
     if (left_rank > 8 || right_rank > 8 || out_rank > 8) return TILER_ORACLE_INVALID_APPLICATION;
     const uint32_t rank[2] = {left_rank, right_rank};
@@ -670,6 +675,8 @@ int32_t tiler_oracle_contract_general(uint32_t dtype, int32_t silu, uint32_t lef
     memset(&base, 0, sizeof base);
     base.dtype = dtype;
     base.silu = silu;
+    base.input_mode = input_mode;
+    base.result_mode = result_mode;
     base.left = left;
     base.right = right;
     base.out = out;

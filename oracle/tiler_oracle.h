@@ -98,7 +98,8 @@ int32_t tiler_oracle_contract_strict_f32(const float *a, const float *b, uint64_
 
 /* Contraction over a general binary index structure (ADR 0087):
  * tiler-reference/src/contraction.rs:346-715 (ContractionFold::plan and
- * evaluate_outputs) under the preserve conformance.  Each operand is dense
+ * evaluate_outputs) under a conformance: the modes at the factors, the
+ * product and every accumulation (contraction.rs:600-625).  Each operand is dense
  * row-major with `*_rank` axes labelled by `*_idx` (any uint32 labels) and
  * sized by `*_dims`; the output is dense row-major over `out_idx`.  The five
  * structural rules (tiler-ir/src/semantic/contraction.rs:804-900) and extent
@@ -113,7 +114,8 @@ int32_t tiler_oracle_contract_general(uint32_t dtype, int32_t silu, uint32_t lef
                                       uint32_t right_rank, const uint32_t *right_idx,
                                       const uint64_t *right_dims, uint32_t out_rank,
                                       const uint32_t *out_idx, const void *left, const void *right,
-                                      void *out, uint32_t threads);
+                                      void *out, uint32_t threads, int32_t input_mode,
+                                      int32_t result_mode);
 
 /* ---- Declared groupings of the tiler-hip reassociating kernels ----------
  * These restate the exact addition order each HIP kernel performs, so the

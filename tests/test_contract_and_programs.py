@@ -83,9 +83,8 @@ def test_strict_contract_selects_the_serial_row_and_contraction_kernels():
 
 
 @pytest.mark.parametrize("program,extents,kw", [
-    (L.PROGRAM_CONTRACTION, (4, 4, 4), {}),
-    (L.PROGRAM_CONTRACTION, (4, 4, 64), dict(dtype=L.BF16, permissions=RE)),
     (L.PROGRAM_CONVERT, (64,), {}),
+    (L.PROGRAM_CONVERT, (64,), dict(variant=L.CONVERT_WIDEN_BF16_F32)),
 ])
 @pytest.mark.parametrize("modes", [(L.SUBNORMALS_FLUSH_SIGN, 0), (0, L.SUBNORMALS_FLUSH_POSITIVE)])
 def test_flushing_modes_refuse_where_not_implemented(program, extents, kw, modes):
@@ -140,6 +139,10 @@ FS, FP = L.SUBNORMALS_FLUSH_SIGN, L.SUBNORMALS_FLUSH_POSITIVE
     (L.PROGRAM_POINTWISE, (1024,), dict(variant=L.MAP_SILU), ["tiler_map_f32_m"]),
     (L.PROGRAM_POINTWISE, (1024,), dict(variant=L.MAP_ADD, dtype=L.BF16), ["tiler_map_bf16_m"]),
     (L.PROGRAM_EXPRESSION, (64,), dict(dtype=L.BF16, nodes=[(0, 0, 0), (2, 0, 0)]), ["tiler_expr_bf16_r16s_i1"]),
+    # contractions: the strict fold with the modes, whatever the permissions
+    (L.PROGRAM_CONTRACTION, (4, 4, 4), {}, ["tiler_contract_general_f32_m"]),
+    (L.PROGRAM_CONTRACTION, (4096, 4096, 64), dict(dtype=L.BF16, variant=L.EPILOGUE_SILU, permissions=RE),
+     ["tiler_contract_general_bf16_silu_m"]),
 ])
 def test_flushing_modes_are_realized(program, extents, kw, symbols):
     """A flushing contract realizes where the kernels apply the modes; the

@@ -169,3 +169,32 @@ def test_form_selection():
     # the strict form's geometry travels in a constant slot
     rz = realize(L.PROGRAM_CONTRACTION, (), dtype=L.F32, structure=score)
     assert rz.slots[3][0] == L.SLOT_CONSTANT and rz.raw.constant_bytes == rz.slots[3][1]
+
+
+def test_contraction_under_modes_closed_forms():
+    """contraction.rs:600-625 under the modes, on closed forms: a subnormal
+    product of normal factors (only the result mode reaches it); a subnormal
+    factor (the input mode); products that cancel to a subnormal sum; the
+    seed is the first product, which a flushing result mode still meets."""
+    PRE, FS, FP = oracle.PRESERVE, oracle.FLUSH_SIGN_PRESERVING, oracle.FLUSH_POSITIVE_ZERO
+    t = np.float32(2.0 ** -70)
+    a = np.array([[t]], np.float32)
+    b = np.array([[-t]], np.float32)
+    got = lambda im, rm: int(bits(oracle.contract_general(a, "mk", b, "nk", "mn", input_mode=im, result_mode=rm))[0])
+    assert got(PRE, PRE) == 0x80000200            # -2^-140 = -(2^9 quanta): a subnormal product
+    assert got(FS, PRE) == 0x80000200             # no factor is subnormal
+    assert got(PRE, FS) == 0x80000000 and got(PRE, FP) == 0x00000000
+    sub = np.array([[np.uint32(0x00000100).view(np.float32)]], np.float32)
+    two = np.array([[2.0]], np.float32)
+    assert int(bits(oracle.contract_general(sub, "mk", two, "nk", "mn"))[0]) == 0x00000200
+    assert int(bits(oracle.contract_general(sub, "mk", two, "nk", "mn", input_mode=FS))[0]) == 0
+    # (2^-126 (1 + 2^-23)) * 1 + (-2^-126) * 1: a normal seed, a Sterbenz difference 2^-149
+    a2 = np.array([[np.uint32(0x00800001).view(np.float32), np.uint32(0x80800000).view(np.float32)]], np.float32)
+    one = np.ones((1, 2), np.float32)
+    assert int(bits(oracle.contract_general(a2, "mk", one, "nk", "mn"))[0]) == 0x00000001
+    assert int(bits(oracle.contract_general(a2, "mk", one, "nk", "mn", result_mode=FS))[0]) == 0x00000000
+    # the same bits as the strict f32 oracle under the preserving modes
+    rng = np.random.default_rng(9)
+    x, y = rng.standard_normal((5, 7)).astype(np.float32), rng.standard_normal((6, 7)).astype(np.float32)
+    assert np.array_equal(bits(oracle.contract_general(x, "mk", y, "nk", "mn")),
+                          bits(oracle.contract_strict_f32(x, y, 5, 6, 7)))

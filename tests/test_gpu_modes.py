@@ -11,7 +11,10 @@ FLUSH_AND_REASSOCIATE_F32 and the bf16 flush, tiler-compiler/src/session.rs:
 * RMSNorm (f32 and bf16 storage) and softmax, with the modes at every site;
 * the f32 maps (scale-bias, SiLU, add, multiply) and the bf16 maps and
   expressions (operand and rounded-result encodings), including bf16.rs's
-  seven counterexamples (bf16/tests.rs:722-835) on the device.
+  seven counterexamples (bf16/tests.rs:722-835) on the device;
+* the contractions (td,od->to in f32 and bf16 with SiLU, and an attention
+  structure) on the strict fold with the modes at every site
+  (contraction.rs:600-625).
 
 Inputs are built so that operands, products and partial sums land in the
 subnormal range.  Mode numbers: the region's (1 preserve, 2 flush to the
@@ -297,3 +300,43 @@ def test_bf16_expressions_and_maps_under_modes(ctx, modes):
     got = _map(ctx, L.MAP_SCALE_BIAS, L.BF16, x, a=0.5, b=float(oracle.bf16_widen(np.array([3], np.uint16))[0]),
                modes=modes)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("modes", MODES)
+def test_contractions_under_modes(ctx, modes):
+    """contraction.rs:600-625 under the modes: td,od->to in f32 and bf16
+    (+SiLU) and an attention-shaped structure, against oracle.contract_general
+    with the same modes; operands ~2^-65 so products and partial sums fall
+    into the subnormal range."""
+    im, rm = modes
+    rng = np.random.default_rng(8)
+    m, n, k = 37, 45, 29
+    a = (rng.standard_normal((m, k)) * 2.0 ** -65).astype(np.float32)
+    b = (rng.standard_normal((n, k)) * 2.0 ** -65).astype(np.float32)
+    a[0, :5] = tiny_f32(rng, 5)
+    b[1, :5] = tiny_f32(rng, 5)
+    b[2] = rng.standard_normal(k).astype(np.float32) * 2.0 ** 60
+    rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), input_subnormals=im, result_subnormals=rm, permissions=RE,
+                 flags=L.REGION_ALIGNED16, ctx=ctx)
+    assert rz.symbols == ["tiler_contract_general_f32_m"], rz.symbols
+    got = _route(ctx, rz, [a, b], (m, n), np.float32)
+    want = oracle.contract_general(a, "mk", b, "nk", "mn", input_mode=om(im), result_mode=om(rm))
+    assert np.array_equal(bits(got), bits(want))
+    a16 = oracle.bf16_narrow(a * np.float32(2.0 ** 60)).reshape(m, k)
+    b16 = oracle.bf16_narrow(b * np.float32(2.0 ** -60)).reshape(n, k)
+    for ep in (L.EPILOGUE_NONE, L.EPILOGUE_SILU):
+        rz = realize(L.PROGRAM_CONTRACTION, (m, n, k), dtype=L.BF16, variant=ep, input_subnormals=im,
+                     result_subnormals=rm, permissions=RE, flags=L.REGION_ALIGNED16, ctx=ctx)
+        got = _route(ctx, rz, [a16, b16], (m, n), np.uint16)
+        want = oracle.contract_general(a16, "mk", b16, "nk", "mn", silu=ep == L.EPILOGUE_SILU,
+                                       input_mode=om(im), result_mode=om(rm))
+        assert np.array_equal(got, want), (ep, rz.symbols)
+    # attention scores bhqd,bkd->bhqk (the key shared across heads)
+    q = (rng.standard_normal((2, 3, 5, 16)) * 2.0 ** -66).astype(np.float32)
+    kk = (rng.standard_normal((2, 7, 16)) * 2.0 ** -66).astype(np.float32)
+    st = L.contraction_structure("bhqd", q.shape, "bkd", kk.shape, "bhqk")
+    rz = realize(L.PROGRAM_CONTRACTION, (), structure=st, input_subnormals=im, result_subnormals=rm,
+                 flags=L.REGION_ALIGNED16, ctx=ctx)
+    got = _route(ctx, rz, [q, kk], (2, 3, 5, 7), np.float32)
+    want = oracle.contract_general(q, "bhqd", kk, "bkd", "bhqk", input_mode=om(im), result_mode=om(rm))
+    assert np.array_equal(bits(got), bits(want)), rz.symbols

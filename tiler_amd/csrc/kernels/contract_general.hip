@@ -30,9 +30,15 @@ __device__ __forceinline__ float widen(T v) {
   else return v;
 }
 
-template <typename T, bool kSilu>
+// kModes: the declared subnormal modes at every site of the fold
+// (contraction.rs:600-625): each factor as an operand, the product and every
+// accumulation as results, the accumulator as an operand; seeded at the first
+// product itself; the SiLU under the same modes (silu.rs:511-533).
+template <typename T, bool kSilu, bool kModes = false>
 __device__ __forceinline__ void general_body(const T* __restrict__ l, const T* __restrict__ r,
-                                             T* __restrict__ out, const GeneralGeometry& g) {
+                                             T* __restrict__ out, const GeneralGeometry& g, uint32_t im = 1u,
+                                             uint32_t rm = 1u) {
+  using tiler::subnormal;
   // g lives in a constant slot: every read is a uniform (scalar) load.
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   const uint32_t inner = g.con_rank - 1;
@@ -58,12 +64,19 @@ __device__ __forceinline__ void general_body(const T* __restrict__ l, const T* _
 #pragma unroll
     for (int d = 0; d < kAxes; ++d) coord[d] = 0;
     float acc = -0.0f;  // -0 + first product == first product, bit for bit
+    bool seeded = false;
     for (;;) {
       const T* lp = l + lb;
       const T* rp = r + rb;
       for (uint64_t i = 0; i < in_dim; ++i) {
-        const float p = widen(lp[i * in_l]) * widen(rp[i * in_r]);
-        acc = acc + p;
+        if constexpr (kModes) {
+          const float p = subnormal(rm, subnormal(im, widen(lp[i * in_l])) * subnormal(im, widen(rp[i * in_r])));
+          acc = seeded ? subnormal(rm, subnormal(im, acc) + subnormal(im, p)) : p;
+          seeded = true;
+        } else {
+          const float p = widen(lp[i * in_l]) * widen(rp[i * in_r]);
+          acc = acc + p;
+        }
       }
       // the next outer contracted coordinate (axes inner-1 .. 0)
       bool carry = true;
@@ -84,7 +97,20 @@ __device__ __forceinline__ void general_body(const T* __restrict__ l, const T* _
     }
     float v = canon(acc);
     if constexpr (sizeof(T) == 2) {
-      if (kSilu) v = tiler::silu_f32(v);
+      if (kSilu) {
+        if constexpr (kModes) {
+          if (v == v && v != __builtin_huge_valf() && v != -__builtin_huge_valf()) {
+            const float a = subnormal(im, v);
+            const float e = subnormal(rm, tiler::exp_f32_cr(subnormal(im, -a)));
+            const float divisor = subnormal(rm, 1.0f + subnormal(im, e));
+            v = subnormal(rm, subnormal(im, a) / subnormal(im, divisor));
+          } else {
+            v = tiler::silu_f32(v);
+          }
+        } else {
+          v = tiler::silu_f32(v);
+        }
+      }
       out[o] = (T)tiler::bf16_narrow(v);
     } else {
       out[o] = v;
@@ -108,6 +134,25 @@ extern "C" __global__ void __launch_bounds__(256)
 tiler_contract_general_bf16_silu(const uint16_t* __restrict__ l, const uint16_t* __restrict__ r,
                                  uint16_t* __restrict__ out, const GeneralGeometry* __restrict__ g) {
   general_body<uint16_t, true>(l, r, out, *g);
+}
+
+// The strict folds under the declared subnormal modes (a flushing contract).
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_general_f32_m(const float* __restrict__ l, const float* __restrict__ r, float* __restrict__ out,
+                             const GeneralGeometry* __restrict__ g, uint32_t in_mode, uint32_t out_mode) {
+  general_body<float, false, true>(l, r, out, *g, in_mode, out_mode);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_general_bf16_m(const uint16_t* __restrict__ l, const uint16_t* __restrict__ r,
+                              uint16_t* __restrict__ out, const GeneralGeometry* __restrict__ g, uint32_t in_mode,
+                              uint32_t out_mode) {
+  general_body<uint16_t, false, true>(l, r, out, *g, in_mode, out_mode);
+}
+extern "C" __global__ void __launch_bounds__(256)
+tiler_contract_general_bf16_silu_m(const uint16_t* __restrict__ l, const uint16_t* __restrict__ r,
+                                   uint16_t* __restrict__ out, const GeneralGeometry* __restrict__ g,
+                                   uint32_t in_mode, uint32_t out_mode) {
+  general_body<uint16_t, true, true>(l, r, out, *g, in_mode, out_mode);
 }
 
 // dst[b][c][r] = src[b][r][c]; grid (ceil(cols/64), min(batches * row tiles,

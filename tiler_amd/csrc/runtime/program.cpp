@@ -853,8 +853,13 @@ bool stride_of(const tiler_hip_contraction_structure& s, int side, uint32_t labe
 }  // namespace
 
 tiler_hip_status plan_contract_general(const Target& t, uint32_t dtype, const tiler_hip_contraction_structure& s,
-                                       uint32_t epilogue, bool strict, const uintptr_t* addr, Program& p) {
+                                       uint32_t epilogue, bool strict, const uintptr_t* addr, Program& p,
+                                       uint32_t in_mode, uint32_t out_mode) {
   using tiler_geom::kAxes;
+  // A flushing contract: the strict fold with the modes at every site (the
+  // MFMA units round each block of products without a per-product flush).
+  const bool modes = in_mode > 1 || out_mode > 1;
+  if (modes) strict = true;
   if (dtype != TILER_HIP_F32 && dtype != TILER_HIP_BF16) return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "contraction dtype");
   if (epilogue > TILER_HIP_EPILOGUE_SILU) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "epilogue");
   if (dtype == TILER_HIP_F32 && epilogue != TILER_HIP_EPILOGUE_NONE)
@@ -1037,10 +1042,11 @@ tiler_hip_status plan_contract_general(const Target& t, uint32_t dtype, const ti
   const uint32_t geo = p.slot(sizeof g, TILER_HIP_SLOT_CONSTANT);
   p.constant_slot = geo;
   p.constant.assign(reinterpret_cast<const uint8_t*>(&g), reinterpret_cast<const uint8_t*>(&g) + sizeof g);
-  const char* name = dtype == TILER_HIP_F32 ? "tiler_contract_general_f32"
-                     : silu                 ? "tiler_contract_general_bf16_silu"
-                                            : "tiler_contract_general_bf16";
-  p.add(name, blocks_capped(outputs, 65536), 1, 256).ptr(l).ptr(r).ptr(o).ptr(geo);
+  const char* name = dtype == TILER_HIP_F32 ? (modes ? "tiler_contract_general_f32_m" : "tiler_contract_general_f32")
+                     : silu ? (modes ? "tiler_contract_general_bf16_silu_m" : "tiler_contract_general_bf16_silu")
+                            : (modes ? "tiler_contract_general_bf16_m" : "tiler_contract_general_bf16");
+  Launch& launch = p.add(name, blocks_capped(outputs, 65536), 1, 256).ptr(l).ptr(r).ptr(o).ptr(geo);
+  if (modes) launch.u32(in_mode).u32(out_mode);
   return TILER_HIP_OK;
 }
 

@@ -201,7 +201,8 @@ tiler_hip_status plan_contract_strict_f32(const Target& t, uint64_t m, uint64_t 
 // reassociation), or under it the batched MFMA forms where the structure is
 // [batch.., m, k] x [batch.., n, k | k, n] -> [batch.., m, n].
 tiler_hip_status plan_contract_general(const Target& t, uint32_t dtype, const tiler_hip_contraction_structure& s,
-                                       uint32_t epilogue, bool strict, const uintptr_t* addr, Program& p);
+                                       uint32_t epilogue, bool strict, const uintptr_t* addr, Program& p,
+                                       uint32_t in_mode = 1, uint32_t out_mode = 1);
 // `form` (TILER_HIP_FORM_CONTRACT_*) forces one MFMA form, refusing when the
 // request does not admit it; TILER_HIP_FORM_AUTO lets the planner choose.
 tiler_hip_status plan_contract_bf16(const Target& t, uint64_t m, uint64_t n, uint64_t k,

@@ -72,6 +72,9 @@ const EntryRow kEntries[] = {
     {"tiler_sum_f32_cooperative_m", "serial-sum-f32/cooperative-workgroup+rule", 2},
     {"tiler_fold_f32_m", "serial-sum-f32/serial-any-axes+rule", 2},
     {"tiler_map_f32_m", "pointwise-f32+modes", 3},
+    {"tiler_contract_general_f32_m", "tensor-contraction-f32/strict-general+modes", 4},
+    {"tiler_contract_general_bf16_m", "tensor-contraction-bf16/strict-general+modes", 4},
+    {"tiler_contract_general_bf16_silu_m", "tensor-contraction-bf16/strict-general+silu+modes", 4},
     {"tiler_map_bf16_m", "pointwise-bf16+modes", 3},
     {"tiler_sum_f32_grid", "strict-serial-sum-f32/tree", 2},
     {"tiler_sum_f32_grid_unaligned", "strict-serial-sum-f32/tree", 2},
@@ -1923,7 +1926,8 @@ bool arithmetic(uint32_t program) {
 bool realizes_modes(uint32_t program) {
   return program == TILER_HIP_PROGRAM_SERIAL_SUM || program == TILER_HIP_PROGRAM_FOLD ||
          program == TILER_HIP_PROGRAM_RMS_NORM || program == TILER_HIP_PROGRAM_SOFTMAX ||
-         program == TILER_HIP_PROGRAM_POINTWISE || program == TILER_HIP_PROGRAM_EXPRESSION;
+         program == TILER_HIP_PROGRAM_POINTWISE || program == TILER_HIP_PROGRAM_EXPRESSION ||
+         program == TILER_HIP_PROGRAM_CONTRACTION;
 }
 
 }  // namespace
@@ -1948,7 +1952,8 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
   // the kernels apply the declared modes at every arithmetic site (the sums
   // and folds, RMSNorm, softmax, the maps and the expressions, f32 and bf16).
   // Byte moves and the strict-affine decode have no site a mode could reach;
-  // the conversions and the contractions refuse it.
+  // the conversions refuse it.  A contraction under a flushing contract runs
+  // the strict fold, whatever its permissions.
   if (c.flushes() && arithmetic(r->program) && !realizes_modes(r->program))
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED,
                     "a flushing subnormal mode is not realized for this program (the device preserves subnormals)");
@@ -2058,7 +2063,31 @@ static tiler_hip_status plan_region(const tiler_hip_context* ctx, const tiler_hi
                : p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "softmax is an f32 family");
       break;
     case TILER_HIP_PROGRAM_CONTRACTION:
-      if (r->structure)
+      if (c.flushes()) {
+        // A flushing contract: the strict fold with the modes at every site
+        // (contraction.rs:600-625), td,od->to as the structure mk,nk->mn.
+        if (live) {
+          st = p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "live-extent: a flushing contraction's extents are fixed");
+          break;
+        }
+        tiler_hip_contraction_structure mk{};
+        if (!r->structure) {
+          mk.operand_rank[0] = mk.operand_rank[1] = mk.output_rank = 2;
+          mk.operand_indices[0][0] = 0, mk.operand_indices[0][1] = 2;  // m, k
+          mk.operand_indices[1][0] = 1, mk.operand_indices[1][1] = 2;  // n, k
+          mk.output_indices[0] = 0, mk.output_indices[1] = 1;
+          mk.operand_dims[0][0] = e[0], mk.operand_dims[0][1] = e[2];
+          mk.operand_dims[1][0] = e[1], mk.operand_dims[1][1] = e[2];
+          if (e[0] == 0 || e[1] == 0) {  // no outputs: nothing to dispatch (the strict plan's own answer)
+            st = r->dtype == TILER_HIP_F32 ? tiler_rt::plan_contract_strict_f32(t, e[0], e[1], e[2], addr, p, false)
+                                           : tiler_rt::plan_contract_bf16(t, e[0], e[1], e[2], r->variant, addr, p,
+                                                                          true, r->form, false);
+            break;
+          }
+        }
+        st = tiler_rt::plan_contract_general(t, r->dtype, r->structure ? *r->structure : mk, r->variant, true, addr, p,
+                                             c.input_mode, c.result_mode);
+      } else if (r->structure)
         st = live ? p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "live-extent: a structured contraction's extents are fixed")
                   : tiler_rt::plan_contract_general(t, r->dtype, *r->structure, r->variant, !c.reassociate, addr, p);
       else if (r->dtype == TILER_HIP_F32)
