@@ -250,6 +250,50 @@ class Softmax(Workload):
                 "sample": f"{done} rows x {self.extent} in {el:.1f} s, single thread (certified exp)"}
 
 
+class SoftmaxStrict(Workload):
+    """configs[2]'s shape under the strict contract (no PERMITS_REASSOCIATION):
+    the reference's serial exponent sum, bit for bit with softmax.rs:237-315
+    (the rows held in registers, tiler_softmax_f32_strict_rr8_p16), realized
+    through tiler_hip_realize and run through the RuntimeAdapter stages."""
+    name = "softmax_strict"
+    kernel = "tiler_softmax_f32_strict_rr8_p16"
+    rows, extent = 32 * 2048, 2048
+    sets = 2
+
+    def config(self):
+        return {"workload": "softmax f32 [32 x 2048 x 2048] ~N(0,3), last axis, strict contract "
+                            "(serial exponent sum in the reference's order)", "buffer_sets": self.sets}
+
+    def work(self):
+        return self.rows * self.extent * 4 * 2
+
+    def setup(self):
+        from tiler_amd import _lib as L
+        from tiler_amd.realize import prepare_route, realize
+        rz = realize(L.PROGRAM_SOFTMAX, (self.rows, self.extent), flags=L.REGION_ALIGNED16, ctx=self.ctx)
+        if rz.symbols != [self.kernel]:
+            raise RuntimeError(f"strict softmax realized as {rz.symbols}, not {self.kernel}")
+        rng = np.random.default_rng(3)
+        self.plans = []
+        for _ in range(self.sets):
+            x = rng.standard_normal((self.rows, self.extent), dtype=np.float32) * np.float32(3.0)
+            bufs = self._keep(self.ctx.to_device(x), self.ctx.alloc(x.nbytes))
+            self.plans.append(prepare_route(self.ctx, rz, list(bufs)))
+        return self.sets
+
+    def launch(self, i):
+        self.plans[i % self.sets].enqueue()
+
+    def teardown(self):
+        for pl in getattr(self, "plans", []):
+            pl.release()
+        self.plans = []
+        super().teardown()
+
+    def cpu_baseline(self, budget_s):
+        return Softmax(self.ctx).cpu_baseline(budget_s)  # the oracle's softmax is the strict fold
+
+
 class SoftmaxDecode(Workload):
     """Few long rows: f32 [32 heads x 131072 keys] softmax over the keys (the
     shape of decode-attention scores).  16 segments a row, 512 workgroups:
@@ -556,8 +600,8 @@ class Dequantize(Workload):
                 "sample": f"{done} elements of the oracle's dequantization in {el:.1f} s, single thread"}
 
 
-WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, SoftmaxDecode, Gather, Contract, Convert, Expression,
-                                 Dequantize)}
+WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, SoftmaxStrict, SoftmaxDecode, Gather, Contract, Convert,
+                                 Expression, Dequantize)}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_all_families.md")

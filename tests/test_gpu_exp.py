@@ -45,3 +45,28 @@ def test_softmax_on_every_nonpositive_hard_exp_input(ctx):
     rows = np.stack([np.zeros(keep.sum(), np.float32), s[keep]], axis=1)
     got = families.softmax_f32(rows.shape, 1, rows, ctx=ctx).reshape(rows.shape)
     assert np.array_equal(bits(got), bits(oracle.softmax_f32(rows, rows.shape, 1).reshape(rows.shape)))
+
+
+def test_resident_strict_softmax_on_every_nonpositive_hard_exp_input(ctx):
+    """The register-resident strict softmax (tiler_softmax_f32_strict_rr8_p8,
+    which evaluates exp_f32_cr_nonpositive) on rows [0, s_1, ..., s_127]
+    whose s cycle through every hard input s <= 0 (the row's maximum is 0,
+    so each exponent is exp(s) itself), bit for bit with the oracle."""
+    from tiler_amd import _lib as L
+    from tiler_amd.realize import realize, route
+
+    s, _ = _hard()
+    s = s[s <= 0]
+    rows, extent = 2048, 128
+    x = np.zeros((rows, extent), np.float32)
+    x[:, 1:] = np.resize(s, (rows, extent - 1))
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), flags=L.REGION_ALIGNED16, ctx=ctx)
+    assert rz.symbols == ["tiler_softmax_f32_strict_rr8_p8"], rz.symbols
+    bufs = [ctx.to_device(x), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[-1].download(np.float32, x.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    assert np.array_equal(bits(got), bits(oracle.softmax_f32(x, x.shape, 1).reshape(x.shape)))

@@ -385,17 +385,25 @@ def test_strict_softmax_is_the_reference_fold(ctx):
 @pytest.mark.parametrize("rows,extent,form", [
     (16384, 64, "_strict_r16"),    # one partial stage (the oracle's certified exp keeps these small)
     (4500, 530, "_strict_r16_u"),  # 4-byte loads, three stages, a ragged last workgroup
-    (4096, 200, "_strict_r16"),
     (1500, 301, "_strict_r4_u"),   # 4-byte loads, a ragged last stage
     (300, 72, "_strict_r1"),
-    (4096, 512, "_strict_r16"),    # 16-byte loads, whole stages only (the C3 kernel's store path)
     (1024, 2048, "_strict_r4"),    # 16-byte loads, whole stages, four rows per workgroup
+    # rows held in registers, 8 per workgroup (tiler_softmax_f32_strict_rr8_p*)
+    (4096, 200, "_strict_rr8_p8"),   # two chunks, the second partial
+    (4096, 512, "_strict_rr8_p8"),
+    (2050, 1100, "_strict_rr8_p16"),  # a ragged last workgroup, a partial ninth chunk, two ring rounds
+    (2048, 1028, "_strict_rr8_p16"),  # one 4-column group in the ninth chunk
+    (2100, 1024, "_strict_rr8_p8"),   # eight whole chunks, one ring round
+    (3000, 128, "_strict_rr8_p8"),    # one chunk
 ])
 def test_strict_softmax_staged_rows(ctx, rows, extent, form):
-    """Rows of >= 64 run the staged strict softmax (tiler_softmax_f32_strict_r*):
-    the maximum, the exponent sum folded in order, the reciprocal multiply --
-    bit for bit against the oracle.  Row 0 all -inf, row 1 with a NaN, row 2
-    with a +inf, row 3 with -0.0 and +0.0 as its only large values."""
+    """Rows of >= 64 run the staged strict softmax (tiler_softmax_f32_strict_r*)
+    or, for 128..2048 aligned elements and enough rows, the register-resident
+    one (_rr8_p*): the maximum, the exponent sum folded in order, the
+    reciprocal multiply -- bit for bit against the oracle.  Row 0 all -inf,
+    row 1 with a NaN, row 2 with a +inf, row 3 with -0.0 and +0.0 as its only
+    large values; a ragged last workgroup also gets a NaN row and a -inf
+    row."""
     rng = np.random.default_rng(rows * 3 + extent)
     x = (rng.standard_normal((rows, extent)) * 3).astype(np.float32)
     x[0] = -np.inf
@@ -403,6 +411,9 @@ def test_strict_softmax_staged_rows(ctx, rows, extent, form):
     x[2, extent - 1] = np.inf
     x[3] = -np.abs(x[3]) - 1
     x[3, 0], x[3, 1] = -0.0, 0.0
+    if rows % 8:
+        x[rows - 1, extent // 2] = np.nan
+        x[rows - 2] = -np.inf
     flags = L.REGION_ALIGNED16
     rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), flags=flags, ctx=ctx)
     assert rz.symbols[-1].endswith(form), rz.symbols
@@ -431,19 +442,47 @@ def _sampled_rows(rng, rows, per_group, groups_sampled):
     return np.array(sorted(picked))
 
 
+def test_strict_softmax_staged_whole_stages_sampled_rows(ctx):
+    """The staged strict softmax with 16 rows per workgroup, 16-byte loads
+    and whole stages (tiler_softmax_f32_strict_r16, rows past the resident
+    form's 2048 elements): 4096 x 2304, 9 stages of 256 -- every row of the
+    first and last workgroup and one row of every residue mod 16 from 14
+    others, bit for bit with the oracle."""
+    rows, extent = 4096, 2304
+    rng = np.random.default_rng(2304)
+    x = rng.standard_normal((rows, extent), dtype=np.float32) * np.float32(3)
+    sample = _sampled_rows(rng, rows, 16, 16)
+    x[sample[1], 100] = np.nan
+    x[sample[20]] = -np.inf
+    x[sample[-3], extent - 1] = np.inf
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), flags=L.REGION_ALIGNED16, ctx=ctx)
+    assert rz.symbols == ["tiler_softmax_f32_strict_r16"], rz.symbols
+    print(f"[strict softmax staged] {rz.symbols} rows={rows} extent={extent} sampled={len(sample)}", flush=True)
+    bufs = [ctx.to_device(x), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[-1].download(np.float32, x.shape)[sample]
+    finally:
+        for b in bufs:
+            b.free()
+    xs = np.ascontiguousarray(x[sample])
+    want = oracle.softmax_f32(xs, xs.shape, 1).reshape(xs.shape)
+    assert np.array_equal(bits(got), bits(want))
+
+
 def test_strict_softmax_c3_shape_sampled_rows(ctx):
     """The strict softmax at the C3 configuration (f32 [32 x 2048 x 2048],
-    65536 rows of 2048; tiler_softmax_f32_strict_r16, 16 rows per workgroup,
-    16-byte loads, whole stages) routed under the strict contract (no
-    PERMITS_REASSOCIATION) -- 512 rows compared bit for bit with the oracle's
+    65536 rows of 2048; tiler_softmax_f32_strict_rr8_p16, 8 rows per
+    workgroup held in registers) routed under the strict contract (no
+    PERMITS_REASSOCIATION) -- 264 rows compared bit for bit with the oracle's
     softmax_f32 (softmax.rs:237-315): the first and last workgroup whole and
-    one row of every residue mod 16 from 30 other workgroups.  Planted rows:
+    one row of every residue mod 8 from 31 other workgroups.  Planted rows:
     all -inf, a NaN, a +inf, -0.0 and +0.0 as the only large values, and a
     row of one repeated value."""
     rows, extent = 65536, 2048
     rng = np.random.default_rng(65536)
     x = rng.standard_normal((rows, extent), dtype=np.float32) * np.float32(3)
-    sample = _sampled_rows(rng, rows, 16, 32)
+    sample = _sampled_rows(rng, rows, 8, 33)
     planted = {int(sample[0]): "ninf", int(sample[17]): "nan", int(sample[40]): "pinf",
                int(sample[-1]): "zeros", int(sample[-6]): "flat", int(sample[100]): "nan"}
     for r, kind in planted.items():
@@ -459,7 +498,7 @@ def test_strict_softmax_c3_shape_sampled_rows(ctx):
         else:
             x[r] = np.float32(0.75)
     rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), flags=L.REGION_ALIGNED16, ctx=ctx)
-    assert rz.symbols == ["tiler_softmax_f32_strict_r16"], rz.symbols
+    assert rz.symbols == ["tiler_softmax_f32_strict_rr8_p16"], rz.symbols
     print(f"[strict softmax C3] {rz.symbols} rows={rows} extent={extent} sampled={len(sample)}", flush=True)
     bufs = [ctx.to_device(x), ctx.alloc(x.nbytes)]
     try:

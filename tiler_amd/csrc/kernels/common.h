@@ -89,10 +89,13 @@ __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
 
 // IEEE 754-2019 maximum with -0 < +0, NaN-propagating
 // (tiler-reference/src/softmax.rs:168-186).
+// Written as selects, so that a run of maxima compiles to a straight line:
+// for non-NaN operands that compare equal the result is the AND of the
+// encodings (+0 for {-0, +0}, the value itself otherwise), else the larger.
 __device__ __forceinline__ float maximum_f32(float a, float b) {
-  if (a != a || b != b) return __uint_as_float(TILER_CANONICAL_F32_NAN);
-  if (a == b) return __uint_as_float(__float_as_uint(a) & __float_as_uint(b));
-  return a > b ? a : b;
+  const float both = __uint_as_float(__float_as_uint(a) & __float_as_uint(b));
+  const float r = a == b ? both : (a > b ? a : b);
+  return (a != a || b != b) ? __uint_as_float(TILER_CANONICAL_F32_NAN) : r;
 }
 
 // Wave64 xor butterfly: after it every lane holds the same value,
@@ -175,6 +178,33 @@ __device__ __forceinline__ float exp_f32_cr(float s, const double* table = kExp2
   double v = exp_f64_core((double)s, m, table);
   v = __builtin_ldexp(v, m);
   return (float)v;
+}
+
+// exp_f32_cr for an argument s <= 0 or NaN -- the softmax's s = fl(x - m)
+// with m the row's maximum -- as one straight line: the s >= 89 guard cannot
+// fire, s <= -104 selects +0, and a NaN argument stays NaN through the core
+// (a NaN value; its payload aside).  The same core arithmetic as
+// exp_f64_core, with k = rint(fl(s * 64/ln2)) formed by adding and removing
+// 1.5 * 2^52 (round to nearest even at integer granularity, the same value
+// as rint for |k| < 2^51) and read from the sum's low word: for an argument
+// at or below -104 (-inf included) the k read is meaningless but defined,
+// its table index k & 63 in range, and the value is selected away.
+__device__ __forceinline__ float exp_f32_cr_nonpositive(float s, const double* table = kExp2Table64) {
+  const double x = (double)s;
+  const double shifted = x * TILER_64_OVER_LN2 + 0x1.8p52;
+  const double kd = shifted - 0x1.8p52;
+  const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, shifted);
+  double r = __builtin_fma(-kd, TILER_LN2_OVER_64_HI, x);
+  r = __builtin_fma(-kd, TILER_LN2_OVER_64_LO, r);
+  double p = 1.0 / 720.0;
+  p = __builtin_fma(p, r, 1.0 / 120.0);
+  p = __builtin_fma(p, r, 1.0 / 24.0);
+  p = __builtin_fma(p, r, 1.0 / 6.0);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const float e = (float)__builtin_ldexp(table[k & 63] * p, k >> 6);
+  return s <= -104.0f ? 0.0f : e;
 }
 
 // Reference SiLU, tiler-reference/src/silu.rs:511-533: x / fl(1 + exp(-x)),

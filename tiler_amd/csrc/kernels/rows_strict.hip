@@ -479,7 +479,135 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
   }
 }
 
+// Strict softmax with a workgroup's rows resident in registers, for rows of
+// at most 128 P elements (extent a multiple of 4, 16-byte aligned rows):
+// R rows per workgroup of 32 R threads, half a wave per row; lane l of a
+// row holds the row's elements 4 (l + 32 j) .. +3 for j < P as P float4
+// pieces.  x is read once and y written once (softmax.rs:237-315):
+// * the maximum: each lane's pieces, then a butterfly over the row's 32
+//   lanes;
+// * the exponents e = certified exp(fl(x - m)), in place in the registers;
+// * the fold: the exponents pass through an LDS ring in 128-column chunks,
+//   laid out so that lane r of one wave reads row r's elements in ascending
+//   order 16 bytes at a time, and those R lanes fold their rows from -0.0
+//   (an exponent is never -0.0, so -0.0 plus the first is the first): one
+//   wave instruction advances R rows' chains;
+// * y = fl(e * fl(1 / d)) from the registers: the reciprocal, then a
+//   multiply (softmax.rs:302-313), canonical NaN where the row's d is NaN.
+// Three steps take the short form because the row's values cannot tell:
+// * the maximum is the hardware one (v_max_f32) instead of the IEEE
+//   maximum: on a row without NaN both are the largest element, up to the
+//   sign of a zero maximum, and fl(x - (+0)) and fl(x - (-0)) differ only
+//   for x = -0, as -0 and +0, whose exponents are both 1; a row with a NaN
+//   gets e = NaN at that element whatever m is, so d = NaN and every output
+//   is the canonical NaN, as under the reference's NaN maximum;
+// * the exponent is exp_f32_cr_nonpositive, since s = fl(x - m) <= 0 or NaN;
+// * the output's NaN test is the row's: an e is NaN only where d is, and
+//   e <= 1 <= d, so a product e * fl(1 / d) is NaN exactly when d is.
+template <int R, int P>
+__device__ __forceinline__ void softmax_strict_resident_body(const float* __restrict__ x, float* __restrict__ y,
+                                                             uint64_t rows, uint32_t extent) {
+  constexpr int Q = 8;                      // ring chunks: the fold runs once per Q chunks
+  constexpr uint32_t kGroup = R + 1;        // float4 slots per 4-column group (a pad slot: no bank aliasing)
+  constexpr uint32_t kChunk = 32 * kGroup;  // float4 slots per 128-column chunk
+  __shared__ f32x4 ring[Q * kChunk];
+  __shared__ float recip[R];
+  __shared__ double tab[64];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t r = wave * 2u + (lane >> 5), l = lane & 31u;
+  if (t < 64) tab[t] = kExp2Table64[t];
+  const uint64_t row0 = (uint64_t)blockIdx.x * R;
+  const bool row_ok = row0 + r < rows;
+  const float* xr = x + (row0 + r) * extent;
+  const float ninf = -__builtin_huge_valf();
+  f32x4 v[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const uint32_t e = 4u * (l + 32u * j);
+    v[j] = row_ok && e < extent ? *reinterpret_cast<const f32x4*>(xr + e) : f32x4{ninf, ninf, ninf, ninf};
+  }
+  float m = ninf;
+#pragma unroll
+  for (int j = 0; j < P; ++j)
+    m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fmaxf(v[j].x, v[j].y)), __builtin_fmaxf(v[j].z, v[j].w));
+#pragma unroll
+  for (uint32_t o = 16; o >= 1; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 64));
+  __syncthreads();  // the exponent table
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    v[j].x = tiler::exp_f32_cr_nonpositive(v[j].x - m, tab);
+    v[j].y = tiler::exp_f32_cr_nonpositive(v[j].y - m, tab);
+    v[j].z = tiler::exp_f32_cr_nonpositive(v[j].z - m, tab);
+    v[j].w = tiler::exp_f32_cr_nonpositive(v[j].w - m, tab);
+  }
+  // Lane f < R of wave 0 folds row f.  Slots past the row's end hold the
+  // -inf fill's values and are never folded.
+  const bool folds = wave == 0 && lane < (uint32_t)R && row0 + lane < rows;
+  float acc = -0.0f;
+#pragma unroll
+  for (int c0 = 0; c0 < P; c0 += Q) {
+    if ((uint32_t)c0 * 128u >= extent) break;
+#pragma unroll
+    for (int q = 0; q < Q && c0 + q < P; ++q) ring[q * kChunk + l * kGroup + r] = v[c0 + q];
+    __syncthreads();
+    if (folds) {
+      for (int q = 0; q < Q && c0 + q < P; ++q) {
+        const uint32_t start = (uint32_t)(c0 + q) * 128u;
+        if (start >= extent) break;
+        const uint32_t groups = extent - start >= 128u ? 32u : (extent - start) / 4u;
+        const f32x4* g = ring + q * kChunk + lane;
+        uint32_t i = 0;
+        for (; i + 8 <= groups; i += 8) {
+          f32x4 e[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) e[u] = g[(i + u) * kGroup];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            acc = acc + e[u].x;
+            acc = acc + e[u].y;
+            acc = acc + e[u].z;
+            acc = acc + e[u].w;
+          }
+        }
+        for (; i < groups; ++i) {
+          const f32x4 e = g[i * kGroup];
+          acc = acc + e.x;
+          acc = acc + e.y;
+          acc = acc + e.z;
+          acc = acc + e.w;
+        }
+      }
+    }
+    __syncthreads();  // the ring is refilled next
+  }
+  if (folds) recip[lane] = 1.0f / acc;
+  __syncthreads();
+  if (!row_ok) return;
+  const float rc = recip[r];
+  const bool nan_row = rc != rc;
+  const float qnan = __uint_as_float(TILER_CANONICAL_F32_NAN);
+  float* yr = y + (row0 + r) * extent;
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const uint32_t e = 4u * (l + 32u * j);
+    if (e < extent) {
+      const f32x4 o = {nan_row ? qnan : v[j].x * rc, nan_row ? qnan : v[j].y * rc, nan_row ? qnan : v[j].z * rc,
+                       nan_row ? qnan : v[j].w * rc};
+      __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + e));
+    }
+  }
+}
+
 }  // namespace
+
+#define TILER_SOFTMAX_STRICT_RESIDENT(R, P)                                                           \
+  extern "C" __global__ void __launch_bounds__(32 * R)                                                \
+      tiler_softmax_f32_strict_rr##R##_p##P(const float* __restrict__ x, float* __restrict__ y,       \
+                                            uint64_t rows, uint32_t extent) {                         \
+    softmax_strict_resident_body<R, P>(x, y, rows, extent);                                           \
+  }
+TILER_SOFTMAX_STRICT_RESIDENT(8, 16)
+TILER_SOFTMAX_STRICT_RESIDENT(8, 8)
 
 #define TILER_SOFTMAX_STRICT_STAGED(R)                                                                \
   extern "C" __global__ void __launch_bounds__(256)                                                   \

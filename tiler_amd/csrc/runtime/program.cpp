@@ -392,18 +392,28 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
   if (extent > 0xffffffffull)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
   if (strict && extent >= 64 && extent <= 0xffffffffull && !modes) {
-    // The reference's serial exponent sum, staged: R rows per workgroup as
-    // for the strict RMSNorm but at most 16 (stages of at least 256
-    // elements, so a stage's fold covers the next stage's loads; 64 rows of
-    // 64-element stages ran the 65536 x 2048 case in 611 us, 16 in 524 on the
-    // same build), three streamed passes (maximum, exponents folded in order,
-    // output).
+    // The reference's serial exponent sum.
     const uint64_t cus = t.compute_units;
+    const bool vec = aligned16(addr[x]) && aligned16(addr[y]) && extent % 4 == 0;
+    char sname[48];
+    if (vec && extent >= 128 && extent <= 2048 && rows >= 8 * cus) {
+      // Rows of at most 2048 held in registers, 8 per workgroup: x read once
+      // and y written once, the fold 8 rows per wave instruction (the
+      // 65536 x 2048 case: 0.50 ms staged, ~0.22 ms resident).
+      if ((rows + 7) / 8 > 0x7fffffffull)
+        return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+      std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_rr8_p%u", extent <= 1024 ? 8u : 16u);
+      p.add(sname, (uint32_t)((rows + 7) / 8), 1, 256).ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
+      return TILER_HIP_OK;
+    }
+    // Otherwise staged: R rows per workgroup as for the strict RMSNorm but
+    // at most 16 (stages of at least 256 elements, so a stage's fold covers
+    // the next stage's loads; 64 rows of 64-element stages ran the
+    // 65536 x 2048 case in 611 us, 16 in 524 on the same build), three
+    // streamed passes (maximum, exponents folded in order, output).
     const uint32_t R = rows >= 16 * cus ? 16 : rows >= 4 * cus ? 4 : 1;
     if ((rows + R - 1) / R > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-    const bool vec = aligned16(addr[x]) && aligned16(addr[y]) && extent % 4 == 0;
-    char sname[48];
     std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_r%u%s", R, vec ? "" : "_u");
     p.add(sname, (uint32_t)((rows + R - 1) / R), 1, 256).ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
     return TILER_HIP_OK;

@@ -241,6 +241,8 @@ const EntryRow kEntries[] = {
     {"tiler_softmax_f32_strict_r4_u", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_r16", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_r16_u", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_rr8_p16", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_rr8_p8", "softmax-f32/strict", 2},
     {"tiler_fold_sum_f32", "strict-serial-sum-f32/serial-any-axes", 3},
     {"tiler_fold_squared_f32", "squared-serial-sum-f32/serial", 3},
     {"tiler_fold_fma_f32", "fused-multiply-add-serial-sum-f32/serial", 3},
