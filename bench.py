@@ -152,6 +152,41 @@ class RmsNorm(Workload):
                                   "sample": f"{single} rows in {single_s:.1f} s"}}
 
 
+class RmsNormStrict(RmsNorm):
+    """configs[1] under the strict contract (no PERMITS_REASSOCIATION): the
+    reference's serial fold of the squares, bit for bit with
+    rms_norm.rs:134-195 on the exactly widened values (the rows held in
+    registers, tiler_rms_norm_bf16_strict_rr8_p16), realized through
+    tiler_hip_realize and run through the RuntimeAdapter stages."""
+    name = "rms_norm_strict"
+    kernel = "tiler_rms_norm_bf16_strict_rr8_p16"
+
+    def config(self):
+        c = super().config()
+        c["workload"] += ", strict contract (serial fold of the squares in the reference's order)"
+        return c
+
+    def setup(self):
+        from tiler_amd import _lib as L
+        from tiler_amd.realize import prepare_route, realize
+        n = super().setup()
+        rz = realize(L.PROGRAM_RMS_NORM, (self.rows, self.extent), dtype=L.BF16, scalars=(EPS_BITS,),
+                     flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=self.ctx)
+        if rz.symbols != [self.kernel]:
+            raise RuntimeError(f"strict rms_norm realized as {rz.symbols}, not {self.kernel}")
+        self.plans = [prepare_route(self.ctx, rz, [x, self.w, y]) for x, y in self.sets_]
+        return n
+
+    def launch(self, i):
+        self.plans[i % len(self.plans)].enqueue()
+
+    def teardown(self):
+        for pl in getattr(self, "plans", []):
+            pl.release()
+        self.plans = []
+        super().teardown()
+
+
 class Sum(Workload):
     """f32[2^24] -> scalar, the two-level tree."""
     name = "sum"
@@ -600,8 +635,8 @@ class Dequantize(Workload):
                 "sample": f"{done} elements of the oracle's dequantization in {el:.1f} s, single thread"}
 
 
-WORKLOADS = {w.name: w for w in (RmsNorm, Sum, Softmax, SoftmaxStrict, SoftmaxDecode, Gather, Contract, Convert,
-                                 Expression, Dequantize)}
+WORKLOADS = {w.name: w for w in (RmsNorm, RmsNormStrict, Sum, Softmax, SoftmaxStrict, SoftmaxDecode, Gather,
+                                 Contract, Convert, Expression, Dequantize)}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_all_families.md")

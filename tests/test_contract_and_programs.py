@@ -66,8 +66,14 @@ def test_reassociating_sums_need_the_permission(topology, grouping):
 def test_strict_contract_selects_the_serial_row_and_contraction_kernels():
     s = realize(L.PROGRAM_RMS_NORM, (8192, 4096), dtype=L.BF16, scalars=(EPS,),
                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST)
-    # rows of >= 64: staged, 16 rows per workgroup at 8192 rows (512 workgroups on 256 CUs)
-    assert s.symbols == ["tiler_rms_norm_bf16_strict_r16"] and s.dispatches[0].grid == (512, 1, 1)
+    # aligned rows of at most 512 16-byte pieces, enough of them: held in registers, 8 per workgroup
+    assert s.symbols == ["tiler_rms_norm_bf16_strict_rr8_p16"] and s.dispatches[0].grid == (1024, 1, 1)
+    assert realize(L.PROGRAM_RMS_NORM, (8192, 2048), scalars=(EPS,), flags=L.REGION_ALIGNED16).symbols == \
+        ["tiler_rms_norm_f32_strict_rr8_p16"]
+    # rows of >= 64 otherwise: staged, 16 rows per workgroup at 8192 rows (512 workgroups on 256 CUs)
+    st = realize(L.PROGRAM_RMS_NORM, (8192, 4104), dtype=L.BF16, scalars=(EPS,),
+                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST)
+    assert st.symbols == ["tiler_rms_norm_bf16_strict_r16"] and st.dispatches[0].grid == (512, 1, 1)
     assert realize(L.PROGRAM_RMS_NORM, (5, 20000), scalars=(EPS,)).symbols == ["tiler_rms_norm_f32_strict_r1"]
     assert realize(L.PROGRAM_RMS_NORM, (5, 40), scalars=(EPS,)).symbols == ["tiler_rms_norm_f32_strict"]
     assert realize(L.PROGRAM_SOFTMAX, (32, 131072)).symbols == ["tiler_softmax_f32_strict_r1"]

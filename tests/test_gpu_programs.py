@@ -328,23 +328,34 @@ def test_strict_rms_norm_is_the_reference_fold(ctx):
 
 
 @pytest.mark.parametrize("rows,extent,dtype,broadcast,form", [
-    (8192, 4096, L.BF16, True, "_strict_r16"),  # the C2 configuration
+    (4096, 4104, L.BF16, True, "_strict_r16"),  # 16-byte loads, staged (rows past 4096 bf16)
     (1500, 300, L.F32, True, "_strict_r4"),
     (20000, 64, L.BF16, True, "_strict_r64"),   # one stage
     (700, 1001, L.F32, False, "_strict_r1_u"),  # 4-byte loads, a weight row per row, a ragged stage
     (300, 1030, L.BF16, True, "_strict_r1_u"),
+    # rows held in registers, 8 per workgroup (tiler_rms_norm_*_strict_rr8_p*)
+    (8192, 4096, L.BF16, True, "_strict_rr8_p16"),   # the C2 configuration
+    (2050, 1100, L.F32, False, "_strict_rr8_p16"),   # a weight row per row, a ragged last workgroup, a partial chunk
+    (2048, 1000, L.BF16, True, "_strict_rr8_p8"),    # a partial fourth chunk, one ring round
+    (2100, 2048, L.BF16, False, "_strict_rr8_p8"),   # two whole ring rounds
+    (3000, 64, L.F32, True, "_strict_rr8_p8"),       # one partial chunk
 ])
 def test_strict_rms_norm_staged_rows(ctx, rows, extent, dtype, broadcast, form):
-    """Rows of >= 64 run the staged strict fold (tiler_rms_norm_*_strict_r*):
-    the reference's serial fold of the squares, then its division, eps and
-    certified rsqrt, bit for bit against the oracle (bf16: on exactly widened
-    values, one narrowing).  Row 0 is all zeros (0 / N + eps), row 1 holds a
-    NaN and row 2 an infinity."""
+    """Rows of >= 64 run the staged strict fold (tiler_rms_norm_*_strict_r*)
+    or, for aligned rows of at most 512 16-byte pieces and enough of them,
+    the register-resident one (_rr8_p*): the reference's serial fold of the
+    squares, then its division, eps and certified rsqrt, bit for bit against
+    the oracle (bf16: on exactly widened values, one narrowing).  Row 0 is all
+    zeros (0 / N + eps), row 1 holds a NaN and row 2 an infinity; a ragged
+    last workgroup also gets a NaN row and a zero row."""
     rng = np.random.default_rng(rows + extent)
     x = rng.standard_normal((rows, extent)).astype(np.float32) * np.float32(3.0)
     x[0] = 0.0
     x[1, extent // 2] = np.nan
     x[2, 0] = np.inf
+    if rows % 8:
+        x[rows - 1, extent - 1] = np.nan
+        x[rows - 2] = 0.0
     w = rng.normal(1.0, 0.1, extent if broadcast else (rows, extent)).astype(np.float32)
     if dtype == L.BF16:
         x, w = oracle.bf16_narrow(x).reshape(x.shape), oracle.bf16_narrow(w).reshape(w.shape)

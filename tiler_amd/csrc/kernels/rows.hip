@@ -235,7 +235,7 @@ __device__ __forceinline__ void softmax_f32_finish(f32x4 (&xv)[CH], float m, flo
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       bool live = (uint32_t)c < nfull || p0 + e < extent;
-      float ex = tiler::exp_f32_cr(v4[e] - m, exp_table);
+      float ex = tiler::exp_f32_cr_nonpositive(v4[e] - m, exp_table);  // m is the IEEE maximum: x - m <= 0 or NaN
       v4[e] = ex;
       if (live) acc = acc + ex;
     }

@@ -229,9 +229,11 @@ __device__ __forceinline__ float max_chunk(float m, f32x4 v) {
   return tiler::maximum_f32(m, v.w);
 }
 
+// m is the row's IEEE maximum, so fl(x - m) <= 0 or NaN for every element of
+// the row (a padding lane's value past the row's end is never used).
 __device__ __forceinline__ f32x4 exp_chunk(f32x4 v, float m, const double* tab) {
-  return f32x4{tiler::exp_f32_cr(v.x - m, tab), tiler::exp_f32_cr(v.y - m, tab),
-               tiler::exp_f32_cr(v.z - m, tab), tiler::exp_f32_cr(v.w - m, tab)};
+  return f32x4{tiler::exp_f32_cr_nonpositive(v.x - m, tab), tiler::exp_f32_cr_nonpositive(v.y - m, tab),
+               tiler::exp_f32_cr_nonpositive(v.z - m, tab), tiler::exp_f32_cr_nonpositive(v.w - m, tab)};
 }
 
 __device__ __forceinline__ float fold_chunk(float acc, f32x4 e, uint64_t q, uint32_t extent) {

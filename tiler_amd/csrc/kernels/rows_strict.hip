@@ -479,6 +479,136 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
   }
 }
 
+// Strict RMSNorm with a workgroup's rows resident in registers, for rows of
+// at most 32 P E elements (E = 8 bf16 or 4 f32 per 16-byte piece; extent a
+// multiple of E, 16-byte aligned rows and weight): R rows per workgroup of
+// 32 R threads, half a wave per row; lane l of a row holds the row's
+// elements E (l + 32 j) .. +E-1 for j < P.  x is read once and y written
+// once (rms_norm.rs:134-195, 453-489):
+// * the squares fl(x * x) of the exactly widened elements go through an LDS
+//   ring in 32 E-column chunks, laid out so that lane r of wave 0 reads row
+//   r's squares in ascending order, and those R lanes fold their rows from
+//   -0.0 (a square is never -0.0, so -0.0 plus the first square is the
+//   first square): one wave instruction advances R rows' chains;
+// * per row the division by N, + eps and the certified rsqrt
+//   (rms_norm.rs:177-187);
+// * y = canon(fl(w * fl(x * s))) from the registers, weight after the
+//   normalization (rms_norm.rs:474-485), narrowed once for bf16.
+template <typename T, int R, int P>
+__device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x, const T* __restrict__ w,
+                                                         uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,
+                                                         uint32_t extent, float eps) {
+  constexpr bool kBf16 = sizeof(T) == 2;
+  constexpr uint32_t E = 16 / sizeof(T);    // elements per piece
+  constexpr uint32_t F4 = E / 4;            // float4 slots of squares per piece
+  constexpr int Q = kBf16 ? 4 : 8;          // ring chunks per fold round
+  constexpr uint32_t kGroup = R * F4 + 1;   // float4 slots per piece column (a pad slot: no bank aliasing)
+  constexpr uint32_t kChunk = 32 * kGroup;  // float4 slots per chunk
+  __shared__ f32x4 ring[Q * kChunk];
+  __shared__ float scale[R];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t r = wave * 2u + (lane >> 5), l = lane & 31u;
+  const uint64_t row0 = (uint64_t)blockIdx.x * R;
+  const bool row_ok = row0 + r < rows;
+  const T* xr = x + (row0 + r) * extent;
+  auto widen = [](uint32_t bits) -> float {
+    if constexpr (kBf16) return tiler::bf16_widen(bits);
+    else return __uint_as_float(bits);
+  };
+  u32x4 v[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const uint32_t e = E * (l + 32u * j);
+    v[j] = row_ok && e < extent ? *reinterpret_cast<const u32x4*>(xr + e) : u32x4{0, 0, 0, 0};
+  }
+  const bool folds = wave == 0 && lane < (uint32_t)R && row0 + lane < rows;
+  float acc = -0.0f;
+  constexpr uint32_t kChunkElems = 32 * E;
+#pragma unroll
+  for (int c0 = 0; c0 < P; c0 += Q) {
+    if ((uint32_t)c0 * kChunkElems >= extent) break;
+#pragma unroll
+    for (int q = 0; q < Q && c0 + q < P; ++q) {
+      const u32x4 u = v[c0 + q];
+      f32x4* dst = ring + q * kChunk + l * kGroup + r * F4;
+      if constexpr (kBf16) {
+        f32x4 lo, hi;
+        lo.x = widen(u.x & 0xffffu); lo.y = widen(u.x >> 16); lo.z = widen(u.y & 0xffffu); lo.w = widen(u.y >> 16);
+        hi.x = widen(u.z & 0xffffu); hi.y = widen(u.z >> 16); hi.z = widen(u.w & 0xffffu); hi.w = widen(u.w >> 16);
+        dst[0] = lo * lo;
+        dst[1] = hi * hi;
+      } else {
+        f32x4 a;
+        a.x = widen(u.x); a.y = widen(u.y); a.z = widen(u.z); a.w = widen(u.w);
+        dst[0] = a * a;
+      }
+    }
+    __syncthreads();
+    if (folds) {
+      for (int q = 0; q < Q && c0 + q < P; ++q) {
+        const uint32_t start = (uint32_t)(c0 + q) * kChunkElems;
+        if (start >= extent) break;
+        const uint32_t slots = (extent - start >= kChunkElems ? kChunkElems : extent - start) / 4u;
+        const f32x4* g = ring + q * kChunk + lane * F4;
+        uint32_t i = 0;
+        for (; i + 8 <= slots; i += 8) {
+          f32x4 e[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) e[u] = g[((i + u) / F4) * kGroup + (i + u) % F4];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            acc = acc + e[u].x;
+            acc = acc + e[u].y;
+            acc = acc + e[u].z;
+            acc = acc + e[u].w;
+          }
+        }
+        for (; i < slots; ++i) {
+          const f32x4 e = g[(i / F4) * kGroup + i % F4];
+          acc = acc + e.x;
+          acc = acc + e.y;
+          acc = acc + e.z;
+          acc = acc + e.w;
+        }
+      }
+    }
+    __syncthreads();  // the ring is refilled next
+  }
+  if (folds) scale[lane] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
+  __syncthreads();
+  if (!row_ok) return;
+  const float sc = scale[r];
+  const T* wr = w + (row0 + r) * w_row_stride;
+  T* yr = y + (row0 + r) * extent;
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const uint32_t e = E * (l + 32u * j);
+    if (e < extent) {
+      const u32x4 xv = v[j];
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + e);
+      u32x4 out;
+      if constexpr (kBf16) {
+        auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
+          return tiler::bf16_narrow(tiler::canon(widen(wb) * (widen(xb) * sc)));
+        };
+        out.x = one(xv.x & 0xffffu, wv.x & 0xffffu) | (one(xv.x >> 16, wv.x >> 16) << 16);
+        out.y = one(xv.y & 0xffffu, wv.y & 0xffffu) | (one(xv.y >> 16, wv.y >> 16) << 16);
+        out.z = one(xv.z & 0xffffu, wv.z & 0xffffu) | (one(xv.z >> 16, wv.z >> 16) << 16);
+        out.w = one(xv.w & 0xffffu, wv.w & 0xffffu) | (one(xv.w >> 16, wv.w >> 16) << 16);
+      } else {
+        auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
+          return __float_as_uint(tiler::canon(widen(wb) * (widen(xb) * sc)));
+        };
+        out.x = one(xv.x, wv.x);
+        out.y = one(xv.y, wv.y);
+        out.z = one(xv.z, wv.z);
+        out.w = one(xv.w, wv.w);
+      }
+      __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(yr + e));
+    }
+  }
+}
+
 // Strict softmax with a workgroup's rows resident in registers, for rows of
 // at most 128 P elements (extent a multiple of 4, 16-byte aligned rows):
 // R rows per workgroup of 32 R threads, half a wave per row; lane l of a
@@ -608,6 +738,18 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
   }
 TILER_SOFTMAX_STRICT_RESIDENT(8, 16)
 TILER_SOFTMAX_STRICT_RESIDENT(8, 8)
+
+#define TILER_RMS_STRICT_RESIDENT(TY, T, R, P)                                                        \
+  extern "C" __global__ void __launch_bounds__(32 * R)                                                \
+      tiler_rms_norm_##TY##_strict_rr##R##_p##P(const T* __restrict__ x, const T* __restrict__ w,     \
+                                                uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,\
+                                                uint32_t extent, float eps) {                         \
+    rms_strict_resident_body<T, R, P>(x, w, w_row_stride, y, rows, extent, eps);                      \
+  }
+TILER_RMS_STRICT_RESIDENT(bf16, uint16_t, 8, 16)
+TILER_RMS_STRICT_RESIDENT(bf16, uint16_t, 8, 8)
+TILER_RMS_STRICT_RESIDENT(f32, float, 8, 16)
+TILER_RMS_STRICT_RESIDENT(f32, float, 8, 8)
 
 #define TILER_SOFTMAX_STRICT_STAGED(R)                                                                \
   extern "C" __global__ void __launch_bounds__(256)                                                   \

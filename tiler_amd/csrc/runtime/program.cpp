@@ -316,10 +316,22 @@ tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_b
   const uint64_t wstride = weight_broadcast ? 0 : extent;
   char name[64];
   if (strict && extent >= 64 && !modes) {
-    // The reference's serial fold of the squares, staged: R rows per
-    // workgroup, the largest of 64, 16, 4 that still gives every CU a
-    // workgroup (else 1), a folding lane per row.
     const uint64_t cus = t.compute_units;
+    const uint64_t per16 = 16 / elem;  // elements per 16-byte piece
+    if (al && extent % per16 == 0 && extent >= 16 * per16 && extent <= 512 * per16 && rows >= 8 * cus) {
+      // Rows of at most 512 pieces held in registers, 8 per workgroup: x
+      // read once, y written once, the fold of the squares 8 rows per wave
+      // instruction.
+      if ((rows + 7) / 8 > 0x7fffffffull)
+        return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+      std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict_rr8_p%u", ty, extent <= 256 * per16 ? 8u : 16u);
+      p.add(name, (uint32_t)((rows + 7) / 8), 1, 256)
+          .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps);
+      return TILER_HIP_OK;
+    }
+    // Otherwise the reference's serial fold of the squares, staged: R rows
+    // per workgroup, the largest of 64, 16, 4 that still gives every CU a
+    // workgroup (else 1), a folding lane per row.
     const uint32_t R = rows >= 64 * cus ? 64 : rows >= 16 * cus ? 16 : rows >= 4 * cus ? 4 : 1;
     if ((rows + R - 1) / R > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");

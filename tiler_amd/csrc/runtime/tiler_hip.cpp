@@ -234,6 +234,10 @@ const EntryRow kEntries[] = {
     {"tiler_rms_norm_bf16_strict_r16_u", "rms-norm/bf16/strict", 3},
     {"tiler_rms_norm_bf16_strict_r64", "rms-norm/bf16/strict", 3},
     {"tiler_rms_norm_bf16_strict_r64_u", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_f32_strict_rr8_p8", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_rr8_p16", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_bf16_strict_rr8_p8", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_rr8_p16", "rms-norm/bf16/strict", 3},
     {"tiler_softmax_f32_strict", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_r1", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_r1_u", "softmax-f32/strict", 2},
