@@ -479,17 +479,87 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
   }
 }
 
+// A folding lane's pass over one round of the resident kernels' LDS ring:
+// folds `count` float4 slots (4 contributors each) in ascending order onto
+// acc, slot n at base[(n / kPerChunk) * kChunk + ((n % kPerChunk) / F4) *
+// kGroup + n % F4], with two batches of B slots in flight: the next batch's
+// LDS reads are issued before the current batch's adds, so the dependent
+// adds do not wait on LDS latency.  A batch never straddles a chunk (B
+// divides kPerChunk), so its reads are one pointer plus constant offsets;
+// B = 4 keeps the two batches within the registers the rows leave free.
+template <uint32_t kPerChunk, uint32_t F4, uint32_t kGroup, uint32_t kChunk, uint32_t B = 4>
+__device__ __forceinline__ float fold_ring_round(const f32x4* base, uint32_t count, float acc) {
+  static_assert(kPerChunk % B == 0 && B % F4 == 0, "a batch lies inside one chunk");
+  const f32x4* p = base;
+  uint32_t in_chunk = 0;  // slots of the current chunk already read
+  auto read = [&](f32x4 (&e)[B]) {
+#pragma unroll
+    for (uint32_t u = 0; u < B; ++u) e[u] = p[(u / F4) * kGroup + u % F4];
+    p += (B / F4) * kGroup;
+    in_chunk += B;
+    if (in_chunk == kPerChunk) {
+      p += kChunk - (kPerChunk / F4) * kGroup;
+      in_chunk = 0;
+    }
+  };
+  auto add = [&](const f32x4 (&e)[B]) {
+#pragma unroll
+    for (uint32_t u = 0; u < B; ++u) {
+      acc = acc + e[u].x;
+      acc = acc + e[u].y;
+      acc = acc + e[u].z;
+      acc = acc + e[u].w;
+    }
+  };
+  // Batches k (in a) and k + 1 (in b) with k + 2 read ahead: the steady
+  // state has no branch, so the LDS wait before each batch's adds counts
+  // only that batch's reads.
+  const uint32_t batches = count / B;
+  f32x4 a[B], b[B];
+  if (batches) read(a);
+  uint32_t k = 0;
+  for (; k + 2 < batches; k += 2) {  // sched_barrier: the compiler would otherwise sink each read to its use
+    read(b);
+    __builtin_amdgcn_sched_barrier(0);
+    add(a);
+    __builtin_amdgcn_sched_barrier(0);
+    read(a);
+    __builtin_amdgcn_sched_barrier(0);
+    add(b);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (k + 1 < batches) {
+    read(b);
+    add(a);
+    add(b);
+  } else if (k < batches) {
+    add(a);
+  }
+  // The last few slots, inside the chunk p is in (a chunk holds a whole
+  // number of batches): slot t past p at p[(t / F4) * kGroup + t % F4].
+  for (uint32_t t = 0; t < count - batches * B; ++t) {
+    const f32x4 e = p[(t / F4) * kGroup + t % F4];
+    acc = acc + e.x;
+    acc = acc + e.y;
+    acc = acc + e.z;
+    acc = acc + e.w;
+  }
+  return acc;
+}
+
 // Strict RMSNorm with a workgroup's rows resident in registers, for rows of
 // at most 32 P E elements (E = 8 bf16 or 4 f32 per 16-byte piece; extent a
 // multiple of E, 16-byte aligned rows and weight): R rows per workgroup of
 // 32 R threads, half a wave per row; lane l of a row holds the row's
 // elements E (l + 32 j) .. +E-1 for j < P.  x is read once and y written
 // once (rms_norm.rs:134-195, 453-489):
-// * the squares fl(x * x) of the exactly widened elements go through an LDS
-//   ring in 32 E-column chunks, laid out so that lane r of wave 0 reads row
-//   r's squares in ascending order, and those R lanes fold their rows from
-//   -0.0 (a square is never -0.0, so -0.0 plus the first square is the
-//   first square): one wave instruction advances R rows' chains;
+// * the squares fl(x * x) of the exactly widened elements go through a
+//   two-chunk LDS ring, chunk j (32 E columns) as soon as piece j of every
+//   lane has landed, laid out so that lane r of wave 0 reads row r's squares
+//   in ascending order; those R lanes fold chunk j while chunk j + 1 is
+//   written, from -0.0 (a square is never -0.0, so -0.0 plus the first square
+//   is the first square): the serial fold runs while the row is still
+//   arriving, one wave instruction advancing R rows' chains;
 // * per row the division by N, + eps and the certified rsqrt
 //   (rms_norm.rs:177-187);
 // * y = canon(fl(w * fl(x * s))) from the registers, weight after the
@@ -501,10 +571,9 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
   constexpr bool kBf16 = sizeof(T) == 2;
   constexpr uint32_t E = 16 / sizeof(T);    // elements per piece
   constexpr uint32_t F4 = E / 4;            // float4 slots of squares per piece
-  constexpr int Q = kBf16 ? 4 : 8;          // ring chunks per fold round
   constexpr uint32_t kGroup = R * F4 + 1;   // float4 slots per piece column (a pad slot: no bank aliasing)
   constexpr uint32_t kChunk = 32 * kGroup;  // float4 slots per chunk
-  __shared__ f32x4 ring[Q * kChunk];
+  __shared__ f32x4 ring[2 * kChunk];
   __shared__ float scale[R];
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t r = wave * 2u + (lane >> 5), l = lane & 31u;
@@ -524,55 +593,31 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
   const bool folds = wave == 0 && lane < (uint32_t)R && row0 + lane < rows;
   float acc = -0.0f;
   constexpr uint32_t kChunkElems = 32 * E;
+  // Chunk j into ring half j & 1, one barrier per chunk: half j & 1 was last
+  // read by the fold of chunk j - 2, which ended before its folding lanes
+  // reached the barrier of chunk j - 1.
 #pragma unroll
-  for (int c0 = 0; c0 < P; c0 += Q) {
-    if ((uint32_t)c0 * kChunkElems >= extent) break;
-#pragma unroll
-    for (int q = 0; q < Q && c0 + q < P; ++q) {
-      const u32x4 u = v[c0 + q];
-      f32x4* dst = ring + q * kChunk + l * kGroup + r * F4;
-      if constexpr (kBf16) {
-        f32x4 lo, hi;
-        lo.x = widen(u.x & 0xffffu); lo.y = widen(u.x >> 16); lo.z = widen(u.y & 0xffffu); lo.w = widen(u.y >> 16);
-        hi.x = widen(u.z & 0xffffu); hi.y = widen(u.z >> 16); hi.z = widen(u.w & 0xffffu); hi.w = widen(u.w >> 16);
-        dst[0] = lo * lo;
-        dst[1] = hi * hi;
-      } else {
-        f32x4 a;
-        a.x = widen(u.x); a.y = widen(u.y); a.z = widen(u.z); a.w = widen(u.w);
-        dst[0] = a * a;
-      }
+  for (int j = 0; j < P; ++j) {
+    if ((uint32_t)j * kChunkElems >= extent) break;
+    const u32x4 u = v[j];
+    f32x4* dst = ring + (j & 1) * kChunk + l * kGroup + r * F4;
+    if constexpr (kBf16) {
+      f32x4 lo, hi;
+      lo.x = widen(u.x & 0xffffu); lo.y = widen(u.x >> 16); lo.z = widen(u.y & 0xffffu); lo.w = widen(u.y >> 16);
+      hi.x = widen(u.z & 0xffffu); hi.y = widen(u.z >> 16); hi.z = widen(u.w & 0xffffu); hi.w = widen(u.w >> 16);
+      dst[0] = lo * lo;
+      dst[1] = hi * hi;
+    } else {
+      f32x4 a;
+      a.x = widen(u.x); a.y = widen(u.y); a.z = widen(u.z); a.w = widen(u.w);
+      dst[0] = a * a;
     }
     __syncthreads();
     if (folds) {
-      for (int q = 0; q < Q && c0 + q < P; ++q) {
-        const uint32_t start = (uint32_t)(c0 + q) * kChunkElems;
-        if (start >= extent) break;
-        const uint32_t slots = (extent - start >= kChunkElems ? kChunkElems : extent - start) / 4u;
-        const f32x4* g = ring + q * kChunk + lane * F4;
-        uint32_t i = 0;
-        for (; i + 8 <= slots; i += 8) {
-          f32x4 e[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) e[u] = g[((i + u) / F4) * kGroup + (i + u) % F4];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            acc = acc + e[u].x;
-            acc = acc + e[u].y;
-            acc = acc + e[u].z;
-            acc = acc + e[u].w;
-          }
-        }
-        for (; i < slots; ++i) {
-          const f32x4 e = g[(i / F4) * kGroup + i % F4];
-          acc = acc + e.x;
-          acc = acc + e.y;
-          acc = acc + e.z;
-          acc = acc + e.w;
-        }
-      }
+      const uint32_t left = extent - (uint32_t)j * kChunkElems;
+      const uint32_t count = (left < kChunkElems ? left : kChunkElems) / 4u;
+      acc = fold_ring_round<kChunkElems / 4, F4, kGroup, kChunk>(ring + (j & 1) * kChunk + lane * F4, count, acc);
     }
-    __syncthreads();  // the ring is refilled next
   }
   if (folds) scale[lane] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
   __syncthreads();
@@ -681,32 +726,9 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
     for (int q = 0; q < Q && c0 + q < P; ++q) ring[q * kChunk + l * kGroup + r] = v[c0 + q];
     __syncthreads();
     if (folds) {
-      for (int q = 0; q < Q && c0 + q < P; ++q) {
-        const uint32_t start = (uint32_t)(c0 + q) * 128u;
-        if (start >= extent) break;
-        const uint32_t groups = extent - start >= 128u ? 32u : (extent - start) / 4u;
-        const f32x4* g = ring + q * kChunk + lane;
-        uint32_t i = 0;
-        for (; i + 8 <= groups; i += 8) {
-          f32x4 e[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) e[u] = g[(i + u) * kGroup];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            acc = acc + e[u].x;
-            acc = acc + e[u].y;
-            acc = acc + e[u].z;
-            acc = acc + e[u].w;
-          }
-        }
-        for (; i < groups; ++i) {
-          const f32x4 e = g[i * kGroup];
-          acc = acc + e.x;
-          acc = acc + e.y;
-          acc = acc + e.z;
-          acc = acc + e.w;
-        }
-      }
+      const uint32_t start = (uint32_t)c0 * 128u, left = extent - start;
+      const uint32_t count = (left < Q * 128u ? left : Q * 128u) / 4u;
+      acc = fold_ring_round<32, 1, kGroup, kChunk>(ring + lane, count, acc);
     }
     __syncthreads();  // the ring is refilled next
   }
