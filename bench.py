@@ -601,7 +601,7 @@ class Dequantize(Workload):
     4 B written per element.  Not a BASELINE config, measured as a family of
     its own."""
     name = "dequantize"
-    kernel = "tiler_dequantize_u4_f32_v4"
+    kernel = "tiler_dequantize_u4_f32_w"
     n = 1 << 28
     scale_bits, zero_point = 0x3C23D70A, 8  # 0.01, zero point 8
     sets = 2  # 2 x 1.125 GiB touched per sweep

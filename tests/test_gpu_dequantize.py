@@ -45,8 +45,10 @@ def test_reference_rows(ctx):
         assert int(bits(got)[0]) == int(row["value_bits"], 16), row["source"]
 
 
-@pytest.mark.parametrize("n", [1, 15, 16, 17, 1000, 4096, (1 << 22) + 5, 1 << 24])
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 1000, 4096, 2048 * 3 + 1030, (1 << 22) + 5, 1 << 24])
 def test_random_codes_with_ragged_tails(ctx, n):
+    """Whole 2048-element wave blocks (tiler_dequantize_u4_f32_w), then
+    4-element chunks (_v4) and single elements for the rest."""
     rng = np.random.default_rng(n)
     codes = rng.integers(0, 16, n, dtype=np.uint8)
     packed = oracle.pack_u4(codes)
@@ -92,7 +94,8 @@ def test_out_of_domain_operands_refuse_before_commit(ctx):
     assert bits(ok).tolist() == bits(oracle.dequantize_u4(packed, 2, 0x00800000, 8)).tolist()
 
 
-@pytest.mark.parametrize("n,form", [(4096, "tiler_dequantize_u4_f32_v4_slots"),
+@pytest.mark.parametrize("n,form", [(4096, "tiler_dequantize_u4_f32_w_slots"),
+                                    (6148, "tiler_dequantize_u4_f32_v4_slots"),
                                     (4097, "tiler_dequantize_u4_f32_slots")])
 def test_realized_region(ctx, n, form):
     rng = np.random.default_rng(n + 3)

@@ -283,11 +283,13 @@ def test_conversion_families():
 
 def test_strict_affine_u4_dequantize():
     """StrictAffineU4Dequantize (model.rs:682-696): slots [codes, scale, zero
-    point, y, domain record]; the vector form for aligned whole 4-element
-    groups, else the scalar form over everything; a flushing contract is
-    realized as the strict one (no operand or product is subnormal)."""
+    point, y, domain record]; aligned: the wave-block form for whole
+    2048-element blocks, the vector form for whole 4-element groups, else the
+    scalar form over everything; a flushing contract is realized as the
+    strict one (no operand or product is subnormal)."""
     rz = realize(L.PROGRAM_DEQUANTIZE_U4, (4096,))
-    assert rz.symbols == ["tiler_dequantize_u4_f32_v4_slots"]
+    assert rz.symbols == ["tiler_dequantize_u4_f32_w_slots"] and rz.dispatches[0].grid == (1, 1, 1)
+    assert realize(L.PROGRAM_DEQUANTIZE_U4, (6148,)).symbols == ["tiler_dequantize_u4_f32_v4_slots"]
     assert rz.slots == [(L.SLOT_INPUT, 2048), (L.SLOT_INPUT, 4), (L.SLOT_INPUT, 1), (L.SLOT_OUTPUT, 16384),
                         (L.SLOT_SCRATCH, 4)]
     assert rz.dispatches[0].bindings == [(0, 0), (1, 16), (2, 24), (3, 32), (4, 40)]

@@ -12,10 +12,11 @@
 // the IEEE product.  No subnormal can arise (|difference| >= 1 and the scale
 // is normal), so the declared subnormal modes have nothing to act on.
 //
-// An HBM stream: 0.5 B read and 4 B written per element.  The vector form
-// moves four elements per chunk (a 2-byte carrier load, one 16-byte store),
-// two chunks in flight per lane, each wave's loads and stores contiguous; the
-// scalar form serves unaligned storage and tails.
+// An HBM stream: 0.5 B read and 4 B written per element.  The wave-block
+// form (_w) takes whole 2048-element blocks with 16-byte code loads; the
+// vector form moves four elements per chunk (a 2-byte carrier load, one
+// 16-byte store), two chunks in flight per lane, each wave's loads and
+// stores contiguous; the scalar form serves unaligned storage and tails.
 //
 // The *_slots forms are the realized region's: the scale and the zero point
 // are read from their own slots and checked against their domains there (the
@@ -70,6 +71,32 @@ __device__ __forceinline__ void dequantize_v4_body(const uint16_t* __restrict__ 
   }
 }
 
+// Whole wave blocks of 2048 elements (1 KiB of codes, 8 KiB of y): each lane
+// loads 16 bytes of codes, and the wave writes eight contiguous 1 KiB runs.
+// Run j's lane t holds chunk 64 j + t, whose two carriers are code bytes
+// 128 j + 2 t .. +1 of the block: bytes 2 (t % 8) .. +1 of lane 8 j + t / 8's
+// load, taken with one cross-lane read per 32-bit word.  Measured at 2^28
+// elements: 204-209 us against 231 us for the two-chunk form, whose 2-byte
+// code loads take eight times the load instructions.
+__device__ __forceinline__ void dequantize_block_body(const u32x4* __restrict__ codes, uint64_t blocks, float scale,
+                                                      int32_t zp, f32x4* __restrict__ y) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint64_t b = (uint64_t)blockIdx.x * (blockDim.x / 64u) + (threadIdx.x >> 6);
+  if (b >= blocks) return;
+  const u32x4 w = __builtin_nontemporal_load(&codes[b * 64u + lane]);
+  f32x4* out = y + b * 512u;
+  const uint32_t word = (lane & 7u) >> 1;
+  const bool high = lane & 1u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int src = 8 * j + (int)(lane >> 3);
+    const uint32_t v0 = __shfl(w.x, src, 64), v1 = __shfl(w.y, src, 64);
+    const uint32_t v2 = __shfl(w.z, src, 64), v3 = __shfl(w.w, src, 64);
+    const uint32_t sel = word == 0 ? v0 : word == 1 ? v1 : word == 2 ? v2 : v3;
+    out[64u * j + lane] = decode4(high ? sel >> 16 : sel & 0xffffu, zp, scale);
+  }
+}
+
 // Elements [first, first + n) of the packed tensor, one per lane.
 __device__ __forceinline__ void dequantize_scalar_body(const uint8_t* __restrict__ codes, uint64_t first,
                                                        uint64_t n, float scale, int32_t zp,
@@ -104,6 +131,12 @@ tiler_dequantize_u4_f32_v4(const uint16_t* __restrict__ codes, uint64_t n4, uint
 }
 
 extern "C" __global__ void __launch_bounds__(256)
+tiler_dequantize_u4_f32_w(const u32x4* __restrict__ codes, uint64_t blocks, uint32_t scale_bits, uint32_t zero_point,
+                          f32x4* __restrict__ y) {
+  dequantize_block_body(codes, blocks, __uint_as_float(scale_bits), (int32_t)zero_point, y);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
 tiler_dequantize_u4_f32(const uint8_t* __restrict__ codes, uint64_t first, uint64_t n, uint32_t scale_bits,
                         uint32_t zero_point, float* __restrict__ y) {
   dequantize_scalar_body(codes, first, n, __uint_as_float(scale_bits), (int32_t)zero_point, y);
@@ -117,6 +150,15 @@ tiler_dequantize_u4_f32_v4_slots(const uint16_t* __restrict__ codes, uint64_t n4
   float scale;
   int32_t zp;
   if (read_operands(scale_slot, zero_slot, record, scale, zp)) dequantize_v4_body(codes, n4, scale, zp, y);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+tiler_dequantize_u4_f32_w_slots(const u32x4* __restrict__ codes, uint64_t blocks,
+                                const uint32_t* __restrict__ scale_slot, const uint8_t* __restrict__ zero_slot,
+                                f32x4* __restrict__ y, uint32_t* __restrict__ record) {
+  float scale;
+  int32_t zp;
+  if (read_operands(scale_slot, zero_slot, record, scale, zp)) dequantize_block_body(codes, blocks, scale, zp, y);
 }
 
 extern "C" __global__ void __launch_bounds__(256)

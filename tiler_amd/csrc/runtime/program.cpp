@@ -658,17 +658,33 @@ tiler_hip_status plan_dequantize_u4(Mode mode, uint64_t n, uint32_t scale_bits, 
     if (zero_point > 15) return p.refuse(TILER_HIP_REFUSE_INVALID_ARGUMENT, "zero point outside the U4 code domain 0..=15");
   }
   if (n == 0) return TILER_HIP_OK;
-  uint64_t head = aligned16(addr[codes]) && aligned16(addr[y]) ? n / 4 * 4 : 0;
-  if (realized && head != n) head = 0;  // a plan binds slot bases: one kernel over all of it
-  if (head) {
-    Launch& l = p.add(realized ? "tiler_dequantize_u4_f32_v4_slots" : "tiler_dequantize_u4_f32_v4",
-                      blocks_capped((head / 4 + 1) / 2, 1u << 30), 1, 256)
+  const bool al = aligned16(addr[codes]) && aligned16(addr[y]);
+  // Whole 2048-element wave blocks first (16-byte code loads), four per workgroup.
+  const uint64_t blocks = al ? n / 2048 : 0;
+  if (blocks && (!realized || blocks * 2048 == n)) {
+    if ((blocks + 3) / 4 > 0xffffffffull) return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more blocks than the launch grid holds");
+    Launch& l = p.add(realized ? "tiler_dequantize_u4_f32_w_slots" : "tiler_dequantize_u4_f32_w",
+                      (uint32_t)((blocks + 3) / 4), 1, 256)
                     .ptr(codes)
-                    .u64(head / 4);
+                    .u64(blocks);
     if (realized) l.ptr(scale).ptr(zero).ptr(y).ptr(record);
     else l.u32(scale_bits).u32(zero_point).ptr(y);
+    if (blocks * 2048 == n) return TILER_HIP_OK;
+  }
+  const uint64_t done = realized ? 0 : blocks * 2048;  // elements the block kernel wrote
+  uint64_t head = al ? n / 4 * 4 : 0;
+  if (realized && head != n) head = 0;  // a plan binds slot bases: one kernel over all of it
+  if (head > done) {
+    const uint64_t n4 = (head - done) / 4;
+    Launch& l = p.add(realized ? "tiler_dequantize_u4_f32_v4_slots" : "tiler_dequantize_u4_f32_v4",
+                      blocks_capped((n4 + 1) / 2, 1u << 30), 1, 256)
+                    .ptr(codes, done / 2)
+                    .u64(n4);
+    if (realized) l.ptr(scale).ptr(zero).ptr(y).ptr(record);
+    else l.u32(scale_bits).u32(zero_point).ptr(y, done * 4);
     if (head == n) return TILER_HIP_OK;
   }
+  if (head < done) head = done;
   if (realized) {
     p.add("tiler_dequantize_u4_f32_slots", blocks_capped(n, 8192), 1, 256)
         .ptr(codes).u64(n).ptr(scale).ptr(zero).ptr(y).ptr(record);

@@ -192,8 +192,10 @@ const EntryRow kEntries[] = {
     {"tiler_narrow_f32_bf16", "convert-f32-to-bf16/narrow", 2},
     {"tiler_widen_bf16_f32_v8", "convert-bf16-to-f32/widen", 2},
     {"tiler_widen_bf16_f32", "convert-bf16-to-f32/widen", 2},
+    {"tiler_dequantize_u4_f32_w", "dequantize-strict-affine-u4", 2},
     {"tiler_dequantize_u4_f32_v4", "dequantize-strict-affine-u4", 2},
     {"tiler_dequantize_u4_f32", "dequantize-strict-affine-u4", 2},
+    {"tiler_dequantize_u4_f32_w_slots", "dequantize-strict-affine-u4", 5},
     {"tiler_dequantize_u4_f32_v4_slots", "dequantize-strict-affine-u4", 5},
     {"tiler_dequantize_u4_f32_slots", "dequantize-strict-affine-u4", 5},
     {"tiler_contract_strict_f32", "tensor-contraction-f32/strict", 3},
