@@ -123,6 +123,72 @@ def test_strict_rows(ctx, case):
     assert np.array_equal(bits(got), bits(want)), rz.symbols
 
 
+@pytest.mark.parametrize("case", range(8))
+def test_resident_strict_rows(ctx, case):
+    """Random shapes through the register-resident strict forms
+    (tiler_{rms_norm_f32,rms_norm_bf16,softmax_f32}_strict_rr8_p*): 2048 to
+    2600 rows (ragged last workgroups included), extents drawn over their
+    whole range, bit for bit -- every RMSNorm row, and for the softmax 64
+    sampled rows plus the last workgroup's."""
+    from tiler_amd.realize import realize, route
+    r = _rng(case, 11)
+    rows = int(r.integers(2048, 2601))
+    # f32 RMSNorm, extent a multiple of 4 in [64, 2048]
+    extent = 4 * int(r.integers(16, 513))
+    x = (r.standard_normal((rows, extent)) * 3).astype(np.float32)
+    x[int(r.integers(rows)), int(r.integers(extent))] = np.nan
+    w = r.normal(1.0, 0.1, extent).astype(np.float32)
+    print(f"[resident rows] case {case}: rms f32 rows={rows} extent={extent}", flush=True)
+    rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), scalars=(EPS,),
+                 flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=ctx)
+    assert "_strict_rr8_p" in rz.symbols[-1], rz.symbols
+    bufs = [ctx.to_device(x), ctx.to_device(w), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[2].download(np.float32, x.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    want = oracle.rms_norm_f32(x, np.broadcast_to(w, x.shape).copy(), x.shape, 1, EPS).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want)), rz.symbols
+    # bf16 RMSNorm, extent a multiple of 8 in [128, 4096], a weight row per row
+    extent = 8 * int(r.integers(16, 513))
+    xb = oracle.bf16_narrow(r.standard_normal((rows, extent)).astype(np.float32)).reshape(rows, extent)
+    wb = oracle.bf16_narrow(r.normal(1.0, 0.1, (rows, extent)).astype(np.float32)).reshape(rows, extent)
+    print(f"[resident rows] case {case}: rms bf16 rows={rows} extent={extent}", flush=True)
+    rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=L.BF16, scalars=(EPS,), flags=L.REGION_ALIGNED16,
+                 ctx=ctx)
+    assert "_strict_rr8_p" in rz.symbols[-1], rz.symbols
+    bufs = [ctx.to_device(xb), ctx.to_device(wb), ctx.alloc(xb.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[2].download(np.uint16, xb.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    wantf = oracle.rms_norm_f32(bf16_widen(xb), bf16_widen(wb), xb.shape, 1, EPS)
+    assert np.array_equal(got.reshape(-1), oracle.bf16_narrow(wantf).reshape(-1)), rz.symbols
+    # softmax, extent a multiple of 4 in [128, 2048]
+    extent = 4 * int(r.integers(32, 513))
+    x = (r.standard_normal((rows, extent)) * 3).astype(np.float32)
+    sample = np.unique(np.concatenate([r.choice(rows, 64, replace=False), np.arange(rows - rows % 8 - 8, rows)]))
+    x[sample[3], int(r.integers(extent))] = np.nan
+    x[sample[5]] = -np.inf
+    print(f"[resident rows] case {case}: softmax rows={rows} extent={extent}", flush=True)
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), flags=L.REGION_ALIGNED16, ctx=ctx)
+    assert "_strict_rr8_p" in rz.symbols[-1], rz.symbols
+    bufs = [ctx.to_device(x), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[1].download(np.float32, x.shape)[sample]
+    finally:
+        for b in bufs:
+            b.free()
+    xs = np.ascontiguousarray(x[sample])
+    want = oracle.softmax_f32(xs, xs.shape, 1).reshape(xs.shape)
+    assert np.array_equal(bits(got), bits(want)), rz.symbols
+
+
 @pytest.mark.parametrize("case", range(CASES))
 def test_tree_sum(ctx, case):
     r = _rng(case, 2)
