@@ -60,3 +60,27 @@ def test_restated_device_exp_matches_certified_at_boundaries(s):
     s = float(np.float32(s))
     assert np.float32(oracle.device_exp_f32(s)).view(np.uint32) == \
         np.float32(oracle.certified_exp_f32(s)).view(np.uint32)
+
+
+def test_nonpositive_exp_reduction_is_the_audited_rint():
+    """tiler::exp_f32_cr_nonpositive forms k as fl(s * 64/ln2) + 1.5 * 2^52
+    minus 1.5 * 2^52 and reads k from the sum's low word, where exp_f32_cr
+    (the audited evaluation) takes rint of the same product and converts it.
+    Every binary32 s in (-104, 0] gives the same binary64 k and the same
+    integer (so the rest of the evaluation is the audited one): checked on
+    every 97th input of the range and on products planted at halfway points
+    (ties round to even in both)."""
+    c = float.fromhex("0x1.71547652b82fep+6")  # TILER_64_OVER_LN2, exp_table.h
+    lo, hi = 0x80000000, 0xC2D00000            # -0 .. -104
+    u = np.arange(lo, hi, 97, dtype=np.uint64).astype(np.uint32)
+    s = u.view(np.float32).astype(np.float64)
+    s = s[s > -104.0]
+    y = s * c
+    magic = float.fromhex("0x1.8p52")
+    shifted = y + magic
+    kd = shifted - magic
+    assert np.array_equal(kd, np.rint(y))
+    low = (shifted.view(np.uint64) & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.int32)
+    assert np.array_equal(low.astype(np.int64), np.rint(y).astype(np.int64))
+    ties = -np.arange(1, 6600, dtype=np.float64) - 0.5  # k + 0.5 for every k the domain reaches
+    assert np.array_equal((ties + magic) - magic, np.rint(ties))
