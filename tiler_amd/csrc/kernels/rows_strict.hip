@@ -547,19 +547,76 @@ __device__ __forceinline__ float fold_ring_round(const f32x4* base, uint32_t cou
   return acc;
 }
 
+// f(Step<0>{}), f(Step<1>{}), ... f(Step<N - 1>{}) while f returns true: a
+// loop unrolled at compile time (the index is a constant in each call, so
+// register arrays indexed by it stay in registers), whatever the loop
+// unroller would decide for a body that holds a loop of its own.
+template <int J>
+struct Step {
+  static constexpr int value = J;
+};
+template <int J, int N, typename F>
+__device__ __forceinline__ void unrolled_while(F& f) {
+  if constexpr (J < N) {
+    if (f(Step<J>{})) unrolled_while<J + 1, N>(f);
+  }
+}
+
+// A DPP move of v across the lanes of each 16-lane row (kCtrl: row_shr:1 =
+// 0x111, lane i takes lane i - 1; row_ror:9 = 0x129, lane i takes lane
+// (i - 9) mod 16, so lanes 7 and 15 go to lanes 0 and 8).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
+}
+
+// The relay fold of one ring chunk by one wave: lane 8 g + s holds in seg the
+// S4 float4 slots (4 S4 consecutive contributors, ascending) of segment s of
+// row g's chunk.  Row g's running sum enters the chunk in lane 8 g; each hop,
+// every lane adds its segment in order and a DPP move hands each sum to the
+// next lane of its group (the eighth hop back to lane 8 g), so the lane
+// holding row g's sum at hop s is lane 8 g + s and the chunk's 32 S4
+// contributors are added in ascending order.  The adds read registers only,
+// and one wave instruction advances the eight rows' chains.  What the other
+// lanes add is never read.
+template <uint32_t S4>
+__device__ __forceinline__ float relay_fold_chunk(const f32x4 (&seg)[S4], float acc) {
+  auto add = [&]() {
+#pragma unroll
+    for (uint32_t k = 0; k < S4; ++k) {
+      acc = acc + seg[k].x;
+      acc = acc + seg[k].y;
+      acc = acc + seg[k].z;
+      acc = acc + seg[k].w;
+    }
+  };
+  // A loop, not unrolled: the callers unroll their chunk loops over the
+  // resident pieces, which must stay small enough to unroll.
+#pragma unroll 1
+  for (int h = 0; h < 7; ++h) {
+    add();
+    acc = dpp_move<0x111>(acc);
+  }
+  add();
+  return dpp_move<0x129>(acc);
+}
+
 // Strict RMSNorm with a workgroup's rows resident in registers, for rows of
 // at most 32 P E elements (E = 8 bf16 or 4 f32 per 16-byte piece; extent a
-// multiple of E, 16-byte aligned rows and weight): R rows per workgroup of
-// 32 R threads, half a wave per row; lane l of a row holds the row's
+// multiple of E, 16-byte aligned rows and weight): 8 rows per workgroup of
+// 256 threads, half a wave per row; lane l of a row holds the row's
 // elements E (l + 32 j) .. +E-1 for j < P.  x is read once and y written
 // once (rms_norm.rs:134-195, 453-489):
 // * the squares fl(x * x) of the exactly widened elements go through a
 //   two-chunk LDS ring, chunk j (32 E columns) as soon as piece j of every
-//   lane has landed, laid out so that lane r of wave 0 reads row r's squares
-//   in ascending order; those R lanes fold chunk j while chunk j + 1 is
-//   written, from -0.0 (a square is never -0.0, so -0.0 plus the first square
-//   is the first square): the serial fold runs while the row is still
-//   arriving, one wave instruction advancing R rows' chains;
+//   lane has landed, laid out so that lane 8 g + s of wave 0 reads segment s
+//   (4 E consecutive columns) of row g's chunk with conflict-free 16-byte
+//   reads; wave 0 relay-folds chunk j (relay_fold_chunk) while chunk j + 1
+//   is written, from -0.0 (a square is never -0.0, so -0.0 plus the first
+//   square is the first square).  Columns past the row's end hold -0.0,
+//   which leaves every sum unchanged (s + -0.0 == s for every s, NaN and the
+//   zeros included), so whole chunks are folded.  The serial fold runs while
+//   the row is still arriving;
 // * per row the division by N, + eps and the certified rsqrt
 //   (rms_norm.rs:177-187);
 // * y = canon(fl(w * fl(x * s))) from the registers, weight after the
@@ -568,58 +625,78 @@ template <typename T, int R, int P>
 __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x, const T* __restrict__ w,
                                                          uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,
                                                          uint32_t extent, float eps) {
+  static_assert(R == 8, "eight rows: one 8-lane relay group per row in wave 0");
   constexpr bool kBf16 = sizeof(T) == 2;
-  constexpr uint32_t E = 16 / sizeof(T);    // elements per piece
-  constexpr uint32_t F4 = E / 4;            // float4 slots of squares per piece
-  constexpr uint32_t kGroup = R * F4 + 1;   // float4 slots per piece column (a pad slot: no bank aliasing)
-  constexpr uint32_t kChunk = 32 * kGroup;  // float4 slots per chunk
+  constexpr uint32_t E = 16 / sizeof(T);  // elements per piece
+  constexpr uint32_t F4 = E / 4;          // float4 slots of squares per piece
+  constexpr uint32_t S4 = 4 * F4;         // float4 slots per relay segment (4 pieces)
+  constexpr uint32_t kChunk = 64 * S4;    // float4 slots per chunk: slot k of lane L at k * 64 + L
   __shared__ f32x4 ring[2 * kChunk];
   __shared__ float scale[R];
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t r = wave * 2u + (lane >> 5), l = lane & 31u;
   const uint64_t row0 = (uint64_t)blockIdx.x * R;
   const bool row_ok = row0 + r < rows;
-  const T* xr = x + (row0 + r) * extent;
   auto widen = [](uint32_t bits) -> float {
     if constexpr (kBf16) return tiler::bf16_widen(bits);
     else return __uint_as_float(bits);
   };
+  // Piece j is loaded while chunk j - W is written (W ahead): with every
+  // piece requested at once the memory system completes chunk 0 late, and
+  // the fold, which needs chunk 0 first, starts late.  The loads are
+  // branch-free (a piece past the row's end, or of a row past the last,
+  // reads a valid element of the last row instead; its square goes to the
+  // ring as -0.0 and it is never stored), so each wait counts exactly the
+  // loads issued after the piece it waits for.
+  constexpr int W = P < 4 ? P : 4;
+  const T* xc = x + (row_ok ? row0 + r : rows - 1) * extent;
   u32x4 v[P];
-#pragma unroll
-  for (int j = 0; j < P; ++j) {
+  auto load = [&](int j) {
     const uint32_t e = E * (l + 32u * j);
-    v[j] = row_ok && e < extent ? *reinterpret_cast<const u32x4*>(xr + e) : u32x4{0, 0, 0, 0};
-  }
-  const bool folds = wave == 0 && lane < (uint32_t)R && row0 + lane < rows;
+    v[j] = *reinterpret_cast<const u32x4*>(xc + (e < extent ? e : extent - E));
+  };
+#pragma unroll
+  for (int j = 0; j < W; ++j) load(j);
   float acc = -0.0f;
   constexpr uint32_t kChunkElems = 32 * E;
+  const f32x4 nz = {-0.0f, -0.0f, -0.0f, -0.0f};
+  // Piece j of lane l is pieces 4 (l / 4) + l % 4 of the chunk's segment
+  // l / 4: its slots are k = F4 (l % 4) + f of relay lane 8 r + l / 4.
+  f32x4* const mine = ring + (l & 3u) * F4 * 64u + 8u * r + (l >> 2);
   // Chunk j into ring half j & 1, one barrier per chunk: half j & 1 was last
-  // read by the fold of chunk j - 2, which ended before its folding lanes
+  // read by the fold of chunk j - 2, whose reads wave 0 waited for before it
   // reached the barrier of chunk j - 1.
-#pragma unroll
-  for (int j = 0; j < P; ++j) {
-    if ((uint32_t)j * kChunkElems >= extent) break;
+  auto chunk = [&](auto step) -> bool {
+    constexpr int j = decltype(step)::value;
+    if ((uint32_t)j * kChunkElems >= extent) return false;
+    if constexpr (j + W < P) load(j + W);
     const u32x4 u = v[j];
-    f32x4* dst = ring + (j & 1) * kChunk + l * kGroup + r * F4;
+    const bool in = E * (l + 32u * j) < extent;
+    f32x4* dst = mine + (j & 1) * kChunk;
     if constexpr (kBf16) {
       f32x4 lo, hi;
       lo.x = widen(u.x & 0xffffu); lo.y = widen(u.x >> 16); lo.z = widen(u.y & 0xffffu); lo.w = widen(u.y >> 16);
       hi.x = widen(u.z & 0xffffu); hi.y = widen(u.z >> 16); hi.z = widen(u.w & 0xffffu); hi.w = widen(u.w >> 16);
-      dst[0] = lo * lo;
-      dst[1] = hi * hi;
+      dst[0] = in ? lo * lo : nz;
+      dst[64] = in ? hi * hi : nz;
     } else {
       f32x4 a;
       a.x = widen(u.x); a.y = widen(u.y); a.z = widen(u.z); a.w = widen(u.w);
-      dst[0] = a * a;
+      dst[0] = in ? a * a : nz;
     }
     __syncthreads();
-    if (folds) {
-      const uint32_t left = extent - (uint32_t)j * kChunkElems;
-      const uint32_t count = (left < kChunkElems ? left : kChunkElems) / 4u;
-      acc = fold_ring_round<kChunkElems / 4, F4, kGroup, kChunk>(ring + (j & 1) * kChunk + lane * F4, count, acc);
+    if (wave == 0) {
+      const f32x4* src = ring + (j & 1) * kChunk + lane;
+      f32x4 seg[S4];
+#pragma unroll
+      for (uint32_t k = 0; k < S4; ++k) seg[k] = src[k * 64u];
+      acc = relay_fold_chunk<S4>(seg, acc);
     }
-  }
-  if (folds) scale[lane] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
+    return true;
+  };
+  unrolled_while<0, P>(chunk);
+  // Row g's sum is in lane 8 g after the last chunk's final hop.
+  if (wave == 0 && (lane & 7u) == 0) scale[lane >> 3] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
   __syncthreads();
   if (!row_ok) return;
   const float sc = scale[r];
