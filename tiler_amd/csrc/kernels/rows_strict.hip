@@ -479,74 +479,6 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
   }
 }
 
-// A folding lane's pass over one round of the resident kernels' LDS ring:
-// folds `count` float4 slots (4 contributors each) in ascending order onto
-// acc, slot n at base[(n / kPerChunk) * kChunk + ((n % kPerChunk) / F4) *
-// kGroup + n % F4], with two batches of B slots in flight: the next batch's
-// LDS reads are issued before the current batch's adds, so the dependent
-// adds do not wait on LDS latency.  A batch never straddles a chunk (B
-// divides kPerChunk), so its reads are one pointer plus constant offsets;
-// B = 4 keeps the two batches within the registers the rows leave free.
-template <uint32_t kPerChunk, uint32_t F4, uint32_t kGroup, uint32_t kChunk, uint32_t B = 4>
-__device__ __forceinline__ float fold_ring_round(const f32x4* base, uint32_t count, float acc) {
-  static_assert(kPerChunk % B == 0 && B % F4 == 0, "a batch lies inside one chunk");
-  const f32x4* p = base;
-  uint32_t in_chunk = 0;  // slots of the current chunk already read
-  auto read = [&](f32x4 (&e)[B]) {
-#pragma unroll
-    for (uint32_t u = 0; u < B; ++u) e[u] = p[(u / F4) * kGroup + u % F4];
-    p += (B / F4) * kGroup;
-    in_chunk += B;
-    if (in_chunk == kPerChunk) {
-      p += kChunk - (kPerChunk / F4) * kGroup;
-      in_chunk = 0;
-    }
-  };
-  auto add = [&](const f32x4 (&e)[B]) {
-#pragma unroll
-    for (uint32_t u = 0; u < B; ++u) {
-      acc = acc + e[u].x;
-      acc = acc + e[u].y;
-      acc = acc + e[u].z;
-      acc = acc + e[u].w;
-    }
-  };
-  // Batches k (in a) and k + 1 (in b) with k + 2 read ahead: the steady
-  // state has no branch, so the LDS wait before each batch's adds counts
-  // only that batch's reads.
-  const uint32_t batches = count / B;
-  f32x4 a[B], b[B];
-  if (batches) read(a);
-  uint32_t k = 0;
-  for (; k + 2 < batches; k += 2) {  // sched_barrier: the compiler would otherwise sink each read to its use
-    read(b);
-    __builtin_amdgcn_sched_barrier(0);
-    add(a);
-    __builtin_amdgcn_sched_barrier(0);
-    read(a);
-    __builtin_amdgcn_sched_barrier(0);
-    add(b);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if (k + 1 < batches) {
-    read(b);
-    add(a);
-    add(b);
-  } else if (k < batches) {
-    add(a);
-  }
-  // The last few slots, inside the chunk p is in (a chunk holds a whole
-  // number of batches): slot t past p at p[(t / F4) * kGroup + t % F4].
-  for (uint32_t t = 0; t < count - batches * B; ++t) {
-    const f32x4 e = p[(t / F4) * kGroup + t % F4];
-    acc = acc + e.x;
-    acc = acc + e.y;
-    acc = acc + e.z;
-    acc = acc + e.w;
-  }
-  return acc;
-}
-
 // f(Step<0>{}), f(Step<1>{}), ... f(Step<N - 1>{}) while f returns true: a
 // loop unrolled at compile time (the index is a constant in each call, so
 // register arrays indexed by it stay in registers), whatever the loop
@@ -740,10 +672,11 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
 //   lanes;
 // * the exponents e = certified exp(fl(x - m)), in place in the registers;
 // * the fold: the exponents pass through an LDS ring in 128-column chunks,
-//   laid out so that lane r of one wave reads row r's elements in ascending
-//   order 16 bytes at a time, and those R lanes fold their rows from -0.0
+//   eight chunks a round, laid out so that lane 8 g + s of wave 0 reads
+//   segment s (16 columns) of row g's chunk with conflict-free 16-byte
+//   reads, and wave 0 relay-folds each chunk (relay_fold_chunk) from -0.0
 //   (an exponent is never -0.0, so -0.0 plus the first is the first): one
-//   wave instruction advances R rows' chains;
+//   wave instruction advances the eight rows' chains;
 // * y = fl(e * fl(1 / d)) from the registers: the reciprocal, then a
 //   multiply (softmax.rs:302-313), canonical NaN where the row's d is NaN.
 // Three steps take the short form because the row's values cannot tell:
@@ -759,9 +692,9 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
 template <int R, int P>
 __device__ __forceinline__ void softmax_strict_resident_body(const float* __restrict__ x, float* __restrict__ y,
                                                              uint64_t rows, uint32_t extent) {
-  constexpr int Q = 8;                      // ring chunks: the fold runs once per Q chunks
-  constexpr uint32_t kGroup = R + 1;        // float4 slots per 4-column group (a pad slot: no bank aliasing)
-  constexpr uint32_t kChunk = 32 * kGroup;  // float4 slots per 128-column chunk
+  static_assert(R == 8, "eight rows: one 8-lane relay group per row in wave 0");
+  constexpr int Q = 8;               // ring chunks: the fold runs once per Q chunks
+  constexpr uint32_t kChunk = 64 * 4;  // float4 slots per 128-column chunk: slot k of lane L at k * 64 + L
   __shared__ f32x4 ring[Q * kChunk];
   __shared__ float recip[R];
   __shared__ double tab[64];
@@ -792,24 +725,48 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
     v[j].z = tiler::exp_f32_cr_nonpositive(v[j].z - m, tab);
     v[j].w = tiler::exp_f32_cr_nonpositive(v[j].w - m, tab);
   }
-  // Lane f < R of wave 0 folds row f.  Slots past the row's end hold the
-  // -inf fill's values and are never folded.
-  const bool folds = wave == 0 && lane < (uint32_t)R && row0 + lane < rows;
+  // Wave 0 relay-folds (relay_fold_chunk): lane 8 g + s holds segment s
+  // (16 columns) of row g's chunk.  Columns past the row's end go to the
+  // ring as -0.0, which leaves every sum unchanged, so whole chunks are
+  // folded; the next chunk's segment is read while the current one is
+  // folded (its address clamped to the current chunk at the round's end, so
+  // the reads are unconditional and each LDS wait counts exactly).
   float acc = -0.0f;
+  const f32x4 nz = {-0.0f, -0.0f, -0.0f, -0.0f};
+  f32x4* const mine = ring + (l & 3u) * 64u + 8u * r + (l >> 2);
+  auto round = [&](auto step) -> bool {
+    constexpr int c0 = decltype(step)::value * Q;
+    if ((uint32_t)c0 * 128u >= extent) return false;
 #pragma unroll
-  for (int c0 = 0; c0 < P; c0 += Q) {
-    if ((uint32_t)c0 * 128u >= extent) break;
-#pragma unroll
-    for (int q = 0; q < Q && c0 + q < P; ++q) ring[q * kChunk + l * kGroup + r] = v[c0 + q];
+    for (int q = 0; q < Q && c0 + q < P; ++q)
+      mine[q * kChunk] = 4u * (l + 32u * (c0 + q)) < extent ? v[c0 + q] : nz;
     __syncthreads();
-    if (folds) {
-      const uint32_t start = (uint32_t)c0 * 128u, left = extent - start;
-      const uint32_t count = (left < Q * 128u ? left : Q * 128u) / 4u;
-      acc = fold_ring_round<32, 1, kGroup, kChunk>(ring + lane, count, acc);
+    if (wave == 0) {
+      const uint32_t left = extent - (uint32_t)c0 * 128u;
+      const uint32_t nq = left < Q * 128u ? (left + 127u) / 128u : (uint32_t)Q;
+      const f32x4* src = ring + lane;
+      f32x4 a[4], b[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a[k] = src[k * 64];
+      auto chunk = [&](auto qs) -> bool {
+        constexpr int q = decltype(qs)::value;
+        if ((uint32_t)q >= nq) return false;
+        f32x4(&cur)[4] = (q & 1) ? b : a;
+        f32x4(&nxt)[4] = (q & 1) ? a : b;
+        const f32x4* next = src + ((uint32_t)q + 1 < nq ? q + 1 : q) * kChunk;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) nxt[k] = next[k * 64];
+        acc = relay_fold_chunk<4>(cur, acc);
+        return true;
+      };
+      unrolled_while<0, Q>(chunk);
     }
     __syncthreads();  // the ring is refilled next
-  }
-  if (folds) recip[lane] = 1.0f / acc;
+    return true;
+  };
+  unrolled_while<0, (P + Q - 1) / Q>(round);
+  // Row g's sum is in lane 8 g after the last chunk's final hop.
+  if (wave == 0 && (lane & 7u) == 0) recip[lane >> 3] = 1.0f / acc;
   __syncthreads();
   if (!row_ok) return;
   const float rc = recip[r];
