@@ -97,7 +97,10 @@ def test_reference_split_rows_on_the_device(ctx, reading):
 
 @pytest.mark.parametrize("rows,extent,flags", [(33, 7, L.REGION_ALIGNED16), (300, 40, L.REGION_ALIGNED16),
                                                (300, 41, 0), (2000, 300, L.REGION_ALIGNED16),
-                                               (5, 20000, L.REGION_ALIGNED16), (1, 1, L.REGION_ALIGNED16)])
+                                               (5, 20000, L.REGION_ALIGNED16), (1, 1, L.REGION_ALIGNED16),
+                                               (10, 100, L.REGION_ALIGNED16), (1, 70, L.REGION_ALIGNED16),
+                                               (700, 1000, L.REGION_ALIGNED16), (3, 512, L.REGION_ALIGNED16),
+                                               (700, 1001, 0)])
 @pytest.mark.parametrize("modes", MODES)
 def test_serial_sum_under_modes(ctx, rows, extent, flags, modes):
     rng = np.random.default_rng(rows * 7 + extent)

@@ -76,6 +76,9 @@ def _order_sensitive(rng, rows, extent):
     (20000, 64, 0),    # sixty-four rows per workgroup, one stage
     (17000, 65, 0),    # sixty-four rows, a second stage of one element
     (1, 70000, 0),     # one long row
+    (2, 100, 0),       # one row per workgroup, one pass that opens and ends the row
+    (3, 8192, 0),      # whole stages and whole 256-element passes
+    (600, 256, 0),     # four rows per workgroup, one whole pass
     (5000, 20, 0),     # rows of 16..63: 256 rows per workgroup, stages of 16
     (300, 63, 0),      # the same, 4-byte loads, a ragged last stage
     (257, 16, 4),      # one stage, an unaligned base, a second workgroup of one row

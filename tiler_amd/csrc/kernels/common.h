@@ -290,4 +290,72 @@ __device__ __forceinline__ float silu_for_bf16(float x) {
   return exact ? silu_f32_straight(x) : v;
 }
 
+// f(Step<0>{}), f(Step<1>{}), ... f(Step<N - 1>{}) while f returns true: a
+// loop unrolled at compile time (the index is a constant in each call, so
+// register arrays indexed by it stay in registers), whatever the loop
+// unroller would decide for a body that holds a loop of its own.
+template <int J>
+struct Step {
+  static constexpr int value = J;
+};
+template <int J, int N, typename F>
+__device__ __forceinline__ void unrolled_while(F& f) {
+  if constexpr (J < N) {
+    if (f(Step<J>{})) unrolled_while<J + 1, N>(f);
+  }
+}
+
+// A DPP move of v across the lanes of each 16-lane row (kCtrl: row_shr:1 =
+// 0x111, lane i takes lane i - 1; row_ror:9 = 0x129, lane i takes lane
+// (i - 9) mod 16, so lanes 7 and 15 go to lanes 0 and 8).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
+}
+
+// The relay fold of one ring chunk by one wave: lane 8 g + s holds in seg the
+// S4 float4 slots (4 S4 consecutive contributors, ascending) of segment s of
+// row g's chunk.  Row g's running value enters the chunk in lane 8 g; each
+// hop, every lane applies acc = step(acc, c) to its segment's contributors in
+// order and a DPP move hands each value to the next lane of its group (the
+// eighth hop back to lane 8 g), so the lane holding row g's value at hop s is
+// lane 8 g + s and the chunk's 32 S4 contributors are taken in ascending
+// order.  The steps read registers only, and one wave instruction advances
+// the eight rows' chains.  What the other lanes compute is never read.
+// kSeed: the chunk opens the row, whose first contributor is the seed (acc
+// becomes it, no step), as a fold seeded at its first contributor does.
+template <uint32_t S4, bool kSeed = false, typename F>
+__device__ __forceinline__ float relay_fold(const f32x4 (&seg)[S4], float acc, F step) {
+  auto add = [&](auto seeded) {
+#pragma unroll
+    for (uint32_t k = 0; k < S4; ++k) {
+      acc = decltype(seeded)::value && k == 0 ? seg[0].x : step(acc, seg[k].x);
+      acc = step(acc, seg[k].y);
+      acc = step(acc, seg[k].z);
+      acc = step(acc, seg[k].w);
+    }
+  };
+  constexpr Step<0> plain{};
+  int h = 0;
+  if constexpr (kSeed) {
+    add(Step<1>{});
+    acc = dpp_move<0x111>(acc);
+    h = 1;
+  }
+  // A loop, not unrolled: the callers unroll their chunk loops over the
+  // resident pieces, which must stay small enough to unroll.
+#pragma unroll 1
+  for (; h < 7; ++h) {
+    add(plain);
+    acc = dpp_move<0x111>(acc);
+  }
+  add(plain);
+  return dpp_move<0x129>(acc);
+}
+// The relay fold of the strict sum: step(acc, c) = fl(acc + c).
+template <uint32_t S4>
+__device__ __forceinline__ float relay_fold_chunk(const f32x4 (&seg)[S4], float acc) {
+  return relay_fold<S4>(seg, acc, [](float a, float c) { return a + c; });
+}
+
 }  // namespace tiler

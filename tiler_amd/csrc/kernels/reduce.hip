@@ -199,6 +199,99 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
   if (folds) out[row0 + fr] = length == 0 ? 0.0f : canon(acc);
 }
 
+// The same stages and the same fold, for R in {1, 4, 16} (rows of at least
+// 256 elements per stage), with the chain kept in registers: the folding
+// waves relay-fold (tiler::relay_fold_chunk) each row's stage in passes of
+// 256 elements, lane 8 g + s of a folding wave holding elements
+// 32 s .. 32 s + 31 of the pass, read from the stage with 16-byte reads; the
+// next pass's segment is read while the current one is folded.  R = 1: wave
+// 0 folds the row; R = 4: wave w folds row w; R = 16: wave w folds rows
+// 4 w .. 4 w + 3 in its groups 0..3 (groups 4..7 repeat groups 0..3's reads
+// and their sums are not used).  Elements past the row's end are staged as
+// -0.0, which leaves every sum unchanged (s + -0.0 == s for every s, the
+// zeros and NaN included), so whole passes are folded.  Same order, same
+// -0.0 seed, same commit as staged_fold_body.
+template <int R, bool kVec>
+__device__ __forceinline__ void staged_relay_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
+                                                  float* __restrict__ out) {
+  static_assert(R == 1 || R == 4 || R == 16, "rows of at least 256 elements per stage");
+  constexpr uint32_t C = 4096 / R;               // elements of a row per stage
+  constexpr uint32_t kStride = C + 4;            // LDS row stride in floats (16-byte aligned)
+  constexpr uint32_t W = kVec ? 4 : 1;           // elements per load
+  constexpr uint32_t kRowPieces = C / W;         // loads per row per stage
+  constexpr uint32_t kPer = 4096 / W / 256;      // loads per thread per stage
+  constexpr uint32_t S4 = 8;                     // 16-byte slots per lane per pass
+  constexpr uint32_t kPass = 32 * S4;            // elements of a row per pass
+  constexpr uint32_t kPasses = C / kPass;        // passes per whole stage
+  constexpr uint32_t kRowsPerWave = R == 16 ? 4u : 1u;
+  __shared__ __align__(16) float stage[2][R * kStride];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, g = lane >> 3, s = lane & 7u;
+  const uint64_t row0 = (uint64_t)blockIdx.x * R;
+  const uint64_t stages = (length + C - 1) / C;
+  typedef typename std::conditional<kVec, f32x4, float>::type piece;
+  const float nz = -0.0f;
+  piece reg[kPer];
+  auto load = [&](uint64_t st) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      const uint64_t e = st * C + (uint64_t)(q % kRowPieces) * W;
+      if (row0 + r < nrows && e < length) {
+        const float* src = x + (row0 + r) * length + e;
+        if constexpr (kVec) reg[i] = *reinterpret_cast<const f32x4*>(src);
+        else reg[i] = *src;
+      } else {
+        if constexpr (kVec) reg[i] = f32x4{nz, nz, nz, nz};
+        else reg[i] = nz;
+      }
+    }
+  };
+  auto store = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      *reinterpret_cast<piece*>(&stage[buf][r * kStride + (q % kRowPieces) * W]) = reg[i];
+    }
+  };
+  const bool folding_wave = R == 1 ? wave == 0 : true;
+  const uint32_t fr = R == 1 ? 0u : wave * kRowsPerWave + g % kRowsPerWave;  // the row this group folds
+  float acc = -0.0f;
+  if (stages > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (uint64_t st = 0; st < stages; ++st) {
+    const bool more = st + 1 < stages;
+    if (more) load(st + 1);
+    if (folding_wave) {
+      const uint32_t count = (uint32_t)(length - st * C < C ? length - st * C : C);
+      const uint32_t passes = (count + kPass - 1) / kPass;
+      const f32x4* src = reinterpret_cast<const f32x4*>(&stage[st & 1][fr * kStride]) + s * S4;
+      f32x4 a[S4], b[S4];
+#pragma unroll
+      for (uint32_t k = 0; k < S4; ++k) a[k] = src[k];
+      auto pass = [&](auto ps) -> bool {
+        constexpr uint32_t p = decltype(ps)::value;
+        if (p >= passes) return false;
+        f32x4(&cur)[S4] = (p & 1) ? b : a;
+        f32x4(&nxt)[S4] = (p & 1) ? a : b;
+        const f32x4* next = src + (p + 1 < passes ? p + 1 : p) * (kPass / 4);
+#pragma unroll
+        for (uint32_t k = 0; k < S4; ++k) nxt[k] = next[k];
+        acc = tiler::relay_fold_chunk<S4>(cur, acc);
+        return true;
+      };
+      tiler::unrolled_while<0, kPasses>(pass);
+    }
+    if (more) store((uint32_t)((st + 1) & 1));
+    __syncthreads();
+  }
+  // A group's row sum is in its lane 8 g after the last pass's final hop.
+  if (folding_wave && s == 0 && g < kRowsPerWave && row0 + fr < nrows)
+    out[row0 + fr] = length == 0 ? 0.0f : canon(acc);
+}
+
 // The same stages under a FoldRule (a flushing contract, a fused prologue),
 // rows of at least 16.  Every thread turns the values it stages into
 // apply_to_operand(contributor(x)) as it stores them to LDS (the prologue and
@@ -303,22 +396,158 @@ __device__ __forceinline__ void staged_rule_body(const float* __restrict__ x, ui
   if (folds) out[row0 + fr] = tiler::canon(acc);
 }
 
-#define TILER_SUM_STAGED(R)                                                                            \
+// R in {1, 4, 16}: the relay fold; R = 64 and 256 (rows of 16..255): the
+// lane-per-row fold of staged_fold_body, whose chains per stage are short.
+#define TILER_SUM_STAGED(R, BODY)                                                                      \
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_sum_f32_staged_r##R(const float* __restrict__ x, uint64_t nrows, uint64_t length,          \
                                 float* __restrict__ out) {                                             \
-    staged_fold_body<R, true, false>(x, nrows, length, nullptr, out);                                                   \
+    BODY<R, true>(x, nrows, length, out);                                                              \
   }                                                                                                    \
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_sum_f32_staged_r##R##_u(const float* __restrict__ x, uint64_t nrows, uint64_t length,      \
                                     float* __restrict__ out) {                                         \
-    staged_fold_body<R, false, false>(x, nrows, length, nullptr, out);                                                  \
+    BODY<R, false>(x, nrows, length, out);                                                             \
   }
-TILER_SUM_STAGED(1)
-TILER_SUM_STAGED(4)
-TILER_SUM_STAGED(16)
-TILER_SUM_STAGED(64)
-TILER_SUM_STAGED(256)  // rows of 16..63: stages of 16 elements, every lane folding a row
+template <int R, bool kVec>
+__device__ __forceinline__ void staged_lane_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
+                                                 float* __restrict__ out) {
+  staged_fold_body<R, kVec, false>(x, nrows, length, nullptr, out);
+}
+TILER_SUM_STAGED(1, staged_relay_body)
+TILER_SUM_STAGED(4, staged_relay_body)
+TILER_SUM_STAGED(16, staged_relay_body)
+TILER_SUM_STAGED(64, staged_lane_body)
+TILER_SUM_STAGED(256, staged_lane_body)  // rows of 16..63: stages of 16 elements, every lane folding a row
+
+// staged_rule_body's fold with the relay of staged_relay_body, for R in
+// {1, 4, 16}: the staged contributors are apply_to_operand(contributor(x)),
+// and the relay's step is the rule's combine acc = R(O(acc) + t), the row
+// opening with its first contributor as the seed (relay_fold<.., true> on
+// the first pass of the first stage).  Positions past the row's end are
+// staged as -0.0 after the prologue and the input mode (which could turn it
+// into +0.0): with a flushing result mode, or with no mode, a -0.0 step
+// leaves the value unchanged (R(acc + -0.0) = R(acc) = acc for a value that
+// came out of R); with only the input mode flushing it would leave O(acc),
+// so there the row's last pass takes a step only below the row's end.
+template <int R, bool kVec, bool kIn, bool kOut>
+__device__ __forceinline__ void staged_rule_relay_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
+                                                       float* __restrict__ out, const tiler::FoldRule& rule,
+                                                       float* __restrict__ lds) {
+  static_assert(R == 1 || R == 4 || R == 16, "rows of at least 256 elements per stage");
+  constexpr uint32_t C = 4096 / R;
+  constexpr uint32_t kStride = C + 4;
+  constexpr uint32_t W = kVec ? 4 : 1;
+  constexpr uint32_t kRowPieces = C / W;
+  constexpr uint32_t kPer = 4096 / W / 256;
+  constexpr uint32_t S4 = 8;
+  constexpr uint32_t kPass = 32 * S4;
+  constexpr uint32_t kRowsPerWave = R == 16 ? 4u : 1u;
+  float(*stage)[R * kStride] = reinterpret_cast<float(*)[R * kStride]>(lds);
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, g = lane >> 3, s = lane & 7u;
+  const uint64_t row0 = (uint64_t)blockIdx.x * R;
+  const uint64_t stages = (length + C - 1) / C;
+  typedef typename std::conditional<kVec, f32x4, float>::type piece;
+  piece reg[kPer];
+  const uint32_t imask = rule.in_mode == 2u ? 0x80000000u : 0u;
+  const uint32_t rmask = rule.out_mode == 2u ? 0x80000000u : 0u;
+  auto flush = [](float v, uint32_t mask) {
+    return __builtin_amdgcn_classf(v, 0x90) ? __uint_as_float(__float_as_uint(v) & mask) : v;
+  };
+  auto operand = [&](float v) {  // apply_to_operand(contributor(v))
+    const float c = tiler::fold_contributor(rule, v);
+    return kIn ? flush(c, imask) : c;
+  };
+  auto load = [&](uint64_t st) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      const uint64_t e = st * C + (uint64_t)(q % kRowPieces) * W;
+      if (row0 + r < nrows && e < length) {
+        const float* src = x + (row0 + r) * length + e;
+        if constexpr (kVec) reg[i] = *reinterpret_cast<const f32x4*>(src);
+        else reg[i] = *src;
+      } else {
+        reg[i] = piece{};
+      }
+    }
+  };
+  auto store = [&](uint32_t buf, uint64_t st) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      const uint64_t e = st * C + (uint64_t)(q % kRowPieces) * W;
+      const bool in = row0 + r < nrows && e < length;  // kVec: length is a multiple of 4
+      piece v = reg[i];
+      if constexpr (kVec) {
+        v = in ? f32x4{operand(v.x), operand(v.y), operand(v.z), operand(v.w)} : f32x4{-0.0f, -0.0f, -0.0f, -0.0f};
+      } else {
+        v = in ? operand(v) : -0.0f;
+      }
+      *reinterpret_cast<piece*>(&stage[buf][r * kStride + (q % kRowPieces) * W]) = v;
+    }
+  };
+  // acc is R's last result; O(acc) is taken at the next step.
+  auto step = [&](float acc, float to) {
+    const float acc_o = (kIn && !kOut) ? flush(acc, imask) : acc;
+    const float sum = acc_o + to;
+    return kOut ? flush(sum, rmask) : sum;
+  };
+  const bool folding_wave = R == 1 ? wave == 0 : true;
+  const uint32_t fr = R == 1 ? 0u : wave * kRowsPerWave + g % kRowsPerWave;
+  float acc = 0.0f;
+  if (stages > 0) {
+    load(0);
+    store(0, 0);
+  }
+  __syncthreads();
+  for (uint64_t st = 0; st < stages; ++st) {
+    const bool more = st + 1 < stages;
+    if (more) load(st + 1);
+    if (folding_wave) {
+      const uint32_t count = (uint32_t)(length - st * C < C ? length - st * C : C);
+      const uint32_t passes = (count + kPass - 1) / kPass;
+      const f32x4* src = reinterpret_cast<const f32x4*>(&stage[st & 1][fr * kStride]) + s * S4;
+      // The row's last pass, when it runs past the row's end: a step only
+      // at positions below the end (this lane's segment holds `valid` of
+      // them).  A -0.0 step is exact only after a step has gone through R,
+      // and a row's only contributor is its seed, so every mode guards it.
+      const bool ragged = !more && passes * kPass != count;
+      const uint32_t seg0 = (passes - 1) * kPass + 32u * s;
+      const uint32_t valid = count > seg0 ? (count - seg0 < 32u ? count - seg0 : 32u) : 0u;
+      // A loop over the passes (not unrolled: each relay variant appears
+      // once); the next pass's segment is read into nxt while cur is folded.
+      f32x4 cur[S4], nxt[S4];
+#pragma unroll
+      for (uint32_t k = 0; k < S4; ++k) cur[k] = src[k];
+      for (uint32_t p = 0; p < passes; ++p) {
+        const f32x4* next = src + (p + 1 < passes ? p + 1 : p) * (kPass / 4);
+#pragma unroll
+        for (uint32_t k = 0; k < S4; ++k) nxt[k] = next[k];
+        const bool seed = p == 0 && st == 0;
+        auto run = [&](auto seeded, auto f) { acc = tiler::relay_fold<S4, decltype(seeded)::value>(cur, acc, f); };
+        if (ragged && p + 1 == passes) {
+          // i counts the contributors taken in step order, the seed included
+          // (it takes no step), so i & 31 is a contributor's position in the
+          // hot lane's segment.
+          uint32_t i = seed ? 1u : 0u;
+          auto guarded = [&](float a0, float c) { return (i++ & 31u) < valid ? step(a0, c) : a0; };
+          if (seed) run(tiler::Step<1>{}, guarded);
+          else run(tiler::Step<0>{}, guarded);
+        } else if (seed) {
+          run(tiler::Step<1>{}, step);
+        } else {
+          run(tiler::Step<0>{}, step);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < S4; ++k) cur[k] = nxt[k];
+      }
+    }
+    if (more) store((uint32_t)((st + 1) & 1), st + 1);
+    __syncthreads();
+  }
+  if (folding_wave && s == 0 && g < kRowsPerWave && row0 + fr < nrows) out[row0 + fr] = tiler::canon(acc);
+}
 
 // The same stages under a FoldRule: a flushing contract's serial fold, and the
 // fused prologues (squared, scale-bias) over a trailing axis; one body per
@@ -328,10 +557,17 @@ __device__ __forceinline__ void staged_rule_dispatch(const float* __restrict__ x
                                                      float* __restrict__ out, const tiler::FoldRule& rule) {
   __shared__ __align__(16) float lds[kRuleStageFloats<R>];
   const bool in = rule.in_mode > 1u, res = rule.out_mode > 1u;
-  if (in && res) staged_rule_body<R, kVec, true, true>(x, nrows, length, out, rule, lds);
-  else if (in) staged_rule_body<R, kVec, true, false>(x, nrows, length, out, rule, lds);
-  else if (res) staged_rule_body<R, kVec, false, true>(x, nrows, length, out, rule, lds);
-  else staged_rule_body<R, kVec, false, false>(x, nrows, length, out, rule, lds);
+  if constexpr (R <= 16) {  // the relay fold (rows of at least 256 elements per stage)
+    if (in && res) staged_rule_relay_body<R, kVec, true, true>(x, nrows, length, out, rule, lds);
+    else if (in) staged_rule_relay_body<R, kVec, true, false>(x, nrows, length, out, rule, lds);
+    else if (res) staged_rule_relay_body<R, kVec, false, true>(x, nrows, length, out, rule, lds);
+    else staged_rule_relay_body<R, kVec, false, false>(x, nrows, length, out, rule, lds);
+  } else {
+    if (in && res) staged_rule_body<R, kVec, true, true>(x, nrows, length, out, rule, lds);
+    else if (in) staged_rule_body<R, kVec, true, false>(x, nrows, length, out, rule, lds);
+    else if (res) staged_rule_body<R, kVec, false, true>(x, nrows, length, out, rule, lds);
+    else staged_rule_body<R, kVec, false, false>(x, nrows, length, out, rule, lds);
+  }
 }
 #define TILER_SUM_STAGED_RULE(R)                                                                       \
   extern "C" __global__ void __launch_bounds__(256)                                                    \

@@ -20,6 +20,9 @@
 
 namespace {
 
+using tiler::relay_fold_chunk;
+using tiler::unrolled_while;
+
 constexpr uint32_t kStrictSeg = 1024;
 constexpr uint32_t kStrictWaves = 4;
 
@@ -477,60 +480,6 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
       y[at] = tiler::canon(y[at] * rc);
     }
   }
-}
-
-// f(Step<0>{}), f(Step<1>{}), ... f(Step<N - 1>{}) while f returns true: a
-// loop unrolled at compile time (the index is a constant in each call, so
-// register arrays indexed by it stay in registers), whatever the loop
-// unroller would decide for a body that holds a loop of its own.
-template <int J>
-struct Step {
-  static constexpr int value = J;
-};
-template <int J, int N, typename F>
-__device__ __forceinline__ void unrolled_while(F& f) {
-  if constexpr (J < N) {
-    if (f(Step<J>{})) unrolled_while<J + 1, N>(f);
-  }
-}
-
-// A DPP move of v across the lanes of each 16-lane row (kCtrl: row_shr:1 =
-// 0x111, lane i takes lane i - 1; row_ror:9 = 0x129, lane i takes lane
-// (i - 9) mod 16, so lanes 7 and 15 go to lanes 0 and 8).
-template <int kCtrl>
-__device__ __forceinline__ float dpp_move(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
-}
-
-// The relay fold of one ring chunk by one wave: lane 8 g + s holds in seg the
-// S4 float4 slots (4 S4 consecutive contributors, ascending) of segment s of
-// row g's chunk.  Row g's running sum enters the chunk in lane 8 g; each hop,
-// every lane adds its segment in order and a DPP move hands each sum to the
-// next lane of its group (the eighth hop back to lane 8 g), so the lane
-// holding row g's sum at hop s is lane 8 g + s and the chunk's 32 S4
-// contributors are added in ascending order.  The adds read registers only,
-// and one wave instruction advances the eight rows' chains.  What the other
-// lanes add is never read.
-template <uint32_t S4>
-__device__ __forceinline__ float relay_fold_chunk(const f32x4 (&seg)[S4], float acc) {
-  auto add = [&]() {
-#pragma unroll
-    for (uint32_t k = 0; k < S4; ++k) {
-      acc = acc + seg[k].x;
-      acc = acc + seg[k].y;
-      acc = acc + seg[k].z;
-      acc = acc + seg[k].w;
-    }
-  };
-  // A loop, not unrolled: the callers unroll their chunk loops over the
-  // resident pieces, which must stay small enough to unroll.
-#pragma unroll 1
-  for (int h = 0; h < 7; ++h) {
-    add();
-    acc = dpp_move<0x111>(acc);
-  }
-  add();
-  return dpp_move<0x129>(acc);
 }
 
 // Strict RMSNorm with a workgroup's rows resident in registers, for rows of
