@@ -204,26 +204,28 @@ tiler_contract_strict_f32_b64(const float* __restrict__ a, const float* __restri
 // Few output rows: output row i = blockIdx.y is the staged strict fold
 // (tiler_sum_f32_staged_r*, reduce.hip) of the products of A's row i with B's
 // rows, which are contiguous in k -- the same first-product fold, ascending k,
-// two roundings per step, bit for bit.  R output columns per workgroup.
-#define TILER_CONTRACT_STRICT_ROWS(R)                                                                  \
+// two roundings per step, bit for bit.  R output columns per workgroup; R in
+// {1, 4, 16} relay-fold the staged products (staged_relay_body), R = 64 folds
+// a row per lane (staged_fold_body).
+#define TILER_CONTRACT_STRICT_ROWS(R, BODY)                                                            \
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_contract_strict_f32_s##R(const float* __restrict__ a, const float* __restrict__ b,          \
                                      uint32_t m, uint32_t n, uint32_t k, float* __restrict__ c) {      \
     (void)m;                                                                                           \
     const uint64_t i = blockIdx.y;                                                                     \
-    staged_fold_body<R, true, true>(b, n, k, a + i * k, c + i * n);                                    \
+    BODY<R, true, true>(b, n, k, a + i * k, c + i * n);                                                \
   }                                                                                                    \
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_contract_strict_f32_s##R##_u(const float* __restrict__ a, const float* __restrict__ b,      \
                                          uint32_t m, uint32_t n, uint32_t k, float* __restrict__ c) {  \
     (void)m;                                                                                           \
     const uint64_t i = blockIdx.y;                                                                     \
-    staged_fold_body<R, false, true>(b, n, k, a + i * k, c + i * n);                                   \
+    BODY<R, false, true>(b, n, k, a + i * k, c + i * n);                                               \
   }
-TILER_CONTRACT_STRICT_ROWS(1)
-TILER_CONTRACT_STRICT_ROWS(4)
-TILER_CONTRACT_STRICT_ROWS(16)
-TILER_CONTRACT_STRICT_ROWS(64)
+TILER_CONTRACT_STRICT_ROWS(1, staged_relay_body)
+TILER_CONTRACT_STRICT_ROWS(4, staged_relay_body)
+TILER_CONTRACT_STRICT_ROWS(16, staged_relay_body)
+TILER_CONTRACT_STRICT_ROWS(64, staged_lane_body)
 
 // ---------------------------------------------------------------------------
 // bf16 MFMA contraction.

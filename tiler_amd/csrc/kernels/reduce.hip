@@ -211,9 +211,15 @@ __device__ __forceinline__ void staged_fold_body(const float* __restrict__ x, ui
 // -0.0, which leaves every sum unchanged (s + -0.0 == s for every s, the
 // zeros and NaN included), so whole passes are folded.  Same order, same
 // -0.0 seed, same commit as staged_fold_body.
-template <int R, bool kVec>
+//
+// kDot: the fold of products fl(a[e] * x[v*length + e]) (staged_fold_body's
+// kDot): the threads that stage x also load the matching elements of the
+// left row `a` (the same for every row, so the caches serve them) and stage
+// the rounded products, each rounded once as the fold would round it; the
+// relay then folds them as it folds a row of the sum.
+template <int R, bool kVec, bool kDot = false>
 __device__ __forceinline__ void staged_relay_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
-                                                  float* __restrict__ out) {
+                                                  const float* __restrict__ a, float* __restrict__ out) {
   static_assert(R == 1 || R == 4 || R == 16, "rows of at least 256 elements per stage");
   constexpr uint32_t C = 4096 / R;               // elements of a row per stage
   constexpr uint32_t kStride = C + 4;            // LDS row stride in floats (16-byte aligned)
@@ -238,8 +244,13 @@ __device__ __forceinline__ void staged_relay_body(const float* __restrict__ x, u
       const uint64_t e = st * C + (uint64_t)(q % kRowPieces) * W;
       if (row0 + r < nrows && e < length) {
         const float* src = x + (row0 + r) * length + e;
-        if constexpr (kVec) reg[i] = *reinterpret_cast<const f32x4*>(src);
-        else reg[i] = *src;
+        if constexpr (kVec) {
+          reg[i] = *reinterpret_cast<const f32x4*>(src);
+          if constexpr (kDot) reg[i] = *reinterpret_cast<const f32x4*>(a + e) * reg[i];  // two roundings: no FMA
+        } else {
+          reg[i] = *src;
+          if constexpr (kDot) reg[i] = a[e] * reg[i];
+        }
       } else {
         if constexpr (kVec) reg[i] = f32x4{nz, nz, nz, nz};
         else reg[i] = nz;
@@ -402,17 +413,17 @@ __device__ __forceinline__ void staged_rule_body(const float* __restrict__ x, ui
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_sum_f32_staged_r##R(const float* __restrict__ x, uint64_t nrows, uint64_t length,          \
                                 float* __restrict__ out) {                                             \
-    BODY<R, true>(x, nrows, length, out);                                                              \
+    BODY<R, true>(x, nrows, length, nullptr, out);                                                     \
   }                                                                                                    \
   extern "C" __global__ void __launch_bounds__(256)                                                    \
       tiler_sum_f32_staged_r##R##_u(const float* __restrict__ x, uint64_t nrows, uint64_t length,      \
                                     float* __restrict__ out) {                                         \
-    BODY<R, false>(x, nrows, length, out);                                                             \
+    BODY<R, false>(x, nrows, length, nullptr, out);                                                    \
   }
-template <int R, bool kVec>
+template <int R, bool kVec, bool kDot = false>
 __device__ __forceinline__ void staged_lane_body(const float* __restrict__ x, uint64_t nrows, uint64_t length,
-                                                 float* __restrict__ out) {
-  staged_fold_body<R, kVec, false>(x, nrows, length, nullptr, out);
+                                                 const float* __restrict__ a, float* __restrict__ out) {
+  staged_fold_body<R, kVec, kDot>(x, nrows, length, a, out);
 }
 TILER_SUM_STAGED(1, staged_relay_body)
 TILER_SUM_STAGED(4, staged_relay_body)

@@ -739,10 +739,13 @@ tiler_hip_status plan_contract_strict_f32(const Target& t, uint64_t m, uint64_t 
   if (m <= 16 && k >= 64) {
     // Few output rows (decode shapes): each output is the staged fold of the
     // products along one row of B (contiguous in k), one workgroup row per
-    // output row, R output columns per workgroup chosen as for the serial
-    // fold by the output count.  With k live the 4-byte-load form takes any k.
+    // output row, R output columns per workgroup chosen by the output count.
+    // R <= 16 relay-fold; up to 32 outputs per CU the relay's R = 16 still
+    // beat R = 64 on the device (1 x 8192 x 1024: 14.0 against 16.6 us; from
+    // 128 per CU R = 64 won, 1 x 32768 x 1024: 21.4 against 30.8 us).  With
+    // k live the 4-byte-load form takes any k.
     const uint64_t outputs = m * n, cus = t.compute_units;
-    const uint32_t R = outputs <= cus ? 1 : outputs <= 4 * cus ? 4 : outputs <= 16 * cus ? 16 : 64;
+    const uint32_t R = outputs <= cus ? 1 : outputs <= 4 * cus ? 4 : outputs <= 32 * cus ? 16 : 64;
     const bool vec = !live_k && k % 4 == 0 && aligned16(addr[a]) && aligned16(addr[b]);
     char name[40];
     std::snprintf(name, sizeof(name), "tiler_contract_strict_f32_s%u%s", R, vec ? "" : "_u");
