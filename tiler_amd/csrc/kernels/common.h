@@ -86,6 +86,17 @@ __device__ __forceinline__ uint32_t bf16_narrow(float v) {
 __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
   return bf16_narrow(lo) | (bf16_narrow(hi) << 16);
 }
+// bf16_pack2 in one v_cvt_pk_bf16_f32, which rounds to nearest even exactly
+// as bf16_narrow does on every non-NaN binary32 input (the narrowing
+// kernels' tests pin it at every rounding boundary); it keeps a NaN's sign
+// and payload, so NaNs are made the canonical 0x7fc00000 first, which it
+// narrows to 0x7fc0.
+typedef float f32x2_pair __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_pair __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16_pack2_rne(float lo, float hi) {
+  const f32x2_pair f = {canon(lo), canon(hi)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_pair));
+}
 
 // IEEE 754-2019 maximum with -0 < +0, NaN-propagating
 // (tiler-reference/src/softmax.rs:168-186).

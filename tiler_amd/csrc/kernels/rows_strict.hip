@@ -591,13 +591,16 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
       const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + e);
       u32x4 out;
       if constexpr (kBf16) {
-        auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
-          return tiler::bf16_narrow(tiler::canon(widen(wb) * (widen(xb) * sc)));
+        // Every workgroup reaches this pass at once, so its VALU work is
+        // issued four waves to a SIMD: the pair narrows in one instruction.
+        auto one = [&](uint32_t xb, uint32_t wb) -> float { return widen(wb) * (widen(xb) * sc); };
+        auto two = [&](uint32_t xw, uint32_t ww) -> uint32_t {
+          return tiler::bf16_pack2_rne(one(xw & 0xffffu, ww & 0xffffu), one(xw >> 16, ww >> 16));
         };
-        out.x = one(xv.x & 0xffffu, wv.x & 0xffffu) | (one(xv.x >> 16, wv.x >> 16) << 16);
-        out.y = one(xv.y & 0xffffu, wv.y & 0xffffu) | (one(xv.y >> 16, wv.y >> 16) << 16);
-        out.z = one(xv.z & 0xffffu, wv.z & 0xffffu) | (one(xv.z >> 16, wv.z >> 16) << 16);
-        out.w = one(xv.w & 0xffffu, wv.w & 0xffffu) | (one(xv.w >> 16, wv.w >> 16) << 16);
+        out.x = two(xv.x, wv.x);
+        out.y = two(xv.y, wv.y);
+        out.z = two(xv.z, wv.z);
+        out.w = two(xv.w, wv.w);
       } else {
         auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
           return __float_as_uint(tiler::canon(widen(wb) * (widen(xb) * sc)));
