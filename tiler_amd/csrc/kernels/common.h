@@ -369,4 +369,31 @@ __device__ __forceinline__ float relay_fold_chunk(const f32x4 (&seg)[S4], float 
   return relay_fold<S4>(seg, acc, [](float a, float c) { return a + c; });
 }
 
+// The strict sum's relay fold over `passes` (at most kMaxPasses) consecutive
+// 256-element passes of a row that lies contiguously in LDS at `row`
+// (16-byte aligned): lane 8 g + s of the folding wave, s = lane % 8, takes
+// elements 32 s .. 32 s + 31 of each pass, and the next pass's segment is
+// read while the current one is folded.  Row g's sum ends in lane 8 g.
+template <uint32_t kMaxPasses>
+__device__ __forceinline__ float relay_fold_row(const f32x4* row, uint32_t s, uint32_t passes, float acc) {
+  constexpr uint32_t S4 = 8;
+  const f32x4* src = row + s * S4;
+  f32x4 a[S4], b[S4];
+#pragma unroll
+  for (uint32_t k = 0; k < S4; ++k) a[k] = src[k];
+  auto pass = [&](auto ps) -> bool {
+    constexpr uint32_t p = decltype(ps)::value;
+    if (p >= passes) return false;
+    f32x4(&cur)[S4] = (p & 1) ? b : a;
+    f32x4(&nxt)[S4] = (p & 1) ? a : b;
+    const f32x4* next = src + (p + 1 < passes ? p + 1 : p) * (32u * S4 / 4u);
+#pragma unroll
+    for (uint32_t k = 0; k < S4; ++k) nxt[k] = next[k];
+    acc = relay_fold_chunk<S4>(cur, acc);
+    return true;
+  };
+  unrolled_while<0, kMaxPasses>(pass);
+  return acc;
+}
+
 }  // namespace tiler

@@ -278,22 +278,8 @@ __device__ __forceinline__ void staged_relay_body(const float* __restrict__ x, u
     if (folding_wave) {
       const uint32_t count = (uint32_t)(length - st * C < C ? length - st * C : C);
       const uint32_t passes = (count + kPass - 1) / kPass;
-      const f32x4* src = reinterpret_cast<const f32x4*>(&stage[st & 1][fr * kStride]) + s * S4;
-      f32x4 a[S4], b[S4];
-#pragma unroll
-      for (uint32_t k = 0; k < S4; ++k) a[k] = src[k];
-      auto pass = [&](auto ps) -> bool {
-        constexpr uint32_t p = decltype(ps)::value;
-        if (p >= passes) return false;
-        f32x4(&cur)[S4] = (p & 1) ? b : a;
-        f32x4(&nxt)[S4] = (p & 1) ? a : b;
-        const f32x4* next = src + (p + 1 < passes ? p + 1 : p) * (kPass / 4);
-#pragma unroll
-        for (uint32_t k = 0; k < S4; ++k) nxt[k] = next[k];
-        acc = tiler::relay_fold_chunk<S4>(cur, acc);
-        return true;
-      };
-      tiler::unrolled_while<0, kPasses>(pass);
+      acc = tiler::relay_fold_row<kPasses>(reinterpret_cast<const f32x4*>(&stage[st & 1][fr * kStride]), s, passes,
+                                           acc);
     }
     if (more) store((uint32_t)((st + 1) & 1));
     __syncthreads();

@@ -194,41 +194,58 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
       else reg[i] = raw{};
     }
   };
-  auto store = [&](uint32_t buf) {
+  // Squares past the row's end (or of a row past the last) are staged as
+  // -0.0 for the relay fold, which folds whole passes (s + -0.0 == s).
+  const f32x4 nz = {-0.0f, -0.0f, -0.0f, -0.0f};
+  auto store = [&](uint32_t buf, uint32_t s) {
 #pragma unroll
     for (uint32_t i = 0; i < kPer; ++i) {
       const uint32_t q = t + 256u * i, r = q / kRowPieces;
+      const bool in = row0 + r < rows && s * C + (q % kRowPieces) * W < extent;
       float* dst = &stage[buf][r * kStride + (q % kRowPieces) * W];
       if constexpr (!kVec) {
         const float v = kBf16 ? tiler::bf16_widen(reg[i]) : (float)reg[i];
-        *dst = v * v;
+        *dst = in ? v * v : -0.0f;
       } else if constexpr (kBf16) {  // 8 bf16 -> 8 squares
         const u32x4 u = reg[i];
         f32x4 lo, hi;
         lo.x = widen(u.x & 0xffffu); lo.y = widen(u.x >> 16); lo.z = widen(u.y & 0xffffu); lo.w = widen(u.y >> 16);
         hi.x = widen(u.z & 0xffffu); hi.y = widen(u.z >> 16); hi.z = widen(u.w & 0xffffu); hi.w = widen(u.w >> 16);
-        *reinterpret_cast<f32x4*>(dst) = lo * lo;
-        *reinterpret_cast<f32x4*>(dst + 4) = hi * hi;
+        *reinterpret_cast<f32x4*>(dst) = in ? lo * lo : nz;
+        *reinterpret_cast<f32x4*>(dst + 4) = in ? hi * hi : nz;
       } else {
         const u32x4 u = reg[i];
         f32x4 v;
         v.x = widen(u.x); v.y = widen(u.y); v.z = widen(u.z); v.w = widen(u.w);
-        *reinterpret_cast<f32x4*>(dst) = v * v;
+        *reinterpret_cast<f32x4*>(dst) = in ? v * v : nz;
       }
     }
   };
-  const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
-  const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < rows;
+  // R <= 16: the relay fold (tiler::relay_fold_row), the folding waves'
+  // 8-lane groups each taking a row in 256-element passes (R = 1: wave 0;
+  // R = 4: wave w row w; R = 16: wave w rows 4 w .. 4 w + 3), every dependent
+  // add on registers.  R = 64: lane r / 4 of wave r % 4 folds row r.
+  constexpr bool kRelay = R <= 16;
+  constexpr uint32_t kRowsPerWave = R == 16 ? 4u : 1u;
+  const uint32_t lane = t & 63u, wave = t >> 6, g = lane >> 3, sg = lane & 7u;
+  const uint32_t fr = kRelay ? (R == 1 ? 0u : wave * kRowsPerWave + g % kRowsPerWave)
+                             : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
+  const bool folds = kRelay ? (R == 1 ? wave == 0 : true)
+                            : (t & 63u) < (uint32_t)R / 4u && row0 + fr < rows;
   float acc = -0.0f;
   if (stages > 0) {
     load(0);
-    store(0);
+    store(0, 0);
   }
   __syncthreads();
   for (uint32_t s = 0; s < stages; ++s) {
     const bool more = s + 1 < stages;
     if (more) load(s + 1);
-    if (folds) {
+    if (kRelay && folds) {
+      const uint32_t count = extent - s * C < C ? extent - s * C : C;
+      acc = tiler::relay_fold_row<(kRelay ? C / 256u : 1u)>(reinterpret_cast<const f32x4*>(&stage[s & 1][fr * kStride]),
+                                                            sg, (count + 255u) / 256u, acc);
+    } else if (folds) {
       const float* row = &stage[s & 1][fr * kStride];
       const uint32_t count = extent - s * C < C ? extent - s * C : C;
       if (count == C) {
@@ -265,10 +282,12 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
         for (uint32_t c = 0; c < count; ++c) acc = acc + row[c];
       }
     }
-    if (more) store((s + 1) & 1u);
+    if (more) store((s + 1) & 1u, s + 1);
     __syncthreads();
   }
-  if (folds) scale[fr] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
+  // A relay group's row sum is in its lane 8 g.
+  if (kRelay ? folds && sg == 0 && g < kRowsPerWave && row0 + fr < rows : folds)
+    scale[fr] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
   __syncthreads();
   for (uint32_t r = 0; r < (uint32_t)R; ++r) {
     if (row0 + r >= rows) break;
@@ -387,8 +406,15 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
     }
     if (cl == 0) rowmax[cr] = m;
   }
-  const uint32_t fr = R == 1 ? 0u : (t & 63u) * 4u + (t >> 6);  // the row this lane folds
-  const bool folds = (R == 1 ? t == 0 : (t & 63u) < (uint32_t)R / 4u) && row0 + fr < rows;
+  // The relay fold (tiler::relay_fold_row): the folding waves' 8-lane groups
+  // each take a row in 256-element passes (R = 1: wave 0; R = 4: wave w row
+  // w; R = 16: wave w rows 4 w .. 4 w + 3), every dependent add on
+  // registers; a group's row sum ends in its lane 8 g.
+  static_assert(R == 1 || R == 4 || R == 16, "stages of at least 256 elements per row");
+  constexpr uint32_t kRowsPerWave = R == 16 ? 4u : 1u;
+  const uint32_t lane = t & 63u, wave = t >> 6, g = lane >> 3, sg = lane & 7u;
+  const uint32_t fr = R == 1 ? 0u : wave * kRowsPerWave + g % kRowsPerWave;  // the row this group folds
+  const bool folds = R == 1 ? wave == 0 : true;
   __syncthreads();
   // Pass 2: the exponents, folded in order.
   piece reg[kPer];
@@ -408,8 +434,13 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
       float* dst = &stage[buf][r * kStride + (q % kRowPieces) * W];
       // The exponents also go to y, where the output pass scales them.
       const uint32_t e = sbuf * C + (q % kRowPieces) * W;
-      // Slots past the row's end or the last row are never folded.
-      if (decltype(guard)::value && !(row0 + r < rows && e < extent)) continue;
+      // Slots past the row's end or the last row hold -0.0, which leaves the
+      // relay's sums unchanged (s + -0.0 == s), and are not written to y.
+      if (decltype(guard)::value && !(row0 + r < rows && e < extent)) {
+        if constexpr (kVec) *reinterpret_cast<f32x4*>(dst) = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};
+        else *dst = -0.0f;
+        continue;
+      }
       if constexpr (kVec) {
         f32x4 ev;
         ev.x = tiler::exp_f32_cr(reg[i].x - m, tab);
@@ -441,22 +472,15 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
     const bool more = s + 1 < stages;
     if (more) load(s + 1);
     if (folds) {
-      const float* row = &stage[s & 1][fr * kStride];
       const uint32_t count = extent - s * C < C ? extent - s * C : C;
-      uint32_t c = 0;
-      for (; c + 4 <= count; c += 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(row + c);
-        acc = acc + v.x;
-        acc = acc + v.y;
-        acc = acc + v.z;
-        acc = acc + v.w;
-      }
-      for (; c < count; ++c) acc = acc + row[c];
+      acc = tiler::relay_fold_row<C / 256u>(reinterpret_cast<const f32x4*>(&stage[s & 1][fr * kStride]), sg,
+                                            (count + 255u) / 256u, acc);
     }
     if (more) store((s + 1) & 1u, s + 1);
     __syncthreads();
   }
-  if (folds) recip[fr] = 1.0f / acc;  // softmax.rs:302-313: the reciprocal, then a multiply
+  // softmax.rs:302-313: the reciprocal, then a multiply.
+  if (folds && sg == 0 && g < kRowsPerWave && row0 + fr < rows) recip[fr] = 1.0f / acc;
   __syncthreads();
   // Pass 3: y, over the workgroup's rows as one flat run of pieces (the
   // iterations are independent, so several loads are in flight per thread).
