@@ -333,6 +333,8 @@ def test_strict_rms_norm_is_the_reference_fold(ctx):
     (20000, 64, L.BF16, True, "_strict_r64"),   # one stage
     (700, 1001, L.F32, False, "_strict_r1_u"),  # 4-byte loads, a weight row per row, a ragged stage
     (300, 1030, L.BF16, True, "_strict_r1_u"),
+    (32, 4096, L.BF16, True, "_strict_r1"),     # decode rows: one row per workgroup, one whole stage
+    (3, 10000, L.F32, True, "_strict_r1"),      # long rows: three stages, the last ragged
     # rows held in registers, 8 per workgroup (tiler_rms_norm_*_strict_rr8_p*)
     (8192, 4096, L.BF16, True, "_strict_rr8_p16"),   # the C2 configuration
     (2050, 1100, L.F32, False, "_strict_rr8_p16"),   # a weight row per row, a ragged last workgroup, a partial chunk
@@ -399,6 +401,8 @@ def test_strict_softmax_is_the_reference_fold(ctx):
     (1500, 301, "_strict_r4_u"),   # 4-byte loads, a ragged last stage
     (300, 72, "_strict_r1"),
     (1024, 2048, "_strict_r4"),    # 16-byte loads, whole stages, four rows per workgroup
+    (32, 2048, "_strict_r1"),      # decode rows: one row per workgroup, one partial stage
+    (4, 9000, "_strict_r1"),       # long rows: three stages, the last ragged
     # rows held in registers, 8 per workgroup (tiler_softmax_f32_strict_rr8_p*)
     (4096, 200, "_strict_rr8_p8"),   # two chunks, the second partial
     (4096, 512, "_strict_rr8_p8"),

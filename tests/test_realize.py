@@ -165,6 +165,13 @@ def test_contraction_paths():
     assert big.symbols == ["tiler_contract_strict_f32_b64"] and big.dispatches[0].grid == (32, 32, 1)
     few = realize(L.PROGRAM_CONTRACTION, (1, 1024, 1024))
     assert few.symbols == ["tiler_contract_strict_f32_s4"] and few.dispatches[0].grid == (256, 1, 1)
+    # up to 32 outputs per CU the relay-folded R = 16, beyond them R = 64 (a lane per output)
+    slice_ = realize(L.PROGRAM_CONTRACTION, (1, 8192, 1024))
+    assert slice_.symbols == ["tiler_contract_strict_f32_s16"] and slice_.dispatches[0].grid == (512, 1, 1)
+    vocab = realize(L.PROGRAM_CONTRACTION, (1, 151936, 1024))
+    assert vocab.symbols == ["tiler_contract_strict_f32_s64"] and vocab.dispatches[0].grid == (2374, 1, 1)
+    prefill = realize(L.PROGRAM_CONTRACTION, (10, 2048, 1024))
+    assert prefill.symbols == ["tiler_contract_strict_f32_s64"] and prefill.dispatches[0].grid == (32, 10, 1)
     for rz in (blocked, big, few):
         _check_segments(rz)
 
