@@ -100,7 +100,7 @@ def test_reference_split_rows_on_the_device(ctx, reading):
                                                (5, 20000, L.REGION_ALIGNED16), (1, 1, L.REGION_ALIGNED16),
                                                (10, 100, L.REGION_ALIGNED16), (1, 70, L.REGION_ALIGNED16),
                                                (700, 1000, L.REGION_ALIGNED16), (3, 512, L.REGION_ALIGNED16),
-                                               (700, 1001, 0)])
+                                               (700, 1001, 0), (701, 1000, L.REGION_ALIGNED16)])
 @pytest.mark.parametrize("modes", MODES)
 def test_serial_sum_under_modes(ctx, rows, extent, flags, modes):
     rng = np.random.default_rng(rows * 7 + extent)

@@ -330,6 +330,7 @@ def test_strict_rms_norm_is_the_reference_fold(ctx):
 @pytest.mark.parametrize("rows,extent,dtype,broadcast,form", [
     (4096, 4104, L.BF16, True, "_strict_r16"),  # 16-byte loads, staged (rows past 4096 bf16)
     (1500, 300, L.F32, True, "_strict_r4"),
+    (1025, 2000, L.BF16, True, "_strict_r4"),  # the last workgroup holding one row
     (20000, 64, L.BF16, True, "_strict_r64"),   # one stage
     (700, 1001, L.F32, False, "_strict_r1_u"),  # 4-byte loads, a weight row per row, a ragged stage
     (300, 1030, L.BF16, True, "_strict_r1_u"),
@@ -401,6 +402,7 @@ def test_strict_softmax_is_the_reference_fold(ctx):
     (1500, 301, "_strict_r4_u"),   # 4-byte loads, a ragged last stage
     (300, 72, "_strict_r1"),
     (1024, 2048, "_strict_r4"),    # 16-byte loads, whole stages, four rows per workgroup
+    (1025, 2048, "_strict_r4"),    # the last workgroup holding one row
     (32, 2048, "_strict_r1"),      # decode rows: one row per workgroup, one partial stage
     (4, 9000, "_strict_r1"),       # long rows: three stages, the last ragged
     # rows held in registers, 8 per workgroup (tiler_softmax_f32_strict_rr8_p*)

@@ -70,6 +70,7 @@ def _order_sensitive(rng, rows, extent):
     (5, 9999, 0),      # rows off the 16-byte grid: 4-byte loads
     (4, 3000, 4),      # an unaligned base
     (700, 1500, 0),    # four rows per workgroup (one per wave), a ragged last workgroup
+    (701, 1500, 0),    # four rows per workgroup, the last holding one row
     (2000, 300, 0),    # sixteen rows per workgroup
     (3000, 259, 0),    # sixteen rows, 4-byte loads
     (5000, 129, 0),    # sixty-four rows per workgroup, 4-byte loads
