@@ -47,14 +47,15 @@ class OracleError(RuntimeError):
 def build() -> str:
     """Compiles the restatement with strict binary32 arithmetic (no FMA)."""
     os.makedirs(BUILD_DIR, exist_ok=True)
+    tmp = f"{LIB_PATH}.{os.getpid()}.tmp"  # one per process: parallel test workers build at once
     cmd = [
         "gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
-        "-Wall", "-o", LIB_PATH + ".tmp", os.path.join(HERE, "tiler_oracle.c"),
+        "-Wall", "-o", tmp, os.path.join(HERE, "tiler_oracle.c"),
         os.path.join(HERE, "device_exp_audit.c"),
         "-lquadmath", "-lm", "-lpthread",
     ]
     subprocess.run(cmd, check=True)
-    os.replace(LIB_PATH + ".tmp", LIB_PATH)
+    os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
 

@@ -144,9 +144,17 @@ FS, FP = L.SUBNORMALS_FLUSH_SIGN, L.SUBNORMALS_FLUSH_POSITIVE
     (L.PROGRAM_FOLD, (4, 5, 6), dict(rank=3, grouping=(5,), variant=L.FOLD_SQUARED), ["tiler_fold_f32_m"]),
     (L.PROGRAM_FOLD, (4, 5, 6), dict(rank=3, grouping=(5,), variant=L.FOLD_MAXIMUM), ["tiler_fold_maximum_f32"]),
     # rows: the serial forms that take the modes, whatever the permissions
-    (L.PROGRAM_RMS_NORM, (8192, 4096), dict(scalars=(EPS,), dtype=L.BF16, permissions=RE),
+    (L.PROGRAM_RMS_NORM, (8192, 4104), dict(scalars=(EPS,), dtype=L.BF16, permissions=RE),
      ["tiler_rms_norm_bf16_strict"]),
     (L.PROGRAM_SOFTMAX, (2, 100), {}, ["tiler_softmax_f32_strict"]),
+    # rows the register-resident forms hold take their _m forms
+    (L.PROGRAM_RMS_NORM, (8192, 4096), dict(scalars=(EPS,), dtype=L.BF16, permissions=RE),
+     ["tiler_rms_norm_bf16_strict_rr8_p16_m"]),
+    (L.PROGRAM_RMS_NORM, (2048, 1024), dict(scalars=(EPS,), flags=L.REGION_ALIGNED16),
+     ["tiler_rms_norm_f32_strict_rr8_p8_m"]),
+    (L.PROGRAM_SOFTMAX, (8192, 2048), {}, ["tiler_softmax_f32_strict_rr8_p16_m"]),
+    (L.PROGRAM_SOFTMAX, (4096, 1024), {}, ["tiler_softmax_f32_strict_rr8_p8_m"]),
+    (L.PROGRAM_SOFTMAX, (1024, 2048), {}, ["tiler_softmax_f32_strict"]),
     # maps: the scalar forms with the modes; bf16 expressions: the one-element form
     (L.PROGRAM_POINTWISE, (1024,), dict(variant=L.MAP_SILU), ["tiler_map_f32_m"]),
     (L.PROGRAM_POINTWISE, (1024,), dict(variant=L.MAP_ADD, dtype=L.BF16), ["tiler_map_bf16_m"]),

@@ -233,6 +233,74 @@ def test_softmax_under_modes(ctx, modes):
     assert np.array_equal(bits(got), bits(want))
 
 
+RESIDENT_RMS = [
+    # (rows, extent, dtype, kernel suffix): rows held in registers, 8 per
+    # workgroup (tiler_rms_norm_*_strict_rr8_p*_m)
+    (2048, 1000, L.BF16, "_strict_rr8_p8_m"),   # a partial fourth chunk
+    (2050, 1100, L.F32, "_strict_rr8_p16_m"),   # a ragged last workgroup, a partial chunk
+    (2100, 4096, L.BF16, "_strict_rr8_p16_m"),  # the longest resident row
+    (2048, 64, L.F32, "_strict_rr8_p8_m"),      # one partial chunk
+]
+
+
+@pytest.mark.parametrize("rows,extent,dtype,kernel", RESIDENT_RMS)
+@pytest.mark.parametrize("modes", MODES)
+def test_resident_rms_norm_under_modes(ctx, rows, extent, dtype, kernel, modes):
+    """The register-resident strict RMSNorm under the modes: rows of ~2^-70
+    (subnormal squares), rows of normal values, rows opening with subnormal
+    entries, a weight with subnormal entries, bit for bit with the oracle."""
+    im, rm = modes
+    rng = np.random.default_rng(rows + extent)
+    x = (rng.standard_normal((rows, extent)) * 2.0 ** -70).astype(np.float32)
+    x[::7] = rng.standard_normal((len(range(0, rows, 7)), extent)).astype(np.float32)
+    x[1::5, :10] = tiny_f32(rng, 10 * len(range(1, rows, 5))).reshape(-1, 10)
+    w = rng.normal(1.0, 0.1, extent).astype(np.float32)
+    w[:5] = tiny_f32(rng, 5)
+    if dtype == L.BF16:
+        x = oracle.bf16_widen(oracle.bf16_narrow(x)).reshape(x.shape)
+        w = oracle.bf16_widen(oracle.bf16_narrow(w)).reshape(w.shape)
+    rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=dtype, scalars=(0x3727C5AC,), input_subnormals=im,
+                 result_subnormals=rm, flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, permissions=RE, ctx=ctx)
+    print(f"[modes rms] {rz.symbols} {rows}x{extent} modes=({im},{rm})", flush=True)
+    assert len(rz.symbols) == 1 and rz.symbols[0].endswith(kernel), rz.symbols
+    host = [x, w] if dtype == L.F32 else [oracle.bf16_narrow(x).reshape(x.shape), oracle.bf16_narrow(w)]
+    got = _route(ctx, rz, host, (rows, extent), np.float32 if dtype == L.F32 else np.uint16)
+    want = oracle.rms_norm_f32(x, np.broadcast_to(w, x.shape).copy(), x.shape, 1, 0x3727C5AC, input_mode=om(im),
+                               result_mode=om(rm)).reshape(rows, extent)
+    if dtype == L.BF16:
+        assert np.array_equal(got, oracle.bf16_narrow(want).reshape(rows, extent))
+    else:
+        assert np.array_equal(bits(got), bits(want))
+
+
+RESIDENT_SOFTMAX = [
+    # (rows, extent, kernel suffix): tiler_softmax_f32_strict_rr8_p*_m
+    (4096, 200, "_strict_rr8_p8_m"),    # two chunks, the second partial
+    (2050, 1100, "_strict_rr8_p16_m"),  # a ragged last workgroup, a partial ninth chunk
+    (2048, 2048, "_strict_rr8_p16_m"),  # two whole ring rounds
+]
+
+
+@pytest.mark.parametrize("rows,extent,kernel", RESIDENT_SOFTMAX)
+@pytest.mark.parametrize("modes", MODES)
+def test_resident_softmax_under_modes(ctx, rows, extent, kernel, modes):
+    """The register-resident strict softmax under the modes: rows spread over
+    ~100 below their maximum (subnormal exponents and products), rows of
+    subnormal inputs, and a NaN row, bit for bit with the oracle."""
+    im, rm = modes
+    rng = np.random.default_rng(rows * 3 + extent)
+    x = rng.uniform(-100.0, 0.0, (rows, extent)).astype(np.float32)
+    x[1::9] = tiny_f32(rng, extent * len(range(1, rows, 9))).reshape(-1, extent)
+    x[5, extent // 2] = np.nan
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), input_subnormals=im, result_subnormals=rm, permissions=RE,
+                 flags=L.REGION_ALIGNED16, ctx=ctx)
+    print(f"[modes softmax] {rz.symbols} {rows}x{extent} modes=({im},{rm})", flush=True)
+    assert len(rz.symbols) == 1 and rz.symbols[0].endswith(kernel), rz.symbols
+    got = _route(ctx, rz, [x], (rows, extent), np.float32)
+    want = oracle.softmax_f32(x, x.shape, 1, input_mode=om(im), result_mode=om(rm)).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want))
+
+
 def _map(ctx, op, dtype, x, x2=None, a=0.0, b=0.0, modes=(P, P)):
     n = x.size
     import struct

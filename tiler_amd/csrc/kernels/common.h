@@ -42,6 +42,23 @@ __device__ __forceinline__ float subnormal(uint32_t mode, float v) {
   return mode == 2u ? __uint_as_float(b & 0x80000000u) : 0.0f;
 }
 
+// subnormal(mode, .) as two masks set up once: a class test (v_cmp_class,
+// classes 4 and 7: negative and positive denormal), a mask keeping the sign
+// (mode 2) or nothing (mode 3), and a select.
+struct Flush {
+  uint32_t cls, keep;
+  __device__ explicit Flush(uint32_t mode) : cls(mode > 1u ? 0x90u : 0u), keep(mode == 2u ? 0x80000000u : 0u) {}
+  __device__ float operator()(float v) const {
+    return __builtin_amdgcn_classf(v, cls) ? __uint_as_float(__float_as_uint(v) & keep) : v;
+  }
+};
+// subnormal(out, .) then subnormal(in, .): a result flushed, then read as an
+// operand, in one flush.  A subnormal result is a zero after a flushing out
+// mode, which the in mode leaves alone; otherwise the in mode decides.
+__device__ __forceinline__ Flush result_as_operand(uint32_t in_mode, uint32_t out_mode) {
+  return Flush(out_mode > 1u ? out_mode : in_mode);
+}
+
 // The per-contributor rule of a serial sum under a declared contract: the
 // prologue (none; the square, SquaredSerialSum; x * scale + bias,
 // FusedMultiplyAddSerialSum, schedule/model.rs:709-760), the two subnormal

@@ -526,10 +526,23 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
 //   (rms_norm.rs:177-187);
 // * y = canon(fl(w * fl(x * s))) from the registers, weight after the
 //   normalization (rms_norm.rs:474-485), narrowed once for bf16.
-template <typename T, int R, int P>
+// The _m forms (kModes, here and in the resident softmax) take a flushing
+// contract's two subnormal modes (tiler::subnormal) at every arithmetic site
+// as rms_norm.rs:405-489 and softmax.rs:200-315 apply them: O (the in mode)
+// on each operand, R (the out mode) on each result.  Every computed value but
+// the outputs is read only as an operand, so the kernels carry O(value): F,
+// O after R, is one flush (tiler::result_as_operand).  The reference's fold
+// acc = R(O(acc) + O(c)), seeded at the first contributor, then carries
+// b = O(acc) as b = F(b + F(c)) from -0.0 (-0.0 + F(c) = F(c) = O(c), c being
+// a result).  The contributors F(c) -- squares, exponents -- are +0, at least
+// 2^-126, infinite or NaN, and so is b, so b + F(c) is never subnormal and F
+// leaves it: under the modes the fold is the plain relay fold of the flushed
+// contributors, the -0.0 padding included.
+template <typename T, int R, int P, bool kModes = false>
 __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x, const T* __restrict__ w,
                                                          uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,
-                                                         uint32_t extent, float eps) {
+                                                         uint32_t extent, float eps, uint32_t im = 1u,
+                                                         uint32_t rm = 1u) {
   static_assert(R == 8, "eight rows: one 8-lane relay group per row in wave 0");
   constexpr bool kBf16 = sizeof(T) == 2;
   constexpr uint32_t E = 16 / sizeof(T);  // elements per piece
@@ -545,6 +558,18 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
   auto widen = [](uint32_t bits) -> float {
     if constexpr (kBf16) return tiler::bf16_widen(bits);
     else return __uint_as_float(bits);
+  };
+  const tiler::Flush O(im), Rz(rm), F = tiler::result_as_operand(im, rm);
+  auto square = [&](f32x4 a) -> f32x4 {
+    if constexpr (kModes) {  // F(O(x) * O(x))
+      auto one = [&](float e) {
+        const float o = O(e);
+        return F(o * o);
+      };
+      return f32x4{one(a.x), one(a.y), one(a.z), one(a.w)};
+    } else {
+      return a * a;
+    }
   };
   // Piece j is loaded while chunk j - W is written (W ahead): with every
   // piece requested at once the memory system completes chunk 0 late, and
@@ -582,12 +607,17 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
       f32x4 lo, hi;
       lo.x = widen(u.x & 0xffffu); lo.y = widen(u.x >> 16); lo.z = widen(u.y & 0xffffu); lo.w = widen(u.y >> 16);
       hi.x = widen(u.z & 0xffffu); hi.y = widen(u.z >> 16); hi.z = widen(u.w & 0xffffu); hi.w = widen(u.w >> 16);
-      dst[0] = in ? lo * lo : nz;
-      dst[64] = in ? hi * hi : nz;
+      if constexpr (kModes) {
+        dst[0] = in ? square(lo) : nz;
+        dst[64] = in ? square(hi) : nz;
+      } else {
+        dst[0] = in ? lo * lo : nz;
+        dst[64] = in ? hi * hi : nz;
+      }
     } else {
       f32x4 a;
       a.x = widen(u.x); a.y = widen(u.y); a.z = widen(u.z); a.w = widen(u.w);
-      dst[0] = in ? a * a : nz;
+      dst[0] = in ? square(a) : nz;
     }
     __syncthreads();
     if (wave == 0) {
@@ -601,10 +631,21 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
   };
   unrolled_while<0, P>(chunk);
   // Row g's sum is in lane 8 g after the last chunk's final hop.
-  if (wave == 0 && (lane & 7u) == 0) scale[lane >> 3] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
+  if (wave == 0 && (lane & 7u) == 0) {
+    if constexpr (kModes)  // O(s) = F(rsqrt(F(F(acc / N) + O(eps)))), N a normal number
+      scale[lane >> 3] = F(tiler::rsqrt_f32_cr(F(F(acc / (float)extent) + O(eps))));
+    else
+      scale[lane >> 3] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
+  }
   __syncthreads();
   if (!row_ok) return;
   const float sc = scale[r];
+  auto scaled = [&](float xf, float wf) -> float {
+    if constexpr (kModes)  // R(O(w) * F(O(x) * O(s)))
+      return Rz(O(wf) * F(O(xf) * sc));
+    else
+      return wf * (xf * sc);
+  };
   const T* wr = w + (row0 + r) * w_row_stride;
   T* yr = y + (row0 + r) * extent;
 #pragma unroll
@@ -617,7 +658,7 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
       if constexpr (kBf16) {
         // Every workgroup reaches this pass at once, so its VALU work is
         // issued four waves to a SIMD: the pair narrows in one instruction.
-        auto one = [&](uint32_t xb, uint32_t wb) -> float { return widen(wb) * (widen(xb) * sc); };
+        auto one = [&](uint32_t xb, uint32_t wb) -> float { return scaled(widen(xb), widen(wb)); };
         auto two = [&](uint32_t xw, uint32_t ww) -> uint32_t {
           return tiler::bf16_pack2_rne(one(xw & 0xffffu, ww & 0xffffu), one(xw >> 16, ww >> 16));
         };
@@ -627,7 +668,7 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
         out.w = two(xv.w, wv.w);
       } else {
         auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
-          return __float_as_uint(tiler::canon(widen(wb) * (widen(xb) * sc)));
+          return __float_as_uint(tiler::canon(scaled(widen(xb), widen(wb))));
         };
         out.x = one(xv.x, wv.x);
         out.y = one(xv.y, wv.y);
@@ -665,9 +706,10 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
 // * the exponent is exp_f32_cr_nonpositive, since s = fl(x - m) <= 0 or NaN;
 // * the output's NaN test is the row's: an e is NaN only where d is, and
 //   e <= 1 <= d, so a product e * fl(1 / d) is NaN exactly when d is.
-template <int R, int P>
+template <int R, int P, bool kModes = false>
 __device__ __forceinline__ void softmax_strict_resident_body(const float* __restrict__ x, float* __restrict__ y,
-                                                             uint64_t rows, uint32_t extent) {
+                                                             uint64_t rows, uint32_t extent, uint32_t im = 1u,
+                                                             uint32_t rm = 1u) {
   static_assert(R == 8, "eight rows: one 8-lane relay group per row in wave 0");
   constexpr int Q = 8;               // ring chunks: the fold runs once per Q chunks
   constexpr uint32_t kChunk = 64 * 4;  // float4 slots per 128-column chunk: slot k of lane L at k * 64 + L
@@ -694,12 +736,20 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
 #pragma unroll
   for (uint32_t o = 16; o >= 1; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 64));
   __syncthreads();  // the exponent table
+  const tiler::Flush O(im), Rz(rm), F = tiler::result_as_operand(im, rm);
+  const float om = O(m);
+  auto expo = [&](float xv) {
+    if constexpr (kModes)  // F(exp(F(O(x) - O(m)))): an argument <= 0 or NaN, O being monotone
+      return F(tiler::exp_f32_cr_nonpositive(F(O(xv) - om), tab));
+    else
+      return tiler::exp_f32_cr_nonpositive(xv - m, tab);
+  };
 #pragma unroll
   for (int j = 0; j < P; ++j) {
-    v[j].x = tiler::exp_f32_cr_nonpositive(v[j].x - m, tab);
-    v[j].y = tiler::exp_f32_cr_nonpositive(v[j].y - m, tab);
-    v[j].z = tiler::exp_f32_cr_nonpositive(v[j].z - m, tab);
-    v[j].w = tiler::exp_f32_cr_nonpositive(v[j].w - m, tab);
+    v[j].x = expo(v[j].x);
+    v[j].y = expo(v[j].y);
+    v[j].z = expo(v[j].z);
+    v[j].w = expo(v[j].w);
   }
   // Wave 0 relay-folds (relay_fold_chunk): lane 8 g + s holds segment s
   // (16 columns) of row g's chunk.  Columns past the row's end go to the
@@ -742,7 +792,7 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
   };
   unrolled_while<0, (P + Q - 1) / Q>(round);
   // Row g's sum is in lane 8 g after the last chunk's final hop.
-  if (wave == 0 && (lane & 7u) == 0) recip[lane >> 3] = 1.0f / acc;
+  if (wave == 0 && (lane & 7u) == 0) recip[lane >> 3] = kModes ? F(1.0f / acc) : 1.0f / acc;
   __syncthreads();
   if (!row_ok) return;
   const float rc = recip[r];
@@ -753,8 +803,14 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
   for (int j = 0; j < P; ++j) {
     const uint32_t e = 4u * (l + 32u * j);
     if (e < extent) {
-      const f32x4 o = {nan_row ? qnan : v[j].x * rc, nan_row ? qnan : v[j].y * rc, nan_row ? qnan : v[j].z * rc,
-                       nan_row ? qnan : v[j].w * rc};
+      f32x4 o;
+      if constexpr (kModes) {  // canon(R(O(e) * O(r)))
+        auto one = [&](float e) { return tiler::canon(Rz(e * rc)); };
+        o = f32x4{one(v[j].x), one(v[j].y), one(v[j].z), one(v[j].w)};
+      } else {
+        o = f32x4{nan_row ? qnan : v[j].x * rc, nan_row ? qnan : v[j].y * rc, nan_row ? qnan : v[j].z * rc,
+                  nan_row ? qnan : v[j].w * rc};
+      }
       __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + e));
     }
   }
@@ -767,6 +823,12 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
       tiler_softmax_f32_strict_rr##R##_p##P(const float* __restrict__ x, float* __restrict__ y,       \
                                             uint64_t rows, uint32_t extent) {                         \
     softmax_strict_resident_body<R, P>(x, y, rows, extent);                                           \
+  }                                                                                                   \
+  extern "C" __global__ void __launch_bounds__(32 * R)                                                \
+      tiler_softmax_f32_strict_rr##R##_p##P##_m(const float* __restrict__ x, float* __restrict__ y,   \
+                                                uint64_t rows, uint32_t extent, uint32_t in_mode,     \
+                                                uint32_t out_mode) {                                  \
+    softmax_strict_resident_body<R, P, true>(x, y, rows, extent, in_mode, out_mode);                 \
   }
 TILER_SOFTMAX_STRICT_RESIDENT(8, 16)
 TILER_SOFTMAX_STRICT_RESIDENT(8, 8)
@@ -777,6 +839,14 @@ TILER_SOFTMAX_STRICT_RESIDENT(8, 8)
                                                 uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,\
                                                 uint32_t extent, float eps) {                         \
     rms_strict_resident_body<T, R, P>(x, w, w_row_stride, y, rows, extent, eps);                      \
+  }                                                                                                   \
+  extern "C" __global__ void __launch_bounds__(32 * R)                                                \
+      tiler_rms_norm_##TY##_strict_rr##R##_p##P##_m(const T* __restrict__ x, const T* __restrict__ w, \
+                                                    uint64_t w_row_stride, T* __restrict__ y,         \
+                                                    uint64_t rows, uint32_t extent, float eps,        \
+                                                    uint32_t in_mode, uint32_t out_mode) {            \
+    rms_strict_resident_body<T, R, P, true>(x, w, w_row_stride, y, rows, extent, eps, in_mode,        \
+                                            out_mode);                                                \
   }
 TILER_RMS_STRICT_RESIDENT(bf16, uint16_t, 8, 16)
 TILER_RMS_STRICT_RESIDENT(bf16, uint16_t, 8, 8)

@@ -292,7 +292,8 @@ tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_b
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
                                Program& p, bool strict, uint32_t in_mode, uint32_t out_mode) {
   // A flushing contract: the serial fold with the modes at every site (the
-  // one-wave-per-row strict kernel, which takes them), whatever the topology.
+  // register-resident or one-wave-per-row strict kernel, which take them),
+  // whatever the topology.
   const bool modes = in_mode > 1 || out_mode > 1;
   if (modes) strict = true;
   float eps;
@@ -315,20 +316,22 @@ tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_b
   const bool al = aligned16(addr[x]) && aligned16(addr[w]) && aligned16(addr[y]) && (extent * elem) % 16 == 0;
   const uint64_t wstride = weight_broadcast ? 0 : extent;
   char name[64];
+  const uint64_t cus = t.compute_units;
+  const uint64_t per16 = 16 / elem;  // elements per 16-byte piece
+  if (strict && al && extent % per16 == 0 && extent >= 16 * per16 && extent <= 512 * per16 && rows >= 8 * cus) {
+    // Rows of at most 512 pieces held in registers, 8 per workgroup: x read
+    // once, y written once, the fold of the squares 8 rows per wave
+    // instruction (under a flushing contract the _m form, with the modes).
+    if ((rows + 7) / 8 > 0x7fffffffull)
+      return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+    std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict_rr8_p%u%s", ty, extent <= 256 * per16 ? 8u : 16u,
+                  modes ? "_m" : "");
+    Launch& l = p.add(name, (uint32_t)((rows + 7) / 8), 1, 256)
+                    .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps);
+    if (modes) l.u32(in_mode).u32(out_mode);
+    return TILER_HIP_OK;
+  }
   if (strict && extent >= 64 && !modes) {
-    const uint64_t cus = t.compute_units;
-    const uint64_t per16 = 16 / elem;  // elements per 16-byte piece
-    if (al && extent % per16 == 0 && extent >= 16 * per16 && extent <= 512 * per16 && rows >= 8 * cus) {
-      // Rows of at most 512 pieces held in registers, 8 per workgroup: x
-      // read once, y written once, the fold of the squares 8 rows per wave
-      // instruction.
-      if ((rows + 7) / 8 > 0x7fffffffull)
-        return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-      std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict_rr8_p%u", ty, extent <= 256 * per16 ? 8u : 16u);
-      p.add(name, (uint32_t)((rows + 7) / 8), 1, 256)
-          .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps);
-      return TILER_HIP_OK;
-    }
     // Otherwise the reference's serial fold of the squares, staged: R rows
     // per workgroup, the largest of 64, 16, 4 that still gives every CU a
     // workgroup (else 1), a folding lane per row.
@@ -403,21 +406,24 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
   if (rows == 0 || extent == 0) return TILER_HIP_OK;
   if (extent > 0xffffffffull)
     return p.refuse(TILER_HIP_REFUSE_CAPACITY, "row longer than 2^32 - 1 elements");
-  if (strict && extent >= 64 && extent <= 0xffffffffull && !modes) {
+  const uint64_t cus = t.compute_units;
+  const bool vec = aligned16(addr[x]) && aligned16(addr[y]) && extent % 4 == 0;
+  char sname[48];
+  if (strict && vec && extent >= 128 && extent <= 2048 && rows >= 8 * cus) {
+    // Rows of at most 2048 held in registers, 8 per workgroup: x read once
+    // and y written once, the fold 8 rows per wave instruction (the
+    // 65536 x 2048 case: 0.50 ms staged, ~0.22 ms resident); under a
+    // flushing contract the _m form, with the modes.
+    if ((rows + 7) / 8 > 0x7fffffffull)
+      return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
+    std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_rr8_p%u%s", extent <= 1024 ? 8u : 16u,
+                  modes ? "_m" : "");
+    Launch& l = p.add(sname, (uint32_t)((rows + 7) / 8), 1, 256).ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
+    if (modes) l.u32(in_mode).u32(out_mode);
+    return TILER_HIP_OK;
+  }
+  if (strict && extent >= 64 && !modes) {
     // The reference's serial exponent sum.
-    const uint64_t cus = t.compute_units;
-    const bool vec = aligned16(addr[x]) && aligned16(addr[y]) && extent % 4 == 0;
-    char sname[48];
-    if (vec && extent >= 128 && extent <= 2048 && rows >= 8 * cus) {
-      // Rows of at most 2048 held in registers, 8 per workgroup: x read once
-      // and y written once, the fold 8 rows per wave instruction (the
-      // 65536 x 2048 case: 0.50 ms staged, ~0.22 ms resident).
-      if ((rows + 7) / 8 > 0x7fffffffull)
-        return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-      std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_rr8_p%u", extent <= 1024 ? 8u : 16u);
-      p.add(sname, (uint32_t)((rows + 7) / 8), 1, 256).ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
-      return TILER_HIP_OK;
-    }
     // Otherwise staged: R rows per workgroup as for the strict RMSNorm but
     // at most 16 (stages of at least 256 elements, so a stage's fold covers
     // the next stage's loads; 64 rows of 64-element stages ran the

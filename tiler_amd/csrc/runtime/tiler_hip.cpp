@@ -240,6 +240,10 @@ const EntryRow kEntries[] = {
     {"tiler_rms_norm_f32_strict_rr8_p16", "rms-norm-f32/strict", 3},
     {"tiler_rms_norm_bf16_strict_rr8_p8", "rms-norm/bf16/strict", 3},
     {"tiler_rms_norm_bf16_strict_rr8_p16", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_f32_strict_rr8_p8_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_rr8_p16_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_bf16_strict_rr8_p8_m", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_rr8_p16_m", "rms-norm/bf16/strict", 3},
     {"tiler_softmax_f32_strict", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_r1", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_r1_u", "softmax-f32/strict", 2},
@@ -249,6 +253,8 @@ const EntryRow kEntries[] = {
     {"tiler_softmax_f32_strict_r16_u", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_rr8_p16", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_rr8_p8", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_rr8_p16_m", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_rr8_p8_m", "softmax-f32/strict", 2},
     {"tiler_fold_sum_f32", "strict-serial-sum-f32/serial-any-axes", 3},
     {"tiler_fold_squared_f32", "squared-serial-sum-f32/serial", 3},
     {"tiler_fold_fma_f32", "fused-multiply-add-serial-sum-f32/serial", 3},
