@@ -145,8 +145,8 @@ FS, FP = L.SUBNORMALS_FLUSH_SIGN, L.SUBNORMALS_FLUSH_POSITIVE
     (L.PROGRAM_FOLD, (4, 5, 6), dict(rank=3, grouping=(5,), variant=L.FOLD_MAXIMUM), ["tiler_fold_maximum_f32"]),
     # rows: the serial forms that take the modes, whatever the permissions
     (L.PROGRAM_RMS_NORM, (8192, 4104), dict(scalars=(EPS,), dtype=L.BF16, permissions=RE),
-     ["tiler_rms_norm_bf16_strict"]),
-    (L.PROGRAM_SOFTMAX, (2, 100), {}, ["tiler_softmax_f32_strict"]),
+     ["tiler_rms_norm_bf16_strict_r16_m"]),
+    (L.PROGRAM_SOFTMAX, (2, 100), {}, ["tiler_softmax_f32_strict_r1_m"]),
     # rows the register-resident forms hold take their _m forms
     (L.PROGRAM_RMS_NORM, (8192, 4096), dict(scalars=(EPS,), dtype=L.BF16, permissions=RE),
      ["tiler_rms_norm_bf16_strict_rr8_p16_m"]),
@@ -154,7 +154,12 @@ FS, FP = L.SUBNORMALS_FLUSH_SIGN, L.SUBNORMALS_FLUSH_POSITIVE
      ["tiler_rms_norm_f32_strict_rr8_p8_m"]),
     (L.PROGRAM_SOFTMAX, (8192, 2048), {}, ["tiler_softmax_f32_strict_rr8_p16_m"]),
     (L.PROGRAM_SOFTMAX, (4096, 1024), {}, ["tiler_softmax_f32_strict_rr8_p8_m"]),
-    (L.PROGRAM_SOFTMAX, (1024, 2048), {}, ["tiler_softmax_f32_strict"]),
+    # rows the staged forms take: their _m forms; rows under 64: one wave per row
+    (L.PROGRAM_SOFTMAX, (1024, 2048), {}, ["tiler_softmax_f32_strict_r4_m"]),
+    (L.PROGRAM_SOFTMAX, (32, 131072), {}, ["tiler_softmax_f32_strict_r1_m"]),
+    (L.PROGRAM_SOFTMAX, (9, 40), {}, ["tiler_softmax_f32_strict"]),
+    (L.PROGRAM_RMS_NORM, (5, 20000), dict(scalars=(EPS,)), ["tiler_rms_norm_f32_strict_r1_m"]),
+    (L.PROGRAM_RMS_NORM, (5, 40), dict(scalars=(EPS,)), ["tiler_rms_norm_f32_strict"]),
     # maps: the scalar forms with the modes; bf16 expressions: the one-element form
     (L.PROGRAM_POINTWISE, (1024,), dict(variant=L.MAP_SILU), ["tiler_map_f32_m"]),
     (L.PROGRAM_POINTWISE, (1024,), dict(variant=L.MAP_ADD, dtype=L.BF16), ["tiler_map_bf16_m"]),

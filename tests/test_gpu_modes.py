@@ -241,14 +241,23 @@ RESIDENT_RMS = [
     (2100, 4096, L.BF16, "_strict_rr8_p16_m"),  # the longest resident row
     (2048, 64, L.F32, "_strict_rr8_p8_m"),      # one partial chunk
 ]
+STAGED_RMS = [
+    # (rows, extent, dtype, kernel suffix): R rows per staged workgroup
+    # (tiler_rms_norm_*_strict_r{1,4,16,64}[_u]_m)
+    (3, 9000, L.BF16, "_strict_r1_m"),       # three stages, the last partial
+    (1025, 2000, L.F32, "_strict_r4_m"),     # a ragged last workgroup
+    (4100, 4104, L.BF16, "_strict_r16_m"),   # longer than the resident rows
+    (16400, 102, L.F32, "_strict_r64_u_m"),  # unaligned rows, a lane per row
+]
 
 
-@pytest.mark.parametrize("rows,extent,dtype,kernel", RESIDENT_RMS)
+@pytest.mark.parametrize("rows,extent,dtype,kernel", RESIDENT_RMS + STAGED_RMS)
 @pytest.mark.parametrize("modes", MODES)
-def test_resident_rms_norm_under_modes(ctx, rows, extent, dtype, kernel, modes):
-    """The register-resident strict RMSNorm under the modes: rows of ~2^-70
-    (subnormal squares), rows of normal values, rows opening with subnormal
-    entries, a weight with subnormal entries, bit for bit with the oracle."""
+def test_strict_rms_norm_forms_under_modes(ctx, rows, extent, dtype, kernel, modes):
+    """The register-resident and staged strict RMSNorm under the modes: rows
+    of ~2^-70 (subnormal squares), rows of normal values, rows opening with
+    subnormal entries, a weight with subnormal entries, bit for bit with the
+    oracle."""
     im, rm = modes
     rng = np.random.default_rng(rows + extent)
     x = (rng.standard_normal((rows, extent)) * 2.0 ** -70).astype(np.float32)
@@ -279,14 +288,21 @@ RESIDENT_SOFTMAX = [
     (2050, 1100, "_strict_rr8_p16_m"),  # a ragged last workgroup, a partial ninth chunk
     (2048, 2048, "_strict_rr8_p16_m"),  # two whole ring rounds
 ]
+STAGED_SOFTMAX = [
+    # (rows, extent, kernel suffix): tiler_softmax_f32_strict_r{1,4,16}[_u]_m
+    (6, 9000, "_strict_r1_m"),      # three stages, the last partial
+    (300, 1001, "_strict_r1_u_m"),  # unaligned rows
+    (1025, 2048, "_strict_r4_m"),   # a ragged last workgroup
+    (4100, 2052, "_strict_r16_m"),  # longer than the resident rows
+]
 
 
-@pytest.mark.parametrize("rows,extent,kernel", RESIDENT_SOFTMAX)
+@pytest.mark.parametrize("rows,extent,kernel", RESIDENT_SOFTMAX + STAGED_SOFTMAX)
 @pytest.mark.parametrize("modes", MODES)
-def test_resident_softmax_under_modes(ctx, rows, extent, kernel, modes):
-    """The register-resident strict softmax under the modes: rows spread over
-    ~100 below their maximum (subnormal exponents and products), rows of
-    subnormal inputs, and a NaN row, bit for bit with the oracle."""
+def test_strict_softmax_forms_under_modes(ctx, rows, extent, kernel, modes):
+    """The register-resident and staged strict softmax under the modes: rows
+    spread over ~100 below their maximum (subnormal exponents and products),
+    rows of subnormal inputs, and a NaN row, bit for bit with the oracle."""
     im, rm = modes
     rng = np.random.default_rng(rows * 3 + extent)
     x = rng.uniform(-100.0, 0.0, (rows, extent)).astype(np.float32)

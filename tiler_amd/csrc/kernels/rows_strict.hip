@@ -164,10 +164,11 @@ __device__ __forceinline__ void softmax_strict_body(const float* __restrict__ x,
 //   first square is the first square.
 // * Then, per row, rms_norm.rs:177-187: the division by N, + eps, the
 //   certified rsqrt. All threads write y = canon(w * fl(x * s)), re-reading x.
-template <typename T, int R, bool kVec>
+template <typename T, int R, bool kVec, bool kModes = false>
 __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, const T* __restrict__ w,
                                                        uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,
-                                                       uint32_t extent, float eps) {
+                                                       uint32_t extent, float eps, uint32_t im = 1u,
+                                                       uint32_t rm = 1u) {
   constexpr bool kBf16 = sizeof(T) == 2;
   constexpr uint32_t C = 4096 / R;
   constexpr uint32_t kStride = C + 4;
@@ -183,6 +184,21 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
   auto widen = [](uint32_t bits) -> float {
     if constexpr (kBf16) return tiler::bf16_widen(bits);
     else return __uint_as_float(bits);
+  };
+  // Under the modes (the _m forms) the squares are staged as F(O(x) * O(x))
+  // and the fold is the plain one, as in rms_strict_resident_body.
+  const tiler::Flush O(im), Rz(rm), F = tiler::result_as_operand(im, rm);
+  auto sq = [&](float v) {
+    if constexpr (kModes) {
+      const float o = O(v);
+      return F(o * o);
+    } else {
+      return v * v;
+    }
+  };
+  auto sq4 = [&](f32x4 a) -> f32x4 {
+    if constexpr (kModes) return f32x4{sq(a.x), sq(a.y), sq(a.z), sq(a.w)};
+    else return a * a;
   };
   raw reg[kPer];
   auto load = [&](uint32_t s) {
@@ -205,19 +221,26 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
       float* dst = &stage[buf][r * kStride + (q % kRowPieces) * W];
       if constexpr (!kVec) {
         const float v = kBf16 ? tiler::bf16_widen(reg[i]) : (float)reg[i];
-        *dst = in ? v * v : -0.0f;
+        if constexpr (kModes) *dst = in ? sq(v) : -0.0f;
+        else *dst = in ? v * v : -0.0f;
       } else if constexpr (kBf16) {  // 8 bf16 -> 8 squares
         const u32x4 u = reg[i];
         f32x4 lo, hi;
         lo.x = widen(u.x & 0xffffu); lo.y = widen(u.x >> 16); lo.z = widen(u.y & 0xffffu); lo.w = widen(u.y >> 16);
         hi.x = widen(u.z & 0xffffu); hi.y = widen(u.z >> 16); hi.z = widen(u.w & 0xffffu); hi.w = widen(u.w >> 16);
-        *reinterpret_cast<f32x4*>(dst) = in ? lo * lo : nz;
-        *reinterpret_cast<f32x4*>(dst + 4) = in ? hi * hi : nz;
+        if constexpr (kModes) {
+          *reinterpret_cast<f32x4*>(dst) = in ? sq4(lo) : nz;
+          *reinterpret_cast<f32x4*>(dst + 4) = in ? sq4(hi) : nz;
+        } else {
+          *reinterpret_cast<f32x4*>(dst) = in ? lo * lo : nz;
+          *reinterpret_cast<f32x4*>(dst + 4) = in ? hi * hi : nz;
+        }
       } else {
         const u32x4 u = reg[i];
         f32x4 v;
         v.x = widen(u.x); v.y = widen(u.y); v.z = widen(u.z); v.w = widen(u.w);
-        *reinterpret_cast<f32x4*>(dst) = in ? v * v : nz;
+        if constexpr (kModes) *reinterpret_cast<f32x4*>(dst) = in ? sq4(v) : nz;
+        else *reinterpret_cast<f32x4*>(dst) = in ? v * v : nz;
       }
     }
   };
@@ -287,8 +310,14 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
   }
   // A relay group's row sum is in its lane 8 g.
   if (kRelay ? folds && sg == 0 && g < kRowsPerWave && row0 + fr < rows : folds)
-    scale[fr] = tiler::rsqrt_f32_cr(acc / (float)extent + eps);
+    scale[fr] = kModes ? F(tiler::rsqrt_f32_cr(F(F(acc / (float)extent) + O(eps))))
+                       : tiler::rsqrt_f32_cr(acc / (float)extent + eps);
   __syncthreads();
+  // w * fl(x * s), under the modes R(O(w) * F(O(x) * O(s))).
+  auto scaled = [&](float xf, float wf, float sc) -> float {
+    if constexpr (kModes) return Rz(O(wf) * F(O(xf) * sc));
+    else return wf * (xf * sc);
+  };
   for (uint32_t r = 0; r < (uint32_t)R; ++r) {
     if (row0 + r >= rows) break;
     const float sc = scale[r];
@@ -300,7 +329,8 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
         u32x4 out;
         if constexpr (kBf16) {
           auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
-            return tiler::bf16_narrow(tiler::canon(widen(wb) * (widen(xb) * sc)));
+            if constexpr (kModes) return tiler::bf16_narrow(tiler::canon(scaled(widen(xb), widen(wb), sc)));
+            else return tiler::bf16_narrow(tiler::canon(widen(wb) * (widen(xb) * sc)));
           };
           out.x = one(xv.x & 0xffffu, wv.x & 0xffffu) | (one(xv.x >> 16, wv.x >> 16) << 16);
           out.y = one(xv.y & 0xffffu, wv.y & 0xffffu) | (one(xv.y >> 16, wv.y >> 16) << 16);
@@ -308,7 +338,8 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
           out.w = one(xv.w & 0xffffu, wv.w & 0xffffu) | (one(xv.w >> 16, wv.w >> 16) << 16);
         } else {
           auto one = [&](uint32_t xb, uint32_t wb) -> uint32_t {
-            return __float_as_uint(tiler::canon(widen(wb) * (widen(xb) * sc)));
+            if constexpr (kModes) return __float_as_uint(tiler::canon(scaled(widen(xb), widen(wb), sc)));
+            else return __float_as_uint(tiler::canon(widen(wb) * (widen(xb) * sc)));
           };
           out.x = one(xv.x, wv.x);
           out.y = one(xv.y, wv.y);
@@ -319,8 +350,13 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
       }
     } else {
       for (uint32_t e = t; e < extent; e += 256u) {
-        const float normalized = load_elem<kBf16>(x, base + e) * sc;
-        store_elem<kBf16>(y, base + e, tiler::canon(load_elem<kBf16>(w, wbase + e) * normalized));
+        if constexpr (kModes) {
+          store_elem<kBf16>(y, base + e,
+                            tiler::canon(scaled(load_elem<kBf16>(x, base + e), load_elem<kBf16>(w, wbase + e), sc)));
+        } else {
+          const float normalized = load_elem<kBf16>(x, base + e) * sc;
+          store_elem<kBf16>(y, base + e, tiler::canon(load_elem<kBf16>(w, wbase + e) * normalized));
+        }
       }
     }
   }
@@ -337,9 +373,10 @@ __device__ __forceinline__ void rms_strict_staged_body(const T* __restrict__ x, 
 //   from -0.0 (an exponent is never -0.0, so -0.0 plus the first is the first).
 // * y = canon(fl(exp(fl(x - m)) * fl(1 / d))): the reciprocal, then a
 //   multiply, the exponent recomputed (the same correctly rounded value).
-template <int R, bool kVec>
+template <int R, bool kVec, bool kModes = false>
 __device__ __forceinline__ void softmax_strict_staged_body(const float* __restrict__ x, float* __restrict__ y,
-                                                           uint64_t rows, uint32_t extent) {
+                                                           uint64_t rows, uint32_t extent, uint32_t im = 1u,
+                                                           uint32_t rm = 1u) {
   constexpr uint32_t C = 4096 / R;
   constexpr uint32_t kStride = C + 4;
   constexpr uint32_t W = kVec ? 4 : 1;
@@ -416,7 +453,14 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
   const uint32_t fr = R == 1 ? 0u : wave * kRowsPerWave + g % kRowsPerWave;  // the row this group folds
   const bool folds = R == 1 ? wave == 0 : true;
   __syncthreads();
-  // Pass 2: the exponents, folded in order.
+  // Pass 2: the exponents, folded in order.  Under the modes (the _m forms)
+  // they are F(exp(F(O(x) - O(m)))), staged and written to y as such, and
+  // the fold is the plain one, as in rms_strict_resident_body.
+  const tiler::Flush O(im), Rz(rm), F = tiler::result_as_operand(im, rm);
+  auto expo = [&](float xv, float m) {
+    if constexpr (kModes) return F(tiler::exp_f32_cr(F(O(xv) - O(m)), tab));
+    else return tiler::exp_f32_cr(xv - m, tab);
+  };
   piece reg[kPer];
   auto load = [&](uint32_t s) {
 #pragma unroll
@@ -443,14 +487,14 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
       }
       if constexpr (kVec) {
         f32x4 ev;
-        ev.x = tiler::exp_f32_cr(reg[i].x - m, tab);
-        ev.y = tiler::exp_f32_cr(reg[i].y - m, tab);
-        ev.z = tiler::exp_f32_cr(reg[i].z - m, tab);
-        ev.w = tiler::exp_f32_cr(reg[i].w - m, tab);
+        ev.x = expo(reg[i].x, m);
+        ev.y = expo(reg[i].y, m);
+        ev.z = expo(reg[i].z, m);
+        ev.w = expo(reg[i].w, m);
         *reinterpret_cast<f32x4*>(dst) = ev;
         *reinterpret_cast<f32x4*>(y + (row0 + r) * extent + e) = ev;
       } else {
-        const float ev = tiler::exp_f32_cr(reg[i] - m, tab);
+        const float ev = expo(reg[i], m);
         *dst = ev;
         y[(row0 + r) * extent + e] = ev;
       }
@@ -480,7 +524,11 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
     __syncthreads();
   }
   // softmax.rs:302-313: the reciprocal, then a multiply.
-  if (folds && sg == 0 && g < kRowsPerWave && row0 + fr < rows) recip[fr] = 1.0f / acc;
+  if (folds && sg == 0 && g < kRowsPerWave && row0 + fr < rows) recip[fr] = kModes ? F(1.0f / acc) : 1.0f / acc;
+  auto out = [&](float e, float rc) {  // canon(fl(e * r)), under the modes canon(R(O(e) * O(r)))
+    if constexpr (kModes) return tiler::canon(Rz(e * rc));
+    else return tiler::canon(e * rc);
+  };
   __syncthreads();
   // Pass 3: y, over the workgroup's rows as one flat run of pieces (the
   // iterations are independent, so several loads are in flight per thread).
@@ -495,13 +543,13 @@ __device__ __forceinline__ void softmax_strict_staged_body(const float* __restri
     if constexpr (kVec) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(y + at);  // the exponents pass 2 wrote
       f32x4 o;
-      o.x = tiler::canon(v.x * rc);
-      o.y = tiler::canon(v.y * rc);
-      o.z = tiler::canon(v.z * rc);
-      o.w = tiler::canon(v.w * rc);
+      o.x = out(v.x, rc);
+      o.y = out(v.y, rc);
+      o.z = out(v.z, rc);
+      o.w = out(v.w, rc);
       *reinterpret_cast<f32x4*>(y + at) = o;
     } else {
-      y[at] = tiler::canon(y[at] * rc);
+      y[at] = out(y[at], rc);
     }
   }
 }
@@ -863,6 +911,18 @@ TILER_RMS_STRICT_RESIDENT(f32, float, 8, 8)
       tiler_softmax_f32_strict_r##R##_u(const float* __restrict__ x, float* __restrict__ y,           \
                                         uint64_t rows, uint32_t extent) {                             \
     softmax_strict_staged_body<R, false>(x, y, rows, extent);                                         \
+  }                                                                                                   \
+  extern "C" __global__ void __launch_bounds__(256)                                                   \
+      tiler_softmax_f32_strict_r##R##_m(const float* __restrict__ x, float* __restrict__ y,           \
+                                        uint64_t rows, uint32_t extent, uint32_t in_mode,             \
+                                        uint32_t out_mode) {                                          \
+    softmax_strict_staged_body<R, true, true>(x, y, rows, extent, in_mode, out_mode);                 \
+  }                                                                                                   \
+  extern "C" __global__ void __launch_bounds__(256)                                                   \
+      tiler_softmax_f32_strict_r##R##_u_m(const float* __restrict__ x, float* __restrict__ y,         \
+                                          uint64_t rows, uint32_t extent, uint32_t in_mode,           \
+                                          uint32_t out_mode) {                                        \
+    softmax_strict_staged_body<R, false, true>(x, y, rows, extent, in_mode, out_mode);                \
   }
 TILER_SOFTMAX_STRICT_STAGED(1)
 TILER_SOFTMAX_STRICT_STAGED(4)
@@ -880,6 +940,22 @@ TILER_SOFTMAX_STRICT_STAGED(16)
                                             uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,  \
                                             uint32_t extent, float eps) {                             \
     rms_strict_staged_body<T, R, false>(x, w, w_row_stride, y, rows, extent, eps);                    \
+  }                                                                                                   \
+  extern "C" __global__ void __launch_bounds__(256)                                                   \
+      tiler_rms_norm_##TY##_strict_r##R##_m(const T* __restrict__ x, const T* __restrict__ w,         \
+                                            uint64_t w_row_stride, T* __restrict__ y, uint64_t rows,  \
+                                            uint32_t extent, float eps, uint32_t in_mode,             \
+                                            uint32_t out_mode) {                                      \
+    rms_strict_staged_body<T, R, true, true>(x, w, w_row_stride, y, rows, extent, eps, in_mode,       \
+                                             out_mode);                                               \
+  }                                                                                                   \
+  extern "C" __global__ void __launch_bounds__(256)                                                   \
+      tiler_rms_norm_##TY##_strict_r##R##_u_m(const T* __restrict__ x, const T* __restrict__ w,       \
+                                              uint64_t w_row_stride, T* __restrict__ y,               \
+                                              uint64_t rows, uint32_t extent, float eps,              \
+                                              uint32_t in_mode, uint32_t out_mode) {                  \
+    rms_strict_staged_body<T, R, false, true>(x, w, w_row_stride, y, rows, extent, eps, in_mode,      \
+                                              out_mode);                                              \
   }
 TILER_RMS_STRICT_STAGED(f32, float, 1)
 TILER_RMS_STRICT_STAGED(f32, float, 4)

@@ -292,8 +292,8 @@ tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_b
                                uint64_t extent, uint32_t eps_bits, const uintptr_t* addr,
                                Program& p, bool strict, uint32_t in_mode, uint32_t out_mode) {
   // A flushing contract: the serial fold with the modes at every site (the
-  // register-resident or one-wave-per-row strict kernel, which take them),
-  // whatever the topology.
+  // _m forms of the strict kernels, or the one-wave-per-row kernel, which
+  // take them), whatever the topology.
   const bool modes = in_mode > 1 || out_mode > 1;
   if (modes) strict = true;
   float eps;
@@ -331,16 +331,18 @@ tiler_hip_status plan_rms_norm(const Target& t, uint32_t dtype, int32_t weight_b
     if (modes) l.u32(in_mode).u32(out_mode);
     return TILER_HIP_OK;
   }
-  if (strict && extent >= 64 && !modes) {
+  if (strict && extent >= 64) {
     // Otherwise the reference's serial fold of the squares, staged: R rows
     // per workgroup, the largest of 64, 16, 4 that still gives every CU a
-    // workgroup (else 1), a folding lane per row.
+    // workgroup (else 1), a folding lane per row (the _m forms with the
+    // modes).
     const uint32_t R = rows >= 64 * cus ? 64 : rows >= 16 * cus ? 16 : rows >= 4 * cus ? 4 : 1;
     if ((rows + R - 1) / R > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-    std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict_r%u%s", ty, R, al ? "" : "_u");
-    p.add(name, (uint32_t)((rows + R - 1) / R), 1, 256)
-        .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps);
+    std::snprintf(name, sizeof(name), "tiler_rms_norm_%s_strict_r%u%s%s", ty, R, al ? "" : "_u", modes ? "_m" : "");
+    Launch& l = p.add(name, (uint32_t)((rows + R - 1) / R), 1, 256)
+                    .ptr(x).ptr(w).u64(wstride).ptr(y).u64(rows).u32((uint32_t)extent).f32(eps);
+    if (modes) l.u32(in_mode).u32(out_mode);
     return TILER_HIP_OK;
   }
   if (strict) {  // short rows: the reference's serial fold of the squares, one wave per row
@@ -391,7 +393,8 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
   const uint32_t x = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotInput);
   const uint32_t y = p.slot(mul_sat(mul_sat(rows, extent), 4), kSlotOutput);
   // A flushing contract: the serial exponent sum with the modes at every site
-  // (the one-wave-per-row strict kernel, which takes them).
+  // (the _m forms of the strict kernels, or the one-wave-per-row kernel,
+  // which take them).
   const bool modes = in_mode > 1 || out_mode > 1;
   if (modes && form != TILER_HIP_FORM_AUTO)
     return p.refuse(TILER_HIP_REFUSE_UNSUPPORTED, "form: a flushing contract has the serial form only");
@@ -422,8 +425,8 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
     if (modes) l.u32(in_mode).u32(out_mode);
     return TILER_HIP_OK;
   }
-  if (strict && extent >= 64 && !modes) {
-    // The reference's serial exponent sum.
+  if (strict && extent >= 64) {
+    // The reference's serial exponent sum (the _m forms with the modes).
     // Otherwise staged: R rows per workgroup as for the strict RMSNorm but
     // at most 16 (stages of at least 256 elements, so a stage's fold covers
     // the next stage's loads; 64 rows of 64-element stages ran the
@@ -432,8 +435,9 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
     const uint32_t R = rows >= 16 * cus ? 16 : rows >= 4 * cus ? 4 : 1;
     if ((rows + R - 1) / R > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-    std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_r%u%s", R, vec ? "" : "_u");
-    p.add(sname, (uint32_t)((rows + R - 1) / R), 1, 256).ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
+    std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_r%u%s%s", R, vec ? "" : "_u", modes ? "_m" : "");
+    Launch& l = p.add(sname, (uint32_t)((rows + R - 1) / R), 1, 256).ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
+    if (modes) l.u32(in_mode).u32(out_mode);
     return TILER_HIP_OK;
   }
   if (strict) {  // short rows: the reference's serial exponent sum, one wave per row

@@ -255,6 +255,28 @@ const EntryRow kEntries[] = {
     {"tiler_softmax_f32_strict_rr8_p8", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_rr8_p16_m", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_rr8_p8_m", "softmax-f32/strict", 2},
+    {"tiler_rms_norm_f32_strict_r1_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r1_u_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r4_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r4_u_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r16_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r16_u_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r64_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_f32_strict_r64_u_m", "rms-norm-f32/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r1_m", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r1_u_m", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r4_m", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r4_u_m", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r16_m", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r16_u_m", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r64_m", "rms-norm/bf16/strict", 3},
+    {"tiler_rms_norm_bf16_strict_r64_u_m", "rms-norm/bf16/strict", 3},
+    {"tiler_softmax_f32_strict_r1_m", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_r1_u_m", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_r4_m", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_r4_u_m", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_r16_m", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_r16_u_m", "softmax-f32/strict", 2},
     {"tiler_fold_sum_f32", "strict-serial-sum-f32/serial-any-axes", 3},
     {"tiler_fold_squared_f32", "squared-serial-sum-f32/serial", 3},
     {"tiler_fold_fma_f32", "fused-multiply-add-serial-sum-f32/serial", 3},
