@@ -189,6 +189,82 @@ def test_resident_strict_rows(ctx, case):
     assert np.array_equal(bits(got), bits(want)), rz.symbols
 
 
+def _tiny_rows(r, rows, extent, scale_log2):
+    """Rows of magnitude 2^scale_log2 (their squares or exponents reach the
+    subnormal range), every fifth row of ordinary values, a few subnormal
+    entries planted."""
+    x = (r.standard_normal((rows, extent)) * 2.0 ** scale_log2).astype(np.float32)
+    x[::5] = r.standard_normal((len(range(0, rows, 5)), extent)).astype(np.float32)
+    n = min(rows * extent, 64)
+    sub = (r.integers(1, 1 << 23, n).astype(np.uint32) | (r.integers(0, 2, n).astype(np.uint32) << 31))
+    x.reshape(-1)[r.choice(rows * extent, n, replace=False)] = sub.view(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_strict_rows_under_modes(ctx, case):
+    """Random shapes through the strict RMSNorm and softmax under a random
+    flushing contract: the register-resident _m forms (2048 to 2600 rows) and
+    the staged _m forms (1 to 1200 rows, aligned or not), bit for bit with the
+    oracle under the same modes."""
+    from tiler_amd.realize import realize, route
+    r = _rng(case, 12)
+    modes = [(2, 1), (1, 2), (2, 2), (3, 3), (2, 3), (3, 1)]
+    im, rm = modes[int(r.integers(len(modes)))]
+    resident = case % 2 == 0
+    rows = int(r.integers(2048, 2601)) if resident else int(r.integers(1, 1201))
+    dtype = L.BF16 if r.integers(2) else L.F32
+    per16 = 8 if dtype == L.BF16 else 4
+    if resident:
+        extent = per16 * int(r.integers(16, 513))
+    else:
+        extent = int(r.integers(64, min(9000, 4_000_000 // rows) + 1))
+    x = _tiny_rows(r, rows, extent, -70)
+    w = r.normal(1.0, 0.1, extent).astype(np.float32)
+    w[:3] = np.array([1, 0x80000001, 0x7FFFFF], np.uint32).view(np.float32)
+    if dtype == L.BF16:
+        x = bf16_widen(oracle.bf16_narrow(x)).reshape(x.shape)
+        w = bf16_widen(oracle.bf16_narrow(w)).reshape(w.shape)
+    print(f"[strict modes] case {case}: rms {'bf16' if dtype == L.BF16 else 'f32'} rows={rows} extent={extent} "
+          f"modes=({im},{rm})", flush=True)
+    rz = realize(L.PROGRAM_RMS_NORM, (rows, extent), dtype=dtype, scalars=(EPS,), input_subnormals=im,
+                 result_subnormals=rm, flags=L.REGION_ALIGNED16 | L.REGION_OPERAND_BROADCAST, ctx=ctx)
+    assert rz.symbols[-1].endswith("_m") and ("_rr8_" in rz.symbols[-1]) == resident, rz.symbols
+    host = [x, w] if dtype == L.F32 else [oracle.bf16_narrow(x).reshape(x.shape), oracle.bf16_narrow(w)]
+    out = np.float32 if dtype == L.F32 else np.uint16
+    bufs = [ctx.to_device(np.ascontiguousarray(h)) for h in host] + [ctx.alloc(rows * extent * np.dtype(out).itemsize)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[2].download(out, x.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    want = oracle.rms_norm_f32(x, np.broadcast_to(w, x.shape).copy(), x.shape, 1, EPS, input_mode=im - 1,
+                               result_mode=rm - 1).reshape(rows, extent)
+    if dtype == L.BF16:
+        assert np.array_equal(got, oracle.bf16_narrow(want).reshape(rows, extent)), rz.symbols
+    else:
+        assert np.array_equal(bits(got), bits(want)), rz.symbols
+    # softmax: rows spread ~100 below their maximum, the same row counts
+    extent = 4 * int(r.integers(32, 513)) if resident else int(r.integers(64, min(9000, 4_000_000 // rows) + 1))
+    x = r.uniform(-100.0, 0.0, (rows, extent)).astype(np.float32)
+    x[1::7] = _tiny_rows(r, len(range(1, rows, 7)), extent, -126)
+    x[int(r.integers(rows)), int(r.integers(extent))] = np.nan
+    print(f"[strict modes] case {case}: softmax rows={rows} extent={extent} modes=({im},{rm})", flush=True)
+    rz = realize(L.PROGRAM_SOFTMAX, (rows, extent), input_subnormals=im, result_subnormals=rm,
+                 flags=L.REGION_ALIGNED16, ctx=ctx)
+    assert rz.symbols[-1].endswith("_m") and ("_rr8_" in rz.symbols[-1]) == resident, rz.symbols
+    bufs = [ctx.to_device(x), ctx.alloc(x.nbytes)]
+    try:
+        route(ctx, rz, bufs)
+        got = bufs[1].download(np.float32, x.shape)
+    finally:
+        for b in bufs:
+            b.free()
+    want = oracle.softmax_f32(x, x.shape, 1, input_mode=im - 1, result_mode=rm - 1).reshape(rows, extent)
+    assert np.array_equal(bits(got), bits(want)), rz.symbols
+
+
 @pytest.mark.parametrize("case", range(CASES))
 def test_tree_sum(ctx, case):
     r = _rng(case, 2)
