@@ -248,6 +248,8 @@ STAGED_RMS = [
     (1025, 2000, L.F32, "_strict_r4_m"),     # a ragged last workgroup
     (4100, 4104, L.BF16, "_strict_r16_m"),   # longer than the resident rows
     (16400, 102, L.F32, "_strict_r64_u_m"),  # unaligned rows, a lane per row
+    (300, 40, L.F32, "_strict"),             # rows under 64: one wave per row
+    (33, 63, L.BF16, "_strict"),
 ]
 
 
@@ -294,6 +296,8 @@ STAGED_SOFTMAX = [
     (300, 1001, "_strict_r1_u_m"),  # unaligned rows
     (1025, 2048, "_strict_r4_m"),   # a ragged last workgroup
     (4100, 2052, "_strict_r16_m"),  # longer than the resident rows
+    (300, 40, "_strict"),           # rows under 64: one wave per row
+    (33, 63, "_strict"),
 ]
 
 

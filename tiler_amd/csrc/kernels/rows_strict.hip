@@ -58,27 +58,21 @@ __device__ __forceinline__ float fold_segment(const float* seg, uint32_t len, fl
   return acc;
 }
 
-// The same fold with the declared subnormal modes at each combine:
-// apply_to_result(apply_to_operand(acc) + apply_to_operand(c)).
-__device__ __forceinline__ float fold_segment_modes(const float* seg, uint32_t len, float acc, bool& seeded,
-                                                    uint32_t im, uint32_t rm) {
-  for (uint32_t i = 0; i < len; ++i) {
-    acc = seeded ? tiler::subnormal(rm, tiler::subnormal(im, acc) + tiler::subnormal(im, seg[i])) : seg[i];
-    seeded = true;
-  }
-  return acc;
-}
-
 // in_mode / out_mode: the declared subnormal modes (tiler::subnormal), applied
 // at every arithmetic site as rms_norm.rs:405-489 and softmax.rs:200-315 apply
 // them under a conformance (operands flushed before, results after); 1 and 1
-// preserve, which is the strict reading.
+// preserve, which is the strict reading.  Under flushing modes the segments
+// hold the contributors as F(c) = O(R(c)) (tiler::result_as_operand) and
+// fold_segment folds them plainly: the fold's sum is read only as an
+// operand, and a sum of two non-negative values that are not subnormal is
+// never subnormal, so the reference's acc = R(O(acc) + O(c)) read as O(acc)
+// is that plain fold (rms_strict_resident_body states the argument).
 template <bool kBf16>
 __device__ __forceinline__ void rms_strict_body(const void* __restrict__ x, const void* __restrict__ w,
                                                 uint64_t w_row_stride, void* __restrict__ y, uint64_t rows,
                                                 uint32_t extent, float eps, uint32_t im, uint32_t rm) {
   using tiler::subnormal;
-  const bool modes = im > 1u || rm > 1u;
+  const tiler::Flush F = tiler::result_as_operand(im, rm);
   __shared__ __attribute__((aligned(16))) float seg[kStrictWaves][kStrictSeg];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint64_t row = (uint64_t)blockIdx.x * kStrictWaves + wave;
@@ -90,12 +84,11 @@ __device__ __forceinline__ void rms_strict_body(const void* __restrict__ x, cons
     const uint32_t len = extent - s0 < kStrictSeg ? extent - s0 : kStrictSeg;
     for (uint32_t i = lane; i < len; i += 64) {
       const float v = subnormal(im, load_elem<kBf16>(x, base + s0 + i));
-      seg[wave][i] = subnormal(rm, v * v);
+      seg[wave][i] = F(v * v);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes landed
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0)
-      acc = modes ? fold_segment_modes(seg[wave], len, acc, seeded, im, rm) : fold_segment(seg[wave], len, acc, seeded);
+    if (lane == 0) acc = fold_segment(seg[wave], len, acc, seeded);
     __builtin_amdgcn_wave_barrier();
   }
   // rms_norm.rs:177-187: a division by N, then + eps, then the certified rsqrt.
@@ -116,12 +109,9 @@ __device__ __forceinline__ void rms_strict_body(const void* __restrict__ x, cons
 __device__ __forceinline__ void softmax_strict_body(const float* __restrict__ x, float* __restrict__ y,
                                                     uint64_t rows, uint32_t extent, uint32_t im, uint32_t rm) {
   using tiler::subnormal;
-  const bool modes = im > 1u || rm > 1u;
-  // e_i = apply_to_result(exp(apply_to_operand(fl(x_i - m) under the modes)))
-  auto expo = [&](float v, float m) {
-    const float shifted = subnormal(rm, subnormal(im, v) - subnormal(im, m));
-    return subnormal(rm, tiler::exp_f32_cr(subnormal(im, shifted)));
-  };
+  const tiler::Flush F = tiler::result_as_operand(im, rm);
+  // O(e_i) = O(apply_to_result(exp(apply_to_operand(fl(x_i - m) under the modes))))
+  auto expo = [&](float v, float m) { return F(tiler::exp_f32_cr(F(subnormal(im, v) - subnormal(im, m)))); };
   __shared__ __attribute__((aligned(16))) float seg[kStrictWaves][kStrictSeg];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint64_t row = (uint64_t)blockIdx.x * kStrictWaves + wave;
@@ -138,15 +128,14 @@ __device__ __forceinline__ void softmax_strict_body(const float* __restrict__ x,
     for (uint32_t i = lane; i < len; i += 64) seg[wave][i] = expo(xr[s0 + i], m);
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0)
-      d = modes ? fold_segment_modes(seg[wave], len, d, seeded, im, rm) : fold_segment(seg[wave], len, d, seeded);
+    if (lane == 0) d = fold_segment(seg[wave], len, d, seeded);
     __builtin_amdgcn_wave_barrier();
   }
   float r = 0.0f;
   if (lane == 0) r = subnormal(rm, 1.0f / subnormal(im, d));  // softmax.rs:302-313: the reciprocal, then a multiply
   r = __shfl(r, 0, 64);
   for (uint32_t i = lane; i < extent; i += 64)
-    yr[i] = tiler::canon(subnormal(rm, subnormal(im, expo(xr[i], m)) * subnormal(im, r)));
+    yr[i] = tiler::canon(subnormal(rm, expo(xr[i], m) * subnormal(im, r)));
 }
 
 // Strict RMSNorm over many rows, staged like the strict serial sum
