@@ -82,7 +82,8 @@ def test_strict_contract_selects_the_serial_row_and_contraction_kernels():
     assert sm.symbols == ["tiler_softmax_f32_strict_rr8_p16"] and sm.dispatches[0].grid == (8192, 1, 1)
     assert sm.dispatches[0].block == (256, 1, 1)
     assert realize(L.PROGRAM_SOFTMAX, (4096, 1024)).symbols == ["tiler_softmax_f32_strict_rr8_p8"]
-    assert realize(L.PROGRAM_SOFTMAX, (4096, 2052)).symbols == ["tiler_softmax_f32_strict_r16"]
+    assert realize(L.PROGRAM_SOFTMAX, (4096, 2052)).symbols == ["tiler_softmax_f32_strict_rr8_p32"]
+    assert realize(L.PROGRAM_SOFTMAX, (4096, 4100)).symbols == ["tiler_softmax_f32_strict_r16"]
     assert realize(L.PROGRAM_SOFTMAX, (1024, 2048)).symbols == ["tiler_softmax_f32_strict_r4"]
     assert realize(L.PROGRAM_SOFTMAX, (9, 40)).symbols == ["tiler_softmax_f32_strict"]
     c = realize(L.PROGRAM_CONTRACTION, (4096, 4096, 4096), dtype=L.BF16, variant=L.EPILOGUE_SILU)

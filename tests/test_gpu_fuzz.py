@@ -168,8 +168,8 @@ def test_resident_strict_rows(ctx, case):
             b.free()
     wantf = oracle.rms_norm_f32(bf16_widen(xb), bf16_widen(wb), xb.shape, 1, EPS)
     assert np.array_equal(got.reshape(-1), oracle.bf16_narrow(wantf).reshape(-1)), rz.symbols
-    # softmax, extent a multiple of 4 in [128, 2048]
-    extent = 4 * int(r.integers(32, 513))
+    # softmax, extent a multiple of 4 in [128, 4096]
+    extent = 4 * int(r.integers(32, 1025))
     x = (r.standard_normal((rows, extent)) * 3).astype(np.float32)
     sample = np.unique(np.concatenate([r.choice(rows, 64, replace=False), np.arange(rows - rows % 8 - 8, rows)]))
     x[sample[3], int(r.integers(extent))] = np.nan

@@ -289,13 +289,14 @@ RESIDENT_SOFTMAX = [
     (4096, 200, "_strict_rr8_p8_m"),    # two chunks, the second partial
     (2050, 1100, "_strict_rr8_p16_m"),  # a ragged last workgroup, a partial ninth chunk
     (2048, 2048, "_strict_rr8_p16_m"),  # two whole ring rounds
+    (2050, 3000, "_strict_rr8_p32_m"),  # a ragged last workgroup, a partial third ring round
 ]
 STAGED_SOFTMAX = [
     # (rows, extent, kernel suffix): tiler_softmax_f32_strict_r{1,4,16}[_u]_m
     (6, 9000, "_strict_r1_m"),      # three stages, the last partial
     (300, 1001, "_strict_r1_u_m"),  # unaligned rows
     (1025, 2048, "_strict_r4_m"),   # a ragged last workgroup
-    (4100, 2052, "_strict_r16_m"),  # longer than the resident rows
+    (4100, 4100, "_strict_r16_m"),  # longer than the resident rows
     (300, 40, "_strict"),           # rows under 64: one wave per row
     (33, 63, "_strict"),
 ]
@@ -317,7 +318,13 @@ def test_strict_softmax_forms_under_modes(ctx, rows, extent, kernel, modes):
     print(f"[modes softmax] {rz.symbols} {rows}x{extent} modes=({im},{rm})", flush=True)
     assert len(rz.symbols) == 1 and rz.symbols[0].endswith(kernel), rz.symbols
     got = _route(ctx, rz, [x], (rows, extent), np.float32)
-    want = oracle.softmax_f32(x, x.shape, 1, input_mode=om(im), result_mode=om(rm)).reshape(rows, extent)
+    # rows are independent: past 2.5M elements (the oracle's certified exp
+    # takes ~1.7 s per million) compare the planted rows, the first and last
+    # workgroups and 64 drawn rows
+    if rows * extent > 2_500_000:
+        keep = np.unique(np.concatenate([np.arange(16), np.arange(rows - 16, rows), rng.choice(rows, 64, replace=False)]))
+        x, got = np.ascontiguousarray(x[keep]), got[keep]
+    want = oracle.softmax_f32(x, x.shape, 1, input_mode=om(im), result_mode=om(rm)).reshape(x.shape)
     assert np.array_equal(bits(got), bits(want))
 
 

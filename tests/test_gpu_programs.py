@@ -412,10 +412,14 @@ def test_strict_softmax_is_the_reference_fold(ctx):
     (2048, 1028, "_strict_rr8_p16"),  # one 4-column group in the ninth chunk
     (2100, 1024, "_strict_rr8_p8"),   # eight whole chunks, one ring round
     (3000, 128, "_strict_rr8_p8"),    # one chunk
+    (2050, 4096, "_strict_rr8_p32"),  # four whole ring rounds, a ragged last workgroup
+    (2048, 2052, "_strict_rr8_p32"),  # one 4-column group in the seventeenth chunk
+    (2048, 3000, "_strict_rr8_p32"),  # a partial third ring round
+    (4100, 4100, "_strict_r16"),      # past the resident rows: staged, 16-byte loads
 ])
 def test_strict_softmax_staged_rows(ctx, rows, extent, form):
     """Rows of >= 64 run the staged strict softmax (tiler_softmax_f32_strict_r*)
-    or, for 128..2048 aligned elements and enough rows, the register-resident
+    or, for 128..4096 aligned elements and enough rows, the register-resident
     one (_rr8_p*): the maximum, the exponent sum folded in order, the
     reciprocal multiply -- bit for bit against the oracle.  Row 0 all -inf,
     row 1 with a NaN, row 2 with a +inf, row 3 with -0.0 and +0.0 as its only
@@ -442,7 +446,13 @@ def test_strict_softmax_staged_rows(ctx, rows, extent, form):
     finally:
         for b in bufs:
             b.free()
-    want = oracle.softmax_f32(x, x.shape, 1).reshape(rows, extent)
+    # rows are independent: past 2.5M elements (the oracle's certified exp
+    # takes ~1.7 s per million) compare the planted rows, every residue mod 8
+    # of the first and last workgroups and 64 drawn rows
+    if rows * extent > 2_500_000:
+        keep = np.unique(np.concatenate([np.arange(16), np.arange(rows - 16, rows), rng.choice(rows, 64, replace=False)]))
+        x, got = np.ascontiguousarray(x[keep]), got[keep]
+    want = oracle.softmax_f32(x, x.shape, 1).reshape(x.shape)
     assert np.array_equal(bits(got), bits(want))
 
 
@@ -462,10 +472,10 @@ def _sampled_rows(rng, rows, per_group, groups_sampled):
 def test_strict_softmax_staged_whole_stages_sampled_rows(ctx):
     """The staged strict softmax with 16 rows per workgroup, 16-byte loads
     and whole stages (tiler_softmax_f32_strict_r16, rows past the resident
-    form's 2048 elements): 4096 x 2304, 9 stages of 256 -- every row of the
+    form's 4096 elements): 4096 x 4352, 17 stages of 256 -- every row of the
     first and last workgroup and one row of every residue mod 16 from 14
     others, bit for bit with the oracle."""
-    rows, extent = 4096, 2304
+    rows, extent = 4096, 4352
     rng = np.random.default_rng(2304)
     x = rng.standard_normal((rows, extent), dtype=np.float32) * np.float32(3)
     sample = _sampled_rows(rng, rows, 16, 16)

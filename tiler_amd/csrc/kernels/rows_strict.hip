@@ -867,6 +867,7 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
                                                 uint32_t out_mode) {                                  \
     softmax_strict_resident_body<R, P, true>(x, y, rows, extent, in_mode, out_mode);                 \
   }
+TILER_SOFTMAX_STRICT_RESIDENT(8, 32)
 TILER_SOFTMAX_STRICT_RESIDENT(8, 16)
 TILER_SOFTMAX_STRICT_RESIDENT(8, 8)
 

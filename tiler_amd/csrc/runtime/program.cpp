@@ -412,15 +412,16 @@ tiler_hip_status plan_softmax_f32(Mode mode, const Target& t, uint64_t rows, uin
   const uint64_t cus = t.compute_units;
   const bool vec = aligned16(addr[x]) && aligned16(addr[y]) && extent % 4 == 0;
   char sname[48];
-  if (strict && vec && extent >= 128 && extent <= 2048 && rows >= 8 * cus) {
-    // Rows of at most 2048 held in registers, 8 per workgroup: x read once
+  if (strict && vec && extent >= 128 && extent <= 4096 && rows >= 8 * cus) {
+    // Rows of at most 4096 held in registers, 8 per workgroup: x read once
     // and y written once, the fold 8 rows per wave instruction (the
-    // 65536 x 2048 case: 0.50 ms staged, ~0.22 ms resident); under a
-    // flushing contract the _m form, with the modes.
+    // 65536 x 2048 case: 0.50 ms staged, ~0.22 ms resident; 8192 x 4096:
+    // 125 us staged, 86 us resident); under a flushing contract the _m
+    // form, with the modes.
     if ((rows + 7) / 8 > 0x7fffffffull)
       return p.refuse(TILER_HIP_REFUSE_CAPACITY, "more rows than the launch grid holds");
-    std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_rr8_p%u%s", extent <= 1024 ? 8u : 16u,
-                  modes ? "_m" : "");
+    std::snprintf(sname, sizeof(sname), "tiler_softmax_f32_strict_rr8_p%u%s",
+                  extent <= 1024 ? 8u : extent <= 2048 ? 16u : 32u, modes ? "_m" : "");
     Launch& l = p.add(sname, (uint32_t)((rows + 7) / 8), 1, 256).ptr(x).ptr(y).u64(rows).u32((uint32_t)extent);
     if (modes) l.u32(in_mode).u32(out_mode);
     return TILER_HIP_OK;

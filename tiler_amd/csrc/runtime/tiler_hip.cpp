@@ -255,6 +255,8 @@ const EntryRow kEntries[] = {
     {"tiler_softmax_f32_strict_rr8_p8", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_rr8_p16_m", "softmax-f32/strict", 2},
     {"tiler_softmax_f32_strict_rr8_p8_m", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_rr8_p32", "softmax-f32/strict", 2},
+    {"tiler_softmax_f32_strict_rr8_p32_m", "softmax-f32/strict", 2},
     {"tiler_rms_norm_f32_strict_r1_m", "rms-norm-f32/strict", 3},
     {"tiler_rms_norm_f32_strict_r1_u_m", "rms-norm-f32/strict", 3},
     {"tiler_rms_norm_f32_strict_r4_m", "rms-norm-f32/strict", 3},
