@@ -726,9 +726,9 @@ __device__ __forceinline__ void rms_strict_resident_body(const T* __restrict__ x
 //   lanes;
 // * the exponents e = certified exp(fl(x - m)), in place in the registers;
 // * the fold: the exponents pass through an LDS ring in 128-column chunks,
-//   eight chunks a round, laid out so that lane 8 g + s of wave 0 reads
+//   eight chunks a round, laid out so that lane 8 g + s of the folding wave reads
 //   segment s (16 columns) of row g's chunk with conflict-free 16-byte
-//   reads, and wave 0 relay-folds each chunk (relay_fold_chunk) from -0.0
+//   reads, and that wave relay-folds each chunk (relay_fold_chunk) from -0.0
 //   (an exponent is never -0.0, so -0.0 plus the first is the first): one
 //   wave instruction advances the eight rows' chains;
 // * y = fl(e * fl(1 / d)) from the registers: the reciprocal, then a
@@ -788,7 +788,7 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
     v[j].z = expo(v[j].z);
     v[j].w = expo(v[j].w);
   }
-  // Wave 0 relay-folds (relay_fold_chunk): lane 8 g + s holds segment s
+  // The folding wave relay-folds (relay_fold_chunk): lane 8 g + s holds segment s
   // (16 columns) of row g's chunk.  Columns past the row's end go to the
   // ring as -0.0, which leaves every sum unchanged, so whole chunks are
   // folded; the next chunk's segment is read while the current one is
@@ -797,6 +797,12 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
   float acc = -0.0f;
   const f32x4 nz = {-0.0f, -0.0f, -0.0f, -0.0f};
   f32x4* const mine = ring + (l & 3u) * 64u + 8u * r + (l >> 2);
+  // The folding wave: wave 0, or for P >= 16 wave blockIdx % 4, so that the
+  // chains of the workgroups a CU holds at once are spread over its SIMDs
+  // rather than all issued by one (65536 x 2048: 217-224 us with wave 0,
+  // 200-204 rotated; 8192 x 4096: 85-86 against 79-80; the same rotation
+  // measured no faster for P = 8 and for the resident RMSNorm).
+  const uint32_t fw = P >= 16 ? (blockIdx.x & 3u) : 0u;
   auto round = [&](auto step) -> bool {
     constexpr int c0 = decltype(step)::value * Q;
     if ((uint32_t)c0 * 128u >= extent) return false;
@@ -804,7 +810,7 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
     for (int q = 0; q < Q && c0 + q < P; ++q)
       mine[q * kChunk] = 4u * (l + 32u * (c0 + q)) < extent ? v[c0 + q] : nz;
     __syncthreads();
-    if (wave == 0) {
+    if (wave == fw) {
       const uint32_t left = extent - (uint32_t)c0 * 128u;
       const uint32_t nq = left < Q * 128u ? (left + 127u) / 128u : (uint32_t)Q;
       const f32x4* src = ring + lane;
@@ -829,7 +835,7 @@ __device__ __forceinline__ void softmax_strict_resident_body(const float* __rest
   };
   unrolled_while<0, (P + Q - 1) / Q>(round);
   // Row g's sum is in lane 8 g after the last chunk's final hop.
-  if (wave == 0 && (lane & 7u) == 0) recip[lane >> 3] = kModes ? F(1.0f / acc) : 1.0f / acc;
+  if (wave == fw && (lane & 7u) == 0) recip[lane >> 3] = kModes ? F(1.0f / acc) : 1.0f / acc;
   __syncthreads();
   if (!row_ok) return;
   const float rc = recip[r];
