@@ -77,7 +77,7 @@ def test_strict_contract_selects_the_serial_row_and_contraction_kernels():
     assert realize(L.PROGRAM_RMS_NORM, (5, 20000), scalars=(EPS,)).symbols == ["tiler_rms_norm_f32_strict_r1"]
     assert realize(L.PROGRAM_RMS_NORM, (5, 40), scalars=(EPS,)).symbols == ["tiler_rms_norm_f32_strict"]
     assert realize(L.PROGRAM_SOFTMAX, (32, 131072)).symbols == ["tiler_softmax_f32_strict_r1"]
-    # rows of 128..2048 aligned elements, enough of them: held in registers, 8 per workgroup
+    # rows of 128..4096 aligned elements, enough of them: held in registers, 8 per workgroup
     sm = realize(L.PROGRAM_SOFTMAX, (65536, 2048))
     assert sm.symbols == ["tiler_softmax_f32_strict_rr8_p16"] and sm.dispatches[0].grid == (8192, 1, 1)
     assert sm.dispatches[0].block == (256, 1, 1)
